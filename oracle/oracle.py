@@ -1,0 +1,227 @@
+"""numpy front end of the C parity oracle (oracle/e8_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, by ``__graft_entry__.smoke()``
+and by the ``cpu_baseline`` leg of bench.py, always as the checker.  The
+product (coset_amd/) never imports it.
+
+Each wrapper restates one reference function (cited in e8_oracle.c); the
+closed forms here (``beta_bounds``, ``layer_backward``) restate
+coset/core/layers.py:381-426 and the autograd chain of layers.py:428-478.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "_build", "libe8oracle.so")
+_lib = None
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+_u32p = np.ctypeslib.ndpointer(dtype=np.uint32, flags="C_CONTIGUOUS")
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_flt = ctypes.c_float
+
+
+def build() -> str:
+    """Compile the oracle with its Makefile (gcc, no contraction)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        L.or_custom_round.argtypes = [_flt]
+        L.or_custom_round.restype = _flt
+        L.or_g_x.argtypes = [_f32p, _int, _f32p]
+        L.or_projection.argtypes = [_f32p, _i64, _int, _f32p]
+        L.or_encode_coords.argtypes = [_f32p, _i64, _int, _i32p]
+        L.or_decode_coords.argtypes = [_i32p, _i64, _f32p]
+        L.or_pack_index.argtypes = [_i32p, _int]
+        L.or_pack_index.restype = ctypes.c_uint32
+        L.or_e8_encode.argtypes = [_f32p, _i64, _flt, _int, _int, _i32p]
+        L.or_e8_decode.argtypes = [_i32p, _i64, _flt, _int, _int, _f32p]
+        L.or_residual.argtypes = [_i32p, _int, _int, _int, _f32p]
+        L.or_layer_quant.argtypes = [_f32p, _i64, _i64, _f32p, _int, _int, _flt,
+                                     _f32p, ctypes.c_void_p, ctypes.c_void_p]
+        L.or_build_one_sided_vlut.argtypes = [_f32p, _int, _int, _f32p]
+        L.or_vlut_matmul.argtypes = [_u32p, _f32p, _int, _f32p, _i64, _i64, _i64,
+                                     _int, _int, _int, _f32p]
+        _lib = L
+    return _lib
+
+
+def _f32(x):
+    return np.ascontiguousarray(x, dtype=np.float32)
+
+
+def custom_round(x):
+    x = _f32(x)
+    f = np.vectorize(lambda v: lib().or_custom_round(float(v)), otypes=[np.float32])
+    return f(x).astype(np.float32)
+
+
+def g_x(x, legacy=False):
+    x = _f32(x).reshape(-1, 8)
+    out = np.empty_like(x)
+    for i in range(x.shape[0]):
+        row = np.empty(8, np.float32)
+        lib().or_g_x(np.ascontiguousarray(x[i]), int(legacy), row)
+        out[i] = row
+    return out
+
+
+def projection(x, legacy=False):
+    x = _f32(x).reshape(-1, 8)
+    y = np.empty_like(x)
+    lib().or_projection(x, x.shape[0], int(legacy), y)
+    return y
+
+
+def encode_coords(y, q):
+    y = _f32(y).reshape(-1, 8)
+    b = np.empty(y.shape, np.int32)
+    lib().or_encode_coords(y, y.shape[0], int(q), b)
+    return b
+
+
+def decode_coords(b):
+    b = np.ascontiguousarray(b, np.int32).reshape(-1, 8)
+    y = np.empty(b.shape, np.float32)
+    lib().or_decode_coords(b, b.shape[0], y)
+    return y
+
+
+def e8_encode(x, q, M, beta=1.0):
+    """Codes [N, M, 8] int32 of coset/core/e8/codecs.py:17-89 (no dither)."""
+    x = _f32(x).reshape(-1, 8)
+    codes = np.empty((x.shape[0], M, 8), np.int32)
+    lib().or_e8_encode(x, x.shape[0], float(np.float32(beta)), int(q), int(M), codes)
+    return codes
+
+
+def e8_decode(codes, q, M, beta=1.0):
+    codes = np.ascontiguousarray(codes, np.int32).reshape(-1, M, 8)
+    out = np.empty((codes.shape[0], 8), np.float32)
+    lib().or_e8_decode(codes, codes.shape[0], float(np.float32(beta)), int(q), int(M), out)
+    return out
+
+
+def residual(b, q, legacy=False, strided=False):
+    b = np.ascontiguousarray(b, np.int32).reshape(-1, 8)
+    out = np.empty(b.shape, np.float32)
+    for i in range(b.shape[0]):
+        r = np.empty(8, np.float32)
+        lib().or_residual(np.ascontiguousarray(b[i]), int(q), int(legacy), int(strided), r)
+        out[i] = r
+    return out
+
+
+def pack_words(codes, q):
+    """[N, M, 8] digits -> [N, M] level words idx(b) = sum_j b_j q^(7-j)."""
+    codes = np.asarray(codes, np.int64)
+    w = np.zeros(codes.shape[:-1], np.int64)
+    for j in range(8):
+        w = w * q + codes[..., j]
+    return w.astype(np.uint32)
+
+
+def unpack_words(words, q):
+    w = np.asarray(words, np.int64)
+    out = np.empty(w.shape + (8,), np.int32)
+    for j in range(7, -1, -1):
+        out[..., j] = w % q
+        w = w // q
+    return out
+
+
+def layer_quant(W, beta_row, q, M, clip):
+    """W_q, unscaled Q and codes of coset/core/layers.py:428-463."""
+    W = _f32(W)
+    rows, cols = W.shape
+    beta_row = _f32(beta_row).reshape(-1)
+    Wq = np.empty_like(W)
+    qraw = np.empty_like(W)
+    codes = np.empty((rows * cols // 8, M, 8), np.int32)
+    lib().or_layer_quant(W, rows, cols, beta_row, int(q), int(M), float(clip), Wq,
+                         qraw.ctypes.data, codes.ctypes.data)
+    return Wq, qraw, codes
+
+
+def build_one_sided_vlut(a, q, legacy=True):
+    a = _f32(a).reshape(8)
+    out = np.empty(q ** 8, np.float32)
+    lib().or_build_one_sided_vlut(a, int(q), int(legacy), out)
+    return out
+
+
+def vlut_matmul(words, scale, act, q, M, scale_mode=0, legacy=False):
+    """out[B, rows] of the one-sided lookup over packed words [rows, K/8, M]."""
+    words = np.ascontiguousarray(words, np.uint32)
+    rows, kb, m = words.shape
+    assert m == M
+    act = _f32(act)
+    B, K = act.shape
+    assert K == 8 * kb
+    out = np.empty((B, rows), np.float32)
+    lib().or_vlut_matmul(words, _f32(scale).reshape(-1), int(scale_mode), act, B, rows, K,
+                         int(q), int(M), int(legacy), out)
+    return out
+
+
+# --------------------------------------------------------------------------
+# beta pipeline and backward closed forms (float64 restatements; the layer
+# tolerances are 1e-3 relative so the float64 form is the stricter checker)
+# --------------------------------------------------------------------------
+
+def delta0(q, M, rho=0.95, r_pack=0.5):
+    """coset/core/base.py:270-284."""
+    return (2.0 * rho * r_pack) / (q ** M - 1)
+
+
+def beta_bounds(q, M, Delta0, eta, sigma_ema, xmax_ema, gamma_inv=12.0):
+    """coset/core/layers.py:381-396 in float64."""
+    qM = float(q ** M)
+    sigma = np.asarray(sigma_ema, np.float64)
+    xmax = np.asarray(xmax_ema, np.float64)
+    bmin = (Delta0 / qM) / (eta * gamma_inv * sigma)
+    bmax = np.minimum((Delta0 * (qM - 1)) / (2 * gamma_inv * xmax),
+                      (Delta0 * (qM - 1)) / (2 * eta * gamma_inv * sigma))
+    bmin = np.minimum(bmin, bmax * 0.9)
+    return bmin, bmax
+
+
+def beta_from_theta(theta, bmin, bmax):
+    """coset/core/layers.py:419-422."""
+    s = 1.0 / (1.0 + np.exp(-np.asarray(theta, np.float64)))
+    return bmin + s * (bmax - bmin)
+
+
+def layer_backward(gWq, W, qraw, beta_row, clip):
+    """dL/dW and dL/dbeta of W_q = clamp(STE(W*beta)/beta, -clip, clip).
+
+    Autograd chain of coset/core/layers.py:431-463: clamp passes the gradient
+    where -clip <= Q/beta <= clip; div gives g/beta to Q and -g*Q/beta^2 to
+    beta; the STE (layers.py:87-95) is the identity; mul gives (.)*beta to W
+    and sum((.)*W) to beta.
+    """
+    g = np.asarray(gWq, np.float64)
+    W = np.asarray(W, np.float64)
+    Q = np.asarray(qraw, np.float64)
+    beta = np.asarray(beta_row, np.float64).reshape(-1, 1)
+    Wq_unclamped = np.asarray(qraw, np.float32) / np.asarray(beta_row, np.float32).reshape(-1, 1)
+    mask = (Wq_unclamped >= -clip) & (Wq_unclamped <= clip)
+    gm = g * mask
+    gQ = gm / beta
+    dW = gQ * beta
+    dbeta = (gQ * W).sum(axis=1) - (gm * Q / (beta * beta)).sum(axis=1)
+    return dW, dbeta, mask
