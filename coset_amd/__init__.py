@@ -1,0 +1,26 @@
+"""coset_amd: MI355X-native E8 hierarchical nested-lattice quantization.
+
+Drop-in for the E8 HNLQ hot path of mlsquare/coset: the reference's public
+names (coset/core/__init__.py:10-22, coset/core/e8/__init__.py:7-33) backed by
+hand-written gfx950 HIP kernels behind a C ABI (include/coset_amd.h).
+"""
+from .lattice import E8Lattice, LatticeConfig, Lattice, LegacyE8Lattice
+from .codecs import (
+    DecodingMethod,
+    E8Decoder,
+    e8_decode,
+    e8_encode,
+    e8_quantize,
+    hnlq_decode,
+    hnlq_encode,
+    hnlq_roundtrip,
+    word_dtype,
+)
+
+__version__ = "0.1.0"
+
+__all__ = [
+    "E8Lattice", "LatticeConfig", "Lattice", "LegacyE8Lattice",
+    "e8_encode", "e8_decode", "e8_quantize", "E8Decoder", "DecodingMethod",
+    "hnlq_encode", "hnlq_decode", "hnlq_roundtrip", "word_dtype",
+]

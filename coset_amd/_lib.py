@@ -1,0 +1,107 @@
+"""ctypes binding of libcoset_amd.so (C ABI in include/coset_amd.h).
+
+The library is loaded after torch, so it binds to the HIP runtime torch
+already mapped (both carry soname libamdhip64.so.7): device pointers and
+streams from torch are valid in it.  There is no fallback: if the library is
+missing or no GPU is visible, every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG, "libcoset_amd.so")
+ABI_VERSION = 1
+
+# mirrors of the enums in include/coset_amd.h
+OK, EINVAL, EUNSUPPORTED, EHIP = 0, -1, -2, -3
+F32, BF16, F16 = 0, 1, 2
+SCALE_NONE, SCALE_CODEC, SCALE_LAYER = 0, 1, 2
+OP_CUSTOM_ROUND, OP_G_X, OP_PROJECT, OP_ENCODE_COORDS, OP_DECODE_COORDS = range(5)
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_flt = ctypes.c_float
+
+# name -> argtypes; every entry point returns int
+SIGNATURES = {
+    "coset_e8_hnlq_encode": [_vp, _int, _i64, _int, _flt, _vp, _i64, _vp, _i64, _int, _int,
+                             _vp, _vp, _vp],
+    "coset_e8_hnlq_decode": [_vp, _vp, _i64, _int, _flt, _vp, _i64, _flt, _int, _int, _int,
+                             _vp, _int, _vp],
+    "coset_e8_hnlq_roundtrip": [_vp, _int, _i64, _int, _flt, _vp, _i64, _flt, _vp, _i64,
+                                _int, _int, _int, _vp, _vp, _vp, _int, _vp],
+    "coset_e8_lattice_op": [_int, _int, _vp, _i64, _int, _vp, _vp],
+}
+
+_lib = None
+
+
+class CosetError(RuntimeError):
+    pass
+
+
+def load():
+    """Load the library (raises if it was not built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise CosetError(f"{LIB_PATH} is missing: run `python -m coset_amd.build` first")
+    lib = ctypes.CDLL(LIB_PATH)
+    lib.coset_abi_version.restype = _int
+    lib.coset_last_error.restype = ctypes.c_char_p
+    lib.coset_word_bytes.argtypes = [_int]
+    lib.coset_word_bytes.restype = _int
+    for name, args in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = _int
+    v = lib.coset_abi_version()
+    if v != ABI_VERSION:
+        raise CosetError(f"libcoset_amd ABI {v}, expected {ABI_VERSION}: rebuild")
+    _lib = lib
+    return lib
+
+
+def call(name: str, *args) -> None:
+    rc = getattr(load(), name)(*args)
+    if rc != OK:
+        msg = load().coset_last_error().decode(errors="replace")
+        if rc == EINVAL:
+            raise ValueError(f"{name}: {msg}")
+        raise CosetError(f"{name} failed ({rc}): {msg}")
+
+
+def word_bytes(q: int) -> int:
+    return 2 if q <= 4 else 4
+
+
+def ptr(t):
+    """Device pointer of a tensor (or None)."""
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def require_gpu() -> torch.device:
+    if not torch.cuda.is_available():
+        raise CosetError("coset_amd needs a ROCm GPU (gfx950); none is visible")
+    load()
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float32:
+        return F32
+    if dt == torch.bfloat16:
+        return BF16
+    raise ValueError(f"unsupported dtype {dt} (float32 or bfloat16)")

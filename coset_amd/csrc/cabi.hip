@@ -1,0 +1,175 @@
+// cabi.hip -- extern "C" entry points of libcoset_amd.so (declared in
+// include/coset_amd.h).  Validates every request on the host before any
+// launch, so that a kernel only ever sees shapes its grid was sized for.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/coset_amd.h"
+#include "codec_kernels.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int check_hip(hipError_t e, const char* what)
+{
+    if (e == hipSuccess) return COSET_OK;
+    return fail(COSET_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+int check_qm(int q, int M)
+{
+    if (q < 2 || q > 16) return fail(COSET_EINVAL, "q=%d outside [2,16]", q);
+    if (M < 1 || M > coset::kMaxM) return fail(COSET_EINVAL, "M=%d outside [1,%d]", M, coset::kMaxM);
+    return COSET_OK;
+}
+
+int check_scale(int scale_mode, float beta, const float* beta_row, int64_t blocks_per_row,
+                int64_t n)
+{
+    switch (scale_mode) {
+    case COSET_SCALE_NONE: return COSET_OK;
+    case COSET_SCALE_CODEC:
+        if (!(beta > 0.f)) return fail(COSET_EINVAL, "beta must be positive (got %g)", (double)beta);
+        return COSET_OK;
+    case COSET_SCALE_LAYER:
+        if (!beta_row) return fail(COSET_EINVAL, "layer scaling needs beta_row");
+        if (blocks_per_row <= 0 || n % blocks_per_row != 0)
+            return fail(COSET_EINVAL, "n_blocks=%lld is not a multiple of blocks_per_row=%lld",
+                        (long long)n, (long long)blocks_per_row);
+        return COSET_OK;
+    default: return fail(COSET_EINVAL, "unknown scale_mode %d", scale_mode);
+    }
+}
+
+int check_dtype(int dt, const char* what)
+{
+    if (dt != COSET_F32 && dt != COSET_BF16)
+        return fail(COSET_EUNSUPPORTED, "%s dtype %d not supported (fp32, bf16)", what, dt);
+    return COSET_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int coset_abi_version(void) { return COSET_ABI_VERSION; }
+
+const char* coset_last_error(void) { return g_last_error.c_str(); }
+
+int coset_word_bytes(int q) { return coset::word_bytes(q); }
+
+static int codec_common(int mode, const void* x, int x_dtype, int64_t n, int scale_mode,
+                        float beta, const float* beta_row, int64_t bpr, float clip,
+                        const float* dither, int64_t dither_stride, int q, int M, int strided,
+                        const void* packed_in, const float* codes_in, void* packed,
+                        float* codes_f32, void* out, int out_dtype, void* stream)
+{
+    int rc;
+    if (n < 0) return fail(COSET_EINVAL, "n_blocks < 0");
+    if (n > (int64_t)0x7fffffff * 256) return fail(COSET_EINVAL, "n_blocks too large");
+    if ((rc = check_qm(q, M))) return rc;
+    if ((rc = check_scale(scale_mode, beta, beta_row, bpr, n))) return rc;
+    if (mode != coset::MODE_DECODE) {
+        if (n > 0 && !x) return fail(COSET_EINVAL, "x is NULL");
+        if ((rc = check_dtype(x_dtype, "input"))) return rc;
+        if (!aligned(x, 16)) return fail(COSET_EINVAL, "x must be 16-byte aligned");
+        if (dither && dither_stride != 0 && dither_stride != 8)
+            return fail(COSET_EINVAL, "dither_stride must be 0 or 8");
+    } else {
+        if (n > 0 && !packed_in && !codes_in) return fail(COSET_EINVAL, "no codes to decode");
+        if (codes_in && !aligned(codes_in, 16)) return fail(COSET_EINVAL, "codes must be 16-byte aligned");
+    }
+    if (mode != coset::MODE_ENCODE && out) {
+        if ((rc = check_dtype(out_dtype, "output"))) return rc;
+        if (!aligned(out, 16)) return fail(COSET_EINVAL, "out must be 16-byte aligned");
+    }
+    if (codes_f32 && !aligned(codes_f32, 16)) return fail(COSET_EINVAL, "codes_f32 must be 16-byte aligned");
+    if (packed && !aligned(packed, 4)) return fail(COSET_EINVAL, "packed must be 4-byte aligned");
+    if (scale_mode == COSET_SCALE_LAYER && !(clip >= 0.f)) return fail(COSET_EINVAL, "clip must be >= 0");
+
+    coset::CodecArgs a{};
+    a.n = n;
+    a.q = q;
+    a.M = M;
+    a.scale_mode = scale_mode;
+    a.beta = beta;
+    a.beta_row = beta_row;
+    a.blocks_per_row = bpr > 0 ? bpr : 1;
+    a.clip = clip;
+    a.strided = strided ? 1 : 0;
+    a.x = x;
+    a.x_dtype = x_dtype;
+    a.dither = dither;
+    a.dither_stride = dither_stride;
+    a.packed = packed;
+    a.codes_f32 = codes_f32;
+    a.packed_in = packed_in;
+    a.codes_in_f32 = packed_in ? nullptr : codes_in;
+    a.out = out;
+    a.out_dtype = out_dtype;
+    return check_hip(coset::launch_codec(a, mode, (hipStream_t)stream), "codec launch");
+}
+
+int coset_e8_hnlq_encode(const void* x, int x_dtype, int64_t n_blocks, int scale_mode,
+                         float beta, const float* beta_row, int64_t blocks_per_row,
+                         const float* dither, int64_t dither_stride, int q, int M,
+                         void* packed, float* codes_f32, void* stream)
+{
+    return codec_common(coset::MODE_ENCODE, x, x_dtype, n_blocks, scale_mode, beta, beta_row,
+                        blocks_per_row, 0.f, dither, dither_stride, q, M, 0, nullptr, nullptr,
+                        packed, codes_f32, nullptr, COSET_F32, stream);
+}
+
+int coset_e8_hnlq_decode(const void* packed, const float* codes_f32, int64_t n_blocks,
+                         int scale_mode, float beta, const float* beta_row,
+                         int64_t blocks_per_row, float clip, int q, int M, int strided,
+                         void* out, int out_dtype, void* stream)
+{
+    if (n_blocks > 0 && !out) return fail(COSET_EINVAL, "out is NULL");
+    return codec_common(coset::MODE_DECODE, nullptr, COSET_F32, n_blocks, scale_mode, beta,
+                        beta_row, blocks_per_row, clip, nullptr, 0, q, M, strided, packed,
+                        codes_f32, nullptr, nullptr, out, out_dtype, stream);
+}
+
+int coset_e8_hnlq_roundtrip(const void* x, int x_dtype, int64_t n_blocks, int scale_mode,
+                            float beta, const float* beta_row, int64_t blocks_per_row,
+                            float clip, const float* dither, int64_t dither_stride, int q,
+                            int M, int strided, void* packed, float* codes_f32, void* out,
+                            int out_dtype, void* stream)
+{
+    return codec_common(coset::MODE_ROUNDTRIP, x, x_dtype, n_blocks, scale_mode, beta, beta_row,
+                        blocks_per_row, clip, dither, dither_stride, q, M, strided, nullptr,
+                        nullptr, packed, codes_f32, out, out_dtype, stream);
+}
+
+int coset_e8_lattice_op(int op, int legacy, const float* in, int64_t n_blocks, int q,
+                        float* out, void* stream)
+{
+    if (n_blocks < 0) return fail(COSET_EINVAL, "n_blocks < 0");
+    if (op < COSET_OP_CUSTOM_ROUND || op > COSET_OP_DECODE_COORDS)
+        return fail(COSET_EINVAL, "unknown lattice op %d", op);
+    if (n_blocks > 0 && (!in || !out)) return fail(COSET_EINVAL, "NULL buffer");
+    if (!aligned(in, 16) || !aligned(out, 16)) return fail(COSET_EINVAL, "buffers must be 16-byte aligned");
+    if (op == COSET_OP_ENCODE_COORDS && q < 1) return fail(COSET_EINVAL, "q must be positive");
+    return check_hip(coset::launch_lattice_op(op, legacy, in, n_blocks, q, out, (hipStream_t)stream),
+                     "lattice op launch");
+}
+
+}  // extern "C"

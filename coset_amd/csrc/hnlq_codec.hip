@@ -1,0 +1,192 @@
+// hnlq_codec.hip -- fused E8 HNLQ encode / decode / round-trip kernels.
+//
+// Replaces the M-level loops of e8_encode (coset/core/e8/codecs.py:63-83) and
+// E8Decoder._full_decode (codecs.py:139-180), including the layer-convention
+// scaling of HNLQLinearQAT._quantize_weights (coset/core/layers.py:428-463).
+//
+// One thread owns one 8-wide block: two 16-byte loads (fp32) or one (bf16),
+// M projections to encode, M more to decode, then packed level words and the
+// decoded block are written with 16-byte stores.  Blocks are contiguous in
+// HBM, so a wavefront reads and writes contiguous 2 KiB (fp32) spans.
+//
+// Scaling conventions
+//   SCALE_CODEC  x_s = x / beta;        out = dec * beta           (codecs.py:64,175)
+//   SCALE_LAYER  x_s = x * beta_row;    out = clamp(dec / beta_row, +-clip)
+//                                                                 (layers.py:431,455,463)
+#include "codec_kernels.hpp"
+
+namespace coset {
+
+template <int Q, int MODE>
+__global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
+{
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= a.n) return;
+    const int q = Q > 0 ? Q : a.q;
+    const float qf = (float)q;
+    const int M = a.M;
+
+    float scale = 1.f;
+    if (a.scale_mode == SCALE_CODEC)
+        scale = a.beta;
+    else if (a.scale_mode == SCALE_LAYER)
+        scale = a.beta_row[i / a.blocks_per_row];
+
+    float acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+
+    if (MODE != MODE_DECODE) {
+        float xl[8];
+        if (a.x_dtype == DT_BF16) {
+            uint4 v = reinterpret_cast<const uint4*>(a.x)[i];
+            uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                xl[2 * j] = __uint_as_float(w[j] << 16);
+                xl[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+            }
+        } else {
+            const float4* p = reinterpret_cast<const float4*>(a.x) + 2 * i;
+            float4 u = p[0], v = p[1];
+            xl[0] = u.x; xl[1] = u.y; xl[2] = u.z; xl[3] = u.w;
+            xl[4] = v.x; xl[5] = v.y; xl[6] = v.z; xl[7] = v.w;
+        }
+        if (a.scale_mode == SCALE_CODEC) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) xl[j] = __fdiv_rn(xl[j], scale);
+        } else if (a.scale_mode == SCALE_LAYER) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) xl[j] = __fmul_rn(xl[j], scale);
+        }
+        if (a.dither) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                xl[j] = __fadd_rn(xl[j], a.dither[a.dither_stride * i + j]);
+        }
+
+        float w = 1.f;
+        uint32_t words[kMaxM];
+        for (int m = 0; m < M; ++m) {
+            float y[8];
+            int b[8];
+            project<false, false>(xl, y);
+            lattice_digits<Q>(y, q, b);
+            words[m] = pack_word<Q>(b, q);
+            if (a.codes_f32) {
+                float4* cp = reinterpret_cast<float4*>(a.codes_f32 + ((size_t)i * M + m) * 8);
+                cp[0] = make_float4((float)b[0], (float)b[1], (float)b[2], (float)b[3]);
+                cp[1] = make_float4((float)b[4], (float)b[5], (float)b[6], (float)b[7]);
+            }
+            if (MODE == MODE_ROUNDTRIP) {
+                float gb[8], r[8];
+                lattice_point(b, gb);
+                if (a.strided)
+                    residual_from_point<false, true, Q>(gb, qf, r);
+                else
+                    residual_from_point<false, false, Q>(gb, qf, r);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[j] = __fadd_rn(acc[j], __fmul_rn(w, r[j]));
+                w = __fmul_rn(w, qf);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) xl[j] = div_q<Q>(xl[j], qf);
+        }
+        if (a.packed) {
+            if (word_bytes(q) == 2) {
+                uint16_t* pw = reinterpret_cast<uint16_t*>(a.packed) + (size_t)i * M;
+                if (M == 2) {
+                    *reinterpret_cast<uint32_t*>(pw) = words[0] | (words[1] << 16);
+                } else {
+                    for (int m = 0; m < M; ++m) pw[m] = (uint16_t)words[m];
+                }
+            } else {
+                uint32_t* pw = reinterpret_cast<uint32_t*>(a.packed) + (size_t)i * M;
+                for (int m = 0; m < M; ++m) pw[m] = words[m];
+            }
+        }
+    } else {
+        float w = 1.f;
+        for (int m = 0; m < M; ++m) {
+            float gb[8], r[8];
+            if (a.codes_in_f32) {
+                const float4* cp = reinterpret_cast<const float4*>(a.codes_in_f32 + ((size_t)i * M + m) * 8);
+                float4 u = cp[0], v = cp[1];
+                float bf[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+                lattice_point_f(bf, gb);
+            } else {
+                uint32_t word;
+                if (word_bytes(q) == 2)
+                    word = reinterpret_cast<const uint16_t*>(a.packed_in)[(size_t)i * M + m];
+                else
+                    word = reinterpret_cast<const uint32_t*>(a.packed_in)[(size_t)i * M + m];
+                int b[8];
+                unpack_word<Q>(word, q, b);
+                lattice_point(b, gb);
+            }
+            if (a.strided)
+                residual_from_point<false, true, Q>(gb, qf, r);
+            else
+                residual_from_point<false, false, Q>(gb, qf, r);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[j] = __fadd_rn(acc[j], __fmul_rn(w, r[j]));
+            w = __fmul_rn(w, qf);
+        }
+    }
+
+    if (MODE == MODE_ENCODE || !a.out) return;
+    float o[8];
+    if (a.scale_mode == SCALE_CODEC) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = __fmul_rn(acc[j], scale);
+    } else if (a.scale_mode == SCALE_LAYER) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            float v = __fdiv_rn(acc[j], scale);
+            o[j] = fminf(fmaxf(v, -a.clip), a.clip);
+            if (v != v) o[j] = v;  // torch.clamp propagates NaN
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = acc[j];
+    }
+    if (a.out_dtype == DT_BF16) {
+        uint4 v;
+        v.x = f32_to_bf16(o[0]) | ((uint32_t)f32_to_bf16(o[1]) << 16);
+        v.y = f32_to_bf16(o[2]) | ((uint32_t)f32_to_bf16(o[3]) << 16);
+        v.z = f32_to_bf16(o[4]) | ((uint32_t)f32_to_bf16(o[5]) << 16);
+        v.w = f32_to_bf16(o[6]) | ((uint32_t)f32_to_bf16(o[7]) << 16);
+        reinterpret_cast<uint4*>(a.out)[i] = v;
+    } else {
+        float4* p = reinterpret_cast<float4*>(a.out) + 2 * i;
+        p[0] = make_float4(o[0], o[1], o[2], o[3]);
+        p[1] = make_float4(o[4], o[5], o[6], o[7]);
+    }
+}
+
+template <int MODE>
+static hipError_t launch_mode(const CodecArgs& a, hipStream_t s)
+{
+    dim3 block(256);
+    dim3 grid((unsigned)((a.n + 255) / 256));
+    switch (a.q) {
+    case 2: hipLaunchKernelGGL((hnlq_codec_kernel<2, MODE>), grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((hnlq_codec_kernel<4, MODE>), grid, block, 0, s, a); break;
+    case 8: hipLaunchKernelGGL((hnlq_codec_kernel<8, MODE>), grid, block, 0, s, a); break;
+    case 16: hipLaunchKernelGGL((hnlq_codec_kernel<16, MODE>), grid, block, 0, s, a); break;
+    default: hipLaunchKernelGGL((hnlq_codec_kernel<0, MODE>), grid, block, 0, s, a); break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_codec(const CodecArgs& a, int mode, hipStream_t s)
+{
+    if (a.n == 0) return hipSuccess;
+    switch (mode) {
+    case MODE_ENCODE: return launch_mode<MODE_ENCODE>(a, s);
+    case MODE_DECODE: return launch_mode<MODE_DECODE>(a, s);
+    default: return launch_mode<MODE_ROUNDTRIP>(a, s);
+    }
+}
+
+}  // namespace coset

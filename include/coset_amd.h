@@ -1,0 +1,112 @@
+/*
+ * coset_amd.h -- C ABI of the MI355X E8 HNLQ library (libcoset_amd.so).
+ *
+ * Plain pointers and sizes only.  Every buffer is device memory allocated by
+ * the caller; `stream` is a hipStream_t (NULL = legacy default stream).  Calls
+ * are asynchronous and stream-ordered; none synchronizes the host.  Return
+ * value: COSET_OK (0) or a negative COSET_E* code; coset_last_error() then
+ * holds a message for the calling thread.
+ *
+ * Packed code format: level word idx(b) = sum_j b_j q^(7-j) for the level's
+ * digits b in [0,q)^8 (the reference vLUT index, coset/legacy/quant/vlut.py:
+ * 217-238); words are stored [n_blocks, M] as uint16 when q <= 4 and uint32
+ * when 4 < q <= 16 (coset_word_bytes).
+ *
+ * Reference interfaces replaced (paths in the mlsquare/coset tree):
+ *   coset_e8_hnlq_encode     e8_encode             coset/core/e8/codecs.py:17-89
+ *   coset_e8_hnlq_decode     e8_decode/_full_decode coset/core/e8/codecs.py:139-218
+ *   coset_e8_hnlq_roundtrip  e8_quantize           coset/core/e8/codecs.py:221-286
+ *                            and the quantize step of HNLQLinearQAT._quantize_weights
+ *                                                  coset/core/layers.py:428-463
+ *   coset_e8_lattice_op      Lattice.custom_round/encode_coords/decode_coords
+ *                                                  coset/core/base.py:134-202,
+ *                            E8Lattice.g_x/projection coset/core/e8/lattice.py:67-169,
+ *                            legacy E8Lattice.g_x/Q coset/legacy/lattices/e8.py:41-103
+ *   coset_e8_qat_fwd         HNLQLinearQAT._quantize_weights (scale, STE quantize,
+ *                            unscale, clamp)       coset/core/layers.py:398-470
+ *   coset_e8_qat_bwd         autograd of that chain through the straight-through
+ *                            estimator             coset/core/layers.py:62-110, 428-463
+ *   coset_vlut_build_one_sided  vLUTManager.build_one_sided_vlut
+ *                                                  coset/legacy/quant/vlut.py:72-117
+ *   coset_vlut_lookup_dot    one-sided lookup sum  tests/legacy/test_one_sided_vlut_pytest.py:22-43
+ *   coset_vlut_matmul        the same lookup over a weight matrix (the reference's
+ *                            placeholder is QLinear._lut_matmul,
+ *                                                  coset/legacy/nn/qlinear.py:272-281)
+ */
+#ifndef COSET_AMD_H
+#define COSET_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define COSET_ABI_VERSION 1
+
+enum {
+    COSET_OK = 0,
+    COSET_EINVAL = -1,       /* bad size, q, M, pointer or alignment */
+    COSET_EUNSUPPORTED = -2, /* valid request this build does not handle */
+    COSET_EHIP = -3          /* HIP runtime error (launch or device) */
+};
+
+enum { COSET_F32 = 0, COSET_BF16 = 1, COSET_F16 = 2 };
+
+/* scale_mode: NONE uses x as is; CODEC divides by beta before encoding and
+ * multiplies the decode by beta (codecs.py:64,175); LAYER multiplies by
+ * beta_row[block / blocks_per_row] before encoding, divides the decode by it
+ * and clamps to [-clip, clip] (layers.py:431,455,463). */
+enum { COSET_SCALE_NONE = 0, COSET_SCALE_CODEC = 1, COSET_SCALE_LAYER = 2 };
+
+/* op codes of coset_e8_lattice_op */
+enum {
+    COSET_OP_CUSTOM_ROUND = 0,
+    COSET_OP_G_X = 1,
+    COSET_OP_PROJECT = 2,
+    COSET_OP_ENCODE_COORDS = 3,
+    COSET_OP_DECODE_COORDS = 4
+};
+
+int coset_abi_version(void);
+const char* coset_last_error(void);
+int coset_word_bytes(int q);
+
+/* Encode n_blocks 8-wide blocks (x: fp32 or bf16, 16-byte aligned).
+ * dither (nullable, fp32): added after scaling; dither_stride 0 broadcasts one
+ * [8] vector, 8 reads [n_blocks, 8].  Outputs (each nullable): packed words
+ * and the reference's float code tensor [n_blocks, M, 8]. */
+int coset_e8_hnlq_encode(const void* x, int x_dtype, int64_t n_blocks,
+                         int scale_mode, float beta, const float* beta_row,
+                         int64_t blocks_per_row, const float* dither, int64_t dither_stride,
+                         int q, int M, void* packed, float* codes_f32, void* stream);
+
+/* Decode from packed words or, when packed is NULL, from a float code tensor
+ * codes_f32 [n_blocks, M, 8].  strided=1 reproduces the reference's batched
+ * decode distance rule (any call on more than one block); it changes results
+ * only for q that is not a power of two.  out: fp32 or bf16 [n_blocks, 8]. */
+int coset_e8_hnlq_decode(const void* packed, const float* codes_f32, int64_t n_blocks,
+                         int scale_mode, float beta, const float* beta_row,
+                         int64_t blocks_per_row, float clip, int q, int M, int strided,
+                         void* out, int out_dtype, void* stream);
+
+/* Fused encode -> decode in one pass (one HBM read, one write).  Any of
+ * packed, codes_f32, out may be NULL. */
+int coset_e8_hnlq_roundtrip(const void* x, int x_dtype, int64_t n_blocks,
+                            int scale_mode, float beta, const float* beta_row,
+                            int64_t blocks_per_row, float clip,
+                            const float* dither, int64_t dither_stride,
+                            int q, int M, int strided,
+                            void* packed, float* codes_f32, void* out, int out_dtype,
+                            void* stream);
+
+/* Elementwise lattice operator over n_blocks fp32 blocks (custom_round is
+ * applied to all 8*n_blocks values).  legacy selects the legacy g_x rule. */
+int coset_e8_lattice_op(int op, int legacy, const float* in, int64_t n_blocks, int q,
+                        float* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,204 @@
+"""Parity of the HIP codec kernels (through the C ABI) with the reference
+goldens and the CPU oracle.  Codes bit-exact; decoded values bit-exact too
+(the reference decode is exact for q = 2^k and the kernels reproduce its
+fp32 operations for every q)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+CODEC_CASES = [("q4M2_b1", 4, 2, 1.0), ("q4M2_b025", 4, 2, 0.25), ("q4M2_b03", 4, 2, 0.3),
+               ("q4M2_b002", 4, 2, 0.02), ("q16M3_b1", 16, 3, 1.0), ("q3M2_b1", 3, 2, 1.0),
+               ("q8M2_b05", 8, 2, 0.5), ("q2M4_b1", 2, 4, 1.0)]
+
+
+@pytest.fixture(scope="module")
+def ca():
+    import coset_amd
+    return coset_amd
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    return t.detach().cpu().numpy()
+
+
+def words(t):
+    """Packed level words as uint32 numpy (uint16/uint32 tensors copy as is)."""
+    return host(t).astype(np.uint32)
+
+
+def test_projection_golden(ca, golden):
+    P = golden("projection")
+    lat = ca.E8Lattice()
+    np.testing.assert_array_equal(host(lat.projection(dev(P["x"]))), P["projection"])
+    np.testing.assert_array_equal(host(lat.g_x(dev(P["x"]))), P["g_x"])
+    np.testing.assert_array_equal(host(lat.custom_round(dev(P["x"]))), P["custom_round"])
+    leg = ca.LegacyE8Lattice()
+    np.testing.assert_array_equal(host(leg.Q(dev(P["legacy_x"]))), P["legacy_q"])
+
+
+def test_coords_roundtrip(ca):
+    lat = ca.E8Lattice()
+    rng = np.random.default_rng(5)
+    for q in (3, 4, 16):
+        z = rng.integers(0, q, size=(1000, 8)).astype(np.float32)
+        y = lat.decode_coords(dev(z), q)
+        np.testing.assert_array_equal(host(y), O.decode_coords(z.astype(np.int32)))
+        np.testing.assert_array_equal(host(lat.encode_coords(y, q)), z)
+    # single vector shape is kept
+    v = lat.projection(torch.randn(8, device="cuda"))
+    assert v.shape == (8,)
+
+
+@pytest.mark.parametrize("name,q,M,beta", CODEC_CASES)
+def test_codec_golden(ca, golden, name, q, M, beta):
+    C = golden("codec")
+    x = C[name + "_x"]
+    cfg = ca.LatticeConfig(lattice_type="E8", q=q, M=M, beta=beta)
+    codes, T = ca.e8_encode(dev(x), cfg)
+    assert T == 0
+    np.testing.assert_array_equal(host(codes).astype(np.int32), C[name + "_codes"].astype(np.int32))
+    dec = ca.e8_decode(dev(C[name + "_codes"].astype(np.float32)), cfg)
+    np.testing.assert_array_equal(host(dec), C[name + "_dec"])
+    # packed path: words equal the reference index of each level's digits
+    packed = ca.hnlq_encode(dev(x), q, M, beta)
+    w = words(packed)
+    np.testing.assert_array_equal(w, O.pack_words(C[name + "_codes"], q))
+    np.testing.assert_array_equal(host(ca.hnlq_decode(packed, q, M, beta)), C[name + "_dec"])
+    pk2, out = ca.hnlq_roundtrip(dev(x), q, M, beta)
+    np.testing.assert_array_equal(words(pk2), w)
+    np.testing.assert_array_equal(host(out), C[name + "_dec"])
+
+
+def test_quantize_golden(ca, golden):
+    C = golden("codec")
+    x = dev(C["quantize_x"])
+    for q in (4, 16):
+        np.testing.assert_array_equal(host(ca.e8_quantize(x, q)), C[f"quantize_q{q}"])
+    codes, _ = ca.e8_encode(dev(C["single_x"]), ca.LatticeConfig(lattice_type="E8", q=4, M=2))
+    assert codes.shape == (2, 8)
+    np.testing.assert_array_equal(host(codes), C["single_codes"].astype(np.float32))
+
+
+@pytest.mark.parametrize("q", [2, 3, 4])
+def test_exhaustive_single_level_decode(ca, golden, q):
+    R = golden("residual_tables")
+    words = torch.arange(q ** 8, dtype=torch.int64).to(ca.word_dtype(q)).cuda().reshape(-1, 1)
+    r = ca.hnlq_decode(words, q, 1, 1.0)
+    np.testing.assert_array_equal(np.rint(2 * host(r)).astype(np.int8), R[f"two_r_q{q}"])
+
+
+def test_q16_decode_sample(ca, golden):
+    R = golden("residual_tables")
+    cfg = ca.LatticeConfig(lattice_type="E8", q=16, M=1)
+    r = ca.e8_decode(dev(R["b_q16"].astype(np.float32).reshape(-1, 1, 8)), cfg)
+    np.testing.assert_array_equal(host(r), R["r_q16"])
+
+
+@pytest.mark.parametrize("n", [0, 1, 2, 255, 257, 1000])
+def test_ragged_sizes(ca, n):
+    rng = np.random.default_rng(n)
+    x = rng.standard_normal((n, 8)).astype(np.float32)
+    for q, M in ((4, 2), (3, 2)):
+        pk, out = ca.hnlq_roundtrip(dev(x), q, M, 1.0)
+        codes = O.e8_encode(x, q, M)
+        np.testing.assert_array_equal(words(pk).reshape(n, M),
+                                      O.pack_words(codes, q).reshape(n, M))
+        np.testing.assert_array_equal(host(out).reshape(n, 8), O.e8_decode(codes, q, M).reshape(n, 8))
+
+
+def test_layer_convention_matches_oracle(ca):
+    """W*beta_row -> quantize -> /beta_row -> clamp (coset/core/layers.py:431-463)."""
+    rng = np.random.default_rng(11)
+    rows, cols = 48, 256
+    W = rng.standard_normal((rows, cols)).astype(np.float32)
+    beta = rng.uniform(0.2, 3.0, size=rows).astype(np.float32)
+    for q, M, clip in ((4, 2, 2.0), (16, 3, 2.0), (4, 2, 0.3)):
+        Wq, qraw, codes = O.layer_quant(W, beta, q, M, clip)
+        pk, out = ca.hnlq_roundtrip(dev(W), q, M, beta_row=dev(beta), blocks_per_row=cols // 8,
+                                    clip=clip)
+        np.testing.assert_array_equal(host(out).reshape(rows, cols), Wq)
+        np.testing.assert_array_equal(words(pk),
+                                      O.pack_words(codes, q).reshape(-1, M))
+
+
+def test_bf16_input_heavy_tailed(ca):
+    """C3 shape in miniature: Student-t(3) clipped at +-2, bf16 in, q16 M3,
+    per-row beta; the kernel upcasts bf16 exactly."""
+    rng = np.random.default_rng(12)
+    rows, cols = 64, 1024
+    x = np.clip(rng.standard_t(3, size=(rows, cols)), -2, 2).astype(np.float32)
+    xb = torch.from_numpy(x).to(torch.bfloat16)
+    x_up = xb.float().numpy()
+    beta = rng.uniform(2.0, 20.0, size=rows).astype(np.float32)
+    Wq, _, codes = O.layer_quant(x_up, beta, 16, 3, 2.0)
+    pk, out = ca.hnlq_roundtrip(xb.cuda(), 16, 3, beta_row=dev(beta), blocks_per_row=cols // 8,
+                                clip=2.0)
+    np.testing.assert_array_equal(host(out).reshape(rows, cols), Wq)
+    np.testing.assert_array_equal(words(pk),
+                                  O.pack_words(codes, 16).reshape(-1, 3))
+    _, outb = ca.hnlq_roundtrip(xb.cuda(), 16, 3, beta_row=dev(beta), blocks_per_row=cols // 8,
+                                clip=2.0, out_dtype=torch.bfloat16)
+    np.testing.assert_array_equal(host(outb.float()).reshape(rows, cols),
+                                  torch.from_numpy(Wq).to(torch.bfloat16).float().numpy())
+
+
+def test_dither(ca):
+    rng = np.random.default_rng(13)
+    x = rng.standard_normal((300, 8)).astype(np.float32)
+    d = (0.3 * rng.standard_normal(8)).astype(np.float32)
+    cfg = ca.LatticeConfig(lattice_type="E8", q=4, M=2, beta=0.5, with_dither=True)
+    codes, _ = ca.e8_encode(dev(x), cfg, dither=dev(d))
+    xs = (x / np.float32(0.5) + d).astype(np.float32)
+    np.testing.assert_array_equal(host(codes).astype(np.int32), O.e8_encode(xs, 4, 2, 1.0))
+    # without with_dither the dither is ignored, as in the reference
+    cfg2 = ca.LatticeConfig(lattice_type="E8", q=4, M=2, beta=0.5)
+    codes2, _ = ca.e8_encode(dev(x), cfg2, dither=dev(d))
+    np.testing.assert_array_equal(host(codes2).astype(np.int32), O.e8_encode(x, 4, 2, 0.5))
+
+
+def test_host_tensors_follow_input_device(ca):
+    x = torch.randn(10, 8)
+    cfg = ca.LatticeConfig(lattice_type="E8", q=4, M=2)
+    codes, _ = ca.e8_encode(x, cfg)
+    assert codes.device.type == "cpu"
+    np.testing.assert_array_equal(codes.numpy().astype(np.int32), O.e8_encode(x.numpy(), 4, 2))
+
+
+def test_errors(ca):
+    cfg = ca.LatticeConfig(lattice_type="E8", q=4, M=2)
+    with pytest.raises(ValueError):
+        ca.e8_encode(torch.randn(4, 7, device="cuda"), cfg)
+    with pytest.raises(ValueError):
+        ca.e8_decode(torch.zeros(4, 2, 8, device="cuda"), cfg, method="fast")
+    with pytest.raises(ValueError):
+        ca.e8_encode(torch.randn(4, 8, device="cuda"),
+                     ca.LatticeConfig(lattice_type="E8", q=17, M=2))
+
+
+def test_full_size_c2_properties(ca):
+    """BASELINE C2 at full size (2^24 blocks, q4 M2, beta 1): a random sample
+    of blocks against the oracle, and the fused pass equal to encode then
+    decode as separate kernels."""
+    n = 1 << 24
+    g = torch.Generator(device="cuda").manual_seed(2)
+    x = torch.randn((n, 8), device="cuda", generator=g)
+    pk, out = ca.hnlq_roundtrip(x, 4, 2, 1.0)
+    idx = torch.randint(0, n, (1 << 15,), device="cuda", generator=g)
+    xs = host(x[idx])
+    codes = O.e8_encode(xs, 4, 2)
+    np.testing.assert_array_equal(words(pk)[host(idx)], O.pack_words(codes, 4))
+    np.testing.assert_array_equal(host(out[idx]), O.e8_decode(codes, 4, 2))
+    pk2 = ca.hnlq_encode(x, 4, 2, 1.0)
+    assert torch.equal(pk2.view(torch.int16), pk.view(torch.int16))
+    out2 = ca.hnlq_decode(pk2, 4, 2, 1.0)
+    assert torch.equal(out2, out)
+    # every decoded block lies in the scaled lattice: 2*out integral
+    assert torch.equal(out * 2, torch.round(out * 2))
