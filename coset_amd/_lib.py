@@ -36,7 +36,12 @@ SIGNATURES = {
     "coset_e8_hnlq_roundtrip": [_vp, _int, _i64, _int, _flt, _vp, _i64, _flt, _vp, _i64,
                                 _int, _int, _int, _vp, _vp, _vp, _int, _vp],
     "coset_e8_lattice_op": [_int, _int, _vp, _i64, _int, _vp, _vp],
+    "coset_init": [_int],
+    "coset_set_option": [_int, _int],
 }
+
+OPT_CODEC_PATH = 1
+CODEC_AUTO, CODEC_GENERIC, CODEC_LUT = 0, 1, 2
 
 _lib = None
 
@@ -92,11 +97,24 @@ def stream_of(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
+_inited = set()
+
+
 def require_gpu() -> torch.device:
+    """The current GPU, with the library's per-device tables built."""
     if not torch.cuda.is_available():
         raise CosetError("coset_amd needs a ROCm GPU (gfx950); none is visible")
     load()
-    return torch.device("cuda", torch.cuda.current_device())
+    dev = torch.cuda.current_device()
+    if dev not in _inited:
+        call("coset_init", dev)
+        _inited.add(dev)
+    return torch.device("cuda", dev)
+
+
+def set_codec_path(path: int) -> None:
+    """0 automatic, 1 generic kernel, 2 LDS-table kernel (q = 2, 4)."""
+    call("coset_set_option", OPT_CODEC_PATH, int(path))
 
 
 def dtype_code(dt: torch.dtype) -> int:

@@ -3,12 +3,14 @@
 // launch, so that a kernel only ever sees shapes its grid was sized for.
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <string>
 
 #include "../../include/coset_amd.h"
 #include "codec_kernels.hpp"
+#include "tables.hpp"
 
 namespace {
 
@@ -75,6 +77,34 @@ const char* coset_last_error(void) { return g_last_error.c_str(); }
 
 int coset_word_bytes(int q) { return coset::word_bytes(q); }
 
+int coset_set_option(int key, int value)
+{
+    switch (key) {
+    case COSET_OPT_CODEC_PATH:
+        if (value < 0 || value > 2) return fail(COSET_EINVAL, "codec path %d not in {0,1,2}", value);
+        coset::g_codec_path = value;
+        return COSET_OK;
+    default: return fail(COSET_EINVAL, "unknown option %d", key);
+    }
+}
+
+int coset_init(int device)
+{
+    int cur = 0;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return check_hip(e, "hipGetDevice");
+    if (device >= 0 && device != cur && (e = hipSetDevice(device)) != hipSuccess)
+        return check_hip(e, "hipSetDevice");
+    int rc = COSET_OK;
+    for (int q : {2, 4})
+        for (int legacy : {0, 1}) {
+            const coset::DecodeTables* t = nullptr;
+            if (rc == COSET_OK) rc = check_hip(coset::get_decode_tables(q, legacy, &t), "decode tables");
+        }
+    if (device >= 0 && device != cur) hipSetDevice(cur);
+    return rc;
+}
+
 static int codec_common(int mode, const void* x, int x_dtype, int64_t n, int scale_mode,
                         float beta, const float* beta_row, int64_t bpr, float clip,
                         const float* dither, int64_t dither_stride, int q, int M, int strided,
@@ -110,6 +140,12 @@ static int codec_common(int mode, const void* x, int x_dtype, int64_t n, int sca
     a.M = M;
     a.scale_mode = scale_mode;
     a.beta = beta;
+    {
+        int ex = 0;
+        float m = std::frexp(beta, &ex);
+        a.beta_is_pow2 = (scale_mode == COSET_SCALE_CODEC && m == 0.5f) ? 1 : 0;
+        a.beta_inv = a.beta_is_pow2 ? std::ldexp(1.0f, 1 - ex) : 1.0f;
+    }
     a.beta_row = beta_row;
     a.blocks_per_row = bpr > 0 ? bpr : 1;
     a.clip = clip;

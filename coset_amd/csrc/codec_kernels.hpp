@@ -22,6 +22,8 @@ struct CodecArgs {
     int q, M;
     int scale_mode;          // ScaleMode
     float beta;              // SCALE_CODEC
+    int beta_is_pow2;        // beta = 2^k: x / beta == x * beta_inv exactly
+    float beta_inv;
     const float* beta_row;   // SCALE_LAYER: [n / blocks_per_row]
     int64_t blocks_per_row;  // SCALE_LAYER
     float clip;              // SCALE_LAYER
@@ -42,7 +44,15 @@ struct CodecArgs {
     int out_dtype;
 };
 
+// Dispatch: the LDS-table kernel (hnlq_lut.hip) for q in {2, 4} and large
+// n, the generic kernel (hnlq_codec.hip) otherwise.  codec_path overrides
+// the choice: 0 automatic, 1 always generic, 2 table kernel when supported.
 hipError_t launch_codec(const CodecArgs& a, int mode, hipStream_t s);
+hipError_t launch_codec_generic(const CodecArgs& a, int mode, hipStream_t s);
+bool lut_path_supported(const CodecArgs& a, int mode);
+hipError_t launch_codec_lut(const CodecArgs& a, int mode, hipStream_t s);
+extern int g_codec_path;
+constexpr int64_t kLutMinBlocks = 1 << 16;
 
 // Elementwise lattice operators (custom_round, g_x, projection,
 // encode_coords, decode_coords) over n blocks.

@@ -110,6 +110,13 @@ __device__ __forceinline__ bool nearer(float a, float b)
     return cr_sqrtf(a) < cr_sqrtf(b);
 }
 
+// Per-element select written as a bit blend, so the compiler keeps both
+// candidates in registers instead of selecting between two stack arrays.
+__device__ __forceinline__ float blend(uint32_t mask, float a, float b)
+{
+    return __uint_as_float((__float_as_uint(a) & mask) | (__float_as_uint(b) & ~mask));
+}
+
 // E8 closest point, reference semantics (core or legacy g_x rule).
 template <bool LEGACY, bool STRIDED>
 __device__ __forceinline__ void project(const float x[8], float out[8])
@@ -123,9 +130,9 @@ __device__ __forceinline__ void project(const float x[8], float out[8])
     for (int i = 0; i < 8; ++i) y1[i] = __fadd_rn(y1[i], 0.5f);
     float a = sumsq_diff<STRIDED>(x, y0);
     float b = sumsq_diff<STRIDED>(x, y1);
-    bool pick0 = nearer(a, b);
+    uint32_t pick0 = nearer(a, b) ? 0xffffffffu : 0u;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) out[i] = pick0 ? y0[i] : y1[i];
+    for (int i = 0; i < 8; ++i) out[i] = blend(pick0, y0[i], y1[i]);
 }
 
 // encode_coords: b = (G^-1 y) mod q for y in E8 (exact integers).

@@ -53,8 +53,13 @@ __global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
             xl[4] = v.x; xl[5] = v.y; xl[6] = v.z; xl[7] = v.w;
         }
         if (a.scale_mode == SCALE_CODEC) {
+            if (a.beta_is_pow2) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) xl[j] = __fdiv_rn(xl[j], scale);
+                for (int j = 0; j < 8; ++j) xl[j] = __fmul_rn(xl[j], a.beta_inv);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) xl[j] = __fdiv_rn(xl[j], scale);
+            }
         } else if (a.scale_mode == SCALE_LAYER) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) xl[j] = __fmul_rn(xl[j], scale);
@@ -66,13 +71,18 @@ __global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
         }
 
         float w = 1.f;
-        uint32_t words[kMaxM];
         for (int m = 0; m < M; ++m) {
             float y[8];
             int b[8];
             project<false, false>(xl, y);
             lattice_digits<Q>(y, q, b);
-            words[m] = pack_word<Q>(b, q);
+            uint32_t word = pack_word<Q>(b, q);
+            if (a.packed) {  // level words stored as produced: [n, M]
+                if (word_bytes(q) == 2)
+                    reinterpret_cast<uint16_t*>(a.packed)[(size_t)i * M + m] = (uint16_t)word;
+                else
+                    reinterpret_cast<uint32_t*>(a.packed)[(size_t)i * M + m] = word;
+            }
             if (a.codes_f32) {
                 float4* cp = reinterpret_cast<float4*>(a.codes_f32 + ((size_t)i * M + m) * 8);
                 cp[0] = make_float4((float)b[0], (float)b[1], (float)b[2], (float)b[3]);
@@ -91,19 +101,6 @@ __global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) xl[j] = div_q<Q>(xl[j], qf);
-        }
-        if (a.packed) {
-            if (word_bytes(q) == 2) {
-                uint16_t* pw = reinterpret_cast<uint16_t*>(a.packed) + (size_t)i * M;
-                if (M == 2) {
-                    *reinterpret_cast<uint32_t*>(pw) = words[0] | (words[1] << 16);
-                } else {
-                    for (int m = 0; m < M; ++m) pw[m] = (uint16_t)words[m];
-                }
-            } else {
-                uint32_t* pw = reinterpret_cast<uint32_t*>(a.packed) + (size_t)i * M;
-                for (int m = 0; m < M; ++m) pw[m] = words[m];
-            }
         }
     } else {
         float w = 1.f;
@@ -179,7 +176,18 @@ static hipError_t launch_mode(const CodecArgs& a, hipStream_t s)
     return hipGetLastError();
 }
 
+int g_codec_path = 0;
+
 hipError_t launch_codec(const CodecArgs& a, int mode, hipStream_t s)
+{
+    if (a.n == 0) return hipSuccess;
+    bool lut = lut_path_supported(a, mode) &&
+               (g_codec_path == 2 || (g_codec_path == 0 && a.n >= kLutMinBlocks));
+    if (lut) return launch_codec_lut(a, mode, s);
+    return launch_codec_generic(a, mode, s);
+}
+
+hipError_t launch_codec_generic(const CodecArgs& a, int mode, hipStream_t s)
 {
     if (a.n == 0) return hipSuccess;
     switch (mode) {

@@ -1,0 +1,254 @@
+// hnlq_lut.hip -- E8 HNLQ codec for q in {2, 4} with table decode in LDS.
+//
+// Same contract and bit-exact results as hnlq_codec.hip (the generic path),
+// but each decode level is two LDS lookups instead of a projection:
+//   2r = 2Gb - q * (2c),  c = coarse[cid_map[idx]]    (tables.hip)
+// 2Gb is integer arithmetic on the digits, and the level sum
+// x_hat = sum_m q^m r_m (exact in the reference's fp32) is accumulated as
+// integers and halved at the end.
+//
+// Launch: persistent grid, one 1024-thread workgroup per CU.  The q = 4 map
+// (65536 x uint16 = 128 KiB) plus the coarse points (<= 8 KiB) fill most of
+// the 160 KiB LDS of a gfx950 CU; every workgroup stages them once and then
+// walks blocks with a grid stride, so HBM sees one contiguous read of x and
+// one write of the outputs.
+#include <algorithm>
+
+#include "codec_kernels.hpp"
+#include "tables.hpp"
+
+namespace coset {
+
+template <int Q>
+struct LutShape {
+    static constexpr int kCodes = Q * Q * Q * Q * Q * Q * Q * Q;
+};
+
+constexpr int kLutThreads = 1024;
+
+template <int Q, int M, int MODE>
+__global__ void __launch_bounds__(kLutThreads) hnlq_lut_kernel(CodecArgs a, const uint16_t* __restrict__ g_map,
+                                                            const uint64_t* __restrict__ g_coarse,
+                                                            int n_coarse)
+{
+    constexpr int NC = LutShape<Q>::kCodes;
+    __shared__ __align__(16) uint16_t s_map[NC];
+    __shared__ uint64_t s_coarse[kMaxCoarse];
+
+    if (MODE != MODE_ENCODE) {
+        const uint4* src = reinterpret_cast<const uint4*>(g_map);
+        uint4* dst = reinterpret_cast<uint4*>(s_map);
+        for (int i = threadIdx.x; i < NC / 8; i += blockDim.x) dst[i] = src[i];
+        for (int i = threadIdx.x; i < n_coarse; i += blockDim.x) s_coarse[i] = g_coarse[i];
+        __syncthreads();
+    }
+
+    const float qf = (float)Q;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n; i += stride) {
+        float scale = 1.f;
+        if (a.scale_mode == SCALE_CODEC)
+            scale = a.beta;
+        else if (a.scale_mode == SCALE_LAYER)
+            scale = a.beta_row[i / a.blocks_per_row];
+
+        // Level words are collected in one 64-bit register (M <= 4 words of
+        // 16 bits); each level is encoded, then decoded from its digits.
+        uint64_t pack = 0;
+        float xl[8];
+        if (MODE != MODE_DECODE) {
+            if (a.x_dtype == DT_BF16) {
+                uint4 v = reinterpret_cast<const uint4*>(a.x)[i];
+                uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    xl[2 * j] = __uint_as_float(w[j] << 16);
+                    xl[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+                }
+            } else {
+                const float4* p = reinterpret_cast<const float4*>(a.x) + 2 * i;
+                float4 u = p[0], v = p[1];
+                xl[0] = u.x; xl[1] = u.y; xl[2] = u.z; xl[3] = u.w;
+                xl[4] = v.x; xl[5] = v.y; xl[6] = v.z; xl[7] = v.w;
+            }
+            if (a.scale_mode == SCALE_CODEC) {
+                if (a.beta_is_pow2) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) xl[j] = __fmul_rn(xl[j], a.beta_inv);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) xl[j] = __fdiv_rn(xl[j], scale);
+                }
+            } else if (a.scale_mode == SCALE_LAYER) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) xl[j] = __fmul_rn(xl[j], scale);
+            }
+            if (a.dither) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    xl[j] = __fadd_rn(xl[j], a.dither[a.dither_stride * i + j]);
+            }
+        } else {
+            const uint16_t* pw = reinterpret_cast<const uint16_t*>(a.packed_in) + (size_t)i * M;
+            if (M == 2) {
+                pack = *reinterpret_cast<const uint32_t*>(pw);
+            } else if (M == 4) {
+                pack = *reinterpret_cast<const uint64_t*>(pw);
+            } else {
+#pragma unroll
+                for (int m = 0; m < M; ++m) pack |= (uint64_t)pw[m] << (16 * m);
+            }
+        }
+
+        int acc2[8];  // sum_m q^m * 2 r_m, exact integers
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc2[j] = 0;
+        int wq = 1;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            int b[8];
+            uint32_t word;
+            if (MODE != MODE_DECODE) {
+                float y[8];
+                project<false, false>(xl, y);
+                lattice_digits<Q>(y, Q, b);
+                word = pack_word<Q>(b, Q);
+                pack |= (uint64_t)word << (16 * m);
+                if (a.codes_f32) {
+                    float4* cp = reinterpret_cast<float4*>(a.codes_f32 + ((size_t)i * M + m) * 8);
+                    cp[0] = make_float4((float)b[0], (float)b[1], (float)b[2], (float)b[3]);
+                    cp[1] = make_float4((float)b[4], (float)b[5], (float)b[6], (float)b[7]);
+                }
+                if (m + 1 < M) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) xl[j] = div_q<Q>(xl[j], qf);
+                }
+            } else {
+                word = (uint32_t)(pack >> (16 * m)) & 0xffffu;
+                unpack_word<Q>(word, Q, b);
+            }
+            if (MODE != MODE_ENCODE) {
+                int u[8];  // 2 G b
+                u[0] = 4 * b[0] - 2 * b[1] + b[7];
+#pragma unroll
+                for (int j = 1; j < 6; ++j) u[j] = 2 * (b[j] - b[j + 1]) + b[7];
+                u[6] = 2 * b[6] + b[7];
+                u[7] = b[7];
+                uint64_t c = s_coarse[s_map[word]];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    int two_c = (int)(int8_t)(uint8_t)(c >> (8 * j));
+                    acc2[j] += wq * (u[j] - Q * two_c);
+                }
+                wq *= Q;
+            }
+        }
+        if (MODE != MODE_DECODE && a.packed) {
+            uint16_t* pw = reinterpret_cast<uint16_t*>(a.packed) + (size_t)i * M;
+            if (M == 1) {
+                pw[0] = (uint16_t)pack;
+            } else if (M == 2) {
+                *reinterpret_cast<uint32_t*>(pw) = (uint32_t)pack;
+            } else {
+#pragma unroll
+                for (int m = 0; m < M; ++m) pw[m] = (uint16_t)(pack >> (16 * m));
+            }
+        }
+        if (MODE == MODE_ENCODE) continue;
+
+        if (!a.out) continue;
+        float o[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            float v = __fmul_rn((float)acc2[j], 0.5f);  // exact
+            if (a.scale_mode == SCALE_CODEC) {
+                v = __fmul_rn(v, scale);
+            } else if (a.scale_mode == SCALE_LAYER) {
+                v = __fdiv_rn(v, scale);
+                v = (v != v) ? v : fminf(fmaxf(v, -a.clip), a.clip);  // clamp keeps NaN
+            }
+            o[j] = v;
+        }
+        if (a.out_dtype == DT_BF16) {
+            uint4 v;
+            v.x = f32_to_bf16(o[0]) | ((uint32_t)f32_to_bf16(o[1]) << 16);
+            v.y = f32_to_bf16(o[2]) | ((uint32_t)f32_to_bf16(o[3]) << 16);
+            v.z = f32_to_bf16(o[4]) | ((uint32_t)f32_to_bf16(o[5]) << 16);
+            v.w = f32_to_bf16(o[6]) | ((uint32_t)f32_to_bf16(o[7]) << 16);
+            reinterpret_cast<uint4*>(a.out)[i] = v;
+        } else {
+            float4* p = reinterpret_cast<float4*>(a.out) + 2 * i;
+            p[0] = make_float4(o[0], o[1], o[2], o[3]);
+            p[1] = make_float4(o[4], o[5], o[6], o[7]);
+        }
+    }
+}
+
+namespace {
+
+int cu_count()
+{
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cached[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
+template <int Q, int MODE>
+hipError_t launch_q(const CodecArgs& a, const DecodeTables* t, hipStream_t s)
+{
+    int64_t need = (a.n + kLutThreads - 1) / kLutThreads;
+    int grid = (int)std::min<int64_t>(need, (int64_t)cu_count());
+    const uint16_t* map = t ? t->cid_map : nullptr;
+    const uint64_t* coarse = t ? t->coarse : nullptr;
+    int nc = t ? t->n_coarse : 0;
+#define COSET_LUT(MM) \
+    hipLaunchKernelGGL((hnlq_lut_kernel<Q, MM, MODE>), dim3(grid), dim3(kLutThreads), 0, s, a, map, coarse, nc)
+    switch (a.M) {
+    case 1: COSET_LUT(1); break;
+    case 2: COSET_LUT(2); break;
+    case 3: COSET_LUT(3); break;
+    case 4: COSET_LUT(4); break;
+    default: return hipErrorInvalidValue;
+    }
+#undef COSET_LUT
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool lut_path_supported(const CodecArgs& a, int mode)
+{
+    if (a.q != 2 && a.q != 4) return false;
+    if (a.M < 1 || a.M > 4) return false;
+    if (mode == MODE_DECODE && a.codes_in_f32) return false;  // float codes may be off-grid
+    return true;
+}
+
+hipError_t launch_codec_lut(const CodecArgs& a, int mode, hipStream_t s)
+{
+    const DecodeTables* t = nullptr;
+    if (mode != MODE_ENCODE) {
+        hipError_t e = get_decode_tables(a.q, 0, &t);
+        if (e != hipSuccess) return e;
+    }
+    if (a.q == 4) {
+        switch (mode) {
+        case MODE_ENCODE: return launch_q<4, MODE_ENCODE>(a, t, s);
+        case MODE_DECODE: return launch_q<4, MODE_DECODE>(a, t, s);
+        default: return launch_q<4, MODE_ROUNDTRIP>(a, t, s);
+        }
+    }
+    switch (mode) {
+    case MODE_ENCODE: return launch_q<2, MODE_ENCODE>(a, t, s);
+    case MODE_DECODE: return launch_q<2, MODE_DECODE>(a, t, s);
+    default: return launch_q<2, MODE_ROUNDTRIP>(a, t, s);
+    }
+}
+
+}  // namespace coset

@@ -68,9 +68,23 @@ enum {
     COSET_OP_DECODE_COORDS = 4
 };
 
+/* option keys of coset_set_option */
+enum {
+    COSET_OPT_CODEC_PATH = 1 /* 0 automatic, 1 generic kernel, 2 LDS-table kernel (q = 2, 4) */
+};
+
 int coset_abi_version(void);
 const char* coset_last_error(void);
 int coset_word_bytes(int q);
+
+/* Build the per-device constant tables (single-level decode and vLUT coarse
+ * points for q = 2 and 4, core and legacy rules) on `device` (-1: current).
+ * Blocking; call once before capturing HIP graphs.  Other entry points build
+ * them on first use. */
+int coset_init(int device);
+
+/* Process-wide tuning/test knobs (see COSET_OPT_*). */
+int coset_set_option(int key, int value);
 
 /* Encode n_blocks 8-wide blocks (x: fp32 or bf16, 16-byte aligned).
  * dither (nullable, fp32): added after scaling; dither_stride 0 broadcasts one

@@ -21,6 +21,16 @@ def ca():
     return coset_amd
 
 
+@pytest.fixture(params=[1, 2], ids=["generic", "lut"])
+def path(request, ca):
+    """Run the test on the generic kernel and on the LDS-table kernel."""
+    from coset_amd import _lib
+    _lib.require_gpu()
+    _lib.set_codec_path(request.param)
+    yield request.param
+    _lib.set_codec_path(0)
+
+
 def dev(a):
     return torch.from_numpy(np.ascontiguousarray(a)).cuda()
 
@@ -58,7 +68,7 @@ def test_coords_roundtrip(ca):
 
 
 @pytest.mark.parametrize("name,q,M,beta", CODEC_CASES)
-def test_codec_golden(ca, golden, name, q, M, beta):
+def test_codec_golden(ca, golden, path, name, q, M, beta):
     C = golden("codec")
     x = C[name + "_x"]
     cfg = ca.LatticeConfig(lattice_type="E8", q=q, M=M, beta=beta)
@@ -88,7 +98,7 @@ def test_quantize_golden(ca, golden):
 
 
 @pytest.mark.parametrize("q", [2, 3, 4])
-def test_exhaustive_single_level_decode(ca, golden, q):
+def test_exhaustive_single_level_decode(ca, golden, path, q):
     R = golden("residual_tables")
     words = torch.arange(q ** 8, dtype=torch.int64).to(ca.word_dtype(q)).cuda().reshape(-1, 1)
     r = ca.hnlq_decode(words, q, 1, 1.0)
@@ -103,10 +113,10 @@ def test_q16_decode_sample(ca, golden):
 
 
 @pytest.mark.parametrize("n", [0, 1, 2, 255, 257, 1000])
-def test_ragged_sizes(ca, n):
+def test_ragged_sizes(ca, path, n):
     rng = np.random.default_rng(n)
     x = rng.standard_normal((n, 8)).astype(np.float32)
-    for q, M in ((4, 2), (3, 2)):
+    for q, M in ((4, 2), (3, 2), (4, 4), (2, 3)):
         pk, out = ca.hnlq_roundtrip(dev(x), q, M, 1.0)
         codes = O.e8_encode(x, q, M)
         np.testing.assert_array_equal(words(pk).reshape(n, M),
@@ -114,13 +124,13 @@ def test_ragged_sizes(ca, n):
         np.testing.assert_array_equal(host(out).reshape(n, 8), O.e8_decode(codes, q, M).reshape(n, 8))
 
 
-def test_layer_convention_matches_oracle(ca):
+def test_layer_convention_matches_oracle(ca, path):
     """W*beta_row -> quantize -> /beta_row -> clamp (coset/core/layers.py:431-463)."""
     rng = np.random.default_rng(11)
     rows, cols = 48, 256
     W = rng.standard_normal((rows, cols)).astype(np.float32)
     beta = rng.uniform(0.2, 3.0, size=rows).astype(np.float32)
-    for q, M, clip in ((4, 2, 2.0), (16, 3, 2.0), (4, 2, 0.3)):
+    for q, M, clip in ((4, 2, 2.0), (16, 3, 2.0), (4, 2, 0.3), (4, 1, 2.0), (4, 3, 1.0), (2, 4, 2.0)):
         Wq, qraw, codes = O.layer_quant(W, beta, q, M, clip)
         pk, out = ca.hnlq_roundtrip(dev(W), q, M, beta_row=dev(beta), blocks_per_row=cols // 8,
                                     clip=clip)
@@ -183,7 +193,7 @@ def test_errors(ca):
                      ca.LatticeConfig(lattice_type="E8", q=17, M=2))
 
 
-def test_full_size_c2_properties(ca):
+def test_full_size_c2_properties(ca, path):
     """BASELINE C2 at full size (2^24 blocks, q4 M2, beta 1): a random sample
     of blocks against the oracle, and the fused pass equal to encode then
     decode as separate kernels."""
