@@ -17,10 +17,24 @@ from .codecs import (
     word_dtype,
 )
 
+from .layers import (
+    E8WeightQuant,
+    HNLQConfig,
+    HNLQLinear,
+    HNLQLinearQAT,
+    LSQActivation,
+    StraightThroughQuantize,
+    create_e8_hnlq_linear,
+    get_generators,
+    ste_quantize,
+)
+
 __version__ = "0.1.0"
 
 __all__ = [
     "E8Lattice", "LatticeConfig", "Lattice", "LegacyE8Lattice",
     "e8_encode", "e8_decode", "e8_quantize", "E8Decoder", "DecodingMethod",
     "hnlq_encode", "hnlq_decode", "hnlq_roundtrip", "word_dtype",
+    "HNLQLinear", "HNLQLinearQAT", "HNLQConfig", "LSQActivation", "StraightThroughQuantize",
+    "E8WeightQuant", "create_e8_hnlq_linear", "get_generators", "ste_quantize",
 ]

@@ -36,6 +36,9 @@ SIGNATURES = {
     "coset_e8_hnlq_roundtrip": [_vp, _int, _i64, _int, _flt, _vp, _i64, _flt, _vp, _i64,
                                 _int, _int, _int, _vp, _vp, _vp, _int, _vp],
     "coset_e8_lattice_op": [_int, _int, _vp, _i64, _int, _vp, _vp],
+    "coset_e8_qat_fwd": [_vp, _i64, _i64, _vp, _i64, _flt, _int, _int, _vp, _int, _vp, _vp],
+    "coset_e8_qat_bwd": [_vp, _int, _vp, _vp, _vp, _i64, _i64, _i64, _flt, _int, _int, _vp, _vp,
+                         _vp],
     "coset_init": [_int],
     "coset_set_option": [_int, _int],
 }

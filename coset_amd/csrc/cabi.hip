@@ -195,6 +195,37 @@ int coset_e8_hnlq_roundtrip(const void* x, int x_dtype, int64_t n_blocks, int sc
                         nullptr, packed, codes_f32, out, out_dtype, stream);
 }
 
+int coset_e8_qat_fwd(const float* W, int64_t rows, int64_t cols, const float* beta,
+                     int64_t blocks_per_tile, float clip, int q, int M, void* Wq, int wq_dtype,
+                     void* packed, void* stream)
+{
+    if (rows < 0 || cols < 0 || cols % 8) return fail(COSET_EINVAL, "W must be [rows, 8k] (got %lld x %lld)",
+                                                      (long long)rows, (long long)cols);
+    int64_t n = rows * (cols / 8);
+    if (n > 0 && !Wq && !packed) return fail(COSET_EINVAL, "nothing to write");
+    return codec_common(coset::MODE_ROUNDTRIP, W, COSET_F32, n, COSET_SCALE_LAYER, 1.f, beta,
+                        blocks_per_tile, clip, nullptr, 0, q, M, n > 1, nullptr, nullptr, packed,
+                        nullptr, Wq, wq_dtype, stream);
+}
+
+int coset_e8_qat_bwd(const void* gWq, int g_dtype, const float* W, const void* packed,
+                     const float* beta, int64_t rows, int64_t cols, int64_t blocks_per_tile,
+                     float clip, int q, int M, float* dW, float* dbeta, void* stream)
+{
+    int rc;
+    if (rows < 0 || cols < 0 || cols % 8) return fail(COSET_EINVAL, "W must be [rows, 8k]");
+    int64_t n = rows * (cols / 8);
+    if ((rc = check_qm(q, M))) return rc;
+    if ((rc = check_dtype(g_dtype, "gradient"))) return rc;
+    if (blocks_per_tile <= 0 || n % blocks_per_tile) return fail(COSET_EINVAL, "blocks_per_tile must divide the block count");
+    if (n > 0 && (!gWq || !W || !packed || !beta || !dW || !dbeta)) return fail(COSET_EINVAL, "NULL buffer");
+    if (!aligned(gWq, 16) || !aligned(W, 16) || !aligned(dW, 16)) return fail(COSET_EINVAL, "g, W, dW must be 16-byte aligned");
+    if (!(clip >= 0.f)) return fail(COSET_EINVAL, "clip must be >= 0");
+    if (n / blocks_per_tile > 0x7fffffff) return fail(COSET_EINVAL, "too many tiles");
+    return check_hip(coset::launch_qat_bwd(gWq, g_dtype, W, packed, beta, n, blocks_per_tile, clip, q, M,
+                                           dW, dbeta, (hipStream_t)stream), "qat backward launch");
+}
+
 int coset_e8_lattice_op(int op, int legacy, const float* in, int64_t n_blocks, int q,
                         float* out, void* stream)
 {

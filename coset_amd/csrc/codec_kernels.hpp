@@ -54,6 +54,11 @@ hipError_t launch_codec_lut(const CodecArgs& a, int mode, hipStream_t s);
 extern int g_codec_path;
 constexpr int64_t kLutMinBlocks = 1 << 16;
 
+// Backward of the QAT weight quantizer (qat.hip).
+hipError_t launch_qat_bwd(const void* g, int g_dtype, const float* W, const void* packed,
+                          const float* beta, int64_t n_blocks, int64_t blocks_per_tile, float clip,
+                          int q, int M, float* dW, float* dbeta, hipStream_t s);
+
 // Elementwise lattice operators (custom_round, g_x, projection,
 // encode_coords, decode_coords) over n blocks.
 enum LatticeOp {

@@ -1,0 +1,481 @@
+"""QAT layer with the reference interface on the MI355X kernels.
+
+Mirrors coset/core/layers.py (StraightThroughQuantize 62-95, ste_quantize
+98-110, LSQActivation 117-137, HNLQConfig 141-163, HNLQLinearQAT 166-658,
+HNLQLinear 662) and the factory coset/core/e8/layers.py:15-66.
+
+When the injected ``quantize_fn`` is this package's ``e8_quantize`` (what the
+factory injects), the weight path scale -> STE quantize -> unscale -> clamp
+runs as one HIP kernel forward (coset_e8_qat_fwd) and one backward
+(coset_e8_qat_bwd) that re-decodes the saved packed codes; the dense
+products go to hipBLASLt through F.linear.  Any other injected quantizer
+runs the reference composition around it.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Any, Dict, List, Optional, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _lib
+from .codecs import e8_quantize, word_dtype
+from .lattice import E8Lattice, default_device
+
+
+def ste_round(x):
+    """Straight-through rounding (coset/core/layers.py:20-22)."""
+    return (x - x.detach()) + torch.round(x).detach()
+
+
+def ste_clip(x, min_val, max_val):
+    """Straight-through clipping (coset/core/layers.py:24-26)."""
+    return (x - x.detach()) + torch.clamp(x, min_val, max_val).detach()
+
+
+def get_generators(lattice) -> Tuple[torch.Tensor, torch.Tensor]:
+    """coset/core/layers.py:29-52."""
+    return lattice.get_generators()
+
+
+class StraightThroughQuantize(torch.autograd.Function):
+    """Forward quantizes with the injected function, backward is the identity
+    (coset/core/layers.py:62-95)."""
+
+    @staticmethod
+    def forward(ctx, x, quantize_fn, q):
+        ctx.quantize_fn = quantize_fn
+        ctx.q = q
+        return quantize_fn(x, q=q)
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        return grad_output, None, None
+
+
+def ste_quantize(x, quantize_fn, q):
+    """coset/core/layers.py:98-110."""
+    return StraightThroughQuantize.apply(x, quantize_fn, q)
+
+
+class LSQActivation(nn.Module):
+    """Learnable per-tensor symmetric activation quantizer
+    (coset/core/layers.py:117-137)."""
+
+    def __init__(self, bit_width: int = 8, init_alpha: float = 1.0):
+        super().__init__()
+        self.bit_width = bit_width
+        self.qmax = 2 ** (bit_width - 1) - 1
+        self.alpha = nn.Parameter(torch.tensor(init_alpha))
+
+    def forward(self, x):
+        alpha = torch.relu(self.alpha) + 1e-8
+        x_clipped = ste_clip(x, -alpha, alpha)
+        scale = alpha / self.qmax
+        y = x_clipped / scale
+        yq = ste_round(y)
+        return yq * scale
+
+
+@dataclass
+class HNLQConfig:
+    """coset/core/layers.py:141-163 (kept for API parity; the layer takes
+    keyword arguments)."""
+    q: int = 4
+    M: int = 2
+    Delta0: float = 1.5
+    eta: float = 0.1
+    k: int = 1
+    tiling: str = "row"
+    block_size: int = 8
+    quantize_activations: bool = False
+    act_bit_width: int = 8
+    act_init_alpha: float = 1.0
+    init_method: str = "normal"
+    init_kwargs: Dict[str, Any] = None
+
+    def __post_init__(self):
+        if self.init_kwargs is None:
+            self.init_kwargs = {}
+        if self.tiling not in ["row", "block"]:
+            raise ValueError(f"tiling must be 'row' or 'block', got {self.tiling}")
+        if self.block_size <= 0:
+            raise ValueError(f"block_size must be positive, got {self.block_size}")
+
+
+class E8WeightQuant(torch.autograd.Function):
+    """W -> clamp(Q(W * beta_t) / beta_t, +-clip) with the straight-through
+    gradient, on the HIP kernels.  beta has one entry per tile of
+    ``blocks_per_tile`` 8-wide blocks (row tiling: one per output row)."""
+
+    @staticmethod
+    def forward(ctx, W, beta, q, M, clip, blocks_per_tile, out_dtype):
+        Wc = W.detach().contiguous()
+        if Wc.dtype != torch.float32:
+            raise ValueError("HNLQ weights must be float32")
+        b = beta.detach().contiguous()
+        rows, cols = Wc.shape
+        n = rows * (cols // 8)
+        Wq = torch.empty((rows, cols), dtype=out_dtype, device=Wc.device)
+        packed = torch.empty((n, M), dtype=word_dtype(q), device=Wc.device)
+        _lib.call("coset_e8_qat_fwd", _lib.ptr(Wc), rows, cols, _lib.ptr(b), int(blocks_per_tile),
+                  float(clip), int(q), int(M), _lib.ptr(Wq), _lib.dtype_code(out_dtype),
+                  _lib.ptr(packed), _lib.stream_of(Wc))
+        ctx.save_for_backward(Wc, b, packed)
+        ctx.cfg = (q, M, float(clip), int(blocks_per_tile), beta.shape)
+        return Wq
+
+    @staticmethod
+    def backward(ctx, g):
+        Wc, b, packed = ctx.saved_tensors
+        q, M, clip, bpt, beta_shape = ctx.cfg
+        if g.dtype not in (torch.float32, torch.bfloat16):
+            g = g.float()
+        g = g.contiguous()
+        rows, cols = Wc.shape
+        dW = torch.empty_like(Wc)
+        dbeta = torch.empty(b.numel(), dtype=torch.float32, device=Wc.device)
+        _lib.call("coset_e8_qat_bwd", _lib.ptr(g), _lib.dtype_code(g.dtype), _lib.ptr(Wc),
+                  _lib.ptr(packed), _lib.ptr(b), rows, cols, bpt, clip, int(q), int(M),
+                  _lib.ptr(dW), _lib.ptr(dbeta), _lib.stream_of(Wc))
+        return dW, dbeta.view(beta_shape), None, None, None, None, None
+
+
+class HNLQLinearQAT(nn.Module):
+    """Hierarchical nested-lattice quantized linear layer with QAT cold start
+    (coset/core/layers.py:166-658); same constructor, buffers, state_dict
+    keys and methods."""
+
+    def __init__(self, in_features: int, out_features: int, lattice, quantize_fn, q: int = 4, M: int = 2,
+                 Delta0: Optional[float] = None, eta: float = 0.1, tiling: str = "row", block_size: int = 8,
+                 quantize_activations: bool = False, act_bit_width: int = 8, act_init_alpha: float = 1.0,
+                 init_method: str = "normal", init_kwargs: Optional[Dict[str, Any]] = None, bias: bool = True,
+                 warmup_epochs: int = 0, enable_diagnostics: bool = False, weight_clip_value: float = 2.0,
+                 theta_trainable: bool = True, theta_init_value: float = 0.0, rho: float = 0.95):
+        super().__init__()
+        self.in_features = in_features
+        self.out_features = out_features
+        self.quantize_fn = quantize_fn
+        self.lattice = lattice
+        self.lattice_type = lattice.name
+        self.q = q
+        self.M = M
+        self.eta = eta
+        self.tiling = tiling
+        self.block_size = block_size
+        self.quantize_activations = quantize_activations
+        self.init_method = init_method
+        self.init_kwargs = init_kwargs or {}
+        self.theta_trainable = theta_trainable
+        self.theta_init_value = theta_init_value
+        self.rho = rho
+        self.Delta0 = lattice.compute_delta0(q, M, rho) if Delta0 is None else Delta0
+
+        device = lattice.G.device
+        G, Ginv = lattice.get_generators()
+        self.register_buffer("G", G)
+        self.register_buffer("Ginv", Ginv)
+
+        self.blocks_per_row = in_features // block_size
+        if in_features % block_size != 0:
+            raise ValueError(f"Input dimension {in_features} must be divisible by block_size {block_size}")
+
+        self.weight = nn.Parameter(torch.empty(out_features, in_features, device=device))
+        self._initialize_weights()
+        if bias:
+            self.bias = nn.Parameter(torch.zeros(out_features, device=device))
+        else:
+            self.register_parameter("bias", None)
+
+        tiles = out_features if tiling == "row" else out_features * (in_features // block_size)
+        theta0 = torch.full((tiles,), theta_init_value, device=device)
+        if theta_trainable:
+            self.theta_beta = nn.Parameter(theta0)
+        else:
+            self.register_buffer("theta_beta", theta0)
+        self.register_buffer("sigma_ema", torch.ones(tiles, device=device))
+        self.register_buffer("xmax_ema", torch.ones(tiles, device=device))
+        self.ema_momentum = 0.99
+        self.stat_update_interval = 256
+        self.register_buffer("step_count", torch.tensor(0, dtype=torch.long, device=device))
+        self.register_buffer("gamma_inv", Ginv.abs().sum(dim=1).max())
+        # host mirrors of buffers the forward reads every step (no device sync)
+        self._host_step: Optional[int] = None
+        self._ginv_f: float = float(self.gamma_inv)
+
+        self.actq = LSQActivation(bit_width=act_bit_width, init_alpha=act_init_alpha) if quantize_activations else None
+        self.warmup_epochs = warmup_epochs
+        self.current_epoch = 0
+        self.quantization_enabled = warmup_epochs == 0
+        self.enable_diagnostics = enable_diagnostics
+        self.weight_clip_value = weight_clip_value
+        self._weight_history = [] if enable_diagnostics else None
+        self._quantization_errors = [] if enable_diagnostics else None
+
+    # ------------------------------------------------------------------
+    def _initialize_weights(self):
+        """coset/core/layers.py:314-330 (normal_ with no kwargs is N(0, 1))."""
+        m = self.init_method
+        if m == "normal":
+            nn.init.normal_(self.weight, **self.init_kwargs)
+        elif m == "xavier":
+            nn.init.xavier_normal_(self.weight, **self.init_kwargs)
+        elif m == "kaiming":
+            nn.init.kaiming_normal_(self.weight, **self.init_kwargs)
+        elif m == "zeros":
+            nn.init.zeros_(self.weight)
+        elif m == "ones":
+            nn.init.ones_(self.weight)
+        elif m == "load":
+            pass
+        else:
+            raise ValueError(f"Unknown init_method: {m}")
+
+    def load_weights(self, weight: torch.Tensor, bias: Optional[torch.Tensor] = None):
+        if weight.shape != (self.out_features, self.in_features):
+            raise ValueError(f"Weight shape {weight.shape} doesn't match expected {(self.out_features, self.in_features)}")
+        self.weight.data = weight.clone().to(self.weight.device, self.weight.dtype)
+        if bias is not None:
+            if self.bias is None:
+                raise ValueError("Cannot load bias: layer was initialized with bias=False")
+            if bias.shape != (self.out_features,):
+                raise ValueError(f"Bias shape {bias.shape} doesn't match expected {(self.out_features,)}")
+            self.bias.data = bias.clone().to(self.bias.device, self.bias.dtype)
+
+    def load_from_linear(self, linear_layer: nn.Linear):
+        if linear_layer.in_features != self.in_features:
+            raise ValueError(f"Input features mismatch: {linear_layer.in_features} vs {self.in_features}")
+        if linear_layer.out_features != self.out_features:
+            raise ValueError(f"Output features mismatch: {linear_layer.out_features} vs {self.out_features}")
+        self.load_weights(linear_layer.weight.data,
+                          linear_layer.bias.data if linear_layer.bias is not None else None)
+
+    def _load_from_state_dict(self, *args, **kwargs):
+        super()._load_from_state_dict(*args, **kwargs)
+        self._host_step = None
+        self._ginv_f = float(self.gamma_inv)
+
+    # ------------------------------------------------------------------
+    def _gather_stats(self, W_blocks):
+        """EMA of the unscaled weights' std and abs-max (layers.py:366-379)."""
+        with torch.no_grad():
+            m = self.ema_momentum
+            if self.tiling == "row":
+                sigma = W_blocks.std(dim=(1, 2)) + 1e-8
+                xmax = W_blocks.abs().amax(dim=(1, 2)) + 1e-8
+                self.sigma_ema[: self.out_features].mul_(m).add_((1 - m) * sigma)
+                self.xmax_ema[: self.out_features].mul_(m).add_((1 - m) * xmax)
+            else:
+                sigma = W_blocks.std(dim=2).reshape(-1) + 1e-8
+                xmax = W_blocks.abs().amax(dim=2).reshape(-1) + 1e-8
+                self.sigma_ema.mul_(m).add_((1 - m) * sigma)
+                self.xmax_ema.mul_(m).add_((1 - m) * xmax)
+
+    def _bounds(self):
+        """Adaptive beta bounds from the EMA statistics (layers.py:381-396)."""
+        qM = float(self.q ** self.M)
+        ginv = self._ginv_f
+        beta_min = (self.Delta0 / qM) / (self.eta * ginv * self.sigma_ema)
+        beta_max_det = (self.Delta0 * (qM - 1)) / (2 * ginv * self.xmax_ema)
+        beta_max_prob = (self.Delta0 * (qM - 1)) / (2 * self.eta * ginv * self.sigma_ema)
+        beta_max = torch.minimum(beta_max_det, beta_max_prob)
+        beta_min = torch.minimum(beta_min, beta_max * 0.9)
+        return beta_min, beta_max
+
+    def _advance_step(self):
+        """step_count += 1 and the every-256-steps statistics update
+        (layers.py:408-413), with the counter mirrored on the host."""
+        if self._host_step is None:
+            self._host_step = int(self.step_count)
+        self._host_step += 1
+        with torch.no_grad():
+            self.step_count += 1
+        if self._host_step % self.stat_update_interval == 0:
+            W = self.weight.view(self.out_features, self.blocks_per_row, self.block_size)
+            self._gather_stats(W.detach())
+
+    def _beta(self):
+        beta_min, beta_max = self._bounds()
+        if self.tiling == "row":
+            theta = self.theta_beta[: self.out_features]
+            return beta_min[: self.out_features] + torch.sigmoid(theta) * (
+                beta_max[: self.out_features] - beta_min[: self.out_features])
+        return beta_min + torch.sigmoid(self.theta_beta) * (beta_max - beta_min)
+
+    def _fused(self) -> bool:
+        return (self.quantize_fn is e8_quantize and self.block_size == 8
+                and self.lattice_type == "E8" and self.weight.is_cuda)
+
+    def _quantize_weights_as(self, out_dtype: torch.dtype):
+        W = self.weight
+        if not self.quantization_enabled:
+            if self.enable_diagnostics:
+                self._weight_history.append(W.detach().clone())
+            return W
+        self._advance_step()
+        beta = self._beta()
+        if self._fused():
+            bpt = self.blocks_per_row if self.tiling == "row" else 1
+            # the injected e8_quantize always encodes with M = 2 (codecs.py:245-254)
+            W_q = E8WeightQuant.apply(W, beta, self.q, 2, self.weight_clip_value, bpt, out_dtype)
+        else:
+            W_q = self._reference_composition(W, beta).to(out_dtype)
+        if self.enable_diagnostics:
+            self._weight_history.append(W.detach().clone())
+            self._quantization_errors.append(torch.norm(W - W_q.float()).item())
+        return W_q
+
+    def _reference_composition(self, W, beta):
+        """layers.py:428-463 around an arbitrary injected quantize_fn."""
+        if self.tiling == "row":
+            beta = beta.view(-1, 1)
+            W_scaled = W * beta
+        else:
+            beta = beta.view(self.out_features, self.blocks_per_row, 1)
+            W_scaled = (W.view(self.out_features, self.blocks_per_row, self.block_size) * beta).reshape(
+                self.out_features, self.in_features)
+        flat = W_scaled.view(self.out_features, self.blocks_per_row, self.block_size).reshape(-1, self.block_size)
+        Wq = ste_quantize(flat, self.quantize_fn, self.q).reshape(self.out_features, self.in_features)
+        Wq = Wq / (beta if self.tiling == "row" else beta.reshape(self.out_features, -1).repeat_interleave(
+            self.block_size, dim=1))
+        return torch.clamp(Wq, -self.weight_clip_value, self.weight_clip_value)
+
+    def _quantize_weights(self):
+        """coset/core/layers.py:398-470 (fp32 W_q)."""
+        return self._quantize_weights_as(torch.float32)
+
+    def forward(self, x):
+        """F.linear(x, W_q, bias) (layers.py:472-484); W_q is produced in the
+        activation dtype (float32 or bfloat16) for the GEMM."""
+        wdt = x.dtype if x.dtype in (torch.bfloat16, torch.float16) else torch.float32
+        if wdt == torch.float16:
+            wdt = torch.float32
+        W_q = self._quantize_weights_as(wdt)
+        if W_q.dtype != x.dtype:
+            W_q = W_q.to(x.dtype)
+        b = self.bias.to(x.dtype) if self.bias is not None else None
+        x = F.linear(x, W_q, b)
+        if self.quantize_activations and self.actq is not None:
+            x = self.actq(x)
+        return x
+
+    # cold start control (layers.py:487-506)
+    def update_epoch(self, epoch: int):
+        self.current_epoch = epoch
+        if epoch >= self.warmup_epochs and not self.quantization_enabled:
+            self.quantization_enabled = True
+            print(f"Epoch {epoch}: Enabling quantization (warmup complete)")
+
+    def enable_quantization(self):
+        self.quantization_enabled = True
+        print("Quantization manually enabled")
+
+    def disable_quantization(self):
+        self.quantization_enabled = False
+        print("Quantization manually disabled")
+
+    def is_quantization_enabled(self) -> bool:
+        return self.quantization_enabled
+
+    # diagnostics (layers.py:509-618)
+    def get_weight_quantiles(self, quantiles: List[float] = None) -> torch.Tensor:
+        if quantiles is None:
+            quantiles = [0.0, 0.1, 0.2, 0.3, 0.4, 0.5, 0.6, 0.7, 0.8, 0.9, 1.0]
+        W = self.weight.detach().flatten()
+        return torch.quantile(W, torch.tensor(quantiles, device=W.device))
+
+    def get_weight_statistics(self) -> Dict[str, float]:
+        W = self.weight.detach()
+        return {"mean": W.mean().item(), "std": W.std().item(), "min": W.min().item(), "max": W.max().item(),
+                "median": W.median().item(), "l2_norm": torch.norm(W).item(), "l1_norm": torch.norm(W, p=1).item()}
+
+    def get_quantization_error(self) -> float:
+        if not self.quantization_enabled:
+            return 0.0
+        return torch.norm(self.weight.detach() - self._quantize_weights().detach()).item()
+
+    def get_scaling_factors(self) -> torch.Tensor:
+        return self.theta_beta.detach()
+
+    def get_quantization_histogram(self, bins: int = 50):
+        W = self.weight.detach() if not self.quantization_enabled else self._quantize_weights().detach()
+        return torch.histogram(W.flatten().cpu(), bins=bins)
+
+    def get_sparsity_ratio(self, threshold: float = 1e-6) -> float:
+        return (self.weight.detach().abs() < threshold).float().mean().item()
+
+    def get_effective_bits(self) -> float:
+        if not self.quantization_enabled:
+            return 32.0
+        u = torch.unique(self._quantize_weights().detach())
+        return torch.log2(torch.tensor(len(u), dtype=torch.float32)).item()
+
+    def compare_weights(self) -> Dict[str, float]:
+        if not self.quantization_enabled:
+            return {"error": 0.0, "relative_error": 0.0, "cosine_similarity": 1.0}
+        W = self.weight.detach()
+        Wq = self._quantize_weights().detach()
+        err = torch.norm(W - Wq).item()
+        return {"error": err, "relative_error": err / torch.norm(W).item(),
+                "cosine_similarity": F.cosine_similarity(W.flatten(), Wq.flatten(), dim=0).item()}
+
+    def get_weight_clipping_stats(self) -> Dict[str, float]:
+        W = self.weight.detach()
+        clipped = torch.sum((W.abs() > self.weight_clip_value).float()).item()
+        return {"clipping_ratio": clipped / W.numel(), "clipped_count": clipped, "total_count": W.numel(),
+                "clip_value": self.weight_clip_value, "max_weight": W.abs().max().item()}
+
+    def get_diagnostic_summary(self) -> Dict[str, Any]:
+        s = {"epoch": self.current_epoch, "quantization_enabled": self.quantization_enabled,
+             "warmup_epochs": self.warmup_epochs, "weight_stats": self.get_weight_statistics(),
+             "quantization_error": self.get_quantization_error(), "effective_bits": self.get_effective_bits(),
+             "sparsity_ratio": self.get_sparsity_ratio(), "weight_clipping": self.get_weight_clipping_stats()}
+        if self.quantization_enabled:
+            s["weight_comparison"] = self.compare_weights()
+        return s
+
+    def export_quantized(self):
+        """layers.py:620-650, plus the packed level words and per-tile beta
+        of the same quantization (keys 'codes', 'beta')."""
+        with torch.no_grad():
+            W_q = self._quantize_weights()
+            metadata = {"lattice_type": self.lattice_type, "q": self.q, "M": self.M, "Delta0": self.Delta0,
+                        "tiling": self.tiling, "block_size": self.block_size,
+                        "quantize_activations": self.quantize_activations}
+            if self.quantize_activations and self.actq is not None:
+                metadata.update({"act_bit_width": self.actq.bit_width, "act_alpha": self.actq.alpha.item()})
+            out = {"weight": W_q, "bias": self.bias, "metadata": metadata}
+            if self._fused():
+                beta = self._beta().detach()
+                from .codecs import hnlq_encode
+                bpt = self.blocks_per_row if self.tiling == "row" else 1
+                out["codes"] = hnlq_encode(self.weight.detach(), self.q, 2, beta_row=beta, blocks_per_row=bpt)
+                out["beta"] = beta
+            return out
+
+    def extra_repr(self):
+        return (f"in_features={self.in_features}, out_features={self.out_features}, "
+                f"lattice_type={self.lattice_type}, q={self.q}, M={self.M}, "
+                f"Delta0={self.Delta0:.4f}, tiling={self.tiling}, block_size={self.block_size}, "
+                f"quantize_activations={self.quantize_activations}, bias={self.bias is not None}, "
+                f"theta_trainable={self.theta_trainable}, theta_init_value={self.theta_init_value}, "
+                f"rho={self.rho}")
+
+
+HNLQLinear = HNLQLinearQAT
+
+
+def create_e8_hnlq_linear(in_dim, out_dim, device=None, **kwargs):
+    """coset/core/e8/layers.py:15-66 with this package's e8_quantize
+    injected.  device defaults to the GPU when one is visible."""
+    if in_dim % 8 != 0:
+        raise ValueError(f"Input dimension {in_dim} must be divisible by 8 for E8 lattice")
+    device = default_device(device)
+    lattice = E8Lattice(device=device)
+    defaults = {"lattice": lattice, "quantize_fn": e8_quantize, "block_size": 8, "q": 4, "M": 2,
+                "Delta0": None, "warmup_epochs": 0, "enable_diagnostics": False, "weight_clip_value": 2.0,
+                "theta_trainable": True, "theta_init_value": 0.0, "rho": 0.95}
+    defaults.update(kwargs)
+    return HNLQLinearQAT(in_dim, out_dim, **defaults)

@@ -114,6 +114,27 @@ int coset_e8_hnlq_roundtrip(const void* x, int x_dtype, int64_t n_blocks,
                             void* packed, float* codes_f32, void* out, int out_dtype,
                             void* stream);
 
+/* QAT weight quantizer forward (coset/core/layers.py:428-463 with the
+ * injected e8_quantize, codecs.py:221-286):
+ *   Wq = clamp(dec(enc(W * beta_t)) / beta_t, -clip, clip)
+ * W fp32 [rows, cols] (cols % 8 == 0), beta_t = beta[block / blocks_per_tile]
+ * (blocks_per_tile = cols/8 for row tiling, 1 for block tiling).  Writes Wq
+ * (fp32 or bf16, nullable) and the packed level words (nullable) that
+ * coset_e8_qat_bwd re-decodes. */
+int coset_e8_qat_fwd(const float* W, int64_t rows, int64_t cols, const float* beta,
+                     int64_t blocks_per_tile, float clip, int q, int M, void* Wq, int wq_dtype,
+                     void* packed, void* stream);
+
+/* QAT weight quantizer backward through the straight-through estimator
+ * (StraightThroughQuantize.backward, coset/core/layers.py:86-95, and the
+ * autograd of layers.py:431-463): from g = dL/dWq (fp32 or bf16) writes
+ *   dW    = ((g*m)/beta)*beta,   m = (-clip <= Q/beta <= clip)
+ *   dbeta[t] = sum_t ((g*m)/beta)*W - (g*m)*((Q/beta)/beta)
+ * with Q re-decoded from `packed`.  dbeta has one entry per tile. */
+int coset_e8_qat_bwd(const void* gWq, int g_dtype, const float* W, const void* packed,
+                     const float* beta, int64_t rows, int64_t cols, int64_t blocks_per_tile,
+                     float clip, int q, int M, float* dW, float* dbeta, void* stream);
+
 /* Elementwise lattice operator over n_blocks fp32 blocks (custom_round is
  * applied to all 8*n_blocks values).  legacy selects the legacy g_x rule. */
 int coset_e8_lattice_op(int op, int legacy, const float* in, int64_t n_blocks, int q,
