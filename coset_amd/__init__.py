@@ -29,6 +29,18 @@ from .layers import (
     ste_quantize,
 )
 
+from .vlut import (
+    QuantizationConfig,
+    _encoding_to_index,
+    build_one_sided_vluts,
+    build_vlut,
+    vLUTManager,
+    vlut_accumulate_operation,
+    vlut_dot,
+    vlut_mac_operation,
+    vlut_matmul,
+)
+
 __version__ = "0.1.0"
 
 __all__ = [
@@ -37,4 +49,6 @@ __all__ = [
     "hnlq_encode", "hnlq_decode", "hnlq_roundtrip", "word_dtype",
     "HNLQLinear", "HNLQLinearQAT", "HNLQConfig", "LSQActivation", "StraightThroughQuantize",
     "E8WeightQuant", "create_e8_hnlq_linear", "get_generators", "ste_quantize",
+    "vLUTManager", "QuantizationConfig", "build_vlut", "_encoding_to_index", "vlut_mac_operation",
+    "vlut_accumulate_operation", "build_one_sided_vluts", "vlut_dot", "vlut_matmul",
 ]

@@ -39,6 +39,10 @@ SIGNATURES = {
     "coset_e8_qat_fwd": [_vp, _i64, _i64, _vp, _i64, _flt, _int, _int, _vp, _int, _vp, _vp],
     "coset_e8_qat_bwd": [_vp, _int, _vp, _vp, _vp, _i64, _i64, _i64, _flt, _int, _int, _vp, _vp,
                          _vp],
+    "coset_vlut_build_one_sided": [_vp, _i64, _int, _int, _vp, _vp],
+    "coset_vlut_lookup_dot": [_vp, _i64, _int, _int, _vp, _vp, _vp],
+    "coset_vlut_matmul": [_vp, _vp, _int, _vp, _int, _i64, _i64, _i64, _int, _int, _int, _int, _vp, _i64,
+                          _vp, _vp],
     "coset_init": [_int],
     "coset_set_option": [_int, _int],
 }
@@ -65,6 +69,8 @@ def load():
     lib.coset_last_error.restype = ctypes.c_char_p
     lib.coset_word_bytes.argtypes = [_int]
     lib.coset_word_bytes.restype = _int
+    lib.coset_vlut_workspace_floats.argtypes = [_i64, _i64, _i64, _int, _int, _int, _int]
+    lib.coset_vlut_workspace_floats.restype = _i64
     for name, args in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.argtypes = args
@@ -125,4 +131,6 @@ def dtype_code(dt: torch.dtype) -> int:
         return F32
     if dt == torch.bfloat16:
         return BF16
+    if dt == torch.float16:
+        return F16
     raise ValueError(f"unsupported dtype {dt} (float32 or bfloat16)")

@@ -11,6 +11,7 @@
 #include "../../include/coset_amd.h"
 #include "codec_kernels.hpp"
 #include "tables.hpp"
+#include "vlut.hpp"
 
 namespace {
 
@@ -101,7 +102,7 @@ int coset_init(int device)
             const coset::DecodeTables* t = nullptr;
             if (rc == COSET_OK) rc = check_hip(coset::get_decode_tables(q, legacy, &t), "decode tables");
         }
-    if (device >= 0 && device != cur) hipSetDevice(cur);
+    if (device >= 0 && device != cur) (void)hipSetDevice(cur);
     return rc;
 }
 
@@ -224,6 +225,92 @@ int coset_e8_qat_bwd(const void* gWq, int g_dtype, const float* W, const void* p
     if (n / blocks_per_tile > 0x7fffffff) return fail(COSET_EINVAL, "too many tiles");
     return check_hip(coset::launch_qat_bwd(gWq, g_dtype, W, packed, beta, n, blocks_per_tile, clip, q, M,
                                            dW, dbeta, (hipStream_t)stream), "qat backward launch");
+}
+
+int coset_vlut_build_one_sided(const float* queries, int64_t n_queries, int q, int legacy, float* vlut,
+                               void* stream)
+{
+    if (n_queries < 0) return fail(COSET_EINVAL, "n_queries < 0");
+    if (q < 2 || q > 8) return fail(COSET_EINVAL, "one-sided vLUT needs q in [2,8] (q^8 entries), got %d", q);
+    if (n_queries > 0 && (!queries || !vlut)) return fail(COSET_EINVAL, "NULL buffer");
+    int64_t n = 1;
+    for (int i = 0; i < 8; ++i) n *= q;
+    if (n_queries * n > ((int64_t)1 << 40)) return fail(COSET_EINVAL, "table too large");
+    return check_hip(coset::vlut_build(queries, n_queries, q, legacy ? 1 : 0, vlut, (hipStream_t)stream),
+                     "vLUT build launch");
+}
+
+int coset_vlut_lookup_dot(const void* words, int64_t n_blocks, int q, int M, const float* vlut, float* out,
+                          void* stream)
+{
+    int rc;
+    if ((rc = check_qm(q, M))) return rc;
+    if (q > 8) return fail(COSET_EINVAL, "one-sided vLUT needs q in [2,8]");
+    if (n_blocks < 0) return fail(COSET_EINVAL, "n_blocks < 0");
+    if (n_blocks > 0 && (!words || !vlut || !out)) return fail(COSET_EINVAL, "NULL buffer");
+    return check_hip(coset::vlut_dot(words, n_blocks, M, q, vlut, out, (hipStream_t)stream), "vLUT dot launch");
+}
+
+static int vlut_method(int method, int act_dtype, int q, int M)
+{
+    // the MFMA path multiplies 2*x_hat held exactly in fp16 (|v| < 2048)
+    // or bf16 (|v| < 256); max |2x_hat| <= 12 q^M at q <= 4
+    int64_t qm = 1;
+    for (int i = 0; i < M; ++i) qm *= q;
+    bool exact = (act_dtype == COSET_F16 && 12 * qm < 2048) || (act_dtype == COSET_BF16 && 12 * qm < 256);
+    if (method == coset::VLUT_METHOD_MFMA && !exact) return -1;
+    if (method == coset::VLUT_METHOD_AUTO) return exact ? coset::VLUT_METHOD_MFMA : coset::VLUT_METHOD_LDS;
+    return method;
+}
+
+int64_t coset_vlut_workspace_floats(int64_t B, int64_t rows, int64_t K, int q, int M, int act_dtype, int method)
+{
+    int m = vlut_method(method, act_dtype, q, M);
+    if (m < 0 || B < 0 || rows < 0 || K < 8) return 0;
+    return (int64_t)coset::vlut_default_splits(rows, B, K, m) * B * rows;
+}
+
+int coset_vlut_matmul(const void* words, const float* scale, int scale_mode, const void* act, int act_dtype,
+                      int64_t B, int64_t rows, int64_t K, int q, int M, int legacy, int method,
+                      float* workspace, int64_t workspace_floats, float* out, void* stream)
+{
+    int rc;
+    if ((rc = check_qm(q, M))) return rc;
+    if (q != 2 && q != 4) return fail(COSET_EUNSUPPORTED, "vLUT matmul supports q = 2 or 4 (got %d)", q);
+    if (M > 4) return fail(COSET_EUNSUPPORTED, "vLUT matmul supports M <= 4");
+    if (B < 0 || rows < 0 || K < 8 || K % 8) return fail(COSET_EINVAL, "bad shape B=%lld rows=%lld K=%lld",
+                                                         (long long)B, (long long)rows, (long long)K);
+    if (act_dtype != COSET_F32 && act_dtype != COSET_BF16 && act_dtype != COSET_F16)
+        return fail(COSET_EINVAL, "activation dtype %d", act_dtype);
+    if (scale_mode != 0 && scale_mode != 1) return fail(COSET_EINVAL, "scale_mode must be 0 or 1");
+    int m = vlut_method(method, act_dtype, q, M);
+    if (m < 0) return fail(COSET_EUNSUPPORTED, "MFMA method needs fp16/bf16 activations holding 2*x_hat exactly");
+    if (m != coset::VLUT_METHOD_LDS && m != coset::VLUT_METHOD_MFMA) return fail(COSET_EINVAL, "unknown method %d", method);
+    if (B == 0 || rows == 0) return COSET_OK;
+    if (!words || !act || !out || !workspace) return fail(COSET_EINVAL, "NULL buffer");
+    if (!aligned(act, 16) || !aligned(words, 4)) return fail(COSET_EINVAL, "act must be 16-byte aligned, words 4-byte");
+    int splits = coset::vlut_default_splits(rows, B, K, m);
+    if (workspace_floats < (int64_t)splits * B * rows)
+        return fail(COSET_EINVAL, "workspace holds %lld floats, needs %lld", (long long)workspace_floats,
+                    (long long)splits * B * rows);
+    coset::VlutMatmulArgs p{};
+    p.words = words;
+    p.scale = scale;
+    p.scale_mode = scale_mode;
+    p.act = act;
+    p.act_dtype = act_dtype;
+    p.B = B;
+    p.rows = rows;
+    p.K = K;
+    p.q = q;
+    p.M = M;
+    p.legacy = legacy ? 1 : 0;
+    p.partial = workspace;
+    p.out = out;
+    const coset::DecodeTables* t = nullptr;
+    if ((rc = check_hip(coset::get_decode_tables(q, p.legacy, &t), "decode tables"))) return rc;
+    if (t->n_coarse > coset::kMaxCoarseVlut) return fail(COSET_EUNSUPPORTED, "too many coarse points");
+    return check_hip(coset::vlut_matmul(p, m, splits, (hipStream_t)stream), "vLUT matmul launch");
 }
 
 int coset_e8_lattice_op(int op, int legacy, const float* in, int64_t n_blocks, int q,

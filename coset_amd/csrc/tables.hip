@@ -103,8 +103,8 @@ hipError_t build(int device, int q, int legacy, DecodeTables* out)
     if ((e = hipMemcpy((void*)out->cid_map, map.data(), n * sizeof(uint16_t), hipMemcpyHostToDevice)) != hipSuccess) goto done;
     e = hipMemcpy((void*)out->coarse, coarse.data(), coarse.size() * sizeof(uint64_t), hipMemcpyHostToDevice);
 done:
-    if (d_keys) hipFree(d_keys);
-    if (cur != device) hipSetDevice(cur);
+    if (d_keys) (void)hipFree(d_keys);
+    if (cur != device) (void)hipSetDevice(cur);
     return e;
 }
 

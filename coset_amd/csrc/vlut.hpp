@@ -1,0 +1,35 @@
+// vlut.hpp -- launch descriptors of the vLUT kernels (vlut.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace coset {
+
+constexpr int kMaxCoarseVlut = 640;  // LDS table slots for <a, c> (637 at q = 4)
+
+enum VlutMethod { VLUT_METHOD_AUTO = 0, VLUT_METHOD_LDS = 1, VLUT_METHOD_MFMA = 2 };
+
+struct VlutMatmulArgs {
+    const void* words;   // [rows, K/8, M] uint16 level words
+    const float* scale;  // [rows] or null
+    int scale_mode;      // 0: out *= scale[o]; 1: out /= scale[o]
+    const void* act;     // [B, K] fp32 / bf16 / fp16
+    int act_dtype;
+    int64_t B, rows, K;
+    int q, M, legacy;
+    float* partial;      // [splits, B, rows] workspace
+    float* out;          // [B, rows]
+    // filled by the launcher
+    const uint16_t* map;
+    const uint64_t* coarse;
+    int n_coarse;
+    int kb_per_chunk;
+};
+
+hipError_t vlut_build(const float* a, int64_t n_queries, int q, int legacy, float* vlut, hipStream_t s);
+hipError_t vlut_dot(const void* words, int64_t n, int M, int q, const float* vlut, float* out, hipStream_t s);
+int vlut_default_splits(int64_t rows, int64_t B, int64_t K, int method);
+hipError_t vlut_matmul(VlutMatmulArgs p, int method, int splits, hipStream_t s);
+
+}  // namespace coset

@@ -135,6 +135,32 @@ int coset_e8_qat_bwd(const void* gWq, int g_dtype, const float* W, const void* p
                      const float* beta, int64_t rows, int64_t cols, int64_t blocks_per_tile,
                      float clip, int q, int M, float* dW, float* dbeta, void* stream);
 
+/* One-sided vLUTs (coset/legacy/quant/vlut.py:72-117): for each query
+ * a[i, 0:8] writes vlut[i, idx] = <a, r(b_idx)> for all q^8 level words in
+ * lexicographic order, r(b) = G b - q P(G b / q).  legacy=1 uses the legacy
+ * textbook P (what vLUTManager uses), legacy=0 the core rule of e8_decode.
+ * q in [2, 8]. */
+int coset_vlut_build_one_sided(const float* queries, int64_t n_queries, int q, int legacy, float* vlut,
+                               void* stream);
+
+/* out[i] = sum_m q^m vlut[words[i, m]] (tests/legacy/test_one_sided_vlut_pytest.py:22-43). */
+int coset_vlut_lookup_dot(const void* words, int64_t n_blocks, int q, int M, const float* vlut, float* out,
+                          void* stream);
+
+/* vLUT matmul: out[t, o] = s_o * sum_k sum_m q^m vLUT_{act[t, 8k:8k+8]}[words[o, k, m]]
+ * for uint16 level words [rows, K/8, M] (q in {2, 4}, M <= 4), activations
+ * [B, K] fp32/bf16/fp16, s_o = scale[o] (scale_mode 0), 1/scale[o] (1) or 1
+ * (scale NULL).  method 1 keeps per-(token, k-block) factorized tables
+ * <a, g_j>, <a, c> in LDS; method 2 decodes 2*x_hat into LDS and runs the
+ * product on the matrix cores (fp16/bf16 activations); 0 picks 2 when it is
+ * exact.  workspace: caller-owned fp32 scratch of coset_vlut_workspace_floats.
+ * The reference has no matmul routine; its placeholder QLinear._lut_matmul is
+ * coset/legacy/nn/qlinear.py:272-281. */
+int64_t coset_vlut_workspace_floats(int64_t B, int64_t rows, int64_t K, int q, int M, int act_dtype, int method);
+int coset_vlut_matmul(const void* words, const float* scale, int scale_mode, const void* act, int act_dtype,
+                      int64_t B, int64_t rows, int64_t K, int q, int M, int legacy, int method,
+                      float* workspace, int64_t workspace_floats, float* out, void* stream);
+
 /* Elementwise lattice operator over n_blocks fp32 blocks (custom_round is
  * applied to all 8*n_blocks values).  legacy selects the legacy g_x rule. */
 int coset_e8_lattice_op(int op, int legacy, const float* in, int64_t n_blocks, int q,

@@ -1,0 +1,121 @@
+"""vLUT kernels against the reference's legacy one-sided tables
+(tests/golden/vlut_legacy.npz), the oracle, and decode-then-dot.  Table
+entries and lookup sums within 1e-6 of the table's magnitude (8-term fp32
+dot products); matmul outputs within 1e-3 of the max magnitude."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def close(a, b, tol):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    scale = max(np.abs(b).max(), 1e-30)
+    assert np.abs(a - b).max() <= tol * scale, (np.abs(a - b).max(), scale)
+
+
+@pytest.mark.parametrize("q", [3, 4])
+def test_legacy_one_sided_matches_reference(golden, q):
+    import coset_amd
+    V = golden("vlut_legacy")
+    mgr = coset_amd.vLUTManager(coset_amd.LegacyE8Lattice(), coset_amd.QuantizationConfig(lattice_type="E8", q=q, M=2))
+    for i in range(2):
+        a = torch.from_numpy(V[f"q{q}_a{i}"])
+        v = mgr.build_one_sided_vlut(a)
+        assert v.device.type == "cpu" and v.shape == (q ** 8,)
+        close(v.numpy(), V[f"q{q}_vlut{i}"], 1e-6)
+        assert mgr.build_one_sided_vlut(a) is v  # cached
+
+
+def test_core_one_sided_matches_oracle():
+    import coset_amd
+    rng = np.random.default_rng(4)
+    a = rng.standard_normal((3, 8)).astype(np.float32)
+    for q in (2, 4):
+        v = coset_amd.build_one_sided_vluts(torch.from_numpy(a), q, legacy=False).cpu().numpy()
+        for i in range(3):
+            ref = np.array([np.dot(a[i].astype(np.float64), r) for r in
+                            O.e8_decode(O.unpack_words(np.arange(q ** 8), q).reshape(-1, 1, 8), q, 1)])
+            close(v[i], ref, 1e-6)
+
+
+def test_equal_sum_queries_get_their_own_tables():
+    import coset_amd
+    mgr = coset_amd.vLUTManager(coset_amd.LegacyE8Lattice(), coset_amd.QuantizationConfig(lattice_type="E8", q=3, M=2))
+    a1 = torch.tensor([1., 0, 0, 0, 0, 0, 0, 0])
+    a2 = torch.tensor([0., 1, 0, 0, 0, 0, 0, 0])
+    assert not torch.equal(mgr.build_one_sided_vlut(a1), mgr.build_one_sided_vlut(a2))
+
+
+def test_lookup_dot_equals_decode_then_dot():
+    """tests/legacy/test_one_sided_vlut_pytest.py:294-333 on the core rule."""
+    import coset_amd
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((500, 8)).astype(np.float32)
+    a = rng.standard_normal(8).astype(np.float32)
+    words = coset_amd.hnlq_encode(torch.from_numpy(x).cuda(), 4, 2, 1.0)
+    vl = coset_amd.build_one_sided_vluts(torch.from_numpy(a).reshape(1, 8), 4, legacy=False)[0]
+    got = coset_amd.vlut_dot(words, vl, 4).cpu().numpy()
+    dec = O.e8_decode(O.e8_encode(x, 4, 2), 4, 2)
+    close(got, dec.astype(np.float64) @ a.astype(np.float64), 1e-6)
+
+
+def test_reference_helpers():
+    import coset_amd
+    enc = torch.tensor([[1, 2, 3, 0, 0, 0, 0, 1]])
+    assert int(coset_amd._encoding_to_index(enc, 4)[0]) == 4 ** 7 + 2 * 4 ** 6 + 3 * 4 ** 5 + 1
+    mgr = coset_amd.vLUTManager(coset_amd.LegacyE8Lattice(), coset_amd.QuantizationConfig(lattice_type="E8", q=2, M=2))
+    two = mgr.build_two_sided_vlut()
+    pts = mgr._decode_encodings_to_lattice_points(mgr._generate_all_encodings()).double()
+    torch.testing.assert_close(two.double(), pts @ pts.T)
+    ex = [torch.randint(0, 2, (5, 8)) for _ in range(2)]
+    ey = [torch.randint(0, 2, (5, 8)) for _ in range(2)]
+    mac = coset_amd.vlut_mac_operation(ex, ey, two)
+    ref = sum(two[coset_amd._encoding_to_index(ex[i], 2), coset_amd._encoding_to_index(ey[i], 2)] for i in range(2))
+    torch.testing.assert_close(mac, ref)
+    assert coset_amd.QuantizationConfig(lattice_type="E8", q=4, M=2).beta == 0.3
+
+
+@pytest.mark.parametrize("method", ["lds", "mfma"])
+@pytest.mark.parametrize("B", [1, 3, 8, 17, 64, 80])
+@pytest.mark.parametrize("adt", [torch.float16, torch.bfloat16, torch.float32])
+def test_vlut_matmul_vs_oracle(method, B, adt):
+    import coset_amd
+    if method == "mfma" and adt == torch.float32:
+        pytest.skip("MFMA path takes fp16/bf16 activations")
+    rng = np.random.default_rng(B)
+    rows, K, q, M = 96, 320, 4, 2
+    W = rng.standard_normal((rows, K)).astype(np.float32)
+    scale = rng.uniform(0.5, 2.0, rows).astype(np.float32)
+    codes = O.e8_encode(W.reshape(-1, 8), q, M)
+    words_np = O.pack_words(codes, q).reshape(rows, K // 8, M)
+    words = torch.from_numpy(words_np.astype(np.int32)).to(torch.uint16).cuda()
+    a = torch.from_numpy(rng.standard_normal((B, K)).astype(np.float32)).to(adt)
+    for legacy in (False, True):
+        for mode in ("mul", "div"):
+            out = coset_amd.vlut_matmul(words, a.cuda(), q, scale=torch.from_numpy(scale), scale_mode=mode,
+                                        legacy=legacy, method=method).cpu().numpy()
+            sm = 0 if mode == "mul" else 1
+            ref = O.vlut_matmul(words_np, scale, a.float().numpy(), q, M, scale_mode=sm, legacy=legacy)
+            close(out, ref, 1e-3)
+
+
+def test_c4_full_size_equals_decoded_product():
+    """C4: 4096 x 4096 weights ~ N(0, 0.02) encoded with beta = 0.02 (q4 M2),
+    fp16 activations at B = 1, 8, 64; both methods equal a @ decode^T."""
+    import coset_amd
+    g = torch.Generator(device="cuda").manual_seed(5)
+    W = 0.02 * torch.randn((4096, 4096), device="cuda", generator=g)
+    words = coset_amd.hnlq_encode(W.reshape(-1, 8), 4, 2, 0.02).reshape(4096, 512, 2)
+    dec = coset_amd.hnlq_decode(words.reshape(-1, 2), 4, 2, 0.02).reshape(4096, 4096)
+    for B in (1, 8, 64):
+        a = torch.randn((B, 4096), device="cuda", generator=g).to(torch.float16)
+        ref = (a.double() @ dec.double().T).float()
+        for method in ("lds", "mfma"):
+            out = coset_amd.vlut_matmul(words, a, 4, scale=torch.full((4096,), 0.02), method=method)
+            err = (out - ref).abs().max().item()
+            assert err <= 1e-3 * ref.abs().max().item(), (B, method, err)
