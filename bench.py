@@ -1,15 +1,20 @@
 """Benchmark of the E8 HNLQ hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2,c4,...]
 
-Workload ("C2"): 2^24 fp32 8-wide blocks ~ N(0,1)
-(seeded), fixed beta = 1, q = 4, M = 2.  One step = the fused encode -> decode
-pass over all blocks, writing packed level words (uint16 x 2 per block) and
-the decoded fp32 blocks.  Inputs are resident in HBM before timing starts.
+Headline workload ("C2"): 2^24 fp32 8-wide blocks
+~ N(0,1) (seeded), fixed beta = 1, q = 4, M = 2.  One step = the fused
+encode -> decode pass over all blocks, writing packed level words (uint16 x 2
+per block) and the decoded fp32 blocks.  Inputs are resident in HBM before
+timing starts; `value` is whole-job Gblocks/s.
 
-Prints one JSON line: whole-job Gblocks/s, the HBM roofline of the codec
-kernel (HIP events on the launch stream) and the CPU oracle timed on a
-bounded sample of the same workload on the host.
+The other BASELINE configurations are measured alongside under "extra":
+  c1  layer forward 768 -> 10 on a 32 x 768 fp32 batch (latency)
+  c3  2^22 Student-t(3) blocks clipped at +-2 in bf16, q16 M3, per-row beta
+  c4  vLUT matmul of 4096 x 4096 q4 M2 codes with fp16 activations, B = 1, 8, 64
+  c5  QAT linear forward + backward, BERT-base shapes, 4096 bf16 tokens
+The roofline object is the C2 codec kernel's (HIP events on its launch
+stream); cpu_baseline is the C oracle on the host, single thread.
 """
 from __future__ import annotations
 
@@ -25,18 +30,39 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+BF16_MFMA_TFLOPS = 2500.0      # dense
+FP16_MFMA_TFLOPS = 2500.0
 C2_BLOCKS = 1 << 24
 C2_BYTES_PER_BLOCK = 32 + 4 + 32   # read x, write 2 u16 words, write decoded
 METRIC = "E8 HNLQ encode+decode Gblocks/s & HBM GB/s; vLUT matmul tokens/s at 4096²"
 
 
 def traffic_from_profile():
-    """HBM bytes per launch measured by rocprofv3 PMC (profiles/), if recorded."""
+    """HBM bytes per launch of the C2 kernel measured with rocprofv3 PMC
+    counters (recorded in profiles/), or None."""
     p = os.path.join(ROOT, "profiles", "hnlq_roundtrip_c2_traffic.json")
     if not os.path.exists(p):
         return None
     with open(p) as f:
         return json.load(f).get("hbm_bytes_per_launch")
+
+
+def gpu_time(torch, fn, steps, warmup):
+    """Average seconds per call of fn, HIP events on the current stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(s)
+    for _ in range(steps):
+        fn()
+    e1.record(s)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return e0.elapsed_time(e1) / 1e3 / steps, wall / steps
 
 
 def cpu_baseline(x_sample: np.ndarray):
@@ -49,27 +75,13 @@ def cpu_baseline(x_sample: np.ndarray):
     dt = time.perf_counter() - t0
     n = x_sample.shape[0]
     return {"value": n / dt / 1e9, "unit": "Gblocks/s", "cores": 1, "kind": "port",
-            "sample": f"first {n} of the 2^24 C2 blocks (q4 M2 beta 1), C oracle enc+dec, "
+            "sample": f"first {n} of the 2^24 C2 blocks (q4 M2 beta 1), C oracle encode+decode, "
                       f"{dt:.1f} s on one host core"}
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--cpu-sample", type=int, default=1 << 23,
-                    help="blocks timed on the host CPU oracle (0 skips it)")
-    args = ap.parse_args()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        sys.exit("bench.py measures one GPU only: this build has no multi-GPU path "
-                 "(run with --gpus 1)")
-
-    import torch
-    import coset_amd
-    from coset_amd import _lib
-
-    dev = _lib.require_gpu()
+# ---------------------------------------------------------------------------
+def bench_c2(torch, ca, args):
+    dev = torch.device("cuda")
     n = C2_BLOCKS
     g = torch.Generator(device=dev).manual_seed(2)
     x = torch.randn((n, 8), device=dev, generator=g, dtype=torch.float32)
@@ -77,64 +89,180 @@ def main():
     out = torch.empty((n, 8), dtype=torch.float32, device=dev)
 
     def step():
-        coset_amd.hnlq_roundtrip(x, 4, 2, 1.0, packed_out=packed, decoded_out=out)
+        ca.hnlq_roundtrip(x, 4, 2, 1.0, packed_out=packed, decoded_out=out)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream(dev)
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    e0.record(stream)
-    for _ in range(args.steps):
-        step()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    gpu_ms = e0.elapsed_time(e1)
-    kernel_s = gpu_ms / 1e3 / args.steps
-    ms_per_step = wall * 1e3 / args.steps
+    kernel_s, wall_s = gpu_time(torch, step, args.steps, args.warmup)
 
-    # parity spot check of this very run (not timed)
     from oracle import oracle as O
     idx = torch.randint(0, n, (4096,), device=dev, generator=g)
     xs = x[idx].cpu().numpy()
     codes = O.e8_encode(xs, 4, 2, 1.0)
-    ok = (np.array_equal(packed.cpu().numpy().astype(np.uint32)[idx.cpu().numpy()],
-                         O.pack_words(codes, 4))
+    ok = (np.array_equal(packed.cpu().numpy().astype(np.uint32)[idx.cpu().numpy()], O.pack_words(codes, 4))
           and np.array_equal(out[idx].cpu().numpy(), O.e8_decode(codes, 4, 2, 1.0)))
     if not ok:
         sys.exit("parity spot check FAILED: GPU codes differ from the oracle")
+    cpu = cpu_baseline(x[: args.cpu_sample].cpu().numpy()) if args.cpu_sample > 0 else None
+    del x, packed, out
+    return kernel_s, wall_s, cpu
 
-    achieved = C2_BYTES_PER_BLOCK * n / kernel_s / 1e9
+
+def bench_c1(torch, ca, args):
+    torch.manual_seed(0)
+    layer = ca.create_e8_hnlq_linear(768, 10, q=4, M=2, theta_trainable=False, theta_init_value=0.0,
+                                     weight_clip_value=2.0)
+    with torch.no_grad():
+        layer.weight.normal_(0.0, 0.02)
+    x = torch.randn(32, 768, device="cuda")
+    with torch.no_grad():
+        k, w = gpu_time(torch, lambda: layer(x), 200, 20)
+    return {"workload": "C1 layer forward 768->10, x 32x768 fp32, q4 M2 theta 0",
+            "us_per_forward_gpu": round(k * 1e6, 2), "us_per_forward_wall": round(w * 1e6, 2)}
+
+
+def bench_c3(torch, ca, args):
+    rows, cols = 4096, 8192                       # 2^22 blocks
+    g = torch.Generator(device="cuda").manual_seed(3)
+    # Student-t(3) = N / sqrt(chi2_3 / 3)
+    z = torch.randn((rows, cols), device="cuda", generator=g)
+    chi = (torch.randn((rows, cols, 3), device="cuda", generator=g) ** 2).sum(-1) / 3
+    x = torch.clamp(z / chi.sqrt(), -2.0, 2.0).to(torch.bfloat16)
+    del z, chi
+    xf = x.float()
+    sigma = xf.std(dim=1) + 1e-8
+    xmax = xf.abs().amax(dim=1) + 1e-8
+    q, M, Delta0, eta, ginv = 16, 3, 1.5, 0.1, 12.0
+    qM = float(q ** M)
+    bmin = (Delta0 / qM) / (eta * ginv * sigma)
+    bmax = torch.minimum((Delta0 * (qM - 1)) / (2 * ginv * xmax), (Delta0 * (qM - 1)) / (2 * eta * ginv * sigma))
+    bmin = torch.minimum(bmin, bmax * 0.9)
+    u = torch.rand(rows, device="cuda", generator=g)
+    beta = (bmin + u * (bmax - bmin)).contiguous()   # sigmoid(theta) uniform in (0, 1)
+    del xf
+    n = rows * cols // 8
+    packed = torch.empty((n, M), dtype=torch.uint32, device="cuda")
+    out = torch.empty((n, 8), dtype=torch.float32, device="cuda")
+    xb = x.reshape(n, 8)
+
+    def step():
+        ca.hnlq_roundtrip(xb, q, M, beta_row=beta, blocks_per_row=cols // 8, clip=2.0, packed_out=packed,
+                          decoded_out=out)
+
+    k, w = gpu_time(torch, step, 30, 3)
+    nbytes = 60 * n
+    return {"workload": "C3 2^22 Student-t(3) blocks clipped +-2, bf16 in, q16 M3, per-row beta, clamp 2",
+            "gblocks_per_s": round(n / k / 1e9, 3), "kernel_us": round(k * 1e6, 1),
+            "hbm_gbs": round(nbytes / k / 1e9, 1), "frac_hbm": round(nbytes / k / 1e9 / HBM_PEAK_GBS, 4),
+            "bytes_per_block": 60}
+
+
+def bench_c4(torch, ca, args):
+    g = torch.Generator(device="cuda").manual_seed(5)
+    W = 0.02 * torch.randn((4096, 4096), device="cuda", generator=g)
+    words = ca.hnlq_encode(W.reshape(-1, 8), 4, 2, 0.02).reshape(4096, 512, 2)
+    scale = torch.full((4096,), 0.02, device="cuda")
+    del W
+    res = {"workload": "C4 vLUT matmul 4096x4096 q4 M2 codes (8 MiB), fp16 activations, fp32 out",
+           "batches": {}}
+    ws = torch.empty(64 * 4096 * 64, dtype=torch.float32, device="cuda")
+    for B in (1, 8, 64):
+        a = torch.randn((B, 4096), device="cuda", generator=g).to(torch.float16)
+        row = {}
+        for method in ("lds", "mfma"):
+            k, w = gpu_time(torch, lambda: ca.vlut_matmul(words, a, 4, scale=scale, method=method, workspace=ws),
+                            100, 10)
+            nbytes = 8 * 2 ** 20 + B * 4096 * 2 + B * 4096 * 4
+            flops = 2.0 * B * 4096 * 4096
+            row[method] = {"tokens_per_s": round(B / k, 1), "us": round(k * 1e6, 2),
+                           "gbs_algorithmic": round(nbytes / k / 1e9, 1),
+                           "frac_hbm": round(nbytes / k / 1e9 / HBM_PEAK_GBS, 4),
+                           "dense_equiv_tflops": round(flops / k / 1e12, 2),
+                           "frac_fp16_mfma": round(flops / k / 1e12 / FP16_MFMA_TFLOPS, 5)}
+        res["batches"][str(B)] = row
+    return res
+
+
+def bench_c5(torch, ca, args):
+    res = {"workload": "C5 QAT E8 HNLQ linear fwd+bwd, 4096 bf16 tokens, q4 M2, W ~ N(0, 0.02)",
+           "shapes": {}}
+    for fin, fout in ((768, 768), (768, 3072), (3072, 768)):
+        torch.manual_seed(7)
+        layer = ca.create_e8_hnlq_linear(fin, fout, q=4, M=2)
+        with torch.no_grad():
+            layer.weight.normal_(0.0, 0.02)
+        x = torch.randn(4096, fin, device="cuda").to(torch.bfloat16).requires_grad_(True)
+        gy = torch.randn(4096, fout, device="cuda").to(torch.bfloat16)
+
+        def step():
+            layer.zero_grad(set_to_none=True)
+            x.grad = None
+            y = layer(x)
+            y.backward(gy)
+
+        k, w = gpu_time(torch, step, 20, 3)
+        flops = 6.0 * 4096 * fin * fout
+        res["shapes"][f"{fin}x{fout}"] = {"tokens_per_s": round(4096 / k, 1), "ms": round(k * 1e3, 3),
+                                          "tflops": round(flops / k / 1e12, 1),
+                                          "frac_bf16_mfma": round(flops / k / 1e12 / BF16_MFMA_TFLOPS, 4)}
+    return res
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--cpu-sample", type=int, default=1 << 24,
+                    help="C2 blocks timed on the host CPU oracle (0 skips it)")
+    ap.add_argument("--only", default="c1,c2,c3,c4,c5", help="comma list of workloads to run")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a plain 512 MiB device copy (HBM counter calibration)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        sys.exit("bench.py measures one GPU only: this build has no multi-GPU path "
+                 "(run with --gpus 1)")
+
+    import torch
+    import coset_amd as ca
+    from coset_amd import _lib
+
+    _lib.require_gpu()
+    only = set(args.only.split(","))
+    extra = {}
+    if args.calibrate_copy:
+        src = torch.empty(1 << 27, dtype=torch.float32, device="cuda").normal_()
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        extra["copy_calibration_bytes"] = 2 * src.numel() * 4
+        del src, dst
+    kernel_s = wall_s = None
     cpu = None
-    if args.cpu_sample > 0:
-        cpu = cpu_baseline(x[: args.cpu_sample].cpu().numpy())
-    value = n / (wall / args.steps) / 1e9
-    rec = {
-        "metric": METRIC,
-        "value": round(value, 3),
-        "unit": "Gblocks/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic N(0,1) blocks, seed 2",
-        "config": {"workload": "C2 bulk E8 HNLQ encode->decode", "blocks": n, "q": 4, "M": 2,
-                   "beta": 1.0, "outputs": "packed u16 words + decoded fp32"},
-        "hbm_gbs": round(achieved, 1),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic_from_profile()},
-        "kernel_us": round(kernel_s * 1e6, 2),
-        "parity": "bit-exact vs oracle on 4096 sampled blocks",
-        "cpu_baseline": cpu,
-    }
+    if "c2" in only:
+        kernel_s, wall_s, cpu = bench_c2(torch, ca, args)
+    for name, fn in (("c1", bench_c1), ("c3", bench_c3), ("c4", bench_c4), ("c5", bench_c5)):
+        if name in only:
+            extra[name] = fn(torch, ca, args)
+            torch.cuda.empty_cache()
+
+    rec = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+           "data": "synthetic N(0,1) blocks, seed 2",
+           "config": {"workload": "C2 bulk E8 HNLQ encode->decode", "blocks": C2_BLOCKS, "q": 4, "M": 2,
+                      "beta": 1.0, "outputs": "packed u16 words + decoded fp32"}}
+    if kernel_s is not None:
+        achieved = C2_BYTES_PER_BLOCK * C2_BLOCKS / kernel_s / 1e9
+        rec.update({
+            "value": round(C2_BLOCKS / wall_s / 1e9, 3), "unit": "Gblocks/s",
+            "ms_per_step": round(wall_s * 1e3, 4),
+            "hbm_gbs": round(achieved, 1),
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile()},
+            "kernel_us": round(kernel_s * 1e6, 2),
+            "parity": "bit-exact vs oracle on 4096 sampled blocks",
+            "cpu_baseline": cpu,
+        })
+    rec["extra"] = extra
     print(json.dumps(rec), flush=True)
 
 
