@@ -159,18 +159,20 @@ def bench_c4(torch, ca, args):
     g = torch.Generator(device="cuda").manual_seed(5)
     W = 0.02 * torch.randn((4096, 4096), device="cuda", generator=g)
     words = ca.hnlq_encode(W.reshape(-1, 8), 4, 2, 0.02).reshape(4096, 512, 2)
+    prepared = ca.vlut_prepare(words, 4)   # once per weight: (coarse id << 16 | idx), 16 MiB
     scale = torch.full((4096,), 0.02, device="cuda")
     del W
-    res = {"workload": "C4 vLUT matmul 4096x4096 q4 M2 codes (8 MiB), fp16 activations, fp32 out",
-           "batches": {}}
+    res = {"workload": "C4 vLUT matmul 4096x4096 q4 M2 codes (8 MiB uint16 words; 16 MiB prepared), "
+                       "fp16 activations, fp32 out", "batches": {}}
     ws = torch.empty(64 * 4096 * 64, dtype=torch.float32, device="cuda")
     for B in (1, 8, 64):
         a = torch.randn((B, 4096), device="cuda", generator=g).to(torch.float16)
         row = {}
-        for method in ("lds", "mfma"):
-            k, w = gpu_time(torch, lambda: ca.vlut_matmul(words, a, 4, scale=scale, method=method, workspace=ws),
+        for method, wts in (("lds", prepared), ("mfma", prepared), ("mfma_raw_words", words)):
+            m = "mfma" if method.startswith("mfma") else "lds"
+            k, w = gpu_time(torch, lambda: ca.vlut_matmul(wts, a, 4, scale=scale, method=m, workspace=ws),
                             100, 10)
-            nbytes = 8 * 2 ** 20 + B * 4096 * 2 + B * 4096 * 4
+            nbytes = wts.numel() * wts.element_size() + B * 4096 * 2 + B * 4096 * 4
             flops = 2.0 * B * 4096 * 4096
             row[method] = {"tokens_per_s": round(B / k, 1), "us": round(k * 1e6, 2),
                            "gbs_algorithmic": round(nbytes / k / 1e9, 1),

@@ -18,6 +18,7 @@ from .codecs import (
 )
 
 from .layers import (
+    E8ThetaWeightQuant,
     E8WeightQuant,
     HNLQConfig,
     HNLQLinear,
@@ -39,6 +40,7 @@ from .vlut import (
     vlut_dot,
     vlut_mac_operation,
     vlut_matmul,
+    vlut_prepare,
 )
 
 __version__ = "0.1.0"
@@ -48,7 +50,7 @@ __all__ = [
     "e8_encode", "e8_decode", "e8_quantize", "E8Decoder", "DecodingMethod",
     "hnlq_encode", "hnlq_decode", "hnlq_roundtrip", "word_dtype",
     "HNLQLinear", "HNLQLinearQAT", "HNLQConfig", "LSQActivation", "StraightThroughQuantize",
-    "E8WeightQuant", "create_e8_hnlq_linear", "get_generators", "ste_quantize",
+    "E8WeightQuant", "E8ThetaWeightQuant", "create_e8_hnlq_linear", "get_generators", "ste_quantize",
     "vLUTManager", "QuantizationConfig", "build_vlut", "_encoding_to_index", "vlut_mac_operation",
-    "vlut_accumulate_operation", "build_one_sided_vluts", "vlut_dot", "vlut_matmul",
+    "vlut_accumulate_operation", "build_one_sided_vluts", "vlut_dot", "vlut_matmul", "vlut_prepare",
 ]

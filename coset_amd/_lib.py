@@ -39,9 +39,14 @@ SIGNATURES = {
     "coset_e8_qat_fwd": [_vp, _i64, _i64, _vp, _i64, _flt, _int, _int, _vp, _int, _vp, _vp],
     "coset_e8_qat_bwd": [_vp, _int, _vp, _vp, _vp, _i64, _i64, _i64, _flt, _int, _int, _vp, _vp,
                          _vp],
+    "coset_e8_qat_fwd_theta": [_vp, _i64, _i64, _i64, _vp, _vp, _vp, ctypes.c_double, ctypes.c_double,
+                               ctypes.c_double, _int, _flt, _int, _int, _vp, _int, _vp, _vp, _vp, _vp, _vp],
+    "coset_e8_qat_bwd_theta": [_vp, _int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _flt, _int, _int, _vp, _vp, _vp,
+                               _vp],
     "coset_vlut_build_one_sided": [_vp, _i64, _int, _int, _vp, _vp],
     "coset_vlut_lookup_dot": [_vp, _i64, _int, _int, _vp, _vp, _vp],
-    "coset_vlut_matmul": [_vp, _vp, _int, _vp, _int, _i64, _i64, _i64, _int, _int, _int, _int, _vp, _i64,
+    "coset_vlut_prepare": [_vp, _i64, _int, _int, _vp, _vp],
+    "coset_vlut_matmul": [_vp, _int, _vp, _int, _vp, _int, _i64, _i64, _i64, _int, _int, _int, _int, _vp, _i64,
                           _vp, _vp],
     "coset_init": [_int],
     "coset_set_option": [_int, _int],

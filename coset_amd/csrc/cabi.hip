@@ -224,7 +224,88 @@ int coset_e8_qat_bwd(const void* gWq, int g_dtype, const float* W, const void* p
     if (!(clip >= 0.f)) return fail(COSET_EINVAL, "clip must be >= 0");
     if (n / blocks_per_tile > 0x7fffffff) return fail(COSET_EINVAL, "too many tiles");
     return check_hip(coset::launch_qat_bwd(gWq, g_dtype, W, packed, beta, n, blocks_per_tile, clip, q, M,
-                                           dW, dbeta, (hipStream_t)stream), "qat backward launch");
+                                           dW, dbeta, nullptr, nullptr, (hipStream_t)stream),
+                     "qat backward launch");
+}
+
+static coset::ThetaBeta make_theta_beta(const float* theta, const float* sigma, const float* xmax, double delta0,
+                                        double eta, double gamma_inv, int q, int M_bounds)
+{
+    // Python-double constants of HNLQLinearQAT._bounds (coset/core/layers.py:383-391),
+    // rounded to fp32 the way torch applies a Python scalar to an fp32 tensor
+    double qM = 1.0;
+    for (int i = 0; i < M_bounds; ++i) qM *= q;
+    coset::ThetaBeta tb{};
+    tb.theta = theta;
+    tb.sigma = sigma;
+    tb.xmax = xmax;
+    tb.c_min = (float)(delta0 / qM);
+    tb.c_eta_ginv = (float)(eta * gamma_inv);
+    tb.c_det = (float)(delta0 * (qM - 1));
+    tb.c_2ginv = (float)(2 * gamma_inv);
+    tb.c_2eta_ginv = (float)(2 * eta * gamma_inv);
+    return tb;
+}
+
+int coset_e8_qat_fwd_theta(const float* W, int64_t rows, int64_t cols, int64_t blocks_per_tile,
+                           const float* theta, const float* sigma_ema, const float* xmax_ema, double delta0,
+                           double eta, double gamma_inv, int M_bounds, float clip, int q, int M, void* Wq,
+                           int wq_dtype, void* packed, float* beta_out, float* dbeta_dtheta_out,
+                           int64_t* step_counter, void* stream)
+{
+    int rc;
+    if (rows < 0 || cols < 0 || cols % 8) return fail(COSET_EINVAL, "W must be [rows, 8k]");
+    int64_t n = rows * (cols / 8);
+    if ((rc = check_qm(q, M))) return rc;
+    if (M_bounds < 1 || M_bounds > 16) return fail(COSET_EINVAL, "M_bounds=%d", M_bounds);
+    if (blocks_per_tile <= 0 || n % blocks_per_tile) return fail(COSET_EINVAL, "blocks_per_tile must divide the block count");
+    if (n > 0 && (!W || !theta || !sigma_ema || !xmax_ema)) return fail(COSET_EINVAL, "NULL buffer");
+    if (n > 0 && !Wq && !packed) return fail(COSET_EINVAL, "nothing to write");
+    if (!aligned(W, 16) || (Wq && !aligned(Wq, 16))) return fail(COSET_EINVAL, "W and Wq must be 16-byte aligned");
+    if (packed && !aligned(packed, 4)) return fail(COSET_EINVAL, "packed must be 4-byte aligned");
+    if ((rc = check_dtype(wq_dtype, "Wq"))) return rc;
+    if (!(clip >= 0.f)) return fail(COSET_EINVAL, "clip must be >= 0");
+    if (!(delta0 > 0) || !(eta > 0) || !(gamma_inv > 0)) return fail(COSET_EINVAL, "delta0, eta, gamma_inv must be positive");
+    coset::CodecArgs a{};
+    a.n = n;
+    a.q = q;
+    a.M = M;
+    a.scale_mode = COSET_SCALE_LAYER;
+    a.beta = 1.f;
+    a.blocks_per_row = blocks_per_tile;
+    a.clip = clip;
+    a.strided = n > 1;
+    a.x = W;
+    a.x_dtype = COSET_F32;
+    a.packed = packed;
+    a.out = Wq;
+    a.out_dtype = wq_dtype;
+    a.use_theta = 1;
+    a.tb = make_theta_beta(theta, sigma_ema, xmax_ema, delta0, eta, gamma_inv, q, M_bounds);
+    a.beta_out = beta_out;
+    a.dbdt_out = dbeta_dtheta_out;
+    a.step_counter = step_counter;
+    return check_hip(coset::launch_codec(a, coset::MODE_ROUNDTRIP, (hipStream_t)stream), "qat forward launch");
+}
+
+int coset_e8_qat_bwd_theta(const void* gWq, int g_dtype, const float* W, const void* packed, const float* beta,
+                           const float* dbeta_dtheta, int64_t rows, int64_t cols, int64_t blocks_per_tile,
+                           float clip, int q, int M, float* dW, float* dbeta, float* dtheta, void* stream)
+{
+    int rc;
+    if (rows < 0 || cols < 0 || cols % 8) return fail(COSET_EINVAL, "W must be [rows, 8k]");
+    int64_t n = rows * (cols / 8);
+    if ((rc = check_qm(q, M))) return rc;
+    if ((rc = check_dtype(g_dtype, "gradient"))) return rc;
+    if (blocks_per_tile <= 0 || n % blocks_per_tile) return fail(COSET_EINVAL, "blocks_per_tile must divide the block count");
+    if (n > 0 && (!gWq || !W || !packed || !beta || !dW || !dbeta || !dbeta_dtheta || !dtheta))
+        return fail(COSET_EINVAL, "NULL buffer");
+    if (!aligned(gWq, 16) || !aligned(W, 16) || !aligned(dW, 16)) return fail(COSET_EINVAL, "g, W, dW must be 16-byte aligned");
+    if (!(clip >= 0.f)) return fail(COSET_EINVAL, "clip must be >= 0");
+    if (n / blocks_per_tile > 0x7fffffff) return fail(COSET_EINVAL, "too many tiles");
+    return check_hip(coset::launch_qat_bwd(gWq, g_dtype, W, packed, beta, n, blocks_per_tile, clip, q, M, dW,
+                                           dbeta, dbeta_dtheta, dtheta, (hipStream_t)stream),
+                     "qat backward launch");
 }
 
 int coset_vlut_build_one_sided(const float* queries, int64_t n_queries, int q, int legacy, float* vlut,
@@ -270,8 +351,17 @@ int64_t coset_vlut_workspace_floats(int64_t B, int64_t rows, int64_t K, int q, i
     return (int64_t)coset::vlut_default_splits(rows, B, K, m) * B * rows;
 }
 
-int coset_vlut_matmul(const void* words, const float* scale, int scale_mode, const void* act, int act_dtype,
-                      int64_t B, int64_t rows, int64_t K, int q, int M, int legacy, int method,
+int coset_vlut_prepare(const void* words, int64_t n_words, int q, int legacy, uint32_t* prepared, void* stream)
+{
+    if (q != 2 && q != 4) return fail(COSET_EUNSUPPORTED, "vLUT prepare supports q = 2 or 4 (got %d)", q);
+    if (n_words < 0) return fail(COSET_EINVAL, "n_words < 0");
+    if (n_words > 0 && (!words || !prepared)) return fail(COSET_EINVAL, "NULL buffer");
+    return check_hip(coset::vlut_prepare((const uint16_t*)words, n_words, q, legacy ? 1 : 0, prepared,
+                                         (hipStream_t)stream), "vLUT prepare launch");
+}
+
+int coset_vlut_matmul(const void* words, int word_format, const float* scale, int scale_mode, const void* act,
+                      int act_dtype, int64_t B, int64_t rows, int64_t K, int q, int M, int legacy, int method,
                       float* workspace, int64_t workspace_floats, float* out, void* stream)
 {
     int rc;
@@ -293,8 +383,10 @@ int coset_vlut_matmul(const void* words, const float* scale, int scale_mode, con
     if (workspace_floats < (int64_t)splits * B * rows)
         return fail(COSET_EINVAL, "workspace holds %lld floats, needs %lld", (long long)workspace_floats,
                     (long long)splits * B * rows);
+    if (word_format != 0 && word_format != 1) return fail(COSET_EINVAL, "word_format must be 0 or 1");
     coset::VlutMatmulArgs p{};
     p.words = words;
+    p.prepared = word_format;
     p.scale = scale;
     p.scale_mode = scale_mode;
     p.act = act;

@@ -17,6 +17,40 @@ constexpr int kMaxM = 8;
 // Bytes of one packed level word: q^8 <= 65536 fits 16 bits.
 __host__ __device__ inline int word_bytes(int q) { return q <= 4 ? 2 : 4; }
 
+// The layer's adaptive scale (coset/core/layers.py:381-396, 418-422) as the
+// fp32 operation sequence torch runs on the device:
+//   beta_min  = recip(c_eta_ginv * sigma) * c_min
+//   beta_max  = min(recip(c_2ginv * xmax) * c_det, recip(c_2eta_ginv * sigma) * c_det)
+//   beta_min  = min(beta_min, beta_max * 0.9)
+//   beta      = beta_min + sigmoid(theta) * (beta_max - beta_min)
+// with the Python-double constants rounded to fp32 as torch does.
+struct ThetaBeta {
+    const float* theta;      // [tiles]
+    const float* sigma;      // [tiles] sigma_ema
+    const float* xmax;       // [tiles] xmax_ema
+    float c_min, c_eta_ginv, c_det, c_2ginv, c_2eta_ginv;
+};
+
+__device__ __forceinline__ void theta_beta_terms(const ThetaBeta& tb, int64_t t, float* bmin, float* bmax, float* sg)
+{
+    float sigma = tb.sigma[t], xmax = tb.xmax[t];
+    float lo = __fmul_rn(__fdiv_rn(1.f, __fmul_rn(tb.c_eta_ginv, sigma)), tb.c_min);
+    float hi_det = __fmul_rn(__fdiv_rn(1.f, __fmul_rn(tb.c_2ginv, xmax)), tb.c_det);
+    float hi_prob = __fmul_rn(__fdiv_rn(1.f, __fmul_rn(tb.c_2eta_ginv, sigma)), tb.c_det);
+    float hi = fminf(hi_det, hi_prob);
+    lo = fminf(lo, __fmul_rn(hi, 0.9f));
+    *bmin = lo;
+    *bmax = hi;
+    *sg = __fdiv_rn(1.f, __fadd_rn(1.f, expf(-tb.theta[t])));
+}
+
+__device__ __forceinline__ float theta_beta(const ThetaBeta& tb, int64_t t)
+{
+    float lo, hi, sg;
+    theta_beta_terms(tb, t, &lo, &hi, &sg);
+    return __fadd_rn(lo, __fmul_rn(sg, __fsub_rn(hi, lo)));
+}
+
 struct CodecArgs {
     int64_t n;               // blocks
     int q, M;
@@ -42,7 +76,29 @@ struct CodecArgs {
     // decode output
     void* out;               // nullable [n, 8] fp32 or bf16
     int out_dtype;
+    // SCALE_LAYER with beta derived in-kernel from theta (beta_row unused)
+    int use_theta;
+    ThetaBeta tb;
+    float* beta_out;         // nullable [tiles]: the beta used, one write per tile
+    float* dbdt_out;         // nullable [tiles]: d beta / d theta at that beta
+    int64_t* step_counter;   // nullable: incremented once per launch
 };
+
+// Per-block scale of SCALE_LAYER (reads beta_row or derives it from theta).
+__device__ __forceinline__ float layer_scale(const CodecArgs& a, int64_t block)
+{
+    int64_t t = block / a.blocks_per_row;
+    if (!a.use_theta) return a.beta_row[t];
+    float lo, hi, sg;
+    theta_beta_terms(a.tb, t, &lo, &hi, &sg);
+    float span = __fsub_rn(hi, lo);
+    float b = __fadd_rn(lo, __fmul_rn(sg, span));
+    if (block == t * a.blocks_per_row) {  // one thread per tile records beta and its derivative
+        if (a.beta_out) a.beta_out[t] = b;
+        if (a.dbdt_out) a.dbdt_out[t] = __fmul_rn(__fmul_rn(span, __fsub_rn(1.f, sg)), sg);
+    }
+    return b;
+}
 
 // Dispatch: the LDS-table kernel (hnlq_lut.hip) for q in {2, 4} and large
 // n, the generic kernel (hnlq_codec.hip) otherwise.  codec_path overrides
@@ -55,9 +111,11 @@ extern int g_codec_path;
 constexpr int64_t kLutMinBlocks = 1 << 16;
 
 // Backward of the QAT weight quantizer (qat.hip).
+// dbdt (nullable): also write dtheta[t] = dbeta[t] * dbdt[t].
 hipError_t launch_qat_bwd(const void* g, int g_dtype, const float* W, const void* packed,
                           const float* beta, int64_t n_blocks, int64_t blocks_per_tile, float clip,
-                          int q, int M, float* dW, float* dbeta, hipStream_t s);
+                          int q, int M, float* dW, float* dbeta, const float* dbdt, float* dtheta,
+                          hipStream_t s);
 
 // Elementwise lattice operators (custom_round, g_x, projection,
 // encode_coords, decode_coords) over n blocks.

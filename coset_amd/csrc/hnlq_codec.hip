@@ -21,6 +21,7 @@ template <int Q, int MODE>
 __global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
 {
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i == 0 && a.step_counter) *a.step_counter += 1;
     if (i >= a.n) return;
     const int q = Q > 0 ? Q : a.q;
     const float qf = (float)q;
@@ -30,7 +31,7 @@ __global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
     if (a.scale_mode == SCALE_CODEC)
         scale = a.beta;
     else if (a.scale_mode == SCALE_LAYER)
-        scale = a.beta_row[i / a.blocks_per_row];
+        scale = layer_scale(a, i);
 
     float acc[8];
 #pragma unroll

@@ -43,6 +43,7 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_lut_kernel(CodecArgs a, cons
         __syncthreads();
     }
 
+    if (blockIdx.x == 0 && threadIdx.x == 0 && a.step_counter) *a.step_counter += 1;
     const float qf = (float)Q;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n; i += stride) {
@@ -50,7 +51,7 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_lut_kernel(CodecArgs a, cons
         if (a.scale_mode == SCALE_CODEC)
             scale = a.beta;
         else if (a.scale_mode == SCALE_LAYER)
-            scale = a.beta_row[i / a.blocks_per_row];
+            scale = layer_scale(a, i);
 
         // Level words are collected in one 64-bit register (M <= 4 words of
         // 16 bits); each level is encoded, then decoded from its digits.

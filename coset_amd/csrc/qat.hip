@@ -33,7 +33,16 @@ struct QatBwdArgs {
     const uint64_t* coarse;
     float* dW;             // [rows, cols]
     float* dbeta;          // [n_tiles]
+    const float* dbdt;     // [n_tiles] d beta / d theta, or null
+    float* dtheta;         // [n_tiles] when dbdt is given
 };
+
+// dL/dtheta = dL/dbeta * (beta_max - beta_min) s (1 - s), s = sigmoid(theta);
+// the factor was recorded by the forward kernel.
+__device__ __forceinline__ void write_dtheta(const QatBwdArgs& a, int64_t t, float dbeta)
+{
+    if (a.dbdt) a.dtheta[t] = __fmul_rn(dbeta, a.dbdt[t]);
+}
 
 // Unscaled quantized block Q = sum_m q^m r_m from packed words.
 template <int Q>
@@ -145,7 +154,11 @@ __global__ void __launch_bounds__(256) qat_bwd_tile_kernel(QatBwdArgs a)
     __shared__ float s_part[4];
     if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = part;
     __syncthreads();
-    if (threadIdx.x == 0) a.dbeta[tile] = (s_part[0] + s_part[1]) + (s_part[2] + s_part[3]);
+    if (threadIdx.x == 0) {
+        float db = (s_part[0] + s_part[1]) + (s_part[2] + s_part[3]);
+        a.dbeta[tile] = db;
+        write_dtheta(a, tile, db);
+    }
 }
 
 template <int Q>
@@ -153,7 +166,9 @@ __global__ void __launch_bounds__(256) qat_bwd_block_kernel(QatBwdArgs a)
 {
     int64_t blk = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (blk >= a.n_blocks) return;
-    a.dbeta[blk] = block_grad<Q>(a, blk, a.beta[blk]);
+    float db = block_grad<Q>(a, blk, a.beta[blk]);
+    a.dbeta[blk] = db;
+    write_dtheta(a, blk, db);
 }
 
 template <int Q>
@@ -170,10 +185,13 @@ static hipError_t launch_bwd_q(const QatBwdArgs& a, hipStream_t s)
 
 hipError_t launch_qat_bwd(const void* g, int g_dtype, const float* W, const void* packed,
                           const float* beta, int64_t n_blocks, int64_t blocks_per_tile, float clip,
-                          int q, int M, float* dW, float* dbeta, hipStream_t s)
+                          int q, int M, float* dW, float* dbeta, const float* dbdt, float* dtheta,
+                          hipStream_t s)
 {
     if (n_blocks == 0) return hipSuccess;
     QatBwdArgs a{};
+    a.dbdt = dbdt;
+    a.dtheta = dtheta;
     a.g = g;
     a.g_dtype = g_dtype;
     a.W = W;

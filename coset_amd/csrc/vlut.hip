@@ -51,6 +51,29 @@ __device__ __forceinline__ void two_r_lut(uint32_t w, const uint16_t* map, const
     for (int j = 0; j < 8; ++j) out[j] -= Q * (int)(int8_t)(uint8_t)(c >> (8 * j));
 }
 
+// Level word index i of the weight tensor -> (idx, coarse id).
+__device__ __forceinline__ void load_word(const VlutMatmulArgs& p, int64_t i, uint32_t* idx, uint32_t* cid)
+{
+    if (p.prepared) {
+        uint32_t v = reinterpret_cast<const uint32_t*>(p.words)[i];
+        *idx = v & 0xffffu;
+        *cid = v >> 16;
+    } else {
+        uint32_t w = reinterpret_cast<const uint16_t*>(p.words)[i];
+        *idx = w;
+        *cid = p.map[w];
+    }
+}
+
+__global__ void __launch_bounds__(256) vlut_prepare_kernel(const uint16_t* words, int64_t n, const uint16_t* map,
+                                                          uint32_t* out)
+{
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    uint32_t w = words[i];
+    out[i] = ((uint32_t)map[w] << 16) | w;
+}
+
 // ---------------------------------------------------------------- build
 template <int Q>
 __global__ void __launch_bounds__(256) vlut_build_kernel(const float* a, int64_t n_queries, uint32_t n_codes,
@@ -104,16 +127,23 @@ __global__ void __launch_bounds__(256) vlut_dot_kernel(const void* words, int wo
 // ---------------------------------------------------------------- LDS vLUT matmul
 constexpr int kVlutThreads = 256;
 constexpr int kVlutRowsPerThread = 2;
-constexpr int kVlutTableFloats = 24 * (8 + kMaxCoarseVlut);  // TT * KBW <= 24
+constexpr int kVlutMaxTables = 24;  // TT * KBW
+constexpr int kVlutTableFloats = kVlutMaxTables * (8 + kMaxCoarseVlut);
 
 template <int Q, int M, int TT>
 __global__ void __launch_bounds__(kVlutThreads) vlut_lds_kernel(VlutMatmulArgs p)
 {
-    // grid.x: row chunks of 512 rows; grid.y: k splits; grid.z: token tiles
+    // grid.x: row chunks of 512 rows; grid.y: k splits; grid.z: token tiles.
+    // LDS holds, for TT tokens x KBW k-blocks, the factorized one-sided vLUT
+    //   T[t][k][j]     = <a_tk, g_j>      j < 8   (g_j: columns of G)
+    //   T[t][k][8 + c] = <a_tk, c>        c = coarse point id
+    // so vLUT_{a_tk}[idx(b)] = sum_j b_j T[j] - q T[8 + cid(b)].
     __shared__ float s_tab[kVlutTableFloats];
+    __shared__ float s_act[kVlutMaxTables * 8];
+    __shared__ uint64_t s_coarse[kMaxCoarseVlut];
     const int nc = p.n_coarse;
-    const int stride = 8 + nc;                    // floats per (token, k-block) table
-    const int kbw = p.kb_per_chunk;               // k-blocks per LDS chunk
+    const int stride = 8 + nc;
+    const int kbw = p.kb_per_chunk;
     const int t0 = blockIdx.z * TT;
     const int nt = min(TT, (int)(p.B - t0));
     const int64_t kb_total = p.K / 8;
@@ -121,6 +151,7 @@ __global__ void __launch_bounds__(kVlutThreads) vlut_lds_kernel(VlutMatmulArgs p
     const int64_t k_begin = blockIdx.y * ks_len;
     const int64_t k_end = min(kb_total, k_begin + ks_len);
     const int64_t r0 = (int64_t)blockIdx.x * kVlutThreads * kVlutRowsPerThread;
+    for (int i = threadIdx.x; i < nc; i += kVlutThreads) s_coarse[i] = p.coarse[i];
 
     float acc[kVlutRowsPerThread][TT];
 #pragma unroll
@@ -131,17 +162,17 @@ __global__ void __launch_bounds__(kVlutThreads) vlut_lds_kernel(VlutMatmulArgs p
     for (int64_t kc = k_begin; kc < k_end; kc += kbw) {
         const int nk = (int)min((int64_t)kbw, k_end - kc);
         __syncthreads();
-        // tables: T[t][k][j] = <a_tk, g_j> (j < 8), T[t][k][8 + c] = <a_tk, c>
-        const int entries = nt * nk * stride;
-        for (int e = threadIdx.x; e < entries; e += kVlutThreads) {
+        for (int e = threadIdx.x; e < nt * nk * 8; e += kVlutThreads) {
+            int t = e / (nk * 8), rem = e - t * nk * 8;
+            s_act[t * kbw * 8 + rem] = load_act(p.act, p.act_dtype, (int64_t)(t0 + t) * p.K + kc * 8 + rem);
+        }
+        __syncthreads();
+        for (int e = threadIdx.x; e < nt * nk * stride; e += kVlutThreads) {
             int t = e / (nk * stride);
             int rem = e - t * nk * stride;
             int k = rem / stride;
             int j = rem - k * stride;
-            int64_t base = (int64_t)(t0 + t) * p.K + (kc + k) * 8;
-            float av[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) av[i] = load_act(p.act, p.act_dtype, base + i);
+            const float* av = s_act + (t * kbw + k) * 8;
             float v;
             if (j == 0) {
                 v = 2.f * av[0];
@@ -153,7 +184,7 @@ __global__ void __launch_bounds__(kVlutThreads) vlut_lds_kernel(VlutMatmulArgs p
                 for (int i = 0; i < 8; ++i) v += av[i];
                 v *= 0.5f;
             } else {
-                uint64_t c = p.coarse[j - 8];
+                uint64_t c = s_coarse[j - 8];
                 v = 0.f;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) v = __fmaf_rn(av[i], (float)(int8_t)(uint8_t)(c >> (8 * i)), v);
@@ -162,28 +193,28 @@ __global__ void __launch_bounds__(kVlutThreads) vlut_lds_kernel(VlutMatmulArgs p
             s_tab[(t * kbw + k) * stride + j] = v;
         }
         __syncthreads();
+        for (int k = 0; k < nk; ++k) {
 #pragma unroll
-        for (int rr = 0; rr < kVlutRowsPerThread; ++rr) {
-            int64_t row = r0 + threadIdx.x + rr * kVlutThreads;
-            if (row >= p.rows) continue;
-            const uint16_t* wrow = reinterpret_cast<const uint16_t*>(p.words) + (row * kb_total + kc) * M;
-            for (int k = 0; k < nk; ++k) {
+            for (int rr = 0; rr < kVlutRowsPerThread; ++rr) {
+                int64_t row = r0 + threadIdx.x + rr * kVlutThreads;
+                if (row >= p.rows) continue;
+                const int64_t wbase = (row * kb_total + kc + k) * M;
                 float qm = 1.f;
 #pragma unroll
                 for (int m = 0; m < M; ++m) {
-                    uint32_t w = wrow[k * M + m];
-                    int cid = p.map[w];
+                    uint32_t w, cid;
+                    load_word(p, wbase + m, &w, &cid);
                     int b[8];
                     unpack_word<Q>(w, Q, b);
 #pragma unroll
                     for (int t = 0; t < TT; ++t) {
                         if (t >= nt) break;
                         const float* T = s_tab + (t * kbw + k) * stride;
-                        float s = 0.f;
+                        float sum = 0.f;
 #pragma unroll
-                        for (int j = 0; j < 8; ++j) s = __fmaf_rn((float)b[j], T[j], s);
-                        s = __fmaf_rn(-(float)Q, T[8 + cid], s);
-                        acc[rr][t] = __fmaf_rn(qm, s, acc[rr][t]);
+                        for (int j = 0; j < 8; ++j) sum = __fmaf_rn((float)b[j], T[j], sum);
+                        sum = __fmaf_rn(-(float)Q, T[8 + cid], sum);
+                        acc[rr][t] = __fmaf_rn(qm, sum, acc[rr][t]);
                     }
                     qm *= (float)Q;
                 }
@@ -195,102 +226,157 @@ __global__ void __launch_bounds__(kVlutThreads) vlut_lds_kernel(VlutMatmulArgs p
         int64_t row = r0 + threadIdx.x + rr * kVlutThreads;
         if (row >= p.rows) continue;
         for (int t = 0; t < nt; ++t)
-            p.partial[((int64_t)blockIdx.y * p.B + t0 + t) * p.rows + row] = acc[rr][t];
+            p.partial[((int64_t)(t0 + t) * p.rows + row) * gridDim.y + blockIdx.y] = acc[rr][t];
     }
 }
 
 // ---------------------------------------------------------------- MFMA matmul
 // Tile: 64 output rows x up to 64 tokens per workgroup (4 waves, one 16-row
-// slice each), K split over grid.y.  Per step of 4 k-blocks (32 K values)
-// each thread decodes one (row, k-block) pair to 8 halves of 2*x_hat in LDS;
-// then each wave runs 16x16x16 MFMAs: A = activations (tokens x K) read
-// straight from HBM/L2, B = the decoded slice (K x rows).
+// slice each), K split over grid.y.  A step covers 16 k-blocks (128 K):
+// every thread decodes 4 (row, k-block) pairs to 8 halves of 2*x_hat in LDS
+// (the 4 word loads and table gathers are issued together), the activation
+// tile [tokens x 128] is staged in LDS with 16-byte loads, then each wave runs
+// 8 K-slices of 16x16x16 MFMAs per 16-token sub-tile.
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef short bf16x4_t __attribute__((ext_vector_type(4)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kMfmaRows = 64;
-constexpr int kMfmaKStep = 32;  // K values per decode step (4 k-blocks)
+constexpr int kMfmaKB = 16;              // k-blocks per step
+constexpr int kMfmaK = kMfmaKB * 8;      // 128 K values per step
+constexpr int kMfmaLd = kMfmaK + 8;      // row pitch in halves (16-byte aligned, skews banks)
+constexpr int kMfmaMaxSteps = 4;         // steps per workgroup: its K range is <= 64 k-blocks
 
 template <int Q, int M, bool BF16>
 __global__ void __launch_bounds__(256) vlut_mfma_kernel(VlutMatmulArgs p)
 {
-    __shared__ __align__(16) uint16_t s_b[kMfmaRows][kMfmaKStep + 4];  // +4 halves: bank skew
+    __shared__ __align__(16) uint16_t s_b[kMfmaRows][kMfmaLd];
+    __shared__ __align__(16) uint16_t s_a[64][kMfmaLd];
+    __shared__ uint64_t s_coarse[kMaxCoarseVlut];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
+
     const int64_t kb_total = p.K / 8;
-    const int64_t ks_len = ((kb_total + gridDim.y - 1) / gridDim.y + 3) / 4 * 4;
+    const int64_t ks_len = ((kb_total + gridDim.y - 1) / gridDim.y + kMfmaKB - 1) / kMfmaKB * kMfmaKB;
     const int64_t k_begin = blockIdx.y * ks_len;
     const int64_t k_end = min(kb_total, k_begin + ks_len);
+    const int n_steps = (int)min((int64_t)kMfmaMaxSteps, (k_end - k_begin + kMfmaKB - 1) / kMfmaKB);
     const int64_t r0 = (int64_t)blockIdx.x * kMfmaRows;
-    const int64_t t_base = (int64_t)blockIdx.z * 64;  // token tile of up to 64
-    const int n_tsub = (int)min((int64_t)4, (p.B - t_base + 15) / 16);
+    const int64_t t_base = (int64_t)blockIdx.z * 64;
+    const int nt = (int)min((int64_t)64, p.B - t_base);
+    const int n_tsub = (nt + 15) / 16;
+    const uint16_t* act = reinterpret_cast<const uint16_t*>(p.act);
+
+    // All level words and coarse ids of this workgroup's tile are requested
+    // up front (4 pairs per thread per step, pair = (row pr/16, k-block pr%16)),
+    // so the global latency is paid once, not once per step.
+    uint32_t words[kMfmaMaxSteps][4][M];
+    uint32_t cids[kMfmaMaxSteps][4][M];
+#pragma unroll
+    for (int st = 0; st < kMfmaMaxSteps; ++st) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int pr = threadIdx.x + 256 * i;
+            const int64_t row = r0 + (pr >> 4);
+            const int64_t kb = k_begin + st * kMfmaKB + (pr & 15);
+            const bool ok = st < n_steps && row < p.rows && kb < k_end;
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                uint32_t w = 0xffffffffu, c = 0u;
+                if (ok) load_word(p, (row * kb_total + kb) * M + m, &w, &c);
+                words[st][i][m] = w;
+                cids[st][i][m] = c;
+            }
+        }
+    }
 
     float4_t acc[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) acc[s] = (float4_t){0.f, 0.f, 0.f, 0.f};
 
-    // this thread decodes row dr, k-block dk of each step
-    const int dr = threadIdx.x >> 2;
-    const int dk = threadIdx.x & 3;
-    const int64_t drow = r0 + dr;
+    // the coarse table is staged after the word loads are in flight, so the
+    // wait for it overlaps their latency
+    for (int i = threadIdx.x; i < p.n_coarse; i += 256) s_coarse[i] = p.coarse[i];
 
-    for (int64_t kc = k_begin; kc < k_end; kc += 4) {
-        int two_x[8];
+    uint4 av[4];
+    auto load_act_tile = [&](int st) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) two_x[j] = 0;
-        if (drow < p.rows && kc + dk < k_end) {
-            const uint16_t* wp = reinterpret_cast<const uint16_t*>(p.words) + (drow * kb_total + kc + dk) * M;
+        for (int j = 0; j < 4; ++j) {
+            const int idx = threadIdx.x + 256 * j;
+            const int tok = idx >> 4, seg = idx & 15;
+            const int64_t kb = k_begin + st * kMfmaKB + seg;
+            av[j] = make_uint4(0u, 0u, 0u, 0u);
+            if (st < n_steps && tok < nt && kb < k_end)
+                av[j] = *reinterpret_cast<const uint4*>(act + (t_base + tok) * p.K + kb * 8);
+        }
+    };
+    load_act_tile(0);
+
+#pragma unroll
+    for (int st = 0; st < kMfmaMaxSteps; ++st) {
+        if (st >= n_steps) break;
+        __syncthreads();  // the previous step's MFMAs are done with s_a / s_b
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int idx = threadIdx.x + 256 * j;
+            *reinterpret_cast<uint4*>(&s_a[idx >> 4][(idx & 15) * 8]) = av[j];
+        }
+        if (st + 1 < n_steps) load_act_tile(st + 1);  // in flight during decode and MFMAs
+        // decode 2 x_hat = sum_m q^m (2Gb - q (2c)) -> halves
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            int two_x[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) two_x[j] = 0;
             int wq = 1;
+            const bool ok = words[st][i][0] != 0xffffffffu;
 #pragma unroll
             for (int m = 0; m < M; ++m) {
-                int tr[8];
-                two_r_lut<Q>(wp[m], p.map, p.coarse, tr);
+                int b[8];
+                unpack_word<Q>(ok ? words[st][i][m] : 0u, Q, b);
+                const uint64_t c = s_coarse[cids[st][i][m]];
+                int u[8];
+                u[0] = 4 * b[0] - 2 * b[1] + b[7];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) two_x[j] += wq * tr[j];
+                for (int j = 1; j < 6; ++j) u[j] = 2 * (b[j] - b[j + 1]) + b[7];
+                u[6] = 2 * b[6] + b[7];
+                u[7] = b[7];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) two_x[j] += wq * (u[j] - Q * (int)(int8_t)(uint8_t)(c >> (8 * j)));
                 wq *= Q;
             }
-        }
-        uint16_t hv[8];
+            uint32_t hv[4];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            if (BF16) {
-                hv[j] = (uint16_t)(__float_as_uint((float)two_x[j]) >> 16);  // exact: |2x| < 256
-            } else {
-                _Float16 h = (_Float16)two_x[j];                              // exact: |2x| < 2048
-                hv[j] = *reinterpret_cast<uint16_t*>(&h);
+            for (int j = 0; j < 4; ++j) {
+                uint32_t lo, hi;
+                if (BF16) {  // exact: |2x| < 256
+                    lo = __float_as_uint((float)two_x[2 * j]) >> 16;
+                    hi = __float_as_uint((float)two_x[2 * j + 1]) >> 16;
+                } else {     // exact: |2x| < 2048
+                    _Float16 l = (_Float16)two_x[2 * j], h = (_Float16)two_x[2 * j + 1];
+                    lo = __builtin_bit_cast(uint16_t, l);
+                    hi = __builtin_bit_cast(uint16_t, h);
+                }
+                hv[j] = ok ? (lo | (hi << 16)) : 0u;
             }
+            const int pr = threadIdx.x + 256 * i;
+            *reinterpret_cast<uint4*>(&s_b[pr >> 4][(pr & 15) * 8]) = make_uint4(hv[0], hv[1], hv[2], hv[3]);
         }
-        __syncthreads();  // previous step's MFMAs are done with s_b
-        uint4 pk;
-        pk.x = hv[0] | ((uint32_t)hv[1] << 16);
-        pk.y = hv[2] | ((uint32_t)hv[3] << 16);
-        pk.z = hv[4] | ((uint32_t)hv[5] << 16);
-        pk.w = hv[6] | ((uint32_t)hv[7] << 16);
-        *reinterpret_cast<uint2*>(&s_b[dr][dk * 8]) = make_uint2(pk.x, pk.y);
-        *reinterpret_cast<uint2*>(&s_b[dr][dk * 8 + 4]) = make_uint2(pk.z, pk.w);
         __syncthreads();
-
+        // D[token][row] += A[token][k] * B[k][row]
+        const int brow = wave * 16 + (lane & 15);
 #pragma unroll
-        for (int kk = 0; kk < kMfmaKStep / 16; ++kk) {
-            // B operand: K rows 4*(lane/16).. of this 16-K slice, column = row lane%16
-            const int brow = wave * 16 + (lane & 15);
+        for (int kk = 0; kk < kMfmaK / 16; ++kk) {
             const int kof = kk * 16 + 4 * (lane >> 4);
             uint2 bv = *reinterpret_cast<const uint2*>(&s_b[brow][kof]);
-            const int64_t kglob = (kc * 8) + kof;
             for (int s = 0; s < n_tsub; ++s) {
-                const int64_t tok = t_base + s * 16 + (lane & 15);
-                uint2 av = make_uint2(0u, 0u);
-                if (tok < p.B && kglob < k_end * 8)
-                    av = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.act) + tok * p.K + kglob);
+                uint2 a2 = *reinterpret_cast<const uint2*>(&s_a[s * 16 + (lane & 15)][kof]);
                 if (BF16) {
-                    bf16x4_t A = *reinterpret_cast<bf16x4_t*>(&av);
-                    bf16x4_t Bv = *reinterpret_cast<bf16x4_t*>(&bv);
-                    acc[s] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(A, Bv, acc[s], 0, 0, 0);
+                    acc[s] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4_t, a2),
+                                                                      __builtin_bit_cast(bf16x4_t, bv), acc[s], 0, 0, 0);
                 } else {
-                    half4_t A = *reinterpret_cast<half4_t*>(&av);
-                    half4_t Bv = *reinterpret_cast<half4_t*>(&bv);
-                    acc[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(A, Bv, acc[s], 0, 0, 0);
+                    acc[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4_t, a2),
+                                                                  __builtin_bit_cast(half4_t, bv), acc[s], 0, 0, 0);
                 }
             }
         }
@@ -302,7 +388,7 @@ __global__ void __launch_bounds__(256) vlut_mfma_kernel(VlutMatmulArgs p)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 int64_t tok = t_base + s * 16 + 4 * (lane >> 4) + i;
-                if (tok < p.B) p.partial[((int64_t)blockIdx.y * p.B + tok) * p.rows + row] = acc[s][i];
+                if (tok < p.B) p.partial[(tok * p.rows + row) * gridDim.y + blockIdx.y] = acc[s][i];
             }
         }
     }
@@ -316,8 +402,16 @@ __global__ void __launch_bounds__(256) vlut_reduce_kernel(const float* partial, 
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= B * rows) return;
     int64_t o = i % rows;
+    const float* pp = partial + i * splits;  // the splits of one output are contiguous
     float acc = 0.f;
-    for (int s = 0; s < splits; ++s) acc += partial[(int64_t)s * B * rows + i];
+    int s = 0;
+    if ((splits & 3) == 0) {
+        for (; s < splits; s += 4) {
+            float4 v = *reinterpret_cast<const float4*>(pp + s);
+            acc += (v.x + v.y) + (v.z + v.w);
+        }
+    }
+    for (; s < splits; ++s) acc += pp[s];
     float sc = scale ? (scale_mode == 0 ? scale[o] : 1.f / scale[o]) : 1.f;
     out[i] = acc * mult * sc;
 }
@@ -329,7 +423,7 @@ template <int Q, int M>
 hipError_t launch_lds(VlutMatmulArgs p, int splits, hipStream_t s)
 {
     int TT = p.B >= 8 ? 8 : (p.B >= 4 ? 4 : (p.B >= 2 ? 2 : 1));
-    p.kb_per_chunk = std::max(1, 24 / TT);
+    p.kb_per_chunk = std::max(1, kVlutMaxTables / TT);
     dim3 grid((unsigned)((p.rows + kVlutThreads * kVlutRowsPerThread - 1) / (kVlutThreads * kVlutRowsPerThread)),
               (unsigned)splits, (unsigned)((p.B + TT - 1) / TT));
     switch (TT) {
@@ -400,9 +494,14 @@ int vlut_default_splits(int64_t rows, int64_t B, int64_t K, int method)
 {
     int64_t kb = K / 8;
     if (method == VLUT_METHOD_MFMA) {
+        // every workgroup covers at most kMfmaMaxSteps * 16 k-blocks; beyond
+        // that minimum, small batches take more splits (more workgroups in
+        // flight) since their partial sums are cheap
+        int64_t min_splits = (kb + kMfmaKB * kMfmaMaxSteps - 1) / (kMfmaKB * kMfmaMaxSteps);
         int64_t row_tiles = (rows + kMfmaRows - 1) / kMfmaRows;
-        int64_t want = std::max<int64_t>(1, 512 / std::max<int64_t>(1, row_tiles));
-        return (int)std::max<int64_t>(1, std::min<int64_t>(want, kb / 4));
+        int64_t want = B <= 16 ? 2048 : 512;
+        int64_t splits = std::max<int64_t>(min_splits, want / std::max<int64_t>(1, row_tiles));
+        return (int)std::max<int64_t>(1, std::min<int64_t>(splits, (kb + kMfmaKB - 1) / kMfmaKB));
     }
     int TT = B >= 8 ? 8 : (B >= 4 ? 4 : (B >= 2 ? 2 : 1));
     int64_t row_chunks = (rows + kVlutThreads * kVlutRowsPerThread - 1) / (kVlutThreads * kVlutRowsPerThread);
@@ -411,9 +510,24 @@ int vlut_default_splits(int64_t rows, int64_t B, int64_t K, int method)
     return (int)std::max<int64_t>(1, std::min<int64_t>(want, kb));
 }
 
+hipError_t vlut_prepare(const uint16_t* words, int64_t n, int q, int legacy, uint32_t* prepared, hipStream_t s)
+{
+    if (n == 0) return hipSuccess;
+    const DecodeTables* t = nullptr;
+    hipError_t e = get_decode_tables(q, legacy, &t);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(vlut_prepare_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, words, n, t->cid_map,
+                       prepared);
+    return hipGetLastError();
+}
+
 hipError_t vlut_matmul(VlutMatmulArgs p, int method, int splits, hipStream_t s)
 {
     if (p.B == 0 || p.rows == 0) return hipSuccess;
+    if (method == VLUT_METHOD_MFMA) {
+        int64_t kb = p.K / 8;
+        if ((kb + splits - 1) / splits > (int64_t)kMfmaKB * kMfmaMaxSteps) return hipErrorInvalidValue;
+    }
     const DecodeTables* t = nullptr;
     hipError_t e = get_decode_tables(p.q, p.legacy, &t);
     if (e != hipSuccess) return e;

@@ -5,9 +5,10 @@ Mirrors coset/core/layers.py (StraightThroughQuantize 62-95, ste_quantize
 HNLQLinear 662) and the factory coset/core/e8/layers.py:15-66.
 
 When the injected ``quantize_fn`` is this package's ``e8_quantize`` (what the
-factory injects), the weight path scale -> STE quantize -> unscale -> clamp
-runs as one HIP kernel forward (coset_e8_qat_fwd) and one backward
-(coset_e8_qat_bwd) that re-decodes the saved packed codes; the dense
+factory injects), the weight path theta -> beta bounds -> scale -> STE
+quantize -> unscale -> clamp (and the step counter) runs as one HIP kernel
+forward (coset_e8_qat_fwd_theta) and one backward (coset_e8_qat_bwd_theta)
+that re-decodes the saved packed codes and returns dW and dtheta; the dense
 products go to hipBLASLt through F.linear.  Any other injected quantizer
 runs the reference composition around it.
 """
@@ -141,6 +142,51 @@ class E8WeightQuant(torch.autograd.Function):
                   _lib.ptr(packed), _lib.ptr(b), rows, cols, bpt, clip, int(q), int(M),
                   _lib.ptr(dW), _lib.ptr(dbeta), _lib.stream_of(Wc))
         return dW, dbeta.view(beta_shape), None, None, None, None, None
+
+
+class E8ThetaWeightQuant(torch.autograd.Function):
+    """The fused QAT weight path: beta from theta and the EMA buffers, scale,
+    quantize (M = 2), unscale, clamp and the step counter in one kernel
+    (coset_e8_qat_fwd_theta); the backward returns dW and dtheta from one
+    kernel (coset_e8_qat_bwd_theta).  The forward records beta and
+    d beta / d theta per tile, so later in-place updates of the EMA buffers
+    do not affect this step's gradient."""
+
+    @staticmethod
+    def forward(ctx, W, theta, sigma, xmax, step_count, bounds, q, M, clip, blocks_per_tile, out_dtype):
+        Wc = W.detach().contiguous()
+        th = theta.detach().contiguous()
+        rows, cols = Wc.shape
+        n = rows * (cols // 8)
+        Wq = torch.empty((rows, cols), dtype=out_dtype, device=Wc.device)
+        packed = torch.empty((n, M), dtype=word_dtype(q), device=Wc.device)
+        beta = torch.empty(th.numel(), dtype=torch.float32, device=Wc.device)
+        dbdt = torch.empty_like(beta)
+        delta0, eta, ginv, m_bounds = bounds
+        _lib.call("coset_e8_qat_fwd_theta", _lib.ptr(Wc), rows, cols, int(blocks_per_tile), _lib.ptr(th),
+                  _lib.ptr(sigma.contiguous()), _lib.ptr(xmax.contiguous()), float(delta0), float(eta),
+                  float(ginv), int(m_bounds), float(clip), int(q), int(M), _lib.ptr(Wq),
+                  _lib.dtype_code(out_dtype), _lib.ptr(packed), _lib.ptr(beta), _lib.ptr(dbdt),
+                  _lib.ptr(step_count), _lib.stream_of(Wc))
+        ctx.save_for_backward(Wc, packed, beta, dbdt)
+        ctx.cfg = (q, M, float(clip), int(blocks_per_tile), theta.shape)
+        return Wq
+
+    @staticmethod
+    def backward(ctx, g):
+        Wc, packed, beta, dbdt = ctx.saved_tensors
+        q, M, clip, bpt, theta_shape = ctx.cfg
+        if g.dtype not in (torch.float32, torch.bfloat16):
+            g = g.float()
+        g = g.contiguous()
+        rows, cols = Wc.shape
+        dW = torch.empty_like(Wc)
+        dbeta = torch.empty_like(beta)
+        dtheta = torch.empty_like(beta)
+        _lib.call("coset_e8_qat_bwd_theta", _lib.ptr(g), _lib.dtype_code(g.dtype), _lib.ptr(Wc), _lib.ptr(packed),
+                  _lib.ptr(beta), _lib.ptr(dbdt), rows, cols, bpt, clip, int(q), int(M), _lib.ptr(dW),
+                  _lib.ptr(dbeta), _lib.ptr(dtheta), _lib.stream_of(Wc))
+        return dW, dtheta.view(theta_shape), None, None, None, None, None, None, None, None, None
 
 
 class HNLQLinearQAT(nn.Module):
@@ -284,14 +330,16 @@ class HNLQLinearQAT(nn.Module):
         beta_min = torch.minimum(beta_min, beta_max * 0.9)
         return beta_min, beta_max
 
-    def _advance_step(self):
+    def _advance_step(self, device_increment: bool = True):
         """step_count += 1 and the every-256-steps statistics update
-        (layers.py:408-413), with the counter mirrored on the host."""
+        (layers.py:408-413), with the counter mirrored on the host.  The
+        fused kernel increments the device buffer itself."""
         if self._host_step is None:
             self._host_step = int(self.step_count)
         self._host_step += 1
-        with torch.no_grad():
-            self.step_count += 1
+        if device_increment:
+            with torch.no_grad():
+                self.step_count += 1
         if self._host_step % self.stat_update_interval == 0:
             W = self.weight.view(self.out_features, self.blocks_per_row, self.block_size)
             self._gather_stats(W.detach())
@@ -314,14 +362,17 @@ class HNLQLinearQAT(nn.Module):
             if self.enable_diagnostics:
                 self._weight_history.append(W.detach().clone())
             return W
-        self._advance_step()
-        beta = self._beta()
-        if self._fused():
+        fused = self._fused()
+        self._advance_step(device_increment=not fused)
+        if fused:
             bpt = self.blocks_per_row if self.tiling == "row" else 1
+            theta = self.theta_beta if self.tiling == "block" else self.theta_beta[: self.out_features]
             # the injected e8_quantize always encodes with M = 2 (codecs.py:245-254)
-            W_q = E8WeightQuant.apply(W, beta, self.q, 2, self.weight_clip_value, bpt, out_dtype)
+            W_q = E8ThetaWeightQuant.apply(W, theta, self.sigma_ema, self.xmax_ema, self.step_count,
+                                           (self.Delta0, self.eta, self._ginv_f, self.M), self.q, 2,
+                                           self.weight_clip_value, bpt, out_dtype)
         else:
-            W_q = self._reference_composition(W, beta).to(out_dtype)
+            W_q = self._reference_composition(W, self._beta()).to(out_dtype)
         if self.enable_diagnostics:
             self._weight_history.append(W.detach().clone())
             self._quantization_errors.append(torch.norm(W - W_q.float()).item())

@@ -190,12 +190,25 @@ def vlut_dot(words: torch.Tensor, vlut: torch.Tensor, q: int) -> torch.Tensor:
 _METHODS = {"auto": 0, "lds": 1, "mfma": 2}
 
 
+def vlut_prepare(words: torch.Tensor, q: int = 4, legacy: bool = False) -> torch.Tensor:
+    """uint16 level words [..., M] -> uint32 (coarse id << 16 | idx), same
+    shape: the weight format vlut_matmul reads without table lookups.  Done
+    once per weight; ``legacy`` must match the vlut_matmul call."""
+    w = on_gpu(words).contiguous()
+    if w.dtype != torch.uint16:
+        raise ValueError("vlut_prepare takes uint16 level words (q <= 4)")
+    out = torch.empty(w.shape, dtype=torch.uint32, device=w.device)
+    _lib.call("coset_vlut_prepare", _lib.ptr(w), w.numel(), int(q), int(legacy), _lib.ptr(out), _lib.stream_of(w))
+    return out
+
+
 def vlut_matmul(words: torch.Tensor, act: torch.Tensor, q: int = 4, *, scale: Optional[torch.Tensor] = None,
                 scale_mode: str = "mul", legacy: bool = False, method: str = "auto",
                 workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
     """out[B, rows] = s_o * sum_k sum_m q^m vLUT_{act[:, 8k:8k+8]}[words[o, k, m]].
 
-    words: packed level words [rows, K/8, M] (uint16, q in {2, 4}); act:
+    words: packed level words [rows, K/8, M] (uint16, q in {2, 4}), or their
+    ``vlut_prepare`` form (uint32, prepared with the same ``legacy``); act:
     [B, K] float32 / bfloat16 / float16.  scale (per output row) multiplies
     (``scale_mode="mul"``, codec convention) or divides (``"div"``, layer
     convention).  With the core rule (legacy=False) the result equals
@@ -218,7 +231,8 @@ def vlut_matmul(words: torch.Tensor, act: torch.Tensor, q: int = 4, *, scale: Op
     if scale is not None:
         s = on_gpu(scale).float().contiguous()
     out = torch.empty((B, rows), dtype=torch.float32, device=a.device)
-    _lib.call("coset_vlut_matmul", _lib.ptr(w), _lib.ptr(s), 0 if scale_mode == "mul" else 1, _lib.ptr(a), dt,
+    fmt = 1 if w.dtype == torch.uint32 else 0
+    _lib.call("coset_vlut_matmul", _lib.ptr(w), fmt, _lib.ptr(s), 0 if scale_mode == "mul" else 1, _lib.ptr(a), dt,
               B, rows, K, int(q), int(M), int(legacy), m, _lib.ptr(workspace), workspace.numel(),
               _lib.ptr(out), _lib.stream_of(a))
     return out

@@ -135,6 +135,26 @@ int coset_e8_qat_bwd(const void* gWq, int g_dtype, const float* W, const void* p
                      const float* beta, int64_t rows, int64_t cols, int64_t blocks_per_tile,
                      float clip, int q, int M, float* dW, float* dbeta, void* stream);
 
+/* Same forward with beta computed in the kernel from the layer's theta and
+ * EMA buffers (coset/core/layers.py:381-396, 418-422: beta = beta_min +
+ * sigmoid(theta)(beta_max - beta_min), one entry per tile), so a QAT step
+ * needs no separate launches for the bounds.  beta_out and dbeta_dtheta_out
+ * (nullable, [tiles]) receive the beta used and (beta_max - beta_min) s (1 - s),
+ * s = sigmoid(theta); step_counter (nullable, int64 device scalar: the layer's
+ * step_count buffer) is incremented once.  M_bounds is the layer's M (the
+ * bounds' q^M); M is the codec depth (2: e8_quantize, codecs.py:245-254). */
+int coset_e8_qat_fwd_theta(const float* W, int64_t rows, int64_t cols, int64_t blocks_per_tile,
+                           const float* theta, const float* sigma_ema, const float* xmax_ema, double delta0,
+                           double eta, double gamma_inv, int M_bounds, float clip, int q, int M, void* Wq,
+                           int wq_dtype, void* packed, float* beta_out, float* dbeta_dtheta_out,
+                           int64_t* step_counter, void* stream);
+
+/* Backward of coset_e8_qat_fwd_theta: dW and dbeta as coset_e8_qat_bwd, plus
+ * dtheta[t] = dbeta[t] * dbeta_dtheta[t] (the factor the forward recorded). */
+int coset_e8_qat_bwd_theta(const void* gWq, int g_dtype, const float* W, const void* packed, const float* beta,
+                           const float* dbeta_dtheta, int64_t rows, int64_t cols, int64_t blocks_per_tile,
+                           float clip, int q, int M, float* dW, float* dbeta, float* dtheta, void* stream);
+
 /* One-sided vLUTs (coset/legacy/quant/vlut.py:72-117): for each query
  * a[i, 0:8] writes vlut[i, idx] = <a, r(b_idx)> for all q^8 level words in
  * lexicographic order, r(b) = G b - q P(G b / q).  legacy=1 uses the legacy
@@ -147,8 +167,16 @@ int coset_vlut_build_one_sided(const float* queries, int64_t n_queries, int q, i
 int coset_vlut_lookup_dot(const void* words, int64_t n_blocks, int q, int M, const float* vlut, float* out,
                           void* stream);
 
+/* Weight preparation for coset_vlut_matmul (once per weight): prepared[i] =
+ * cid << 16 | words[i], cid the id of the coarse point c(b) the uint16 level
+ * word decodes through (core rule, or legacy with legacy=1), so the matmul
+ * reads it instead of gathering from the per-device map. */
+int coset_vlut_prepare(const void* words, int64_t n_words, int q, int legacy, uint32_t* prepared, void* stream);
+
 /* vLUT matmul: out[t, o] = s_o * sum_k sum_m q^m vLUT_{act[t, 8k:8k+8]}[words[o, k, m]]
- * for uint16 level words [rows, K/8, M] (q in {2, 4}, M <= 4), activations
+ * for level words [rows, K/8, M] (q in {2, 4}, M <= 4): uint16 idx
+ * (word_format 0) or coset_vlut_prepare output (word_format 1, same legacy
+ * flag), activations
  * [B, K] fp32/bf16/fp16, s_o = scale[o] (scale_mode 0), 1/scale[o] (1) or 1
  * (scale NULL).  method 1 keeps per-(token, k-block) factorized tables
  * <a, g_j>, <a, c> in LDS; method 2 decodes 2*x_hat into LDS and runs the
@@ -157,8 +185,8 @@ int coset_vlut_lookup_dot(const void* words, int64_t n_blocks, int q, int M, con
  * The reference has no matmul routine; its placeholder QLinear._lut_matmul is
  * coset/legacy/nn/qlinear.py:272-281. */
 int64_t coset_vlut_workspace_floats(int64_t B, int64_t rows, int64_t K, int q, int M, int act_dtype, int method);
-int coset_vlut_matmul(const void* words, const float* scale, int scale_mode, const void* act, int act_dtype,
-                      int64_t B, int64_t rows, int64_t K, int q, int M, int legacy, int method,
+int coset_vlut_matmul(const void* words, int word_format, const float* scale, int scale_mode, const void* act,
+                      int act_dtype, int64_t B, int64_t rows, int64_t K, int q, int M, int legacy, int method,
                       float* workspace, int64_t workspace_floats, float* out, void* stream);
 
 /* Elementwise lattice operator over n_blocks fp32 blocks (custom_round is

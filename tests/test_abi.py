@@ -44,7 +44,7 @@ def test_host_side_validation_without_gpu():
     rc = lib.coset_e8_hnlq_roundtrip(None, 0, 4, 0, 1.0, None, 0, 0.0, None, 0, 17, 2, 0, None, None, None, 0,
                                      None)
     assert rc == _lib.EINVAL and b"q=17" in lib.coset_last_error()
-    rc = lib.coset_vlut_matmul(None, None, 0, None, 0, 1, 1, 8, 3, 2, 0, 0, None, 0, None, None)
+    rc = lib.coset_vlut_matmul(None, 0, None, 0, None, 0, 1, 1, 8, 3, 2, 0, 0, None, 0, None, None)
     assert rc == _lib.EUNSUPPORTED
 
 

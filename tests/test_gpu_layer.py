@@ -163,3 +163,33 @@ def test_state_dict_roundtrip():
     assert int(b.step_count) == 2
     ex = b.export_quantized()
     assert ex["codes"].shape == (32, 2) and ex["weight"].shape == (8, 32)
+
+
+@pytest.mark.parametrize("tiling", ["row", "block"])
+def test_fused_theta_path_matches_torch_beta_path(tiling):
+    """The in-kernel beta (theta, EMA buffers) equals the torch composition of
+    _bounds/_beta to 1 ulp-level tolerance, and dtheta equals autograd through
+    it; W_q is bit-equal wherever beta is."""
+    import coset_amd
+    from coset_amd import E8WeightQuant
+    torch.manual_seed(3)
+    layer = coset_amd.create_e8_hnlq_linear(128, 24, Delta0=1.5, tiling=tiling)
+    with torch.no_grad():
+        layer.theta_beta.uniform_(-3, 3)
+        layer.sigma_ema.uniform_(0.5, 2.0)
+        layer.xmax_ema.uniform_(1.0, 4.0)
+    Wq = layer._quantize_weights()
+    g = torch.randn_like(Wq)
+    (Wq * g).sum().backward()
+    dtheta_fused = layer.theta_beta.grad.clone()
+    dW_fused = layer.weight.grad.clone()
+    layer.zero_grad()
+    beta = layer._beta()
+    bpt = 16 if tiling == "row" else 1
+    Wq2 = E8WeightQuant.apply(layer.weight, beta, 4, 2, 2.0, bpt, torch.float32)
+    (Wq2 * g).sum().backward()
+    close(dtheta_fused.cpu().numpy(), layer.theta_beta.grad.cpu().numpy(), 1e-5)
+    close(dW_fused.cpu().numpy(), layer.weight.grad.cpu().numpy(), 1e-6)
+    diff = (Wq != Wq2).float().mean().item()
+    assert diff < 1e-3, diff
+    assert int(layer.step_count) == 1

@@ -96,12 +96,14 @@ def test_vlut_matmul_vs_oracle(method, B, adt):
     words = torch.from_numpy(words_np.astype(np.int32)).to(torch.uint16).cuda()
     a = torch.from_numpy(rng.standard_normal((B, K)).astype(np.float32)).to(adt)
     for legacy in (False, True):
+        prepared = coset_amd.vlut_prepare(words, q, legacy=legacy)
         for mode in ("mul", "div"):
-            out = coset_amd.vlut_matmul(words, a.cuda(), q, scale=torch.from_numpy(scale), scale_mode=mode,
-                                        legacy=legacy, method=method).cpu().numpy()
             sm = 0 if mode == "mul" else 1
             ref = O.vlut_matmul(words_np, scale, a.float().numpy(), q, M, scale_mode=sm, legacy=legacy)
-            close(out, ref, 1e-3)
+            for w in (words, prepared):
+                out = coset_amd.vlut_matmul(w, a.cuda(), q, scale=torch.from_numpy(scale), scale_mode=mode,
+                                            legacy=legacy, method=method).cpu().numpy()
+                close(out, ref, 1e-3)
 
 
 def test_c4_full_size_equals_decoded_product():
@@ -111,11 +113,13 @@ def test_c4_full_size_equals_decoded_product():
     g = torch.Generator(device="cuda").manual_seed(5)
     W = 0.02 * torch.randn((4096, 4096), device="cuda", generator=g)
     words = coset_amd.hnlq_encode(W.reshape(-1, 8), 4, 2, 0.02).reshape(4096, 512, 2)
+    prepared = coset_amd.vlut_prepare(words, 4)
     dec = coset_amd.hnlq_decode(words.reshape(-1, 2), 4, 2, 0.02).reshape(4096, 4096)
     for B in (1, 8, 64):
         a = torch.randn((B, 4096), device="cuda", generator=g).to(torch.float16)
         ref = (a.double() @ dec.double().T).float()
         for method in ("lds", "mfma"):
-            out = coset_amd.vlut_matmul(words, a, 4, scale=torch.full((4096,), 0.02), method=method)
-            err = (out - ref).abs().max().item()
-            assert err <= 1e-3 * ref.abs().max().item(), (B, method, err)
+            for w in (words, prepared):
+                out = coset_amd.vlut_matmul(w, a, 4, scale=torch.full((4096,), 0.02), method=method)
+                err = (out - ref).abs().max().item()
+                assert err <= 1e-3 * ref.abs().max().item(), (B, method, w.dtype, err)
