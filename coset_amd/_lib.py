@@ -53,6 +53,8 @@ SIGNATURES = {
 }
 
 OPT_CODEC_PATH = 1
+OPT_VLUT_DECODE = 2
+OPT_VLUT_SPLITS = 3
 CODEC_AUTO, CODEC_GENERIC, CODEC_LUT = 0, 1, 2
 
 _lib = None
@@ -129,6 +131,16 @@ def require_gpu() -> torch.device:
 def set_codec_path(path: int) -> None:
     """0 automatic, 1 generic kernel, 2 LDS-table kernel (q = 2, 4)."""
     call("coset_set_option", OPT_CODEC_PATH, int(path))
+
+
+def set_vlut_decode(byte_tables: bool) -> None:
+    """MFMA vLUT decode through byte tables (default) or integer digits."""
+    call("coset_set_option", OPT_VLUT_DECODE, int(bool(byte_tables)))
+
+
+def set_vlut_splits(splits: int) -> None:
+    """0 automatic, n > 0 forces the vLUT matmul's K splits."""
+    call("coset_set_option", OPT_VLUT_SPLITS, int(splits))
 
 
 def dtype_code(dt: torch.dtype) -> int:

@@ -85,6 +85,14 @@ int coset_set_option(int key, int value)
         if (value < 0 || value > 2) return fail(COSET_EINVAL, "codec path %d not in {0,1,2}", value);
         coset::g_codec_path = value;
         return COSET_OK;
+    case COSET_OPT_VLUT_DECODE:
+        if (value < 0 || value > 1) return fail(COSET_EINVAL, "vLUT decode %d not in {0,1}", value);
+        coset::g_vlut_swar = value;
+        return COSET_OK;
+    case COSET_OPT_VLUT_SPLITS:
+        if (value < 0) return fail(COSET_EINVAL, "vLUT splits %d < 0", value);
+        coset::g_vlut_splits = value;
+        return COSET_OK;
     default: return fail(COSET_EINVAL, "unknown option %d", key);
     }
 }

@@ -14,6 +14,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <array>
 #include <map>
 #include <mutex>
 #include <vector>
@@ -47,6 +48,84 @@ __global__ void __launch_bounds__(256) coarse_key_kernel(int q, uint32_t n, uint
 
 namespace {
 
+// U(b) = 2 G b for the digit vector of idx (same rows as lattice_point).
+void two_gb(uint32_t idx, int q, int u[8])
+{
+    int b[8];
+    for (int j = 7; j >= 0; --j) {
+        b[j] = (int)(idx % (uint32_t)q);
+        idx /= (uint32_t)q;
+    }
+    u[0] = 4 * b[0] - 2 * b[1] + b[7];
+    for (int j = 1; j < 6; ++j) u[j] = 2 * (b[j] - b[j + 1]) + b[7];
+    u[6] = 2 * b[6] + b[7];
+    u[7] = b[7];
+}
+
+uint64_t pack_bytes(const int v[8], int bias)
+{
+    uint64_t w = 0;
+    for (int j = 0; j < 8; ++j) w |= (uint64_t)(uint8_t)(v[j] + bias) << (8 * j);
+    return w;
+}
+
+// Byte tables of the SWAR decode and the levels they can combine.
+void build_swar(int q, uint32_t n, const std::vector<uint16_t>& map, const std::vector<uint64_t>& coarse,
+                std::vector<uint64_t>& swar, int* max_m, int bias[5])
+{
+    int hi[256][8], lo[256][8];
+    std::vector<std::array<int, 8>> cc(coarse.size());
+    int min_hi = 0, max_hi = 0, min_lo = 0, max_lo = 0, min_c = 0, max_c = 0;
+    for (int h = 0; h < 256; ++h) {
+        if (q == 4)
+            two_gb((uint32_t)h << 8, q, hi[h]);
+        else
+            for (int j = 0; j < 8; ++j) hi[h][j] = 0;  // q = 2 words fit in the low byte
+        two_gb((uint32_t)h, q, lo[h]);
+        for (int j = 0; j < 8; ++j) {
+            min_hi = std::min(min_hi, hi[h][j]);
+            max_hi = std::max(max_hi, hi[h][j]);
+            min_lo = std::min(min_lo, lo[h][j]);
+            max_lo = std::max(max_lo, lo[h][j]);
+        }
+    }
+    for (size_t c = 0; c < coarse.size(); ++c)
+        for (int j = 0; j < 8; ++j) {
+            cc[c][j] = -q * (int)(int8_t)(uint8_t)(coarse[c] >> (8 * j));
+            min_c = std::min(min_c, cc[c][j]);
+            max_c = std::max(max_c, cc[c][j]);
+        }
+    int r_max = -1 << 20;  // largest coordinate of 2r over all words
+    for (uint32_t i = 0; i < n; ++i) {
+        int u[8];
+        two_gb(i, q, u);
+        for (int j = 0; j < 8; ++j) r_max = std::max(r_max, u[j] + cc[map[i]][j]);
+    }
+    const int b_hi = -min_hi, b_lo = -min_lo, b_c = -min_c, b_l = b_hi + b_lo + b_c;
+    swar.resize(512 + coarse.size());
+    for (int h = 0; h < 256; ++h) {
+        swar[h] = pack_bytes(hi[h], b_hi);
+        swar[256 + h] = pack_bytes(lo[h], b_lo);
+    }
+    for (size_t c = 0; c < coarse.size(); ++c) swar[512 + c] = pack_bytes(cc[c].data(), b_c);
+    // partial sums: T_hi + T_lo, then + C (= 2r + b_l)
+    bool ok = max_hi + b_hi + max_lo + b_lo <= 255 && max_c + b_c <= 255 && r_max + b_l <= 255;
+    const int l_max = r_max + b_l;
+    int acc = l_max, off = b_l;
+    *max_m = 0;
+    for (int m = 1; m <= 4 && ok; ++m) {
+        if (m > 1) {
+            ok = acc * q <= 255 && acc * q + l_max <= 255;
+            acc = acc * q + l_max;
+            off = off * q + b_l;
+        }
+        if (ok) {
+            *max_m = m;
+            bias[m] = off;
+        }
+    }
+}
+
 struct Slot {
     std::once_flag once;
     DecodeTables t{};
@@ -67,7 +146,7 @@ hipError_t build(int device, int q, int legacy, DecodeTables* out)
     uint32_t* d_keys = nullptr;
     std::vector<uint32_t> keys(n);
     std::vector<uint16_t> map(n);
-    std::vector<uint64_t> coarse;
+    std::vector<uint64_t> coarse, swar;
     if ((e = hipMalloc(&d_keys, n * sizeof(uint32_t))) != hipSuccess) goto done;
     if (legacy)
         hipLaunchKernelGGL(coarse_key_kernel<true>, dim3((n + 255) / 256), dim3(256), 0, nullptr, q, n, d_keys);
@@ -95,12 +174,16 @@ hipError_t build(int device, int q, int legacy, DecodeTables* out)
             coarse[c] = packed;
         }
     }
+    build_swar(q, n, map, coarse, swar, &out->swar_max_m, out->swar_bias);
     out->q = q;
     out->n_codes = n;
     out->n_coarse = (int)coarse.size();
     if ((e = hipMalloc((void**)&out->cid_map, n * sizeof(uint16_t))) != hipSuccess) goto done;
     if ((e = hipMalloc((void**)&out->coarse, coarse.size() * sizeof(uint64_t))) != hipSuccess) goto done;
+    if ((e = hipMalloc((void**)&out->swar, swar.size() * sizeof(uint64_t))) != hipSuccess) goto done;
     if ((e = hipMemcpy((void*)out->cid_map, map.data(), n * sizeof(uint16_t), hipMemcpyHostToDevice)) != hipSuccess) goto done;
+    if ((e = hipMemcpy((void*)out->swar, swar.data(), swar.size() * sizeof(uint64_t), hipMemcpyHostToDevice)) != hipSuccess)
+        goto done;
     e = hipMemcpy((void*)out->coarse, coarse.data(), coarse.size() * sizeof(uint64_t), hipMemcpyHostToDevice);
 done:
     if (d_keys) (void)hipFree(d_keys);

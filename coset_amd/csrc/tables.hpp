@@ -14,6 +14,18 @@ struct DecodeTables {
     int n_coarse;
     const uint16_t* cid_map;  // [n_codes]
     const uint64_t* coarse;   // [n_coarse], 8 x int8 of 2c
+    // Byte-lane (SWAR) form of 2r = U(b) - q (2c), U(b) = 2Gb split over the
+    // two bytes of the level word (U is linear in the digits):
+    //   swar[h]         U(digits of h << 8) + bias_hi   (q = 4; zero for q = 2)
+    //   swar[256 + l]   U(digits of l) + bias_lo
+    //   swar[512 + c]   -q (2c) + bias_c
+    // as 8 unsigned bytes (byte j = coordinate j).  Every entry and every
+    // partial sum stays in [0, 255], so the three are added as two 32-bit
+    // words with no carry between bytes; M levels combine as acc = acc*q + L_m
+    // while swar_max_m allows it, leaving 2 x_hat + swar_bias[M] per byte.
+    const uint64_t* swar;     // [512 + n_coarse]
+    int swar_max_m;           // largest M whose combined bytes stay < 256 (0: none)
+    int swar_bias[5];         // byte offset of 2 x_hat after combining M levels
 };
 
 // Tables of the core (legacy = 0) or legacy residual rule for q in {2, 4} on

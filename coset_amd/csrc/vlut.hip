@@ -231,12 +231,20 @@ __global__ void __launch_bounds__(kVlutThreads) vlut_lds_kernel(VlutMatmulArgs p
 }
 
 // ---------------------------------------------------------------- MFMA matmul
-// Tile: 64 output rows x up to 64 tokens per workgroup (4 waves, one 16-row
+// Tile: 64 output rows x up to NT tokens per workgroup (4 waves, one 16-row
 // slice each), K split over grid.y.  A step covers 16 k-blocks (128 K):
-// every thread decodes 4 (row, k-block) pairs to 8 halves of 2*x_hat in LDS
-// (the 4 word loads and table gathers are issued together), the activation
-// tile [tokens x 128] is staged in LDS with 16-byte loads, then each wave runs
-// 8 K-slices of 16x16x16 MFMAs per 16-token sub-tile.
+// every thread decodes 4 (row, k-block) pairs to 8 halves of 2*x_hat in LDS,
+// the activation tile [NT x 128] is staged in LDS with 16-byte loads, then
+// each wave runs 8 K-slices of 16x16x16 MFMAs per 16-token sub-tile.  All
+// level words of the workgroup are loaded before the first step.
+//
+// Decode (SWAR): the three byte tables of 2r (tables.hpp) are added as two
+// 32-bit words per level, levels combine as acc = acc*q + L_m, and each byte
+// b = 2x + bias becomes a half through the bit pattern 0x64bb (= 1024 + b)
+// minus (1024 + bias), exact as every value is an integer below 2048.
+// Decode (integer): 2x = sum_m q^m (2Gb - q (2c)) with the digits unpacked,
+// for the (q, M) whose bytes would overflow.
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef short bf16x4_t __attribute__((ext_vector_type(4)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
@@ -246,13 +254,21 @@ constexpr int kMfmaKB = 16;              // k-blocks per step
 constexpr int kMfmaK = kMfmaKB * 8;      // 128 K values per step
 constexpr int kMfmaLd = kMfmaK + 8;      // row pitch in halves (16-byte aligned, skews banks)
 constexpr int kMfmaMaxSteps = 4;         // steps per workgroup: its K range is <= 64 k-blocks
+constexpr int kSwarSlots = 512 + kMaxCoarseVlut;
 
-template <int Q, int M, bool BF16>
+// two halves (bit patterns 0x64bb) from bytes k, k+1 of w
+__device__ __forceinline__ uint32_t bytes_to_f16_bits(uint32_t w, bool upper)
+{
+    return __builtin_amdgcn_perm(0x64646464u, w, upper ? 0x04030402u : 0x04010400u);
+}
+
+template <int Q, int M, bool BF16, bool SWAR, int NT>
 __global__ void __launch_bounds__(256) vlut_mfma_kernel(VlutMatmulArgs p)
 {
+    constexpr int kTSub = NT / 16;
     __shared__ __align__(16) uint16_t s_b[kMfmaRows][kMfmaLd];
-    __shared__ __align__(16) uint16_t s_a[64][kMfmaLd];
-    __shared__ uint64_t s_coarse[kMaxCoarseVlut];
+    __shared__ __align__(16) uint16_t s_a[NT][kMfmaLd];
+    __shared__ uint64_t s_tab[SWAR ? kSwarSlots : kMaxCoarseVlut];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
 
@@ -262,16 +278,14 @@ __global__ void __launch_bounds__(256) vlut_mfma_kernel(VlutMatmulArgs p)
     const int64_t k_end = min(kb_total, k_begin + ks_len);
     const int n_steps = (int)min((int64_t)kMfmaMaxSteps, (k_end - k_begin + kMfmaKB - 1) / kMfmaKB);
     const int64_t r0 = (int64_t)blockIdx.x * kMfmaRows;
-    const int64_t t_base = (int64_t)blockIdx.z * 64;
-    const int nt = (int)min((int64_t)64, p.B - t_base);
+    const int64_t t_base = (int64_t)blockIdx.z * NT;
+    const int nt = (int)min((int64_t)NT, p.B - t_base);
     const int n_tsub = (nt + 15) / 16;
     const uint16_t* act = reinterpret_cast<const uint16_t*>(p.act);
 
-    // All level words and coarse ids of this workgroup's tile are requested
-    // up front (4 pairs per thread per step, pair = (row pr/16, k-block pr%16)),
-    // so the global latency is paid once, not once per step.
+    // (row pr/16, k-block pr%16) pairs, 4 per thread per step; a word is kept
+    // as cid << 16 | idx, all-ones marking a pair outside the matrix
     uint32_t words[kMfmaMaxSteps][4][M];
-    uint32_t cids[kMfmaMaxSteps][4][M];
 #pragma unroll
     for (int st = 0; st < kMfmaMaxSteps; ++st) {
 #pragma unroll
@@ -282,26 +296,38 @@ __global__ void __launch_bounds__(256) vlut_mfma_kernel(VlutMatmulArgs p)
             const bool ok = st < n_steps && row < p.rows && kb < k_end;
 #pragma unroll
             for (int m = 0; m < M; ++m) {
-                uint32_t w = 0xffffffffu, c = 0u;
-                if (ok) load_word(p, (row * kb_total + kb) * M + m, &w, &c);
-                words[st][i][m] = w;
-                cids[st][i][m] = c;
+                uint32_t v = 0xffffffffu;
+                if (ok) {
+                    const int64_t wi = (row * kb_total + kb) * M + m;
+                    if (p.prepared) {
+                        v = reinterpret_cast<const uint32_t*>(p.words)[wi];
+                    } else {
+                        const uint32_t w = reinterpret_cast<const uint16_t*>(p.words)[wi];
+                        v = ((uint32_t)p.map[w] << 16) | w;
+                    }
+                }
+                words[st][i][m] = v;
             }
         }
     }
 
-    float4_t acc[4];
+    float4_t acc[kTSub];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) acc[s] = (float4_t){0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < kTSub; ++s) acc[s] = (float4_t){0.f, 0.f, 0.f, 0.f};
 
-    // the coarse table is staged after the word loads are in flight, so the
-    // wait for it overlaps their latency
-    for (int i = threadIdx.x; i < p.n_coarse; i += 256) s_coarse[i] = p.coarse[i];
+    // tables are staged while the word loads are in flight
+    if (SWAR) {
+        for (int i = threadIdx.x; i < 512 + p.n_coarse; i += 256) s_tab[i] = p.swar[i];
+    } else {
+        for (int i = threadIdx.x; i < p.n_coarse; i += 256) s_tab[i] = p.coarse[i];
+    }
+    const _Float16 f16_off = (_Float16)(1024 + p.swar_bias);
+    const float f32_off = (float)p.swar_bias;
 
-    uint4 av[4];
+    uint4 av[NT / 16];
     auto load_act_tile = [&](int st) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < NT / 16; ++j) {
             const int idx = threadIdx.x + 256 * j;
             const int tok = idx >> 4, seg = idx & 15;
             const int64_t kb = k_begin + st * kMfmaKB + seg;
@@ -315,52 +341,91 @@ __global__ void __launch_bounds__(256) vlut_mfma_kernel(VlutMatmulArgs p)
 #pragma unroll
     for (int st = 0; st < kMfmaMaxSteps; ++st) {
         if (st >= n_steps) break;
-        __syncthreads();  // the previous step's MFMAs are done with s_a / s_b
+        __syncthreads();  // the previous step's MFMAs are done with s_a / s_b (first step: s_tab is written)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < NT / 16; ++j) {
             const int idx = threadIdx.x + 256 * j;
             *reinterpret_cast<uint4*>(&s_a[idx >> 4][(idx & 15) * 8]) = av[j];
         }
         if (st + 1 < n_steps) load_act_tile(st + 1);  // in flight during decode and MFMAs
-        // decode 2 x_hat = sum_m q^m (2Gb - q (2c)) -> halves
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            int two_x[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) two_x[j] = 0;
-            int wq = 1;
             const bool ok = words[st][i][0] != 0xffffffffu;
-#pragma unroll
-            for (int m = 0; m < M; ++m) {
-                int b[8];
-                unpack_word<Q>(ok ? words[st][i][m] : 0u, Q, b);
-                const uint64_t c = s_coarse[cids[st][i][m]];
-                int u[8];
-                u[0] = 4 * b[0] - 2 * b[1] + b[7];
-#pragma unroll
-                for (int j = 1; j < 6; ++j) u[j] = 2 * (b[j] - b[j + 1]) + b[7];
-                u[6] = 2 * b[6] + b[7];
-                u[7] = b[7];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) two_x[j] += wq * (u[j] - Q * (int)(int8_t)(uint8_t)(c >> (8 * j)));
-                wq *= Q;
-            }
             uint32_t hv[4];
+            if (SWAR) {
+                uint32_t x0 = 0u, x1 = 0u;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                uint32_t lo, hi;
-                if (BF16) {  // exact: |2x| < 256
-                    lo = __float_as_uint((float)two_x[2 * j]) >> 16;
-                    hi = __float_as_uint((float)two_x[2 * j + 1]) >> 16;
-                } else {     // exact: |2x| < 2048
-                    _Float16 l = (_Float16)two_x[2 * j], h = (_Float16)two_x[2 * j + 1];
-                    lo = __builtin_bit_cast(uint16_t, l);
-                    hi = __builtin_bit_cast(uint16_t, h);
+                for (int m = M - 1; m >= 0; --m) {
+                    const uint32_t v = ok ? words[st][i][m] : 0u;
+                    const uint2 tl = *reinterpret_cast<const uint2*>(&s_tab[256 + (v & 0xffu)]);
+                    const uint2 tc = *reinterpret_cast<const uint2*>(&s_tab[512 + (v >> 16)]);
+                    uint32_t l0 = tl.x + tc.x, l1 = tl.y + tc.y;
+                    if (Q != 2) {
+                        const uint2 th = *reinterpret_cast<const uint2*>(&s_tab[(v >> 8) & 0xffu]);
+                        l0 += th.x;
+                        l1 += th.y;
+                    }
+                    x0 = x0 * Q + l0;
+                    x1 = x1 * Q + l1;
                 }
-                hv[j] = ok ? (lo | (hi << 16)) : 0u;
+                if (BF16) {
+                    float f[8];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        f[j] = (float)((x0 >> (8 * j)) & 0xffu) - f32_off;
+                        f[4 + j] = (float)((x1 >> (8 * j)) & 0xffu) - f32_off;
+                    }
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)  // exact: small integers
+                        hv[j] = __builtin_amdgcn_perm(__float_as_uint(f[2 * j + 1]), __float_as_uint(f[2 * j]),
+                                                      0x07060302u);
+                } else {
+                    const uint32_t raw[4] = {bytes_to_f16_bits(x0, false), bytes_to_f16_bits(x0, true),
+                                             bytes_to_f16_bits(x1, false), bytes_to_f16_bits(x1, true)};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        half2_t h = __builtin_bit_cast(half2_t, raw[j]) - (half2_t){f16_off, f16_off};
+                        hv[j] = __builtin_bit_cast(uint32_t, h);
+                    }
+                }
+            } else {
+                int two_x[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) two_x[j] = 0;
+                int wq = 1;
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const uint32_t v = ok ? words[st][i][m] : 0u;
+                    int b[8];
+                    unpack_word<Q>(v & 0xffffu, Q, b);
+                    const uint64_t c = s_tab[v >> 16];
+                    int u[8];
+                    u[0] = 4 * b[0] - 2 * b[1] + b[7];
+#pragma unroll
+                    for (int j = 1; j < 6; ++j) u[j] = 2 * (b[j] - b[j + 1]) + b[7];
+                    u[6] = 2 * b[6] + b[7];
+                    u[7] = b[7];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) two_x[j] += wq * (u[j] - Q * (int)(int8_t)(uint8_t)(c >> (8 * j)));
+                    wq *= Q;
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    uint32_t lo, hi;
+                    if (BF16) {  // exact: |2x| < 256
+                        lo = __float_as_uint((float)two_x[2 * j]) >> 16;
+                        hi = __float_as_uint((float)two_x[2 * j + 1]) >> 16;
+                    } else {     // exact: |2x| < 2048
+                        _Float16 l = (_Float16)two_x[2 * j], h = (_Float16)two_x[2 * j + 1];
+                        lo = __builtin_bit_cast(uint16_t, l);
+                        hi = __builtin_bit_cast(uint16_t, h);
+                    }
+                    hv[j] = lo | (hi << 16);
+                }
             }
             const int pr = threadIdx.x + 256 * i;
-            *reinterpret_cast<uint4*>(&s_b[pr >> 4][(pr & 15) * 8]) = make_uint4(hv[0], hv[1], hv[2], hv[3]);
+            *reinterpret_cast<uint4*>(&s_b[pr >> 4][(pr & 15) * 8]) =
+                ok ? make_uint4(hv[0], hv[1], hv[2], hv[3]) : make_uint4(0u, 0u, 0u, 0u);
         }
         __syncthreads();
         // D[token][row] += A[token][k] * B[k][row]
@@ -369,7 +434,9 @@ __global__ void __launch_bounds__(256) vlut_mfma_kernel(VlutMatmulArgs p)
         for (int kk = 0; kk < kMfmaK / 16; ++kk) {
             const int kof = kk * 16 + 4 * (lane >> 4);
             uint2 bv = *reinterpret_cast<const uint2*>(&s_b[brow][kof]);
-            for (int s = 0; s < n_tsub; ++s) {
+#pragma unroll
+            for (int s = 0; s < kTSub; ++s) {
+                if (s >= n_tsub) break;
                 uint2 a2 = *reinterpret_cast<const uint2*>(&s_a[s * 16 + (lane & 15)][kof]);
                 if (BF16) {
                     acc[s] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4_t, a2),
@@ -384,7 +451,9 @@ __global__ void __launch_bounds__(256) vlut_mfma_kernel(VlutMatmulArgs p)
     // D[token = 16 s + 4 (lane/16) + i][row = 16 wave + lane%16]
     const int64_t row = r0 + wave * 16 + (lane & 15);
     if (row < p.rows) {
-        for (int s = 0; s < n_tsub; ++s) {
+#pragma unroll
+        for (int s = 0; s < kTSub; ++s) {
+            if (s >= n_tsub) break;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 int64_t tok = t_base + s * 16 + 4 * (lane >> 4) + i;
@@ -435,14 +504,30 @@ hipError_t launch_lds(VlutMatmulArgs p, int splits, hipStream_t s)
     return hipGetLastError();
 }
 
+template <int Q, int M, bool SWAR, int NT>
+void launch_mfma_nt(const VlutMatmulArgs& p, int splits, hipStream_t s)
+{
+    dim3 grid((unsigned)((p.rows + kMfmaRows - 1) / kMfmaRows), (unsigned)splits, (unsigned)((p.B + NT - 1) / NT));
+    if (p.act_dtype == DT_BF16)
+        hipLaunchKernelGGL((vlut_mfma_kernel<Q, M, true, SWAR, NT>), grid, dim3(256), 0, s, p);
+    else
+        hipLaunchKernelGGL((vlut_mfma_kernel<Q, M, false, SWAR, NT>), grid, dim3(256), 0, s, p);
+}
+
 template <int Q, int M>
 hipError_t launch_mfma(const VlutMatmulArgs& p, int splits, hipStream_t s)
 {
-    dim3 grid((unsigned)((p.rows + kMfmaRows - 1) / kMfmaRows), (unsigned)splits, (unsigned)((p.B + 63) / 64));
-    if (p.act_dtype == DT_BF16)
-        hipLaunchKernelGGL((vlut_mfma_kernel<Q, M, true>), grid, dim3(256), 0, s, p);
-    else
-        hipLaunchKernelGGL((vlut_mfma_kernel<Q, M, false>), grid, dim3(256), 0, s, p);
+    // byte decode where the tables allow it (q = 4: M <= 2, q = 2: M <= 4)
+    if constexpr (Q == 2 || M <= 2) {
+        if (p.swar_ok) {
+            if (p.B <= 16)
+                launch_mfma_nt<Q, M, true, 16>(p, splits, s);
+            else
+                launch_mfma_nt<Q, M, true, 64>(p, splits, s);
+            return hipGetLastError();
+        }
+    }
+    launch_mfma_nt<Q, M, false, 64>(p, splits, s);
     return hipGetLastError();
 }
 
@@ -490,6 +575,9 @@ hipError_t vlut_dot(const void* words, int64_t n, int M, int q, const float* vlu
     return hipGetLastError();
 }
 
+int g_vlut_swar = 1;
+int g_vlut_splits = 0;
+
 int vlut_default_splits(int64_t rows, int64_t B, int64_t K, int method)
 {
     int64_t kb = K / 8;
@@ -498,15 +586,17 @@ int vlut_default_splits(int64_t rows, int64_t B, int64_t K, int method)
         // that minimum, small batches take more splits (more workgroups in
         // flight) since their partial sums are cheap
         int64_t min_splits = (kb + kMfmaKB * kMfmaMaxSteps - 1) / (kMfmaKB * kMfmaMaxSteps);
+        int64_t max_splits = (kb + kMfmaKB - 1) / kMfmaKB;
         int64_t row_tiles = (rows + kMfmaRows - 1) / kMfmaRows;
         int64_t want = B <= 16 ? 2048 : 512;
-        int64_t splits = std::max<int64_t>(min_splits, want / std::max<int64_t>(1, row_tiles));
-        return (int)std::max<int64_t>(1, std::min<int64_t>(splits, (kb + kMfmaKB - 1) / kMfmaKB));
+        int64_t splits = g_vlut_splits > 0 ? g_vlut_splits
+                                           : std::max<int64_t>(min_splits, want / std::max<int64_t>(1, row_tiles));
+        return (int)std::max<int64_t>(1, std::min<int64_t>(std::max(splits, min_splits), max_splits));
     }
     int TT = B >= 8 ? 8 : (B >= 4 ? 4 : (B >= 2 ? 2 : 1));
     int64_t row_chunks = (rows + kVlutThreads * kVlutRowsPerThread - 1) / (kVlutThreads * kVlutRowsPerThread);
     int64_t tiles = (B + TT - 1) / TT;
-    int64_t want = std::max<int64_t>(1, 256 / std::max<int64_t>(1, row_chunks * tiles));
+    int64_t want = g_vlut_splits > 0 ? g_vlut_splits : std::max<int64_t>(1, 256 / std::max<int64_t>(1, row_chunks * tiles));
     return (int)std::max<int64_t>(1, std::min<int64_t>(want, kb));
 }
 
@@ -534,6 +624,9 @@ hipError_t vlut_matmul(VlutMatmulArgs p, int method, int splits, hipStream_t s)
     p.map = t->cid_map;
     p.coarse = t->coarse;
     p.n_coarse = t->n_coarse;
+    p.swar = t->swar;
+    p.swar_ok = p.M <= t->swar_max_m && g_vlut_swar;
+    p.swar_bias = p.swar_ok ? t->swar_bias[p.M] : 0;
     e = p.q == 4 ? dispatch_m<4>(p, method, splits, s) : dispatch_m<2>(p, method, splits, s);
     if (e != hipSuccess) return e;
     int64_t n = p.B * p.rows;

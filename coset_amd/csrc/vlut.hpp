@@ -26,7 +26,15 @@ struct VlutMatmulArgs {
     const uint64_t* coarse;
     int n_coarse;
     int kb_per_chunk;
+    const uint64_t* swar;  // byte tables of the MFMA decode (tables.hpp)
+    int swar_ok;
+    int swar_bias;
 };
+
+// 0 forces the integer decode in the MFMA kernel (tests compare both)
+extern int g_vlut_swar;
+// > 0 forces the number of K splits (clamped to what the method allows)
+extern int g_vlut_splits;
 
 hipError_t vlut_build(const float* a, int64_t n_queries, int q, int legacy, float* vlut, hipStream_t s);
 hipError_t vlut_dot(const void* words, int64_t n, int M, int q, const float* vlut, float* out, hipStream_t s);

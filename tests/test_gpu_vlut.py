@@ -80,13 +80,24 @@ def test_reference_helpers():
     assert coset_amd.QuantizationConfig(lattice_type="E8", q=4, M=2).beta == 0.3
 
 
+@pytest.fixture(params=["bytes", "integer"])
+def mfma_decode(request):
+    """The MFMA kernel's two decoders: byte tables (default) and digits."""
+    from coset_amd import _lib
+    _lib.set_vlut_decode(request.param == "bytes")
+    yield request.param
+    _lib.set_vlut_decode(True)
+
+
 @pytest.mark.parametrize("method", ["lds", "mfma"])
 @pytest.mark.parametrize("B", [1, 3, 8, 17, 64, 80])
 @pytest.mark.parametrize("adt", [torch.float16, torch.bfloat16, torch.float32])
-def test_vlut_matmul_vs_oracle(method, B, adt):
+def test_vlut_matmul_vs_oracle(method, B, adt, mfma_decode):
     import coset_amd
     if method == "mfma" and adt == torch.float32:
         pytest.skip("MFMA path takes fp16/bf16 activations")
+    if method == "lds" and mfma_decode == "integer":
+        pytest.skip("decoder choice applies to the MFMA path")
     rng = np.random.default_rng(B)
     rows, K, q, M = 96, 320, 4, 2
     W = rng.standard_normal((rows, K)).astype(np.float32)
@@ -104,6 +115,53 @@ def test_vlut_matmul_vs_oracle(method, B, adt):
                 out = coset_amd.vlut_matmul(w, a.cuda(), q, scale=torch.from_numpy(scale), scale_mode=mode,
                                             legacy=legacy, method=method).cpu().numpy()
                 close(out, ref, 1e-3)
+
+
+@pytest.mark.parametrize("q,M", [(2, 1), (2, 2), (2, 3), (2, 4), (4, 1), (4, 3)])
+@pytest.mark.parametrize("B", [1, 20])
+def test_vlut_matmul_other_levels(q, M, B, mfma_decode):
+    """q = 2 (byte decode up to M = 4) and q = 4 at M = 1 / 3 (M = 3 takes
+    the integer decode): both methods against the oracle, raw and prepared
+    words, core and legacy rules."""
+    import coset_amd
+    rng = np.random.default_rng(100 * q + 10 * M + B)
+    rows, K = 80, 192
+    W = rng.standard_normal((rows, K)).astype(np.float32)
+    codes = O.e8_encode(W.reshape(-1, 8), q, M)
+    words_np = O.pack_words(codes, q).reshape(rows, K // 8, M)
+    words = torch.from_numpy(words_np.astype(np.int32)).to(torch.uint16).cuda()
+    a = torch.from_numpy(rng.standard_normal((B, K)).astype(np.float32)).to(torch.float16)
+    scale = np.ones(rows, np.float32)
+    for legacy in (False, True):
+        ref = O.vlut_matmul(words_np, scale, a.float().numpy(), q, M, scale_mode=0, legacy=legacy)
+        prepared = coset_amd.vlut_prepare(words, q, legacy=legacy)
+        for method in ("lds", "mfma"):
+            for w in (words, prepared):
+                out = coset_amd.vlut_matmul(w, a.cuda(), q, legacy=legacy, method=method).cpu().numpy()
+                close(out, ref, 1e-3)
+
+
+@pytest.mark.parametrize("splits", [1, 2, 5, 64])
+def test_vlut_matmul_forced_splits(splits):
+    """Any K split count (clamped to the method's range) gives the same
+    product; workspace sizing follows the forced count."""
+    import coset_amd
+    from coset_amd import _lib
+    rng = np.random.default_rng(splits)
+    rows, K, q, M = 128, 1024, 4, 2
+    W = rng.standard_normal((rows, K)).astype(np.float32)
+    codes = O.e8_encode(W.reshape(-1, 8), q, M)
+    words_np = O.pack_words(codes, q).reshape(rows, K // 8, M)
+    words = torch.from_numpy(words_np.astype(np.int32)).to(torch.uint16).cuda()
+    a = torch.from_numpy(rng.standard_normal((4, K)).astype(np.float32)).to(torch.float16)
+    ref = O.vlut_matmul(words_np, np.ones(rows, np.float32), a.float().numpy(), q, M)
+    _lib.set_vlut_splits(splits)
+    try:
+        for method in ("lds", "mfma"):
+            out = coset_amd.vlut_matmul(words, a.cuda(), q, method=method).cpu().numpy()
+            close(out, ref, 1e-3)
+    finally:
+        _lib.set_vlut_splits(0)
 
 
 def test_c4_full_size_equals_decoded_product():
