@@ -55,6 +55,7 @@ SIGNATURES = {
 OPT_CODEC_PATH = 1
 OPT_VLUT_DECODE = 2
 OPT_VLUT_SPLITS = 3
+OPT_FAST_PROJECTION = 4
 CODEC_AUTO, CODEC_GENERIC, CODEC_LUT = 0, 1, 2
 
 _lib = None
@@ -131,6 +132,12 @@ def require_gpu() -> torch.device:
 def set_codec_path(path: int) -> None:
     """0 automatic, 1 generic kernel, 2 LDS-table kernel (q = 2, 4)."""
     call("coset_set_option", OPT_CODEC_PATH, int(path))
+
+
+def set_fast_projection(enabled: bool) -> None:
+    """Encoders try the fast projection first (default) or always run the
+    reference operation sequence; results are identical either way."""
+    call("coset_set_option", OPT_FAST_PROJECTION, int(bool(enabled)))
 
 
 def set_vlut_decode(byte_tables: bool) -> None:

@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include "e8_core.hpp"
+#include "e8_fast.hpp"
 
 namespace coset {
 
@@ -82,7 +83,15 @@ struct CodecArgs {
     float* beta_out;         // nullable [tiles]: the beta used, one write per tile
     float* dbdt_out;         // nullable [tiles]: d beta / d theta at that beta
     int64_t* step_counter;   // nullable: incremented once per launch
+    int fast_projection;     // encoders try project_fast first (set by the launcher)
 };
+
+// Encoder projection (core rule, contiguous distances): the fast path where
+// its conditions hold, the reference sequence for the lanes where they fail.
+__device__ __forceinline__ void project_encode(const float x[8], float y[8], int fast)
+{
+    if (!(fast && project_fast(x, y))) project<false, false>(x, y);
+}
 
 // Per-block scale of SCALE_LAYER (reads beta_row or derives it from theta).
 __device__ __forceinline__ float layer_scale(const CodecArgs& a, int64_t block)
@@ -108,6 +117,7 @@ hipError_t launch_codec_generic(const CodecArgs& a, int mode, hipStream_t s);
 bool lut_path_supported(const CodecArgs& a, int mode);
 hipError_t launch_codec_lut(const CodecArgs& a, int mode, hipStream_t s);
 extern int g_codec_path;
+extern int g_fast_projection;  // 1 (default): encoders use project_fast where exact
 constexpr int64_t kLutMinBlocks = 1 << 16;
 
 // Backward of the QAT weight quantizer (qat.hip).

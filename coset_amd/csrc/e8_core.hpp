@@ -136,26 +136,24 @@ __device__ __forceinline__ void project(const float x[8], float out[8])
 }
 
 // encode_coords: b = (G^-1 y) mod q for y in E8 (exact integers).
-//   (G^-1 y)_0 = (y0+..+y6)/2 - 3.5 y7
-//   (G^-1 y)_r = (y_r+..+y6) - (7-r) y7     r = 1..6
+//   (G^-1 y)_0 = (y0+..+y6)/2 - 3.5 y7 = (z0+..+z6)/2
+//   (G^-1 y)_r = (y_r+..+y6) - (7-r) y7 = z_r+..+z6      r = 1..6
 //   (G^-1 y)_7 = 2 y7
+// with z_j = y_j - y_7: y in E8 has all coordinates integral or all
+// half-integral, so every z_j is an exact integer (and so is each row).
 template <int Q>
 __device__ __forceinline__ void lattice_digits(const float y[8], int q, int b[8])
 {
-    int u[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) u[i] = (int)__fmul_rn(2.f, y[i]);  // 2y: exact integers
-    int suf = 0;  // 2 * (y_r + .. + y6)
     int c[8];
+    int suf = 0;  // z_r + .. + z_6
 #pragma unroll
     for (int r = 6; r >= 1; --r) {
-        suf += u[r];
-        c[r] = (suf - (7 - r) * u[7]) >> 1;
+        suf += (int)__fsub_rn(y[r], y[7]);
+        c[r] = suf;
     }
-    suf += u[0];
-    c[0] = (suf - 7 * u[7]) >> 2;
-    c[7] = u[7];
-    // c[] are exact: y in E8 makes every row an integer
+    suf += (int)__fsub_rn(y[0], y[7]);
+    c[0] = suf >> 1;
+    c[7] = (int)__fmul_rn(2.f, y[7]);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         if (Q > 0 && (Q & (Q - 1)) == 0) {

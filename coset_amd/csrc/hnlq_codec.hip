@@ -75,7 +75,7 @@ __global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
         for (int m = 0; m < M; ++m) {
             float y[8];
             int b[8];
-            project<false, false>(xl, y);
+            project_encode(xl, y, a.fast_projection);
             lattice_digits<Q>(y, q, b);
             uint32_t word = pack_word<Q>(b, q);
             if (a.packed) {  // level words stored as produced: [n, M]
@@ -178,10 +178,13 @@ static hipError_t launch_mode(const CodecArgs& a, hipStream_t s)
 }
 
 int g_codec_path = 0;
+int g_fast_projection = 1;
 
-hipError_t launch_codec(const CodecArgs& a, int mode, hipStream_t s)
+hipError_t launch_codec(const CodecArgs& args, int mode, hipStream_t s)
 {
-    if (a.n == 0) return hipSuccess;
+    if (args.n == 0) return hipSuccess;
+    CodecArgs a = args;
+    a.fast_projection = g_fast_projection;
     bool lut = lut_path_supported(a, mode) &&
                (g_codec_path == 2 || (g_codec_path == 0 && a.n >= kLutMinBlocks));
     if (lut) return launch_codec_lut(a, mode, s);

@@ -26,22 +26,27 @@ struct LutShape {
 
 constexpr int kLutThreads = 1024;
 
-template <int Q, int M, int MODE>
+// SWAR: each level's 2r comes from three byte tables (tables.hpp) added as
+// two 32-bit words, levels are summed with shifts, and the bytes hold
+// 2 x_hat + swar_bias; otherwise 2r = 2Gb - q (2c) from the unpacked digits.
+template <int Q, int M, int MODE, bool SWAR>
 __global__ void __launch_bounds__(kLutThreads) hnlq_lut_kernel(CodecArgs a, const uint16_t* __restrict__ g_map,
-                                                            const uint64_t* __restrict__ g_coarse,
-                                                            int n_coarse)
+                                                            const uint64_t* __restrict__ g_tab,
+                                                            int n_coarse, int swar_bias)
 {
     constexpr int NC = LutShape<Q>::kCodes;
     __shared__ __align__(16) uint16_t s_map[NC];
-    __shared__ uint64_t s_coarse[kMaxCoarse];
+    __shared__ uint64_t s_tab[SWAR ? 512 + kMaxCoarse : kMaxCoarse];
 
     if (MODE != MODE_ENCODE) {
         const uint4* src = reinterpret_cast<const uint4*>(g_map);
         uint4* dst = reinterpret_cast<uint4*>(s_map);
         for (int i = threadIdx.x; i < NC / 8; i += blockDim.x) dst[i] = src[i];
-        for (int i = threadIdx.x; i < n_coarse; i += blockDim.x) s_coarse[i] = g_coarse[i];
+        const int n_tab = SWAR ? 512 + n_coarse : n_coarse;
+        for (int i = threadIdx.x; i < n_tab; i += blockDim.x) s_tab[i] = g_tab[i];
         __syncthreads();
     }
+    const float half_bias = 0.5f * (float)swar_bias;
 
     if (blockIdx.x == 0 && threadIdx.x == 0 && a.step_counter) *a.step_counter += 1;
     const float qf = (float)Q;
@@ -74,8 +79,10 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_lut_kernel(CodecArgs a, cons
             }
             if (a.scale_mode == SCALE_CODEC) {
                 if (a.beta_is_pow2) {
+                    if (a.beta_inv != 1.f) {  // x / 1 = x
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) xl[j] = __fmul_rn(xl[j], a.beta_inv);
+                        for (int j = 0; j < 8; ++j) xl[j] = __fmul_rn(xl[j], a.beta_inv);
+                    }
                 } else {
 #pragma unroll
                     for (int j = 0; j < 8; ++j) xl[j] = __fdiv_rn(xl[j], scale);
@@ -104,6 +111,7 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_lut_kernel(CodecArgs a, cons
         int acc2[8];  // sum_m q^m * 2 r_m, exact integers
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc2[j] = 0;
+        uint32_t sw0 = 0u, sw1 = 0u;  // SWAR: bytes 0-3 / 4-7 of sum_m q^m (2 r_m + bias)
         int wq = 1;
 #pragma unroll
         for (int m = 0; m < M; ++m) {
@@ -111,7 +119,7 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_lut_kernel(CodecArgs a, cons
             uint32_t word;
             if (MODE != MODE_DECODE) {
                 float y[8];
-                project<false, false>(xl, y);
+                project_encode(xl, y, a.fast_projection);
                 lattice_digits<Q>(y, Q, b);
                 word = pack_word<Q>(b, Q);
                 pack |= (uint64_t)word << (16 * m);
@@ -128,14 +136,26 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_lut_kernel(CodecArgs a, cons
                 word = (uint32_t)(pack >> (16 * m)) & 0xffffu;
                 unpack_word<Q>(word, Q, b);
             }
-            if (MODE != MODE_ENCODE) {
+            if (MODE != MODE_ENCODE && SWAR) {
+                const uint2 tl = *reinterpret_cast<const uint2*>(&s_tab[256 + (word & 0xffu)]);
+                const uint2 tc = *reinterpret_cast<const uint2*>(&s_tab[512 + s_map[word]]);
+                uint32_t l0 = tl.x + tc.x, l1 = tl.y + tc.y;
+                if (Q != 2) {
+                    const uint2 th = *reinterpret_cast<const uint2*>(&s_tab[(word >> 8) & 0xffu]);
+                    l0 += th.x;
+                    l1 += th.y;
+                }
+                sw0 += l0 * (uint32_t)wq;  // q^m: a shift, no byte overflows (checked when tables are built)
+                sw1 += l1 * (uint32_t)wq;
+                wq *= Q;
+            } else if (MODE != MODE_ENCODE) {
                 int u[8];  // 2 G b
                 u[0] = 4 * b[0] - 2 * b[1] + b[7];
 #pragma unroll
                 for (int j = 1; j < 6; ++j) u[j] = 2 * (b[j] - b[j + 1]) + b[7];
                 u[6] = 2 * b[6] + b[7];
                 u[7] = b[7];
-                uint64_t c = s_coarse[s_map[word]];
+                uint64_t c = s_tab[s_map[word]];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     int two_c = (int)(int8_t)(uint8_t)(c >> (8 * j));
@@ -161,9 +181,15 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_lut_kernel(CodecArgs a, cons
         float o[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            float v = __fmul_rn((float)acc2[j], 0.5f);  // exact
+            float v;
+            if (SWAR) {  // (byte - bias) / 2, exact
+                const uint32_t w = j < 4 ? sw0 : sw1;
+                v = __fmaf_rn((float)((w >> (8 * (j & 3))) & 0xffu), 0.5f, -half_bias);
+            } else {
+                v = __fmul_rn((float)acc2[j], 0.5f);  // exact
+            }
             if (a.scale_mode == SCALE_CODEC) {
-                v = __fmul_rn(v, scale);
+                if (a.beta != 1.f) v = __fmul_rn(v, scale);  // x * 1 = x
             } else if (a.scale_mode == SCALE_LAYER) {
                 v = __fdiv_rn(v, scale);
                 v = (v != v) ? v : fminf(fmaxf(v, -a.clip), a.clip);  // clamp keeps NaN
@@ -206,15 +232,17 @@ hipError_t launch_q(const CodecArgs& a, const DecodeTables* t, hipStream_t s)
     int64_t need = (a.n + kLutThreads - 1) / kLutThreads;
     int grid = (int)std::min<int64_t>(need, (int64_t)cu_count());
     const uint16_t* map = t ? t->cid_map : nullptr;
-    const uint64_t* coarse = t ? t->coarse : nullptr;
     int nc = t ? t->n_coarse : 0;
-#define COSET_LUT(MM) \
-    hipLaunchKernelGGL((hnlq_lut_kernel<Q, MM, MODE>), dim3(grid), dim3(kLutThreads), 0, s, a, map, coarse, nc)
+    const bool swar = t && a.M <= t->swar_max_m;
+    const uint64_t* tab = t ? (swar ? t->swar : t->coarse) : nullptr;
+    const int bias = swar ? t->swar_bias[a.M] : 0;
+#define COSET_LUT(MM, SW) \
+    hipLaunchKernelGGL((hnlq_lut_kernel<Q, MM, MODE, SW>), dim3(grid), dim3(kLutThreads), 0, s, a, map, tab, nc, bias)
     switch (a.M) {
-    case 1: COSET_LUT(1); break;
-    case 2: COSET_LUT(2); break;
-    case 3: COSET_LUT(3); break;
-    case 4: COSET_LUT(4); break;
+    case 1: if (swar) COSET_LUT(1, true); else COSET_LUT(1, false); break;
+    case 2: if (swar) COSET_LUT(2, true); else COSET_LUT(2, false); break;
+    case 3: if (Q == 2 && swar) COSET_LUT(3, Q == 2); else COSET_LUT(3, false); break;
+    case 4: if (Q == 2 && swar) COSET_LUT(4, Q == 2); else COSET_LUT(4, false); break;
     default: return hipErrorInvalidValue;
     }
 #undef COSET_LUT

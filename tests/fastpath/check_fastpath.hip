@@ -1,0 +1,174 @@
+// CPU check of coset_amd/csrc/e8_fast.hpp against the C oracle (test
+// infrastructure; built by tests/fastpath/Makefile, run by
+// tests/test_fastpath.py).  The device header is compiled for the host here:
+// every operation in project_fast is an IEEE fp32 operation on both.
+//
+//   check_fastpath lemma [limit]    every float |t| < 2^22: t - rint(t) is
+//                                   exact, and |t - rint t| < 1/2 - 2^-20
+//                                   implies custom_round(t) == rint(t)
+//   check_fastpath blocks N seed    N blocks from each input family: where
+//                                   project_fast succeeds its point equals
+//                                   the oracle's projection bit for bit
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <atomic>
+#include <random>
+#include <thread>
+#include <vector>
+
+#include "e8_fast.hpp"
+
+extern "C" {
+float or_custom_round(float x);
+void or_projection(const float* x, int64_t n, int legacy, float* y);
+}
+
+static float from_bits(uint32_t u)
+{
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+static uint32_t to_bits(float f)
+{
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    return u;
+}
+
+static int lemma(float tie_limit)
+{
+    const uint32_t limit = to_bits(4194304.0f);  // 2^22: magnitudes below it
+    const int n_threads = 8;
+    std::atomic<uint64_t> bad_exact{0}, bad_round{0}, checked{0};
+    std::vector<std::thread> pool;
+    for (int th = 0; th < n_threads; ++th) {
+        pool.emplace_back([&, th] {
+            uint64_t be = 0, br = 0, ck = 0;
+            for (uint32_t mag = th; mag < limit; mag += n_threads) {
+                for (uint32_t sign = 0; sign < 2; ++sign) {
+                    float t = from_bits(mag | (sign << 31));
+                    float r = rintf(t);
+                    float d = t - r;
+                    if ((double)d != (double)t - (double)r) ++be;
+                    if (fabsf(d) < tie_limit) {
+                        ++ck;
+                        if (or_custom_round(t) != r) ++br;
+                    }
+                }
+            }
+            bad_exact += be;
+            bad_round += br;
+            checked += ck;
+        });
+    }
+    for (auto& t : pool) t.join();
+    printf("lemma: %llu floats below the tie limit, %llu inexact t - rint(t), %llu custom_round != rint\n",
+           (unsigned long long)checked.load(), (unsigned long long)bad_exact.load(),
+           (unsigned long long)bad_round.load());
+    return (bad_exact.load() || bad_round.load()) ? 1 : 0;
+}
+
+// Input families: each fills one block of 8.
+static void family(int fam, std::mt19937_64& g, float x[8])
+{
+    std::normal_distribution<float> nd(0.f, 1.f);
+    std::uniform_real_distribution<float> ud(0.f, 1.f);
+    std::uniform_int_distribution<int> id(-8, 8);
+    static const float scales[] = {1.f, 0.25f, 0.0625f, 3.f, 100.f, 1e4f, 1048576.f, 1e-20f};
+    switch (fam) {
+    case 0:  // Gaussian at several scales
+    case 1: {
+        float s = scales[g() % 8];
+        for (int i = 0; i < 8; ++i) x[i] = nd(g) * s;
+        break;
+    }
+    case 2:  // dyadic grid values (ties and exact lattice points)
+        for (int i = 0; i < 8; ++i) x[i] = (float)id(g) / (float)(1 << (g() % 5));
+        break;
+    case 3:  // within a few ulp of half-integers and integers
+        for (int i = 0; i < 8; ++i) {
+            float base = 0.5f * (float)id(g);
+            int k = (int)(g() % 9) - 4;
+            float v = base;
+            for (int s = 0; s < abs(k); ++s) v = nextafterf(v, k > 0 ? INFINITY : -INFINITY);
+            x[i] = g() % 2 ? v : nd(g);
+        }
+        break;
+    case 4: {  // near the boundary between a D8 point and a D8 + 1/2 point
+        float p[8], q[8];
+        int s = 0;
+        for (int i = 0; i < 8; ++i) {
+            p[i] = (float)id(g);
+            s += (int)p[i];
+        }
+        if (s & 1) p[0] += 1.f;
+        s = 0;
+        for (int i = 0; i < 8; ++i) {
+            q[i] = (float)id(g) + 0.5f;
+            s += (int)floorf(q[i]);
+        }
+        if (s & 1) q[1] += 1.f;
+        float lam = 0.5f + (ud(g) - 0.5f) * (g() % 2 ? 1e-3f : 1e-6f);
+        for (int i = 0; i < 8; ++i) x[i] = p[i] + lam * (q[i] - p[i]) + nd(g) * 1e-7f;
+        break;
+    }
+    case 5: {  // large, tiny, signed zeros, denormals, non-finite
+        static const float sp[] = {0.f, -0.f, 1e-40f, -1e-40f, 2097151.f, -2097152.5f, 4194304.f,
+                                   8388609.f, INFINITY, -INFINITY, NAN, 0.5f, -0.5f, 1.5f, -1.5f};
+        for (int i = 0; i < 8; ++i) x[i] = g() % 3 ? sp[g() % 15] : nd(g);
+        break;
+    }
+    default: {  // uniform in a box
+        for (int i = 0; i < 8; ++i) x[i] = (ud(g) - 0.5f) * 16.f;
+        break;
+    }
+    }
+}
+
+static int blocks(long n, unsigned seed)
+{
+    const int n_fam = 7;
+    int rc = 0;
+    for (int fam = 0; fam < n_fam; ++fam) {
+        std::mt19937_64 g(seed * 7919u + fam);
+        long ok = 0, bad = 0;
+        float x[8], yf[8], yr[8];
+        for (long it = 0; it < n; ++it) {
+            family(fam, g, x);
+            if (!coset::project_fast(x, yf)) continue;
+            ++ok;
+            or_projection(x, 1, 0, yr);
+            if (memcmp(yf, yr, sizeof yf) != 0) {
+                if (bad < 5) {
+                    printf("mismatch family %d:", fam);
+                    for (int i = 0; i < 8; ++i) printf(" %.9g", x[i]);
+                    printf("\n  fast:");
+                    for (int i = 0; i < 8; ++i) printf(" %g", yf[i]);
+                    printf("\n  ref: ");
+                    for (int i = 0; i < 8; ++i) printf(" %g", yr[i]);
+                    printf("\n");
+                }
+                ++bad;
+            }
+        }
+        printf("family %d: %ld blocks, fast path taken %ld (%.4f%%), mismatches %ld\n", fam, n, ok,
+               100.0 * ok / n, bad);
+        if (bad) rc = 1;
+    }
+    return rc;
+}
+
+int main(int argc, char** argv)
+{
+    // an optional second argument replaces the tie limit (a looser one must fail)
+    if (argc >= 2 && !strcmp(argv[1], "lemma")) return lemma(argc >= 3 ? strtof(argv[2], nullptr) : coset::kFastTieLimit);
+    if (argc >= 4 && !strcmp(argv[1], "blocks")) return blocks(atol(argv[2]), (unsigned)atoi(argv[3]));
+    fprintf(stderr, "usage: %s lemma [limit] | blocks N seed\n", argv[0]);
+    return 2;
+}

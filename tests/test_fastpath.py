@@ -1,0 +1,52 @@
+"""CPU checks of the encoder's fast projection (coset_amd/csrc/e8_fast.hpp).
+
+The header is compiled for the host (tests/fastpath/Makefile) and checked
+against the C oracle's projection: exhaustively for the rounding lemma it
+rests on (every float below 2^22), with a looser tie limit as the negative
+control that must fail, and bit for bit on blocks from seven input families
+(Gaussian at eight scales, dyadic grids, near-ties, points on the boundary
+between the two D8 cosets, specials, uniform)."""
+import os
+import shutil
+import subprocess
+
+import pytest
+
+HERE = os.path.join(os.path.dirname(__file__), "fastpath")
+EXE = os.path.join(HERE, "_build", "check_fastpath")
+
+
+@pytest.fixture(scope="module")
+def checker():
+    if shutil.which("hipcc") is None and not os.path.exists("/opt/rocm/bin/hipcc"):
+        pytest.skip("hipcc not available")
+    subprocess.run(["make", "-s", "-C", HERE], check=True, capture_output=True)
+    return EXE
+
+
+def run(exe, *args):
+    p = subprocess.run([exe, *args], capture_output=True, text=True, timeout=600)
+    return p.returncode, p.stdout
+
+
+def test_rounding_lemma_exhaustive(checker):
+    rc, out = run(checker, "lemma")
+    assert rc == 0, out
+    assert " 0 inexact" in out and " 0 custom_round != rint" in out, out
+
+
+def test_rounding_lemma_fails_at_the_tie(checker):
+    """Negative control: at |t - rint t| < 1/2 the lemma is false, so the
+    exhaustive check must report the floats where custom_round differs."""
+    rc, out = run(checker, "lemma", "0.5")
+    assert rc == 1, out
+
+
+def test_fast_projection_matches_oracle(checker):
+    rc, out = run(checker, "blocks", "300000", "11")
+    assert rc == 0, out
+    rates = {int(l.split()[1].rstrip(":")): float(l.split("(")[1].split("%")[0])
+             for l in out.splitlines() if l.startswith("family")}
+    assert len(rates) == 7
+    assert rates[6] > 99.0, out   # uniform box: almost always fast
+    assert rates[4] > 10.0, out   # near coset boundaries: many decided, the rest fall back

@@ -212,3 +212,46 @@ def test_full_size_c2_properties(ca, path):
     assert torch.equal(out2, out)
     # every decoded block lies in the scaled lattice: 2*out integral
     assert torch.equal(out * 2, torch.round(out * 2))
+
+
+def _adversarial_blocks(rng, n):
+    """Blocks the encoder's fast projection must hand to the exact sequence:
+    dyadic grids (ties), values a few ulp from half-integers, points on the
+    boundary between the D8 and D8 + 1/2 candidates, large and tiny values,
+    mixed with ordinary Gaussian coordinates."""
+    fam = []
+    fam.append(rng.integers(-8, 9, (n, 8)) / 2.0 ** rng.integers(0, 5, (n, 1)))
+    base = 0.5 * rng.integers(-8, 9, (n, 8))
+    fam.append(np.nextafter(base.astype(np.float32), np.float32(np.inf) * rng.choice([-1, 1], (n, 8))))
+    p = rng.integers(-6, 7, (n, 8)).astype(np.float64)
+    p[:, 0] += p.sum(1) % 2
+    h = rng.integers(-6, 7, (n, 8)) + 0.5
+    h[:, 1] += np.floor(h).sum(1) % 2
+    lam = 0.5 + (rng.random((n, 1)) - 0.5) * 1e-5
+    fam.append(p + lam * (h - p))
+    fam.append(rng.standard_normal((n, 8)) * rng.choice([1e-30, 1e-6, 3e3, 1e6], (n, 1)))
+    x = np.concatenate(fam).astype(np.float32)
+    mix = rng.random(x.shape) < 0.3
+    x[mix] = rng.standard_normal(mix.sum()).astype(np.float32)
+    return x
+
+
+@pytest.mark.parametrize("q,M", [(4, 2), (16, 3), (2, 4)])
+def test_fast_projection_same_codes(ca, path, q, M):
+    """Encoder codes with the fast projection equal those of the reference
+    operation sequence and of the oracle, on Gaussian and adversarial blocks."""
+    from coset_amd import _lib
+    rng = np.random.default_rng(17 + q)
+    x = np.concatenate([rng.standard_normal((20000, 8)).astype(np.float32),
+                        _adversarial_blocks(rng, 5000)])
+    xd = dev(x)
+    try:
+        outs = []
+        for fast in (True, False):
+            _lib.set_fast_projection(fast)
+            outs.append(words(ca.hnlq_encode(xd, q, M, 1.0)))
+    finally:
+        _lib.set_fast_projection(True)
+    np.testing.assert_array_equal(outs[0], outs[1])
+    ref = O.pack_words(O.e8_encode(x, q, M), q)
+    np.testing.assert_array_equal(outs[0], ref)
