@@ -56,6 +56,7 @@ OPT_CODEC_PATH = 1
 OPT_VLUT_DECODE = 2
 OPT_VLUT_SPLITS = 3
 OPT_FAST_PROJECTION = 4
+OPT_CODEC_PLAIN = 5
 CODEC_AUTO, CODEC_GENERIC, CODEC_LUT = 0, 1, 2
 
 _lib = None
@@ -138,6 +139,12 @@ def set_fast_projection(enabled: bool) -> None:
     """Encoders try the fast projection first (default) or always run the
     reference operation sequence; results are identical either way."""
     call("coset_set_option", OPT_FAST_PROJECTION, int(bool(enabled)))
+
+
+def set_codec_plain(enabled: bool) -> None:
+    """The table kernel's fixed-format variant (fp32 in/out, beta = 2^k, no
+    dither) where a call qualifies (default), or always the general one."""
+    call("coset_set_option", OPT_CODEC_PLAIN, int(bool(enabled)))
 
 
 def set_vlut_decode(byte_tables: bool) -> None:

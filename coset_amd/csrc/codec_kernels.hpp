@@ -117,7 +117,8 @@ hipError_t launch_codec_generic(const CodecArgs& a, int mode, hipStream_t s);
 bool lut_path_supported(const CodecArgs& a, int mode);
 hipError_t launch_codec_lut(const CodecArgs& a, int mode, hipStream_t s);
 extern int g_codec_path;
-extern int g_fast_projection;  // 1 (default): encoders use project_fast where exact
+extern int g_fast_projection;
+extern int g_codec_plain;      // 1 (default): the table kernel's fixed-format variant where it applies  // 1 (default): encoders use project_fast where exact
 constexpr int64_t kLutMinBlocks = 1 << 16;
 
 // Backward of the QAT weight quantizer (qat.hip).

@@ -19,6 +19,8 @@
 
 namespace coset {
 
+int g_codec_plain = 1;
+
 template <int Q>
 struct LutShape {
     static constexpr int kCodes = Q * Q * Q * Q * Q * Q * Q * Q;
@@ -211,6 +213,125 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_lut_kernel(CodecArgs a, cons
     }
 }
 
+// Same contract for the common case, with everything the general kernel
+// decides per block fixed at compile time: fp32 input and output, no scale
+// or a codec beta = 2^k (x / beta == x * 2^-k exactly), no dither, no float
+// code tensor, byte-table decode.  The next block's input is loaded before
+// the current one is processed.
+template <int Q, int M, int MODE>
+__global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, const uint16_t* __restrict__ g_map,
+                                                              const uint64_t* __restrict__ g_tab, int n_coarse,
+                                                              int swar_bias)
+{
+    constexpr int NC = LutShape<Q>::kCodes;
+    __shared__ __align__(16) uint16_t s_map[NC];
+    __shared__ uint64_t s_tab[512 + kMaxCoarse];
+    if (MODE != MODE_ENCODE) {
+        const uint4* src = reinterpret_cast<const uint4*>(g_map);
+        uint4* dst = reinterpret_cast<uint4*>(s_map);
+        for (int i = threadIdx.x; i < NC / 8; i += blockDim.x) dst[i] = src[i];
+        for (int i = threadIdx.x; i < 512 + n_coarse; i += blockDim.x) s_tab[i] = g_tab[i];
+        __syncthreads();
+    }
+    const float half_bias = 0.5f * (float)swar_bias;
+    const bool scale_in = a.scale_mode == SCALE_CODEC && a.beta_inv != 1.f;
+    const bool scale_out = a.scale_mode == SCALE_CODEC && a.beta != 1.f;
+    const float4* xs = reinterpret_cast<const float4*>(a.x);
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    float4 nu = make_float4(0.f, 0.f, 0.f, 0.f), nv = nu;
+    uint64_t nw = 0;
+    if (i < a.n) {
+        if (MODE != MODE_DECODE) {
+            nu = xs[2 * i];
+            nv = xs[2 * i + 1];
+        } else {
+            const uint16_t* pw = reinterpret_cast<const uint16_t*>(a.packed_in) + (size_t)i * M;
+#pragma unroll
+            for (int m = 0; m < M; ++m) nw |= (uint64_t)pw[m] << (16 * m);
+        }
+    }
+    for (; i < a.n; i += stride) {
+        float xl[8] = {nu.x, nu.y, nu.z, nu.w, nv.x, nv.y, nv.z, nv.w};
+        uint64_t pack = nw;
+        const int64_t nx = i + stride;
+        if (nx < a.n) {  // prefetch
+            if (MODE != MODE_DECODE) {
+                nu = xs[2 * nx];
+                nv = xs[2 * nx + 1];
+            } else {
+                const uint16_t* pw = reinterpret_cast<const uint16_t*>(a.packed_in) + (size_t)nx * M;
+                nw = 0;
+#pragma unroll
+                for (int m = 0; m < M; ++m) nw |= (uint64_t)pw[m] << (16 * m);
+            }
+        }
+        if (MODE != MODE_DECODE && scale_in) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) xl[j] = __fmul_rn(xl[j], a.beta_inv);
+        }
+        uint32_t sw0 = 0u, sw1 = 0u;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            uint32_t word;
+            if (MODE != MODE_DECODE) {
+                float y[8];
+                int b[8];
+                project_encode(xl, y, a.fast_projection);
+                lattice_digits<Q>(y, Q, b);
+                word = pack_word<Q>(b, Q);
+                pack |= (uint64_t)word << (16 * m);
+                if (m + 1 < M) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) xl[j] = __fmul_rn(xl[j], 1.0f / (float)Q);  // exact: Q = 2^k
+                }
+            } else {
+                word = (uint32_t)(pack >> (16 * m)) & 0xffffu;
+            }
+            if (MODE != MODE_ENCODE) {
+                const uint2 tl = *reinterpret_cast<const uint2*>(&s_tab[256 + (word & 0xffu)]);
+                const uint2 tc = *reinterpret_cast<const uint2*>(&s_tab[512 + s_map[word]]);
+                uint32_t l0 = tl.x + tc.x, l1 = tl.y + tc.y;
+                if (Q != 2) {
+                    const uint2 th = *reinterpret_cast<const uint2*>(&s_tab[(word >> 8) & 0xffu]);
+                    l0 += th.x;
+                    l1 += th.y;
+                }
+                constexpr int L = Q == 2 ? 1 : 2;
+                sw0 += l0 << (L * m);  // q^m, no byte overflows (checked when the tables are built)
+                sw1 += l1 << (L * m);
+            }
+        }
+        if (MODE != MODE_DECODE && a.packed) {
+            uint16_t* pw = reinterpret_cast<uint16_t*>(a.packed) + (size_t)i * M;
+            if (M == 1) {
+                pw[0] = (uint16_t)pack;
+            } else if (M == 2) {
+                *reinterpret_cast<uint32_t*>(pw) = (uint32_t)pack;
+            } else if (M == 4) {
+                *reinterpret_cast<uint64_t*>(pw) = pack;
+            } else {
+#pragma unroll
+                for (int m = 0; m < M; ++m) pw[m] = (uint16_t)(pack >> (16 * m));
+            }
+        }
+        if (MODE == MODE_ENCODE || !a.out) continue;
+        float o[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t w = j < 4 ? sw0 : sw1;
+            o[j] = __fmaf_rn((float)((w >> (8 * (j & 3))) & 0xffu), 0.5f, -half_bias);  // (byte - bias) / 2, exact
+        }
+        if (scale_out) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] = __fmul_rn(o[j], a.beta);
+        }
+        float4* p = reinterpret_cast<float4*>(a.out) + 2 * i;
+        p[0] = make_float4(o[0], o[1], o[2], o[3]);
+        p[1] = make_float4(o[4], o[5], o[6], o[7]);
+    }
+}
+
 namespace {
 
 int cu_count()
@@ -226,6 +347,20 @@ int cu_count()
     return cached[dev];
 }
 
+// Byte tables hold q^M-weighted sums for q = 2 (M <= 4) and q = 4 (M <= 2);
+// the encoder alone needs no tables.
+template <int Q, int M, int MODE>
+hipError_t launch_plain(const CodecArgs& a, int grid, const uint16_t* map, const uint64_t* sw, int nc, int bias,
+                        hipStream_t s)
+{
+    if constexpr (MODE == MODE_ENCODE || Q == 2 || M <= 2) {
+        hipLaunchKernelGGL((hnlq_plain_kernel<Q, M, MODE>), dim3(grid), dim3(kLutThreads), 0, s, a, map, sw, nc,
+                           bias);
+        return hipGetLastError();
+    }
+    return hipErrorInvalidValue;
+}
+
 template <int Q, int MODE>
 hipError_t launch_q(const CodecArgs& a, const DecodeTables* t, hipStream_t s)
 {
@@ -236,6 +371,22 @@ hipError_t launch_q(const CodecArgs& a, const DecodeTables* t, hipStream_t s)
     const bool swar = t && a.M <= t->swar_max_m;
     const uint64_t* tab = t ? (swar ? t->swar : t->coarse) : nullptr;
     const int bias = swar ? t->swar_bias[a.M] : 0;
+    // the plain kernel: fp32 in and out, no scale or a codec beta = 2^k, no
+    // dither, no float codes, no step counter, byte tables for the decode
+    const bool plain = (MODE == MODE_DECODE || a.x_dtype == DT_F32) && a.out_dtype == DT_F32 &&
+                       (a.scale_mode == SCALE_NONE || (a.scale_mode == SCALE_CODEC && a.beta_is_pow2)) &&
+                       !a.dither && !a.codes_f32 && !a.step_counter && (MODE == MODE_ENCODE || swar) &&
+                       g_codec_plain;
+    if (plain) {
+        const uint64_t* sw = t ? t->swar : nullptr;
+        switch (a.M) {
+        case 1: return launch_plain<Q, 1, MODE>(a, grid, map, sw, nc, bias, s);
+        case 2: return launch_plain<Q, 2, MODE>(a, grid, map, sw, nc, bias, s);
+        case 3: return launch_plain<Q, 3, MODE>(a, grid, map, sw, nc, bias, s);
+        case 4: return launch_plain<Q, 4, MODE>(a, grid, map, sw, nc, bias, s);
+        default: return hipErrorInvalidValue;
+        }
+    }
 #define COSET_LUT(MM, SW) \
     hipLaunchKernelGGL((hnlq_lut_kernel<Q, MM, MODE, SW>), dim3(grid), dim3(kLutThreads), 0, s, a, map, tab, nc, bias)
     switch (a.M) {

@@ -21,14 +21,18 @@ def ca():
     return coset_amd
 
 
-@pytest.fixture(params=[1, 2], ids=["generic", "lut"])
+@pytest.fixture(params=[(1, True), (2, True), (2, False)], ids=["generic", "lut", "lut_general"])
 def path(request, ca):
-    """Run the test on the generic kernel and on the LDS-table kernel."""
+    """Run the test on the generic kernel and on the LDS-table kernel, the
+    latter with and without its fixed-format variant (fp32, beta = 2^k)."""
     from coset_amd import _lib
     _lib.require_gpu()
-    _lib.set_codec_path(request.param)
-    yield request.param
+    kernel, plain = request.param
+    _lib.set_codec_path(kernel)
+    _lib.set_codec_plain(plain)
+    yield kernel
     _lib.set_codec_path(0)
+    _lib.set_codec_plain(True)
 
 
 def dev(a):
