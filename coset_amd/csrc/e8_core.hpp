@@ -166,6 +166,30 @@ __device__ __forceinline__ void lattice_digits(const float y[8], int q, int b[8]
     }
 }
 
+// The same digits through the row sums of 2y (for q = 2^k).  A second
+// instruction sequence for one result: the encoders use it on their exact
+// fallback so the two branches meet at the packed word, not at y.
+template <int Q>
+__device__ __forceinline__ void lattice_digits_2y(const float y[8], int b[8])
+{
+    static_assert(Q > 0 && (Q & (Q - 1)) == 0, "power-of-two q");
+    int u[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) u[i] = (int)__fmul_rn(2.f, y[i]);  // exact integers
+    int suf = 0;  // 2 (y_r + .. + y_6)
+    int c[8];
+#pragma unroll
+    for (int r = 6; r >= 1; --r) {
+        suf += u[r];
+        c[r] = (suf - (7 - r) * u[7]) >> 1;
+    }
+    suf += u[0];
+    c[0] = (suf - 7 * u[7]) >> 2;
+    c[7] = u[7];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) b[i] = c[i] & (Q - 1);
+}
+
 // decode_coords: y = G b (exact).
 __device__ __forceinline__ void lattice_point(const int b[8], float y[8])
 {

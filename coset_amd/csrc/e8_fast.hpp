@@ -19,10 +19,12 @@
 //       d1 = t - f1 is again exact.
 //   (4) The two squared distances, evaluated as sum d^2 (+ 1 - 2 adj d_k for
 //       the flipped coordinate) with fused multiply-adds, differ by more than
-//       2^-14.  Both evaluations and the reference's rounded sums of rounded
-//       squares stay within 140 ulp(1) of the exact sums (all terms are below
-//       5), and a gap of 2^-14 also keeps the correctly rounded square roots
-//       apart, so the reference's strict comparison has the same outcome.
+//       2^-14.  For the D8 + 1/2 candidate the terms use |x - f1 - 1/2| =
+//       1/2 - |d0| (equal as reals under (2)).  Both evaluations and the
+//       reference's rounded sums of rounded squares stay within 140 ulp(1)
+//       of the exact sums (all terms are below 5), and a gap of 2^-14 also
+//       keeps the correctly rounded square roots apart, so the reference's
+//       strict comparison has the same outcome.
 // NaN or infinite inputs fail (1) or (4).
 #pragma once
 
@@ -39,27 +41,30 @@ constexpr float kFastDistGap = 6.103515625e-05f;        // 2^-14
 // when a condition above fails; y is then unspecified.
 __host__ __device__ inline bool project_fast(const float x[8], float y[8])
 {
-    float f0[8], d0[8], f1[8], t1[8], d1[8], e1[8];
-    float m = 0.f, best0 = 0.f, best1 = 0.f, s0 = 0.f, s1 = 0.f;
+    float f0[8], d0[8], f1[8], d1[8];
+    float m = 0.f, best0 = 0.f, best1 = 0.f, s0 = 0.f, s1 = 0.f, a = 0.f, b = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         f0[i] = rintf(x[i]);
         d0[i] = x[i] - f0[i];
         f1[i] = floorf(x[i]);
-        t1[i] = x[i] - 0.5f;
-        d1[i] = t1[i] - f1[i];
-        e1[i] = x[i] - (f1[i] + 0.5f);
+        d1[i] = (x[i] - 0.5f) - f1[i];
         m = fmaxf(m, fabsf(x[i]));
         best0 = fmaxf(best0, fabsf(d0[i]));
         best1 = fmaxf(best1, fabsf(d1[i]));
         s0 += f0[i];
         s1 += f1[i];
+        a = fmaf(d0[i], d0[i], a);
+        // x - floor(x) - 1/2 = d0 - 1/2 (d0 > 0) or d0 + 1/2 (d0 < 0) under
+        // (2): its magnitude is 1/2 - |d0|, exact up to one rounding
+        const float e = 0.5f - fabsf(d0[i]);
+        b = fmaf(e, e, b);
     }
     bool ok = m < kFastMaxAbs && best0 < kFastTieLimit && best1 < kFastTieLimit;
 
     // first index of the largest |d| (torch.argmax): scan from the back
     bool first0[8], first1[8];
-    float xk0 = 0.f, dk0 = 0.f, tk1 = 0.f, dk1 = 0.f, ek1 = 0.f;
+    float xk0 = x[0], xk1 = x[0];
     bool seen0 = false, seen1 = false;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -68,27 +73,21 @@ __host__ __device__ inline bool project_fast(const float x[8], float y[8])
         first1[i] = h1 && !seen1;
         seen0 = seen0 || h0;
         seen1 = seen1 || h1;
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
         xk0 = first0[i] ? x[i] : xk0;
-        dk0 = first0[i] ? d0[i] : dk0;
-        tk1 = first1[i] ? t1[i] : tk1;
-        dk1 = first1[i] ? d1[i] : dk1;
-        ek1 = first1[i] ? e1[i] : ek1;
+        xk1 = first1[i] ? x[i] : xk1;
     }
+    // the worst coordinates' differences, recomputed from x_k
+    const float dk0 = xk0 - rintf(xk0);
+    const float fk1 = floorf(xk1);
+    const float tk1 = xk1 - 0.5f;
+    const float dk1 = tk1 - fk1;
+    const float ek1 = (xk1 - fk1) - 0.5f;  // within 2^-25 of x_k - (f_k + 1/2)
     // core g_x: an odd coordinate sum moves the worst coordinate by +1 when
     // t_k >= 0 and f_k < t_k (d_k > 0), by -1 otherwise
     const bool odd0 = ((int)s0 & 1) != 0, odd1 = ((int)s1 & 1) != 0;
     const float adj0 = odd0 ? ((xk0 >= 0.f && dk0 > 0.f) ? 1.f : -1.f) : 0.f;
     const float adj1 = odd1 ? ((tk1 >= 0.f && dk1 > 0.f) ? 1.f : -1.f) : 0.f;
 
-    float a = 0.f, b = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        a = fmaf(d0[i], d0[i], a);
-        b = fmaf(e1[i], e1[i], b);
-    }
     // (d - adj)^2 = d^2 - 2 adj d + adj^2, adj^2 = |adj|
     a += fmaf(-2.f * adj0, dk0, fabsf(adj0));
     b += fmaf(-2.f * adj1, ek1, fabsf(adj1));

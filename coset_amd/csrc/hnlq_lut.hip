@@ -215,10 +215,25 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_lut_kernel(CodecArgs a, cons
 
 // Same contract for the common case, with everything the general kernel
 // decides per block fixed at compile time: fp32 input and output, no scale
-// or a codec beta = 2^k (x / beta == x * 2^-k exactly), no dither, no float
-// code tensor, byte-table decode.  The next block's input is loaded before
-// the current one is processed.
-template <int Q, int M, int MODE>
+// or a codec beta = 2^k (x / beta == x * 2^-k exactly; SCALED false when
+// beta = 1), no dither, no float code tensor, byte-table decode.  The loop is
+// unrolled twice so the next block's input loads into the other register set
+// while the current block is processed.
+template <int Q>
+__device__ __forceinline__ uint32_t encode_level_word(const float xl[8], int fast)
+{
+    float y[8];
+    int b[8];
+    if (fast && project_fast(xl, y)) {
+        lattice_digits<Q>(y, Q, b);
+    } else {
+        project<false, false>(xl, y);
+        lattice_digits_2y<Q>(y, b);
+    }
+    return pack_word<Q>(b, Q);
+}
+
+template <int Q, int M, int MODE, bool SCALED>
 __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, const uint16_t* __restrict__ g_map,
                                                               const uint64_t* __restrict__ g_tab, int n_coarse,
                                                               int swar_bias)
@@ -234,39 +249,30 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
         __syncthreads();
     }
     const float half_bias = 0.5f * (float)swar_bias;
-    const bool scale_in = a.scale_mode == SCALE_CODEC && a.beta_inv != 1.f;
-    const bool scale_out = a.scale_mode == SCALE_CODEC && a.beta != 1.f;
     const float4* xs = reinterpret_cast<const float4*>(a.x);
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    float4 nu = make_float4(0.f, 0.f, 0.f, 0.f), nv = nu;
-    uint64_t nw = 0;
-    if (i < a.n) {
+    const int64_t n = a.n;
+    const int fast = a.fast_projection;
+
+    struct In {
+        float4 u, v;
+        uint64_t w;
+    };
+    auto load = [&](int64_t i, In& in) {
         if (MODE != MODE_DECODE) {
-            nu = xs[2 * i];
-            nv = xs[2 * i + 1];
+            in.u = xs[2 * i];
+            in.v = xs[2 * i + 1];
         } else {
             const uint16_t* pw = reinterpret_cast<const uint16_t*>(a.packed_in) + (size_t)i * M;
+            uint64_t w = 0;
 #pragma unroll
-            for (int m = 0; m < M; ++m) nw |= (uint64_t)pw[m] << (16 * m);
+            for (int m = 0; m < M; ++m) w |= (uint64_t)pw[m] << (16 * m);
+            in.w = w;
         }
-    }
-    for (; i < a.n; i += stride) {
-        float xl[8] = {nu.x, nu.y, nu.z, nu.w, nv.x, nv.y, nv.z, nv.w};
-        uint64_t pack = nw;
-        const int64_t nx = i + stride;
-        if (nx < a.n) {  // prefetch
-            if (MODE != MODE_DECODE) {
-                nu = xs[2 * nx];
-                nv = xs[2 * nx + 1];
-            } else {
-                const uint16_t* pw = reinterpret_cast<const uint16_t*>(a.packed_in) + (size_t)nx * M;
-                nw = 0;
-#pragma unroll
-                for (int m = 0; m < M; ++m) nw |= (uint64_t)pw[m] << (16 * m);
-            }
-        }
-        if (MODE != MODE_DECODE && scale_in) {
+    };
+    auto body = [&](int64_t i, const In& in) {
+        float xl[8] = {in.u.x, in.u.y, in.u.z, in.u.w, in.v.x, in.v.y, in.v.z, in.v.w};
+        uint64_t pack = MODE == MODE_DECODE ? in.w : 0;
+        if (MODE != MODE_DECODE && SCALED) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) xl[j] = __fmul_rn(xl[j], a.beta_inv);
         }
@@ -275,11 +281,7 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
         for (int m = 0; m < M; ++m) {
             uint32_t word;
             if (MODE != MODE_DECODE) {
-                float y[8];
-                int b[8];
-                project_encode(xl, y, a.fast_projection);
-                lattice_digits<Q>(y, Q, b);
-                word = pack_word<Q>(b, Q);
+                word = encode_level_word<Q>(xl, fast);
                 pack |= (uint64_t)word << (16 * m);
                 if (m + 1 < M) {
 #pragma unroll
@@ -315,20 +317,31 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
                 for (int m = 0; m < M; ++m) pw[m] = (uint16_t)(pack >> (16 * m));
             }
         }
-        if (MODE == MODE_ENCODE || !a.out) continue;
+        if (MODE == MODE_ENCODE || !a.out) return;
         float o[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const uint32_t w = j < 4 ? sw0 : sw1;
             o[j] = __fmaf_rn((float)((w >> (8 * (j & 3))) & 0xffu), 0.5f, -half_bias);  // (byte - bias) / 2, exact
-        }
-        if (scale_out) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) o[j] = __fmul_rn(o[j], a.beta);
+            if (SCALED) o[j] = __fmul_rn(o[j], a.beta);
         }
         float4* p = reinterpret_cast<float4*>(a.out) + 2 * i;
         p[0] = make_float4(o[0], o[1], o[2], o[3]);
         p[1] = make_float4(o[4], o[5], o[6], o[7]);
+    };
+
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    In in0{}, in1{};
+    if (i < n) load(i, in0);
+    for (; i < n; i += 2 * stride) {
+        const int64_t i1 = i + stride;
+        if (i1 < n) load(i1, in1);
+        body(i, in0);
+        if (i1 >= n) break;
+        const int64_t i2 = i1 + stride;
+        if (i2 < n) load(i2, in0);
+        body(i1, in1);
     }
 }
 
@@ -354,8 +367,13 @@ hipError_t launch_plain(const CodecArgs& a, int grid, const uint16_t* map, const
                         hipStream_t s)
 {
     if constexpr (MODE == MODE_ENCODE || Q == 2 || M <= 2) {
-        hipLaunchKernelGGL((hnlq_plain_kernel<Q, M, MODE>), dim3(grid), dim3(kLutThreads), 0, s, a, map, sw, nc,
-                           bias);
+        const bool scaled = a.scale_mode == SCALE_CODEC && a.beta != 1.f;
+        if (scaled)
+            hipLaunchKernelGGL((hnlq_plain_kernel<Q, M, MODE, true>), dim3(grid), dim3(kLutThreads), 0, s, a, map,
+                               sw, nc, bias);
+        else
+            hipLaunchKernelGGL((hnlq_plain_kernel<Q, M, MODE, false>), dim3(grid), dim3(kLutThreads), 0, s, a, map,
+                               sw, nc, bias);
         return hipGetLastError();
     }
     return hipErrorInvalidValue;
