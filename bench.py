@@ -155,26 +155,59 @@ def bench_c3(torch, ca, args):
             "bytes_per_block": 60}
 
 
+def graph_time(torch, fn, n_calls=20, reps=10):
+    """Per-call GPU time of fn() replayed from a HIP graph of n_calls calls
+    (launch overhead amortized, as in a captured serving step).  Every
+    output of every replay is checked bit for bit against an eager call."""
+    ref = fn()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        graph.capture_begin()
+        outs = [fn() for _ in range(n_calls)]
+        graph.capture_end()
+    torch.cuda.current_stream().wait_stream(side)
+    for _ in range(2):
+        graph.replay()
+        torch.cuda.synchronize()
+        for o in outs:
+            if not torch.equal(o, ref):
+                raise RuntimeError("graph replay differs from the eager call")
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / 1e3 / (reps * n_calls)
+
+
 def bench_c4(torch, ca, args):
     g = torch.Generator(device="cuda").manual_seed(5)
     W = 0.02 * torch.randn((4096, 4096), device="cuda", generator=g)
     words = ca.hnlq_encode(W.reshape(-1, 8), 4, 2, 0.02).reshape(4096, 512, 2)
-    prepared = ca.vlut_prepare(words, 4)   # once per weight: (coarse id << 16 | idx), 16 MiB
+    tiled = ca.vlut_prepare(words, 4)   # once per weight: cid << 16 | idx in fragment order, 16 MiB
     scale = torch.full((4096,), 0.02, device="cuda")
     del W
-    res = {"workload": "C4 vLUT matmul 4096x4096 q4 M2 codes (8 MiB uint16 words; 16 MiB prepared), "
-                       "fp16 activations, fp32 out", "batches": {}}
+    res = {"workload": "C4 vLUT matmul 4096x4096 q4 M2 codes (8 MiB uint16 words; 16 MiB tiled prepared), "
+                       "fp16 activations, fp32 out; us_graph = per call replayed from a HIP graph, "
+                       "us_eager = per call from Python", "batches": {}}
     ws = torch.empty(64 * 4096 * 64, dtype=torch.float32, device="cuda")
     for B in (1, 8, 64):
         a = torch.randn((B, 4096), device="cuda", generator=g).to(torch.float16)
         row = {}
-        for method, wts in (("lds", prepared), ("mfma", prepared), ("mfma_raw_words", words)):
+        for method, wts in (("mfma", tiled), ("mfma_raw_words", words), ("lds", tiled)):
             m = "mfma" if method.startswith("mfma") else "lds"
-            k, w = gpu_time(torch, lambda: ca.vlut_matmul(wts, a, 4, scale=scale, method=m, workspace=ws),
-                            100, 10)
-            nbytes = wts.numel() * wts.element_size() + B * 4096 * 2 + B * 4096 * 4
+            fn = lambda: ca.vlut_matmul(wts, a, 4, scale=scale, method=m, workspace=ws)
+            k_eager, _ = gpu_time(torch, fn, 50 if m == "lds" else 100, 5)
+            k = graph_time(torch, fn)
+            wbytes = wts.data.numel() * 4 if isinstance(wts, ca.PreparedWords) else wts.numel() * wts.element_size()
+            nbytes = wbytes + B * 4096 * 2 + B * 4096 * 4
             flops = 2.0 * B * 4096 * 4096
-            row[method] = {"tokens_per_s": round(B / k, 1), "us": round(k * 1e6, 2),
+            row[method] = {"tokens_per_s": round(B / k, 1), "us_graph": round(k * 1e6, 2),
+                           "us_eager": round(k_eager * 1e6, 2),
                            "gbs_algorithmic": round(nbytes / k / 1e9, 1),
                            "frac_hbm": round(nbytes / k / 1e9 / HBM_PEAK_GBS, 4),
                            "dense_equiv_tflops": round(flops / k / 1e12, 2),

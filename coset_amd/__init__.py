@@ -41,6 +41,7 @@ from .vlut import (
     vlut_mac_operation,
     vlut_matmul,
     vlut_prepare,
+    PreparedWords,
 )
 
 __version__ = "0.1.0"
@@ -52,5 +53,5 @@ __all__ = [
     "HNLQLinear", "HNLQLinearQAT", "HNLQConfig", "LSQActivation", "StraightThroughQuantize",
     "E8WeightQuant", "E8ThetaWeightQuant", "create_e8_hnlq_linear", "get_generators", "ste_quantize",
     "vLUTManager", "QuantizationConfig", "build_vlut", "_encoding_to_index", "vlut_mac_operation",
-    "vlut_accumulate_operation", "build_one_sided_vluts", "vlut_dot", "vlut_matmul", "vlut_prepare",
+    "vlut_accumulate_operation", "build_one_sided_vluts", "vlut_dot", "vlut_matmul", "vlut_prepare", "PreparedWords",
 ]

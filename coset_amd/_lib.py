@@ -14,7 +14,7 @@ import torch
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_PKG, "libcoset_amd.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # mirrors of the enums in include/coset_amd.h
 OK, EINVAL, EUNSUPPORTED, EHIP = 0, -1, -2, -3
@@ -45,11 +45,17 @@ SIGNATURES = {
                                _vp],
     "coset_vlut_build_one_sided": [_vp, _i64, _int, _int, _vp, _vp],
     "coset_vlut_lookup_dot": [_vp, _i64, _int, _int, _vp, _vp, _vp],
-    "coset_vlut_prepare": [_vp, _i64, _int, _int, _vp, _vp],
+    "coset_vlut_prepare": [_vp, _i64, _i64, _int, _int, _int, _int, _vp, _vp],
     "coset_vlut_matmul": [_vp, _int, _vp, _int, _vp, _int, _i64, _i64, _i64, _int, _int, _int, _int, _vp, _i64,
                           _vp, _vp],
     "coset_init": [_int],
     "coset_set_option": [_int, _int],
+}
+
+# name -> argtypes of the int64 size queries
+SIZE_QUERIES = {
+    "coset_vlut_workspace_floats": [_i64, _i64, _i64, _int, _int, _int, _int],
+    "coset_vlut_prepared_words": [_i64, _i64, _int, _int],
 }
 
 OPT_CODEC_PATH = 1
@@ -78,8 +84,10 @@ def load():
     lib.coset_last_error.restype = ctypes.c_char_p
     lib.coset_word_bytes.argtypes = [_int]
     lib.coset_word_bytes.restype = _int
-    lib.coset_vlut_workspace_floats.argtypes = [_i64, _i64, _i64, _int, _int, _int, _int]
-    lib.coset_vlut_workspace_floats.restype = _i64
+    for name, args in SIZE_QUERIES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = _i64
     for name, args in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.argtypes = args

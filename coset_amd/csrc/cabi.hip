@@ -364,15 +364,25 @@ int64_t coset_vlut_workspace_floats(int64_t B, int64_t rows, int64_t K, int q, i
 {
     int m = vlut_method(method, act_dtype, q, M);
     if (m < 0 || B < 0 || rows < 0 || K < 8) return 0;
-    return (int64_t)coset::vlut_default_splits(rows, B, K, m) * B * rows;
+    return coset::vlut_workspace_floats(coset::vlut_plan(rows, B, K, q, M, m), B, rows);
 }
 
-int coset_vlut_prepare(const void* words, int64_t n_words, int q, int legacy, uint32_t* prepared, void* stream)
+int64_t coset_vlut_prepared_words(int64_t rows, int64_t kb, int M, int word_format)
+{
+    if (rows < 0 || kb < 0 || M < 1 || word_format < 0 || word_format > 2) return 0;
+    return coset::vlut_prepared_words(rows, kb, M, word_format);
+}
+
+int coset_vlut_prepare(const void* words, int64_t rows, int64_t kb, int M, int q, int legacy, int word_format,
+                       uint32_t* prepared, void* stream)
 {
     if (q != 2 && q != 4) return fail(COSET_EUNSUPPORTED, "vLUT prepare supports q = 2 or 4 (got %d)", q);
-    if (n_words < 0) return fail(COSET_EINVAL, "n_words < 0");
-    if (n_words > 0 && (!words || !prepared)) return fail(COSET_EINVAL, "NULL buffer");
-    return check_hip(coset::vlut_prepare((const uint16_t*)words, n_words, q, legacy ? 1 : 0, prepared,
+    if (rows < 0 || kb < 0 || M < 1 || M > 4) return fail(COSET_EINVAL, "bad shape rows=%lld kb=%lld M=%d",
+                                                         (long long)rows, (long long)kb, M);
+    if (word_format != 1 && word_format != 2) return fail(COSET_EINVAL, "prepared word_format must be 1 or 2");
+    if (rows * kb > 0 && (!words || !prepared)) return fail(COSET_EINVAL, "NULL buffer");
+    if (!aligned(prepared, 16)) return fail(COSET_EINVAL, "prepared must be 16-byte aligned");
+    return check_hip(coset::vlut_prepare((const uint16_t*)words, rows, kb, M, q, legacy ? 1 : 0, word_format, prepared,
                                          (hipStream_t)stream), "vLUT prepare launch");
 }
 
@@ -393,13 +403,16 @@ int coset_vlut_matmul(const void* words, int word_format, const float* scale, in
     if (m < 0) return fail(COSET_EUNSUPPORTED, "MFMA method needs fp16/bf16 activations holding 2*x_hat exactly");
     if (m != coset::VLUT_METHOD_LDS && m != coset::VLUT_METHOD_MFMA) return fail(COSET_EINVAL, "unknown method %d", method);
     if (B == 0 || rows == 0) return COSET_OK;
-    if (!words || !act || !out || !workspace) return fail(COSET_EINVAL, "NULL buffer");
+    if (!words || !act || !out) return fail(COSET_EINVAL, "NULL buffer");
     if (!aligned(act, 16) || !aligned(words, 4)) return fail(COSET_EINVAL, "act must be 16-byte aligned, words 4-byte");
-    int splits = coset::vlut_default_splits(rows, B, K, m);
-    if (workspace_floats < (int64_t)splits * B * rows)
+    const coset::VlutPlan plan = coset::vlut_plan(rows, B, K, q, M, m);
+    const int64_t need = coset::vlut_workspace_floats(plan, B, rows);
+    if (workspace_floats < need)
         return fail(COSET_EINVAL, "workspace holds %lld floats, needs %lld", (long long)workspace_floats,
-                    (long long)splits * B * rows);
-    if (word_format != 0 && word_format != 1) return fail(COSET_EINVAL, "word_format must be 0 or 1");
+                    (long long)need);
+    if (need > 0 && !workspace) return fail(COSET_EINVAL, "NULL workspace");
+    if (word_format < 0 || word_format > 2) return fail(COSET_EINVAL, "word_format must be 0, 1 or 2");
+    if (word_format != 0 && !aligned(words, 16)) return fail(COSET_EINVAL, "prepared words must be 16-byte aligned");
     coset::VlutMatmulArgs p{};
     p.words = words;
     p.prepared = word_format;
@@ -418,7 +431,7 @@ int coset_vlut_matmul(const void* words, int word_format, const float* scale, in
     const coset::DecodeTables* t = nullptr;
     if ((rc = check_hip(coset::get_decode_tables(q, p.legacy, &t), "decode tables"))) return rc;
     if (t->n_coarse > coset::kMaxCoarseVlut) return fail(COSET_EUNSUPPORTED, "too many coarse points");
-    return check_hip(coset::vlut_matmul(p, m, splits, (hipStream_t)stream), "vLUT matmul launch");
+    return check_hip(coset::vlut_matmul(p, plan, (hipStream_t)stream), "vLUT matmul launch");
 }
 
 int coset_e8_lattice_op(int op, int legacy, const float* in, int64_t n_blocks, int q,

@@ -135,7 +135,7 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_lut_kernel(CodecArgs a, cons
                     for (int j = 0; j < 8; ++j) xl[j] = div_q<Q>(xl[j], qf);
                 }
             } else {
-                word = (uint32_t)(pack >> (16 * m)) & 0xffffu;
+                word = (uint32_t)(pack >> (16 * m)) & (uint32_t)(NC - 1);  // table bounds for any input
                 unpack_word<Q>(word, Q, b);
             }
             if (MODE != MODE_ENCODE && SWAR) {
@@ -288,7 +288,7 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
                     for (int j = 0; j < 8; ++j) xl[j] = __fmul_rn(xl[j], 1.0f / (float)Q);  // exact: Q = 2^k
                 }
             } else {
-                word = (uint32_t)(pack >> (16 * m)) & 0xffffu;
+                word = (uint32_t)(pack >> (16 * m)) & (uint32_t)(NC - 1);  // table bounds for any input
             }
             if (MODE != MODE_ENCODE) {
                 const uint2 tl = *reinterpret_cast<const uint2*>(&s_tab[256 + (word & 0xffu)]);

@@ -56,7 +56,7 @@ __device__ __forceinline__ void decode_q(const QatBwdArgs& a, int64_t blk, float
         for (int j = 0; j < 8; ++j) acc2[j] = 0;
         int wq = 1;
         for (int m = 0; m < a.M; ++m) {
-            uint32_t w = reinterpret_cast<const uint16_t*>(a.packed)[blk * a.M + m];
+            uint32_t w = reinterpret_cast<const uint16_t*>(a.packed)[blk * a.M + m] & (Q == 2 ? 0xffu : 0xffffu);
             int b[8];
             unpack_word<Q>(w, q, b);
             int u[8];

@@ -54,23 +54,39 @@ __device__ __forceinline__ void two_r_lut(uint32_t w, const uint16_t* map, const
 // Level word index i of the weight tensor -> (idx, coarse id).
 __device__ __forceinline__ void load_word(const VlutMatmulArgs& p, int64_t i, uint32_t* idx, uint32_t* cid)
 {
-    if (p.prepared) {
+    if (p.prepared != VLUT_RAW) {
         uint32_t v = reinterpret_cast<const uint32_t*>(p.words)[i];
         *idx = v & 0xffffu;
         *cid = v >> 16;
     } else {
-        uint32_t w = reinterpret_cast<const uint16_t*>(p.words)[i];
+        uint32_t w = reinterpret_cast<const uint16_t*>(p.words)[i] & (p.q == 2 ? 0xffu : 0xffffu);  // map bounds
         *idx = w;
         *cid = p.map[w];
     }
 }
 
-__global__ void __launch_bounds__(256) vlut_prepare_kernel(const uint16_t* words, int64_t n, const uint16_t* map,
-                                                          uint32_t* out)
+// One thread per output word: the raw word of (row, kb, m) or, past the
+// matrix in the tiled format, the word 0 (which decodes to 0).
+__global__ void __launch_bounds__(256) vlut_prepare_kernel(const uint16_t* words, int64_t rows, int64_t kb_total,
+                                                          int M, int fmt, int64_t n_out, const uint16_t* map,
+                                                          uint32_t mask, uint32_t* out)
 {
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    uint32_t w = words[i];
+    if (i >= n_out) return;
+    uint32_t w = 0;
+    if (fmt == VLUT_TILED) {
+        const int m = (int)(i % M);
+        const int64_t e = i / M;  // entry
+        const int lane = (int)(e & 63);
+        const int64_t tile = e >> 6;
+        const int64_t kq = (kb_total + 3) / 4;
+        const int64_t row = (tile / kq) * 16 + (lane & 15);
+        const int64_t kb = (tile % kq) * 4 + (lane >> 4);
+        if (row < rows && kb < kb_total) w = words[(row * kb_total + kb) * M + m];
+    } else {
+        w = words[i];
+    }
+    w &= mask;  // q^8 - 1: map bounds for any input
     out[i] = ((uint32_t)map[w] << 16) | w;
 }
 
@@ -110,7 +126,7 @@ __global__ void __launch_bounds__(256) vlut_build_kernel(const float* a, int64_t
 
 // ---------------------------------------------------------------- lookup
 __global__ void __launch_bounds__(256) vlut_dot_kernel(const void* words, int word_bytes_, int64_t n, int M,
-                                                      int q, const float* vlut, float* out)
+                                                      int q, uint32_t n_codes, const float* vlut, float* out)
 {
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
@@ -118,6 +134,7 @@ __global__ void __launch_bounds__(256) vlut_dot_kernel(const void* words, int wo
     for (int m = 0; m < M; ++m) {
         uint32_t idx = word_bytes_ == 2 ? reinterpret_cast<const uint16_t*>(words)[i * M + m]
                                         : reinterpret_cast<const uint32_t*>(words)[i * M + m];
+        idx = min(idx, n_codes - 1u);  // table bounds for any input
         acc = __fmaf_rn(w, vlut[idx], acc);
         w *= (float)q;
     }
@@ -198,12 +215,11 @@ __global__ void __launch_bounds__(kVlutThreads) vlut_lds_kernel(VlutMatmulArgs p
             for (int rr = 0; rr < kVlutRowsPerThread; ++rr) {
                 int64_t row = r0 + threadIdx.x + rr * kVlutThreads;
                 if (row >= p.rows) continue;
-                const int64_t wbase = (row * kb_total + kc + k) * M;
                 float qm = 1.f;
 #pragma unroll
                 for (int m = 0; m < M; ++m) {
                     uint32_t w, cid;
-                    load_word(p, wbase + m, &w, &cid);
+                    load_word(p, vlut_word_index(p.prepared, row, kc + k, m, kb_total, M), &w, &cid);
                     int b[8];
                     unpack_word<Q>(w, Q, b);
 #pragma unroll
@@ -298,8 +314,8 @@ __global__ void __launch_bounds__(256) vlut_mfma_kernel(VlutMatmulArgs p)
             for (int m = 0; m < M; ++m) {
                 uint32_t v = 0xffffffffu;
                 if (ok) {
-                    const int64_t wi = (row * kb_total + kb) * M + m;
-                    if (p.prepared) {
+                    const int64_t wi = vlut_word_index(p.prepared, row, kb, m, kb_total, M);
+                    if (p.prepared != VLUT_RAW) {
                         v = reinterpret_cast<const uint32_t*>(p.words)[wi];
                     } else {
                         const uint32_t w = reinterpret_cast<const uint16_t*>(p.words)[wi];
@@ -463,6 +479,197 @@ __global__ void __launch_bounds__(256) vlut_mfma_kernel(VlutMatmulArgs p)
     }
 }
 
+// ---------------------------------------------------------------- MFMA rows kernel
+// Tile: 16 output rows per workgroup, K split over its 8 waves (and over
+// grid.y when the row tiles alone cannot fill the GPU), up to 16 * NTILE
+// tokens (grid.z beyond).  In each step lane l owns row l % 16 and k-block
+// 4 kq + l / 16: it decodes that pair's 2 x_hat through the byte tables
+// straight into its 8-half B operand of one 16x16x32 MFMA and loads
+// act[token][8 kb, 8 kb + 8) as its A operand, so neither goes through LDS.
+// Any assignment of K positions to (lane group, operand slot) works as long
+// as A and B use the same one, which holds since both come from the same kb.
+// In the tiled format a step's 64 word groups are one contiguous run.  The
+// waves' sums meet in LDS; with one K split the workgroup writes the output.
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+
+constexpr int kRowsWaves = 8;
+
+template <int Q, int M>
+__device__ __forceinline__ void load_pair(const VlutMatmulArgs& p, int fmt, int64_t row, int64_t kb, int64_t kb_total,
+                                          uint32_t w[M])
+{
+    const int64_t i0 = vlut_word_index(fmt, row, kb, 0, kb_total, M);
+    if (fmt == VLUT_RAW) {
+        const uint16_t* src = reinterpret_cast<const uint16_t*>(p.words) + i0;
+        constexpr uint32_t kMask = Q == 2 ? 0xffu : 0xffffu;  // q^8 - 1: map bounds for any input
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const uint32_t x = src[m] & kMask;
+            w[m] = ((uint32_t)p.map[x] << 16) | x;
+        }
+    } else {
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(p.words) + i0;
+        if (M == 2) {
+            const uint2 v = *reinterpret_cast<const uint2*>(src);
+            w[0] = v.x;
+            w[1 % M] = v.y;
+        } else if (M == 4) {
+            const uint4 v = *reinterpret_cast<const uint4*>(src);
+            w[0] = v.x;
+            w[1 % M] = v.y;
+            w[2 % M] = v.z;
+            w[3 % M] = v.w;
+        } else {
+#pragma unroll
+            for (int m = 0; m < M; ++m) w[m] = src[m];
+        }
+    }
+}
+
+// 2 x_hat of one pair as 8 halves (fp16) or bf16 values, exact.
+template <int Q, int M, bool BF16>
+__device__ __forceinline__ uint4 decode_pair_swar(const uint64_t* s_tab, const uint32_t w[M], _Float16 f16_off,
+                                                  float f32_off)
+{
+    uint32_t x0 = 0u, x1 = 0u;
+#pragma unroll
+    for (int m = M - 1; m >= 0; --m) {
+        const uint32_t v = w[m];
+        const uint2 tl = *reinterpret_cast<const uint2*>(&s_tab[256 + (v & 0xffu)]);
+        const uint2 tc = *reinterpret_cast<const uint2*>(&s_tab[512 + (v >> 16)]);
+        uint32_t l0 = tl.x + tc.x, l1 = tl.y + tc.y;
+        if (Q != 2) {
+            const uint2 th = *reinterpret_cast<const uint2*>(&s_tab[(v >> 8) & 0xffu]);
+            l0 += th.x;
+            l1 += th.y;
+        }
+        x0 = x0 * Q + l0;
+        x1 = x1 * Q + l1;
+    }
+    uint32_t hv[4];
+    if (BF16) {
+        float f[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            f[j] = (float)((x0 >> (8 * j)) & 0xffu) - f32_off;
+            f[4 + j] = (float)((x1 >> (8 * j)) & 0xffu) - f32_off;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            hv[j] = __builtin_amdgcn_perm(__float_as_uint(f[2 * j + 1]), __float_as_uint(f[2 * j]), 0x07060302u);
+    } else {
+        const uint32_t raw[4] = {bytes_to_f16_bits(x0, false), bytes_to_f16_bits(x0, true),
+                                 bytes_to_f16_bits(x1, false), bytes_to_f16_bits(x1, true)};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            hv[j] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, raw[j]) - (half2_t){f16_off, f16_off});
+    }
+    return make_uint4(hv[0], hv[1], hv[2], hv[3]);
+}
+
+template <int Q, int M, bool BF16, int NTILE, int FMT>
+__global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulArgs p)
+{
+    constexpr int CH = 8 / NTILE;  // steps per prefetch chunk
+    __shared__ uint64_t s_tab[kSwarSlots];
+    __shared__ float s_red[kRowsWaves][NTILE * 4][64];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4;
+    const int64_t kb_total = p.K / 8;
+    const int64_t kq_total = (kb_total + 3) / 4;
+    const int64_t kq_wg = (kq_total + gridDim.y - 1) / gridDim.y;
+    const int64_t kq_begin = blockIdx.y * kq_wg;
+    const int64_t kq_end = min(kq_total, kq_begin + kq_wg);
+    const int64_t kq_wave = (kq_end - kq_begin + kRowsWaves - 1) / kRowsWaves;
+    const int64_t w0 = kq_begin + wave * kq_wave;
+    const int64_t w1 = min(kq_end, w0 + kq_wave);
+    const int64_t r0 = (int64_t)blockIdx.x * 16;
+    const int64_t row = r0 + (lane & 15);
+    const int64_t t_base = (int64_t)blockIdx.z * 16 * NTILE;
+    const uint16_t* act = reinterpret_cast<const uint16_t*>(p.act);
+    const _Float16 f16_off = (_Float16)(1024 + p.swar_bias);
+    const float f32_off = (float)p.swar_bias;
+
+    struct Chunk {
+        uint32_t w[CH][M];
+        uint4 a[CH][NTILE];
+    };
+    auto load = [&](int64_t c0, Chunk& ck) {
+#pragma unroll
+        for (int st = 0; st < CH; ++st) {
+            const int64_t kq = c0 + st;
+            const int64_t kb = 4 * kq + g;
+            const bool kb_ok = kq < w1 && kb < kb_total;
+#pragma unroll
+            for (int m = 0; m < M; ++m) ck.w[st][m] = 0u;
+            if (kb_ok && (FMT == VLUT_TILED || row < p.rows)) load_pair<Q, M>(p, FMT, row, kb, kb_total, ck.w[st]);
+#pragma unroll
+            for (int s = 0; s < NTILE; ++s) {
+                const int64_t tok = t_base + 16 * s + (lane & 15);
+                ck.a[st][s] = make_uint4(0u, 0u, 0u, 0u);
+                if (kb_ok && tok < p.B) ck.a[st][s] = *reinterpret_cast<const uint4*>(act + tok * p.K + kb * 8);
+            }
+        }
+    };
+    float4_t acc[NTILE];
+#pragma unroll
+    for (int s = 0; s < NTILE; ++s) acc[s] = (float4_t){0.f, 0.f, 0.f, 0.f};
+    auto run = [&](const Chunk& ck) {
+#pragma unroll
+        for (int st = 0; st < CH; ++st) {
+            const uint4 bw = decode_pair_swar<Q, M, BF16>(s_tab, ck.w[st], f16_off, f32_off);
+#pragma unroll
+            for (int s = 0; s < NTILE; ++s) {
+                if (BF16)
+                    acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ck.a[st][s]),
+                                                                    __builtin_bit_cast(bf16x8_t, bw), acc[s], 0, 0, 0);
+                else
+                    acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, ck.a[st][s]),
+                                                                   __builtin_bit_cast(half8_t, bw), acc[s], 0, 0, 0);
+            }
+        }
+    };
+
+    Chunk c_a, c_b;
+    int64_t c0 = w0;
+    if (c0 < w1) load(c0, c_a);
+    // the tables are staged while the first chunk's loads are in flight
+    for (int i = threadIdx.x; i < 512 + p.n_coarse; i += blockDim.x) s_tab[i] = p.swar[i];
+    __syncthreads();
+    for (; c0 < w1; c0 += 2 * CH) {
+        const int64_t c1 = c0 + CH;
+        if (c1 < w1) load(c1, c_b);
+        run(c_a);
+        if (c1 >= w1) break;
+        const int64_t c2 = c1 + CH;
+        if (c2 < w1) load(c2, c_a);
+        run(c_b);
+    }
+
+    // D[token = 16 s + 4 (lane / 16) + i][row = lane % 16]; sum the waves
+#pragma unroll
+    for (int s = 0; s < NTILE; ++s)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s_red[wave][s * 4 + i][lane] = acc[s][i];
+    __syncthreads();
+    for (int e = threadIdx.x; e < NTILE * 256; e += blockDim.x) {
+        const int si = e >> 6, ln = e & 63;
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < kRowsWaves; ++w) v += s_red[w][si][ln];
+        const int64_t tok = t_base + 16 * (si >> 2) + 4 * (ln >> 4) + (si & 3);
+        const int64_t o = r0 + (ln & 15);
+        if (tok >= p.B || o >= p.rows) continue;
+        if (gridDim.y == 1) {
+            float sc = p.scale ? (p.scale_mode == 0 ? p.scale[o] : 1.f / p.scale[o]) : 1.f;
+            p.out[tok * p.rows + o] = v * 0.5f * sc;
+        } else {
+            p.partial[(tok * p.rows + o) * gridDim.y + blockIdx.y] = v;
+        }
+    }
+}
+
 // ---------------------------------------------------------------- reduce
 __global__ void __launch_bounds__(256) vlut_reduce_kernel(const float* partial, int splits, int64_t B,
                                                          int64_t rows, const float* scale, int scale_mode,
@@ -518,15 +725,7 @@ template <int Q, int M>
 hipError_t launch_mfma(const VlutMatmulArgs& p, int splits, hipStream_t s)
 {
     // byte decode where the tables allow it (q = 4: M <= 2, q = 2: M <= 4)
-    if constexpr (Q == 2 || M <= 2) {
-        if (p.swar_ok) {
-            if (p.B <= 16)
-                launch_mfma_nt<Q, M, true, 16>(p, splits, s);
-            else
-                launch_mfma_nt<Q, M, true, 64>(p, splits, s);
-            return hipGetLastError();
-        }
-    }
+    // the byte decode of this kernel is superseded by vlut_rows_kernel
     launch_mfma_nt<Q, M, false, 64>(p, splits, s);
     return hipGetLastError();
 }
@@ -570,51 +769,128 @@ hipError_t vlut_build(const float* a, int64_t n_queries, int q, int legacy, floa
 hipError_t vlut_dot(const void* words, int64_t n, int M, int q, const float* vlut, float* out, hipStream_t s)
 {
     if (n == 0) return hipSuccess;
+    uint32_t n_codes = 1;
+    for (int i = 0; i < 8; ++i) n_codes *= (uint32_t)q;
     hipLaunchKernelGGL(vlut_dot_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, words, word_bytes(q), n,
-                       M, q, vlut, out);
+                       M, q, n_codes, vlut, out);
     return hipGetLastError();
 }
 
 int g_vlut_swar = 1;
 int g_vlut_splits = 0;
 
-int vlut_default_splits(int64_t rows, int64_t B, int64_t K, int method)
+namespace {
+
+int device_cu_count()
 {
-    int64_t kb = K / 8;
-    if (method == VLUT_METHOD_MFMA) {
-        // every workgroup covers at most kMfmaMaxSteps * 16 k-blocks; beyond
-        // that minimum, small batches take more splits (more workgroups in
-        // flight) since their partial sums are cheap
-        int64_t min_splits = (kb + kMfmaKB * kMfmaMaxSteps - 1) / (kMfmaKB * kMfmaMaxSteps);
-        int64_t max_splits = (kb + kMfmaKB - 1) / kMfmaKB;
-        int64_t row_tiles = (rows + kMfmaRows - 1) / kMfmaRows;
-        int64_t want = B <= 16 ? 2048 : 512;
-        int64_t splits = g_vlut_splits > 0 ? g_vlut_splits
-                                           : std::max<int64_t>(min_splits, want / std::max<int64_t>(1, row_tiles));
-        return (int)std::max<int64_t>(1, std::min<int64_t>(std::max(splits, min_splits), max_splits));
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cached[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
     }
-    int TT = B >= 8 ? 8 : (B >= 4 ? 4 : (B >= 2 ? 2 : 1));
-    int64_t row_chunks = (rows + kVlutThreads * kVlutRowsPerThread - 1) / (kVlutThreads * kVlutRowsPerThread);
-    int64_t tiles = (B + TT - 1) / TT;
-    int64_t want = g_vlut_splits > 0 ? g_vlut_splits : std::max<int64_t>(1, 256 / std::max<int64_t>(1, row_chunks * tiles));
-    return (int)std::max<int64_t>(1, std::min<int64_t>(want, kb));
+    return cached[dev];
 }
 
-hipError_t vlut_prepare(const uint16_t* words, int64_t n, int q, int legacy, uint32_t* prepared, hipStream_t s)
+}  // namespace
+
+VlutPlan vlut_plan(int64_t rows, int64_t B, int64_t K, int q, int M, int method)
 {
+    const int64_t kb = K / 8;
+    if (method == VLUT_METHOD_LDS) {
+        int TT = B >= 8 ? 8 : (B >= 4 ? 4 : (B >= 2 ? 2 : 1));
+        int64_t row_chunks = (rows + kVlutThreads * kVlutRowsPerThread - 1) / (kVlutThreads * kVlutRowsPerThread);
+        int64_t tiles = (B + TT - 1) / TT;
+        int64_t want = g_vlut_splits > 0 ? g_vlut_splits : std::max<int64_t>(1, 256 / std::max<int64_t>(1, row_chunks * tiles));
+        return {VK_LDS, (int)std::max<int64_t>(1, std::min<int64_t>(want, kb))};
+    }
+    const bool swar = g_vlut_swar && ((q == 2 && M <= 4) || (q == 4 && M <= 2));
+    if (swar) {
+        // one workgroup of 16 rows per CU when the rows allow, else K splits
+        // (each keeping at least one 4-k-block step per wave)
+        const int64_t row_tiles = (rows + 15) / 16;
+        const int64_t max_splits = std::max<int64_t>(1, ((kb + 3) / 4) / kRowsWaves);
+        int64_t splits = g_vlut_splits > 0 ? g_vlut_splits
+                                           : (device_cu_count() + row_tiles - 1) / std::max<int64_t>(1, row_tiles);
+        return {VK_MFMA_ROWS, (int)std::max<int64_t>(1, std::min<int64_t>(splits, max_splits))};
+    }
+    // every workgroup covers at most kMfmaMaxSteps * 16 k-blocks; beyond
+    // that minimum, small batches take more splits (more workgroups in
+    // flight) since their partial sums are cheap
+    int64_t min_splits = (kb + kMfmaKB * kMfmaMaxSteps - 1) / (kMfmaKB * kMfmaMaxSteps);
+    int64_t max_splits = (kb + kMfmaKB - 1) / kMfmaKB;
+    int64_t row_tiles = (rows + kMfmaRows - 1) / kMfmaRows;
+    int64_t want = B <= 16 ? 2048 : 512;
+    int64_t splits = g_vlut_splits > 0 ? g_vlut_splits
+                                       : std::max<int64_t>(min_splits, want / std::max<int64_t>(1, row_tiles));
+    return {VK_MFMA_TILE, (int)std::max<int64_t>(1, std::min<int64_t>(std::max(splits, min_splits), max_splits))};
+}
+
+hipError_t vlut_prepare(const uint16_t* words, int64_t rows, int64_t kb, int M, int q, int legacy, int fmt,
+                        uint32_t* prepared, hipStream_t s)
+{
+    const int64_t n = vlut_prepared_words(rows, kb, M, fmt);
     if (n == 0) return hipSuccess;
     const DecodeTables* t = nullptr;
     hipError_t e = get_decode_tables(q, legacy, &t);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(vlut_prepare_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, words, n, t->cid_map,
-                       prepared);
+    hipLaunchKernelGGL(vlut_prepare_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, words, rows, kb, M, fmt,
+                       n, t->cid_map, t->n_codes - 1u, prepared);
     return hipGetLastError();
 }
 
-hipError_t vlut_matmul(VlutMatmulArgs p, int method, int splits, hipStream_t s)
+namespace {
+
+template <int Q, int M, bool BF16, int NTILE>
+void launch_rows_fmt(const VlutMatmulArgs& p, int splits, hipStream_t s)
+{
+    dim3 grid((unsigned)((p.rows + 15) / 16), (unsigned)splits, (unsigned)((p.B + 16 * NTILE - 1) / (16 * NTILE)));
+    switch (p.prepared) {
+    case VLUT_RAW: hipLaunchKernelGGL((vlut_rows_kernel<Q, M, BF16, NTILE, VLUT_RAW>), grid, dim3(kRowsWaves * 64), 0, s, p); break;
+    case VLUT_PREPARED: hipLaunchKernelGGL((vlut_rows_kernel<Q, M, BF16, NTILE, VLUT_PREPARED>), grid, dim3(kRowsWaves * 64), 0, s, p); break;
+    default: hipLaunchKernelGGL((vlut_rows_kernel<Q, M, BF16, NTILE, VLUT_TILED>), grid, dim3(kRowsWaves * 64), 0, s, p); break;
+    }
+}
+
+template <int Q, int M>
+hipError_t launch_rows(const VlutMatmulArgs& p, int splits, hipStream_t s)
+{
+    if constexpr (Q == 2 || M <= 2) {
+        const bool bf = p.act_dtype == DT_BF16;
+        if (p.B <= 16) {
+            if (bf) launch_rows_fmt<Q, M, true, 1>(p, splits, s); else launch_rows_fmt<Q, M, false, 1>(p, splits, s);
+        } else if (p.B <= 32) {
+            if (bf) launch_rows_fmt<Q, M, true, 2>(p, splits, s); else launch_rows_fmt<Q, M, false, 2>(p, splits, s);
+        } else {
+            if (bf) launch_rows_fmt<Q, M, true, 4>(p, splits, s); else launch_rows_fmt<Q, M, false, 4>(p, splits, s);
+        }
+        return hipGetLastError();
+    }
+    return hipErrorInvalidValue;
+}
+
+template <int Q>
+hipError_t dispatch_rows(const VlutMatmulArgs& p, int splits, hipStream_t s)
+{
+    switch (p.M) {
+    case 1: return launch_rows<Q, 1>(p, splits, s);
+    case 2: return launch_rows<Q, 2>(p, splits, s);
+    case 3: return launch_rows<Q, 3>(p, splits, s);
+    case 4: return launch_rows<Q, 4>(p, splits, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+hipError_t vlut_matmul(VlutMatmulArgs p, const VlutPlan& plan, hipStream_t s)
 {
     if (p.B == 0 || p.rows == 0) return hipSuccess;
-    if (method == VLUT_METHOD_MFMA) {
+    const int splits = plan.splits;
+    if (vlut_workspace_floats(plan, p.B, p.rows) > 0 && !p.partial) return hipErrorInvalidValue;
+    if (plan.kernel == VK_MFMA_TILE) {
         int64_t kb = p.K / 8;
         if ((kb + splits - 1) / splits > (int64_t)kMfmaKB * kMfmaMaxSteps) return hipErrorInvalidValue;
     }
@@ -627,10 +903,17 @@ hipError_t vlut_matmul(VlutMatmulArgs p, int method, int splits, hipStream_t s)
     p.swar = t->swar;
     p.swar_ok = p.M <= t->swar_max_m && g_vlut_swar;
     p.swar_bias = p.swar_ok ? t->swar_bias[p.M] : 0;
-    e = p.q == 4 ? dispatch_m<4>(p, method, splits, s) : dispatch_m<2>(p, method, splits, s);
-    if (e != hipSuccess) return e;
+    if (plan.kernel == VK_MFMA_ROWS) {
+        if (!p.swar_ok) return hipErrorInvalidValue;
+        e = p.q == 4 ? dispatch_rows<4>(p, splits, s) : dispatch_rows<2>(p, splits, s);
+        if (e != hipSuccess || splits == 1) return e;
+    } else {
+        const int method = plan.kernel == VK_LDS ? VLUT_METHOD_LDS : VLUT_METHOD_MFMA;
+        e = p.q == 4 ? dispatch_m<4>(p, method, splits, s) : dispatch_m<2>(p, method, splits, s);
+        if (e != hipSuccess) return e;
+    }
     int64_t n = p.B * p.rows;
-    float mult = method == VLUT_METHOD_MFMA ? 0.5f : 1.f;
+    float mult = plan.kernel == VK_LDS ? 1.f : 0.5f;
     hipLaunchKernelGGL(vlut_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p.partial, splits,
                        p.B, p.rows, p.scale, p.scale_mode, mult, p.out);
     return hipGetLastError();

@@ -10,9 +10,13 @@ constexpr int kMaxCoarseVlut = 640;  // LDS table slots for <a, c> (637 at q = 4
 
 enum VlutMethod { VLUT_METHOD_AUTO = 0, VLUT_METHOD_LDS = 1, VLUT_METHOD_MFMA = 2 };
 
+// Weight formats (include/coset_amd.h): raw uint16 words, row-major
+// prepared uint32 (cid << 16 | idx), tiled prepared (matrix-core fragments).
+enum VlutFormat { VLUT_RAW = 0, VLUT_PREPARED = 1, VLUT_TILED = 2 };
+
 struct VlutMatmulArgs {
-    const void* words;   // [rows, K/8, M] uint16 level words, or uint32 (cid << 16 | idx) when prepared
-    int prepared;
+    const void* words;   // [rows, K/8, M] (VLUT_RAW / VLUT_PREPARED) or tiles (VLUT_TILED)
+    int prepared;        // VlutFormat
     const float* scale;  // [rows] or null
     int scale_mode;      // 0: out *= scale[o]; 1: out /= scale[o]
     const void* act;     // [B, K] fp32 / bf16 / fp16
@@ -36,12 +40,44 @@ extern int g_vlut_swar;
 // > 0 forces the number of K splits (clamped to what the method allows)
 extern int g_vlut_splits;
 
+// Index of level word m of (row, k-block kb) in a weight of format fmt.
+__host__ __device__ inline int64_t vlut_word_index(int fmt, int64_t row, int64_t kb, int m, int64_t kb_total, int M)
+{
+    if (fmt != VLUT_TILED) return (row * kb_total + kb) * M + m;
+    const int64_t kq = (kb_total + 3) / 4;
+    return ((((row >> 4) * kq + (kb >> 2)) * 64) + (row & 15) + 16 * (kb & 3)) * M + m;
+}
+
+__host__ __device__ inline int64_t vlut_prepared_words(int64_t rows, int64_t kb, int M, int fmt)
+{
+    if (fmt != VLUT_TILED) return rows * kb * M;
+    return ((rows + 15) / 16) * ((kb + 3) / 4) * 64 * M;
+}
+
+// Launch plan of a matmul: kernel and K splits (splits > 1 needs a
+// workspace of splits * B * rows floats and a reduce launch).
+enum VlutKernel { VK_LDS = 0, VK_MFMA_TILE = 1, VK_MFMA_ROWS = 2 };
+struct VlutPlan {
+    int kernel;
+    int splits;
+};
+VlutPlan vlut_plan(int64_t rows, int64_t B, int64_t K, int q, int M, int method);
+// Workspace floats a plan needs: the split-K partials [B, rows, splits],
+// none when the rows kernel runs unsplit and writes the output itself.
+inline int64_t vlut_workspace_floats(const VlutPlan& plan, int64_t B, int64_t rows)
+{
+    if (plan.kernel == VK_MFMA_ROWS && plan.splits == 1) return 0;
+    return (int64_t)plan.splits * B * rows;
+}
+
 hipError_t vlut_build(const float* a, int64_t n_queries, int q, int legacy, float* vlut, hipStream_t s);
 hipError_t vlut_dot(const void* words, int64_t n, int M, int q, const float* vlut, float* out, hipStream_t s);
-int vlut_default_splits(int64_t rows, int64_t B, int64_t K, int method);
-hipError_t vlut_matmul(VlutMatmulArgs p, int method, int splits, hipStream_t s);
-// prepared[i] = cid(words[i]) << 16 | words[i]: the coarse-point id each level
-// word decodes through, stored next to it so the matmul needs no map lookup.
-hipError_t vlut_prepare(const uint16_t* words, int64_t n, int q, int legacy, uint32_t* prepared, hipStream_t s);
+hipError_t vlut_matmul(VlutMatmulArgs p, const VlutPlan& plan, hipStream_t s);
+// prepared = cid(word) << 16 | word for raw words [rows, kb, M]: the
+// coarse-point id each level word decodes through, stored next to it so the
+// matmul needs no map lookup; fmt VLUT_PREPARED keeps the layout,
+// VLUT_TILED writes the fragment order (padding decodes to 0).
+hipError_t vlut_prepare(const uint16_t* words, int64_t rows, int64_t kb, int M, int q, int legacy, int fmt,
+                        uint32_t* prepared, hipStream_t s);
 
 }  // namespace coset

@@ -188,36 +188,67 @@ def vlut_dot(words: torch.Tensor, vlut: torch.Tensor, q: int) -> torch.Tensor:
 
 
 _METHODS = {"auto": 0, "lds": 1, "mfma": 2}
+_LAYOUTS = {"rowmajor": 1, "tiled": 2}
 
 
-def vlut_prepare(words: torch.Tensor, q: int = 4, legacy: bool = False) -> torch.Tensor:
-    """uint16 level words [..., M] -> uint32 (coarse id << 16 | idx), same
-    shape: the weight format vlut_matmul reads without table lookups.  Done
-    once per weight; ``legacy`` must match the vlut_matmul call."""
+@dataclass
+class PreparedWords:
+    """Level words converted once for vlut_matmul (coset_vlut_prepare):
+    uint32 cid << 16 | idx values, row-major or tiled in matrix-core fragment
+    order (16 rows x 4 k-blocks per 64-entry tile)."""
+    data: torch.Tensor
+    rows: int
+    kb: int
+    M: int
+    q: int
+    legacy: bool
+    layout: str
+
+    @property
+    def word_format(self) -> int:
+        return _LAYOUTS[self.layout]
+
+
+def vlut_prepare(words: torch.Tensor, q: int = 4, legacy: bool = False, layout: str = "tiled") -> PreparedWords:
+    """uint16 level words [rows, K/8, M] -> PreparedWords, the weight format
+    vlut_matmul reads without table lookups.  Done once per weight; ``legacy``
+    fixes the residual rule the matmul will use."""
     w = on_gpu(words).contiguous()
-    if w.dtype != torch.uint16:
-        raise ValueError("vlut_prepare takes uint16 level words (q <= 4)")
-    out = torch.empty(w.shape, dtype=torch.uint32, device=w.device)
-    _lib.call("coset_vlut_prepare", _lib.ptr(w), w.numel(), int(q), int(legacy), _lib.ptr(out), _lib.stream_of(w))
-    return out
+    if w.dtype != torch.uint16 or w.dim() != 3:
+        raise ValueError("vlut_prepare takes uint16 level words [rows, K/8, M] (q <= 4)")
+    if layout not in _LAYOUTS:
+        raise ValueError(f"layout must be one of {sorted(_LAYOUTS)}")
+    rows, kb, M = w.shape
+    fmt = _LAYOUTS[layout]
+    n = _lib.load().coset_vlut_prepared_words(rows, kb, M, fmt)
+    out = torch.empty(max(int(n), 1), dtype=torch.uint32, device=w.device)
+    _lib.call("coset_vlut_prepare", _lib.ptr(w), rows, kb, int(M), int(q), int(legacy), fmt, _lib.ptr(out),
+              _lib.stream_of(w))
+    return PreparedWords(out, rows, kb, M, int(q), bool(legacy), layout)
 
 
-def vlut_matmul(words: torch.Tensor, act: torch.Tensor, q: int = 4, *, scale: Optional[torch.Tensor] = None,
+def vlut_matmul(words, act: torch.Tensor, q: int = 4, *, scale: Optional[torch.Tensor] = None,
                 scale_mode: str = "mul", legacy: bool = False, method: str = "auto",
                 workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
     """out[B, rows] = s_o * sum_k sum_m q^m vLUT_{act[:, 8k:8k+8]}[words[o, k, m]].
 
-    words: packed level words [rows, K/8, M] (uint16, q in {2, 4}), or their
-    ``vlut_prepare`` form (uint32, prepared with the same ``legacy``); act:
+    words: packed level words [rows, K/8, M] (uint16, q in {2, 4}), or a
+    PreparedWords from vlut_prepare (its q and legacy rule are used); act:
     [B, K] float32 / bfloat16 / float16.  scale (per output row) multiplies
     (``scale_mode="mul"``, codec convention) or divides (``"div"``, layer
     convention).  With the core rule (legacy=False) the result equals
     act @ (e8_decode(codes) * s)^T.
     """
-    w = on_gpu(words).contiguous()
-    if w.dim() != 3:
-        raise ValueError("words must be [rows, K/8, M]")
-    rows, kb, M = w.shape
+    if isinstance(words, PreparedWords):
+        rows, kb, M = words.rows, words.kb, words.M
+        q, legacy, fmt = words.q, words.legacy, words.word_format
+        w = words.data
+    else:
+        w = on_gpu(words).contiguous()
+        if w.dim() != 3 or w.dtype != torch.uint16:
+            raise ValueError("words must be uint16 [rows, K/8, M] or PreparedWords")
+        rows, kb, M = w.shape
+        fmt = 0
     a = on_gpu(act).contiguous()
     if a.dim() != 2 or a.shape[1] != 8 * kb:
         raise ValueError(f"act must be [B, {8 * kb}]")
@@ -225,14 +256,13 @@ def vlut_matmul(words: torch.Tensor, act: torch.Tensor, q: int = 4, *, scale: Op
     m = _METHODS[method]
     dt = _lib.dtype_code(a.dtype)
     need = _lib.load().coset_vlut_workspace_floats(B, rows, K, int(q), int(M), dt, m)
-    if workspace is None or workspace.numel() < need:
-        workspace = torch.empty(max(int(need), 1), dtype=torch.float32, device=a.device)
+    if need > 0 and (workspace is None or workspace.numel() < need):
+        workspace = torch.empty(int(need), dtype=torch.float32, device=a.device)
     s = None
     if scale is not None:
         s = on_gpu(scale).float().contiguous()
     out = torch.empty((B, rows), dtype=torch.float32, device=a.device)
-    fmt = 1 if w.dtype == torch.uint32 else 0
     _lib.call("coset_vlut_matmul", _lib.ptr(w), fmt, _lib.ptr(s), 0 if scale_mode == "mul" else 1, _lib.ptr(a), dt,
-              B, rows, K, int(q), int(M), int(legacy), m, _lib.ptr(workspace), workspace.numel(),
-              _lib.ptr(out), _lib.stream_of(a))
+              B, rows, K, int(q), int(M), int(legacy), m, _lib.ptr(workspace),
+              workspace.numel() if workspace is not None else 0, _lib.ptr(out), _lib.stream_of(a))
     return out

@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define COSET_ABI_VERSION 1
+#define COSET_ABI_VERSION 2
 
 enum {
     COSET_OK = 0,
@@ -171,21 +171,32 @@ int coset_vlut_build_one_sided(const float* queries, int64_t n_queries, int q, i
 int coset_vlut_lookup_dot(const void* words, int64_t n_blocks, int q, int M, const float* vlut, float* out,
                           void* stream);
 
-/* Weight preparation for coset_vlut_matmul (once per weight): prepared[i] =
- * cid << 16 | words[i], cid the id of the coarse point c(b) the uint16 level
- * word decodes through (core rule, or legacy with legacy=1), so the matmul
- * reads it instead of gathering from the per-device map. */
-int coset_vlut_prepare(const void* words, int64_t n_words, int q, int legacy, uint32_t* prepared, void* stream);
+/* Weight formats of coset_vlut_matmul (word_format):
+ *   0  the uint16 level words [rows, K/8, M] as encoded (q^8 <= 65536)
+ *   1  row-major prepared: uint32 cid << 16 | idx, same shape, cid the id of
+ *      the coarse point c(b) the word decodes through, so the matmul reads it
+ *      instead of gathering from the per-device map
+ *   2  tiled prepared: the format-1 values in matrix-core fragment order:
+ *      tiles of 16 rows x 4 k-blocks, tile (row / 16, kb / 4) at index
+ *      (row / 16) * ceil(kb_total / 4) + kb / 4, 64 entries per tile (entry
+ *      row % 16 + 16 * (kb % 4)) of M words each; rows are padded to 16 and
+ *      k-blocks to 4 with the word 0, which decodes to 0.
+ * coset_vlut_prepared_words gives the uint32 count of a format; prepare
+ * (once per weight) converts format-0 words [rows, kb, M] into format 1 or 2
+ * for the core rule (legacy = 0) or the legacy one. */
+int64_t coset_vlut_prepared_words(int64_t rows, int64_t kb, int M, int word_format);
+int coset_vlut_prepare(const void* words, int64_t rows, int64_t kb, int M, int q, int legacy, int word_format,
+                       uint32_t* prepared, void* stream);
 
 /* vLUT matmul: out[t, o] = s_o * sum_k sum_m q^m vLUT_{act[t, 8k:8k+8]}[words[o, k, m]]
- * for level words [rows, K/8, M] (q in {2, 4}, M <= 4): uint16 idx
- * (word_format 0) or coset_vlut_prepare output (word_format 1, same legacy
- * flag), activations
+ * for level words of q in {2, 4}, M <= 4 in any word_format above (a
+ * prepared format with the legacy flag it was prepared with), activations
  * [B, K] fp32/bf16/fp16, s_o = scale[o] (scale_mode 0), 1/scale[o] (1) or 1
  * (scale NULL).  method 1 keeps per-(token, k-block) factorized tables
- * <a, g_j>, <a, c> in LDS; method 2 decodes 2*x_hat into LDS and runs the
- * product on the matrix cores (fp16/bf16 activations); 0 picks 2 when it is
- * exact.  workspace: caller-owned fp32 scratch of coset_vlut_workspace_floats.
+ * <a, g_j>, <a, c> in LDS; method 2 decodes 2*x_hat and runs the product on
+ * the matrix cores (fp16/bf16 activations holding 2*x_hat exactly); 0 picks 2
+ * when it is exact.  workspace: caller-owned fp32 scratch of
+ * coset_vlut_workspace_floats floats (0 is a valid size).
  * The reference has no matmul routine; its placeholder QLinear._lut_matmul is
  * coset/legacy/nn/qlinear.py:272-281. */
 int64_t coset_vlut_workspace_floats(int64_t B, int64_t rows, int64_t K, int q, int M, int act_dtype, int method);

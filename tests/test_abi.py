@@ -32,8 +32,8 @@ def test_library_exports_every_declared_symbol():
 
 def test_python_signatures_cover_the_header():
     from coset_amd import _lib
-    bound = set(_lib.SIGNATURES) | {"coset_abi_version", "coset_last_error", "coset_word_bytes",
-                                    "coset_vlut_workspace_floats"}
+    bound = set(_lib.SIGNATURES) | set(_lib.SIZE_QUERIES) | {"coset_abi_version", "coset_last_error",
+                                                             "coset_word_bytes"}
     assert set(declared()) <= bound
 
 

@@ -107,11 +107,11 @@ def test_vlut_matmul_vs_oracle(method, B, adt, mfma_decode):
     words = torch.from_numpy(words_np.astype(np.int32)).to(torch.uint16).cuda()
     a = torch.from_numpy(rng.standard_normal((B, K)).astype(np.float32)).to(adt)
     for legacy in (False, True):
-        prepared = coset_amd.vlut_prepare(words, q, legacy=legacy)
+        prepared = [coset_amd.vlut_prepare(words, q, legacy=legacy, layout=lay) for lay in ("rowmajor", "tiled")]
         for mode in ("mul", "div"):
             sm = 0 if mode == "mul" else 1
             ref = O.vlut_matmul(words_np, scale, a.float().numpy(), q, M, scale_mode=sm, legacy=legacy)
-            for w in (words, prepared):
+            for w in [words] + prepared:
                 out = coset_amd.vlut_matmul(w, a.cuda(), q, scale=torch.from_numpy(scale), scale_mode=mode,
                                             legacy=legacy, method=method).cpu().numpy()
                 close(out, ref, 1e-3)
@@ -134,9 +134,9 @@ def test_vlut_matmul_other_levels(q, M, B, mfma_decode):
     scale = np.ones(rows, np.float32)
     for legacy in (False, True):
         ref = O.vlut_matmul(words_np, scale, a.float().numpy(), q, M, scale_mode=0, legacy=legacy)
-        prepared = coset_amd.vlut_prepare(words, q, legacy=legacy)
+        prepared = [coset_amd.vlut_prepare(words, q, legacy=legacy, layout=lay) for lay in ("rowmajor", "tiled")]
         for method in ("lds", "mfma"):
-            for w in (words, prepared):
+            for w in [words] + prepared:
                 out = coset_amd.vlut_matmul(w, a.cuda(), q, legacy=legacy, method=method).cpu().numpy()
                 close(out, ref, 1e-3)
 
@@ -164,6 +164,28 @@ def test_vlut_matmul_forced_splits(splits):
         _lib.set_vlut_splits(0)
 
 
+@pytest.mark.parametrize("B", [1, 5, 17, 40, 70])
+def test_vlut_matmul_ragged_shapes(B, mfma_decode):
+    """Rows and k-blocks that fill no tile (37 rows, 13 k-blocks), token
+    counts across the 16 / 32 / 64-token tilings, every weight format."""
+    import coset_amd
+    rng = np.random.default_rng(1000 + B)
+    rows, K, q, M = 37, 104, 4, 2
+    W = rng.standard_normal((rows, K)).astype(np.float32)
+    codes = O.e8_encode(W.reshape(-1, 8), q, M)
+    words_np = O.pack_words(codes, q).reshape(rows, K // 8, M)
+    words = torch.from_numpy(words_np.astype(np.int32)).to(torch.uint16).cuda()
+    a = torch.from_numpy(rng.standard_normal((B, K)).astype(np.float32))
+    scale = rng.uniform(0.5, 2.0, rows).astype(np.float32)
+    ref = O.vlut_matmul(words_np, scale, a.numpy().astype(np.float16).astype(np.float32), q, M)
+    forms = [words] + [coset_amd.vlut_prepare(words, q, layout=lay) for lay in ("rowmajor", "tiled")]
+    for w in forms:
+        for method in ("lds", "mfma"):
+            out = coset_amd.vlut_matmul(w, a.half().cuda(), q, scale=torch.from_numpy(scale),
+                                        method=method).cpu().numpy()
+            close(out, ref, 1e-3)
+
+
 def test_c4_full_size_equals_decoded_product():
     """C4: 4096 x 4096 weights ~ N(0, 0.02) encoded with beta = 0.02 (q4 M2),
     fp16 activations at B = 1, 8, 64; both methods equal a @ decode^T."""
@@ -180,4 +202,4 @@ def test_c4_full_size_equals_decoded_product():
             for w in (words, prepared):
                 out = coset_amd.vlut_matmul(w, a, 4, scale=torch.full((4096,), 0.02), method=method)
                 err = (out - ref).abs().max().item()
-                assert err <= 1e-3 * ref.abs().max().item(), (B, method, w.dtype, err)
+                assert err <= 1e-3 * ref.abs().max().item(), (B, method, type(w).__name__, err)
