@@ -100,12 +100,7 @@ def load():
 
 
 def call(name: str, *args) -> None:
-    rc = getattr(load(), name)(*args)
-    if rc != OK:
-        msg = load().coset_last_error().decode(errors="replace")
-        if rc == EINVAL:
-            raise ValueError(f"{name}: {msg}")
-        raise CosetError(f"{name} failed ({rc}): {msg}")
+    check(name, getattr(load(), name)(*args))
 
 
 def word_bytes(q: int) -> int:
@@ -120,7 +115,22 @@ def ptr(t):
 
 
 def stream_of(t: torch.Tensor) -> int:
-    return torch.cuda.current_stream(t.device).cuda_stream
+    """torch's current HIP stream on t's device (the raw handle)."""
+    return torch._C._cuda_getCurrentRawStream(t.device.index)
+
+
+def fn(name: str):
+    """The bound entry point (for hot paths that call it directly and check
+    the return code with check())."""
+    return getattr(load(), name)
+
+
+def check(name: str, rc: int) -> None:
+    if rc != OK:
+        msg = load().coset_last_error().decode(errors="replace")
+        if rc == EINVAL:
+            raise ValueError(f"{name}: {msg}")
+        raise CosetError(f"{name} failed ({rc}): {msg}")
 
 
 _inited = set()

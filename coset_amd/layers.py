@@ -157,19 +157,19 @@ class E8ThetaWeightQuant(torch.autograd.Function):
         Wc = W.detach().contiguous()
         th = theta.detach().contiguous()
         rows, cols = Wc.shape
-        n = rows * (cols // 8)
-        Wq = torch.empty((rows, cols), dtype=out_dtype, device=Wc.device)
-        packed = torch.empty((n, M), dtype=word_dtype(q), device=Wc.device)
-        beta = torch.empty(th.numel(), dtype=torch.float32, device=Wc.device)
+        dev = Wc.device
+        Wq = torch.empty((rows, cols), dtype=out_dtype, device=dev)
+        packed = torch.empty((rows * (cols // 8), M), dtype=word_dtype(q), device=dev)
+        beta = torch.empty(th.numel(), dtype=torch.float32, device=dev)
         dbdt = torch.empty_like(beta)
         delta0, eta, ginv, m_bounds = bounds
-        _lib.call("coset_e8_qat_fwd_theta", _lib.ptr(Wc), rows, cols, int(blocks_per_tile), _lib.ptr(th),
-                  _lib.ptr(sigma.contiguous()), _lib.ptr(xmax.contiguous()), float(delta0), float(eta),
-                  float(ginv), int(m_bounds), float(clip), int(q), int(M), _lib.ptr(Wq),
-                  _lib.dtype_code(out_dtype), _lib.ptr(packed), _lib.ptr(beta), _lib.ptr(dbdt),
-                  _lib.ptr(step_count), _lib.stream_of(Wc))
+        _lib.check("coset_e8_qat_fwd_theta", _lib.fn("coset_e8_qat_fwd_theta")(
+            Wc.data_ptr(), rows, cols, blocks_per_tile, th.data_ptr(), sigma.contiguous().data_ptr(),
+            xmax.contiguous().data_ptr(), delta0, eta, ginv, m_bounds, clip, q, M, Wq.data_ptr(),
+            _lib.dtype_code(out_dtype), packed.data_ptr(), beta.data_ptr(), dbdt.data_ptr(),
+            step_count.data_ptr(), _lib.stream_of(Wc)))
         ctx.save_for_backward(Wc, packed, beta, dbdt)
-        ctx.cfg = (q, M, float(clip), int(blocks_per_tile), theta.shape)
+        ctx.cfg = (q, M, clip, blocks_per_tile, theta.shape)
         return Wq
 
     @staticmethod
@@ -183,9 +183,10 @@ class E8ThetaWeightQuant(torch.autograd.Function):
         dW = torch.empty_like(Wc)
         dbeta = torch.empty_like(beta)
         dtheta = torch.empty_like(beta)
-        _lib.call("coset_e8_qat_bwd_theta", _lib.ptr(g), _lib.dtype_code(g.dtype), _lib.ptr(Wc), _lib.ptr(packed),
-                  _lib.ptr(beta), _lib.ptr(dbdt), rows, cols, bpt, clip, int(q), int(M), _lib.ptr(dW),
-                  _lib.ptr(dbeta), _lib.ptr(dtheta), _lib.stream_of(Wc))
+        _lib.check("coset_e8_qat_bwd_theta", _lib.fn("coset_e8_qat_bwd_theta")(
+            g.data_ptr(), _lib.dtype_code(g.dtype), Wc.data_ptr(), packed.data_ptr(), beta.data_ptr(),
+            dbdt.data_ptr(), rows, cols, bpt, clip, q, M, dW.data_ptr(), dbeta.data_ptr(), dtheta.data_ptr(),
+            _lib.stream_of(Wc)))
         return dW, dtheta.view(theta_shape), None, None, None, None, None, None, None, None, None
 
 
@@ -366,11 +367,11 @@ class HNLQLinearQAT(nn.Module):
         self._advance_step(device_increment=not fused)
         if fused:
             bpt = self.blocks_per_row if self.tiling == "row" else 1
-            theta = self.theta_beta if self.tiling == "block" else self.theta_beta[: self.out_features]
+            # one theta per tile: out_features entries for row tiling, so no slice is needed
             # the injected e8_quantize always encodes with M = 2 (codecs.py:245-254)
-            W_q = E8ThetaWeightQuant.apply(W, theta, self.sigma_ema, self.xmax_ema, self.step_count,
-                                           (self.Delta0, self.eta, self._ginv_f, self.M), self.q, 2,
-                                           self.weight_clip_value, bpt, out_dtype)
+            W_q = E8ThetaWeightQuant.apply(W, self.theta_beta, self.sigma_ema, self.xmax_ema, self.step_count,
+                                           (float(self.Delta0), float(self.eta), self._ginv_f, int(self.M)),
+                                           int(self.q), 2, float(self.weight_clip_value), int(bpt), out_dtype)
         else:
             W_q = self._reference_composition(W, self._beta()).to(out_dtype)
         if self.enable_diagnostics:
