@@ -22,6 +22,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "e8_fast.hpp"
+
 namespace coset {
 
 constexpr float kEps32 = 1.1920928955078125e-07f;  // torch.finfo(float32).eps
@@ -260,13 +262,18 @@ __device__ __forceinline__ float div_q(float x, float qf)
 }
 
 // One level's residual r = G b - q * P(G b / q) (coset/core/e8/codecs.py:164-166).
+// For q = 2^k the core rule goes through project_dyadic (e8_fast.hpp): G b / q
+// is dyadic and small, where it equals the reference sequence exactly.
 template <bool LEGACY, bool STRIDED, int Q = 0>
 __device__ __forceinline__ void residual_from_point(const float gb[8], float qf, float r[8])
 {
     float z[8], c[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) z[i] = div_q<Q>(gb[i], qf);
-    project<LEGACY, STRIDED>(z, c);
+    if constexpr (!LEGACY && Q > 0 && Q <= 32 && (Q & (Q - 1)) == 0)
+        project_dyadic(z, c);
+    else
+        project<LEGACY, STRIDED>(z, c);
 #pragma unroll
     for (int i = 0; i < 8; ++i) r[i] = __fsub_rn(gb[i], __fmul_rn(qf, c[i]));
 }

@@ -105,4 +105,69 @@ __host__ __device__ inline bool project_fast(const float x[8], float y[8])
     return ok;
 }
 
+// custom_round (coset/core/base.py:179-202): floor((x - sign(x) eps) + 1/2)
+// in fp32, for host and device.
+__host__ __device__ inline float custom_round_hd(float x)
+{
+    const float y = x - copysignf(1.1920928955078125e-07f, x);
+    return floorf(y + 0.5f);
+}
+
+// Exact core-rule E8 projection of a block whose coordinates are multiples
+// of 2^-6 with |x| < 8 -- the decoders' input G b / q for q = 2^k <= 32.
+// For such blocks every difference, square and sum of the reference's
+// projection is exact in fp32, so the reference's comparison of correctly
+// rounded norms is the exact comparison a < b of the squared distances
+// (distinct sums differ by >= 2^-12, far above the roots' rounding), and the
+// contiguous and batched distance rules coincide.  custom_round, the
+// first-index argmax and the core g_x step are the reference's.
+__host__ __device__ inline void project_dyadic(const float x[8], float y[8])
+{
+    float f0[8], d0[8], t1[8], f1[8], d1[8];
+    float best0 = 0.f, best1 = 0.f, s0 = 0.f, s1 = 0.f, a = 0.f, b = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        f0[i] = custom_round_hd(x[i]);
+        d0[i] = x[i] - f0[i];
+        t1[i] = x[i] - 0.5f;
+        f1[i] = custom_round_hd(t1[i]);
+        d1[i] = t1[i] - f1[i];
+        best0 = fmaxf(best0, fabsf(d0[i]));
+        best1 = fmaxf(best1, fabsf(d1[i]));
+        s0 += f0[i];
+        s1 += f1[i];
+        a = fmaf(d0[i], d0[i], a);
+        b = fmaf(d1[i], d1[i], b);
+    }
+    bool first0[8], first1[8];
+    float xk0 = x[0], dk0 = d0[0], tk1 = t1[0], dk1 = d1[0];
+    bool seen0 = false, seen1 = false;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const bool h0 = fabsf(d0[i]) == best0, h1 = fabsf(d1[i]) == best1;
+        first0[i] = h0 && !seen0;
+        first1[i] = h1 && !seen1;
+        seen0 = seen0 || h0;
+        seen1 = seen1 || h1;
+        xk0 = first0[i] ? x[i] : xk0;
+        dk0 = first0[i] ? d0[i] : dk0;
+        tk1 = first1[i] ? t1[i] : tk1;
+        dk1 = first1[i] ? d1[i] : dk1;
+    }
+    const bool odd0 = ((int)s0 & 1) != 0, odd1 = ((int)s1 & 1) != 0;
+    const float adj0 = odd0 ? ((xk0 >= 0.f && dk0 > 0.f) ? 1.f : -1.f) : 0.f;
+    const float adj1 = odd1 ? ((tk1 >= 0.f && dk1 > 0.f) ? 1.f : -1.f) : 0.f;
+    // (d - adj)^2 = d^2 - 2 adj d + |adj|, all exact here
+    a += fmaf(-2.f * adj0, dk0, fabsf(adj0));
+    b += fmaf(-2.f * adj1, dk1, fabsf(adj1));
+    const bool pick0 = a < b;  // ties go to D8 + 1/2, as the reference's strict <
+    const float adj = pick0 ? adj0 : adj1;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const bool at_k = pick0 ? first0[i] : first1[i];
+        const float base = pick0 ? f0[i] : f1[i] + 0.5f;
+        y[i] = base + (at_k ? adj : 0.f);
+    }
+}
+
 }  // namespace coset

@@ -9,6 +9,12 @@
 //   check_fastpath blocks N seed    N blocks from each input family: where
 //                                   project_fast succeeds its point equals
 //                                   the oracle's projection bit for bit
+//   check_fastpath dyadic q N       the decoders' residual G b - q P(G b / q)
+//                                   through project_dyadic against the
+//                                   oracle's (both distance rules): every
+//                                   code for q^8 <= N, else N random codes
+//                                   plus every code with digits in
+//                                   {0, 1, q/2 - 1, q/2, q - 1}
 #include <math.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -25,6 +31,7 @@
 extern "C" {
 float or_custom_round(float x);
 void or_projection(const float* x, int64_t n, int legacy, float* y);
+void or_residual(const int32_t* b, int q, int legacy, int strided, float* r);
 }
 
 static float from_bits(uint32_t u)
@@ -164,11 +171,74 @@ static int blocks(long n, unsigned seed)
     return rc;
 }
 
+static int residual_check(const int32_t b[8], int q, long* bad)
+{
+    float gb[8], z[8], c[8], r[8], ref0[8], ref1[8];
+    const float h = 0.5f * (float)b[7];
+    gb[0] = (float)(2 * b[0] - b[1]) + h;
+    for (int i = 1; i < 6; ++i) gb[i] = (float)(b[i] - b[i + 1]) + h;
+    gb[6] = (float)b[6] + h;
+    gb[7] = h;
+    for (int i = 0; i < 8; ++i) z[i] = gb[i] / (float)q;
+    coset::project_dyadic(z, c);
+    for (int i = 0; i < 8; ++i) r[i] = gb[i] - (float)q * c[i];
+    or_residual(b, q, 0, 0, ref0);
+    or_residual(b, q, 0, 1, ref1);
+    if (memcmp(r, ref0, sizeof r) != 0 || memcmp(r, ref1, sizeof r) != 0) {
+        if (*bad < 5) {
+            printf("mismatch q=%d b=", q);
+            for (int i = 0; i < 8; ++i) printf("%d ", b[i]);
+            printf("\n");
+        }
+        ++*bad;
+        return 1;
+    }
+    return 0;
+}
+
+static int dyadic(int q, long n)
+{
+    long total = 1, bad = 0, checked = 0;
+    for (int i = 0; i < 8; ++i) total *= q;
+    int32_t b[8];
+    if (total <= n) {
+        for (long idx = 0; idx < total; ++idx) {
+            long v = idx;
+            for (int j = 7; j >= 0; --j) {
+                b[j] = (int32_t)(v % q);
+                v /= q;
+            }
+            residual_check(b, q, &bad);
+            ++checked;
+        }
+    } else {
+        const int pick[5] = {0, 1, q / 2 - 1, q / 2, q - 1};
+        for (long idx = 0; idx < 390625; ++idx) {  // 5^8
+            long v = idx;
+            for (int j = 7; j >= 0; --j) {
+                b[j] = pick[v % 5];
+                v /= 5;
+            }
+            residual_check(b, q, &bad);
+            ++checked;
+        }
+        std::mt19937_64 g(1234 + q);
+        for (long it = 0; it < n; ++it) {
+            for (int j = 0; j < 8; ++j) b[j] = (int32_t)(g() % (uint64_t)q);
+            residual_check(b, q, &bad);
+            ++checked;
+        }
+    }
+    printf("dyadic q=%d: %ld codes, mismatches %ld\n", q, checked, bad);
+    return bad ? 1 : 0;
+}
+
 int main(int argc, char** argv)
 {
+    if (argc >= 4 && !strcmp(argv[1], "dyadic")) return dyadic(atoi(argv[2]), atol(argv[3]));
     // an optional second argument replaces the tie limit (a looser one must fail)
     if (argc >= 2 && !strcmp(argv[1], "lemma")) return lemma(argc >= 3 ? strtof(argv[2], nullptr) : coset::kFastTieLimit);
     if (argc >= 4 && !strcmp(argv[1], "blocks")) return blocks(atol(argv[2]), (unsigned)atoi(argv[3]));
-    fprintf(stderr, "usage: %s lemma [limit] | blocks N seed\n", argv[0]);
+    fprintf(stderr, "usage: %s lemma [limit] | blocks N seed | dyadic q N\n", argv[0]);
     return 2;
 }

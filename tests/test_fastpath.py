@@ -1,4 +1,5 @@
-"""CPU checks of the encoder's fast projection (coset_amd/csrc/e8_fast.hpp).
+"""CPU checks of the fast projections (coset_amd/csrc/e8_fast.hpp): the
+encoder's project_fast and the decoders' project_dyadic.
 
 The header is compiled for the host (tests/fastpath/Makefile) and checked
 against the C oracle's projection: exhaustively for the rounding lemma it
@@ -50,3 +51,13 @@ def test_fast_projection_matches_oracle(checker):
     assert len(rates) == 7
     assert rates[6] > 99.0, out   # uniform box: almost always fast
     assert rates[4] > 10.0, out   # near coset boundaries: many decided, the rest fall back
+
+
+@pytest.mark.parametrize("q,n", [(2, 1 << 20), (4, 1 << 20), (8, 1 << 24), (16, 1000000)])
+def test_dyadic_projection_matches_oracle(checker, q, n):
+    """The decoders' exact projection of G b / q for q = 2^k: every code for
+    q <= 8 (16.7 M at q = 8), a structured and random sample at q = 16,
+    residuals equal to the oracle's under both distance rules."""
+    rc, out = run(checker, "dyadic", str(q), str(n))
+    assert rc == 0, out
+    assert " mismatches 0" in out, out
