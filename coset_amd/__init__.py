@@ -44,6 +44,8 @@ from .vlut import (
     PreparedWords,
 )
 
+from . import legacy  # coset.legacy.quant.functional: encode / decode / quantize with the overload loop
+
 __version__ = "0.1.0"
 
 __all__ = [
@@ -54,4 +56,5 @@ __all__ = [
     "E8WeightQuant", "E8ThetaWeightQuant", "create_e8_hnlq_linear", "get_generators", "ste_quantize",
     "vLUTManager", "QuantizationConfig", "build_vlut", "_encoding_to_index", "vlut_mac_operation",
     "vlut_accumulate_operation", "build_one_sided_vluts", "vlut_dot", "vlut_matmul", "vlut_prepare", "PreparedWords",
+    "legacy",
 ]

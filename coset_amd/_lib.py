@@ -48,6 +48,9 @@ SIGNATURES = {
     "coset_vlut_prepare": [_vp, _i64, _i64, _int, _int, _int, _int, _vp, _vp],
     "coset_vlut_matmul": [_vp, _int, _vp, _int, _vp, _int, _i64, _i64, _i64, _int, _int, _int, _int, _vp, _i64,
                           _vp, _vp],
+    "coset_e8_legacy_encode": [_vp, _int, _i64, _flt, ctypes.c_double, _int, _int, _vp, _i64, _int, _int, _vp,
+                               _vp, _vp, _vp, _vp, _vp],
+    "coset_e8_legacy_decode": [_vp, _vp, _vp, _i64, _flt, ctypes.c_double, _vp, _i64, _int, _int, _vp, _vp],
     "coset_init": [_int],
     "coset_set_option": [_int, _int],
 }

@@ -10,6 +10,7 @@
 
 #include "../../include/coset_amd.h"
 #include "codec_kernels.hpp"
+#include "legacy.hpp"
 #include "tables.hpp"
 #include "vlut.hpp"
 
@@ -178,6 +179,77 @@ static int codec_common(int mode, const void* x, int x_dtype, int64_t n, int sca
     a.out = out;
     a.out_dtype = out_dtype;
     return check_hip(coset::launch_codec(a, mode, (hipStream_t)stream), "codec launch");
+}
+
+static int legacy_common(coset::LegacyArgs& a, int64_t n, float beta, double alpha, int q, int M,
+                         const float* dither, int64_t dither_stride)
+{
+    int rc;
+    if (n < 0) return fail(COSET_EINVAL, "n_blocks < 0");
+    if (n > (int64_t)0x7fffffff * 256) return fail(COSET_EINVAL, "n_blocks too large");
+    if ((rc = check_qm(q, M))) return rc;
+    if (!(beta > 0.f) || !std::isfinite(beta)) return fail(COSET_EINVAL, "beta must be positive (got %g)", (double)beta);
+    if (!(alpha >= 0.0) || !std::isfinite(alpha)) return fail(COSET_EINVAL, "alpha must be >= 0 (got %g)", alpha);
+    if (dither && dither_stride != 0 && dither_stride != 8) return fail(COSET_EINVAL, "dither_stride must be 0 or 8");
+    a.n = n;
+    a.q = q;
+    a.M = M;
+    a.beta = beta;
+    int ex = 0;
+    const float m = std::frexp(beta, &ex);
+    a.beta_is_pow2 = m == 0.5f ? 1 : 0;
+    a.beta_inv = a.beta_is_pow2 ? std::ldexp(1.0f, 1 - ex) : 1.0f;
+    // Python's 2 ** alpha and 2 ** (alpha * T) are doubles, rounded to fp32
+    // where they meet the fp32 tensor
+    a.two_alpha = (float)std::pow(2.0, alpha);
+    for (int t = 0; t <= coset::kLegacyMaxT; ++t) a.scale_T[t] = (float)std::pow(2.0, alpha * t);
+    a.dither = dither;
+    a.dither_stride = dither_stride;
+    return COSET_OK;
+}
+
+int coset_e8_legacy_encode(const void* x, int x_dtype, int64_t n_blocks, float beta, double alpha, int max_iter,
+                           int protect, const float* dither, int64_t dither_stride, int q, int M, void* packed,
+                           float* codes_f32, int32_t* T, uint8_t* overload, float* decoded, void* stream)
+{
+    int rc;
+    coset::LegacyArgs a{};
+    if ((rc = legacy_common(a, n_blocks, beta, alpha, q, M, dither, dither_stride))) return rc;
+    if (max_iter < 0 || max_iter > coset::kLegacyMaxT)
+        return fail(COSET_EINVAL, "max_iter=%d outside [0,%d]", max_iter, coset::kLegacyMaxT);
+    if (n_blocks > 0 && !x) return fail(COSET_EINVAL, "x is NULL");
+    if ((rc = check_dtype(x_dtype, "input"))) return rc;
+    if (!aligned(x, 16)) return fail(COSET_EINVAL, "x must be 16-byte aligned");
+    if (codes_f32 && !aligned(codes_f32, 16)) return fail(COSET_EINVAL, "codes_f32 must be 16-byte aligned");
+    if (decoded && !aligned(decoded, 16)) return fail(COSET_EINVAL, "decoded must be 16-byte aligned");
+    if (packed && !aligned(packed, 4)) return fail(COSET_EINVAL, "packed must be 4-byte aligned");
+    a.max_iter = max_iter;
+    a.protect = protect ? 1 : 0;
+    a.x = x;
+    a.x_dtype = x_dtype;
+    a.packed = packed;
+    a.codes_f32 = codes_f32;
+    a.T = T;
+    a.overload = overload;
+    a.out = decoded;
+    return check_hip(coset::launch_legacy(a, false, (hipStream_t)stream), "legacy encode launch");
+}
+
+int coset_e8_legacy_decode(const void* packed, const float* codes_f32, const int32_t* T, int64_t n_blocks,
+                           float beta, double alpha, const float* dither, int64_t dither_stride, int q, int M,
+                           float* out, void* stream)
+{
+    int rc;
+    coset::LegacyArgs a{};
+    if ((rc = legacy_common(a, n_blocks, beta, alpha, q, M, dither, dither_stride))) return rc;
+    if (n_blocks > 0 && ((!packed && !codes_f32) || !out)) return fail(COSET_EINVAL, "NULL buffer");
+    if (codes_f32 && !aligned(codes_f32, 16)) return fail(COSET_EINVAL, "codes_f32 must be 16-byte aligned");
+    if (!aligned(out, 16)) return fail(COSET_EINVAL, "out must be 16-byte aligned");
+    a.packed_in = packed;
+    a.codes_in_f32 = packed ? nullptr : codes_f32;
+    a.T_in = T;
+    a.out = out;
+    return check_hip(coset::launch_legacy(a, true, (hipStream_t)stream), "legacy decode launch");
 }
 
 int coset_e8_hnlq_encode(const void* x, int x_dtype, int64_t n_blocks, int scale_mode,

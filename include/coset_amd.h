@@ -81,6 +81,25 @@ int coset_abi_version(void);
 const char* coset_last_error(void);
 int coset_word_bytes(int q);
 
+/* The paper's hierarchical quantizer with overload handling
+ * (coset/legacy/quant/functional.py:15-181, Algorithms 1 and 2), per 8-wide
+ * block: xs = x / beta (+ dither), level chain y = Q(x_l), x_l = y / q with
+ * the legacy (textbook) Q; a block overloads when Q(x_M) != 0.  With protect
+ * set, an overloading block is rescaled xs /= 2^alpha and re-encoded up to
+ * max_iter (<= 63) times.  Outputs (each nullable): the final chain's level
+ * words and float codes [n, M, 8], T [n] (int32 rescale count), overload
+ * [n] (uint8, the final chain's flag; the core codecs have none, their T is
+ * always 0 as in codecs.py:89) and decoded [n, 8]: Algorithm 2 of the same
+ * codes.  Decode: x_hat = sum_i q^i r(b_i) with the legacy residual, minus
+ * dither, times beta, times (float)2^(alpha T) (T NULL: T = 0). */
+int coset_e8_legacy_encode(const void* x, int x_dtype, int64_t n_blocks, float beta, double alpha,
+                           int max_iter, int protect, const float* dither, int64_t dither_stride,
+                           int q, int M, void* packed, float* codes_f32, int32_t* T,
+                           uint8_t* overload, float* decoded, void* stream);
+int coset_e8_legacy_decode(const void* packed, const float* codes_f32, const int32_t* T,
+                           int64_t n_blocks, float beta, double alpha, const float* dither,
+                           int64_t dither_stride, int q, int M, float* out, void* stream);
+
 /* Build the per-device constant tables (single-level decode and vLUT coarse
  * points for q = 2 and 4, core and legacy rules) on `device` (-1: current).
  * Blocking; call once before capturing HIP graphs.  Other entry points build

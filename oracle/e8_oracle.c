@@ -321,3 +321,73 @@ void or_vlut_matmul(const uint32_t* words, const float* scale, int scale_mode,
         }
     }
 }
+
+/* ---------------------------------------------------------------- legacy
+ * Hierarchical encode/decode of coset/legacy/quant/functional.py (the
+ * paper's Algorithms 1 and 2), one 8-vector at a time as the reference. */
+
+/* _encode_internal (functional.py:83-116): y = Q(x_l), b = coords(y),
+ * x_l = y / q for M levels with the legacy Q; overload = Q(x_M) != 0
+ * (allclose to 0 at atol 1e-8 on lattice points). */
+static int legacy_chain(const float* xs, int q, int M, int32_t* codes)
+{
+    float xl[8], y[8];
+    memcpy(xl, xs, sizeof xl);
+    for (int m = 0; m < M; ++m) {
+        project1(xl, 1, 0, y);
+        encode_coords1(y, q, codes + 8 * m);
+        for (int i = 0; i < 8; ++i) xl[i] = y[i] / (float)q;
+    }
+    project1(xl, 1, 0, y);
+    for (int i = 0; i < 8; ++i)
+        if (!(fabsf(y[i]) <= 1e-8f)) return 1;  /* NaN also fails allclose */
+    return 0;
+}
+
+/* encode (functional.py:15-80): xs = x / beta (+ dither), then while
+ * overload and t < max_iter (protect only): xs = xs / two_alpha, t += 1.
+ * codes [n, M, 8]; T [n]; overload [n] = the final chain's flag. */
+void or_legacy_encode(const float* x, int64_t n, float beta, float two_alpha, int max_iter, int protect,
+                      const float* dither, int64_t dither_stride, int q, int M, int32_t* codes, int32_t* T,
+                      uint8_t* overload)
+{
+    for (int64_t b = 0; b < n; ++b) {
+        float xs[8];
+        for (int i = 0; i < 8; ++i) {
+            xs[i] = x[8 * b + i] / beta;
+            if (dither) xs[i] = xs[i] + dither[dither_stride * b + i];
+        }
+        int t = 0;
+        int ov = legacy_chain(xs, q, M, codes + (size_t)b * M * 8);
+        while (protect && ov && t < max_iter) {
+            ++t;
+            for (int i = 0; i < 8; ++i) xs[i] = xs[i] / two_alpha;
+            ov = legacy_chain(xs, q, M, codes + (size_t)b * M * 8);
+        }
+        T[b] = t;
+        overload[b] = (uint8_t)ov;
+    }
+}
+
+/* decode (functional.py:119-181): x_hat = sum_i q^i (G b_i - q Q(G b_i / q))
+ * accumulated in fp32 from zero, minus dither, then (beta * x_hat) * s_T
+ * with s_T = (float)2^(alpha T) (scale_T[T[b]]). */
+void or_legacy_decode(const int32_t* codes, const int32_t* T, int64_t n, float beta, const float* scale_T,
+                      const float* dither, int64_t dither_stride, int q, int M, float* out)
+{
+    for (int64_t b = 0; b < n; ++b) {
+        float acc[8] = {0};
+        float w = 1.f;
+        for (int m = 0; m < M; ++m) {
+            float r[8];
+            or_residual(codes + ((size_t)b * M + m) * 8, q, 1, 0, r);
+            for (int i = 0; i < 8; ++i) acc[i] = acc[i] + w * r[i];
+            w = w * (float)q;
+        }
+        for (int i = 0; i < 8; ++i) {
+            float v = acc[i];
+            if (dither) v = v - dither[dither_stride * b + i];
+            out[8 * b + i] = (beta * v) * scale_T[T[b]];
+        }
+    }
+}

@@ -78,6 +78,22 @@ void or_vlut_matmul(const uint32_t* words, const float* scale, int scale_mode,
                     const float* act, int64_t B, int64_t rows, int64_t K,
                     int q, int M, int legacy, float* out);
 
+/* coset/legacy/quant/functional.py:15-116 (encode with the overload loop,
+ * the paper's Algorithm 1) for n 8-vectors: xs = x / beta (+ dither
+ * [8] or [n, 8] by dither_stride 0 / 8), the chain y = Q(xs), xs = y / q
+ * over M levels with the legacy Q, and while the chain overloads
+ * (Q(x_M) != 0), protect is set and t < max_iter: xs /= two_alpha.
+ * codes [n, M, 8]; T [n]; overload [n]: the final chain's flag. */
+void or_legacy_encode(const float* x, int64_t n, float beta, float two_alpha, int max_iter, int protect,
+                      const float* dither, int64_t dither_stride, int q, int M, int32_t* codes, int32_t* T,
+                      uint8_t* overload);
+
+/* coset/legacy/quant/functional.py:119-181 (decode, Algorithm 2): legacy
+ * residuals summed with q^i in fp32, minus dither, times beta, times
+ * scale_T[T] = (float)2^(alpha T). */
+void or_legacy_decode(const int32_t* codes, const int32_t* T, int64_t n, float beta, const float* scale_T,
+                      const float* dither, int64_t dither_stride, int q, int M, float* out);
+
 #ifdef __cplusplus
 }
 #endif

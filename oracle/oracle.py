@@ -56,6 +56,11 @@ def lib():
         L.or_build_one_sided_vlut.argtypes = [_f32p, _int, _int, _f32p]
         L.or_vlut_matmul.argtypes = [_u32p, _f32p, _int, _f32p, _i64, _i64, _i64,
                                      _int, _int, _int, _f32p]
+        _u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
+        L.or_legacy_encode.argtypes = [_f32p, _i64, _flt, _flt, _int, _int, ctypes.c_void_p, _i64, _int, _int,
+                                       _i32p, _i32p, _u8p]
+        L.or_legacy_decode.argtypes = [_i32p, _i32p, _i64, _flt, _f32p, ctypes.c_void_p, _i64, _int, _int,
+                                       _f32p]
         _lib = L
     return _lib
 
@@ -225,3 +230,40 @@ def layer_backward(gWq, W, qraw, beta_row, clip):
     dW = gQ * beta
     dbeta = (gQ * W).sum(axis=1) - (gm * Q / (beta * beta)).sum(axis=1)
     return dW, dbeta, mask
+
+
+# --------------------------------------------------------------------------
+# legacy hierarchical encode / decode (coset/legacy/quant/functional.py)
+# --------------------------------------------------------------------------
+
+def legacy_scale_table(alpha, n=64):
+    """(float)2^(alpha t), t = 0..n-1: the decode's 2 ** (alpha * T) in fp32."""
+    return np.array([np.float32(2.0 ** (alpha * t)) for t in range(n)], np.float32)
+
+
+def legacy_encode(x, q, M, beta, alpha=1.0, max_iter=10, protect=True, dither=None):
+    """functional.py:15-116 per 8-vector: codes [N, M, 8], T [N], overload [N]."""
+    x = _f32(x).reshape(-1, 8)
+    n = x.shape[0]
+    codes = np.empty((n, M, 8), np.int32)
+    T = np.empty(n, np.int32)
+    ov = np.empty(n, np.uint8)
+    d = None if dither is None else _f32(dither)
+    stride = 0 if d is None or d.size == 8 else 8
+    lib().or_legacy_encode(x, n, float(np.float32(beta)), float(np.float32(2.0 ** alpha)), int(max_iter),
+                           int(bool(protect)), None if d is None else d.ctypes.data, stride, int(q), int(M),
+                           codes, T, ov)
+    return codes, T, ov
+
+
+def legacy_decode(codes, T, q, M, beta, alpha=1.0, dither=None):
+    """functional.py:119-181 per 8-vector: [N, 8]."""
+    codes = np.ascontiguousarray(codes, np.int32).reshape(-1, M, 8)
+    n = codes.shape[0]
+    T = np.ascontiguousarray(T, np.int32).reshape(-1)
+    out = np.empty((n, 8), np.float32)
+    d = None if dither is None else _f32(dither)
+    stride = 0 if d is None or d.size == 8 else 8
+    lib().or_legacy_decode(codes, T, n, float(np.float32(beta)), legacy_scale_table(alpha),
+                           None if d is None else d.ctypes.data, stride, int(q), int(M), out)
+    return out

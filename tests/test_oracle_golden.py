@@ -183,3 +183,46 @@ def test_pack_roundtrip():
     # idx(b) = sum_j b_j q^(7-j) (coset/legacy/quant/vlut.py:231-236)
     b = np.array([[[1, 2, 3, 0, 0, 0, 0, 1]]], np.int32)
     assert O.pack_words(b, 4)[0, 0] == 1 * 4 ** 7 + 2 * 4 ** 6 + 3 * 4 ** 5 + 1
+
+
+LEGACY_CASES = ["q4M2_p", "q3M2_p", "q8M2_a2", "q4M3_np", "q2M4_p", "q4M2_dither"]
+
+
+def _legacy_case(golden, name):
+    z = golden("legacy_functional")
+    cfg = z[f"{name}_cfg"]
+    q, M, beta, alpha, mi, prot = int(cfg[0]), int(cfg[1]), float(cfg[2]), float(cfg[3]), int(cfg[4]), int(cfg[5])
+    d = z[f"{name}_dither"] if f"{name}_dither" in z else None
+    return z, q, M, beta, alpha, mi, prot, d
+
+
+@pytest.mark.parametrize("name", LEGACY_CASES)
+def test_oracle_legacy_functional(golden, name):
+    """coset/legacy/quant/functional.py encode (overload loop) / decode:
+    codes, T, final overload flag and decode bit-exact against the
+    reference's own outputs (tests/golden/legacy_functional.npz)."""
+    z, q, M, beta, alpha, mi, prot, d = _legacy_case(golden, name)
+    codes, T, ov = O.legacy_encode(z[f"{name}_x"], q, M, beta, alpha, mi, prot, d)
+    np.testing.assert_array_equal(codes, z[f"{name}_codes"])
+    np.testing.assert_array_equal(T, z[f"{name}_T"])
+    np.testing.assert_array_equal(ov, z[f"{name}_overload"])
+    np.testing.assert_array_equal(O.legacy_decode(codes, T, q, M, beta, alpha, d), z[f"{name}_decoded"])
+
+
+def test_oracle_legacy_closed_forms():
+    """Cases the definition fixes: tiny inputs never overload (T = 0, codes
+    of Q(x/beta)); without protection T stays 0; a huge block exhausts the
+    loop (T = max_iter, still overloading); the decode scales by 2^(alpha T)."""
+    x = np.full((1, 8), 1e-6, np.float32)
+    c, T, ov = O.legacy_encode(x, 4, 2, 0.3, 1.0, 10, True)
+    assert T[0] == 0 and ov[0] == 0 and not c.any()
+    big = np.full((1, 8), 1e6, np.float32)
+    c, T, ov = O.legacy_encode(big, 4, 2, 0.3, 1.0, 3, True)
+    assert T[0] == 3 and ov[0] == 1
+    c0, T0, ov0 = O.legacy_encode(big, 4, 2, 0.3, 1.0, 3, False)
+    assert T0[0] == 0 and ov0[0] == 1
+    rng = np.random.default_rng(4)
+    codes = rng.integers(0, 4, (16, 2, 8)).astype(np.int32)
+    d0 = O.legacy_decode(codes, np.zeros(16, np.int32), 4, 2, 0.5, 1.0)
+    d3 = O.legacy_decode(codes, np.full(16, 3, np.int32), 4, 2, 0.5, 1.0)
+    np.testing.assert_array_equal(d3, d0 * np.float32(8.0))
