@@ -1,6 +1,6 @@
 """Benchmark of the E8 HNLQ hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2,c4,...]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2,c2codes,c4,...]
 
 Headline workload ("C2"): 2^24 fp32 8-wide blocks
 ~ N(0,1) (seeded), fixed beta = 1, q = 4, M = 2.  One step = the fused
@@ -9,9 +9,12 @@ per block) and the decoded fp32 blocks.  Inputs are resident in HBM before
 timing starts; `value` is whole-job Gblocks/s.
 
 The other BASELINE configurations are measured alongside under "extra":
-  c1  layer forward 768 -> 10 on a 32 x 768 fp32 batch (latency)
+  c1  layer forward 768 -> 10 on a 32 x 768 fp32 batch (latency), and its
+      non-degenerate variant (Delta0 = 1.5, W ~ N(0, 1))
+  c2codes  the C2 round trip also writing the reference's float code tensor
   c3  2^22 Student-t(3) blocks clipped at +-2 in bf16, q16 M3, per-row beta
   c4  vLUT matmul of 4096 x 4096 q4 M2 codes with fp16 activations, B = 1, 8, 64
+      (core and legacy-Q residuals, tiled prepared and raw words, LDS-table method)
   c5  QAT linear forward + backward, BERT-base shapes, 4096 bf16 tokens
 The roofline object is the C2 codec kernel's (HIP events on its launch
 stream); cpu_baseline is the C oracle on the host, single thread.
@@ -115,8 +118,44 @@ def bench_c1(torch, ca, args):
     x = torch.randn(32, 768, device="cuda")
     with torch.no_grad():
         k, w = gpu_time(torch, lambda: layer(x), 200, 20)
-    return {"workload": "C1 layer forward 768->10, x 32x768 fp32, q4 M2 theta 0",
-            "us_per_forward_gpu": round(k * 1e6, 2), "us_per_forward_wall": round(w * 1e6, 2)}
+    res = {"workload": "C1 layer forward 768->10, x 32x768 fp32, q4 M2 theta 0 (W_q == 0 at these settings)",
+           "us_per_forward_gpu": round(k * 1e6, 2), "us_per_forward_wall": round(w * 1e6, 2)}
+    # the non-degenerate variant: Delta0 = 1.5, W ~ N(0, 1)
+    torch.manual_seed(0)
+    layer2 = ca.create_e8_hnlq_linear(768, 10, q=4, M=2, theta_trainable=False, theta_init_value=0.0,
+                                      weight_clip_value=2.0, Delta0=1.5)
+    with torch.no_grad():
+        layer2.weight.normal_(0.0, 1.0)
+        nz = float((layer2._quantize_weights() != 0).float().mean())
+        k2, w2 = gpu_time(torch, lambda: layer2(x), 200, 20)
+    res["nondegenerate"] = {"workload": "Delta0 1.5, W ~ N(0,1)", "nonzero_weight_frac": round(nz, 3),
+                            "us_per_forward_gpu": round(k2 * 1e6, 2), "us_per_forward_wall": round(w2 * 1e6, 2)}
+    return res
+
+
+def bench_c2_codes(torch, ca, args):
+    """The C2 round trip on the reference's float code tensor too (the
+    e8_encode compat layout [N, M, 8] fp32: +64 B per block)."""
+    dev = torch.device("cuda")
+    n = C2_BLOCKS
+    g = torch.Generator(device=dev).manual_seed(2)
+    x = torch.randn((n, 8), device=dev, generator=g, dtype=torch.float32)
+    packed = torch.empty((n, 2), dtype=torch.uint16, device=dev)
+    codes = torch.empty((n, 2, 8), dtype=torch.float32, device=dev)
+    out = torch.empty((n, 8), dtype=torch.float32, device=dev)
+    from coset_amd import _lib
+
+    def step():
+        _lib.call("coset_e8_hnlq_roundtrip", _lib.ptr(x), _lib.F32, n, _lib.SCALE_CODEC, 1.0, None, 0, 0.0,
+                  None, 0, 4, 2, 1, _lib.ptr(packed), _lib.ptr(codes), _lib.ptr(out), _lib.F32, _lib.stream_of(x))
+
+    k, _ = gpu_time(torch, step, 20, 3)
+    nbytes = n * (C2_BYTES_PER_BLOCK + 64)
+    del x, packed, codes, out
+    return {"workload": "C2 round trip also writing float codes [2^24, 2, 8] (compat layout)",
+            "kernel_us": round(k * 1e6, 2), "gblocks_per_s": round(n / k / 1e9, 3),
+            "hbm_gbs": round(nbytes / k / 1e9, 1), "frac_hbm": round(nbytes / k / 1e9 / HBM_PEAK_GBS, 4),
+            "bytes_per_block": C2_BYTES_PER_BLOCK + 64}
 
 
 def bench_c3(torch, ca, args):
@@ -189,6 +228,7 @@ def bench_c4(torch, ca, args):
     W = 0.02 * torch.randn((4096, 4096), device="cuda", generator=g)
     words = ca.hnlq_encode(W.reshape(-1, 8), 4, 2, 0.02).reshape(4096, 512, 2)
     tiled = ca.vlut_prepare(words, 4)   # once per weight: cid << 16 | idx in fragment order, 16 MiB
+    tiled_legacy = ca.vlut_prepare(words, 4, legacy=True)   # the reference vLUT's textbook-Q residuals
     scale = torch.full((4096,), 0.02, device="cuda")
     del W
     res = {"workload": "C4 vLUT matmul 4096x4096 q4 M2 codes (8 MiB uint16 words; 16 MiB tiled prepared), "
@@ -198,7 +238,8 @@ def bench_c4(torch, ca, args):
     for B in (1, 8, 64):
         a = torch.randn((B, 4096), device="cuda", generator=g).to(torch.float16)
         row = {}
-        for method, wts in (("mfma", tiled), ("mfma_raw_words", words), ("lds", tiled)):
+        for method, wts in (("mfma", tiled), ("mfma_legacy_q", tiled_legacy), ("mfma_raw_words", words),
+                            ("lds", tiled)):
             m = "mfma" if method.startswith("mfma") else "lds"
             fn = lambda: ca.vlut_matmul(wts, a, 4, scale=scale, method=m, workspace=ws)
             k_eager, _ = gpu_time(torch, fn, 50 if m == "lds" else 100, 5)
@@ -248,7 +289,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-sample", type=int, default=1 << 24,
                     help="C2 blocks timed on the host CPU oracle (0 skips it)")
-    ap.add_argument("--only", default="c1,c2,c3,c4,c5", help="comma list of workloads to run")
+    ap.add_argument("--only", default="c1,c2,c2codes,c3,c4,c5", help="comma list of workloads to run")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 512 MiB device copy (HBM counter calibration)")
     args = ap.parse_args()
@@ -275,7 +316,8 @@ def main():
     cpu = None
     if "c2" in only:
         kernel_s, wall_s, cpu = bench_c2(torch, ca, args)
-    for name, fn in (("c1", bench_c1), ("c3", bench_c3), ("c4", bench_c4), ("c5", bench_c5)):
+    for name, fn in (("c1", bench_c1), ("c2codes", bench_c2_codes), ("c3", bench_c3), ("c4", bench_c4),
+                     ("c5", bench_c5)):
         if name in only:
             extra[name] = fn(torch, ca, args)
             torch.cuda.empty_cache()
