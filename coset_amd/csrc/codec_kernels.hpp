@@ -86,11 +86,24 @@ struct CodecArgs {
     int fast_projection;     // encoders try project_fast first (set by the launcher)
 };
 
-// Encoder projection (core rule, contiguous distances): the fast path where
-// its conditions hold, the reference sequence for the lanes where they fail.
-__device__ __forceinline__ void project_encode(const float x[8], float y[8], int fast)
+// One encoder level (core rule, contiguous distances): the projection --
+// the fast path where its conditions hold, the reference sequence for the
+// lanes where they fail -- and the digits of the chosen point.  The branches
+// meet at the digits, and the fast branch (|y| < 2^21 + 1) takes the shorter
+// digit form.
+template <int Q>
+__device__ __forceinline__ void encode_level(const float x[8], int fast, int q, int b[8])
 {
-    if (!(fast && project_fast(x, y))) project<false, false>(x, y);
+    float y[8];
+    if (fast && project_fast(x, y)) {
+        if constexpr (Q > 0 && (Q & (Q - 1)) == 0)
+            lattice_digits_small<Q>(y, b);
+        else
+            lattice_digits<Q>(y, q, b);
+    } else {
+        project<false, false>(x, y);
+        lattice_digits<Q>(y, q, b);
+    }
 }
 
 // Per-block scale of SCALE_LAYER (reads beta_row or derives it from theta).

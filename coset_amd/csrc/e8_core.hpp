@@ -138,24 +138,32 @@ __device__ __forceinline__ void project(const float x[8], float out[8])
 }
 
 // encode_coords: b = (G^-1 y) mod q for y in E8 (exact integers).
-//   (G^-1 y)_0 = (y0+..+y6)/2 - 3.5 y7 = (z0+..+z6)/2
-//   (G^-1 y)_r = (y_r+..+y6) - (7-r) y7 = z_r+..+z6      r = 1..6
+//   (G^-1 y)_0 = (y0+..+y6)/2 - 3.5 y7
+//   (G^-1 y)_r = (y_r+..+y6) - (7-r) y7     r = 1..6
 //   (G^-1 y)_7 = 2 y7
-// with z_j = y_j - y_7: y in E8 has all coordinates integral or all
-// half-integral, so every z_j is an exact integer (and so is each row).
+// computed on u = 2y as int32: exact for |y| < 2^30 (for q = 2^k the digits
+// only need the low bits, which wrap-around keeps).  y in E8 makes every row
+// an integer; a row can be fractional only for |x| >= 2^23, where fp32 cannot
+// hold the D8 + 1/2 coset and the projection leaves E8 -- such rows are
+// rounded half to even, the reference's torch.round of the exact product.
 template <int Q>
 __device__ __forceinline__ void lattice_digits(const float y[8], int q, int b[8])
 {
+    int u[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) u[i] = (int)__fmul_rn(2.f, y[i]);  // 2y: exact integers
+    int suf = 0;  // 2 * (y_r + .. + y6)
     int c[8];
-    int suf = 0;  // z_r + .. + z_6
 #pragma unroll
     for (int r = 6; r >= 1; --r) {
-        suf += (int)__fsub_rn(y[r], y[7]);
-        c[r] = suf;
+        suf += u[r];
+        const int v = suf - (7 - r) * u[7];  // 2 * row
+        c[r] = (v + ((v >> 1) & 1)) >> 1;    // v / 2, ties to even
     }
-    suf += (int)__fsub_rn(y[0], y[7]);
-    c[0] = suf >> 1;
-    c[7] = (int)__fmul_rn(2.f, y[7]);
+    suf += u[0];
+    const int v0 = suf - 7 * u[7];           // 4 * row 0
+    c[0] = (v0 + 1 + ((v0 >> 2) & 1)) >> 2;  // v0 / 4, nearest, ties to even
+    c[7] = u[7];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         if (Q > 0 && (Q & (Q - 1)) == 0) {
@@ -168,26 +176,26 @@ __device__ __forceinline__ void lattice_digits(const float y[8], int q, int b[8]
     }
 }
 
-// The same digits through the row sums of 2y (for q = 2^k).  A second
-// instruction sequence for one result: the encoders use it on their exact
-// fallback so the two branches meet at the packed word, not at y.
+// The same digits for |y| < 2^22 and q = 2^k, through z_j = y_j - y_7: y in
+// E8 has all coordinates integral or all half-integral, so every z_j is an
+// integer, exact in fp32 at these magnitudes, and
+//   (G^-1 y)_r = z_r + .. + z_6 (r >= 1),  (G^-1 y)_0 = (z_0 + .. + z_6) / 2.
+// Fewer operations than lattice_digits; the encoders use it where the fast
+// projection (|x| < 2^21) produced y.
 template <int Q>
-__device__ __forceinline__ void lattice_digits_2y(const float y[8], int b[8])
+__device__ __forceinline__ void lattice_digits_small(const float y[8], int b[8])
 {
     static_assert(Q > 0 && (Q & (Q - 1)) == 0, "power-of-two q");
-    int u[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) u[i] = (int)__fmul_rn(2.f, y[i]);  // exact integers
-    int suf = 0;  // 2 (y_r + .. + y_6)
     int c[8];
+    int suf = 0;  // z_r + .. + z_6
 #pragma unroll
     for (int r = 6; r >= 1; --r) {
-        suf += u[r];
-        c[r] = (suf - (7 - r) * u[7]) >> 1;
+        suf += (int)__fsub_rn(y[r], y[7]);
+        c[r] = suf;
     }
-    suf += u[0];
-    c[0] = (suf - 7 * u[7]) >> 2;
-    c[7] = u[7];
+    suf += (int)__fsub_rn(y[0], y[7]);
+    c[0] = suf >> 1;
+    c[7] = (int)__fmul_rn(2.f, y[7]);
 #pragma unroll
     for (int i = 0; i < 8; ++i) b[i] = c[i] & (Q - 1);
 }

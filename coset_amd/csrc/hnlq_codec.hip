@@ -73,10 +73,8 @@ __global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
 
         float w = 1.f;
         for (int m = 0; m < M; ++m) {
-            float y[8];
             int b[8];
-            project_encode(xl, y, a.fast_projection);
-            lattice_digits<Q>(y, q, b);
+            encode_level<Q>(xl, a.fast_projection, q, b);
             uint32_t word = pack_word<Q>(b, q);
             if (a.packed) {  // level words stored as produced: [n, M]
                 if (word_bytes(q) == 2)

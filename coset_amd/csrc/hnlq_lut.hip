@@ -120,9 +120,7 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_lut_kernel(CodecArgs a, cons
             int b[8];
             uint32_t word;
             if (MODE != MODE_DECODE) {
-                float y[8];
-                project_encode(xl, y, a.fast_projection);
-                lattice_digits<Q>(y, Q, b);
+                encode_level<Q>(xl, a.fast_projection, Q, b);
                 word = pack_word<Q>(b, Q);
                 pack |= (uint64_t)word << (16 * m);
                 if (a.codes_f32) {
@@ -216,24 +214,18 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_lut_kernel(CodecArgs a, cons
 // Same contract for the common case, with everything the general kernel
 // decides per block fixed at compile time: fp32 input and output, no scale
 // or a codec beta = 2^k (x / beta == x * 2^-k exactly; SCALED false when
-// beta = 1), no dither, no float code tensor, byte-table decode.  The loop is
-// unrolled twice so the next block's input loads into the other register set
+// beta = 1), no dither, byte-table decode; the float code tensor is an
+// optional output (CODES).  The loop is unrolled twice so the next block's input loads into the other register set
 // while the current block is processed.
 template <int Q>
 __device__ __forceinline__ uint32_t encode_level_word(const float xl[8], int fast)
 {
-    float y[8];
     int b[8];
-    if (fast && project_fast(xl, y)) {
-        lattice_digits<Q>(y, Q, b);
-    } else {
-        project<false, false>(xl, y);
-        lattice_digits_2y<Q>(y, b);
-    }
+    encode_level<Q>(xl, fast, Q, b);
     return pack_word<Q>(b, Q);
 }
 
-template <int Q, int M, int MODE, bool SCALED>
+template <int Q, int M, int MODE, bool SCALED, bool CODES>
 __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, const uint16_t* __restrict__ g_map,
                                                               const uint64_t* __restrict__ g_tab, int n_coarse,
                                                               int swar_bias)
@@ -283,6 +275,13 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
             if (MODE != MODE_DECODE) {
                 word = encode_level_word<Q>(xl, fast);
                 pack |= (uint64_t)word << (16 * m);
+                if (CODES) {  // the reference's float code tensor [n, M, 8]
+                    int b[8];
+                    unpack_word<Q>(word, Q, b);
+                    float4* cp = reinterpret_cast<float4*>(a.codes_f32 + ((size_t)i * M + m) * 8);
+                    cp[0] = make_float4((float)b[0], (float)b[1], (float)b[2], (float)b[3]);
+                    cp[1] = make_float4((float)b[4], (float)b[5], (float)b[6], (float)b[7]);
+                }
                 if (m + 1 < M) {
 #pragma unroll
                     for (int j = 0; j < 8; ++j) xl[j] = __fmul_rn(xl[j], 1.0f / (float)Q);  // exact: Q = 2^k
@@ -368,12 +367,15 @@ hipError_t launch_plain(const CodecArgs& a, int grid, const uint16_t* map, const
 {
     if constexpr (MODE == MODE_ENCODE || Q == 2 || M <= 2) {
         const bool scaled = a.scale_mode == SCALE_CODEC && a.beta != 1.f;
-        if (scaled)
-            hipLaunchKernelGGL((hnlq_plain_kernel<Q, M, MODE, true>), dim3(grid), dim3(kLutThreads), 0, s, a, map,
-                               sw, nc, bias);
-        else
-            hipLaunchKernelGGL((hnlq_plain_kernel<Q, M, MODE, false>), dim3(grid), dim3(kLutThreads), 0, s, a, map,
-                               sw, nc, bias);
+        const bool codes = MODE != MODE_DECODE && a.codes_f32;
+#define COSET_PLAIN(SC, CO) \
+    hipLaunchKernelGGL((hnlq_plain_kernel<Q, M, MODE, SC, CO>), dim3(grid), dim3(kLutThreads), 0, s, a, map, sw, nc, bias)
+        if (scaled) {
+            if (codes) COSET_PLAIN(true, true); else COSET_PLAIN(true, false);
+        } else {
+            if (codes) COSET_PLAIN(false, true); else COSET_PLAIN(false, false);
+        }
+#undef COSET_PLAIN
         return hipGetLastError();
     }
     return hipErrorInvalidValue;
@@ -390,10 +392,10 @@ hipError_t launch_q(const CodecArgs& a, const DecodeTables* t, hipStream_t s)
     const uint64_t* tab = t ? (swar ? t->swar : t->coarse) : nullptr;
     const int bias = swar ? t->swar_bias[a.M] : 0;
     // the plain kernel: fp32 in and out, no scale or a codec beta = 2^k, no
-    // dither, no float codes, no step counter, byte tables for the decode
-    const bool plain = (MODE == MODE_DECODE || a.x_dtype == DT_F32) && a.out_dtype == DT_F32 &&
+    // dither, no step counter, byte tables for the decode
+    const bool plain = (MODE == MODE_DECODE || a.x_dtype == DT_F32) && (MODE == MODE_ENCODE || a.out_dtype == DT_F32) &&
                        (a.scale_mode == SCALE_NONE || (a.scale_mode == SCALE_CODEC && a.beta_is_pow2)) &&
-                       !a.dither && !a.codes_f32 && !a.step_counter && (MODE == MODE_ENCODE || swar) &&
+                       !a.dither && !a.step_counter && (MODE == MODE_ENCODE || swar) &&
                        g_codec_plain;
     if (plain) {
         const uint64_t* sw = t ? t->swar : nullptr;

@@ -259,3 +259,23 @@ def test_fast_projection_same_codes(ca, path, q, M):
     np.testing.assert_array_equal(outs[0], outs[1])
     ref = O.pack_words(O.e8_encode(x, q, M), q)
     np.testing.assert_array_equal(outs[0], ref)
+
+
+@pytest.mark.parametrize("beta", [1.0, 0.25, 0.3])
+def test_roundtrip_with_float_codes(ca, path, beta):
+    """One round trip writing packed words, the reference's float code
+    tensor and the decoded blocks together (every kernel variant)."""
+    from coset_amd import _lib
+    rng = np.random.default_rng(int(beta * 100))
+    x = np.concatenate([rng.standard_normal((70000, 8)), _adversarial_blocks(rng, 2000)]).astype(np.float32)
+    n = x.shape[0]
+    xd = dev(x)
+    packed = torch.empty((n, 2), dtype=torch.uint16, device="cuda")
+    codes = torch.empty((n, 2, 8), dtype=torch.float32, device="cuda")
+    out = torch.empty((n, 8), dtype=torch.float32, device="cuda")
+    _lib.call("coset_e8_hnlq_roundtrip", _lib.ptr(xd), _lib.F32, n, _lib.SCALE_CODEC, beta, None, 0, 0.0,
+              None, 0, 4, 2, 1, _lib.ptr(packed), _lib.ptr(codes), _lib.ptr(out), _lib.F32, _lib.stream_of(xd))
+    ref = O.e8_encode(x, 4, 2, beta)
+    np.testing.assert_array_equal(host(codes).astype(np.int32), ref)
+    np.testing.assert_array_equal(words(packed), O.pack_words(ref, 4))
+    np.testing.assert_array_equal(host(out), O.e8_decode(ref, 4, 2, beta))
