@@ -45,6 +45,7 @@ from .vlut import (
 )
 
 from . import legacy  # coset.legacy.quant.functional: encode / decode / quantize with the overload loop
+from .packed import PackedLinear, load_packed, packed_state, save_packed
 
 __version__ = "0.1.0"
 
@@ -56,5 +57,5 @@ __all__ = [
     "E8WeightQuant", "E8ThetaWeightQuant", "create_e8_hnlq_linear", "get_generators", "ste_quantize",
     "vLUTManager", "QuantizationConfig", "build_vlut", "_encoding_to_index", "vlut_mac_operation",
     "vlut_accumulate_operation", "build_one_sided_vluts", "vlut_dot", "vlut_matmul", "vlut_prepare", "PreparedWords",
-    "legacy",
+    "legacy", "PackedLinear", "load_packed", "packed_state", "save_packed",
 ]

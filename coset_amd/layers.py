@@ -144,6 +144,25 @@ class E8WeightQuant(torch.autograd.Function):
         return dW, dbeta.view(beta_shape), None, None, None, None, None
 
 
+def qat_fwd_theta(Wc, theta, sigma, xmax, step_count, bounds, q, M, clip, blocks_per_tile, out_dtype):
+    """One coset_e8_qat_fwd_theta call: (W_q [rows, cols] in out_dtype,
+    level words [rows * cols / 8, M], beta [tiles], d beta / d theta [tiles])."""
+    th = theta.contiguous()
+    rows, cols = Wc.shape
+    dev = Wc.device
+    Wq = torch.empty((rows, cols), dtype=out_dtype, device=dev)
+    packed = torch.empty((rows * (cols // 8), M), dtype=word_dtype(q), device=dev)
+    beta = torch.empty(th.numel(), dtype=torch.float32, device=dev)
+    dbdt = torch.empty_like(beta)
+    delta0, eta, ginv, m_bounds = bounds
+    _lib.check("coset_e8_qat_fwd_theta", _lib.fn("coset_e8_qat_fwd_theta")(
+        Wc.data_ptr(), rows, cols, blocks_per_tile, th.data_ptr(), sigma.contiguous().data_ptr(),
+        xmax.contiguous().data_ptr(), delta0, eta, ginv, m_bounds, clip, q, M, Wq.data_ptr(),
+        _lib.dtype_code(out_dtype), packed.data_ptr(), beta.data_ptr(), dbdt.data_ptr(),
+        _lib.ptr(step_count), _lib.stream_of(Wc)))
+    return Wq, packed, beta, dbdt
+
+
 class E8ThetaWeightQuant(torch.autograd.Function):
     """The fused QAT weight path: beta from theta and the EMA buffers, scale,
     quantize (M = 2), unscale, clamp and the step counter in one kernel
@@ -155,19 +174,8 @@ class E8ThetaWeightQuant(torch.autograd.Function):
     @staticmethod
     def forward(ctx, W, theta, sigma, xmax, step_count, bounds, q, M, clip, blocks_per_tile, out_dtype):
         Wc = W.detach().contiguous()
-        th = theta.detach().contiguous()
-        rows, cols = Wc.shape
-        dev = Wc.device
-        Wq = torch.empty((rows, cols), dtype=out_dtype, device=dev)
-        packed = torch.empty((rows * (cols // 8), M), dtype=word_dtype(q), device=dev)
-        beta = torch.empty(th.numel(), dtype=torch.float32, device=dev)
-        dbdt = torch.empty_like(beta)
-        delta0, eta, ginv, m_bounds = bounds
-        _lib.check("coset_e8_qat_fwd_theta", _lib.fn("coset_e8_qat_fwd_theta")(
-            Wc.data_ptr(), rows, cols, blocks_per_tile, th.data_ptr(), sigma.contiguous().data_ptr(),
-            xmax.contiguous().data_ptr(), delta0, eta, ginv, m_bounds, clip, q, M, Wq.data_ptr(),
-            _lib.dtype_code(out_dtype), packed.data_ptr(), beta.data_ptr(), dbdt.data_ptr(),
-            step_count.data_ptr(), _lib.stream_of(Wc)))
+        Wq, packed, beta, dbdt = qat_fwd_theta(Wc, theta.detach(), sigma, xmax, step_count, bounds, q, M, clip,
+                                               blocks_per_tile, out_dtype)
         ctx.save_for_backward(Wc, packed, beta, dbdt)
         ctx.cfg = (q, M, clip, blocks_per_tile, theta.shape)
         return Wq
@@ -499,11 +507,15 @@ class HNLQLinearQAT(nn.Module):
             if self.quantize_activations and self.actq is not None:
                 metadata.update({"act_bit_width": self.actq.bit_width, "act_alpha": self.actq.alpha.item()})
             out = {"weight": W_q, "bias": self.bias, "metadata": metadata}
-            if self._fused():
-                beta = self._beta().detach()
-                from .codecs import hnlq_encode
+            if self._fused() and self.quantization_enabled:
+                # the same quantization again, without advancing the step:
+                # its level words and beta reproduce W_q bit for bit
                 bpt = self.blocks_per_row if self.tiling == "row" else 1
-                out["codes"] = hnlq_encode(self.weight.detach(), self.q, 2, beta_row=beta, blocks_per_row=bpt)
+                _, packed, beta, _ = qat_fwd_theta(
+                    self.weight.detach().contiguous(), self.theta_beta.detach(), self.sigma_ema, self.xmax_ema,
+                    None, (float(self.Delta0), float(self.eta), self._ginv_f, int(self.M)), int(self.q), 2,
+                    float(self.weight_clip_value), int(bpt), torch.float32)
+                out["codes"] = packed.view(self.out_features, self.blocks_per_row, 2)
                 out["beta"] = beta
             return out
 

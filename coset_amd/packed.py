@@ -1,0 +1,108 @@
+"""Persistent packed-code format for QAT -> inference hand-off.
+
+The reference exports only the dequantized fp32 weight (export_quantized,
+coset/core/layers.py:620-650).  Here a trained HNLQLinearQAT (row tiling,
+the fused E8 path) is stored as what it really is: its level words
+idx(b) = sum_j b_j q^(7-j) (the reference vLUT index, coset/legacy/quant/
+vlut.py:217-238), [out, in/8, M] uint16, and its per-row beta, in a
+safetensors file that executes nothing when loaded.  ``PackedLinear`` serves
+such a file with the vLUT matmul: y = x @ (decode(words) / beta)^T + bias,
+which equals the layer's F.linear(x, W_q, bias) wherever no weight was
+clipped at +-weight_clip_value (the count of clipped weights is recorded).
+"""
+from __future__ import annotations
+
+import json
+from typing import Dict, Optional
+
+import torch
+from torch import nn
+
+from .codecs import hnlq_decode
+from .lattice import on_gpu
+from .vlut import vlut_matmul, vlut_prepare
+
+FORMAT = "coset_amd.hnlq_packed.v1"
+
+
+def packed_state(layer) -> Dict[str, object]:
+    """The packed form of a layer's current quantization: tensors (words,
+    beta, bias) and metadata.  Uses export_quantized (which, like the
+    reference's, advances the layer's step counter once)."""
+    if getattr(layer, "tiling", "row") != "row":
+        raise ValueError("the packed format stores per-row beta (tiling='row')")
+    ex = layer.export_quantized()
+    if "codes" not in ex:
+        raise ValueError("packed export needs the fused E8 path with quantization enabled")
+    words, beta = ex["codes"], ex["beta"]
+    q, M = int(layer.q), int(words.shape[-1])
+    dec = hnlq_decode(words.reshape(-1, M), q, M, None).reshape(layer.out_features, layer.in_features)
+    unclipped = (dec / beta.view(-1, 1))
+    clipped = int((unclipped.abs() > float(layer.weight_clip_value)).sum())
+    tensors = {"words": words.contiguous(), "beta": beta.contiguous()}
+    if layer.bias is not None:
+        tensors["bias"] = layer.bias.detach().float().contiguous()
+    meta = {"format": FORMAT, "lattice": "E8", "rule": "core", "q": q, "M": M,
+            "in_features": int(layer.in_features), "out_features": int(layer.out_features),
+            "weight_clip_value": float(layer.weight_clip_value), "clipped_weights": clipped,
+            "scale": "divide: W = decode(words) / beta[row]"}
+    return {"tensors": tensors, "metadata": meta}
+
+
+def save_packed(layer_or_state, path: str) -> Dict[str, object]:
+    """Write a layer (or a packed_state) to a safetensors file; returns the state."""
+    from safetensors.torch import save_file
+    st = layer_or_state if isinstance(layer_or_state, dict) else packed_state(layer_or_state)
+    save_file({k: v.detach().cpu().contiguous() for k, v in st["tensors"].items()}, path,
+              metadata={"coset_amd": json.dumps(st["metadata"])})
+    return st
+
+
+def load_packed(path: str, device: Optional[torch.device] = None) -> "PackedLinear":
+    """Read a file written by save_packed (safetensors: tensors and a JSON
+    metadata string, nothing executed) into a PackedLinear on the GPU."""
+    from safetensors import safe_open
+    tensors = {}
+    with safe_open(path, framework="pt") as f:
+        meta = json.loads(f.metadata()["coset_amd"])
+        for k in f.keys():
+            tensors[k] = f.get_tensor(k)
+    if meta.get("format") != FORMAT:
+        raise ValueError(f"{path}: not a {FORMAT} file")
+    return PackedLinear(tensors, meta, device=device)
+
+
+class PackedLinear(nn.Module):
+    """y = x @ (decode(words) / beta)^T + bias through the vLUT matmul, with
+    the words prepared once (tiled fragment order).  x: [..., in] fp16 or
+    bf16 (fp32 is cast to bf16: 2 x_hat is exact in both) -> fp32."""
+
+    def __init__(self, tensors: Dict[str, torch.Tensor], meta: Dict[str, object],
+                 device: Optional[torch.device] = None):
+        super().__init__()
+        self.meta = dict(meta)
+        self.q, self.M = int(meta["q"]), int(meta["M"])
+        self.in_features, self.out_features = int(meta["in_features"]), int(meta["out_features"])
+        words = on_gpu(tensors["words"]) if device is None else tensors["words"].to(device)
+        if words.shape != (self.out_features, self.in_features // 8, self.M):
+            raise ValueError(f"words shape {tuple(words.shape)} does not match the metadata")
+        self.words = words
+        self.prepared = vlut_prepare(words, self.q, legacy=False, layout="tiled")
+        self.register_buffer("beta", tensors["beta"].to(words.device).float())
+        bias = tensors.get("bias")
+        self.register_buffer("bias", None if bias is None else bias.to(words.device).float())
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        lead = x.shape[:-1]
+        a = x.reshape(-1, self.in_features)
+        if a.dtype not in (torch.float16, torch.bfloat16):
+            a = a.to(torch.bfloat16)
+        y = vlut_matmul(self.prepared, a, scale=self.beta, scale_mode="div")
+        if self.bias is not None:
+            y = y + self.bias
+        return y.reshape(*lead, self.out_features)
+
+    def dequantized_weight(self) -> torch.Tensor:
+        """decode(words) / beta, [out, in] fp32 (no clamp)."""
+        dec = hnlq_decode(self.words.reshape(-1, self.M), self.q, self.M, None)
+        return dec.reshape(self.out_features, self.in_features) / self.beta.view(-1, 1)

@@ -162,7 +162,7 @@ def test_state_dict_roundtrip():
     torch.testing.assert_close(a(x), b(x))
     assert int(b.step_count) == 2
     ex = b.export_quantized()
-    assert ex["codes"].shape == (32, 2) and ex["weight"].shape == (8, 32)
+    assert ex["codes"].shape == (8, 4, 2) and ex["weight"].shape == (8, 32) and ex["beta"].shape == (8,)
 
 
 @pytest.mark.parametrize("tiling", ["row", "block"])
