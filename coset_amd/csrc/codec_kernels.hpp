@@ -86,24 +86,45 @@ struct CodecArgs {
     int fast_projection;     // encoders try project_fast first (set by the launcher)
 };
 
-// One encoder level (core rule, contiguous distances): the projection --
-// the fast path where its conditions hold, the reference sequence for the
-// lanes where they fail -- and the digits of the chosen point.  The branches
-// meet at the digits, and the fast branch (|y| < 2^21 + 1) takes the shorter
-// digit form.
+// One encoder level (core rule, contiguous distances): the projection's
+// fast path where its conditions hold, straight to the rows of G^-1 y, and
+// the reference sequence for the lanes where they fail.  Digits are the rows
+// mod q either way.  in_range is max |x_i| < 2^21 (fast_in_range).
 template <int Q>
-__device__ __forceinline__ void encode_level(const float x[8], int fast, int q, int b[8])
+__device__ __forceinline__ void encode_level(const float x[8], int fast, int q, int b[8], bool in_range)
 {
-    float y[8];
-    if (fast && project_fast(x, y)) {
-        if constexpr (Q > 0 && (Q & (Q - 1)) == 0)
-            lattice_digits_small<Q>(y, b);
-        else
-            lattice_digits<Q>(y, q, b);
+    int c[8];
+    bool ok = false;
+    if (fast) {
+        ok = fast_rows(x, c, in_range);
+        // the rows stay computed here, ahead of the fallback branch: sunk past
+        // it they would keep the argmax lane masks live across the fallback's
+        // code
+#pragma unroll
+        for (int i = 0; i < 8; ++i) __asm__ volatile("" : "+v"(c[i]));
+    }
+    if (ok) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            if (Q > 0 && (Q & (Q - 1)) == 0) {
+                b[i] = c[i] & (Q - 1);  // two's complement & == Python-style mod
+            } else {
+                const int qq = Q > 0 ? Q : q;
+                const int m = c[i] % qq;
+                b[i] = m < 0 ? m + qq : m;
+            }
+        }
     } else {
+        float y[8];
         project<false, false>(x, y);
         lattice_digits<Q>(y, q, b);
     }
+}
+
+template <int Q>
+__device__ __forceinline__ void encode_level(const float x[8], int fast, int q, int b[8])
+{
+    encode_level<Q>(x, fast, q, b, fast && fast_in_range(x));
 }
 
 // Per-block scale of SCALE_LAYER (reads beta_row or derives it from theta).

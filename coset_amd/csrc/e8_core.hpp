@@ -176,30 +176,6 @@ __device__ __forceinline__ void lattice_digits(const float y[8], int q, int b[8]
     }
 }
 
-// The same digits for |y| < 2^22 and q = 2^k, through z_j = y_j - y_7: y in
-// E8 has all coordinates integral or all half-integral, so every z_j is an
-// integer, exact in fp32 at these magnitudes, and
-//   (G^-1 y)_r = z_r + .. + z_6 (r >= 1),  (G^-1 y)_0 = (z_0 + .. + z_6) / 2.
-// Fewer operations than lattice_digits; the encoders use it where the fast
-// projection (|x| < 2^21) produced y.
-template <int Q>
-__device__ __forceinline__ void lattice_digits_small(const float y[8], int b[8])
-{
-    static_assert(Q > 0 && (Q & (Q - 1)) == 0, "power-of-two q");
-    int c[8];
-    int suf = 0;  // z_r + .. + z_6
-#pragma unroll
-    for (int r = 6; r >= 1; --r) {
-        suf += (int)__fsub_rn(y[r], y[7]);
-        c[r] = suf;
-    }
-    suf += (int)__fsub_rn(y[0], y[7]);
-    c[0] = suf >> 1;
-    c[7] = (int)__fmul_rn(2.f, y[7]);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) b[i] = c[i] & (Q - 1);
-}
-
 // decode_coords: y = G b (exact).
 __device__ __forceinline__ void lattice_point(const int b[8], float y[8])
 {

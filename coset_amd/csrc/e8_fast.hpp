@@ -17,19 +17,24 @@
 //       integer nearest to t = fl(x_i - 1/2), so custom_round(t) = rint(t) =
 //       floor(x_i): the D8 + 1/2 candidate rounds to f1 = floor(x), and
 //       d1 = t - f1 is again exact.
-//   (4) The two squared distances, evaluated as sum d^2 (+ 1 - 2 adj d_k for
-//       the flipped coordinate) with fused multiply-adds, differ by more than
-//       2^-14.  For the D8 + 1/2 candidate the terms use |x - f1 - 1/2| =
-//       1/2 - |d0| (equal as reals under (2)).  Both evaluations and the
-//       reference's rounded sums of rounded squares stay within 140 ulp(1)
-//       of the exact sums (all terms are below 5), and a gap of 2^-14 also
-//       keeps the correctly rounded square roots apart, so the reference's
-//       strict comparison has the same outcome.
+//   (4) The two squared distances differ by more than 2^-14, evaluated as
+//       a = sum d0^2 and b = 2 - sum |d0| + sum d0^2 (+ 1 - 2 adj d_k for the
+//       flipped coordinate).  b is sum (1/2 - |d0|)^2, and 1/2 - |d0_i| =
+//       |x_i - f1_i - 1/2| as reals under (2).  These evaluations (within
+//       13 ulp(1) before the flip term) and the reference's rounded sums of
+//       rounded squares stay within 140 ulp(1) of the exact sums (all terms
+//       are below 5), and a gap of 2^-14 also keeps the correctly rounded
+//       square roots apart, so the reference's strict comparison has the
+//       same outcome.
+// Under (2) and (3) floor x_i = rint x_i - [d0_i < 0] (d0_i = 0 fails (3)),
+// so the parity of sum floor x is that of sum rint x plus the number of
+// negative d0_i.
 // NaN or infinite inputs fail (1) or (4).
 #pragma once
 
 #include <hip/hip_runtime.h>
 #include <math.h>
+#include <stdint.h>
 
 namespace coset {
 
@@ -37,44 +42,91 @@ constexpr float kFastMaxAbs = 2097152.0f;              // 2^21
 constexpr float kFastTieLimit = 0.5f - 9.5367431640625e-07f;  // 1/2 - 2^-20
 constexpr float kFastDistGap = 6.103515625e-05f;        // 2^-14
 
-// Core-rule E8 closest point of x (contiguous distance rule).  Returns false
-// when a condition above fails; y is then unspecified.
-__host__ __device__ inline bool project_fast(const float x[8], float y[8])
+// Lane conditions as masks.  On the device a mask is the wave's 64-bit
+// ballot: the first-index scan and the choice between the two candidates'
+// masks are then scalar operations, and a mask is read back per lane for
+// free (a per-lane select of two booleans costs five vector operations
+// there).  On the host a mask is all ones or zero, with the same algebra.
+typedef uint64_t lanes_t;
+
+__host__ __device__ inline lanes_t lanes_of(bool c)
 {
-    float f0[8], d0[8], f1[8], d1[8];
-    float m = 0.f, best0 = 0.f, best1 = 0.f, s0 = 0.f, s1 = 0.f, a = 0.f, b = 0.f;
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __builtin_amdgcn_ballot_w64(c);
+#else
+    return c ? ~0ull : 0ull;
+#endif
+}
+
+__host__ __device__ inline bool lane_in(lanes_t m)
+{
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __builtin_amdgcn_inverse_ballot_w64(m);
+#else
+    return m != 0ull;
+#endif
+}
+
+// The decision of the fast path: both candidates' integer parts, the first
+// index of each one's worst coordinate, each one's parity adjustment and
+// which candidate is closer.  Returns false when a condition above fails.
+struct FastChoice {
+    float f0[8];        // rint(x): the D8 candidate before its adjustment
+    float f1[8];        // floor(x): the D8 + 1/2 candidate is f1 + 1/2
+    lanes_t first0[8];  // worst coordinate of each candidate (first index)
+    lanes_t first1[8];
+    float adj0, adj1;   // -1, 0 or +1 added at that coordinate
+    lanes_t pick0;      // the D8 candidate is the closer one
+};
+
+// Condition (1).  Callers that know a bound on |x| pass it to fast_choose.
+__host__ __device__ inline bool fast_in_range(const float x[8])
+{
+    float m = fabsf(x[0]);
+#pragma unroll
+    for (int i = 1; i < 8; ++i) m = fmaxf(m, fabsf(x[i]));
+    return m < kFastMaxAbs;
+}
+
+__host__ __device__ inline bool fast_choose(const float x[8], FastChoice& c, bool in_range)
+{
+    float d0[8], d1[8];
+    float best0 = 0.f, best1 = 0.f, s0, sa, a;
+    uint32_t neg = 0u;  // sign bits of d0, xor-ed
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        f0[i] = rintf(x[i]);
-        d0[i] = x[i] - f0[i];
-        f1[i] = floorf(x[i]);
-        d1[i] = (x[i] - 0.5f) - f1[i];
-        m = fmaxf(m, fabsf(x[i]));
+        c.f0[i] = rintf(x[i]);
+        d0[i] = x[i] - c.f0[i];
+        c.f1[i] = floorf(x[i]);
+        d1[i] = (x[i] - 0.5f) - c.f1[i];
         best0 = fmaxf(best0, fabsf(d0[i]));
         best1 = fmaxf(best1, fabsf(d1[i]));
-        s0 += f0[i];
-        s1 += f1[i];
-        a = fmaf(d0[i], d0[i], a);
-        // x - floor(x) - 1/2 = d0 - 1/2 (d0 > 0) or d0 + 1/2 (d0 < 0) under
-        // (2): its magnitude is 1/2 - |d0|, exact up to one rounding
-        const float e = 0.5f - fabsf(d0[i]);
-        b = fmaf(e, e, b);
+        neg ^= __builtin_bit_cast(uint32_t, d0[i]);
+        if (i == 0) {
+            s0 = c.f0[0];
+            sa = fabsf(d0[0]);
+            a = d0[0] * d0[0];
+        } else {
+            s0 += c.f0[i];
+            sa += fabsf(d0[i]);
+            a = fmaf(d0[i], d0[i], a);
+        }
     }
-    bool ok = m < kFastMaxAbs && best0 < kFastTieLimit && best1 < kFastTieLimit;
+    bool ok = in_range && best0 < kFastTieLimit && best1 < kFastTieLimit;
+    float b = (2.f - sa) + a;
 
-    // first index of the largest |d| (torch.argmax): scan from the back
-    bool first0[8], first1[8];
+    // first index of the largest |d| (torch.argmax)
     float xk0 = x[0], xk1 = x[0];
-    bool seen0 = false, seen1 = false;
+    lanes_t seen0 = 0ull, seen1 = 0ull;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        bool h0 = fabsf(d0[i]) == best0, h1 = fabsf(d1[i]) == best1;
-        first0[i] = h0 && !seen0;
-        first1[i] = h1 && !seen1;
-        seen0 = seen0 || h0;
-        seen1 = seen1 || h1;
-        xk0 = first0[i] ? x[i] : xk0;
-        xk1 = first1[i] ? x[i] : xk1;
+        const lanes_t h0 = lanes_of(fabsf(d0[i]) == best0), h1 = lanes_of(fabsf(d1[i]) == best1);
+        c.first0[i] = h0 & ~seen0;
+        c.first1[i] = h1 & ~seen1;
+        seen0 |= h0;
+        seen1 |= h1;
+        xk0 = lane_in(c.first0[i]) ? x[i] : xk0;
+        xk1 = lane_in(c.first1[i]) ? x[i] : xk1;
     }
     // the worst coordinates' differences, recomputed from x_k
     const float dk0 = xk0 - rintf(xk0);
@@ -84,24 +136,70 @@ __host__ __device__ inline bool project_fast(const float x[8], float y[8])
     const float ek1 = (xk1 - fk1) - 0.5f;  // within 2^-25 of x_k - (f_k + 1/2)
     // core g_x: an odd coordinate sum moves the worst coordinate by +1 when
     // t_k >= 0 and f_k < t_k (d_k > 0), by -1 otherwise
-    const bool odd0 = ((int)s0 & 1) != 0, odd1 = ((int)s1 & 1) != 0;
-    const float adj0 = odd0 ? ((xk0 >= 0.f && dk0 > 0.f) ? 1.f : -1.f) : 0.f;
-    const float adj1 = odd1 ? ((tk1 >= 0.f && dk1 > 0.f) ? 1.f : -1.f) : 0.f;
+    const bool odd0 = ((int)s0 & 1) != 0, odd1 = odd0 != ((neg >> 31) != 0u);
+    c.adj0 = odd0 ? ((xk0 >= 0.f && dk0 > 0.f) ? 1.f : -1.f) : 0.f;
+    c.adj1 = odd1 ? ((tk1 >= 0.f && dk1 > 0.f) ? 1.f : -1.f) : 0.f;
 
     // (d - adj)^2 = d^2 - 2 adj d + adj^2, adj^2 = |adj|
-    a += fmaf(-2.f * adj0, dk0, fabsf(adj0));
-    b += fmaf(-2.f * adj1, ek1, fabsf(adj1));
+    a += fmaf(-2.f * c.adj0, dk0, fabsf(c.adj0));
+    b += fmaf(-2.f * c.adj1, ek1, fabsf(c.adj1));
     const bool pick0 = b - a > kFastDistGap;
-    ok = ok && (pick0 || a - b > kFastDistGap);
+    c.pick0 = lanes_of(pick0);
+    return ok && (pick0 || a - b > kFastDistGap);
+}
 
-    const float adj = pick0 ? adj0 : adj1;
+// The chosen candidate's worst coordinate, as a lane mask.
+__host__ __device__ inline lanes_t fast_at(const FastChoice& c, int i)
+{
+    return (c.pick0 & c.first0[i]) | (~c.pick0 & c.first1[i]);
+}
+
+// Core-rule E8 closest point of x (contiguous distance rule).  Returns false
+// when a condition above fails; y is then unspecified.
+__host__ __device__ inline bool project_fast(const float x[8], float y[8])
+{
+    FastChoice c;
+    const bool ok = fast_choose(x, c, fast_in_range(x));
+    const bool pick0 = lane_in(c.pick0);
+    const float adj = pick0 ? c.adj0 : c.adj1;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const bool at_k = pick0 ? first0[i] : first1[i];
-        const float base = pick0 ? f0[i] : f1[i] + 0.5f;
+        const float base = pick0 ? c.f0[i] : c.f1[i] + 0.5f;
         // adding the (possibly zero) adjustment also turns rint's -0 into +0
-        y[i] = base + (at_k ? adj : 0.f);
+        y[i] = base + (lane_in(fast_at(c, i)) ? adj : 0.f);
     }
+    return ok;
+}
+
+// The rows of G^-1 y (coset/core/base.py:134-155) for the point project_fast
+// chooses, without forming y.  With Y the chosen candidate's integer part
+// after the adjustment (y = Y, or Y + 1/2 on the D8 + 1/2 coset):
+//   (G^-1 y)_r = sum_{j = r..6} (Y_j - Y_7)        r = 1..6
+//   (G^-1 y)_0 = sum_{j = 0..6} (Y_j - Y_7) / 2    (an even sum for y in E8)
+//   (G^-1 y)_7 = 2 Y_7 (+ 1 on the coset)
+// all exact in int32 under condition (1).  The adjustment enters the sums
+// through the single term j = k.  Returns false exactly when project_fast
+// does (in_range = fast_in_range(x)); rows are then unspecified.
+__host__ __device__ inline bool fast_rows(const float x[8], int rows[8], bool in_range)
+{
+    FastChoice c;
+    const bool ok = fast_choose(x, c, in_range);
+    const bool pick0 = lane_in(c.pick0);
+    const uint32_t adj = (uint32_t)(int)(pick0 ? c.adj0 : c.adj1);
+    uint32_t Y[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) Y[i] = (uint32_t)(int)(pick0 ? c.f0[i] : c.f1[i]);
+    const uint32_t y7 = Y[7] + (lane_in(fast_at(c, 7)) ? adj : 0u);
+    const uint32_t n7 = 0u - y7, n7a = n7 + adj;  // -Y_7, and -Y_7 + adj for j = k
+    uint32_t w = 0u;                               // wrapping sums: no signed overflow on failed lanes
+#pragma unroll
+    for (int r = 6; r >= 1; --r) {
+        w += Y[r] + (lane_in(fast_at(c, r)) ? n7a : n7);
+        rows[r] = (int)w;
+    }
+    w += Y[0] + (lane_in(fast_at(c, 0)) ? n7a : n7);
+    rows[0] = (int)w >> 1;
+    rows[7] = (int)(2u * y7 + (pick0 ? 0u : 1u));
     return ok;
 }
 

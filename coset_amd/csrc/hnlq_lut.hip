@@ -214,14 +214,32 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_lut_kernel(CodecArgs a, cons
 // Same contract for the common case, with everything the general kernel
 // decides per block fixed at compile time: fp32 input and output, no scale
 // or a codec beta = 2^k (x / beta == x * 2^-k exactly; SCALED false when
-// beta = 1), no dither, byte-table decode; the float code tensor is an
-// optional output (CODES).  The loop is unrolled twice so the next block's input loads into the other register set
-// while the current block is processed.
+// beta = 1), no dither, byte-table decode, the encoder's fast projection
+// on; the float code tensor is an optional output (CODES).  The loop is
+// unrolled twice so the next block's input loads into the other register
+// set while the current block is processed.
+// One encoder level straight to its word idx(b).  On the fast path each
+// digit (the low bits of a row) is funnelled into the top of an accumulator
+// as the accumulator shifts right, one v_alignbit per digit.
 template <int Q>
-__device__ __forceinline__ uint32_t encode_level_word(const float xl[8], int fast)
+__device__ __forceinline__ uint32_t encode_level_word(const float xl[8], bool in_range)
 {
+    static_assert(Q == 2 || Q == 4, "byte-table formats");
+    constexpr int L = Q == 2 ? 1 : 2;
+    int c[8];
+    const bool ok = fast_rows(xl, c, in_range);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) __asm__ volatile("" : "+v"(c[i]));  // rows computed ahead of the fallback
+    if (ok) {
+        uint32_t acc = 0u;
+#pragma unroll
+        for (int j = 7; j >= 0; --j) acc = __builtin_amdgcn_alignbit((uint32_t)c[j], acc, L);
+        return acc >> (32 - 8 * L);  // digit 0 highest: sum_j b_j Q^(7-j)
+    }
+    float y[8];
     int b[8];
-    encode_level<Q>(xl, fast, Q, b);
+    project<false, false>(xl, y);
+    lattice_digits<Q>(y, Q, b);
     return pack_word<Q>(b, Q);
 }
 
@@ -243,7 +261,6 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
     const float half_bias = 0.5f * (float)swar_bias;
     const float4* xs = reinterpret_cast<const float4*>(a.x);
     const int64_t n = a.n;
-    const int fast = a.fast_projection;
 
     struct In {
         float4 u, v;
@@ -268,12 +285,22 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
 #pragma unroll
             for (int j = 0; j < 8; ++j) xl[j] = __fmul_rn(xl[j], a.beta_inv);
         }
+        // level m's input is xl * Q^-m exactly, so max |x_m| < 2^21 is
+        // max |x_0| < 2^21 Q^m
+        float amax = 0.f;
+        if (MODE != MODE_DECODE) {
+            amax = fabsf(xl[0]);
+#pragma unroll
+            for (int j = 1; j < 8; ++j) amax = fmaxf(amax, fabsf(xl[j]));
+        }
         uint32_t sw0 = 0u, sw1 = 0u;
+        float lim = kFastMaxAbs;
 #pragma unroll
         for (int m = 0; m < M; ++m) {
             uint32_t word;
             if (MODE != MODE_DECODE) {
-                word = encode_level_word<Q>(xl, fast);
+                word = encode_level_word<Q>(xl, amax < lim);
+                lim *= (float)Q;
                 pack |= (uint64_t)word << (16 * m);
                 if (CODES) {  // the reference's float code tensor [n, M, 8]
                     int b[8];
@@ -392,8 +419,10 @@ hipError_t launch_q(const CodecArgs& a, const DecodeTables* t, hipStream_t s)
     const uint64_t* tab = t ? (swar ? t->swar : t->coarse) : nullptr;
     const int bias = swar ? t->swar_bias[a.M] : 0;
     // the plain kernel: fp32 in and out, no scale or a codec beta = 2^k, no
-    // dither, no step counter, byte tables for the decode
-    const bool plain = (MODE == MODE_DECODE || a.x_dtype == DT_F32) && (MODE == MODE_ENCODE || a.out_dtype == DT_F32) &&
+    // dither, no step counter, byte tables for the decode, and the encoder's
+    // fast projection on (it is a compile-time constant there)
+    const bool plain = (MODE == MODE_DECODE || (a.x_dtype == DT_F32 && a.fast_projection)) &&
+                       (MODE == MODE_ENCODE || a.out_dtype == DT_F32) &&
                        (a.scale_mode == SCALE_NONE || (a.scale_mode == SCALE_CODEC && a.beta_is_pow2)) &&
                        !a.dither && !a.step_counter && (MODE == MODE_ENCODE || swar) &&
                        g_codec_plain;

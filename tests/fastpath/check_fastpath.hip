@@ -8,7 +8,9 @@
 //                                   implies custom_round(t) == rint(t)
 //   check_fastpath blocks N seed    N blocks from each input family: where
 //                                   project_fast succeeds its point equals
-//                                   the oracle's projection bit for bit
+//                                   the oracle's projection bit for bit, and
+//                                   fast_rows succeeds on the same blocks
+//                                   with the exact rows of G^-1 y
 //   check_fastpath dyadic q N       the decoders' residual G b - q P(G b / q)
 //                                   through project_dyadic against the
 //                                   oracle's (both distance rules): every
@@ -144,13 +146,42 @@ static int blocks(long n, unsigned seed)
     int rc = 0;
     for (int fam = 0; fam < n_fam; ++fam) {
         std::mt19937_64 g(seed * 7919u + fam);
-        long ok = 0, bad = 0;
+        long ok = 0, bad = 0, bad_rows = 0;
         float x[8], yf[8], yr[8];
         for (long it = 0; it < n; ++it) {
             family(fam, g, x);
-            if (!coset::project_fast(x, yf)) continue;
+            int rows[8];
+            const bool fast_ok = coset::project_fast(x, yf);
+            const bool rows_ok = coset::fast_rows(x, rows, coset::fast_in_range(x));
+            if (fast_ok != rows_ok) {
+                ++bad_rows;
+                continue;
+            }
+            if (!fast_ok) continue;
             ++ok;
             or_projection(x, 1, 0, yr);
+            // rows of G^-1 y_ref, exact in double
+            double suf = 0.0, want[8];
+            for (int r = 6; r >= 0; --r) {
+                suf += (double)yr[r];
+                if (r >= 1) want[r] = suf - (double)(7 - r) * yr[7];
+            }
+            want[0] = suf / 2.0 - 3.5 * (double)yr[7];
+            want[7] = 2.0 * (double)yr[7];
+            bool rows_match = true;
+            for (int r = 0; r < 8; ++r) rows_match = rows_match && (double)rows[r] == want[r];
+            if (!rows_match) {
+                if (bad_rows < 5) {
+                    printf("rows mismatch family %d:", fam);
+                    for (int i = 0; i < 8; ++i) printf(" %.9g", x[i]);
+                    printf("\n  fast rows:");
+                    for (int i = 0; i < 8; ++i) printf(" %d", rows[i]);
+                    printf("\n  ref rows: ");
+                    for (int i = 0; i < 8; ++i) printf(" %.1f", want[i]);
+                    printf("\n");
+                }
+                ++bad_rows;
+            }
             if (memcmp(yf, yr, sizeof yf) != 0) {
                 if (bad < 5) {
                     printf("mismatch family %d:", fam);
@@ -164,9 +195,9 @@ static int blocks(long n, unsigned seed)
                 ++bad;
             }
         }
-        printf("family %d: %ld blocks, fast path taken %ld (%.4f%%), mismatches %ld\n", fam, n, ok,
-               100.0 * ok / n, bad);
-        if (bad) rc = 1;
+        printf("family %d: %ld blocks, fast path taken %ld (%.4f%%), mismatches %ld, row mismatches %ld\n", fam, n,
+               ok, 100.0 * ok / n, bad, bad_rows);
+        if (bad || bad_rows) rc = 1;
     }
     return rc;
 }
