@@ -51,6 +51,10 @@ SIGNATURES = {
     "coset_e8_legacy_encode": [_vp, _int, _i64, _flt, ctypes.c_double, _int, _int, _vp, _i64, _int, _int, _vp,
                                _vp, _vp, _vp, _vp, _vp],
     "coset_e8_legacy_decode": [_vp, _vp, _vp, _i64, _flt, ctypes.c_double, _vp, _i64, _int, _int, _vp, _vp],
+    "coset_vlut_linear": [_vp, _int, _vp, _int, _vp, _int, _i64, _i64, _i64, _int, _int, _int, _int, _vp, _vp, _int,
+                          _vp, _i64, _vp, _vp],
+    "coset_lsq_fwd": [_vp, _int, _i64, _vp, _int, _vp, _vp],
+    "coset_lsq_bwd": [_vp, _vp, _int, _i64, _vp, _int, _vp, _vp, _vp, _i64, _vp],
     "coset_init": [_int],
     "coset_set_option": [_int, _int],
 }
@@ -59,6 +63,7 @@ SIGNATURES = {
 SIZE_QUERIES = {
     "coset_vlut_workspace_floats": [_i64, _i64, _i64, _int, _int, _int, _int],
     "coset_vlut_prepared_words": [_i64, _i64, _int, _int],
+    "coset_lsq_workspace_floats": [_i64],
 }
 
 OPT_CODEC_PATH = 1

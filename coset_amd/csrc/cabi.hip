@@ -439,6 +439,40 @@ int64_t coset_vlut_workspace_floats(int64_t B, int64_t rows, int64_t K, int q, i
     return coset::vlut_workspace_floats(coset::vlut_plan(rows, B, K, q, M, m), B, rows);
 }
 
+int64_t coset_lsq_workspace_floats(int64_t n) { return n < 0 ? 0 : coset::lsq_workspace_floats(n); }
+
+static int check_lsq(const void* x, int dtype, int64_t n, const float* alpha, int qmax)
+{
+    if (n < 0) return fail(COSET_EINVAL, "n must be >= 0");
+    if (dtype != COSET_F32 && dtype != COSET_BF16 && dtype != COSET_F16)
+        return fail(COSET_EUNSUPPORTED, "activation dtype %d not supported (fp32, bf16, fp16)", dtype);
+    if (qmax < 1) return fail(COSET_EINVAL, "qmax must be >= 1 (bit_width >= 2)");
+    if (!alpha) return fail(COSET_EINVAL, "NULL alpha");
+    if (n > 0 && !x) return fail(COSET_EINVAL, "NULL buffer");
+    return COSET_OK;
+}
+
+int coset_lsq_fwd(const void* x, int dtype, int64_t n, const float* alpha, int qmax, void* out, void* stream)
+{
+    int rc;
+    if ((rc = check_lsq(x, dtype, n, alpha, qmax))) return rc;
+    if (n > 0 && !out) return fail(COSET_EINVAL, "NULL buffer");
+    return check_hip(coset::launch_lsq_fwd(x, dtype, n, alpha, qmax, out, (hipStream_t)stream), "lsq forward launch");
+}
+
+int coset_lsq_bwd(const void* x, const void* g, int dtype, int64_t n, const float* alpha, int qmax, void* dx,
+                  float* d_alpha, float* workspace, int64_t workspace_floats, void* stream)
+{
+    int rc;
+    if ((rc = check_lsq(x, dtype, n, alpha, qmax))) return rc;
+    if ((n > 0 && (!g || !dx)) || !d_alpha || !workspace) return fail(COSET_EINVAL, "NULL buffer");
+    if (workspace_floats < coset::lsq_workspace_floats(n))
+        return fail(COSET_EINVAL, "workspace holds %lld floats, %lld needed", (long long)workspace_floats,
+                    (long long)coset::lsq_workspace_floats(n));
+    return check_hip(coset::launch_lsq_bwd(x, g, dtype, n, alpha, qmax, dx, d_alpha, workspace, (hipStream_t)stream),
+                     "lsq backward launch");
+}
+
 int64_t coset_vlut_prepared_words(int64_t rows, int64_t kb, int M, int word_format)
 {
     if (rows < 0 || kb < 0 || M < 1 || word_format < 0 || word_format > 2) return 0;
@@ -458,11 +492,13 @@ int coset_vlut_prepare(const void* words, int64_t rows, int64_t kb, int M, int q
                                          (hipStream_t)stream), "vLUT prepare launch");
 }
 
-int coset_vlut_matmul(const void* words, int word_format, const float* scale, int scale_mode, const void* act,
-                      int act_dtype, int64_t B, int64_t rows, int64_t K, int q, int M, int legacy, int method,
-                      float* workspace, int64_t workspace_floats, float* out, void* stream)
+static int vlut_matmul_impl(const void* words, int word_format, const float* scale, int scale_mode, const void* act,
+                            int act_dtype, int64_t B, int64_t rows, int64_t K, int q, int M, int legacy, int method,
+                            const float* bias, const float* lsq_alpha, int lsq_qmax, float* workspace,
+                            int64_t workspace_floats, float* out, void* stream)
 {
     int rc;
+    if (lsq_alpha && lsq_qmax < 1) return fail(COSET_EINVAL, "lsq_qmax must be >= 1 (bit_width >= 2)");
     if ((rc = check_qm(q, M))) return rc;
     if (q != 2 && q != 4) return fail(COSET_EUNSUPPORTED, "vLUT matmul supports q = 2 or 4 (got %d)", q);
     if (M > 4) return fail(COSET_EUNSUPPORTED, "vLUT matmul supports M <= 4");
@@ -500,10 +536,30 @@ int coset_vlut_matmul(const void* words, int word_format, const float* scale, in
     p.legacy = legacy ? 1 : 0;
     p.partial = workspace;
     p.out = out;
+    p.bias = bias;
+    p.lsq_alpha = lsq_alpha;
+    p.lsq_qmax = lsq_qmax;
     const coset::DecodeTables* t = nullptr;
     if ((rc = check_hip(coset::get_decode_tables(q, p.legacy, &t), "decode tables"))) return rc;
     if (t->n_coarse > coset::kMaxCoarseVlut) return fail(COSET_EUNSUPPORTED, "too many coarse points");
     return check_hip(coset::vlut_matmul(p, plan, (hipStream_t)stream), "vLUT matmul launch");
+}
+
+int coset_vlut_matmul(const void* words, int word_format, const float* scale, int scale_mode, const void* act,
+                      int act_dtype, int64_t B, int64_t rows, int64_t K, int q, int M, int legacy, int method,
+                      float* workspace, int64_t workspace_floats, float* out, void* stream)
+{
+    return vlut_matmul_impl(words, word_format, scale, scale_mode, act, act_dtype, B, rows, K, q, M, legacy, method,
+                            nullptr, nullptr, 0, workspace, workspace_floats, out, stream);
+}
+
+int coset_vlut_linear(const void* words, int word_format, const float* scale, int scale_mode, const void* act,
+                      int act_dtype, int64_t B, int64_t rows, int64_t K, int q, int M, int legacy, int method,
+                      const float* bias, const float* lsq_alpha, int lsq_qmax, float* workspace,
+                      int64_t workspace_floats, float* out, void* stream)
+{
+    return vlut_matmul_impl(words, word_format, scale, scale_mode, act, act_dtype, B, rows, K, q, M, legacy, method,
+                            bias, lsq_alpha, lsq_qmax, workspace, workspace_floats, out, stream);
 }
 
 int coset_e8_lattice_op(int op, int legacy, const float* in, int64_t n_blocks, int q,

@@ -151,8 +151,8 @@ hipError_t launch_codec_generic(const CodecArgs& a, int mode, hipStream_t s);
 bool lut_path_supported(const CodecArgs& a, int mode);
 hipError_t launch_codec_lut(const CodecArgs& a, int mode, hipStream_t s);
 extern int g_codec_path;
-extern int g_fast_projection;
-extern int g_codec_plain;      // 1 (default): the table kernel's fixed-format variant where it applies  // 1 (default): encoders use project_fast where exact
+extern int g_fast_projection;  // 1 (default): encoders use the fast projection where it is exact
+extern int g_codec_plain;      // 1 (default): the table kernel's fixed-format variant where it applies
 constexpr int64_t kLutMinBlocks = 1 << 16;
 
 // Backward of the QAT weight quantizer (qat.hip).
@@ -161,6 +161,13 @@ hipError_t launch_qat_bwd(const void* g, int g_dtype, const float* W, const void
                           const float* beta, int64_t n_blocks, int64_t blocks_per_tile, float clip,
                           int q, int M, float* dW, float* dbeta, const float* dbdt, float* dtheta,
                           hipStream_t s);
+
+// LSQ activation quantizer (lsq.hip): forward, and backward with dalpha
+// reduced through a caller-owned workspace of lsq_workspace_floats(n) floats.
+int64_t lsq_workspace_floats(int64_t n);
+hipError_t launch_lsq_fwd(const void* x, int dt, int64_t n, const float* alpha, int qmax, void* out, hipStream_t s);
+hipError_t launch_lsq_bwd(const void* x, const void* g, int dt, int64_t n, const float* alpha, int qmax, void* dx,
+                          float* d_alpha, float* workspace, hipStream_t s);
 
 // Elementwise lattice operators (custom_round, g_x, projection,
 // encode_coords, decode_coords) over n blocks.

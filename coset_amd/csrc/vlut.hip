@@ -23,6 +23,7 @@
 #include "codec_kernels.hpp"
 #include "tables.hpp"
 #include "vlut.hpp"
+#include "lsq.hpp"
 
 namespace coset {
 
@@ -568,6 +569,17 @@ __device__ __forceinline__ uint4 decode_pair_swar(const uint64_t* s_tab, const u
     return make_uint4(hv[0], hv[1], hv[2], hv[3]);
 }
 
+// Output epilogue: + bias[o], then the LSQ activation quantizer (fp32, the
+// reference's order: the value F.linear(x, W, b) followed by actq,
+// coset/core/layers.py:472-484).
+__device__ __forceinline__ float vlut_epilogue(float y, int64_t o, const float* bias, const float* lsq_alpha,
+                                               int lsq_qmax)
+{
+    if (bias) y = __fadd_rn(y, bias[o]);
+    if (lsq_alpha) y = lsq_value(y, lsq_scale(lsq_alpha, lsq_qmax));
+    return y;
+}
+
 template <int Q, int M, bool BF16, int NTILE, int FMT>
 __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulArgs p)
 {
@@ -663,7 +675,7 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulAr
         if (tok >= p.B || o >= p.rows) continue;
         if (gridDim.y == 1) {
             float sc = p.scale ? (p.scale_mode == 0 ? p.scale[o] : 1.f / p.scale[o]) : 1.f;
-            p.out[tok * p.rows + o] = v * 0.5f * sc;
+            p.out[tok * p.rows + o] = vlut_epilogue(v * 0.5f * sc, o, p.bias, p.lsq_alpha, p.lsq_qmax);
         } else {
             p.partial[(tok * p.rows + o) * gridDim.y + blockIdx.y] = v;
         }
@@ -673,7 +685,8 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulAr
 // ---------------------------------------------------------------- reduce
 __global__ void __launch_bounds__(256) vlut_reduce_kernel(const float* partial, int splits, int64_t B,
                                                          int64_t rows, const float* scale, int scale_mode,
-                                                         float mult, float* out)
+                                                         float mult, const float* bias, const float* lsq_alpha,
+                                                         int lsq_qmax, float* out)
 {
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= B * rows) return;
@@ -689,7 +702,7 @@ __global__ void __launch_bounds__(256) vlut_reduce_kernel(const float* partial, 
     }
     for (; s < splits; ++s) acc += pp[s];
     float sc = scale ? (scale_mode == 0 ? scale[o] : 1.f / scale[o]) : 1.f;
-    out[i] = acc * mult * sc;
+    out[i] = vlut_epilogue(acc * mult * sc, o, bias, lsq_alpha, lsq_qmax);
 }
 
 // ---------------------------------------------------------------- launchers
@@ -915,7 +928,7 @@ hipError_t vlut_matmul(VlutMatmulArgs p, const VlutPlan& plan, hipStream_t s)
     int64_t n = p.B * p.rows;
     float mult = plan.kernel == VK_LDS ? 1.f : 0.5f;
     hipLaunchKernelGGL(vlut_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p.partial, splits,
-                       p.B, p.rows, p.scale, p.scale_mode, mult, p.out);
+                       p.B, p.rows, p.scale, p.scale_mode, mult, p.bias, p.lsq_alpha, p.lsq_qmax, p.out);
     return hipGetLastError();
 }
 

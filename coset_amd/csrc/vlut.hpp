@@ -25,6 +25,11 @@ struct VlutMatmulArgs {
     int q, M, legacy;
     float* partial;      // [B, rows, splits] workspace
     float* out;          // [B, rows]
+    // epilogue after the scale: + bias[o] (nullable), then the LSQ activation
+    // quantizer with parameter *lsq_alpha and lsq_qmax (nullable alpha: none)
+    const float* bias;
+    const float* lsq_alpha;
+    int lsq_qmax;
     // filled by the launcher
     const uint16_t* map;
     const uint64_t* coarse;

@@ -23,7 +23,7 @@ import torch.nn.functional as F
 
 from . import _lib
 from .codecs import e8_quantize, word_dtype
-from .lattice import E8Lattice, default_device
+from .lattice import E8Lattice, default_device, on_gpu
 
 
 def ste_round(x):
@@ -61,9 +61,44 @@ def ste_quantize(x, quantize_fn, q):
     return StraightThroughQuantize.apply(x, quantize_fn, q)
 
 
+class _LSQFunction(torch.autograd.Function):
+    """LSQActivation's forward and its autograd as two fused kernels
+    (coset_lsq_fwd / coset_lsq_bwd): the value and the gradients of
+    coset/core/layers.py:129-137, computed in fp32 on the GPU."""
+
+    @staticmethod
+    def forward(ctx, x, alpha, qmax):
+        xg = x.contiguous()
+        a = alpha.detach().to(torch.float32).reshape(1).contiguous()
+        out = torch.empty_like(xg)
+        _lib.call("coset_lsq_fwd", _lib.ptr(xg), _lib.dtype_code(xg.dtype), xg.numel(), _lib.ptr(a), int(qmax),
+                  _lib.ptr(out), _lib.stream_of(xg))
+        ctx.save_for_backward(xg, a)
+        ctx.qmax = int(qmax)
+        ctx.alpha_meta = (alpha.shape, alpha.dtype)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad):
+        xg, a = ctx.saved_tensors
+        g = grad.to(xg.dtype).contiguous()
+        dx = torch.empty_like(xg)
+        d_alpha = torch.empty(1, dtype=torch.float32, device=xg.device)
+        ws = torch.empty(max(1, _lib.load().coset_lsq_workspace_floats(xg.numel())), dtype=torch.float32,
+                         device=xg.device)
+        _lib.call("coset_lsq_bwd", _lib.ptr(xg), _lib.ptr(g), _lib.dtype_code(xg.dtype), xg.numel(), _lib.ptr(a),
+                  ctx.qmax, _lib.ptr(dx), _lib.ptr(d_alpha), _lib.ptr(ws), ws.numel(), _lib.stream_of(xg))
+        shape, dtype = ctx.alpha_meta
+        return dx, d_alpha.reshape(shape).to(dtype), None
+
+
 class LSQActivation(nn.Module):
     """Learnable per-tensor symmetric activation quantizer
-    (coset/core/layers.py:117-137)."""
+    (coset/core/layers.py:117-137): out = round(clamp(x, -a, a) / s) * s with
+    a = relu(alpha) + 1e-8, s = a / qmax, straight-through gradients to x and
+    alpha.  One fused kernel each way (fp32 arithmetic in the reference's
+    order, the result written in x's dtype); host tensors are processed on the
+    GPU and returned on the host."""
 
     def __init__(self, bit_width: int = 8, init_alpha: float = 1.0):
         super().__init__()
@@ -72,12 +107,13 @@ class LSQActivation(nn.Module):
         self.alpha = nn.Parameter(torch.tensor(init_alpha))
 
     def forward(self, x):
-        alpha = torch.relu(self.alpha) + 1e-8
-        x_clipped = ste_clip(x, -alpha, alpha)
-        scale = alpha / self.qmax
-        y = x_clipped / scale
-        yq = ste_round(y)
-        return yq * scale
+        home = x.device
+        xg = on_gpu(x)
+        if xg.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+            xg = xg.float()
+        alpha = self.alpha if self.alpha.device == xg.device else self.alpha.to(xg.device)
+        out = _LSQFunction.apply(xg, alpha, self.qmax)
+        return out if out.device == home else out.to(home)
 
 
 @dataclass

@@ -9,6 +9,9 @@ safetensors file that executes nothing when loaded.  ``PackedLinear`` serves
 such a file with the vLUT matmul: y = x @ (decode(words) / beta)^T + bias,
 which equals the layer's F.linear(x, W_q, bias) wherever no weight was
 clipped at +-weight_clip_value (the count of clipped weights is recorded).
+A layer trained with quantize_activations also stores its LSQ parameter
+(act_alpha, act_bit_width); the bias add and the activation quantizer then
+run in the matmul's epilogue (coset_vlut_linear).
 """
 from __future__ import annotations
 
@@ -42,10 +45,15 @@ def packed_state(layer) -> Dict[str, object]:
     tensors = {"words": words.contiguous(), "beta": beta.contiguous()}
     if layer.bias is not None:
         tensors["bias"] = layer.bias.detach().float().contiguous()
+    actq = getattr(layer, "actq", None)
+    if getattr(layer, "quantize_activations", False) and actq is not None:
+        tensors["act_alpha"] = actq.alpha.detach().float().reshape(1).contiguous()
     meta = {"format": FORMAT, "lattice": "E8", "rule": "core", "q": q, "M": M,
             "in_features": int(layer.in_features), "out_features": int(layer.out_features),
             "weight_clip_value": float(layer.weight_clip_value), "clipped_weights": clipped,
             "scale": "divide: W = decode(words) / beta[row]"}
+    if "act_alpha" in tensors:
+        meta["act_bit_width"] = int(actq.bit_width)
     return {"tensors": tensors, "metadata": meta}
 
 
@@ -91,15 +99,19 @@ class PackedLinear(nn.Module):
         self.register_buffer("beta", tensors["beta"].to(words.device).float())
         bias = tensors.get("bias")
         self.register_buffer("bias", None if bias is None else bias.to(words.device).float())
+        alpha = tensors.get("act_alpha")
+        self.register_buffer("act_alpha", None if alpha is None else alpha.to(words.device).float())
+        self.act_qmax = 2 ** (int(meta["act_bit_width"]) - 1) - 1 if alpha is not None else 0
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        """bias and the LSQ activation quantizer (when the layer had one) run
+        in the matmul's epilogue."""
         lead = x.shape[:-1]
         a = x.reshape(-1, self.in_features)
         if a.dtype not in (torch.float16, torch.bfloat16):
             a = a.to(torch.bfloat16)
-        y = vlut_matmul(self.prepared, a, scale=self.beta, scale_mode="div")
-        if self.bias is not None:
-            y = y + self.bias
+        aq = None if self.act_alpha is None else (self.act_alpha, self.act_qmax)
+        y = vlut_matmul(self.prepared, a, scale=self.beta, scale_mode="div", bias=self.bias, act_quant=aq)
         return y.reshape(*lead, self.out_features)
 
     def dequantized_weight(self) -> torch.Tensor:

@@ -17,7 +17,7 @@ Differences from the reference, by design:
 from __future__ import annotations
 
 from dataclasses import dataclass
-from typing import Dict, List, Optional
+from typing import Dict, List, Optional, Tuple
 
 import torch
 
@@ -229,7 +229,8 @@ def vlut_prepare(words: torch.Tensor, q: int = 4, legacy: bool = False, layout: 
 
 def vlut_matmul(words, act: torch.Tensor, q: int = 4, *, scale: Optional[torch.Tensor] = None,
                 scale_mode: str = "mul", legacy: bool = False, method: str = "auto",
-                workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+                workspace: Optional[torch.Tensor] = None, bias: Optional[torch.Tensor] = None,
+                act_quant: Optional[Tuple[torch.Tensor, int]] = None) -> torch.Tensor:
     """out[B, rows] = s_o * sum_k sum_m q^m vLUT_{act[:, 8k:8k+8]}[words[o, k, m]].
 
     words: packed level words [rows, K/8, M] (uint16, q in {2, 4}), or a
@@ -238,6 +239,10 @@ def vlut_matmul(words, act: torch.Tensor, q: int = 4, *, scale: Optional[torch.T
     (``scale_mode="mul"``, codec convention) or divides (``"div"``, layer
     convention).  With the core rule (legacy=False) the result equals
     act @ (e8_decode(codes) * s)^T.
+
+    Epilogue, fused into the output write (coset_vlut_linear): ``bias``
+    [rows] is added, then ``act_quant = (alpha, qmax)`` applies the LSQ
+    activation quantizer with that parameter (inference: no gradient).
     """
     if isinstance(words, PreparedWords):
         rows, kb, M = words.rows, words.kb, words.M
@@ -262,7 +267,18 @@ def vlut_matmul(words, act: torch.Tensor, q: int = 4, *, scale: Optional[torch.T
     if scale is not None:
         s = on_gpu(scale).float().contiguous()
     out = torch.empty((B, rows), dtype=torch.float32, device=a.device)
-    _lib.call("coset_vlut_matmul", _lib.ptr(w), fmt, _lib.ptr(s), 0 if scale_mode == "mul" else 1, _lib.ptr(a), dt,
-              B, rows, K, int(q), int(M), int(legacy), m, _lib.ptr(workspace),
-              workspace.numel() if workspace is not None else 0, _lib.ptr(out), _lib.stream_of(a))
+    ws_n = workspace.numel() if workspace is not None else 0
+    if bias is None and act_quant is None:
+        _lib.call("coset_vlut_matmul", _lib.ptr(w), fmt, _lib.ptr(s), 0 if scale_mode == "mul" else 1, _lib.ptr(a),
+                  dt, B, rows, K, int(q), int(M), int(legacy), m, _lib.ptr(workspace), ws_n, _lib.ptr(out),
+                  _lib.stream_of(a))
+        return out
+    b = None if bias is None else on_gpu(bias).float().contiguous()
+    if b is not None and b.numel() != rows:
+        raise ValueError(f"bias must hold {rows} values")
+    alpha, qmax = (None, 0) if act_quant is None else act_quant
+    al = None if alpha is None else on_gpu(alpha).detach().float().reshape(1).contiguous()
+    _lib.call("coset_vlut_linear", _lib.ptr(w), fmt, _lib.ptr(s), 0 if scale_mode == "mul" else 1, _lib.ptr(a), dt,
+              B, rows, K, int(q), int(M), int(legacy), m, _lib.ptr(b), _lib.ptr(al), int(qmax),
+              _lib.ptr(workspace), ws_n, _lib.ptr(out), _lib.stream_of(a))
     return out

@@ -223,6 +223,33 @@ int coset_vlut_matmul(const void* words, int word_format, const float* scale, in
                       int act_dtype, int64_t B, int64_t rows, int64_t K, int q, int M, int legacy, int method,
                       float* workspace, int64_t workspace_floats, float* out, void* stream);
 
+/* LSQ activation quantizer forward (LSQActivation.forward with ste_clip and
+ * ste_round, coset/core/layers.py:117-137, 20-26), over n values of x
+ * (COSET_F32, COSET_BF16 or COSET_F16), computed in fp32 in the reference's
+ * operation order and written once in x's dtype:
+ *   a = relu(alpha) + 1e-8, s = a / qmax,
+ *   out = ((y - y) + round(y)) * s,  y = ((x - x) + clamp(x, -a, a)) / s.
+ * alpha: device pointer to the fp32 parameter (read on the device). */
+int coset_lsq_fwd(const void* x, int dtype, int64_t n, const float* alpha, int qmax, void* out, void* stream);
+
+/* Its backward (the autograd of the same chain): dx = (g s) / s in x's dtype
+ * and d_alpha[0] = relu(alpha) > 0 ? (sum g yq - sum (g s)((xc / s) / s)) / qmax
+ * : 0, written (not accumulated), summed in a fixed order through a
+ * caller-owned workspace of coset_lsq_workspace_floats(n) floats. */
+int64_t coset_lsq_workspace_floats(int64_t n);
+int coset_lsq_bwd(const void* x, const void* g, int dtype, int64_t n, const float* alpha, int qmax, void* dx,
+                  float* d_alpha, float* workspace, int64_t workspace_floats, void* stream);
+
+/* coset_vlut_matmul with the layer's epilogue fused into the output write:
+ * out = actq(matmul + bias[o]), the value of HNLQLinearQAT.forward
+ * (F.linear then the LSQ activation quantizer, coset/core/layers.py:472-484).
+ * bias: [rows] fp32 or NULL; lsq_alpha: device pointer to the LSQ parameter
+ * (as coset_lsq_fwd, fp32 result) or NULL for no activation quantizer. */
+int coset_vlut_linear(const void* words, int word_format, const float* scale, int scale_mode, const void* act,
+                      int act_dtype, int64_t B, int64_t rows, int64_t K, int q, int M, int legacy, int method,
+                      const float* bias, const float* lsq_alpha, int lsq_qmax, float* workspace,
+                      int64_t workspace_floats, float* out, void* stream);
+
 /* Elementwise lattice operator over n_blocks fp32 blocks (custom_round is
  * applied to all 8*n_blocks values).  legacy selects the legacy g_x rule. */
 int coset_e8_lattice_op(int op, int legacy, const float* in, int64_t n_blocks, int q,

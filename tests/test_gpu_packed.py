@@ -55,3 +55,53 @@ def test_rejects_block_tiling_and_foreign_files(tmp_path):
     save_file({"w": torch.zeros(2)}, str(tmp_path / "other.safetensors"), metadata={"coset_amd": '{"format": "x"}'})
     with pytest.raises(ValueError):
         ca.load_packed(str(tmp_path / "other.safetensors"))
+
+
+@pytest.mark.parametrize("splits", [0, 3])
+def test_vlut_epilogue_bias_and_lsq(splits):
+    """coset_vlut_linear's epilogue equals the LSQ kernel applied to
+    matmul + bias, bit for bit, on the direct write and on the split-K
+    reduce path."""
+    import coset_amd as ca
+    from coset_amd import _lib
+    torch.manual_seed(4)
+    rows, K, B = 96, 512, 5
+    words = ca.hnlq_encode(torch.randn(rows * K // 8, 8, device="cuda") * 2, 4, 2, 1.0).reshape(rows, K // 8, 2)
+    prep = ca.vlut_prepare(words, 4)
+    a = torch.randn(B, K, device="cuda").to(torch.bfloat16)
+    beta = torch.rand(rows, device="cuda") + 0.5
+    bias = torch.randn(rows, device="cuda")
+    m = ca.LSQActivation(bit_width=6, init_alpha=3.0).cuda()
+    try:
+        _lib.set_vlut_splits(splits)
+        plain = ca.vlut_matmul(prep, a, scale=beta, scale_mode="div")
+        fused = ca.vlut_matmul(prep, a, scale=beta, scale_mode="div", bias=bias, act_quant=(m.alpha, m.qmax))
+        only_bias = ca.vlut_matmul(prep, a, scale=beta, scale_mode="div", bias=bias)
+    finally:
+        _lib.set_vlut_splits(0)
+    assert torch.equal(only_bias, plain + bias)
+    with torch.no_grad():
+        assert torch.equal(fused, m(plain + bias))
+
+
+def test_packed_layer_with_activation_quantizer(tmp_path):
+    import coset_amd as ca
+    torch.manual_seed(6)
+    layer = ca.create_e8_hnlq_linear(256, 64, q=4, M=2, Delta0=1.5, quantize_activations=True, act_bit_width=8,
+                                     act_init_alpha=4.0)
+    with torch.no_grad():
+        layer.weight.normal_(0.0, 0.5)
+    x = torch.randn(8, 256, device="cuda").to(torch.bfloat16)
+    ca.save_packed(layer, str(tmp_path / "a.safetensors"))
+    pl = ca.load_packed(str(tmp_path / "a.safetensors"))
+    assert pl.meta["act_bit_width"] == 8 and pl.act_qmax == 127
+    y = pl(x)
+    with torch.no_grad():
+        W_q = pl.dequantized_weight()
+        ref = layer.actq(torch.nn.functional.linear(x.float(), W_q, layer.bias.float()))
+    s = (4.0 + 1e-8) / 127
+    d = (y - ref).abs()
+    # the matmul's fp32 order differs from F.linear; LSQ maps a difference
+    # across a rounding boundary to one step s
+    assert d.max().item() <= s * 1.001 + 1e-5
+    assert (d > 1e-5).float().mean().item() < 0.02
