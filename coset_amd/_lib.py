@@ -53,6 +53,11 @@ SIGNATURES = {
     "coset_e8_legacy_decode": [_vp, _vp, _vp, _i64, _flt, ctypes.c_double, _vp, _i64, _int, _int, _vp, _vp],
     "coset_vlut_linear": [_vp, _int, _vp, _int, _vp, _int, _i64, _i64, _i64, _int, _int, _int, _int, _vp, _vp, _int,
                           _vp, _i64, _vp, _vp],
+    "coset_d4_lattice_op": [_int, _vp, _i64, _int, _vp, _vp],
+    "coset_d4_qat_fwd": [_vp, _i64, _i64, _vp, _i64, _flt, _vp, _int, _vp],
+    "coset_d4_qat_fwd_theta": [_vp, _i64, _i64, _i64, _vp, _vp, _vp, ctypes.c_double, ctypes.c_double,
+                               ctypes.c_double, _int, _int, _flt, _vp, _int, _vp, _vp, _vp, _vp],
+    "coset_d4_qat_bwd": [_vp, _int, _vp, _vp, _vp, _i64, _i64, _i64, _flt, _vp, _vp, _vp, _vp],
     "coset_lsq_fwd": [_vp, _int, _i64, _vp, _int, _vp, _vp],
     "coset_lsq_bwd": [_vp, _vp, _int, _i64, _vp, _int, _vp, _vp, _vp, _i64, _vp],
     "coset_init": [_int],

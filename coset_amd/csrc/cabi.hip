@@ -439,6 +439,79 @@ int64_t coset_vlut_workspace_floats(int64_t B, int64_t rows, int64_t K, int q, i
     return coset::vlut_workspace_floats(coset::vlut_plan(rows, B, K, q, M, m), B, rows);
 }
 
+int coset_d4_lattice_op(int op, const float* in, int64_t n_blocks, int q, float* out, void* stream)
+{
+    if (n_blocks < 0) return fail(COSET_EINVAL, "n_blocks < 0");
+    if (op < COSET_OP_G_X || op > COSET_OP_DECODE_COORDS) return fail(COSET_EINVAL, "unknown D4 lattice op %d", op);
+    if (n_blocks > 0 && (!in || !out)) return fail(COSET_EINVAL, "NULL buffer");
+    if (!aligned(in, 16) || !aligned(out, 16)) return fail(COSET_EINVAL, "buffers must be 16-byte aligned");
+    if (op == COSET_OP_ENCODE_COORDS && q < 1) return fail(COSET_EINVAL, "q must be positive");
+    return check_hip(coset::launch_d4_lattice_op(op, in, n_blocks, q, out, (hipStream_t)stream), "D4 lattice op launch");
+}
+
+static int check_d4_qat(const float* W, int64_t rows, int64_t cols, int64_t blocks_per_tile, float clip,
+                        int64_t* n_blocks)
+{
+    if (rows < 0 || cols < 0 || cols % 4) return fail(COSET_EINVAL, "W must be [rows, 4k]");
+    const int64_t n = rows * (cols / 4);
+    if (blocks_per_tile <= 0 || n % blocks_per_tile) return fail(COSET_EINVAL, "blocks_per_tile must divide the block count");
+    if (n / blocks_per_tile > 0x7fffffff) return fail(COSET_EINVAL, "too many tiles");
+    if (!(clip >= 0.f)) return fail(COSET_EINVAL, "clip must be >= 0");
+    if (n > 0 && !W) return fail(COSET_EINVAL, "NULL buffer");
+    if (!aligned(W, 16)) return fail(COSET_EINVAL, "W must be 16-byte aligned");
+    *n_blocks = n;
+    return COSET_OK;
+}
+
+int coset_d4_qat_fwd(const float* W, int64_t rows, int64_t cols, const float* beta, int64_t blocks_per_tile,
+                     float clip, void* Wq, int wq_dtype, void* stream)
+{
+    int rc;
+    int64_t n = 0;
+    if ((rc = check_d4_qat(W, rows, cols, blocks_per_tile, clip, &n))) return rc;
+    if ((rc = check_dtype(wq_dtype, "Wq"))) return rc;
+    if (n > 0 && (!beta || !Wq)) return fail(COSET_EINVAL, "NULL buffer");
+    if (!aligned(Wq, wq_dtype == COSET_F32 ? 16 : 8)) return fail(COSET_EINVAL, "Wq misaligned");
+    if (n == 0) return COSET_OK;
+    return check_hip(coset::launch_d4_qat_fwd(W, n, blocks_per_tile, beta, nullptr, clip, Wq, wq_dtype, nullptr,
+                                              nullptr, nullptr, (hipStream_t)stream),
+                     "D4 qat forward launch");
+}
+
+int coset_d4_qat_fwd_theta(const float* W, int64_t rows, int64_t cols, int64_t blocks_per_tile, const float* theta,
+                           const float* sigma_ema, const float* xmax_ema, double delta0, double eta,
+                           double gamma_inv, int q, int M_bounds, float clip, void* Wq, int wq_dtype,
+                           float* beta_out, float* dbeta_dtheta_out, int64_t* step_counter, void* stream)
+{
+    int rc;
+    int64_t n = 0;
+    if ((rc = check_d4_qat(W, rows, cols, blocks_per_tile, clip, &n))) return rc;
+    if ((rc = check_dtype(wq_dtype, "Wq"))) return rc;
+    if (q < 2 || M_bounds < 1 || M_bounds > 16) return fail(COSET_EINVAL, "bad q=%d / M=%d for the bounds", q, M_bounds);
+    if (n > 0 && (!theta || !sigma_ema || !xmax_ema || !Wq)) return fail(COSET_EINVAL, "NULL buffer");
+    if (!aligned(Wq, wq_dtype == COSET_F32 ? 16 : 8)) return fail(COSET_EINVAL, "Wq misaligned");
+    const coset::ThetaBeta tb = make_theta_beta(theta, sigma_ema, xmax_ema, delta0, eta, gamma_inv, q, M_bounds);
+    return check_hip(coset::launch_d4_qat_fwd(W, n, blocks_per_tile, nullptr, &tb, clip, Wq, wq_dtype, beta_out,
+                                              dbeta_dtheta_out, step_counter, (hipStream_t)stream),
+                     "D4 qat forward launch");
+}
+
+int coset_d4_qat_bwd(const void* gWq, int g_dtype, const float* W, const float* beta, const float* dbeta_dtheta,
+                     int64_t rows, int64_t cols, int64_t blocks_per_tile, float clip, float* dW, float* dbeta,
+                     float* dtheta, void* stream)
+{
+    int rc;
+    int64_t n = 0;
+    if ((rc = check_d4_qat(W, rows, cols, blocks_per_tile, clip, &n))) return rc;
+    if ((rc = check_dtype(g_dtype, "gradient"))) return rc;
+    if (n > 0 && (!gWq || !beta || !dW || !dbeta)) return fail(COSET_EINVAL, "NULL buffer");
+    if (dbeta_dtheta && !dtheta) return fail(COSET_EINVAL, "dtheta needed with dbeta_dtheta");
+    if (!aligned(gWq, g_dtype == COSET_F32 ? 16 : 8) || !aligned(dW, 16)) return fail(COSET_EINVAL, "g or dW misaligned");
+    return check_hip(coset::launch_d4_qat_bwd(gWq, g_dtype, W, beta, dbeta_dtheta, n, blocks_per_tile, clip, dW,
+                                              dbeta, dtheta, (hipStream_t)stream),
+                     "D4 qat backward launch");
+}
+
 int64_t coset_lsq_workspace_floats(int64_t n) { return n < 0 ? 0 : coset::lsq_workspace_floats(n); }
 
 static int check_lsq(const void* x, int dtype, int64_t n, const float* alpha, int qmax)

@@ -162,6 +162,16 @@ hipError_t launch_qat_bwd(const void* g, int g_dtype, const float* W, const void
                           int q, int M, float* dW, float* dbeta, const float* dbdt, float* dtheta,
                           hipStream_t s);
 
+// D4 variant (d4.hip): lattice operators over [n, 4] blocks, and the D4
+// layer's fused weight quantizer (tb non-null: beta from theta).
+hipError_t launch_d4_lattice_op(int op, const float* in, int64_t n, int q, float* out, hipStream_t s);
+hipError_t launch_d4_qat_fwd(const float* W, int64_t n_blocks, int64_t blocks_per_tile, const float* beta,
+                             const ThetaBeta* tb, float clip, void* Wq, int wq_dtype, float* beta_out,
+                             float* dbdt_out, int64_t* step_counter, hipStream_t s);
+hipError_t launch_d4_qat_bwd(const void* g, int g_dtype, const float* W, const float* beta, const float* dbdt,
+                             int64_t n_blocks, int64_t blocks_per_tile, float clip, float* dW, float* dbeta,
+                             float* dtheta, hipStream_t s);
+
 // LSQ activation quantizer (lsq.hip): forward, and backward with dalpha
 // reduced through a caller-owned workspace of lsq_workspace_floats(n) floats.
 int64_t lsq_workspace_floats(int64_t n);

@@ -43,16 +43,17 @@ __device__ __forceinline__ float odd_f(float s)
     return __fsub_rn(s, __fmul_rn(2.f, floorf(__fmul_rn(s, 0.5f))));
 }
 
-// One D8 coset candidate for input t: f = round(t) if sum(f) is even, else
-// g(t) (f with the worst coordinate pushed by +-1).  ALWAYS_G returns g(t)
-// whatever the parity (the reference g_x itself).
-template <bool LEGACY, bool ALWAYS_G = false>
-__device__ __forceinline__ void d8_candidate(const float t[8], float y[8])
+// One D_n candidate for input t (n = 8: the D8 cosets of E8; n = 4: the D4
+// lattice, coset/core/d4/lattice.py:62-146): f = round(t) if sum(f) is even,
+// else g(t) (f with the worst coordinate pushed by +-1).  ALWAYS_G returns
+// g(t) whatever the parity (the reference g_x itself).
+template <int D, bool LEGACY, bool ALWAYS_G = false>
+__device__ __forceinline__ void dn_candidate(const float t[D], float y[D])
 {
-    float f[8];
+    float f[D];
     float s = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < D; ++i) {
         f[i] = custom_round(t[i]);
         s = __fadd_rn(s, f[i]);
     }
@@ -61,7 +62,7 @@ __device__ __forceinline__ void d8_candidate(const float t[8], float y[8])
     int k = 0;
     float tk = t[0], fk = f[0];
 #pragma unroll
-    for (int i = 1; i < 8; ++i) {
+    for (int i = 1; i < D; ++i) {
         float d = fabsf(__fsub_rn(t[i], f[i]));
         bool gt = d > best;
         best = gt ? d : best;
@@ -76,7 +77,13 @@ __device__ __forceinline__ void d8_candidate(const float t[8], float y[8])
         up = (tk >= 0.f) && (fk < tk);
     float adj = (ALWAYS_G || odd_f(s) != 0.f) ? (up ? 1.f : -1.f) : 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) y[i] = (i == k) ? __fadd_rn(f[i], adj) : f[i];
+    for (int i = 0; i < D; ++i) y[i] = (i == k) ? __fadd_rn(f[i], adj) : f[i];
+}
+
+template <bool LEGACY, bool ALWAYS_G = false>
+__device__ __forceinline__ void d8_candidate(const float t[8], float y[8])
+{
+    dn_candidate<8, LEGACY, ALWAYS_G>(t, y);
 }
 
 template <bool STRIDED>

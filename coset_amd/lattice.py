@@ -232,3 +232,62 @@ class LegacyE8Lattice(Lattice):
         return self._lattice_op(_lib.OP_PROJECT, x, legacy=True)
 
     projection = Q
+
+
+_D4_ROWS = [[-1, -1, 0, 0], [1, -1, 0, 0], [0, 1, -1, 0], [0, 0, 1, -1]]
+
+
+class D4Lattice(Lattice):
+    """coset/core/d4/lattice.py:14-146: integer points with an even
+    coordinate sum.  ``projection`` rounds with custom_round and, for an odd
+    sum, moves the first coordinate farthest from an integer by +1 when it is
+    >= 0 and above its rounding, by -1 otherwise (the reference's g_x).  The
+    operators run in coset_d4_lattice_op over [N, 4] blocks."""
+
+    def __init__(self, device=None, config: Optional[LatticeConfig] = None):
+        device = default_device(device)
+        G = torch.tensor(_D4_ROWS, dtype=torch.float32, device=device).T
+        super().__init__(G, "D4", device=device, config=config)
+
+    def _compute_packing_radius(self) -> float:
+        return 1.0 / np.sqrt(2)
+
+    def _compute_covering_radius(self) -> float:
+        return 1.0
+
+    def _d4_op(self, op: int, x: torch.Tensor, q: int = 0) -> torch.Tensor:
+        if x.shape[-1] != 4:
+            raise ValueError(f"Input dimension {x.shape[-1]} doesn't match D4 dimension 4")
+        squeeze = x.dim() == 1
+        xb = on_gpu(x).to(torch.float32).contiguous().reshape(-1, 4)
+        out = torch.empty_like(xb)
+        _lib.call("coset_d4_lattice_op", op, _lib.ptr(xb), xb.shape[0], int(q), _lib.ptr(out), _lib.stream_of(xb))
+        out = out.to(x.device)
+        return out.reshape(4) if squeeze else out.reshape(x.shape)
+
+    def g_x(self, x: torch.Tensor) -> torch.Tensor:
+        return self._d4_op(_lib.OP_G_X, x)
+
+    def projection(self, x: torch.Tensor) -> torch.Tensor:
+        return self._d4_op(_lib.OP_PROJECT, x)
+
+    def encode_coords(self, x: torch.Tensor, q: int) -> torch.Tensor:
+        """round(G^-1 x) mod q (coset/core/base.py:134-154)."""
+        return self._d4_op(_lib.OP_ENCODE_COORDS, x, q)
+
+    def decode_coords(self, b: torch.Tensor, q: int) -> torch.Tensor:
+        """G b (coset/core/base.py:156-176)."""
+        return self._d4_op(_lib.OP_DECODE_COORDS, b.float(), q)
+
+
+_D4_BY_DEVICE: Dict[str, "D4Lattice"] = {}
+
+
+def d4_quantize(x: torch.Tensor, q: int) -> torch.Tensor:
+    """The D4 layer's quantizer: the closest D4 point, q unused
+    (coset/core/d4/layers.py:46-47)."""
+    key = str(x.device)
+    lat = _D4_BY_DEVICE.get(key)
+    if lat is None:
+        lat = _D4_BY_DEVICE[key] = D4Lattice(device=x.device)
+    return lat.projection(x)

@@ -23,7 +23,7 @@ import torch.nn.functional as F
 
 from . import _lib
 from .codecs import e8_quantize, word_dtype
-from .lattice import E8Lattice, default_device, on_gpu
+from .lattice import D4Lattice, E8Lattice, d4_quantize, default_device, on_gpu
 
 
 def ste_round(x):
@@ -234,6 +234,55 @@ class E8ThetaWeightQuant(torch.autograd.Function):
         return dW, dtheta.view(theta_shape), None, None, None, None, None, None, None, None, None
 
 
+def d4_qat_fwd_theta(Wc, theta, sigma, xmax, step_count, bounds, q, clip, blocks_per_tile, out_dtype):
+    """One coset_d4_qat_fwd_theta call: (W_q [rows, cols] in out_dtype,
+    beta [tiles], d beta / d theta [tiles])."""
+    th = theta.contiguous()
+    rows, cols = Wc.shape
+    dev = Wc.device
+    Wq = torch.empty((rows, cols), dtype=out_dtype, device=dev)
+    beta = torch.empty(th.numel(), dtype=torch.float32, device=dev)
+    dbdt = torch.empty_like(beta)
+    delta0, eta, ginv, m_bounds = bounds
+    _lib.check("coset_d4_qat_fwd_theta", _lib.fn("coset_d4_qat_fwd_theta")(
+        Wc.data_ptr(), rows, cols, blocks_per_tile, th.data_ptr(), sigma.contiguous().data_ptr(),
+        xmax.contiguous().data_ptr(), delta0, eta, ginv, q, m_bounds, clip, Wq.data_ptr(),
+        _lib.dtype_code(out_dtype), beta.data_ptr(), dbdt.data_ptr(), _lib.ptr(step_count), _lib.stream_of(Wc)))
+    return Wq, beta, dbdt
+
+
+class D4ThetaWeightQuant(torch.autograd.Function):
+    """The D4 layer's fused weight path (coset_d4_qat_fwd_theta /
+    coset_d4_qat_bwd): beta from theta, scale, D4 projection, unscale, clamp
+    and the step counter in one kernel; the backward recomputes the
+    projection and returns dW and dtheta."""
+
+    @staticmethod
+    def forward(ctx, W, theta, sigma, xmax, step_count, bounds, q, clip, blocks_per_tile, out_dtype):
+        Wc = W.detach().contiguous()
+        Wq, beta, dbdt = d4_qat_fwd_theta(Wc, theta.detach(), sigma, xmax, step_count, bounds, q, clip,
+                                          blocks_per_tile, out_dtype)
+        ctx.save_for_backward(Wc, beta, dbdt)
+        ctx.cfg = (clip, blocks_per_tile, theta.shape)
+        return Wq
+
+    @staticmethod
+    def backward(ctx, g):
+        Wc, beta, dbdt = ctx.saved_tensors
+        clip, bpt, theta_shape = ctx.cfg
+        if g.dtype not in (torch.float32, torch.bfloat16):
+            g = g.float()
+        g = g.contiguous()
+        rows, cols = Wc.shape
+        dW = torch.empty_like(Wc)
+        dbeta = torch.empty_like(beta)
+        dtheta = torch.empty_like(beta)
+        _lib.check("coset_d4_qat_bwd", _lib.fn("coset_d4_qat_bwd")(
+            g.data_ptr(), _lib.dtype_code(g.dtype), Wc.data_ptr(), beta.data_ptr(), dbdt.data_ptr(), rows, cols,
+            bpt, clip, dW.data_ptr(), dbeta.data_ptr(), dtheta.data_ptr(), _lib.stream_of(Wc)))
+        return dW, dtheta.view(theta_shape), None, None, None, None, None, None, None, None
+
+
 class HNLQLinearQAT(nn.Module):
     """Hierarchical nested-lattice quantized linear layer with QAT cold start
     (coset/core/layers.py:166-658); same constructor, buffers, state_dict
@@ -401,6 +450,10 @@ class HNLQLinearQAT(nn.Module):
         return (self.quantize_fn is e8_quantize and self.block_size == 8
                 and self.lattice_type == "E8" and self.weight.is_cuda)
 
+    def _fused_d4(self) -> bool:
+        return (self.quantize_fn is d4_quantize and self.block_size == 4
+                and self.lattice_type == "D4" and self.weight.is_cuda)
+
     def _quantize_weights_as(self, out_dtype: torch.dtype):
         W = self.weight
         if not self.quantization_enabled:
@@ -408,8 +461,14 @@ class HNLQLinearQAT(nn.Module):
                 self._weight_history.append(W.detach().clone())
             return W
         fused = self._fused()
-        self._advance_step(device_increment=not fused)
-        if fused:
+        fused_d4 = self._fused_d4()
+        self._advance_step(device_increment=not (fused or fused_d4))
+        if fused_d4:
+            bpt = self.blocks_per_row if self.tiling == "row" else 1
+            W_q = D4ThetaWeightQuant.apply(W, self.theta_beta, self.sigma_ema, self.xmax_ema, self.step_count,
+                                           (float(self.Delta0), float(self.eta), self._ginv_f, int(self.M)),
+                                           int(self.q), float(self.weight_clip_value), int(bpt), out_dtype)
+        elif fused:
             bpt = self.blocks_per_row if self.tiling == "row" else 1
             # one theta per tile: out_features entries for row tiling, so no slice is needed
             # the injected e8_quantize always encodes with M = 2 (codecs.py:245-254)
@@ -565,6 +624,21 @@ class HNLQLinearQAT(nn.Module):
 
 
 HNLQLinear = HNLQLinearQAT
+
+
+def create_d4_hnlq_linear(in_dim, out_dim, device=None, **kwargs):
+    """coset/core/d4/layers.py:14-68: HNLQLinearQAT over 4-wide blocks
+    quantized by the D4 projection (d4_quantize; q sets only the beta
+    bounds).  device defaults to the GPU when one is visible."""
+    if in_dim % 4 != 0:
+        raise ValueError(f"Input dimension {in_dim} must be divisible by 4 for D4 lattice")
+    device = default_device(device)
+    lattice = D4Lattice(device=device)
+    defaults = {"lattice": lattice, "quantize_fn": d4_quantize, "block_size": 4, "q": 4, "M": 2,
+                "Delta0": None, "warmup_epochs": 0, "enable_diagnostics": False, "weight_clip_value": 2.0,
+                "theta_trainable": True, "theta_init_value": 0.0, "rho": 0.95}
+    defaults.update(kwargs)
+    return HNLQLinearQAT(in_dim, out_dim, **defaults)
 
 
 def create_e8_hnlq_linear(in_dim, out_dim, device=None, **kwargs):

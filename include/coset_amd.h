@@ -223,6 +223,38 @@ int coset_vlut_matmul(const void* words, int word_format, const float* scale, in
                       int act_dtype, int64_t B, int64_t rows, int64_t K, int q, int M, int legacy, int method,
                       float* workspace, int64_t workspace_floats, float* out, void* stream);
 
+/* D4 lattice operator over n_blocks fp32 [n, 4] blocks (coset/core/d4/lattice.py:62-146,
+ * coset/core/base.py:134-176): COSET_OP_G_X, COSET_OP_PROJECT (closest point,
+ * the reference's rule), COSET_OP_ENCODE_COORDS (round(G^-1 x) mod q),
+ * COSET_OP_DECODE_COORDS (G b).  custom_round is elementwise: use
+ * coset_e8_lattice_op. */
+int coset_d4_lattice_op(int op, const float* in, int64_t n_blocks, int q, float* out, void* stream);
+
+/* The D4 layer's weight quantizer (create_d4_hnlq_linear,
+ * coset/core/d4/layers.py:14-68, which quantizes by projection only, with
+ * HNLQLinearQAT._quantize_weights, coset/core/layers.py:428-463):
+ *   Wq = clamp(P_D4(W * beta_t) / beta_t, -clip, clip)
+ * W fp32 [rows, cols] (cols % 4 == 0), beta_t per tile of blocks_per_tile
+ * 4-wide blocks (cols/4: row tiling, 1: block tiling); Wq fp32 or bf16. */
+int coset_d4_qat_fwd(const float* W, int64_t rows, int64_t cols, const float* beta, int64_t blocks_per_tile,
+                     float clip, void* Wq, int wq_dtype, void* stream);
+
+/* Same with beta derived from theta and the EMA buffers as in
+ * coset_e8_qat_fwd_theta (q and M_bounds give the bounds' q^M), writing the
+ * beta used, d beta / d theta and incrementing step_counter (nullables). */
+int coset_d4_qat_fwd_theta(const float* W, int64_t rows, int64_t cols, int64_t blocks_per_tile, const float* theta,
+                           const float* sigma_ema, const float* xmax_ema, double delta0, double eta,
+                           double gamma_inv, int q, int M_bounds, float clip, void* Wq, int wq_dtype,
+                           float* beta_out, float* dbeta_dtheta_out, int64_t* step_counter, void* stream);
+
+/* Backward of either forward (P recomputed from W and beta):
+ *   dW = ((g m) / beta) beta, m = (-clip <= P/beta <= clip),
+ *   dbeta[t] = sum_t ((g m) / beta) W - (g m) ((P / beta) / beta),
+ * and with dbeta_dtheta non-NULL dtheta[t] = dbeta[t] * dbeta_dtheta[t]. */
+int coset_d4_qat_bwd(const void* gWq, int g_dtype, const float* W, const float* beta, const float* dbeta_dtheta,
+                     int64_t rows, int64_t cols, int64_t blocks_per_tile, float clip, float* dW, float* dbeta,
+                     float* dtheta, void* stream);
+
 /* LSQ activation quantizer forward (LSQActivation.forward with ste_clip and
  * ste_round, coset/core/layers.py:117-137, 20-26), over n values of x
  * (COSET_F32, COSET_BF16 or COSET_F16), computed in fp32 in the reference's

@@ -18,6 +18,8 @@
  *   _full_decode        coset/core/e8/codecs.py:139-180
  *   layer quantization  coset/core/layers.py:428-463
  *   one-sided vLUT      coset/legacy/quant/vlut.py:72-156, 217-238
+ *   D4 g_x / projection coset/core/d4/lattice.py:62-146
+ *   D4 layer quantizer  coset/core/d4/layers.py:46-47 with layers.py:428-463
  */
 #include "e8_oracle.h"
 
@@ -388,6 +390,91 @@ void or_legacy_decode(const int32_t* codes, const int32_t* T, int64_t n, float b
             float v = acc[i];
             if (dither) v = v - dither[dither_stride * b + i];
             out[8 * b + i] = (beta * v) * scale_T[T[b]];
+        }
+    }
+}
+
+/* ------------------------------------------------------------------ D4 */
+
+/* D4 g_x (coset/core/d4/lattice.py:62-111): the first coordinate farthest
+ * from its rounding moves +1 when x_k >= 0 and f_k < x_k, -1 otherwise. */
+void or_d4_g_x(const float* x, float* out)
+{
+    float f[4], delta[4];
+    for (int i = 0; i < 4; ++i) {
+        f[i] = or_custom_round(x[i]);
+        delta[i] = fabsf(x[i] - f[i]);
+    }
+    int k = 0;
+    for (int i = 1; i < 4; ++i)
+        if (delta[i] > delta[k]) k = i;
+    memcpy(out, f, sizeof f);
+    out[k] = (x[k] >= 0.f && f[k] < x[k]) ? f[k] + 1.f : f[k] - 1.f;
+}
+
+/* D4 projection (lattice.py:113-146): custom_round(x) when torch.sum of it
+ * % 2 == 0, else g_x(x). */
+void or_d4_projection(const float* x, int64_t n, float* y)
+{
+    for (int64_t i = 0; i < n; ++i) {
+        const float* xi = x + 4 * i;
+        float f[4], s = 0.f;
+        for (int j = 0; j < 4; ++j) {
+            f[j] = or_custom_round(xi[j]);
+            s += f[j];
+        }
+        float r = s - 2.f * floorf(s / 2.f); /* torch.remainder(s, 2) */
+        if (r == 0.f)
+            memcpy(y + 4 * i, f, sizeof f);
+        else
+            or_d4_g_x(xi, y + 4 * i);
+    }
+}
+
+/* Exact inverse of the D4 generator (columns (-1,-1,0,0), (1,-1,0,0),
+ * (0,1,-1,0), (0,0,1,-1)). */
+static const double D4GINV[4][4] = {
+    {-0.5, -0.5, -0.5, -0.5}, {0.5, -0.5, -0.5, -0.5}, {0., 0., -1., -1.}, {0., 0., 0., -1.}};
+
+/* round(G^-1 y) mod q (coset/core/base.py:134-154) from the exact product. */
+void or_d4_encode_coords(const float* y, int64_t n, int q, int32_t* b)
+{
+    for (int64_t i = 0; i < n; ++i)
+        for (int r = 0; r < 4; ++r) {
+            double c = 0.0;
+            for (int j = 0; j < 4; ++j) c += D4GINV[r][j] * (double)y[4 * i + j];
+            b[4 * i + r] = pymod_int(nearbyint(c), q);
+        }
+}
+
+/* G b (coset/core/base.py:156-176). */
+void or_d4_decode_coords(const int32_t* b, int64_t n, float* y)
+{
+    for (int64_t i = 0; i < n; ++i) {
+        const int32_t* c = b + 4 * i;
+        y[4 * i + 0] = (float)(-c[0] + c[1]);
+        y[4 * i + 1] = (float)(-c[0] - c[1] + c[2]);
+        y[4 * i + 2] = (float)(-c[2] + c[3]);
+        y[4 * i + 3] = (float)(-c[3]);
+    }
+}
+
+/* The D4 layer's weight quantization (layers.py:428-463 with d4_quantize):
+ * Wq = clamp(P(W * beta_t) / beta_t, -clip, clip), beta_t per tile of
+ * blocks_per_tile 4-wide blocks. */
+void or_d4_layer_quant(const float* W, int64_t rows, int64_t cols, const float* beta, int64_t blocks_per_tile,
+                       float clip, float* Wq)
+{
+    const int64_t n = rows * (cols / 4);
+    for (int64_t blk = 0; blk < n; ++blk) {
+        const float bt = beta[blk / blocks_per_tile];
+        float x[4], p[4];
+        for (int j = 0; j < 4; ++j) x[j] = W[4 * blk + j] * bt;
+        or_d4_projection(x, 1, p);
+        for (int j = 0; j < 4; ++j) {
+            float v = p[j] / bt;
+            if (v == v) v = v < -clip ? -clip : (v > clip ? clip : v);
+            Wq[4 * blk + j] = v;
         }
     }
 }

@@ -94,6 +94,14 @@ void or_legacy_encode(const float* x, int64_t n, float beta, float two_alpha, in
 void or_legacy_decode(const int32_t* codes, const int32_t* T, int64_t n, float beta, const float* scale_T,
                       const float* dither, int64_t dither_stride, int q, int M, float* out);
 
+/* D4 (coset/core/d4/lattice.py:62-146, d4/layers.py:46-47). */
+void or_d4_g_x(const float* x, float* out);
+void or_d4_projection(const float* x, int64_t n, float* y);
+void or_d4_encode_coords(const float* y, int64_t n, int q, int32_t* b);
+void or_d4_decode_coords(const int32_t* b, int64_t n, float* y);
+void or_d4_layer_quant(const float* W, int64_t rows, int64_t cols, const float* beta, int64_t blocks_per_tile,
+                       float clip, float* Wq);
+
 #ifdef __cplusplus
 }
 #endif

@@ -61,6 +61,11 @@ def lib():
                                        _i32p, _i32p, _u8p]
         L.or_legacy_decode.argtypes = [_i32p, _i32p, _i64, _flt, _f32p, ctypes.c_void_p, _i64, _int, _int,
                                        _f32p]
+        L.or_d4_g_x.argtypes = [_f32p, _f32p]
+        L.or_d4_projection.argtypes = [_f32p, _i64, _f32p]
+        L.or_d4_encode_coords.argtypes = [_f32p, _i64, _int, _i32p]
+        L.or_d4_decode_coords.argtypes = [_i32p, _i64, _f32p]
+        L.or_d4_layer_quant.argtypes = [_f32p, _i64, _i64, _f32p, _i64, _flt, _f32p]
         _lib = L
     return _lib
 
@@ -267,3 +272,47 @@ def legacy_decode(codes, T, q, M, beta, alpha=1.0, dither=None):
     lib().or_legacy_decode(codes, T, n, float(np.float32(beta)), legacy_scale_table(alpha),
                            None if d is None else d.ctypes.data, stride, int(q), int(M), out)
     return out
+
+
+# ---------------------------------------------------------------- D4
+
+def d4_g_x(x):
+    """coset/core/d4/lattice.py:62-111 on [N, 4] rows."""
+    x = _f32(x).reshape(-1, 4)
+    out = np.empty_like(x)
+    for i in range(x.shape[0]):
+        row = np.empty(4, np.float32)
+        lib().or_d4_g_x(np.ascontiguousarray(x[i]), row)
+        out[i] = row
+    return out
+
+
+def d4_projection(x):
+    """coset/core/d4/lattice.py:113-146 on [N, 4] rows."""
+    x = _f32(x).reshape(-1, 4)
+    y = np.empty_like(x)
+    lib().or_d4_projection(x, x.shape[0], y)
+    return y
+
+
+def d4_encode_coords(y, q):
+    y = _f32(y).reshape(-1, 4)
+    b = np.empty(y.shape, np.int32)
+    lib().or_d4_encode_coords(y, y.shape[0], int(q), b)
+    return b
+
+
+def d4_decode_coords(b):
+    b = np.ascontiguousarray(b, dtype=np.int32).reshape(-1, 4)
+    y = np.empty(b.shape, np.float32)
+    lib().or_d4_decode_coords(b, b.shape[0], y)
+    return y
+
+
+def d4_layer_quant(W, beta, blocks_per_tile, clip):
+    """coset/core/layers.py:428-463 with the D4 quantizer (d4/layers.py:46-47)."""
+    W = _f32(W)
+    rows, cols = W.shape
+    Wq = np.empty_like(W)
+    lib().or_d4_layer_quant(W, rows, cols, _f32(beta).reshape(-1), int(blocks_per_tile), float(clip), Wq)
+    return Wq

@@ -1,0 +1,142 @@
+"""D4 variant on the GPU: coset_d4_lattice_op and the D4 layer's fused
+weight quantizer (coset_d4_qat_fwd / _fwd_theta / _bwd) against the oracle
+(tests/test_oracle_d4.py pins it) and against torch autograd of the
+reference composition (coset/core/layers.py:428-463 with d4_quantize)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _x(n, seed):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((n, 4)) * 3).astype(np.float32)
+    x[: n // 8] = np.round(x[: n // 8] * 4) / 4                 # ties of rounding and argmax
+    x[n // 8: n // 8 + 64] = rng.choice(np.array([0.5, -0.5, 1.5, -1.5, 0.0, -0.0, 1e-30, 2.0 ** 23 + 1, -(2.0 ** 23) - 3,
+                                                  2.5e7, -7.5], np.float32), size=(64, 4))
+    return x
+
+
+def test_lattice_ops_match_oracle():
+    import coset_amd as ca
+    lat = ca.D4Lattice()
+    x = _x(20000, 1)
+    xt = torch.from_numpy(x).cuda()
+    assert np.array_equal(lat.projection(xt).cpu().numpy().view(np.int32), orc.d4_projection(x).view(np.int32))
+    assert np.array_equal(lat.g_x(xt).cpu().numpy(), orc.d4_g_x(x))
+    y = orc.d4_projection(x[:5000] / 64)    # small lattice points
+    for q in (2, 3, 4, 7):
+        b = lat.encode_coords(torch.from_numpy(y).cuda(), q).cpu().numpy()
+        assert np.array_equal(b, orc.d4_encode_coords(y, q).astype(np.float32))
+        assert np.array_equal(lat.decode_coords(torch.from_numpy(b).cuda(), q).cpu().numpy(),
+                              orc.d4_decode_coords(b.astype(np.int32)))
+    one = lat.projection(torch.tensor([0.6, 0.6, 0.2, -0.1], device="cuda"))    # single-vector form
+    assert one.shape == (4,)
+
+
+@pytest.mark.parametrize("tiling", ["row", "block"])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_qat_forward_matches_oracle(tiling, out_dtype):
+    from coset_amd import _lib
+    rng = np.random.default_rng(2)
+    rows, cols = 24, 64
+    W = (rng.standard_normal((rows, cols)) * 0.7).astype(np.float32)
+    bpt = cols // 4 if tiling == "row" else 1
+    beta = (rng.random(rows * cols // 4 // bpt) * 3 + 0.5).astype(np.float32)
+    Wg = torch.from_numpy(W).cuda()
+    bg = torch.from_numpy(beta).cuda()
+    Wq = torch.empty((rows, cols), dtype=out_dtype, device="cuda")
+    _lib.call("coset_d4_qat_fwd", Wg.data_ptr(), rows, cols, bg.data_ptr(), bpt, 2.0, Wq.data_ptr(),
+              _lib.dtype_code(out_dtype), _lib.stream_of(Wg))
+    want = torch.from_numpy(orc.d4_layer_quant(W, beta, bpt, 2.0)).to(out_dtype)
+    assert torch.equal(Wq.cpu(), want)
+
+
+class _STE(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, p):
+        return p
+
+    @staticmethod
+    def backward(ctx, g):
+        return g, None
+
+
+@pytest.mark.parametrize("tiling", ["row", "block"])
+def test_qat_backward_matches_autograd(tiling):
+    """dW bit for bit and dbeta to summation order against torch autograd of
+    the reference composition on the CPU (STE identity backward)."""
+    from coset_amd import _lib
+    rng = np.random.default_rng(3)
+    rows, cols, clip = 16, 48, 1.0
+    W = (rng.standard_normal((rows, cols)) * 0.8).astype(np.float32)
+    bpt = cols // 4 if tiling == "row" else 1
+    nt = rows * cols // 4 // bpt
+    beta = (rng.random(nt) * 2 + 0.5).astype(np.float32)
+    g = rng.standard_normal((rows, cols)).astype(np.float32)
+
+    Wt = torch.from_numpy(W).requires_grad_(True)
+    bt = torch.from_numpy(beta).requires_grad_(True)
+    bfull = bt.view(-1, 1) if tiling == "row" else bt.view(rows, cols // 4, 1)
+    Ws = Wt * bfull if tiling == "row" else (Wt.view(rows, cols // 4, 4) * bfull).reshape(rows, cols)
+    P = torch.from_numpy(orc.d4_projection(Ws.detach().numpy()).reshape(rows, cols))
+    Q = _STE.apply(Ws, P)
+    den = bfull if tiling == "row" else bt.view(rows, cols // 4).repeat_interleave(4, dim=1)
+    out = torch.clamp(Q / den, -clip, clip)
+    out.backward(torch.from_numpy(g))
+
+    dW = torch.empty((rows, cols), device="cuda")
+    dbeta = torch.empty(nt, device="cuda")
+    gg, Wg, bg = (torch.from_numpy(a).cuda() for a in (g, W, beta))
+    _lib.call("coset_d4_qat_bwd", gg.data_ptr(), _lib.dtype_code(gg.dtype), Wg.data_ptr(), bg.data_ptr(), None,
+              rows, cols, bpt, clip, dW.data_ptr(), dbeta.data_ptr(), None, _lib.stream_of(gg))
+    assert torch.equal(dW.cpu(), Wt.grad)
+    np.testing.assert_allclose(dbeta.cpu().numpy(), bt.grad.numpy(), rtol=2e-5, atol=2e-5)
+
+
+@pytest.mark.parametrize("tiling", ["row", "block"])
+def test_d4_layer_fused_matches_torch_composition(tiling):
+    """create_d4_hnlq_linear takes the fused D4 path; its W_q and gradients
+    agree with the reference composition driven by torch's beta (in-kernel
+    beta equals it to ulp level, as on the E8 path)."""
+    import coset_amd as ca
+    torch.manual_seed(5)
+    layer = ca.create_d4_hnlq_linear(64, 24, tiling=tiling)
+    assert layer._fused_d4() and layer.block_size == 4 and layer.q == 4 and layer.M == 2
+    assert abs(layer.Delta0 - 2 * 0.95 * (1 / np.sqrt(2)) / 15) < 1e-12
+    assert float(layer.gamma_inv) == 2.0
+    with torch.no_grad():
+        layer.theta_beta.uniform_(-3, 3)
+        layer.sigma_ema.uniform_(0.5, 2.0)
+        layer.xmax_ema.uniform_(1.0, 4.0)
+    Wq = layer._quantize_weights()
+    g = torch.randn_like(Wq)
+    (Wq * g).sum().backward()
+    dtheta, dW = layer.theta_beta.grad.clone(), layer.weight.grad.clone()
+    layer.zero_grad()
+    Wq2 = layer._reference_composition(layer.weight, layer._beta())
+    (Wq2 * g).sum().backward()
+    assert (Wq != Wq2).float().mean().item() < 1e-3
+    torch.testing.assert_close(dW, layer.weight.grad, rtol=1e-6, atol=1e-6)
+    torch.testing.assert_close(dtheta, layer.theta_beta.grad, rtol=1e-5, atol=1e-5)
+    assert int(layer.step_count) == 1
+
+
+def test_d4_layer_trains():
+    import coset_amd as ca
+    torch.manual_seed(1)
+    layer = ca.create_d4_hnlq_linear(128, 32, quantize_activations=True)
+    opt = torch.optim.SGD(layer.parameters(), lr=1e-2)
+    x = torch.randn(64, 128, device="cuda")
+    target = torch.randn(64, 32, device="cuda")
+    for _ in range(3):
+        opt.zero_grad()
+        loss = torch.nn.functional.mse_loss(layer(x), target)
+        loss.backward()
+        opt.step()
+    assert torch.isfinite(loss) and int(layer.step_count) == 3
+    with pytest.raises(ValueError):
+        ca.create_d4_hnlq_linear(10, 4)
