@@ -548,7 +548,7 @@ int coset_lsq_bwd(const void* x, const void* g, int dtype, int64_t n, const floa
 
 int64_t coset_vlut_prepared_words(int64_t rows, int64_t kb, int M, int word_format)
 {
-    if (rows < 0 || kb < 0 || M < 1 || word_format < 0 || word_format > 2) return 0;
+    if (rows < 0 || kb < 0 || M < 1 || word_format < 0 || word_format > 3) return 0;
     return coset::vlut_prepared_words(rows, kb, M, word_format);
 }
 
@@ -558,7 +558,9 @@ int coset_vlut_prepare(const void* words, int64_t rows, int64_t kb, int M, int q
     if (q != 2 && q != 4) return fail(COSET_EUNSUPPORTED, "vLUT prepare supports q = 2 or 4 (got %d)", q);
     if (rows < 0 || kb < 0 || M < 1 || M > 4) return fail(COSET_EINVAL, "bad shape rows=%lld kb=%lld M=%d",
                                                          (long long)rows, (long long)kb, M);
-    if (word_format != 1 && word_format != 2) return fail(COSET_EINVAL, "prepared word_format must be 1 or 2");
+    if (word_format < 1 || word_format > 3) return fail(COSET_EINVAL, "prepared word_format must be 1, 2 or 3");
+    if (word_format == 3 && !((q == 4 && M <= 2) || (q == 2 && M <= 4)))
+        return fail(COSET_EUNSUPPORTED, "decoded format needs |2 x_hat| <= 127: q = 4 with M <= 2 or q = 2 with M <= 4");
     if (rows * kb > 0 && (!words || !prepared)) return fail(COSET_EINVAL, "NULL buffer");
     if (!aligned(prepared, 16)) return fail(COSET_EINVAL, "prepared must be 16-byte aligned");
     return check_hip(coset::vlut_prepare((const uint16_t*)words, rows, kb, M, q, legacy ? 1 : 0, word_format, prepared,
@@ -592,7 +594,9 @@ static int vlut_matmul_impl(const void* words, int word_format, const float* sca
         return fail(COSET_EINVAL, "workspace holds %lld floats, needs %lld", (long long)workspace_floats,
                     (long long)need);
     if (need > 0 && !workspace) return fail(COSET_EINVAL, "NULL workspace");
-    if (word_format < 0 || word_format > 2) return fail(COSET_EINVAL, "word_format must be 0, 1 or 2");
+    if (word_format < 0 || word_format > 3) return fail(COSET_EINVAL, "word_format must be 0, 1, 2 or 3");
+    if (word_format == 3 && plan.kernel != coset::VK_MFMA_ROWS)
+        return fail(COSET_EUNSUPPORTED, "the decoded format runs on the matrix-core rows kernel only (fp16/bf16 activations)");
     if (word_format != 0 && !aligned(words, 16)) return fail(COSET_EINVAL, "prepared words must be 16-byte aligned");
     coset::VlutMatmulArgs p{};
     p.words = words;

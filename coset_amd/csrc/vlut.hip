@@ -496,12 +496,16 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
 constexpr int kRowsWaves = 8;
 
-template <int Q, int M>
+template <int Q, int M, int WN>
 __device__ __forceinline__ void load_pair(const VlutMatmulArgs& p, int fmt, int64_t row, int64_t kb, int64_t kb_total,
-                                          uint32_t w[M])
+                                          uint32_t w[WN])
 {
     const int64_t i0 = vlut_word_index(fmt, row, kb, 0, kb_total, M);
-    if (fmt == VLUT_RAW) {
+    if (fmt == VLUT_DECODED) {
+        const uint2 v = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint32_t*>(p.words) + i0);
+        w[0] = v.x;
+        w[1 % WN] = v.y;
+    } else if (fmt == VLUT_RAW) {
         const uint16_t* src = reinterpret_cast<const uint16_t*>(p.words) + i0;
         constexpr uint32_t kMask = Q == 2 ? 0xffu : 0xffffu;  // q^8 - 1: map bounds for any input
 #pragma unroll
@@ -528,6 +532,32 @@ __device__ __forceinline__ void load_pair(const VlutMatmulArgs& p, int fmt, int6
     }
 }
 
+// Eight biased bytes (x0: coordinates 0-3, x1: 4-7) minus the bias as 8
+// halves (fp16) or bf16 values, exact.
+template <bool BF16>
+__device__ __forceinline__ uint4 bytes_to_operand(uint32_t x0, uint32_t x1, _Float16 f16_off, float f32_off)
+{
+    uint32_t hv[4];
+    if (BF16) {
+        float f[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            f[j] = (float)((x0 >> (8 * j)) & 0xffu) - f32_off;
+            f[4 + j] = (float)((x1 >> (8 * j)) & 0xffu) - f32_off;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            hv[j] = __builtin_amdgcn_perm(__float_as_uint(f[2 * j + 1]), __float_as_uint(f[2 * j]), 0x07060302u);
+    } else {
+        const uint32_t raw[4] = {bytes_to_f16_bits(x0, false), bytes_to_f16_bits(x0, true),
+                                 bytes_to_f16_bits(x1, false), bytes_to_f16_bits(x1, true)};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            hv[j] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, raw[j]) - (half2_t){f16_off, f16_off});
+    }
+    return make_uint4(hv[0], hv[1], hv[2], hv[3]);
+}
+
 // 2 x_hat of one pair as 8 halves (fp16) or bf16 values, exact.
 template <int Q, int M, bool BF16>
 __device__ __forceinline__ uint4 decode_pair_swar(const uint64_t* s_tab, const uint32_t w[M], _Float16 f16_off,
@@ -548,25 +578,7 @@ __device__ __forceinline__ uint4 decode_pair_swar(const uint64_t* s_tab, const u
         x0 = x0 * Q + l0;
         x1 = x1 * Q + l1;
     }
-    uint32_t hv[4];
-    if (BF16) {
-        float f[8];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            f[j] = (float)((x0 >> (8 * j)) & 0xffu) - f32_off;
-            f[4 + j] = (float)((x1 >> (8 * j)) & 0xffu) - f32_off;
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            hv[j] = __builtin_amdgcn_perm(__float_as_uint(f[2 * j + 1]), __float_as_uint(f[2 * j]), 0x07060302u);
-    } else {
-        const uint32_t raw[4] = {bytes_to_f16_bits(x0, false), bytes_to_f16_bits(x0, true),
-                                 bytes_to_f16_bits(x1, false), bytes_to_f16_bits(x1, true)};
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            hv[j] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, raw[j]) - (half2_t){f16_off, f16_off});
-    }
-    return make_uint4(hv[0], hv[1], hv[2], hv[3]);
+    return bytes_to_operand<BF16>(x0, x1, f16_off, f32_off);
 }
 
 // Output epilogue: + bias[o], then the LSQ activation quantizer (fp32, the
@@ -600,11 +612,13 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulAr
     const int64_t row = r0 + (lane & 15);
     const int64_t t_base = (int64_t)blockIdx.z * 16 * NTILE;
     const uint16_t* act = reinterpret_cast<const uint16_t*>(p.act);
-    const _Float16 f16_off = (_Float16)(1024 + p.swar_bias);
-    const float f32_off = (float)p.swar_bias;
+    const int bias = FMT == VLUT_DECODED ? kVlutDecodedBias : p.swar_bias;
+    const _Float16 f16_off = (_Float16)(1024 + bias);
+    const float f32_off = (float)bias;
+    constexpr int WN = FMT == VLUT_DECODED ? 2 : M;  // uint32 per pair
 
     struct Chunk {
-        uint32_t w[CH][M];
+        uint32_t w[CH][WN];
         uint4 a[CH][NTILE];
     };
     auto load = [&](int64_t c0, Chunk& ck) {
@@ -614,8 +628,9 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulAr
             const int64_t kb = 4 * kq + g;
             const bool kb_ok = kq < w1 && kb < kb_total;
 #pragma unroll
-            for (int m = 0; m < M; ++m) ck.w[st][m] = 0u;
-            if (kb_ok && (FMT == VLUT_TILED || row < p.rows)) load_pair<Q, M>(p, FMT, row, kb, kb_total, ck.w[st]);
+            for (int m = 0; m < WN; ++m) ck.w[st][m] = 0u;
+            if (kb_ok && (FMT == VLUT_TILED || FMT == VLUT_DECODED || row < p.rows))
+                load_pair<Q, M, WN>(p, FMT, row, kb, kb_total, ck.w[st]);
 #pragma unroll
             for (int s = 0; s < NTILE; ++s) {
                 const int64_t tok = t_base + 16 * s + (lane & 15);
@@ -630,7 +645,11 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulAr
     auto run = [&](const Chunk& ck) {
 #pragma unroll
         for (int st = 0; st < CH; ++st) {
-            const uint4 bw = decode_pair_swar<Q, M, BF16>(s_tab, ck.w[st], f16_off, f32_off);
+            uint4 bw;
+            if constexpr (FMT == VLUT_DECODED)
+                bw = bytes_to_operand<BF16>(ck.w[st][0], ck.w[st][1 % WN], f16_off, f32_off);
+            else
+                bw = decode_pair_swar<Q, M, BF16>(s_tab, ck.w[st], f16_off, f32_off);
 #pragma unroll
             for (int s = 0; s < NTILE; ++s) {
                 if (BF16)
@@ -647,8 +666,10 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulAr
     int64_t c0 = w0;
     if (c0 < w1) load(c0, c_a);
     // the tables are staged while the first chunk's loads are in flight
-    for (int i = threadIdx.x; i < 512 + p.n_coarse; i += blockDim.x) s_tab[i] = p.swar[i];
-    __syncthreads();
+    if constexpr (FMT != VLUT_DECODED) {
+        for (int i = threadIdx.x; i < 512 + p.n_coarse; i += blockDim.x) s_tab[i] = p.swar[i];
+        __syncthreads();
+    }
     for (; c0 < w1; c0 += 2 * CH) {
         const int64_t c1 = c0 + CH;
         if (c1 < w1) load(c1, c_b);
@@ -841,6 +862,42 @@ VlutPlan vlut_plan(int64_t rows, int64_t B, int64_t K, int q, int M, int method)
     return {VK_MFMA_TILE, (int)std::max<int64_t>(1, std::min<int64_t>(std::max(splits, min_splits), max_splits))};
 }
 
+// One tile entry (pair) per thread: 2 x_hat = sum_m q^m 2 r(b_m) with the
+// integer decode, stored as bytes + 128; padding pairs decode to 0.
+template <int Q>
+__global__ void __launch_bounds__(256) vlut_prepare_decoded_kernel(const uint16_t* words, int64_t rows,
+                                                                  int64_t kb_total, int M, int64_t n_pairs,
+                                                                  const uint16_t* map, const uint64_t* coarse,
+                                                                  uint32_t mask, uint32_t* out)
+{
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n_pairs) return;
+    const int lane = (int)(e & 63);
+    const int64_t tile = e >> 6;
+    const int64_t kq = (kb_total + 3) / 4;
+    const int64_t row = (tile / kq) * 16 + (lane & 15);
+    const int64_t kb = (tile % kq) * 4 + (lane >> 4);
+    int acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (row < rows && kb < kb_total) {
+        int qm = 1;
+        for (int m = 0; m < M; ++m) {
+            int r2[8];
+            two_r_lut<Q>(words[(row * kb_total + kb) * M + m] & mask, map, coarse, r2);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[j] += qm * r2[j];
+            qm *= Q;
+        }
+    }
+    uint32_t lo = 0u, hi = 0u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        lo |= (uint32_t)(acc[j] + kVlutDecodedBias) << (8 * j);
+        hi |= (uint32_t)(acc[4 + j] + kVlutDecodedBias) << (8 * j);
+    }
+    out[2 * e] = lo;
+    out[2 * e + 1] = hi;
+}
+
 hipError_t vlut_prepare(const uint16_t* words, int64_t rows, int64_t kb, int M, int q, int legacy, int fmt,
                         uint32_t* prepared, hipStream_t s)
 {
@@ -849,6 +906,18 @@ hipError_t vlut_prepare(const uint16_t* words, int64_t rows, int64_t kb, int M, 
     const DecodeTables* t = nullptr;
     hipError_t e = get_decode_tables(q, legacy, &t);
     if (e != hipSuccess) return e;
+    if (fmt == VLUT_DECODED) {
+        if (M > t->swar_max_m || (q != 2 && q != 4)) return hipErrorInvalidValue;  // bytes would overflow
+        const int64_t pairs = n / 2;
+        const dim3 grid((unsigned)((pairs + 255) / 256)), block(256);
+        if (q == 4)
+            hipLaunchKernelGGL(vlut_prepare_decoded_kernel<4>, grid, block, 0, s, words, rows, kb, M, pairs,
+                               t->cid_map, t->coarse, t->n_codes - 1u, prepared);
+        else
+            hipLaunchKernelGGL(vlut_prepare_decoded_kernel<2>, grid, block, 0, s, words, rows, kb, M, pairs,
+                               t->cid_map, t->coarse, t->n_codes - 1u, prepared);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(vlut_prepare_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, words, rows, kb, M, fmt,
                        n, t->cid_map, t->n_codes - 1u, prepared);
     return hipGetLastError();
@@ -863,6 +932,7 @@ void launch_rows_fmt(const VlutMatmulArgs& p, int splits, hipStream_t s)
     switch (p.prepared) {
     case VLUT_RAW: hipLaunchKernelGGL((vlut_rows_kernel<Q, M, BF16, NTILE, VLUT_RAW>), grid, dim3(kRowsWaves * 64), 0, s, p); break;
     case VLUT_PREPARED: hipLaunchKernelGGL((vlut_rows_kernel<Q, M, BF16, NTILE, VLUT_PREPARED>), grid, dim3(kRowsWaves * 64), 0, s, p); break;
+    case VLUT_DECODED: hipLaunchKernelGGL((vlut_rows_kernel<Q, M, BF16, NTILE, VLUT_DECODED>), grid, dim3(kRowsWaves * 64), 0, s, p); break;
     default: hipLaunchKernelGGL((vlut_rows_kernel<Q, M, BF16, NTILE, VLUT_TILED>), grid, dim3(kRowsWaves * 64), 0, s, p); break;
     }
 }
@@ -916,6 +986,7 @@ hipError_t vlut_matmul(VlutMatmulArgs p, const VlutPlan& plan, hipStream_t s)
     p.swar = t->swar;
     p.swar_ok = p.M <= t->swar_max_m && g_vlut_swar;
     p.swar_bias = p.swar_ok ? t->swar_bias[p.M] : 0;
+    if (p.prepared == VLUT_DECODED && plan.kernel != VK_MFMA_ROWS) return hipErrorInvalidValue;
     if (plan.kernel == VK_MFMA_ROWS) {
         if (!p.swar_ok) return hipErrorInvalidValue;
         e = p.q == 4 ? dispatch_rows<4>(p, splits, s) : dispatch_rows<2>(p, splits, s);

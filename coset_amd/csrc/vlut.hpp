@@ -12,7 +12,11 @@ enum VlutMethod { VLUT_METHOD_AUTO = 0, VLUT_METHOD_LDS = 1, VLUT_METHOD_MFMA = 
 
 // Weight formats (include/coset_amd.h): raw uint16 words, row-major
 // prepared uint32 (cid << 16 | idx), tiled prepared (matrix-core fragments).
-enum VlutFormat { VLUT_RAW = 0, VLUT_PREPARED = 1, VLUT_TILED = 2 };
+// VLUT_DECODED: per (row, k-block) pair the 8 bytes 2 x_hat + 128 of its
+// M-level decode (exact for the byte-table formats, |2 x_hat| <= 127), in the
+// tiled fragment order; two uint32 per pair.
+enum VlutFormat { VLUT_RAW = 0, VLUT_PREPARED = 1, VLUT_TILED = 2, VLUT_DECODED = 3 };
+constexpr int kVlutDecodedBias = 128;
 
 struct VlutMatmulArgs {
     const void* words;   // [rows, K/8, M] (VLUT_RAW / VLUT_PREPARED) or tiles (VLUT_TILED)
@@ -46,17 +50,19 @@ extern int g_vlut_swar;
 extern int g_vlut_splits;
 
 // Index of level word m of (row, k-block kb) in a weight of format fmt.
+// (VLUT_DECODED: index of the pair's first uint32; m and M are ignored.)
 __host__ __device__ inline int64_t vlut_word_index(int fmt, int64_t row, int64_t kb, int m, int64_t kb_total, int M)
 {
-    if (fmt != VLUT_TILED) return (row * kb_total + kb) * M + m;
+    if (fmt != VLUT_TILED && fmt != VLUT_DECODED) return (row * kb_total + kb) * M + m;
     const int64_t kq = (kb_total + 3) / 4;
-    return ((((row >> 4) * kq + (kb >> 2)) * 64) + (row & 15) + 16 * (kb & 3)) * M + m;
+    const int64_t entry = (((row >> 4) * kq + (kb >> 2)) * 64) + (row & 15) + 16 * (kb & 3);
+    return fmt == VLUT_DECODED ? 2 * entry : entry * M + m;
 }
 
 __host__ __device__ inline int64_t vlut_prepared_words(int64_t rows, int64_t kb, int M, int fmt)
 {
-    if (fmt != VLUT_TILED) return rows * kb * M;
-    return ((rows + 15) / 16) * ((kb + 3) / 4) * 64 * M;
+    if (fmt != VLUT_TILED && fmt != VLUT_DECODED) return rows * kb * M;
+    return ((rows + 15) / 16) * ((kb + 3) / 4) * 64 * (fmt == VLUT_DECODED ? 2 : M);
 }
 
 // Launch plan of a matmul: kernel and K splits (splits > 1 needs a

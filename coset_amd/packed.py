@@ -82,7 +82,7 @@ def load_packed(path: str, device: Optional[torch.device] = None) -> "PackedLine
 
 class PackedLinear(nn.Module):
     """y = x @ (decode(words) / beta)^T + bias through the vLUT matmul, with
-    the words prepared once (tiled fragment order).  x: [..., in] fp16 or
+    the words prepared once (decoded to bytes in fragment order).  x: [..., in] fp16 or
     bf16 (fp32 is cast to bf16: 2 x_hat is exact in both) -> fp32."""
 
     def __init__(self, tensors: Dict[str, torch.Tensor], meta: Dict[str, object],
@@ -95,7 +95,9 @@ class PackedLinear(nn.Module):
         if words.shape != (self.out_features, self.in_features // 8, self.M):
             raise ValueError(f"words shape {tuple(words.shape)} does not match the metadata")
         self.words = words
-        self.prepared = vlut_prepare(words, self.q, legacy=False, layout="tiled")
+        # decoded once to 2 x_hat bytes where they fit (q = 4, M <= 2; q = 2, M <= 4), else cid | idx words
+        fits = (self.q == 4 and self.M <= 2) or (self.q == 2 and self.M <= 4)
+        self.prepared = vlut_prepare(words, self.q, legacy=False, layout="decoded" if fits else "tiled")
         self.register_buffer("beta", tensors["beta"].to(words.device).float())
         bias = tensors.get("bias")
         self.register_buffer("bias", None if bias is None else bias.to(words.device).float())

@@ -188,14 +188,15 @@ def vlut_dot(words: torch.Tensor, vlut: torch.Tensor, q: int) -> torch.Tensor:
 
 
 _METHODS = {"auto": 0, "lds": 1, "mfma": 2}
-_LAYOUTS = {"rowmajor": 1, "tiled": 2}
+_LAYOUTS = {"rowmajor": 1, "tiled": 2, "decoded": 3}
 
 
 @dataclass
 class PreparedWords:
     """Level words converted once for vlut_matmul (coset_vlut_prepare):
     uint32 cid << 16 | idx values, row-major or tiled in matrix-core fragment
-    order (16 rows x 4 k-blocks per 64-entry tile)."""
+    order (16 rows x 4 k-blocks per 64-entry tile), or ("decoded") the
+    pairs' 2 x_hat as biased bytes in the tiled order."""
     data: torch.Tensor
     rows: int
     kb: int
@@ -211,8 +212,10 @@ class PreparedWords:
 
 def vlut_prepare(words: torch.Tensor, q: int = 4, legacy: bool = False, layout: str = "tiled") -> PreparedWords:
     """uint16 level words [rows, K/8, M] -> PreparedWords, the weight format
-    vlut_matmul reads without table lookups.  Done once per weight; ``legacy``
-    fixes the residual rule the matmul will use."""
+    vlut_matmul reads without the coarse-id gather ("rowmajor", "tiled") or
+    without any table lookup ("decoded": 8 bytes per pair, q = 4 with M <= 2
+    or q = 2 with M <= 4, fp16/bf16 activations).  Done once per weight;
+    ``legacy`` fixes the residual rule the matmul will use."""
     w = on_gpu(words).contiguous()
     if w.dtype != torch.uint16 or w.dim() != 3:
         raise ValueError("vlut_prepare takes uint16 level words [rows, K/8, M] (q <= 4)")

@@ -200,9 +200,15 @@ int coset_vlut_lookup_dot(const void* words, int64_t n_blocks, int q, int M, con
  *      (row / 16) * ceil(kb_total / 4) + kb / 4, 64 entries per tile (entry
  *      row % 16 + 16 * (kb % 4)) of M words each; rows are padded to 16 and
  *      k-blocks to 4 with the word 0, which decodes to 0.
+ *   3  decoded: the same tile order with, per entry, the 8 bytes
+ *      2 x_hat + 128 of the pair's M-level decode (two uint32, coordinates
+ *      0-3 then 4-7; padding decodes to 0): the weight decoded once, at the
+ *      footprint of format 2 for M = 2, so the matmul reads no tables.
+ *      q = 4 with M <= 2 or q = 2 with M <= 4 (|2 x_hat| <= 127); matrix-core
+ *      method only.
  * coset_vlut_prepared_words gives the uint32 count of a format; prepare
- * (once per weight) converts format-0 words [rows, kb, M] into format 1 or 2
- * for the core rule (legacy = 0) or the legacy one. */
+ * (once per weight) converts format-0 words [rows, kb, M] into format 1, 2
+ * or 3 for the core rule (legacy = 0) or the legacy one. */
 int64_t coset_vlut_prepared_words(int64_t rows, int64_t kb, int M, int word_format);
 int coset_vlut_prepare(const void* words, int64_t rows, int64_t kb, int M, int q, int legacy, int word_format,
                        uint32_t* prepared, void* stream);

@@ -203,3 +203,37 @@ def test_c4_full_size_equals_decoded_product():
                 out = coset_amd.vlut_matmul(w, a, 4, scale=torch.full((4096,), 0.02), method=method)
                 err = (out - ref).abs().max().item()
                 assert err <= 1e-3 * ref.abs().max().item(), (B, method, type(w).__name__, err)
+
+
+@pytest.mark.parametrize("q,M", [(4, 2), (4, 1), (2, 3), (2, 4)])
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("B", [1, 8, 40, 64])
+def test_decoded_format_equals_tiled(q, M, dt, B):
+    """Format 3 (2 x_hat bytes decoded once) feeds the same MFMA operands as
+    the tiled cid|idx format, so the outputs are bit-equal; both equal the
+    dense product with the decoded weights to fp32 summation order."""
+    import coset_amd as ca
+    torch.manual_seed(11 + B)
+    rows, K = 72, 520                      # ragged: rows % 16 != 0, K/8 % 4 != 0
+    x = torch.randn(rows * K // 8, 8, device="cuda") * 1.5
+    words = ca.hnlq_encode(x, q, M, 1.0).reshape(rows, K // 8, M)
+    tiled = ca.vlut_prepare(words, q, layout="tiled")
+    dec = ca.vlut_prepare(words, q, layout="decoded")
+    a = torch.randn(B, K, device="cuda").to(dt)
+    scale = torch.rand(rows, device="cuda") + 0.5
+    y2 = ca.vlut_matmul(tiled, a, scale=scale)
+    y3 = ca.vlut_matmul(dec, a, scale=scale)
+    assert torch.equal(y2, y3)
+    W = ca.hnlq_decode(words.reshape(-1, M), q, M, None).reshape(rows, K) * scale.view(-1, 1)
+    ref = a.float() @ W.t()
+    assert (y3 - ref).abs().max().item() <= 1e-3 * max(1.0, ref.abs().max().item())
+
+
+def test_decoded_format_rejects_what_it_cannot_hold():
+    import coset_amd as ca
+    words = torch.zeros(16, 4, 3, dtype=torch.uint16, device="cuda")
+    with pytest.raises(Exception):
+        ca.vlut_prepare(words, 4, layout="decoded")      # q = 4, M = 3 overflows a byte
+    dec = ca.vlut_prepare(torch.zeros(16, 4, 2, dtype=torch.uint16, device="cuda"), 4, layout="decoded")
+    with pytest.raises(Exception):
+        ca.vlut_matmul(dec, torch.randn(2, 32, device="cuda"))   # fp32 activations: no matrix-core path
