@@ -28,6 +28,45 @@ struct LutShape {
 
 constexpr int kLutThreads = 1024;
 
+// Copies the decode tables to LDS: the map (n_map uint4) and the byte or
+// coarse table (n_tab uint64).  Each thread issues all its loads before any
+// LDS store (one round trip to L2, not one per element), and each workgroup
+// starts at its own offset so the CUs do not all request the same lines at
+// once.  blockDim.x == kLutThreads.
+template <int PM, int PT>
+__device__ __forceinline__ void stage_tables(const uint4* __restrict__ g_map, uint4* s_map, int n_map,
+                                             const uint64_t* __restrict__ g_tab, uint64_t* s_tab, int n_tab)
+{
+    // loads are unconditional (an index past the end reads the last element)
+    // so none of them waits behind a branch; only the stores are predicated
+    const unsigned salt = blockIdx.x * 2459u;
+    const int rm = n_map > 0 ? (int)(salt % (unsigned)n_map) : 0;
+    const int rt = n_tab > 0 ? (int)(salt % (unsigned)n_tab) : 0;
+    auto at = [](int i, int r, int n) {
+        if (i >= n) return n - 1;
+        const int j = i + r;
+        return j >= n ? j - n : j;
+    };
+    uint4 m[PM];
+    uint64_t t[PT];
+#pragma unroll
+    for (int k = 0; k < PM; ++k) m[k] = g_map[at(threadIdx.x + k * kLutThreads, rm, n_map)];
+    if (n_tab > 0) {
+#pragma unroll
+        for (int k = 0; k < PT; ++k) t[k] = g_tab[at(threadIdx.x + k * kLutThreads, rt, n_tab)];
+    }
+#pragma unroll
+    for (int k = 0; k < PM; ++k) {
+        const int i = threadIdx.x + k * kLutThreads;
+        if (i < n_map) s_map[at(i, rm, n_map)] = m[k];
+    }
+#pragma unroll
+    for (int k = 0; k < PT; ++k) {
+        const int i = threadIdx.x + k * kLutThreads;
+        if (i < n_tab) s_tab[at(i, rt, n_tab)] = t[k];
+    }
+}
+
 // SWAR: each level's 2r comes from three byte tables (tables.hpp) added as
 // two 32-bit words, levels are summed with shifts, and the bytes hold
 // 2 x_hat + swar_bias; otherwise 2r = 2Gb - q (2c) from the unpacked digits.
@@ -41,11 +80,10 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_lut_kernel(CodecArgs a, cons
     __shared__ uint64_t s_tab[SWAR ? 512 + kMaxCoarse : kMaxCoarse];
 
     if (MODE != MODE_ENCODE) {
-        const uint4* src = reinterpret_cast<const uint4*>(g_map);
-        uint4* dst = reinterpret_cast<uint4*>(s_map);
-        for (int i = threadIdx.x; i < NC / 8; i += blockDim.x) dst[i] = src[i];
-        const int n_tab = SWAR ? 512 + n_coarse : n_coarse;
-        for (int i = threadIdx.x; i < n_tab; i += blockDim.x) s_tab[i] = g_tab[i];
+        stage_tables<(NC / 8 + kLutThreads - 1) / kLutThreads,
+                     ((SWAR ? 512 : 0) + kMaxCoarse + kLutThreads - 1) / kLutThreads>(
+            reinterpret_cast<const uint4*>(g_map), reinterpret_cast<uint4*>(s_map), NC / 8, g_tab, s_tab,
+            SWAR ? 512 + n_coarse : n_coarse);
         __syncthreads();
     }
     const float half_bias = 0.5f * (float)swar_bias;
@@ -131,6 +169,10 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_lut_kernel(CodecArgs a, cons
                 if (m + 1 < M) {
 #pragma unroll
                     for (int j = 0; j < 8; ++j) xl[j] = div_q<Q>(xl[j], qf);
+                }
+                if (m + 1 < M) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) xl[j] = __fmul_rn(xl[j], 1.0f / (float)Q);  // exact: Q = 2^k
                 }
             } else {
                 word = (uint32_t)(pack >> (16 * m)) & (uint32_t)(NC - 1);  // table bounds for any input
@@ -252,10 +294,9 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
     __shared__ __align__(16) uint16_t s_map[NC];
     __shared__ uint64_t s_tab[512 + kMaxCoarse];
     if (MODE != MODE_ENCODE) {
-        const uint4* src = reinterpret_cast<const uint4*>(g_map);
-        uint4* dst = reinterpret_cast<uint4*>(s_map);
-        for (int i = threadIdx.x; i < NC / 8; i += blockDim.x) dst[i] = src[i];
-        for (int i = threadIdx.x; i < 512 + n_coarse; i += blockDim.x) s_tab[i] = g_tab[i];
+        stage_tables<(NC / 8 + kLutThreads - 1) / kLutThreads, (512 + kMaxCoarse + kLutThreads - 1) / kLutThreads>(
+            reinterpret_cast<const uint4*>(g_map), reinterpret_cast<uint4*>(s_map), NC / 8, g_tab, s_tab,
+            512 + n_coarse);
         __syncthreads();
     }
     const float half_bias = 0.5f * (float)swar_bias;
@@ -308,10 +349,6 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
                     float4* cp = reinterpret_cast<float4*>(a.codes_f32 + ((size_t)i * M + m) * 8);
                     cp[0] = make_float4((float)b[0], (float)b[1], (float)b[2], (float)b[3]);
                     cp[1] = make_float4((float)b[4], (float)b[5], (float)b[6], (float)b[7]);
-                }
-                if (m + 1 < M) {
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) xl[j] = __fmul_rn(xl[j], 1.0f / (float)Q);  // exact: Q = 2^k
                 }
             } else {
                 word = (uint32_t)(pack >> (16 * m)) & (uint32_t)(NC - 1);  // table bounds for any input
