@@ -170,10 +170,6 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_lut_kernel(CodecArgs a, cons
 #pragma unroll
                     for (int j = 0; j < 8; ++j) xl[j] = div_q<Q>(xl[j], qf);
                 }
-                if (m + 1 < M) {
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) xl[j] = __fmul_rn(xl[j], 1.0f / (float)Q);  // exact: Q = 2^k
-                }
             } else {
                 word = (uint32_t)(pack >> (16 * m)) & (uint32_t)(NC - 1);  // table bounds for any input
                 unpack_word<Q>(word, Q, b);
@@ -349,6 +345,10 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
                     float4* cp = reinterpret_cast<float4*>(a.codes_f32 + ((size_t)i * M + m) * 8);
                     cp[0] = make_float4((float)b[0], (float)b[1], (float)b[2], (float)b[3]);
                     cp[1] = make_float4((float)b[4], (float)b[5], (float)b[6], (float)b[7]);
+                }
+                if (m + 1 < M) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) xl[j] = __fmul_rn(xl[j], 1.0f / (float)Q);  // exact: Q = 2^k
                 }
             } else {
                 word = (uint32_t)(pack >> (16 * m)) & (uint32_t)(NC - 1);  // table bounds for any input
