@@ -76,6 +76,7 @@ OPT_VLUT_DECODE = 2
 OPT_VLUT_SPLITS = 3
 OPT_FAST_PROJECTION = 4
 OPT_CODEC_PLAIN = 5
+OPT_CODEC_DYNAMIC = 6
 CODEC_AUTO, CODEC_GENERIC, CODEC_LUT = 0, 1, 2
 
 _lib = None
@@ -176,6 +177,12 @@ def set_codec_plain(enabled: bool) -> None:
     """The table kernel's fixed-format variant (fp32 in/out, beta = 2^k, no
     dither) where a call qualifies (default), or always the general one."""
     call("coset_set_option", OPT_CODEC_PLAIN, int(bool(enabled)))
+
+
+def set_codec_dynamic(enabled: bool) -> None:
+    """Fixed-format table kernel: tiles handed out by a per-stream counter
+    (default) or a static grid stride."""
+    call("coset_set_option", OPT_CODEC_DYNAMIC, int(bool(enabled)))
 
 
 def set_vlut_decode(byte_tables: bool) -> None:

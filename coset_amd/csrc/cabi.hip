@@ -98,6 +98,10 @@ int coset_set_option(int key, int value)
         if (value < 0 || value > 1) return fail(COSET_EINVAL, "codec plain %d not in {0,1}", value);
         coset::g_codec_plain = value;
         return COSET_OK;
+    case COSET_OPT_CODEC_DYNAMIC:
+        if (value < 0 || value > 1) return fail(COSET_EINVAL, "codec dynamic %d not in {0,1}", value);
+        coset::g_codec_dynamic = value;
+        return COSET_OK;
     case COSET_OPT_VLUT_SPLITS:
         if (value < 0) return fail(COSET_EINVAL, "vLUT splits %d < 0", value);
         coset::g_vlut_splits = value;

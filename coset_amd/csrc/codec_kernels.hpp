@@ -153,6 +153,7 @@ hipError_t launch_codec_lut(const CodecArgs& a, int mode, hipStream_t s);
 extern int g_codec_path;
 extern int g_fast_projection;  // 1 (default): encoders use the fast projection where it is exact
 extern int g_codec_plain;      // 1 (default): the table kernel's fixed-format variant where it applies
+extern int g_codec_dynamic;    // 1 (default): the fixed-format kernel takes its tiles from a counter
 constexpr int64_t kLutMinBlocks = 1 << 20;  // below it the table staging does not pay (layer-sized calls)
 
 // Backward of the QAT weight quantizer (qat.hip).

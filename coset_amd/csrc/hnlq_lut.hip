@@ -13,6 +13,9 @@
 // walks blocks with a grid stride, so HBM sees one contiguous read of x and
 // one write of the outputs.
 #include <algorithm>
+#include <map>
+#include <mutex>
+#include <utility>
 
 #include "codec_kernels.hpp"
 #include "tables.hpp"
@@ -20,6 +23,7 @@
 namespace coset {
 
 int g_codec_plain = 1;
+int g_codec_dynamic = 1;
 
 template <int Q>
 struct LutShape {
@@ -27,6 +31,26 @@ struct LutShape {
 };
 
 constexpr int kLutThreads = 1024;
+
+// Tile counters of the dynamic schedule: one pair per (device, stream) --
+// [0] hands out tiles, [1] counts finished workgroups, and the workgroup that
+// finishes last puts both back to zero, so every call starts from zero.
+// Calls on one stream run one after another and so never share a pair while
+// it counts.  Zero-initialised when the code object is loaded.
+constexpr int kTileSlots = 64;
+constexpr int kTileBlocks = 2;  // blocks per thread in a dynamic tile
+static __device__ __align__(256) unsigned g_tile_ctr[kTileSlots][2];
+
+// Workgroup barrier that orders LDS only: waits for this wave's LDS
+// operations, not for its loads and stores in flight (__syncthreads would
+// drain those too).
+__device__ __forceinline__ void lds_barrier()
+{
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt, expcnt unrestricted
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+}
 
 // Copies the decode tables to LDS: the map (n_map uint4) and the byte or
 // coarse table (n_tab uint64).  Each thread issues all its loads before any
@@ -284,11 +308,12 @@ __device__ __forceinline__ uint32_t encode_level_word(const float xl[8], bool in
 template <int Q, int M, int MODE, bool SCALED, bool CODES>
 __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, const uint16_t* __restrict__ g_map,
                                                               const uint64_t* __restrict__ g_tab, int n_coarse,
-                                                              int swar_bias)
+                                                              int swar_bias, unsigned* tiles)
 {
     constexpr int NC = LutShape<Q>::kCodes;
     __shared__ __align__(16) uint16_t s_map[NC];
     __shared__ uint64_t s_tab[512 + kMaxCoarse];
+    __shared__ unsigned s_tile[4];
     if (MODE != MODE_ENCODE) {
         stage_tables<(NC / 8 + kLutThreads - 1) / kLutThreads, (512 + kMaxCoarse + kLutThreads - 1) / kLutThreads>(
             reinterpret_cast<const uint4*>(g_map), reinterpret_cast<uint4*>(s_map), NC / 8, g_tab, s_tab,
@@ -367,7 +392,7 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
                 sw1 += l1 << (L * m);
             }
         }
-        if (MODE != MODE_DECODE && a.packed) {
+        if (MODE != MODE_DECODE) {
             uint16_t* pw = reinterpret_cast<uint16_t*>(a.packed) + (size_t)i * M;
             if (M == 1) {
                 pw[0] = (uint16_t)pack;
@@ -380,7 +405,7 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
                 for (int m = 0; m < M; ++m) pw[m] = (uint16_t)(pack >> (16 * m));
             }
         }
-        if (MODE == MODE_ENCODE || !a.out) return;
+        if (MODE == MODE_ENCODE) return;
         float o[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -393,22 +418,140 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
         p[1] = make_float4(o[4], o[5], o[6], o[7]);
     };
 
+    // Loads and stores share one in-order completion counter, so the wait
+    // before a body can leave the other register set's loads and the last
+    // body's stores in flight only if their number is the same on every path
+    // into it: the loads are unconditional (past the end they read block
+    // n - 1, n >= 1) and every store of a body is unconditional.
+    const int64_t last = n - 1;
+    In in0, in1;
+    if (tiles) {
+        // Dynamic schedule: tiles of kTileBlocks x kLutThreads consecutive
+        // blocks (kTileBlocks per thread, kLutThreads apart), taken from a
+        // counter two tiles ahead: thread 0 asks for the next one while the
+        // current tile is processed, one LDS barrier per tile.  In a last,
+        // partial tile the threads past the end redo block n - 1 and store the
+        // same values to it.
+        constexpr int KT = kTileBlocks;
+        static_assert(KT % 2 == 0 || KT == 1, "register sets alternate per block");
+        const int64_t ntiles = (n + KT * kLutThreads - 1) / (KT * kLutThreads);
+        auto blk = [&](int64_t t, int j) {
+            const int64_t b = (t * KT + j) * kLutThreads + threadIdx.x;
+            return b < n ? b : last;
+        };
+        // atomicInc (wrapping at 2^32 - 1, never reached) rather than
+        // atomicAdd: the compiler rewrites a uniform-address atomicAdd into a
+        // wave reduction that waits for the result at once
+        if (threadIdx.x == 0) {
+            s_tile[2] = atomicInc(tiles, ~0u);
+            s_tile[3] = atomicInc(tiles, ~0u);
+        }
+        lds_barrier();
+        const int64_t t0 = s_tile[2];
+        int64_t t1 = s_tile[3];
+        // one tile: each block step loads the next block into one register
+        // set and processes the current one from the other; the last step
+        // also asks for the tile after next and publishes the answer.  The
+        // first tile is peeled so the loop is entered as it is re-entered
+        // (one load pair, then one body's stores).
+        auto tile = [&](int64_t cur, int64_t nxt, In& s0, In& s1, int slot) {
+#pragma unroll
+            for (int j = 0; j < KT - 1; ++j) {
+                load(blk(cur, j + 1), j % 2 ? s0 : s1);
+                body(blk(cur, j), j % 2 ? s1 : s0);
+            }
+            In& now = (KT - 1) % 2 ? s1 : s0;
+            In& ahead = (KT - 1) % 2 ? s0 : s1;
+            unsigned grab = 0;
+            if (threadIdx.x == 0) grab = atomicInc(tiles, ~0u);
+            load(blk(nxt, 0), ahead);
+            body(blk(cur, KT - 1), now);
+            if (threadIdx.x == 0) s_tile[slot] = grab;
+            lds_barrier();
+            return (int64_t)s_tile[slot];
+        };
+        if (t0 < ntiles) {
+            load(blk(t0, 0), in0);
+            if constexpr (KT == 1) {
+                int64_t t2 = tile(t0, t1, in0, in1, 0);
+                while (t1 < ntiles) {
+                    const int64_t t3 = tile(t1, t2, in1, in0, 1);
+                    if (t2 >= ntiles) break;
+                    t1 = tile(t2, t3, in0, in1, 0);
+                    if (t3 >= ntiles) break;
+                    t2 = t1;
+                    t1 = t3;
+                }
+            } else {  // every tile starts in in0
+                int64_t t2 = tile(t0, t1, in0, in1, 0);
+                int slot = 1;
+                while (t1 < ntiles) {
+                    const int64_t t3 = tile(t1, t2, in0, in1, slot);
+                    slot ^= 1;
+                    t1 = t2;
+                    t2 = t3;
+                }
+            }
+        }
+        // every tile request of this workgroup has returned: count it done;
+        // the last one resets the pair for the next call on this stream
+        if (threadIdx.x == 0 && atomicAdd(tiles + 1, 1u) == gridDim.x - 1) {
+            atomicExch(tiles, 0u);
+            atomicExch(tiles + 1, 0u);
+        }
+        return;
+    }
+    // Static schedule (no counter pair free): a grid stride, the first body
+    // peeled so the loop is entered as it is re-entered, with one load pair
+    // followed by one body's stores.
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    In in0{}, in1{};
-    if (i < n) load(i, in0);
-    for (; i < n; i += 2 * stride) {
-        const int64_t i1 = i + stride;
-        if (i1 < n) load(i1, in1);
-        body(i, in0);
-        if (i1 >= n) break;
+    if (i >= n) return;
+    load(i, in0);
+    int64_t i1 = i + stride;
+    load(i1 < n ? i1 : last, in1);
+    body(i, in0);
+    while (i1 < n) {
         const int64_t i2 = i1 + stride;
-        if (i2 < n) load(i2, in0);
+        load(i2 < n ? i2 : last, in0);
         body(i1, in1);
+        if (i2 >= n) break;
+        i1 = i2 + stride;
+        load(i1 < n ? i1 : last, in1);
+        body(i2, in0);
     }
 }
 
 namespace {
+
+// The counter pair of the current device for stream s, or null when all
+// kTileSlots pairs of the device are taken (the kernels then use the
+// static schedule).
+unsigned* tile_counters(hipStream_t s)
+{
+    static std::mutex mu;
+    static std::map<std::pair<int, hipStream_t>, int> slot_of;
+    static unsigned* base[64] = {nullptr};
+    static int used[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!base[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_tile_ctr)) != hipSuccess || !p) return nullptr;
+        base[dev] = static_cast<unsigned*>(p);
+    }
+    auto it = slot_of.find({dev, s});
+    int slot;
+    if (it != slot_of.end()) {
+        slot = it->second;
+    } else {
+        if (used[dev] >= kTileSlots) return nullptr;
+        slot = used[dev]++;
+        slot_of[{dev, s}] = slot;
+    }
+    return base[dev] + 2 * slot;
+}
 
 int cu_count()
 {
@@ -432,8 +575,10 @@ hipError_t launch_plain(const CodecArgs& a, int grid, const uint16_t* map, const
     if constexpr (MODE == MODE_ENCODE || Q == 2 || M <= 2) {
         const bool scaled = a.scale_mode == SCALE_CODEC && a.beta != 1.f;
         const bool codes = MODE != MODE_DECODE && a.codes_f32;
+        unsigned* tiles = g_codec_dynamic ? tile_counters(s) : nullptr;
 #define COSET_PLAIN(SC, CO) \
-    hipLaunchKernelGGL((hnlq_plain_kernel<Q, M, MODE, SC, CO>), dim3(grid), dim3(kLutThreads), 0, s, a, map, sw, nc, bias)
+    hipLaunchKernelGGL((hnlq_plain_kernel<Q, M, MODE, SC, CO>), dim3(grid), dim3(kLutThreads), 0, s, a, map, sw, nc, bias, \
+                       tiles)
         if (scaled) {
             if (codes) COSET_PLAIN(true, true); else COSET_PLAIN(true, false);
         } else {
@@ -457,12 +602,13 @@ hipError_t launch_q(const CodecArgs& a, const DecodeTables* t, hipStream_t s)
     const int bias = swar ? t->swar_bias[a.M] : 0;
     // the plain kernel: fp32 in and out, no scale or a codec beta = 2^k, no
     // dither, no step counter, byte tables for the decode, and the encoder's
-    // fast projection on (it is a compile-time constant there)
+    // fast projection on (it is a compile-time constant there), and every
+    // output of the mode present (its stores are unconditional)
     const bool plain = (MODE == MODE_DECODE || (a.x_dtype == DT_F32 && a.fast_projection)) &&
                        (MODE == MODE_ENCODE || a.out_dtype == DT_F32) &&
                        (a.scale_mode == SCALE_NONE || (a.scale_mode == SCALE_CODEC && a.beta_is_pow2)) &&
                        !a.dither && !a.step_counter && (MODE == MODE_ENCODE || swar) &&
-                       g_codec_plain;
+                       (MODE == MODE_DECODE || a.packed) && (MODE == MODE_ENCODE || a.out) && g_codec_plain;
     if (plain) {
         const uint64_t* sw = t ? t->swar : nullptr;
         switch (a.M) {
