@@ -279,3 +279,43 @@ def test_roundtrip_with_float_codes(ca, path, beta):
     np.testing.assert_array_equal(host(codes).astype(np.int32), ref)
     np.testing.assert_array_equal(words(packed), O.pack_words(ref, 4))
     np.testing.assert_array_equal(host(out), O.e8_decode(ref, 4, 2, beta))
+
+
+def test_dynamic_schedule_matches_static(ca):
+    """The fixed-format table kernel's dynamic tile schedule (per-stream
+    counter pair, reset by the last workgroup) against its static grid
+    stride: partial last tiles, fewer tiles than workgroups, calls repeated
+    on one stream and interleaved over three streams, all three modes."""
+    from coset_amd import _lib
+    _lib.require_gpu()
+    rng = np.random.default_rng(31)
+    streams = [torch.cuda.current_stream(), torch.cuda.Stream(), torch.cuda.Stream()]
+    try:
+        _lib.set_codec_path(2)
+        for n in (1, 1000, 2047, 2049, 300001, (1 << 21) + 5):
+            x = dev(rng.standard_normal((n, 8)).astype(np.float32))
+            _lib.set_codec_dynamic(False)
+            pk_s, out_s = ca.hnlq_roundtrip(x, 4, 2, 1.0)
+            enc_s = ca.hnlq_encode(x, 2, 4, 1.0)
+            dec_s = ca.hnlq_decode(enc_s, 2, 4, 1.0)
+            _lib.set_codec_dynamic(True)
+            torch.cuda.synchronize()
+            for rep in range(3):
+                for s in streams:
+                    with torch.cuda.stream(s):
+                        pk, out = ca.hnlq_roundtrip(x, 4, 2, 1.0)
+                        enc = ca.hnlq_encode(x, 2, 4, 1.0)
+                        dec = ca.hnlq_decode(enc, 2, 4, 1.0)
+                    s.synchronize()
+                    assert torch.equal(pk.view(torch.int16), pk_s.view(torch.int16)), (n, rep)
+                    assert torch.equal(out, out_s), (n, rep)
+                    assert torch.equal(enc.view(torch.int16), enc_s.view(torch.int16)), (n, rep)
+                    assert torch.equal(dec, dec_s), (n, rep)
+            k = min(n, 4096)
+            xs = host(x[:k])
+            codes = O.e8_encode(xs, 4, 2)
+            np.testing.assert_array_equal(words(pk)[:k], O.pack_words(codes, 4))
+            np.testing.assert_array_equal(host(out[:k]), O.e8_decode(codes, 4, 2))
+    finally:
+        _lib.set_codec_dynamic(True)
+        _lib.set_codec_path(0)
