@@ -287,8 +287,10 @@ def bench_c5(torch, ca, args):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    # the GPU takes tens of milliseconds of sustained load to reach its
+    # steady clock: 200 untimed C2 steps are about 45 ms
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--cpu-sample", type=int, default=1 << 24,
                     help="C2 blocks timed on the host CPU oracle (0 skips it)")
     ap.add_argument("--only", default="c1,c2,c2codes,c3,c4,c5", help="comma list of workloads to run")

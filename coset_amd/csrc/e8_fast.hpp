@@ -17,15 +17,15 @@
 //       integer nearest to t = fl(x_i - 1/2), so custom_round(t) = rint(t) =
 //       floor(x_i): the D8 + 1/2 candidate rounds to f1 = floor(x), and
 //       d1 = t - f1 is again exact.
-//   (4) The two squared distances differ by more than 2^-14, evaluated as
-//       a = sum d0^2 and b = 2 - sum |d0| + sum d0^2 (+ 1 - 2 adj d_k for the
-//       flipped coordinate).  b is sum (1/2 - |d0|)^2, and 1/2 - |d0_i| =
-//       |x_i - f1_i - 1/2| as reals under (2).  These evaluations (within
-//       13 ulp(1) before the flip term) and the reference's rounded sums of
-//       rounded squares stay within 140 ulp(1) of the exact sums (all terms
-//       are below 5), and a gap of 2^-14 also keeps the correctly rounded
-//       square roots apart, so the reference's strict comparison has the
-//       same outcome.
+//   (4) The two squared distances a (D8) and b (D8 + 1/2) differ by more
+//       than 2^-14, with b - a evaluated as 2 - sum |d0| (+ |adj1| -
+//       2 adj1 e_k1 - |adj0| + 2 adj0 d0_k for the flipped coordinates):
+//       x_i - f1_i - 1/2 = d0_i -+ 1/2 as reals under (2) and (3), and
+//       (1/2 - |d0_i|)^2 - d0_i^2 = 1/4 - |d0_i|.  This evaluation (within
+//       12 ulp(1)) and the reference's rounded sums of rounded squares
+//       (within 140 ulp(1) of the exact sums, all terms are below 5) keep
+//       a gap of 2^-14 from reversing the reference's strict comparison, and
+//       the gap also keeps the correctly rounded square roots apart.
 // Under (2) and (3) floor x_i = rint x_i - [d0_i < 0] (d0_i = 0 fails (3)),
 // so the parity of sum floor x is that of sum rint x plus the number of
 // negative d0_i.
@@ -91,7 +91,7 @@ __host__ __device__ inline bool fast_in_range(const float x[8])
 __host__ __device__ inline bool fast_choose(const float x[8], FastChoice& c, bool in_range)
 {
     float d0[8], d1[8];
-    float best0 = 0.f, best1 = 0.f, s0, sa, a;
+    float best0 = 0.f, best1 = 0.f, s0, sa;
     uint32_t neg = 0u;  // sign bits of d0, xor-ed
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -105,15 +105,12 @@ __host__ __device__ inline bool fast_choose(const float x[8], FastChoice& c, boo
         if (i == 0) {
             s0 = c.f0[0];
             sa = fabsf(d0[0]);
-            a = d0[0] * d0[0];
         } else {
             s0 += c.f0[i];
             sa += fabsf(d0[i]);
-            a = fmaf(d0[i], d0[i], a);
         }
     }
     bool ok = in_range && best0 < kFastTieLimit && best1 < kFastTieLimit;
-    float b = (2.f - sa) + a;
 
     // first index of the largest |d| (torch.argmax)
     float xk0 = x[0], xk1 = x[0];
@@ -140,12 +137,12 @@ __host__ __device__ inline bool fast_choose(const float x[8], FastChoice& c, boo
     c.adj0 = odd0 ? ((xk0 >= 0.f && dk0 > 0.f) ? 1.f : -1.f) : 0.f;
     c.adj1 = odd1 ? ((tk1 >= 0.f && dk1 > 0.f) ? 1.f : -1.f) : 0.f;
 
-    // (d - adj)^2 = d^2 - 2 adj d + adj^2, adj^2 = |adj|
-    a += fmaf(-2.f * c.adj0, dk0, fabsf(c.adj0));
-    b += fmaf(-2.f * c.adj1, ek1, fabsf(c.adj1));
-    const bool pick0 = b - a > kFastDistGap;
+    // b - a, with (d - adj)^2 - d^2 = adj^2 - 2 adj d and adj^2 = |adj|
+    const float diff =
+        (2.f - sa) + (fmaf(-2.f * c.adj1, ek1, fabsf(c.adj1)) - fmaf(-2.f * c.adj0, dk0, fabsf(c.adj0)));
+    const bool pick0 = diff > kFastDistGap;
     c.pick0 = lanes_of(pick0);
-    return ok && (pick0 || a - b > kFastDistGap);
+    return ok && (pick0 || diff < -kFastDistGap);
 }
 
 // The chosen candidate's worst coordinate, as a lane mask.
