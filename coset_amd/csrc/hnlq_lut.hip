@@ -10,8 +10,10 @@
 // Launch: persistent grid, one 1024-thread workgroup per CU.  The q = 4 map
 // (65536 x uint16 = 128 KiB) plus the coarse points (<= 8 KiB) fill most of
 // the 160 KiB LDS of a gfx950 CU; every workgroup stages them once and then
-// walks blocks with a grid stride, so HBM sees one contiguous read of x and
-// one write of the outputs.
+// walks blocks: the general kernel with a grid stride, the fixed-format one
+// in tiles handed out by a per-stream counter (so workgroups that run ahead
+// take more tiles), and HBM sees one contiguous read of x and one write of
+// the outputs.
 #include <algorithm>
 #include <map>
 #include <mutex>
