@@ -261,10 +261,16 @@ __device__ __forceinline__ void residual_from_point(const float gb[8], float qf,
     float z[8], c[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) z[i] = div_q<Q>(gb[i], qf);
-    if constexpr (!LEGACY && Q > 0 && Q <= 32 && (Q & (Q - 1)) == 0)
+    if constexpr (!LEGACY && Q > 0 && Q <= 32 && (Q & (Q - 1)) == 0) {
         project_dyadic(z, c);
-    else
+        // q c and G b - q c are exact here (small dyadic values), so one
+        // fused operation gives the reference's two
+#pragma unroll
+        for (int i = 0; i < 8; ++i) r[i] = __fmaf_rn(-qf, c[i], gb[i]);
+        return;
+    } else {
         project<LEGACY, STRIDED>(z, c);
+    }
 #pragma unroll
     for (int i = 0; i < 8; ++i) r[i] = __fsub_rn(gb[i], __fmul_rn(qf, c[i]));
 }

@@ -218,37 +218,39 @@ __host__ __device__ inline float custom_round_hd(float x)
 // first-index argmax and the core g_x step are the reference's.
 __host__ __device__ inline void project_dyadic(const float x[8], float y[8])
 {
-    float f0[8], d0[8], t1[8], f1[8], d1[8];
-    float best0 = 0.f, best1 = 0.f, s0 = 0.f, s1 = 0.f, a = 0.f, b = 0.f;
+    float f0[8], d0[8], f1[8], d1[8];
+    float best0 = 0.f, best1 = 0.f, s0, s1, a, b;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         f0[i] = custom_round_hd(x[i]);
         d0[i] = x[i] - f0[i];
-        t1[i] = x[i] - 0.5f;
-        f1[i] = custom_round_hd(t1[i]);
-        d1[i] = t1[i] - f1[i];
+        const float t1 = x[i] - 0.5f;
+        f1[i] = custom_round_hd(t1);
+        d1[i] = t1 - f1[i];
         best0 = fmaxf(best0, fabsf(d0[i]));
         best1 = fmaxf(best1, fabsf(d1[i]));
-        s0 += f0[i];
-        s1 += f1[i];
-        a = fmaf(d0[i], d0[i], a);
-        b = fmaf(d1[i], d1[i], b);
+        s0 = i == 0 ? f0[0] : s0 + f0[i];
+        s1 = i == 0 ? f1[0] : s1 + f1[i];
+        a = i == 0 ? d0[0] * d0[0] : fmaf(d0[i], d0[i], a);
+        b = i == 0 ? d1[0] * d1[0] : fmaf(d1[i], d1[i], b);
     }
-    bool first0[8], first1[8];
-    float xk0 = x[0], dk0 = d0[0], tk1 = t1[0], dk1 = d1[0];
-    bool seen0 = false, seen1 = false;
+    // first index of each candidate's largest |d| as lane masks, and x at it
+    lanes_t first0[8], first1[8], seen0 = 0ull, seen1 = 0ull;
+    float xk0 = x[0], xk1 = x[0];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const bool h0 = fabsf(d0[i]) == best0, h1 = fabsf(d1[i]) == best1;
-        first0[i] = h0 && !seen0;
-        first1[i] = h1 && !seen1;
-        seen0 = seen0 || h0;
-        seen1 = seen1 || h1;
-        xk0 = first0[i] ? x[i] : xk0;
-        dk0 = first0[i] ? d0[i] : dk0;
-        tk1 = first1[i] ? t1[i] : tk1;
-        dk1 = first1[i] ? d1[i] : dk1;
+        const lanes_t h0 = lanes_of(fabsf(d0[i]) == best0), h1 = lanes_of(fabsf(d1[i]) == best1);
+        first0[i] = h0 & ~seen0;
+        first1[i] = h1 & ~seen1;
+        seen0 |= h0;
+        seen1 |= h1;
+        xk0 = lane_in(first0[i]) ? x[i] : xk0;
+        xk1 = lane_in(first1[i]) ? x[i] : xk1;
     }
+    // the worst coordinates' differences, recomputed from x_k (same operations)
+    const float dk0 = xk0 - custom_round_hd(xk0);
+    const float tk1 = xk1 - 0.5f;
+    const float dk1 = tk1 - custom_round_hd(tk1);
     const bool odd0 = ((int)s0 & 1) != 0, odd1 = ((int)s1 & 1) != 0;
     const float adj0 = odd0 ? ((xk0 >= 0.f && dk0 > 0.f) ? 1.f : -1.f) : 0.f;
     const float adj1 = odd1 ? ((tk1 >= 0.f && dk1 > 0.f) ? 1.f : -1.f) : 0.f;
@@ -256,12 +258,13 @@ __host__ __device__ inline void project_dyadic(const float x[8], float y[8])
     a += fmaf(-2.f * adj0, dk0, fabsf(adj0));
     b += fmaf(-2.f * adj1, dk1, fabsf(adj1));
     const bool pick0 = a < b;  // ties go to D8 + 1/2, as the reference's strict <
+    const lanes_t p0 = lanes_of(pick0);
     const float adj = pick0 ? adj0 : adj1;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const bool at_k = pick0 ? first0[i] : first1[i];
+        const lanes_t at = (p0 & first0[i]) | (~p0 & first1[i]);
         const float base = pick0 ? f0[i] : f1[i] + 0.5f;
-        y[i] = base + (at_k ? adj : 0.f);
+        y[i] = base + (lane_in(at) ? adj : 0.f);
     }
 }
 
