@@ -527,10 +527,18 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
 namespace {
 
 // The counter pair of the current device for stream s, or null when all
-// kTileSlots pairs of the device are taken (the kernels then use the
-// static schedule).
+// kTileSlots pairs of the device are taken or s is capturing a graph (the
+// kernels then use the static schedule: a replayed graph may run beside
+// later calls on the stream it was captured from, so it must not share
+// that stream's pair).
 unsigned* tile_counters(hipStream_t s)
 {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cap) != hipSuccess) {
+        (void)hipGetLastError();  // the query's own error, not the launch's
+        return nullptr;
+    }
+    if (cap != hipStreamCaptureStatusNone) return nullptr;
     static std::mutex mu;
     static std::map<std::pair<int, hipStream_t>, int> slot_of;
     static unsigned* base[64] = {nullptr};

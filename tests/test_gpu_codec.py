@@ -319,3 +319,42 @@ def test_dynamic_schedule_matches_static(ca):
     finally:
         _lib.set_codec_dynamic(True)
         _lib.set_codec_path(0)
+
+
+def test_fixed_format_kernel_in_a_graph(ca):
+    """A round trip captured in a HIP graph (the fixed-format kernel takes the
+    static schedule there) replayed three times, with eager calls on the
+    capturing stream between the replays: every replay equals the eager
+    result, and so does every eager call."""
+    from coset_amd import _lib
+    _lib.require_gpu()
+    n = (1 << 20) + 777
+    g = torch.Generator(device="cuda").manual_seed(41)
+    x = torch.randn((n, 8), device="cuda", generator=g)
+    x2 = torch.randn((n, 8), device="cuda", generator=g)
+    pk_ref, out_ref = ca.hnlq_roundtrip(x, 4, 2, 1.0)
+    pk_ref2, out_ref2 = ca.hnlq_roundtrip(x2, 4, 2, 1.0)
+    pk = torch.empty_like(pk_ref)
+    out = torch.empty_like(out_ref)
+    pk2 = torch.empty_like(pk_ref)
+    out2 = torch.empty_like(out_ref)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        ca.hnlq_roundtrip(x, 4, 2, 1.0, packed_out=pk, decoded_out=out)   # warm-up on the side stream
+        s.synchronize()
+        with torch.cuda.graph(graph, stream=s):
+            ca.hnlq_roundtrip(x, 4, 2, 1.0, packed_out=pk, decoded_out=out)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        pk.zero_()
+        out.zero_()
+        graph.replay()
+        with torch.cuda.stream(s):
+            ca.hnlq_roundtrip(x2, 4, 2, 1.0, packed_out=pk2, decoded_out=out2)
+        torch.cuda.synchronize()
+        assert torch.equal(pk.view(torch.int16), pk_ref.view(torch.int16)), rep
+        assert torch.equal(out, out_ref), rep
+        assert torch.equal(pk2.view(torch.int16), pk_ref2.view(torch.int16)), rep
+        assert torch.equal(out2, out_ref2), rep
