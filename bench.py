@@ -50,11 +50,18 @@ def traffic_from_profile():
         return json.load(f).get("hbm_bytes_per_launch")
 
 
-def gpu_time(torch, fn, steps, warmup):
-    """Average seconds per call of fn, HIP events on the current stream."""
+def gpu_time(torch, fn, steps, warmup, warm_s=0.0):
+    """Average seconds per call of fn, HIP events on the current stream,
+    after `warmup` untimed calls (and more until warm_s seconds have passed:
+    the GPU needs tens of milliseconds of load to reach its steady clock)."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    t_warm = time.perf_counter()
+    while time.perf_counter() - t_warm < warm_s:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
     s = torch.cuda.current_stream()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
@@ -149,7 +156,7 @@ def bench_c2_codes(torch, ca, args):
         _lib.call("coset_e8_hnlq_roundtrip", _lib.ptr(x), _lib.F32, n, _lib.SCALE_CODEC, 1.0, None, 0, 0.0,
                   None, 0, 4, 2, 1, _lib.ptr(packed), _lib.ptr(codes), _lib.ptr(out), _lib.F32, _lib.stream_of(x))
 
-    k, _ = gpu_time(torch, step, 20, 3)
+    k, _ = gpu_time(torch, step, 100, 3, 0.1)
     nbytes = n * (C2_BYTES_PER_BLOCK + 64)
     del x, packed, codes, out
     return {"workload": "C2 round trip also writing float codes [2^24, 2, 8] (compat layout)",
@@ -186,7 +193,7 @@ def bench_c3(torch, ca, args):
         ca.hnlq_roundtrip(xb, q, M, beta_row=beta, blocks_per_row=cols // 8, clip=2.0, packed_out=packed,
                           decoded_out=out)
 
-    k, w = gpu_time(torch, step, 30, 3)
+    k, w = gpu_time(torch, step, 100, 3, 0.1)
     nbytes = 60 * n
     return {"workload": "C3 2^22 Student-t(3) blocks clipped +-2, bf16 in, q16 M3, per-row beta, clamp 2",
             "gblocks_per_s": round(n / k / 1e9, 3), "kernel_us": round(k * 1e6, 1),
@@ -244,7 +251,7 @@ def bench_c4(torch, ca, args):
                             ("mfma_raw_words", words), ("lds", tiled)):
             m = "mfma" if method.startswith("mfma") else "lds"
             fn = lambda: ca.vlut_matmul(wts, a, 4, scale=scale, method=m, workspace=ws)
-            k_eager, _ = gpu_time(torch, fn, 50 if m == "lds" else 100, 5)
+            k_eager, _ = gpu_time(torch, fn, 50 if m == "lds" else 100, 5, 0.05)
             k = graph_time(torch, fn)
             wbytes = wts.data.numel() * 4 if isinstance(wts, ca.PreparedWords) else wts.numel() * wts.element_size()
             nbytes = wbytes + B * 4096 * 2 + B * 4096 * 4
@@ -276,7 +283,7 @@ def bench_c5(torch, ca, args):
             y = layer(x)
             y.backward(gy)
 
-        k, w = gpu_time(torch, step, 20, 3)
+        k, w = gpu_time(torch, step, 100, 3, 0.1)
         flops = 6.0 * 4096 * fin * fout
         res["shapes"][f"{fin}x{fout}"] = {"tokens_per_s": round(4096 / k, 1), "ms": round(k * 1e3, 3),
                                           "tflops": round(flops / k / 1e12, 1),
