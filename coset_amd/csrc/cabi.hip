@@ -599,7 +599,7 @@ static int vlut_matmul_impl(const void* words, int word_format, const float* sca
                     (long long)need);
     if (need > 0 && !workspace) return fail(COSET_EINVAL, "NULL workspace");
     if (word_format < 0 || word_format > 3) return fail(COSET_EINVAL, "word_format must be 0, 1, 2 or 3");
-    if (word_format == 3 && plan.kernel != coset::VK_MFMA_ROWS)
+    if (word_format == 3 && plan.kernel != coset::VK_MFMA_ROWS && plan.kernel != coset::VK_MFMA_WIDE)
         return fail(COSET_EUNSUPPORTED, "the decoded format runs on the matrix-core rows kernel only (fp16/bf16 activations)");
     if (word_format != 0 && !aligned(words, 16)) return fail(COSET_EINVAL, "prepared words must be 16-byte aligned");
     coset::VlutMatmulArgs p{};

@@ -156,6 +156,17 @@ extern int g_codec_plain;      // 1 (default): the table kernel's fixed-format v
 extern int g_codec_dynamic;    // 1 (default): the fixed-format kernel takes its tiles from a counter
 constexpr int64_t kLutMinBlocks = 1 << 20;  // below it the table staging does not pay (layer-sized calls)
 
+// Workgroup barrier that orders LDS only: waits for this wave's LDS
+// operations, not for its loads and stores in flight (__syncthreads would
+// drain those too).
+__device__ __forceinline__ void lds_barrier()
+{
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt, expcnt unrestricted
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+}
+
 // Backward of the QAT weight quantizer (qat.hip).
 // dbdt (nullable): also write dtheta[t] = dbeta[t] * dbdt[t].
 hipError_t launch_qat_bwd(const void* g, int g_dtype, const float* W, const void* packed,

@@ -43,16 +43,6 @@ constexpr int kTileSlots = 64;
 constexpr int kTileBlocks = 2;  // blocks per thread in a dynamic tile
 static __device__ __align__(256) unsigned g_tile_ctr[kTileSlots][2];
 
-// Workgroup barrier that orders LDS only: waits for this wave's LDS
-// operations, not for its loads and stores in flight (__syncthreads would
-// drain those too).
-__device__ __forceinline__ void lds_barrier()
-{
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt, expcnt unrestricted
-    __asm__ volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    __asm__ volatile("" ::: "memory");
-}
 
 // Copies the decode tables to LDS: the map (n_map uint4) and the byte or
 // coarse table (n_tab uint64).  Each thread issues all its loads before any

@@ -703,6 +703,150 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulAr
     }
 }
 
+// ---------------------------------------------------------------- MFMA wide kernel
+// Tile: 128 output rows (8 row tiles of 16, one per wave) x 64 tokens per
+// workgroup, K split over grid.y (partials [split][B][rows]), token tiles of
+// 64 over grid.z.  The activations of a stage (64 tokens x 128 K) are loaded
+// once per workgroup, two 16-byte loads per thread, and shared by the 8
+// waves through LDS (double-buffered, one LDS-only barrier per stage); each
+// wave decodes its own row tile's weight pairs into the B operand as the rows
+// kernel does and runs 4 MFMAs (one per 16-token tile) per k-quad.  Every
+// global load is unconditional (clamped; what lies outside the matrix or the
+// workgroup's K range has zero activations), so the waits before a stage
+// leave the next stage's loads in flight.
+constexpr int kWideRows = 128;
+constexpr int kWideTokens = 64;
+constexpr int kWideStageKq = 4;                       // k-quads (4 k-blocks of 8, 32 K) per stage
+constexpr int kWideActStride = 32 * kWideStageKq + 8; // halves per token row in LDS (16-byte pad)
+
+template <int Q, int M, bool BF16, int FMT>
+__global__ void __launch_bounds__(kRowsWaves * 64) vlut_wide_kernel(VlutMatmulArgs p)
+{
+    constexpr int WN = FMT == VLUT_DECODED ? 2 : M;  // uint32 per pair
+    __shared__ uint64_t s_tab[FMT == VLUT_DECODED ? 1 : kSwarSlots];
+    __shared__ __align__(16) uint16_t s_act[2][kWideTokens][kWideActStride];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4;
+    const int64_t kb_total = p.K / 8;
+    const int64_t kq_total = (kb_total + 3) / 4;
+    const int64_t kq_wg = (kq_total + gridDim.y - 1) / gridDim.y;
+    const int64_t kq_begin = blockIdx.y * kq_wg;
+    const int64_t kq_end = min(kq_total, kq_begin + kq_wg);
+    const int64_t r0 = (int64_t)blockIdx.x * kWideRows + wave * 16;
+    const int64_t row = r0 + (lane & 15);
+    const int64_t t_base = (int64_t)blockIdx.z * kWideTokens;
+    const uint16_t* act = reinterpret_cast<const uint16_t*>(p.act);
+    const int bias = FMT == VLUT_DECODED ? kVlutDecodedBias : p.swar_bias;
+    const _Float16 f16_off = (_Float16)(1024 + bias);
+    const float f32_off = (float)bias;
+    // rows of this wave that hold weights (whole tiles in the tiled formats)
+    const bool rows_ok = (FMT == VLUT_TILED || FMT == VLUT_DECODED) ? r0 < p.rows : row < p.rows;
+
+    // this thread's share of a stage's activations: token a_tok, k-blocks
+    // a_part + 8 i of the stage (16 bytes each)
+    constexpr int AL = kWideStageKq / 2;  // 16-byte loads per thread and stage
+    struct Act {
+        uint4 v[AL];
+    };
+    const int a_tok = threadIdx.x >> 3, a_part = threadIdx.x & 7;
+    const bool tok_ok = t_base + a_tok < p.B;
+    const int64_t a_row = tok_ok ? t_base + a_tok : 0;
+    auto load_act = [&](int64_t kq0, Act& ac) {
+#pragma unroll
+        for (int i = 0; i < AL; ++i) {
+            const int part = a_part + 8 * i;
+            const int64_t kb = 4 * kq0 + part;
+            const bool ok = tok_ok && kb < kb_total && kq0 + (part >> 2) < kq_end;
+            const uint4 v = *reinterpret_cast<const uint4*>(act + a_row * p.K + (ok ? kb : 0) * 8);
+            // zeroed through a mask the compiler cannot trace back to ok: a
+            // select would let it branch around the load, and the waits after
+            // a conditional load drain the queue
+            uint32_t m;
+            __asm__("v_mov_b32 %0, %1" : "=v"(m) : "v"(ok ? ~0u : 0u));
+            ac.v[i] = make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
+        }
+    };
+    struct W {
+        uint32_t w[kWideStageKq][WN];
+    };
+    auto load_w = [&](int64_t kq0, W& ws) {
+#pragma unroll
+        for (int j = 0; j < kWideStageKq; ++j) {
+            const int64_t kb = 4 * (kq0 + j) + g;
+            const bool ok = rows_ok && kb < kb_total;
+            // outside the matrix: pair (0, 0) instead, under zero activations
+            // or an output that is not stored
+            load_pair<Q, M, WN>(p, FMT, ok ? row : 0, ok ? kb : 0, kb_total, ws.w[j]);
+        }
+    };
+    float4_t acc[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) acc[s] = (float4_t){0.f, 0.f, 0.f, 0.f};
+
+    if (FMT != VLUT_DECODED) {
+        for (int i = threadIdx.x; i < 512 + p.n_coarse; i += blockDim.x) s_tab[i] = p.swar[i];
+    }
+    const int stages = (int)((kq_end - kq_begin + kWideStageKq - 1) / kWideStageKq);
+    W w_now, w_next;
+    Act a_next;
+    load_act(kq_begin, a_next);
+    load_w(kq_begin, w_now);
+    for (int st = 0; st < stages; ++st) {
+        const int64_t kq0 = kq_begin + (int64_t)st * kWideStageKq;
+        const int buf = st & 1;
+#pragma unroll
+        for (int i = 0; i < AL; ++i)
+            *reinterpret_cast<uint4*>(&s_act[buf][a_tok][(a_part + 8 * i) * 8]) = a_next.v[i];
+        lds_barrier();
+        // the next stage's loads go out before this stage's products
+        const int64_t kq1 = st + 1 < stages ? kq0 + kWideStageKq : kq0;
+        load_act(kq1, a_next);
+        load_w(kq1, w_next);
+        __asm__ volatile("" ::: "memory");  // the loads stay ahead of the products
+        uint4 av_all[kWideStageKq][4];
+#pragma unroll
+        for (int j = 0; j < kWideStageKq; ++j)
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+                av_all[j][s] = *reinterpret_cast<const uint4*>(&s_act[buf][16 * s + (lane & 15)][(4 * j + g) * 8]);
+#pragma unroll
+        for (int j = 0; j < kWideStageKq; ++j) {
+            uint4 bw;
+            if constexpr (FMT == VLUT_DECODED)
+                bw = bytes_to_operand<BF16>(w_now.w[j][0], w_now.w[j][1 % WN], f16_off, f32_off);
+            else
+                bw = decode_pair_swar<Q, M, BF16>(s_tab, w_now.w[j], f16_off, f32_off);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const uint4 av = av_all[j][s];
+                if (BF16)
+                    acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av),
+                                                                    __builtin_bit_cast(bf16x8_t, bw), acc[s], 0, 0, 0);
+                else
+                    acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, av),
+                                                                   __builtin_bit_cast(half8_t, bw), acc[s], 0, 0, 0);
+            }
+        }
+        w_now = w_next;
+    }
+
+    // D[token = 16 s + 4 (lane / 16) + i][row = lane % 16]
+    const int64_t o = row;
+    if (o >= p.rows) return;
+    const float sc = p.scale ? (p.scale_mode == 0 ? p.scale[o] : 1.f / p.scale[o]) : 1.f;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int64_t tok = t_base + 16 * s + 4 * g + i;
+            if (tok >= p.B) continue;
+            if (gridDim.y == 1)
+                p.out[tok * p.rows + o] = vlut_epilogue(acc[s][i] * 0.5f * sc, o, p.bias, p.lsq_alpha, p.lsq_qmax);
+            else
+                p.partial[((int64_t)blockIdx.y * p.B + tok) * p.rows + o] = acc[s][i];
+        }
+}
+
 // ---------------------------------------------------------------- reduce
 __global__ void __launch_bounds__(256) vlut_reduce_kernel(const float* partial, int splits, int64_t B,
                                                          int64_t rows, const float* scale, int scale_mode,
@@ -722,6 +866,23 @@ __global__ void __launch_bounds__(256) vlut_reduce_kernel(const float* partial, 
         }
     }
     for (; s < splits; ++s) acc += pp[s];
+    float sc = scale ? (scale_mode == 0 ? scale[o] : 1.f / scale[o]) : 1.f;
+    out[i] = vlut_epilogue(acc * mult * sc, o, bias, lsq_alpha, lsq_qmax);
+}
+
+// Same for partials stored split-major, [splits][B][rows] (the wide kernel);
+// the splits are summed in order.
+__global__ void __launch_bounds__(256) vlut_reduce_sm_kernel(const float* partial, int splits, int64_t B,
+                                                            int64_t rows, const float* scale, int scale_mode,
+                                                            float mult, const float* bias, const float* lsq_alpha,
+                                                            int lsq_qmax, float* out)
+{
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= B * rows) return;
+    int64_t o = i % rows;
+    const int64_t n = B * rows;
+    float acc = 0.f;
+    for (int s = 0; s < splits; ++s) acc += partial[s * n + i];
     float sc = scale ? (scale_mode == 0 ? scale[o] : 1.f / scale[o]) : 1.f;
     out[i] = vlut_epilogue(acc * mult * sc, o, bias, lsq_alpha, lsq_qmax);
 }
@@ -841,6 +1002,15 @@ VlutPlan vlut_plan(int64_t rows, int64_t B, int64_t K, int q, int M, int method)
         return {VK_LDS, (int)std::max<int64_t>(1, std::min<int64_t>(want, kb))};
     }
     const bool swar = g_vlut_swar && ((q == 2 && M <= 4) || (q == 4 && M <= 2));
+    if (swar && B > 32) {
+        // 128-row, 64-token workgroups sharing the activations through LDS,
+        // with K splits to fill the CUs (each keeping at least one stage)
+        const int64_t groups = ((rows + kWideRows - 1) / kWideRows) * ((B + kWideTokens - 1) / kWideTokens);
+        const int64_t max_splits = std::max<int64_t>(1, ((kb + 3) / 4) / kWideStageKq);
+        int64_t splits = g_vlut_splits > 0 ? g_vlut_splits
+                                           : std::max<int64_t>(1, device_cu_count() / std::max<int64_t>(1, groups));
+        return {VK_MFMA_WIDE, (int)std::max<int64_t>(1, std::min<int64_t>(splits, max_splits))};
+    }
     if (swar) {
         // one workgroup of 16 rows per CU when the rows allow, else K splits
         // (each keeping at least one 4-k-block step per wave)
@@ -954,6 +1124,39 @@ hipError_t launch_rows(const VlutMatmulArgs& p, int splits, hipStream_t s)
     return hipErrorInvalidValue;
 }
 
+template <int Q, int M, bool BF16>
+void launch_wide_fmt(const VlutMatmulArgs& p, int splits, hipStream_t s)
+{
+    dim3 grid((unsigned)((p.rows + kWideRows - 1) / kWideRows), (unsigned)splits,
+              (unsigned)((p.B + kWideTokens - 1) / kWideTokens));
+#define COSET_WIDE(F) hipLaunchKernelGGL((vlut_wide_kernel<Q, M, BF16, F>), grid, dim3(kRowsWaves * 64), 0, s, p)
+    switch (p.prepared) {
+    case VLUT_RAW: COSET_WIDE(VLUT_RAW); break;
+    case VLUT_PREPARED: COSET_WIDE(VLUT_PREPARED); break;
+    case VLUT_DECODED: COSET_WIDE(VLUT_DECODED); break;
+    default: COSET_WIDE(VLUT_TILED); break;
+    }
+#undef COSET_WIDE
+}
+
+template <int Q>
+hipError_t dispatch_wide(const VlutMatmulArgs& p, int splits, hipStream_t s)
+{
+    const bool bf = p.act_dtype == DT_BF16;
+    switch (p.M) {
+#define COSET_M(MM) \
+    case MM: \
+        if constexpr (Q == 2 || MM <= 2) { \
+            if (bf) launch_wide_fmt<Q, MM, true>(p, splits, s); else launch_wide_fmt<Q, MM, false>(p, splits, s); \
+            return hipGetLastError(); \
+        } \
+        return hipErrorInvalidValue;
+    COSET_M(1) COSET_M(2) COSET_M(3) COSET_M(4)
+#undef COSET_M
+    default: return hipErrorInvalidValue;
+    }
+}
+
 template <int Q>
 hipError_t dispatch_rows(const VlutMatmulArgs& p, int splits, hipStream_t s)
 {
@@ -986,7 +1189,18 @@ hipError_t vlut_matmul(VlutMatmulArgs p, const VlutPlan& plan, hipStream_t s)
     p.swar = t->swar;
     p.swar_ok = p.M <= t->swar_max_m && g_vlut_swar;
     p.swar_bias = p.swar_ok ? t->swar_bias[p.M] : 0;
-    if (p.prepared == VLUT_DECODED && plan.kernel != VK_MFMA_ROWS) return hipErrorInvalidValue;
+    if (p.prepared == VLUT_DECODED && plan.kernel != VK_MFMA_ROWS && plan.kernel != VK_MFMA_WIDE)
+        return hipErrorInvalidValue;
+    if (plan.kernel == VK_MFMA_WIDE) {
+        if (!p.swar_ok) return hipErrorInvalidValue;
+        e = p.q == 4 ? dispatch_wide<4>(p, splits, s) : dispatch_wide<2>(p, splits, s);
+        if (e != hipSuccess || splits == 1) return e;
+        const int64_t nw = p.B * p.rows;
+        hipLaunchKernelGGL(vlut_reduce_sm_kernel, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, s, p.partial,
+                           splits, p.B, p.rows, p.scale, p.scale_mode, 0.5f, p.bias, p.lsq_alpha, p.lsq_qmax,
+                           p.out);
+        return hipGetLastError();
+    }
     if (plan.kernel == VK_MFMA_ROWS) {
         if (!p.swar_ok) return hipErrorInvalidValue;
         e = p.q == 4 ? dispatch_rows<4>(p, splits, s) : dispatch_rows<2>(p, splits, s);

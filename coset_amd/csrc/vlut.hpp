@@ -67,17 +67,18 @@ __host__ __device__ inline int64_t vlut_prepared_words(int64_t rows, int64_t kb,
 
 // Launch plan of a matmul: kernel and K splits (splits > 1 needs a
 // workspace of splits * B * rows floats and a reduce launch).
-enum VlutKernel { VK_LDS = 0, VK_MFMA_TILE = 1, VK_MFMA_ROWS = 2 };
+enum VlutKernel { VK_LDS = 0, VK_MFMA_TILE = 1, VK_MFMA_ROWS = 2, VK_MFMA_WIDE = 3 };
 struct VlutPlan {
     int kernel;
     int splits;
 };
 VlutPlan vlut_plan(int64_t rows, int64_t B, int64_t K, int q, int M, int method);
-// Workspace floats a plan needs: the split-K partials [B, rows, splits],
-// none when the rows kernel runs unsplit and writes the output itself.
+// Workspace floats a plan needs: the split-K partials ([B, rows, splits],
+// or [splits, B, rows] for the wide kernel), none when the rows or wide
+// kernel runs unsplit and writes the output itself.
 inline int64_t vlut_workspace_floats(const VlutPlan& plan, int64_t B, int64_t rows)
 {
-    if (plan.kernel == VK_MFMA_ROWS && plan.splits == 1) return 0;
+    if ((plan.kernel == VK_MFMA_ROWS || plan.kernel == VK_MFMA_WIDE) && plan.splits == 1) return 0;
     return (int64_t)plan.splits * B * rows;
 }
 
