@@ -714,15 +714,21 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulAr
 // global load is unconditional (clamped; what lies outside the matrix or the
 // workgroup's K range has zero activations), so the waits before a stage
 // leave the next stage's loads in flight.
-constexpr int kWideRows = 128;
+constexpr int kWideRT = 1;                            // row tiles of 16 per wave
+constexpr int kWideNW = 8;                            // waves per workgroup
+constexpr int kWideRows = 16 * kWideRT * kWideNW;     // rows per workgroup
 constexpr int kWideTokens = 64;
 constexpr int kWideStageKq = 4;                       // k-quads (4 k-blocks of 8, 32 K) per stage
 constexpr int kWideActStride = 32 * kWideStageKq + 8; // halves per token row in LDS (16-byte pad)
 
-template <int Q, int M, bool BF16, int FMT>
-__global__ void __launch_bounds__(kRowsWaves * 64) vlut_wide_kernel(VlutMatmulArgs p)
+template <int Q, int M, bool BF16, int FMT, int RT, int NW>
+__global__ void __launch_bounds__(NW * 64) vlut_wide_kernel(VlutMatmulArgs p)
 {
     constexpr int WN = FMT == VLUT_DECODED ? 2 : M;  // uint32 per pair
+    constexpr int T = NW * 64;                       // threads
+    constexpr int P = 4 * kWideStageKq;              // 16-byte k-block chunks per token and stage
+    constexpr int AL = kWideTokens * P / T;          // activation loads per thread and stage
+    static_assert(kWideTokens * P % T == 0, "whole activation loads per thread");
     __shared__ uint64_t s_tab[FMT == VLUT_DECODED ? 1 : kSwarSlots];
     __shared__ __align__(16) uint16_t s_act[2][kWideTokens][kWideActStride];
 
@@ -732,32 +738,27 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_wide_kernel(VlutMatmulAr
     const int64_t kq_wg = (kq_total + gridDim.y - 1) / gridDim.y;
     const int64_t kq_begin = blockIdx.y * kq_wg;
     const int64_t kq_end = min(kq_total, kq_begin + kq_wg);
-    const int64_t r0 = (int64_t)blockIdx.x * kWideRows + wave * 16;
-    const int64_t row = r0 + (lane & 15);
+    const int64_t rt0 = ((int64_t)blockIdx.x * NW + wave) * RT;  // first row tile of this wave
     const int64_t t_base = (int64_t)blockIdx.z * kWideTokens;
     const uint16_t* act = reinterpret_cast<const uint16_t*>(p.act);
     const int bias = FMT == VLUT_DECODED ? kVlutDecodedBias : p.swar_bias;
     const _Float16 f16_off = (_Float16)(1024 + bias);
     const float f32_off = (float)bias;
-    // rows of this wave that hold weights (whole tiles in the tiled formats)
-    const bool rows_ok = (FMT == VLUT_TILED || FMT == VLUT_DECODED) ? r0 < p.rows : row < p.rows;
 
-    // this thread's share of a stage's activations: token a_tok, k-blocks
-    // a_part + 8 i of the stage (16 bytes each)
-    constexpr int AL = kWideStageKq / 2;  // 16-byte loads per thread and stage
+    // this thread's share of a stage's activations: chunks threadIdx.x + T i
+    // (token c / P, k-block c % P of the stage, 16 bytes each)
     struct Act {
         uint4 v[AL];
     };
-    const int a_tok = threadIdx.x >> 3, a_part = threadIdx.x & 7;
-    const bool tok_ok = t_base + a_tok < p.B;
-    const int64_t a_row = tok_ok ? t_base + a_tok : 0;
+    const int a_part = threadIdx.x % P;
     auto load_act = [&](int64_t kq0, Act& ac) {
 #pragma unroll
         for (int i = 0; i < AL; ++i) {
-            const int part = a_part + 8 * i;
-            const int64_t kb = 4 * kq0 + part;
-            const bool ok = tok_ok && kb < kb_total && kq0 + (part >> 2) < kq_end;
-            const uint4 v = *reinterpret_cast<const uint4*>(act + a_row * p.K + (ok ? kb : 0) * 8);
+            const int tok = (threadIdx.x + T * i) / P;
+            const int64_t kb = 4 * kq0 + a_part;
+            const bool ok = t_base + tok < p.B && kb < kb_total && kq0 + a_part / 4 < kq_end;
+            const uint4 v =
+                *reinterpret_cast<const uint4*>(act + (ok ? (t_base + tok) * p.K + kb * 8 : 0));
             // zeroed through a mask the compiler cannot trace back to ok: a
             // select would let it branch around the load, and the waits after
             // a conditional load drain the queue
@@ -767,21 +768,29 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_wide_kernel(VlutMatmulAr
         }
     };
     struct W {
-        uint32_t w[kWideStageKq][WN];
+        uint32_t w[RT][kWideStageKq][WN];
     };
     auto load_w = [&](int64_t kq0, W& ws) {
 #pragma unroll
-        for (int j = 0; j < kWideStageKq; ++j) {
-            const int64_t kb = 4 * (kq0 + j) + g;
-            const bool ok = rows_ok && kb < kb_total;
-            // outside the matrix: pair (0, 0) instead, under zero activations
-            // or an output that is not stored
-            load_pair<Q, M, WN>(p, FMT, ok ? row : 0, ok ? kb : 0, kb_total, ws.w[j]);
+        for (int t = 0; t < RT; ++t) {
+            const int64_t r0 = (rt0 + t) * 16, row = r0 + (lane & 15);
+            // rows that hold weights (whole tiles in the tiled formats)
+            const bool rows_ok = (FMT == VLUT_TILED || FMT == VLUT_DECODED) ? r0 < p.rows : row < p.rows;
+#pragma unroll
+            for (int j = 0; j < kWideStageKq; ++j) {
+                const int64_t kb = 4 * (kq0 + j) + g;
+                const bool ok = rows_ok && kb < kb_total;
+                // outside the matrix: pair (0, 0) instead, under zero
+                // activations or an output that is not stored
+                load_pair<Q, M, WN>(p, FMT, ok ? row : 0, ok ? kb : 0, kb_total, ws.w[t][j]);
+            }
         }
     };
-    float4_t acc[4];
+    float4_t acc[RT][4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) acc[s] = (float4_t){0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < RT; ++t)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc[t][s] = (float4_t){0.f, 0.f, 0.f, 0.f};
 
     if (FMT != VLUT_DECODED) {
         for (int i = threadIdx.x; i < 512 + p.n_coarse; i += blockDim.x) s_tab[i] = p.swar[i];
@@ -796,7 +805,7 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_wide_kernel(VlutMatmulAr
         const int buf = st & 1;
 #pragma unroll
         for (int i = 0; i < AL; ++i)
-            *reinterpret_cast<uint4*>(&s_act[buf][a_tok][(a_part + 8 * i) * 8]) = a_next.v[i];
+            *reinterpret_cast<uint4*>(&s_act[buf][(threadIdx.x + T * i) / P][a_part * 8]) = a_next.v[i];
         lds_barrier();
         // the next stage's loads go out before this stage's products
         const int64_t kq1 = st + 1 < stages ? kq0 + kWideStageKq : kq0;
@@ -811,40 +820,47 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_wide_kernel(VlutMatmulAr
                 av_all[j][s] = *reinterpret_cast<const uint4*>(&s_act[buf][16 * s + (lane & 15)][(4 * j + g) * 8]);
 #pragma unroll
         for (int j = 0; j < kWideStageKq; ++j) {
-            uint4 bw;
-            if constexpr (FMT == VLUT_DECODED)
-                bw = bytes_to_operand<BF16>(w_now.w[j][0], w_now.w[j][1 % WN], f16_off, f32_off);
-            else
-                bw = decode_pair_swar<Q, M, BF16>(s_tab, w_now.w[j], f16_off, f32_off);
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const uint4 av = av_all[j][s];
-                if (BF16)
-                    acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av),
-                                                                    __builtin_bit_cast(bf16x8_t, bw), acc[s], 0, 0, 0);
+            for (int t = 0; t < RT; ++t) {
+                uint4 bw;
+                if constexpr (FMT == VLUT_DECODED)
+                    bw = bytes_to_operand<BF16>(w_now.w[t][j][0], w_now.w[t][j][1 % WN], f16_off, f32_off);
                 else
-                    acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, av),
-                                                                   __builtin_bit_cast(half8_t, bw), acc[s], 0, 0, 0);
+                    bw = decode_pair_swar<Q, M, BF16>(s_tab, w_now.w[t][j], f16_off, f32_off);
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const uint4 av = av_all[j][s];
+                    if (BF16)
+                        acc[t][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            __builtin_bit_cast(bf16x8_t, av), __builtin_bit_cast(bf16x8_t, bw), acc[t][s], 0, 0, 0);
+                    else
+                        acc[t][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            __builtin_bit_cast(half8_t, av), __builtin_bit_cast(half8_t, bw), acc[t][s], 0, 0, 0);
+                }
             }
         }
         w_now = w_next;
     }
 
     // D[token = 16 s + 4 (lane / 16) + i][row = lane % 16]
-    const int64_t o = row;
-    if (o >= p.rows) return;
-    const float sc = p.scale ? (p.scale_mode == 0 ? p.scale[o] : 1.f / p.scale[o]) : 1.f;
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
+    for (int t = 0; t < RT; ++t) {
+        const int64_t o = (rt0 + t) * 16 + (lane & 15);
+        if (o >= p.rows) continue;
+        const float sc = p.scale ? (p.scale_mode == 0 ? p.scale[o] : 1.f / p.scale[o]) : 1.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int64_t tok = t_base + 16 * s + 4 * g + i;
-            if (tok >= p.B) continue;
-            if (gridDim.y == 1)
-                p.out[tok * p.rows + o] = vlut_epilogue(acc[s][i] * 0.5f * sc, o, p.bias, p.lsq_alpha, p.lsq_qmax);
-            else
-                p.partial[((int64_t)blockIdx.y * p.B + tok) * p.rows + o] = acc[s][i];
-        }
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int64_t tok = t_base + 16 * s + 4 * g + i;
+                if (tok >= p.B) continue;
+                if (gridDim.y == 1)
+                    p.out[tok * p.rows + o] =
+                        vlut_epilogue(acc[t][s][i] * 0.5f * sc, o, p.bias, p.lsq_alpha, p.lsq_qmax);
+                else
+                    p.partial[((int64_t)blockIdx.y * p.B + tok) * p.rows + o] = acc[t][s][i];
+            }
+    }
 }
 
 // ---------------------------------------------------------------- reduce
@@ -1129,7 +1145,8 @@ void launch_wide_fmt(const VlutMatmulArgs& p, int splits, hipStream_t s)
 {
     dim3 grid((unsigned)((p.rows + kWideRows - 1) / kWideRows), (unsigned)splits,
               (unsigned)((p.B + kWideTokens - 1) / kWideTokens));
-#define COSET_WIDE(F) hipLaunchKernelGGL((vlut_wide_kernel<Q, M, BF16, F>), grid, dim3(kRowsWaves * 64), 0, s, p)
+#define COSET_WIDE(F) \
+    hipLaunchKernelGGL((vlut_wide_kernel<Q, M, BF16, F, kWideRT, kWideNW>), grid, dim3(kWideNW * 64), 0, s, p)
     switch (p.prepared) {
     case VLUT_RAW: COSET_WIDE(VLUT_RAW); break;
     case VLUT_PREPARED: COSET_WIDE(VLUT_PREPARED); break;
