@@ -40,7 +40,8 @@ constexpr int kLutThreads = 1024;
 // Calls on one stream run one after another and so never share a pair while
 // it counts.  Zero-initialised when the code object is loaded.
 constexpr int kTileSlots = 64;
-constexpr int kTileBlocks = 2;  // blocks per thread in a dynamic tile
+constexpr int kTileBlocks = 2;        // blocks per thread in a dynamic tile
+constexpr int kTileBlocksDecode = 8;  // the same for the decoder (a few input bytes per block)
 static __device__ __align__(256) unsigned g_tile_ctr[kTileSlots][2];
 
 
@@ -297,7 +298,7 @@ __device__ __forceinline__ uint32_t encode_level_word(const float xl[8], bool in
     return pack_word<Q>(b, Q);
 }
 
-template <int Q, int M, int MODE, bool SCALED, bool CODES>
+template <int Q, int M, int MODE, bool SCALED, bool CODES, bool PK>
 __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, const uint16_t* __restrict__ g_map,
                                                               const uint64_t* __restrict__ g_tab, int n_coarse,
                                                               int swar_bias, unsigned* tiles)
@@ -326,10 +327,16 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
             in.v = xs[2 * i + 1];
         } else {
             const uint16_t* pw = reinterpret_cast<const uint16_t*>(a.packed_in) + (size_t)i * M;
-            uint64_t w = 0;
+            if (M == 2) {
+                in.w = *reinterpret_cast<const uint32_t*>(pw);
+            } else if (M == 4) {
+                in.w = *reinterpret_cast<const uint64_t*>(pw);
+            } else {
+                uint64_t w = 0;
 #pragma unroll
-            for (int m = 0; m < M; ++m) w |= (uint64_t)pw[m] << (16 * m);
-            in.w = w;
+                for (int m = 0; m < M; ++m) w |= (uint64_t)pw[m] << (16 * m);
+                in.w = w;
+            }
         }
     };
     auto body = [&](int64_t i, const In& in) {
@@ -384,7 +391,7 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
                 sw1 += l1 << (L * m);
             }
         }
-        if (MODE != MODE_DECODE) {
+        if (MODE != MODE_DECODE && PK) {
             uint16_t* pw = reinterpret_cast<uint16_t*>(a.packed) + (size_t)i * M;
             if (M == 1) {
                 pw[0] = (uint16_t)pack;
@@ -417,6 +424,56 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
     // n - 1, n >= 1) and every store of a body is unconditional.
     const int64_t last = n - 1;
     In in0, in1;
+    if constexpr (MODE == MODE_DECODE) if (tiles) {
+        // Decode: the input is a few bytes per block, so a tile holds
+        // kTileBlocksDecode blocks per thread and all of the next tile's
+        // words are loaded while the current tile is decoded (otherwise the
+        // reads are bound by their latency).  Counter protocol as below.
+        constexpr int KD = kTileBlocksDecode;
+        const int64_t ntiles = (n + KD * kLutThreads - 1) / (KD * kLutThreads);
+        auto blk = [&](int64_t t, int j) {
+            const int64_t b = (t * KD + j) * kLutThreads + threadIdx.x;
+            return b < n ? b : last;
+        };
+        if (threadIdx.x == 0) {
+            s_tile[2] = atomicInc(tiles, ~0u);
+            s_tile[3] = atomicInc(tiles, ~0u);
+        }
+        lds_barrier();
+        const int64_t t0 = s_tile[2];
+        int64_t t1 = s_tile[3];
+        In A[KD], B[KD];
+        auto tile = [&](int64_t cur, int64_t nxt, In (&now)[KD], In (&ahead)[KD], int slot) {
+            unsigned grab = 0;
+            if (threadIdx.x == 0) grab = atomicInc(tiles, ~0u);
+#pragma unroll
+            for (int j = 0; j < KD; ++j) load(blk(nxt, j), ahead[j]);
+            __asm__ volatile("" ::: "memory");  // the loads stay ahead of the decodes
+#pragma unroll
+            for (int j = 0; j < KD; ++j) body(blk(cur, j), now[j]);
+            if (threadIdx.x == 0) s_tile[slot] = grab;
+            lds_barrier();
+            return (int64_t)s_tile[slot];
+        };
+        if (t0 < ntiles) {
+#pragma unroll
+            for (int j = 0; j < KD; ++j) load(blk(t0, j), A[j]);
+            int64_t t2 = tile(t0, t1, A, B, 0);
+            while (t1 < ntiles) {
+                const int64_t t3 = tile(t1, t2, B, A, 1);
+                if (t2 >= ntiles) break;
+                t1 = tile(t2, t3, A, B, 0);
+                if (t3 >= ntiles) break;
+                t2 = t1;
+                t1 = t3;
+            }
+        }
+        if (threadIdx.x == 0 && atomicAdd(tiles + 1, 1u) == gridDim.x - 1) {
+            atomicExch(tiles, 0u);
+            atomicExch(tiles + 1, 0u);
+        }
+        return;
+    }
     if (tiles) {
         // Dynamic schedule: tiles of kTileBlocks x kLutThreads consecutive
         // blocks (kTileBlocks per thread, kLutThreads apart), taken from a
@@ -576,13 +633,32 @@ hipError_t launch_plain(const CodecArgs& a, int grid, const uint16_t* map, const
         const bool scaled = a.scale_mode == SCALE_CODEC && a.beta != 1.f;
         const bool codes = MODE != MODE_DECODE && a.codes_f32;
         unsigned* tiles = g_codec_dynamic ? tile_counters(s) : nullptr;
-#define COSET_PLAIN(SC, CO) \
-    hipLaunchKernelGGL((hnlq_plain_kernel<Q, M, MODE, SC, CO>), dim3(grid), dim3(kLutThreads), 0, s, a, map, sw, nc, bias, \
-                       tiles)
-        if (scaled) {
-            if (codes) COSET_PLAIN(true, true); else COSET_PLAIN(true, false);
+        // packed words are always written by the encoder, optional in the
+        // round trip (e8_quantize asks for the decoded blocks only)
+        const bool pk = MODE == MODE_ENCODE || (MODE == MODE_ROUNDTRIP && a.packed);
+#define COSET_PLAIN(SC, CO, P) \
+    hipLaunchKernelGGL((hnlq_plain_kernel<Q, M, MODE, SC, CO, P>), dim3(grid), dim3(kLutThreads), 0, s, a, map, sw, nc, \
+                       bias, tiles)
+        if constexpr (MODE == MODE_DECODE) {
+            if (scaled) COSET_PLAIN(true, false, false); else COSET_PLAIN(false, false, false);
+        } else if constexpr (MODE == MODE_ENCODE) {
+            if (scaled) {
+                if (codes) COSET_PLAIN(true, true, true); else COSET_PLAIN(true, false, true);
+            } else {
+                if (codes) COSET_PLAIN(false, true, true); else COSET_PLAIN(false, false, true);
+            }
+        } else if (pk) {
+            if (scaled) {
+                if (codes) COSET_PLAIN(true, true, true); else COSET_PLAIN(true, false, true);
+            } else {
+                if (codes) COSET_PLAIN(false, true, true); else COSET_PLAIN(false, false, true);
+            }
         } else {
-            if (codes) COSET_PLAIN(false, true); else COSET_PLAIN(false, false);
+            if (scaled) {
+                if (codes) COSET_PLAIN(true, true, false); else COSET_PLAIN(true, false, false);
+            } else {
+                if (codes) COSET_PLAIN(false, true, false); else COSET_PLAIN(false, false, false);
+            }
         }
 #undef COSET_PLAIN
         return hipGetLastError();
@@ -602,13 +678,14 @@ hipError_t launch_q(const CodecArgs& a, const DecodeTables* t, hipStream_t s)
     const int bias = swar ? t->swar_bias[a.M] : 0;
     // the plain kernel: fp32 in and out, no scale or a codec beta = 2^k, no
     // dither, no step counter, byte tables for the decode, and the encoder's
-    // fast projection on (it is a compile-time constant there), and every
-    // output of the mode present (its stores are unconditional)
+    // fast projection on (it is a compile-time constant there), and the
+    // mode's outputs present (its stores are unconditional; the round trip's
+    // packed words are a compile-time option)
     const bool plain = (MODE == MODE_DECODE || (a.x_dtype == DT_F32 && a.fast_projection)) &&
                        (MODE == MODE_ENCODE || a.out_dtype == DT_F32) &&
                        (a.scale_mode == SCALE_NONE || (a.scale_mode == SCALE_CODEC && a.beta_is_pow2)) &&
                        !a.dither && !a.step_counter && (MODE == MODE_ENCODE || swar) &&
-                       (MODE == MODE_DECODE || a.packed) && (MODE == MODE_ENCODE || a.out) && g_codec_plain;
+                       (MODE != MODE_ENCODE || a.packed) && (MODE == MODE_ENCODE || a.out) && g_codec_plain;
     if (plain) {
         const uint64_t* sw = t ? t->swar : nullptr;
         switch (a.M) {

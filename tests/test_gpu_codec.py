@@ -316,6 +316,17 @@ def test_dynamic_schedule_matches_static(ca):
             codes = O.e8_encode(xs, 4, 2)
             np.testing.assert_array_equal(words(pk)[:k], O.pack_words(codes, 4))
             np.testing.assert_array_equal(host(out[:k]), O.e8_decode(codes, 4, 2))
+            # the round trip without packed words, and decodes of 1 and 3 levels
+            _, out_np = ca.hnlq_roundtrip(x, 4, 2, 1.0, want_packed=False)
+            assert torch.equal(out_np, out_s), n
+            for q, M in ((4, 1), (2, 3)):
+                pw = ca.hnlq_encode(x, q, M, 1.0)
+                _lib.set_codec_dynamic(False)
+                dec_static = ca.hnlq_decode(pw, q, M, 1.0)
+                _lib.set_codec_dynamic(True)
+                assert torch.equal(ca.hnlq_decode(pw, q, M, 1.0), dec_static), (n, q, M)
+                c = O.e8_encode(xs, q, M)
+                np.testing.assert_array_equal(host(dec_static[:k]), O.e8_decode(c, q, M))
     finally:
         _lib.set_codec_dynamic(True)
         _lib.set_codec_path(0)
