@@ -116,6 +116,31 @@ def bench_c2(torch, ca, args):
     return kernel_s, wall_s, cpu
 
 
+def bench_c2_api(torch, ca, args):
+    """The C2 blocks through each codec entry point on its own: the
+    reference signatures (e8_encode with its float code tensor [N, 2, 8],
+    e8_decode from it, e8_quantize) and the packed encode and decode."""
+    dev = torch.device("cuda")
+    n = C2_BLOCKS
+    g = torch.Generator(device=dev).manual_seed(2)
+    x = torch.randn((n, 8), device=dev, generator=g, dtype=torch.float32)
+    cfg = ca.LatticeConfig(lattice_type="E8", q=4, M=2, beta=1.0)
+    codes, _ = ca.e8_encode(x, cfg)
+    packed = ca.hnlq_encode(x, 4, 2, 1.0)
+    res = {"workload": "C2 blocks (2^24, q4 M2, beta 1) through single entry points", "calls": {}}
+    for name, fn, nbytes in (("e8_encode", lambda: ca.e8_encode(x, cfg), 32 + 64 + 4),
+                             ("e8_decode", lambda: ca.e8_decode(codes, cfg), 64 + 32),
+                             ("e8_quantize", lambda: ca.e8_quantize(x, 4), 32 + 32),
+                             ("hnlq_encode", lambda: ca.hnlq_encode(x, 4, 2, 1.0), 32 + 4),
+                             ("hnlq_decode", lambda: ca.hnlq_decode(packed, 4, 2, 1.0), 4 + 32)):
+        k, _ = gpu_time(torch, fn, 50, 3, 0.1)
+        res["calls"][name] = {"kernel_us": round(k * 1e6, 1), "bytes_per_block": nbytes,
+                              "hbm_gbs": round(nbytes * n / k / 1e9, 1),
+                              "frac_hbm": round(nbytes * n / k / 1e9 / HBM_PEAK_GBS, 4)}
+    del x, codes, packed
+    return res
+
+
 def bench_c1(torch, ca, args):
     torch.manual_seed(0)
     layer = ca.create_e8_hnlq_linear(768, 10, q=4, M=2, theta_trainable=False, theta_init_value=0.0,
@@ -300,7 +325,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--cpu-sample", type=int, default=1 << 24,
                     help="C2 blocks timed on the host CPU oracle (0 skips it)")
-    ap.add_argument("--only", default="c1,c2,c2codes,c3,c4,c5", help="comma list of workloads to run")
+    ap.add_argument("--only", default="c1,c2,c2codes,c2api,c3,c4,c5", help="comma list of workloads to run")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 512 MiB device copy (HBM counter calibration)")
     args = ap.parse_args()
@@ -327,8 +352,8 @@ def main():
     cpu = None
     if "c2" in only:
         kernel_s, wall_s, cpu = bench_c2(torch, ca, args)
-    for name, fn in (("c1", bench_c1), ("c2codes", bench_c2_codes), ("c3", bench_c3), ("c4", bench_c4),
-                     ("c5", bench_c5)):
+    for name, fn in (("c1", bench_c1), ("c2codes", bench_c2_codes), ("c2api", bench_c2_api), ("c3", bench_c3),
+                     ("c4", bench_c4), ("c5", bench_c5)):
         if name in only:
             extra[name] = fn(torch, ca, args)
             torch.cuda.empty_cache()
