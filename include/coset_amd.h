@@ -5,7 +5,10 @@
  * the caller; `stream` is a hipStream_t (NULL = legacy default stream).  Calls
  * are asynchronous and stream-ordered; none synchronizes the host.  Return
  * value: COSET_OK (0) or a negative COSET_E* code; coset_last_error() then
- * holds a message for the calling thread.
+ * holds a message for the calling thread.  Work runs on the calling thread's
+ * current HIP device (hipSetDevice): the buffers and the stream passed in
+ * must belong to it (per-device state -- decode tables, tile counters -- is
+ * looked up from it).
  *
  * Packed code format: level word idx(b) = sum_j b_j q^(7-j) for the level's
  * digits b in [0,q)^8 (the reference vLUT index, coset/legacy/quant/vlut.py:
