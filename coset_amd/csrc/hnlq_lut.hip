@@ -84,6 +84,166 @@ __device__ __forceinline__ void stage_tables(const uint4* __restrict__ g_map, ui
     }
 }
 
+// Block schedules of the persistent kernels.  Each walks blocks 0..n-1
+// (n >= 1) of its workgroup's share, calling load(i, in) for a block's input
+// into a register set and body(i, in) for the rest, with the next input in
+// flight while a body runs.  Loads and stores share one in-order completion
+// counter, so the wait before a body leaves the other set's loads and the
+// last body's stores in flight only if their number is the same on every
+// path into it: the loads are unconditional (past the end they read block
+// n - 1), and the first step is peeled so each loop is entered as it is
+// re-entered.  A partial last tile recomputes block n - 1 and stores the same
+// values to it.
+
+// Grid stride (no tile counter): one block ahead.
+template <typename In, typename Load, typename Body>
+__device__ __forceinline__ void schedule_stride(int64_t n, Load& load, Body& body)
+{
+    const int64_t last = n - 1;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    In in0, in1;
+    load(i, in0);
+    int64_t i1 = i + stride;
+    load(i1 < n ? i1 : last, in1);
+    body(i, in0);
+    while (i1 < n) {
+        const int64_t i2 = i1 + stride;
+        load(i2 < n ? i2 : last, in0);
+        body(i1, in1);
+        if (i2 >= n) break;
+        i1 = i2 + stride;
+        load(i1 < n ? i1 : last, in1);
+        body(i2, in0);
+    }
+}
+
+// The counter pair's protocol: thread 0 takes tiles with atomicInc (the
+// compiler rewrites a uniform-address atomicAdd into a wave reduction that
+// waits for its result at once) two tiles ahead and publishes them through
+// LDS behind an LDS-only barrier; when a workgroup has seen its last tile it
+// counts itself done, and the last one resets the pair for the next call on
+// the stream.
+__device__ __forceinline__ void tiles_first_two(unsigned* tiles, unsigned* s_tile, int64_t& t0, int64_t& t1)
+{
+    if (threadIdx.x == 0) {
+        s_tile[2] = atomicInc(tiles, ~0u);
+        s_tile[3] = atomicInc(tiles, ~0u);
+    }
+    lds_barrier();
+    t0 = s_tile[2];
+    t1 = s_tile[3];
+}
+
+__device__ __forceinline__ void tiles_done(unsigned* tiles)
+{
+    if (threadIdx.x == 0 && atomicAdd(tiles + 1, 1u) == gridDim.x - 1) {
+        atomicExch(tiles, 0u);
+        atomicExch(tiles + 1, 0u);
+    }
+}
+
+// Dynamic tiles of KT x blockDim.x consecutive blocks (KT per thread,
+// blockDim.x apart) with one block ahead; one LDS barrier per tile.
+template <int KT, typename In, typename Load, typename Body>
+__device__ __forceinline__ void schedule_tiles(int64_t n, unsigned* tiles, unsigned* s_tile, Load& load, Body& body)
+{
+    static_assert(KT % 2 == 0 || KT == 1, "register sets alternate per block");
+    const int64_t last = n - 1;
+    const int64_t ntiles = (n + KT * (int64_t)blockDim.x - 1) / (KT * (int64_t)blockDim.x);
+    auto blk = [&](int64_t t, int j) {
+        const int64_t b = (t * KT + j) * blockDim.x + threadIdx.x;
+        return b < n ? b : last;
+    };
+    int64_t t0, t1;
+    tiles_first_two(tiles, s_tile, t0, t1);
+    In in0, in1;
+    auto tile = [&](int64_t cur, int64_t nxt, In& s0, In& s1, int slot) {
+#pragma unroll
+        for (int j = 0; j < KT - 1; ++j) {
+            load(blk(cur, j + 1), j % 2 ? s0 : s1);
+            body(blk(cur, j), j % 2 ? s1 : s0);
+        }
+        In& now = (KT - 1) % 2 ? s1 : s0;
+        In& ahead = (KT - 1) % 2 ? s0 : s1;
+        unsigned grab = 0;
+        if (threadIdx.x == 0) grab = atomicInc(tiles, ~0u);
+        load(blk(nxt, 0), ahead);
+        body(blk(cur, KT - 1), now);
+        if (threadIdx.x == 0) s_tile[slot] = grab;
+        lds_barrier();
+        return (int64_t)s_tile[slot];
+    };
+    if (t0 < ntiles) {
+        load(blk(t0, 0), in0);
+        if constexpr (KT == 1) {
+            int64_t t2 = tile(t0, t1, in0, in1, 0);
+            while (t1 < ntiles) {
+                const int64_t t3 = tile(t1, t2, in1, in0, 1);
+                if (t2 >= ntiles) break;
+                t1 = tile(t2, t3, in0, in1, 0);
+                if (t3 >= ntiles) break;
+                t2 = t1;
+                t1 = t3;
+            }
+        } else {  // every tile starts in in0
+            int64_t t2 = tile(t0, t1, in0, in1, 0);
+            int slot = 1;
+            while (t1 < ntiles) {
+                const int64_t t3 = tile(t1, t2, in0, in1, slot);
+                slot ^= 1;
+                t1 = t2;
+                t2 = t3;
+            }
+        }
+    }
+    tiles_done(tiles);
+}
+
+// Dynamic tiles of KD blocks per thread with all of the next tile's inputs
+// in flight while the current tile is processed (inputs of a few bytes).
+template <int KD, typename In, typename Load, typename Body>
+__device__ __forceinline__ void schedule_tiles_whole(int64_t n, unsigned* tiles, unsigned* s_tile, Load& load,
+                                                     Body& body)
+{
+    const int64_t last = n - 1;
+    const int64_t ntiles = (n + KD * (int64_t)blockDim.x - 1) / (KD * (int64_t)blockDim.x);
+    auto blk = [&](int64_t t, int j) {
+        const int64_t b = (t * KD + j) * blockDim.x + threadIdx.x;
+        return b < n ? b : last;
+    };
+    int64_t t0, t1;
+    tiles_first_two(tiles, s_tile, t0, t1);
+    In A[KD], B[KD];
+    auto tile = [&](int64_t cur, int64_t nxt, In (&now)[KD], In (&ahead)[KD], int slot) {
+        unsigned grab = 0;
+        if (threadIdx.x == 0) grab = atomicInc(tiles, ~0u);
+#pragma unroll
+        for (int j = 0; j < KD; ++j) load(blk(nxt, j), ahead[j]);
+        __asm__ volatile("" ::: "memory");  // the loads stay ahead of the bodies
+#pragma unroll
+        for (int j = 0; j < KD; ++j) body(blk(cur, j), now[j]);
+        if (threadIdx.x == 0) s_tile[slot] = grab;
+        lds_barrier();
+        return (int64_t)s_tile[slot];
+    };
+    if (t0 < ntiles) {
+#pragma unroll
+        for (int j = 0; j < KD; ++j) load(blk(t0, j), A[j]);
+        int64_t t2 = tile(t0, t1, A, B, 0);
+        while (t1 < ntiles) {
+            const int64_t t3 = tile(t1, t2, B, A, 1);
+            if (t2 >= ntiles) break;
+            t1 = tile(t2, t3, A, B, 0);
+            if (t3 >= ntiles) break;
+            t2 = t1;
+            t1 = t3;
+        }
+    }
+    tiles_done(tiles);
+}
+
 // SWAR: each level's 2r comes from three byte tables (tables.hpp) added as
 // two 32-bit words, levels are summed with shifts, and the bytes hold
 // 2 x_hat + swar_bias; otherwise 2r = 2Gb - q (2c) from the unpacked digits.
@@ -417,158 +577,18 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
         p[1] = make_float4(o[4], o[5], o[6], o[7]);
     };
 
-    // Loads and stores share one in-order completion counter, so the wait
-    // before a body can leave the other register set's loads and the last
-    // body's stores in flight only if their number is the same on every path
-    // into it: the loads are unconditional (past the end they read block
-    // n - 1, n >= 1) and every store of a body is unconditional.
-    const int64_t last = n - 1;
-    In in0, in1;
-    if constexpr (MODE == MODE_DECODE) if (tiles) {
-        // Decode: the input is a few bytes per block, so a tile holds
-        // kTileBlocksDecode blocks per thread and all of the next tile's
-        // words are loaded while the current tile is decoded (otherwise the
-        // reads are bound by their latency).  Counter protocol as below.
-        constexpr int KD = kTileBlocksDecode;
-        const int64_t ntiles = (n + KD * kLutThreads - 1) / (KD * kLutThreads);
-        auto blk = [&](int64_t t, int j) {
-            const int64_t b = (t * KD + j) * kLutThreads + threadIdx.x;
-            return b < n ? b : last;
-        };
-        if (threadIdx.x == 0) {
-            s_tile[2] = atomicInc(tiles, ~0u);
-            s_tile[3] = atomicInc(tiles, ~0u);
+    // every store of a body is unconditional (see the schedules above)
+    if constexpr (MODE == MODE_DECODE) {
+        if (tiles) {
+            schedule_tiles_whole<kTileBlocksDecode, In>(n, tiles, s_tile, load, body);
+            return;
         }
-        lds_barrier();
-        const int64_t t0 = s_tile[2];
-        int64_t t1 = s_tile[3];
-        In A[KD], B[KD];
-        auto tile = [&](int64_t cur, int64_t nxt, In (&now)[KD], In (&ahead)[KD], int slot) {
-            unsigned grab = 0;
-            if (threadIdx.x == 0) grab = atomicInc(tiles, ~0u);
-#pragma unroll
-            for (int j = 0; j < KD; ++j) load(blk(nxt, j), ahead[j]);
-            __asm__ volatile("" ::: "memory");  // the loads stay ahead of the decodes
-#pragma unroll
-            for (int j = 0; j < KD; ++j) body(blk(cur, j), now[j]);
-            if (threadIdx.x == 0) s_tile[slot] = grab;
-            lds_barrier();
-            return (int64_t)s_tile[slot];
-        };
-        if (t0 < ntiles) {
-#pragma unroll
-            for (int j = 0; j < KD; ++j) load(blk(t0, j), A[j]);
-            int64_t t2 = tile(t0, t1, A, B, 0);
-            while (t1 < ntiles) {
-                const int64_t t3 = tile(t1, t2, B, A, 1);
-                if (t2 >= ntiles) break;
-                t1 = tile(t2, t3, A, B, 0);
-                if (t3 >= ntiles) break;
-                t2 = t1;
-                t1 = t3;
-            }
-        }
-        if (threadIdx.x == 0 && atomicAdd(tiles + 1, 1u) == gridDim.x - 1) {
-            atomicExch(tiles, 0u);
-            atomicExch(tiles + 1, 0u);
-        }
-        return;
     }
     if (tiles) {
-        // Dynamic schedule: tiles of kTileBlocks x kLutThreads consecutive
-        // blocks (kTileBlocks per thread, kLutThreads apart), taken from a
-        // counter two tiles ahead: thread 0 asks for the next one while the
-        // current tile is processed, one LDS barrier per tile.  In a last,
-        // partial tile the threads past the end redo block n - 1 and store the
-        // same values to it.
-        constexpr int KT = kTileBlocks;
-        static_assert(KT % 2 == 0 || KT == 1, "register sets alternate per block");
-        const int64_t ntiles = (n + KT * kLutThreads - 1) / (KT * kLutThreads);
-        auto blk = [&](int64_t t, int j) {
-            const int64_t b = (t * KT + j) * kLutThreads + threadIdx.x;
-            return b < n ? b : last;
-        };
-        // atomicInc (wrapping at 2^32 - 1, never reached) rather than
-        // atomicAdd: the compiler rewrites a uniform-address atomicAdd into a
-        // wave reduction that waits for the result at once
-        if (threadIdx.x == 0) {
-            s_tile[2] = atomicInc(tiles, ~0u);
-            s_tile[3] = atomicInc(tiles, ~0u);
-        }
-        lds_barrier();
-        const int64_t t0 = s_tile[2];
-        int64_t t1 = s_tile[3];
-        // one tile: each block step loads the next block into one register
-        // set and processes the current one from the other; the last step
-        // also asks for the tile after next and publishes the answer.  The
-        // first tile is peeled so the loop is entered as it is re-entered
-        // (one load pair, then one body's stores).
-        auto tile = [&](int64_t cur, int64_t nxt, In& s0, In& s1, int slot) {
-#pragma unroll
-            for (int j = 0; j < KT - 1; ++j) {
-                load(blk(cur, j + 1), j % 2 ? s0 : s1);
-                body(blk(cur, j), j % 2 ? s1 : s0);
-            }
-            In& now = (KT - 1) % 2 ? s1 : s0;
-            In& ahead = (KT - 1) % 2 ? s0 : s1;
-            unsigned grab = 0;
-            if (threadIdx.x == 0) grab = atomicInc(tiles, ~0u);
-            load(blk(nxt, 0), ahead);
-            body(blk(cur, KT - 1), now);
-            if (threadIdx.x == 0) s_tile[slot] = grab;
-            lds_barrier();
-            return (int64_t)s_tile[slot];
-        };
-        if (t0 < ntiles) {
-            load(blk(t0, 0), in0);
-            if constexpr (KT == 1) {
-                int64_t t2 = tile(t0, t1, in0, in1, 0);
-                while (t1 < ntiles) {
-                    const int64_t t3 = tile(t1, t2, in1, in0, 1);
-                    if (t2 >= ntiles) break;
-                    t1 = tile(t2, t3, in0, in1, 0);
-                    if (t3 >= ntiles) break;
-                    t2 = t1;
-                    t1 = t3;
-                }
-            } else {  // every tile starts in in0
-                int64_t t2 = tile(t0, t1, in0, in1, 0);
-                int slot = 1;
-                while (t1 < ntiles) {
-                    const int64_t t3 = tile(t1, t2, in0, in1, slot);
-                    slot ^= 1;
-                    t1 = t2;
-                    t2 = t3;
-                }
-            }
-        }
-        // every tile request of this workgroup has returned: count it done;
-        // the last one resets the pair for the next call on this stream
-        if (threadIdx.x == 0 && atomicAdd(tiles + 1, 1u) == gridDim.x - 1) {
-            atomicExch(tiles, 0u);
-            atomicExch(tiles + 1, 0u);
-        }
+        schedule_tiles<kTileBlocks, In>(n, tiles, s_tile, load, body);
         return;
     }
-    // Static schedule (no counter pair free): a grid stride, the first body
-    // peeled so the loop is entered as it is re-entered, with one load pair
-    // followed by one body's stores.
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    load(i, in0);
-    int64_t i1 = i + stride;
-    load(i1 < n ? i1 : last, in1);
-    body(i, in0);
-    while (i1 < n) {
-        const int64_t i2 = i1 + stride;
-        load(i2 < n ? i2 : last, in0);
-        body(i1, in1);
-        if (i2 >= n) break;
-        i1 = i2 + stride;
-        load(i1 < n ? i1 : last, in1);
-        body(i2, in0);
-    }
+    schedule_stride<In>(n, load, body);
 }
 
 namespace {
