@@ -369,3 +369,32 @@ def test_fixed_format_kernel_in_a_graph(ca):
         assert torch.equal(out, out_ref), rep
         assert torch.equal(pk2.view(torch.int16), pk_ref2.view(torch.int16)), rep
         assert torch.equal(out2, out_ref2), rep
+
+
+def test_full_size_c3(ca):
+    """C3 at full size (4096 x 8192 Student-t(3) clipped at +-2, bf16 in,
+    q16 M3, per-row beta, clamp 2): 48 sampled rows against the oracle bit
+    for bit (decoded values and level words), and over every block the clamp
+    bound and the lattice property: 2 W_q beta is an integer vector (up to
+    the rounding of the division by beta) wherever the clamp did not bind."""
+    rows, cols = 4096, 8192
+    g = torch.Generator(device="cuda").manual_seed(3)
+    z = torch.randn((rows, cols), device="cuda", generator=g)
+    chi = (torch.randn((rows, cols, 3), device="cuda", generator=g) ** 2).sum(-1) / 3
+    x = torch.clamp(z / chi.sqrt(), -2.0, 2.0).to(torch.bfloat16)
+    del z, chi
+    beta = torch.rand(rows, device="cuda", generator=g) * 30 + 5
+    n = rows * cols // 8
+    pk, out = ca.hnlq_roundtrip(x.reshape(n, 8), 16, 3, beta_row=beta, blocks_per_row=cols // 8, clip=2.0)
+    W = out.reshape(rows, cols)
+    assert float(W.abs().max()) <= 2.0
+    scaled = (W * beta[:, None]).double() * 2.0
+    inside = W.abs() < 2.0
+    err = (scaled - scaled.round()).abs()
+    assert float(err[inside].max()) < 2e-3          # one fp32 division's rounding, relative to |2 W beta| < 2^7
+    sel = torch.randperm(rows, generator=torch.Generator().manual_seed(5))[:48]
+    xs = x[sel.cuda()].float().cpu().numpy()
+    Wq, _, codes = O.layer_quant(xs, host(beta[sel.cuda()]), 16, 3, 2.0)
+    np.testing.assert_array_equal(host(W[sel.cuda()]), Wq)
+    got = words(pk).reshape(rows, cols // 8, 3)[sel.numpy()]
+    np.testing.assert_array_equal(got.reshape(-1, 3), O.pack_words(codes, 16).reshape(-1, 3))
