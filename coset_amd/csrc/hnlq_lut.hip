@@ -426,6 +426,57 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_lut_kernel(CodecArgs a, cons
     }
 }
 
+// The float code tensor [n, 2, 8] of the two level words of a block (low 16
+// bits: level 0).  The four lanes of a quad hold four consecutive blocks
+// (every schedule hands them out that way; a lane past the end holds block
+// n - 1, as do all lanes after it): a 4 x 4 transpose of their 16-byte
+// chunks over quad DPP moves lets each store write one block's 64 bytes
+// from four adjacent lanes, whole 64-byte lines, instead of every lane
+// writing 16 bytes 64 bytes apart.
+template <int Q>
+__device__ __forceinline__ void store_codes_quad(float* codes, int64_t i, uint32_t words)
+{
+    uint32_t e[4][4];  // e[chunk][dword]: chunk c = level c / 2, coordinates 4 (c % 2) ..
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+        int b[8];
+        unpack_word<Q>((words >> (16 * m)) & 0xffffu, Q, b);
+#pragma unroll
+        for (int d = 0; d < 8; ++d) e[2 * m + d / 4][d % 4] = __float_as_uint((float)b[d]);
+    }
+    const int j = threadIdx.x & 3;
+    // lane j of the quad ends with chunk j of the quad's block s in e[s]:
+    // exchange lane bit 0 with chunk bit 0, then lane bit 1 with chunk bit 1
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        uint32_t t[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) t[c] = __builtin_amdgcn_mov_dpp(e[c ^ 1][d], 0xB1, 0xF, 0xF, false);  // [1,0,3,2]
+#pragma unroll
+        for (int c = 0; c < 4; ++c) e[c][d] = ((j ^ c) & 1) ? t[c] : e[c][d];
+    }
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        uint32_t t[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) t[c] = __builtin_amdgcn_mov_dpp(e[c ^ 2][d], 0x4E, 0xF, 0xF, false);  // [2,3,0,1]
+#pragma unroll
+        for (int c = 0; c < 4; ++c) e[c][d] = ((j ^ c) & 2) ? t[c] : e[c][d];
+    }
+    // the quad's block s is lane s's block: i of lane s
+    const uint32_t lo = (uint32_t)i, hi = (uint32_t)((uint64_t)i >> 32);
+    uint4* out = reinterpret_cast<uint4*>(codes);
+    auto put = [&](int sblk, uint32_t blo, uint32_t bhi) {
+        const int64_t blk = (int64_t)(((uint64_t)bhi << 32) | blo);
+        out[blk * 4 + j] = make_uint4(e[sblk][0], e[sblk][1], e[sblk][2], e[sblk][3]);
+    };
+    // quad_perm [s, s, s, s] = s * 0x55
+    put(0, __builtin_amdgcn_mov_dpp(lo, 0x00, 0xF, 0xF, false), __builtin_amdgcn_mov_dpp(hi, 0x00, 0xF, 0xF, false));
+    put(1, __builtin_amdgcn_mov_dpp(lo, 0x55, 0xF, 0xF, false), __builtin_amdgcn_mov_dpp(hi, 0x55, 0xF, 0xF, false));
+    put(2, __builtin_amdgcn_mov_dpp(lo, 0xAA, 0xF, 0xF, false), __builtin_amdgcn_mov_dpp(hi, 0xAA, 0xF, 0xF, false));
+    put(3, __builtin_amdgcn_mov_dpp(lo, 0xFF, 0xF, 0xF, false), __builtin_amdgcn_mov_dpp(hi, 0xFF, 0xF, 0xF, false));
+}
+
 // Same contract for the common case, with everything the general kernel
 // decides per block fixed at compile time: fp32 input and output, no scale
 // or a codec beta = 2^k (x / beta == x * 2^-k exactly; SCALED false when
@@ -523,7 +574,7 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
                 word = encode_level_word<Q>(xl, amax < lim);
                 lim *= (float)Q;
                 pack |= (uint64_t)word << (16 * m);
-                if (CODES) {  // the reference's float code tensor [n, M, 8]
+                if (CODES && M != 2) {  // the reference's float code tensor [n, M, 8]
                     int b[8];
                     unpack_word<Q>(word, Q, b);
                     float4* cp = reinterpret_cast<float4*>(a.codes_f32 + ((size_t)i * M + m) * 8);
@@ -551,6 +602,7 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
                 sw1 += l1 << (L * m);
             }
         }
+        if (MODE != MODE_DECODE && CODES && M == 2) store_codes_quad<Q>(a.codes_f32, i, (uint32_t)pack);
         if (MODE != MODE_DECODE && PK) {
             uint16_t* pw = reinterpret_cast<uint16_t*>(a.packed) + (size_t)i * M;
             if (M == 1) {

@@ -261,13 +261,16 @@ def test_fast_projection_same_codes(ca, path, q, M):
     np.testing.assert_array_equal(outs[0], ref)
 
 
-@pytest.mark.parametrize("beta", [1.0, 0.25, 0.3])
-def test_roundtrip_with_float_codes(ca, path, beta):
+@pytest.mark.parametrize("beta,extra", [(1.0, 0), (0.25, 3), (0.3, 1), (1.0, 2)])
+def test_roundtrip_with_float_codes(ca, path, beta, extra):
     """One round trip writing packed words, the reference's float code
-    tensor and the decoded blocks together (every kernel variant)."""
+    tensor and the decoded blocks together (every kernel variant); block
+    counts that end inside a group of four lanes too (the fixed-format
+    kernel writes the codes of four lanes' blocks together)."""
     from coset_amd import _lib
-    rng = np.random.default_rng(int(beta * 100))
-    x = np.concatenate([rng.standard_normal((70000, 8)), _adversarial_blocks(rng, 2000)]).astype(np.float32)
+    rng = np.random.default_rng(int(beta * 100) + extra)
+    x = np.concatenate([rng.standard_normal((70000 + extra, 8)),
+                        _adversarial_blocks(rng, 2000)]).astype(np.float32)
     n = x.shape[0]
     xd = dev(x)
     packed = torch.empty((n, 2), dtype=torch.uint16, device="cuda")
