@@ -95,27 +95,34 @@ __device__ __forceinline__ void stage_tables(const uint4* __restrict__ g_map, ui
 // re-entered.  A partial last tile recomputes block n - 1 and stores the same
 // values to it.
 
-// Grid stride (no tile counter): one block ahead.
+// Grid stride (no tile counter): one block ahead.  The loop runs on the
+// workgroup's base index, so every lane of a wave takes every step (a lane
+// past the end works on block n - 1): the bodies' quad exchanges read only
+// active lanes.
 template <typename In, typename Load, typename Body>
 __device__ __forceinline__ void schedule_stride(int64_t n, Load& load, Body& body)
 {
     const int64_t last = n - 1;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
+    auto blk = [&](int64_t b) {
+        const int64_t i = b + threadIdx.x;
+        return i < n ? i : last;
+    };
+    int64_t b = (int64_t)blockIdx.x * blockDim.x;
+    if (b >= n) return;
     In in0, in1;
-    load(i, in0);
-    int64_t i1 = i + stride;
-    load(i1 < n ? i1 : last, in1);
-    body(i, in0);
-    while (i1 < n) {
-        const int64_t i2 = i1 + stride;
-        load(i2 < n ? i2 : last, in0);
-        body(i1, in1);
-        if (i2 >= n) break;
-        i1 = i2 + stride;
-        load(i1 < n ? i1 : last, in1);
-        body(i2, in0);
+    load(blk(b), in0);
+    int64_t b1 = b + stride;
+    load(blk(b1), in1);
+    body(blk(b), in0);
+    while (b1 < n) {
+        const int64_t b2 = b1 + stride;
+        load(blk(b2), in0);
+        body(blk(b1), in1);
+        if (b2 >= n) break;
+        b1 = b2 + stride;
+        load(blk(b1), in1);
+        body(blk(b2), in0);
     }
 }
 
@@ -428,8 +435,8 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_lut_kernel(CodecArgs a, cons
 
 // The float code tensor [n, 2, 8] of the two level words of a block (low 16
 // bits: level 0).  The four lanes of a quad hold four consecutive blocks
-// (every schedule hands them out that way; a lane past the end holds block
-// n - 1, as do all lanes after it): a 4 x 4 transpose of their 16-byte
+// (every schedule hands them out that way, with every lane active; a lane
+// past the end holds block n - 1, as do all lanes after it): a 4 x 4 transpose of their 16-byte
 // chunks over quad DPP moves lets each store write one block's 64 bytes
 // from four adjacent lanes, whole 64-byte lines, instead of every lane
 // writing 16 bytes 64 bytes apart.
@@ -477,6 +484,39 @@ __device__ __forceinline__ void store_codes_quad(float* codes, int64_t i, uint32
     put(3, __builtin_amdgcn_mov_dpp(lo, 0xFF, 0xF, 0xF, false), __builtin_amdgcn_mov_dpp(hi, 0xFF, 0xF, 0xF, false));
 }
 
+// Stores one block's 8 decoded floats (32 bytes) through the wave's 1 KiB
+// LDS slice st: half the wave at a time writes its blocks' 32 bytes there
+// and the whole wave reads them back 16 bytes a lane, so each of the two
+// stores writes 32 consecutive blocks (1 KiB) rather than every lane 32
+// bytes.  Every lane is active and the lanes of a wave hold consecutive
+// blocks clamped to n - 1 (the schedules' contract), so lane q's block is
+// min(i_0 + q, n - 1), i_0 being lane 0's.  LDS operations of one wave
+// complete in order, so the slice needs no barrier, only compiler fences:
+// a lane reads what other lanes wrote, which a single lane's view of
+// memory does not show.
+__device__ __forceinline__ void store_out_wave(float* out, int64_t n, int64_t i, const float o[8], float4* st)
+{
+    const int lane = threadIdx.x & 63;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)i);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)i >> 32));
+    const int64_t i0 = (int64_t)(((uint64_t)hi << 32) | lo);
+    const int64_t room = n - 1 - i0;
+    const int lim = room < 63 ? (int)room : 63;
+    char* dst = reinterpret_cast<char*>(out + 8 * i0);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        if ((lane >> 5) == h) {
+            st[2 * (lane & 31)] = make_float4(o[0], o[1], o[2], o[3]);
+            st[2 * (lane & 31) + 1] = make_float4(o[4], o[5], o[6], o[7]);
+        }
+        __asm__ volatile("" ::: "memory");
+        const float4 v = st[lane];
+        __asm__ volatile("" ::: "memory");
+        const uint32_t q = min(32 * h + (lane >> 1), lim);
+        *reinterpret_cast<float4*>(dst + (q * 32u + (lane & 1) * 16u)) = v;  // 32-bit lane offset
+    }
+}
+
 // Same contract for the common case, with everything the general kernel
 // decides per block fixed at compile time: fp32 input and output, no scale
 // or a codec beta = 2^k (x / beta == x * 2^-k exactly; SCALED false when
@@ -518,6 +558,7 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
     __shared__ __align__(16) uint16_t s_map[NC];
     __shared__ uint64_t s_tab[512 + kMaxCoarse];
     __shared__ unsigned s_tile[4];
+    __shared__ float4 s_stage[MODE == MODE_ENCODE ? 1 : kLutThreads / 64][64];  // store_out_wave
     if (MODE != MODE_ENCODE) {
         stage_tables<(NC / 8 + kLutThreads - 1) / kLutThreads, (512 + kMaxCoarse + kLutThreads - 1) / kLutThreads>(
             reinterpret_cast<const uint4*>(g_map), reinterpret_cast<uint4*>(s_map), NC / 8, g_tab, s_tab,
@@ -624,9 +665,7 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
             o[j] = __fmaf_rn((float)((w >> (8 * (j & 3))) & 0xffu), 0.5f, -half_bias);  // (byte - bias) / 2, exact
             if (SCALED) o[j] = __fmul_rn(o[j], a.beta);
         }
-        float4* p = reinterpret_cast<float4*>(a.out) + 2 * i;
-        p[0] = make_float4(o[0], o[1], o[2], o[3]);
-        p[1] = make_float4(o[4], o[5], o[6], o[7]);
+        store_out_wave(static_cast<float*>(a.out), n, i, o, s_stage[threadIdx.x >> 6]);
     };
 
     // every store of a body is unconditional (see the schedules above)

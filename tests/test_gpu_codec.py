@@ -261,12 +261,14 @@ def test_fast_projection_same_codes(ca, path, q, M):
     np.testing.assert_array_equal(outs[0], ref)
 
 
+@pytest.mark.parametrize("dynamic", [True, False])
 @pytest.mark.parametrize("beta,extra", [(1.0, 0), (0.25, 3), (0.3, 1), (1.0, 2)])
-def test_roundtrip_with_float_codes(ca, path, beta, extra):
+def test_roundtrip_with_float_codes(ca, path, beta, extra, dynamic):
     """One round trip writing packed words, the reference's float code
-    tensor and the decoded blocks together (every kernel variant); block
-    counts that end inside a group of four lanes too (the fixed-format
-    kernel writes the codes of four lanes' blocks together)."""
+    tensor and the decoded blocks together (every kernel variant, both
+    schedules of the fixed-format kernel); block counts that end inside a
+    group of four lanes too (the fixed-format kernel writes the codes and
+    the decoded values of four lanes' blocks together)."""
     from coset_amd import _lib
     rng = np.random.default_rng(int(beta * 100) + extra)
     x = np.concatenate([rng.standard_normal((70000 + extra, 8)),
@@ -276,8 +278,13 @@ def test_roundtrip_with_float_codes(ca, path, beta, extra):
     packed = torch.empty((n, 2), dtype=torch.uint16, device="cuda")
     codes = torch.empty((n, 2, 8), dtype=torch.float32, device="cuda")
     out = torch.empty((n, 8), dtype=torch.float32, device="cuda")
-    _lib.call("coset_e8_hnlq_roundtrip", _lib.ptr(xd), _lib.F32, n, _lib.SCALE_CODEC, beta, None, 0, 0.0,
-              None, 0, 4, 2, 1, _lib.ptr(packed), _lib.ptr(codes), _lib.ptr(out), _lib.F32, _lib.stream_of(xd))
+    _lib.set_codec_dynamic(dynamic)
+    try:
+        _lib.call("coset_e8_hnlq_roundtrip", _lib.ptr(xd), _lib.F32, n, _lib.SCALE_CODEC, beta, None, 0, 0.0,
+                  None, 0, 4, 2, 1, _lib.ptr(packed), _lib.ptr(codes), _lib.ptr(out), _lib.F32,
+                  _lib.stream_of(xd))
+    finally:
+        _lib.set_codec_dynamic(True)
     ref = O.e8_encode(x, 4, 2, beta)
     np.testing.assert_array_equal(host(codes).astype(np.int32), ref)
     np.testing.assert_array_equal(words(packed), O.pack_words(ref, 4))
