@@ -97,8 +97,8 @@ __device__ __forceinline__ void stage_tables(const uint4* __restrict__ g_map, ui
 
 // Grid stride (no tile counter): one block ahead.  The loop runs on the
 // workgroup's base index, so every lane of a wave takes every step (a lane
-// past the end works on block n - 1): the bodies' quad exchanges read only
-// active lanes.
+// past the end works on block n - 1), which the bodies' wave-wide stores
+// assume.
 template <typename In, typename Load, typename Body>
 __device__ __forceinline__ void schedule_stride(int64_t n, Load& load, Body& body)
 {
@@ -433,57 +433,6 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_lut_kernel(CodecArgs a, cons
     }
 }
 
-// The float code tensor [n, 2, 8] of the two level words of a block (low 16
-// bits: level 0).  The four lanes of a quad hold four consecutive blocks
-// (every schedule hands them out that way, with every lane active; a lane
-// past the end holds block n - 1, as do all lanes after it): a 4 x 4 transpose of their 16-byte
-// chunks over quad DPP moves lets each store write one block's 64 bytes
-// from four adjacent lanes, whole 64-byte lines, instead of every lane
-// writing 16 bytes 64 bytes apart.
-template <int Q>
-__device__ __forceinline__ void store_codes_quad(float* codes, int64_t i, uint32_t words)
-{
-    uint32_t e[4][4];  // e[chunk][dword]: chunk c = level c / 2, coordinates 4 (c % 2) ..
-#pragma unroll
-    for (int m = 0; m < 2; ++m) {
-        int b[8];
-        unpack_word<Q>((words >> (16 * m)) & 0xffffu, Q, b);
-#pragma unroll
-        for (int d = 0; d < 8; ++d) e[2 * m + d / 4][d % 4] = __float_as_uint((float)b[d]);
-    }
-    const int j = threadIdx.x & 3;
-    // lane j of the quad ends with chunk j of the quad's block s in e[s]:
-    // exchange lane bit 0 with chunk bit 0, then lane bit 1 with chunk bit 1
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-        uint32_t t[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) t[c] = __builtin_amdgcn_mov_dpp(e[c ^ 1][d], 0xB1, 0xF, 0xF, false);  // [1,0,3,2]
-#pragma unroll
-        for (int c = 0; c < 4; ++c) e[c][d] = ((j ^ c) & 1) ? t[c] : e[c][d];
-    }
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-        uint32_t t[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) t[c] = __builtin_amdgcn_mov_dpp(e[c ^ 2][d], 0x4E, 0xF, 0xF, false);  // [2,3,0,1]
-#pragma unroll
-        for (int c = 0; c < 4; ++c) e[c][d] = ((j ^ c) & 2) ? t[c] : e[c][d];
-    }
-    // the quad's block s is lane s's block: i of lane s
-    const uint32_t lo = (uint32_t)i, hi = (uint32_t)((uint64_t)i >> 32);
-    uint4* out = reinterpret_cast<uint4*>(codes);
-    auto put = [&](int sblk, uint32_t blo, uint32_t bhi) {
-        const int64_t blk = (int64_t)(((uint64_t)bhi << 32) | blo);
-        out[blk * 4 + j] = make_uint4(e[sblk][0], e[sblk][1], e[sblk][2], e[sblk][3]);
-    };
-    // quad_perm [s, s, s, s] = s * 0x55
-    put(0, __builtin_amdgcn_mov_dpp(lo, 0x00, 0xF, 0xF, false), __builtin_amdgcn_mov_dpp(hi, 0x00, 0xF, 0xF, false));
-    put(1, __builtin_amdgcn_mov_dpp(lo, 0x55, 0xF, 0xF, false), __builtin_amdgcn_mov_dpp(hi, 0x55, 0xF, 0xF, false));
-    put(2, __builtin_amdgcn_mov_dpp(lo, 0xAA, 0xF, 0xF, false), __builtin_amdgcn_mov_dpp(hi, 0xAA, 0xF, 0xF, false));
-    put(3, __builtin_amdgcn_mov_dpp(lo, 0xFF, 0xF, 0xF, false), __builtin_amdgcn_mov_dpp(hi, 0xFF, 0xF, 0xF, false));
-}
-
 // Stores one block's 8 decoded floats (32 bytes) through the wave's 1 KiB
 // LDS slice st: half the wave at a time writes its blocks' 32 bytes there
 // and the whole wave reads them back 16 bytes a lane, so each of the two
@@ -514,6 +463,43 @@ __device__ __forceinline__ void store_out_wave(float* out, int64_t n, int64_t i,
         __asm__ volatile("" ::: "memory");
         const uint32_t q = min(32 * h + (lane >> 1), lim);
         *reinterpret_cast<float4*>(dst + (q * 32u + (lane & 1) * 16u)) = v;  // 32-bit lane offset
+    }
+}
+
+// The float code tensor [n, 2, 8] of the two level words of a block (low 16
+// bits: level 0), 64 bytes a block, through the wave's 1 KiB LDS slice as
+// in store_out_wave: a quarter of the wave at a time writes its blocks'
+// codes there and the whole wave reads them back 16 bytes a lane, so each
+// of the four stores writes 16 consecutive blocks (1 KiB).
+template <int Q>
+__device__ __forceinline__ void store_codes_wave(float* codes, int64_t n, int64_t i, uint32_t words, uint4* st)
+{
+    uint32_t e[4][4];  // e[chunk][dword]: chunk c = level c / 2, coordinates 4 (c % 2) ..
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+        int b[8];
+        unpack_word<Q>((words >> (16 * m)) & 0xffffu, Q, b);
+#pragma unroll
+        for (int d = 0; d < 8; ++d) e[2 * m + d / 4][d % 4] = __float_as_uint((float)b[d]);
+    }
+    const int lane = threadIdx.x & 63;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)i);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)i >> 32));
+    const int64_t i0 = (int64_t)(((uint64_t)hi << 32) | lo);
+    const int64_t room = n - 1 - i0;
+    const int lim = room < 63 ? (int)room : 63;
+    char* dst = reinterpret_cast<char*>(codes + 16 * i0);
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+        if ((lane >> 4) == h) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) st[4 * (lane & 15) + c] = make_uint4(e[c][0], e[c][1], e[c][2], e[c][3]);
+        }
+        __asm__ volatile("" ::: "memory");
+        const uint4 v = st[lane];
+        __asm__ volatile("" ::: "memory");
+        const uint32_t q = min(16 * h + (lane >> 2), lim);
+        *reinterpret_cast<uint4*>(dst + (q * 64u + (lane & 3) * 16u)) = v;  // 32-bit lane offset
     }
 }
 
@@ -558,7 +544,7 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
     __shared__ __align__(16) uint16_t s_map[NC];
     __shared__ uint64_t s_tab[512 + kMaxCoarse];
     __shared__ unsigned s_tile[4];
-    __shared__ float4 s_stage[MODE == MODE_ENCODE ? 1 : kLutThreads / 64][64];  // store_out_wave
+    __shared__ float4 s_stage[MODE == MODE_ENCODE && !CODES ? 1 : kLutThreads / 64][64];  // store_*_wave
     if (MODE != MODE_ENCODE) {
         stage_tables<(NC / 8 + kLutThreads - 1) / kLutThreads, (512 + kMaxCoarse + kLutThreads - 1) / kLutThreads>(
             reinterpret_cast<const uint4*>(g_map), reinterpret_cast<uint4*>(s_map), NC / 8, g_tab, s_tab,
@@ -643,7 +629,8 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
                 sw1 += l1 << (L * m);
             }
         }
-        if (MODE != MODE_DECODE && CODES && M == 2) store_codes_quad<Q>(a.codes_f32, i, (uint32_t)pack);
+        if (MODE != MODE_DECODE && CODES && M == 2)
+            store_codes_wave<Q>(a.codes_f32, n, i, (uint32_t)pack, reinterpret_cast<uint4*>(s_stage[threadIdx.x >> 6]));
         if (MODE != MODE_DECODE && PK) {
             uint16_t* pw = reinterpret_cast<uint16_t*>(a.packed) + (size_t)i * M;
             if (M == 1) {

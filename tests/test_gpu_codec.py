@@ -267,8 +267,9 @@ def test_roundtrip_with_float_codes(ca, path, beta, extra, dynamic):
     """One round trip writing packed words, the reference's float code
     tensor and the decoded blocks together (every kernel variant, both
     schedules of the fixed-format kernel); block counts that end inside a
-    group of four lanes too (the fixed-format kernel writes the codes and
-    the decoded values of four lanes' blocks together)."""
+    wave and inside a group of four lanes too (the fixed-format kernel
+    writes the codes and the decoded values of a wave's blocks together,
+    clamping lanes past the end to the last block)."""
     from coset_amd import _lib
     rng = np.random.default_rng(int(beta * 100) + extra)
     x = np.concatenate([rng.standard_normal((70000 + extra, 8)),
