@@ -93,14 +93,17 @@ __device__ __forceinline__ void stage_tables(const uint4* __restrict__ g_map, ui
 // path into it: the loads are unconditional (past the end they read block
 // n - 1), and the first step is peeled so each loop is entered as it is
 // re-entered.  A partial last tile recomputes block n - 1 and stores the same
-// values to it.
+// values to it.  In the grid stride and the whole-tile schedule pro() runs
+// once, by every thread of a workgroup that has work, after its first loads
+// are issued (the decoder stages its LDS tables there, so the first input
+// and the tables arrive together).
 
 // Grid stride (no tile counter): one block ahead.  The loop runs on the
 // workgroup's base index, so every lane of a wave takes every step (a lane
 // past the end works on block n - 1), which the bodies' wave-wide stores
 // assume.
-template <typename In, typename Load, typename Body>
-__device__ __forceinline__ void schedule_stride(int64_t n, Load& load, Body& body)
+template <typename In, typename Load, typename Body, typename Pro>
+__device__ __forceinline__ void schedule_stride(int64_t n, Load& load, Body& body, Pro& pro)
 {
     const int64_t last = n - 1;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -114,6 +117,7 @@ __device__ __forceinline__ void schedule_stride(int64_t n, Load& load, Body& bod
     load(blk(b), in0);
     int64_t b1 = b + stride;
     load(blk(b1), in1);
+    pro();
     body(blk(b), in0);
     while (b1 < n) {
         const int64_t b2 = b1 + stride;
@@ -210,9 +214,9 @@ __device__ __forceinline__ void schedule_tiles(int64_t n, unsigned* tiles, unsig
 
 // Dynamic tiles of KD blocks per thread with all of the next tile's inputs
 // in flight while the current tile is processed (inputs of a few bytes).
-template <int KD, typename In, typename Load, typename Body>
+template <int KD, typename In, typename Load, typename Body, typename Pro>
 __device__ __forceinline__ void schedule_tiles_whole(int64_t n, unsigned* tiles, unsigned* s_tile, Load& load,
-                                                     Body& body)
+                                                     Body& body, Pro& pro)
 {
     const int64_t last = n - 1;
     const int64_t ntiles = (n + KD * (int64_t)blockDim.x - 1) / (KD * (int64_t)blockDim.x);
@@ -238,6 +242,9 @@ __device__ __forceinline__ void schedule_tiles_whole(int64_t n, unsigned* tiles,
     if (t0 < ntiles) {
 #pragma unroll
         for (int j = 0; j < KD; ++j) load(blk(t0, j), A[j]);
+    }
+    pro();
+    if (t0 < ntiles) {
         int64_t t2 = tile(t0, t1, A, B, 0);
         while (t1 < ntiles) {
             const int64_t t3 = tile(t1, t2, B, A, 1);
@@ -545,12 +552,25 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
     __shared__ uint64_t s_tab[512 + kMaxCoarse];
     __shared__ unsigned s_tile[4];
     __shared__ float4 s_stage[MODE == MODE_ENCODE && !CODES ? 1 : kLutThreads / 64][64];  // store_*_wave
-    if (MODE != MODE_ENCODE) {
+    auto stage = [&]() {
         stage_tables<(NC / 8 + kLutThreads - 1) / kLutThreads, (512 + kMaxCoarse + kLutThreads - 1) / kLutThreads>(
             reinterpret_cast<const uint4*>(g_map), reinterpret_cast<uint4*>(s_map), NC / 8, g_tab, s_tab,
             512 + n_coarse);
+    };
+    // The decoder stages its tables after the first tile's loads are issued
+    // (an LDS-only barrier: the loads stay in flight), 2.5 us sooner per
+    // launch at 2^24 blocks; the round trip stages them first (measured
+    // faster that way on the same box).
+    if constexpr (MODE == MODE_ROUNDTRIP) {
+        stage();
         __syncthreads();
     }
+    auto pro = [&]() {
+        if constexpr (MODE == MODE_DECODE) {
+            stage();
+            lds_barrier();
+        }
+    };
     const float half_bias = 0.5f * (float)swar_bias;
     const float4* xs = reinterpret_cast<const float4*>(a.x);
     const int64_t n = a.n;
@@ -658,15 +678,17 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
     // every store of a body is unconditional (see the schedules above)
     if constexpr (MODE == MODE_DECODE) {
         if (tiles) {
-            schedule_tiles_whole<kTileBlocksDecode, In>(n, tiles, s_tile, load, body);
+            schedule_tiles_whole<kTileBlocksDecode, In>(n, tiles, s_tile, load, body, pro);
             return;
         }
     }
-    if (tiles) {
-        schedule_tiles<kTileBlocks, In>(n, tiles, s_tile, load, body);
-        return;
+    if constexpr (MODE != MODE_DECODE) {
+        if (tiles) {
+            schedule_tiles<kTileBlocks, In>(n, tiles, s_tile, load, body);
+            return;
+        }
     }
-    schedule_stride<In>(n, load, body);
+    schedule_stride<In>(n, load, body, pro);
 }
 
 namespace {
