@@ -41,7 +41,7 @@ constexpr int kLutThreads = 1024;
 // it counts.  Zero-initialised when the code object is loaded.
 constexpr int kTileSlots = 64;
 constexpr int kTileBlocks = 2;        // blocks per thread in a dynamic tile
-constexpr int kTileBlocksDecode = 8;  // the same for the decoder (a few input bytes per block)
+constexpr int kTileBlocksDecode = 2;  // the decoder's, whole next tile ahead (1, 4, 8 measured slower)
 static __device__ __align__(256) unsigned g_tile_ctr[kTileSlots][2];
 
 
