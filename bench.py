@@ -150,8 +150,19 @@ def bench_c1(torch, ca, args):
     x = torch.randn(32, 768, device="cuda")
     with torch.no_grad():
         k, w = gpu_time(torch, lambda: layer(x), 200, 20)
+    # the same forward replayed from a HIP graph, on a fresh layer of the same
+    # seed so both loops run steps 1-220 (no every-256-steps statistics update
+    # falls in either timed region)
+    torch.manual_seed(0)
+    layer_g = ca.create_e8_hnlq_linear(768, 10, q=4, M=2, theta_trainable=False, theta_init_value=0.0,
+                                       weight_clip_value=2.0)
+    with torch.no_grad():
+        layer_g.weight.normal_(0.0, 0.02)
+    cap = ca.CapturedQATStep(layer_g, x.clone())
+    kg, wg = gpu_time(torch, cap.step, 200, 20)
     res = {"workload": "C1 layer forward 768->10, x 32x768 fp32, q4 M2 theta 0 (W_q == 0 at these settings)",
-           "us_per_forward_gpu": round(k * 1e6, 2), "us_per_forward_wall": round(w * 1e6, 2)}
+           "us_per_forward_gpu": round(k * 1e6, 2), "us_per_forward_wall": round(w * 1e6, 2),
+           "graph": {"us_per_forward_gpu": round(kg * 1e6, 2), "us_per_forward_wall": round(wg * 1e6, 2)}}
     # the non-degenerate variant: Delta0 = 1.5, W ~ N(0, 1)
     torch.manual_seed(0)
     layer2 = ca.create_e8_hnlq_linear(768, 10, q=4, M=2, theta_trainable=False, theta_init_value=0.0,
@@ -292,7 +303,7 @@ def bench_c4(torch, ca, args):
 
 
 def bench_c5(torch, ca, args):
-    res = {"workload": "C5 QAT E8 HNLQ linear fwd+bwd, 4096 bf16 tokens, q4 M2, W ~ N(0, 0.02)",
+    res = {"workload": "C5 QAT E8 HNLQ linear fwd+bwd, 4096 bf16 tokens, q4 M2, W ~ N(0, 0.02); graph = the step replayed by CapturedQATStep",
            "shapes": {}}
     for fin, fout in ((768, 768), (768, 3072), (3072, 768)):
         torch.manual_seed(7)
@@ -310,9 +321,17 @@ def bench_c5(torch, ca, args):
 
         k, w = gpu_time(torch, step, 100, 3, 0.1)
         flops = 6.0 * 4096 * fin * fout
+        # the same step captured once into a HIP graph and replayed
+        xs = x.detach().clone().requires_grad_(True)
+        cap = ca.CapturedQATStep(layer, xs, gy.clone())
+        kg, wg = gpu_time(torch, cap.step, 100, 3, 0.1)
         res["shapes"][f"{fin}x{fout}"] = {"tokens_per_s": round(4096 / k, 1), "ms": round(k * 1e3, 3),
                                           "tflops": round(flops / k / 1e12, 1),
-                                          "frac_bf16_mfma": round(flops / k / 1e12 / BF16_MFMA_TFLOPS, 4)}
+                                          "frac_bf16_mfma": round(flops / k / 1e12 / BF16_MFMA_TFLOPS, 4),
+                                          "graph": {"tokens_per_s": round(4096 / kg, 1),
+                                                    "ms": round(kg * 1e3, 3), "ms_wall": round(wg * 1e3, 3),
+                                                    "tflops": round(flops / kg / 1e12, 1),
+                                                    "frac_bf16_mfma": round(flops / kg / 1e12 / BF16_MFMA_TFLOPS, 4)}}
     return res
 
 

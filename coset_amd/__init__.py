@@ -18,6 +18,7 @@ from .codecs import (
 )
 
 from .layers import (
+    CapturedQATStep,
     E8ThetaWeightQuant,
     E8WeightQuant,
     HNLQConfig,
@@ -52,6 +53,7 @@ from .packed import PackedLinear, load_packed, packed_state, save_packed
 __version__ = "0.1.0"
 
 __all__ = [
+    "CapturedQATStep",
     "D4Lattice", "E8Lattice", "LatticeConfig", "Lattice", "LegacyE8Lattice", "d4_quantize",
     "e8_encode", "e8_decode", "e8_quantize", "E8Decoder", "DecodingMethod",
     "hnlq_encode", "hnlq_decode", "hnlq_roundtrip", "word_dtype",

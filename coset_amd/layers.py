@@ -434,9 +434,15 @@ class HNLQLinearQAT(nn.Module):
         if device_increment:
             with torch.no_grad():
                 self.step_count += 1
-        if self._host_step % self.stat_update_interval == 0:
-            W = self.weight.view(self.out_features, self.blocks_per_row, self.block_size)
-            self._gather_stats(W.detach())
+        if self._host_step % self.stat_update_interval == 0 and not (
+                self.weight.is_cuda and torch.cuda.is_current_stream_capturing()):
+            # under graph capture the statistics update stays out of the graph:
+            # CapturedQATStep runs it eagerly before the replay that needs it
+            self.gather_step_stats()
+
+    def gather_step_stats(self):
+        W = self.weight.view(self.out_features, self.blocks_per_row, self.block_size)
+        self._gather_stats(W.detach())
 
     def _beta(self):
         beta_min, beta_max = self._bounds()
@@ -624,6 +630,98 @@ class HNLQLinearQAT(nn.Module):
 
 
 HNLQLinear = HNLQLinearQAT
+
+
+class CapturedQATStep:
+    """One QAT layer step (forward, and backward when ``grad_output`` is
+    given) captured once into a HIP graph and replayed by ``step()``.
+
+    No counterpart in the reference, whose layer runs eagerly on the CPU.
+    An eager step issues about fifteen small launches from Python (bias cast,
+    the fused quantizer, hipBLASLt's products, the bias-gradient reduction),
+    so at BERT shapes the host, not the GPU, sets its time; a replay issues
+    them as one graph launch.
+
+    Semantics per ``step()`` are those of an eager step preceded by
+    ``layer.zero_grad(set_to_none=True)``: the gradients of the layer's
+    parameters and of the static input are overwritten, not accumulated, and
+    live in tensors owned by the graph (``param.grad`` after the first
+    step).  The device step counter advances inside the graph (the fused
+    kernel increments it); the host mirror of the counter and the
+    every-``stat_update_interval``-steps EMA update of the weight statistics
+    run eagerly, on the same stream, before the replay that reads them
+    (coset/core/layers.py:408-413 updates them before the bounds).  The
+    returned output is the graph's static tensor, overwritten by the next
+    step.  A change of ``quantization_enabled`` (warm-up epochs) needs a new
+    capture; ``step()`` raises instead of replaying a stale graph.  The
+    warm-up runs that torch needs before capture leave the layer's buffers
+    and counters as they were.
+    """
+
+    def __init__(self, layer: HNLQLinearQAT, x: torch.Tensor, grad_output: Optional[torch.Tensor] = None,
+                 warmup: int = 3):
+        if not x.is_cuda or not layer.weight.is_cuda:
+            raise ValueError("CapturedQATStep needs the layer and its input on a GPU")
+        if layer.enable_diagnostics:
+            raise ValueError("CapturedQATStep: diagnostics read values back to the host on every step")
+        self.layer = layer
+        self.x = x
+        self.grad_output = grad_output
+        self._mode = layer.quantization_enabled
+        if layer._host_step is None:
+            layer._host_step = int(layer.step_count)
+        host_step = layer._host_step
+        saved = {name: b.clone() for name, b in layer.named_buffers()}
+
+        side = torch.cuda.Stream(device=x.device)
+        side.wait_stream(torch.cuda.current_stream(x.device))
+        with torch.cuda.stream(side):
+            for _ in range(max(1, int(warmup))):
+                self._zero_grads()
+                self._run()
+        torch.cuda.current_stream(x.device).wait_stream(side)
+        with torch.no_grad():
+            for name, b in layer.named_buffers():
+                b.copy_(saved[name])
+        self._zero_grads()
+
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.y = self._run()
+        layer._host_step = host_step
+
+    def _zero_grads(self):
+        self.layer.zero_grad(set_to_none=True)
+        if self.x.requires_grad:
+            self.x.grad = None
+
+    def _run(self):
+        if self.grad_output is None:
+            with torch.no_grad():
+                return self.layer(self.x)
+        y = self.layer(self.x)
+        y.backward(self.grad_output)
+        return y.detach()
+
+    def step(self, x: Optional[torch.Tensor] = None, grad_output: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Replay the step, after copying new values (if given) into the
+        static input and output-gradient tensors."""
+        L = self.layer
+        if L.quantization_enabled != self._mode:
+            raise RuntimeError("CapturedQATStep: quantization was switched since the capture; capture again")
+        if grad_output is not None and self.grad_output is None:
+            raise ValueError("CapturedQATStep: captured without a backward")
+        with torch.no_grad():
+            if x is not None:
+                self.x.copy_(x)
+            if grad_output is not None:
+                self.grad_output.copy_(grad_output)
+        if self._mode:
+            L._host_step += 1
+            if L._host_step % L.stat_update_interval == 0:
+                L.gather_step_stats()
+        self.graph.replay()
+        return self.y
 
 
 def create_d4_hnlq_linear(in_dim, out_dim, device=None, **kwargs):

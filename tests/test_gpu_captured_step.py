@@ -1,0 +1,102 @@
+"""CapturedQATStep: the QAT layer step replayed from a HIP graph against the
+same steps run eagerly on an identical layer.  Every replay is checked, with
+eager work (an SGD update of the parameters, the eager layer's own step and
+host synchronisations) between replays, and with the statistics update
+falling between replays."""
+import pytest
+import torch
+
+import coset_amd
+
+
+def _pair(fin, fout, tiling, interval):
+    layers = []
+    for _ in range(2):
+        torch.manual_seed(11)
+        L = coset_amd.create_e8_hnlq_linear(fin, fout, q=4, M=2, tiling=tiling)
+        with torch.no_grad():
+            L.weight.normal_(0.0, 0.05)
+            L.theta_beta.uniform_(-1.0, 1.0)
+        L.stat_update_interval = interval
+        layers.append(L)
+    return layers
+
+
+def _grads(L, x):
+    return [x.grad, L.weight.grad, L.theta_beta.grad, L.bias.grad]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("tiling", ["row", "block"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_captured_step_matches_eager_steps(tiling, dtype):
+    fin, fout, tokens, steps = 256, 384, 512, 7
+    eager, cap_layer = _pair(fin, fout, tiling, interval=3)
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    xs = [torch.randn(tokens, fin, device="cuda", generator=gen).to(dtype) for _ in range(steps)]
+    gys = [torch.randn(tokens, fout, device="cuda", generator=gen).to(dtype) for _ in range(steps)]
+
+    x_static = torch.zeros(tokens, fin, device="cuda", dtype=dtype, requires_grad=True)
+    gy_static = torch.zeros(tokens, fout, device="cuda", dtype=dtype)
+    cap = coset_amd.CapturedQATStep(cap_layer, x_static, gy_static)
+    # the warm-up before capture leaves counters and statistics untouched
+    assert int(cap_layer.step_count) == 0 and cap_layer._host_step == 0
+    assert torch.equal(cap_layer.sigma_ema, eager.sigma_ema)
+
+    for i in range(steps):
+        eager.zero_grad(set_to_none=True)
+        xa = xs[i].clone().requires_grad_(True)
+        ya = eager(xa)
+        ya.backward(gys[i])
+        yb = cap.step(xs[i], gys[i])
+        torch.cuda.synchronize()
+        print(f"step {i}: tiling={tiling} dtype={dtype}", flush=True)
+        assert torch.equal(ya, yb), f"output differs at step {i}"
+        for name, ga, gb in zip(("x", "weight", "theta", "bias"), _grads(eager, xa), _grads(cap_layer, x_static)):
+            assert gb is not None, name
+            assert torch.equal(ga, gb), f"{name} gradient differs at step {i}"
+        assert int(eager.step_count) == int(cap_layer.step_count) == i + 1
+        assert cap_layer._host_step == i + 1
+        assert torch.equal(eager.sigma_ema, cap_layer.sigma_ema), f"sigma EMA differs at step {i}"
+        assert torch.equal(eager.xmax_ema, cap_layer.xmax_ema), f"abs-max EMA differs at step {i}"
+        # the same in-place parameter update on both layers: the graph reads the live parameters
+        with torch.no_grad():
+            for pa, pb in ((eager.weight, cap_layer.weight), (eager.theta_beta, cap_layer.theta_beta),
+                           (eager.bias, cap_layer.bias)):
+                pa.add_(pa.grad, alpha=-1e-2)
+                pb.add_(pb.grad, alpha=-1e-2)
+    # the statistics were updated at steps 3 and 6, so they moved off their initial ones
+    assert not torch.equal(cap_layer.sigma_ema, torch.ones_like(cap_layer.sigma_ema))
+
+
+@pytest.mark.gpu
+def test_captured_forward_only_matches_eager():
+    eager, cap_layer = _pair(768, 10, "row", interval=256)
+    x = torch.zeros(32, 768, device="cuda")
+    cap = coset_amd.CapturedQATStep(cap_layer, x)
+    gen = torch.Generator(device="cuda").manual_seed(9)
+    for i in range(4):
+        xi = torch.randn(32, 768, device="cuda", generator=gen)
+        with torch.no_grad():
+            ya = eager(xi)
+        yb = cap.step(xi)
+        torch.cuda.synchronize()
+        assert torch.equal(ya, yb), f"forward differs at call {i}"
+    assert int(cap_layer.step_count) == int(eager.step_count) == 4
+
+
+@pytest.mark.gpu
+def test_captured_step_refuses_stale_mode():
+    _, L = _pair(64, 16, "row", interval=256)
+    x = torch.randn(8, 64, device="cuda", requires_grad=True)
+    cap = coset_amd.CapturedQATStep(L, x, torch.randn(8, 16, device="cuda"))
+    cap.step()
+    L.disable_quantization()
+    with pytest.raises(RuntimeError):
+        cap.step()
+
+
+def test_captured_step_needs_gpu_tensors():
+    L = coset_amd.create_e8_hnlq_linear(16, 8, device="cpu")
+    with pytest.raises(ValueError):
+        coset_amd.CapturedQATStep(L, torch.zeros(2, 16))
