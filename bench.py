@@ -17,7 +17,11 @@ The other BASELINE configurations are measured alongside under "extra":
       (core and legacy-Q residuals, tiled prepared and raw words, LDS-table method)
   c5  QAT linear forward + backward, BERT-base shapes, 4096 bf16 tokens
 The roofline object is the C2 codec kernel's (HIP events on its launch
-stream); cpu_baseline is the C oracle on the host, single thread.
+stream).  cpu_baseline is the C restatement of the reference algorithm
+(oracle/) on the host: every configuration is timed on all the host threads
+this process may use (capped at the box's 16-thread share) and on one thread,
+with the CPU model recorded; the top-level object is C2's, the others sit
+under extra.<config>.cpu_baseline.
 """
 from __future__ import annotations
 
@@ -37,6 +41,7 @@ BF16_MFMA_TFLOPS = 2500.0      # dense
 FP16_MFMA_TFLOPS = 2500.0
 C2_BLOCKS = 1 << 24
 C2_BYTES_PER_BLOCK = 32 + 4 + 32   # read x, write 2 u16 words, write decoded
+C2_WARM_S = 0.3                    # seconds of untimed C2 steps before the timed ones
 METRIC = "E8 HNLQ encode+decode Gblocks/s & HBM GB/s; vLUT matmul tokens/s at 4096²"
 
 
@@ -75,18 +80,193 @@ def gpu_time(torch, fn, steps, warmup, warm_s=0.0):
     return e0.elapsed_time(e1) / 1e3 / steps, wall / steps
 
 
-def cpu_baseline(x_sample: np.ndarray):
-    """The C oracle (single thread) on a bounded slice of the same workload."""
+# ---------------------------------------------------------------------------
+# host-CPU baseline: the C oracle (a restatement of the reference algorithm,
+# test infrastructure) run on the host cores.  ctypes releases the GIL for the
+# duration of each C call, so a thread pool runs the chunks in parallel.
+# ---------------------------------------------------------------------------
+CPU_THREAD_CAP = 16            # one GPU's share of the box's cores
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_threads() -> int:
+    return max(1, min(len(os.sched_getaffinity(0)), CPU_THREAD_CAP))
+
+
+def _run_pool(tasks, threads):
+    from concurrent.futures import ThreadPoolExecutor
+    if threads == 1:
+        return [t() for t in tasks]
+    with ThreadPoolExecutor(threads) as ex:
+        return list(ex.map(lambda t: t(), tasks))
+
+
+def _cpu_time(make_tasks, threads, reps):
+    """Median wall seconds over `reps` runs of the task list on `threads`
+    threads (one untimed run first)."""
+    _run_pool(make_tasks(), threads)
+    ts = []
+    for _ in range(reps):
+        tasks = make_tasks()
+        t0 = time.perf_counter()
+        _run_pool(tasks, threads)
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts))
+
+
+def _cpu_record(value_all, value_one, unit, threads, sample, method, **kw):
+    rec = {"value": value_all, "unit": unit, "cores": threads, "kind": "port", "sample": sample,
+           "value_1thread": value_one, "threads": threads, "host_threads_visible": len(os.sched_getaffinity(0)),
+           "cpu_model": cpu_model(), "method": method}
+    rec.update(kw)
+    return rec
+
+
+def cpu_c2(x_host: np.ndarray, one_thread_blocks: int):
+    """C2 on the host: the oracle's e8_encode + e8_decode (q4 M2 beta 1) over
+    all blocks in chunks of 2^20, and on one thread over a leading slice."""
     from oracle import oracle as O
-    O.lib()
-    t0 = time.perf_counter()
-    codes = O.e8_encode(x_sample, 4, 2, 1.0)
-    O.e8_decode(codes, 4, 2, 1.0)
-    dt = time.perf_counter() - t0
-    n = x_sample.shape[0]
-    return {"value": n / dt / 1e9, "unit": "Gblocks/s", "cores": 1, "kind": "port",
-            "sample": f"first {n} of the 2^24 C2 blocks (q4 M2 beta 1), C oracle encode+decode, "
-                      f"{dt:.1f} s on one host core"}
+    chunk = 1 << 20
+    n = x_host.shape[0]
+    thr = cpu_threads()
+
+    def tasks(xs):
+        return [lambda c=xs[i:i + chunk]: O.e8_decode(O.e8_encode(c, 4, 2, 1.0), 4, 2, 1.0)
+                for i in range(0, xs.shape[0], chunk)]
+    t_all = _cpu_time(lambda: tasks(x_host), thr, 1)
+    xs1 = x_host[:one_thread_blocks]
+    t_one = _cpu_time(lambda: tasks(xs1), 1, 1)
+    return _cpu_record(n / t_all / 1e9, xs1.shape[0] / t_one / 1e9, "Gblocks/s", thr,
+                       f"all {n} C2 blocks on {thr} threads ({t_all:.2f} s); the first {xs1.shape[0]} "
+                       f"on one thread ({t_one:.2f} s)",
+                       "C oracle encode+decode in 2^20-block chunks, median of 1 run after 1 untimed run",
+                       chunk_blocks=chunk)
+
+
+def cpu_c3(x_host: np.ndarray, beta_host: np.ndarray, rows_one: int):
+    """C3 on the host: the oracle's layer-convention round trip (x * beta_row,
+    q16 M3, / beta_row, clamp 2) over the rows, chunked by 64 rows."""
+    from oracle import oracle as O
+    rows, cols = x_host.shape
+    thr = cpu_threads()
+    step = 64
+
+    def tasks(r1):
+        return [lambda r=r: O.layer_quant(x_host[r:r + step], beta_host[r:r + step], 16, 3, 2.0)
+                for r in range(0, r1, step)]
+    t_all = _cpu_time(lambda: tasks(rows), thr, 1)
+    t_one = _cpu_time(lambda: tasks(rows_one), 1, 1)
+    n_all, n_one = rows * cols // 8, rows_one * cols // 8
+    return _cpu_record(n_all / t_all / 1e9, n_one / t_one / 1e9, "Gblocks/s", thr,
+                       f"all {n_all} C3 blocks on {thr} threads ({t_all:.2f} s); {n_one} blocks "
+                       f"({rows_one} rows) on one thread ({t_one:.2f} s)",
+                       "C oracle layer quantizer (fp32 upcast of the bf16 input) in 64-row chunks",
+                       chunk_blocks=step * cols // 8)
+
+
+def cpu_c4(words_host: np.ndarray, act_host: np.ndarray):
+    """C4 on the host for one batch: the reference's one-sided vLUT method
+    (a q^8-entry table per activation block, then the lookup sum over the
+    codes) with the residual table computed once.  All threads: tokens x
+    k-block chunks spread over the pool; one thread: one token's worth."""
+    from oracle import oracle as O
+    R = O.residual_table(4, legacy=False, strided=True)
+    rows, kb, M = words_host.shape
+    B = act_host.shape[0]
+    thr = cpu_threads()
+    parts = max(1, -(-thr // B))          # split k so that every thread has work
+    kstep = -(-kb // parts)
+
+    def tasks(tokens):
+        return [lambda t=t, k0=k0: O.vlut_onesided_rows(words_host, R, act_host[t], 4, k0, min(kb, k0 + kstep))
+                for t in range(tokens) for k0 in range(0, kb, kstep)]
+
+    t_all = _cpu_time(lambda: tasks(B), thr, 1)
+    t_one = _cpu_time(lambda: [lambda: O.vlut_onesided_rows(words_host, R, act_host[0], 4)], 1, 1)
+    return _cpu_record(B / t_all, 1 / t_one, "tokens/s", thr,
+                       f"B={B}: all {B} tokens on {thr} threads ({t_all:.2f} s); one token on one thread "
+                       f"({t_one:.2f} s)",
+                       "C oracle one-sided vLUT (q^8 table per 8-wide activation block, residuals computed "
+                       "once) + lookup sum, fp32 tables, float64 row sums")
+
+
+def cpu_c5(fin: int, fout: int, W: np.ndarray, beta: np.ndarray, x: np.ndarray, gy: np.ndarray):
+    """C5 on the host, one fwd+bwd step in fp32 as the reference (which has
+    no bf16 path): the oracle's weight quantizer (row chunks over the pool),
+    the three dense products in torch on the CPU (F.linear, as the
+    reference's layer), and the straight-through backward's closed form."""
+    import torch
+    from oracle import oracle as O
+    thr = cpu_threads()
+    xt = torch.from_numpy(x)
+    gt = torch.from_numpy(gy)
+
+    def step(threads):
+        torch.set_num_threads(threads)
+        chunk = max(1, fout // threads)
+        parts = _run_pool([lambda r=r: O.layer_quant(W[r:r + chunk], beta[r:r + chunk], 4, 2, 2.0)
+                           for r in range(0, fout, chunk)], threads)
+        Wq = np.concatenate([p[0] for p in parts])
+        qraw = np.concatenate([p[1] for p in parts])
+        Wqt = torch.from_numpy(Wq)
+        y = torch.nn.functional.linear(xt, Wqt)          # [4096, fout]
+        dx = gt @ Wqt                                     # [4096, fin]
+        dWq = (gt.t() @ xt).numpy()                       # [fout, fin]
+        db = gt.sum(0)
+        O.layer_backward(dWq, W, qraw, beta, 2.0)
+        return y, dx, db
+
+    def timed(threads, reps):
+        step(threads)
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            step(threads)
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts))
+    n_threads_before = torch.get_num_threads()
+    try:
+        t_all = timed(thr, 3)
+        t_one = timed(1, 1)
+    finally:
+        torch.set_num_threads(n_threads_before)
+    return _cpu_record(4096 / t_all, 4096 / t_one, "tokens/s", thr,
+                       f"{fin}x{fout}, 4096 fp32 tokens: {t_all * 1e3:.1f} ms per step on {thr} threads, "
+                       f"{t_one * 1e3:.1f} ms on one",
+                       "C oracle weight quantizer + torch CPU fp32 products + closed-form STE backward "
+                       "(numpy float64), median of 3 (all threads) / 1 (one thread) after 1 untimed step")
+
+
+def cpu_c1(W: np.ndarray, beta: np.ndarray, x: np.ndarray, bias: np.ndarray):
+    """C1 on the host: the oracle's weight quantizer (960 blocks) + the
+    32 x 768 x 10 product in numpy, median of 50 forwards.  The work is too
+    small to split: the all-thread figure is the same single call."""
+    from oracle import oracle as O
+
+    def fwd():
+        Wq = O.layer_quant(W, beta, 4, 2, 2.0)[0]
+        return x @ Wq.T + bias
+    fwd()
+    ts = []
+    for _ in range(50):
+        t0 = time.perf_counter()
+        fwd()
+        ts.append(time.perf_counter() - t0)
+    t = float(np.median(ts))
+    return _cpu_record(1e6 * t, 1e6 * t, "us per forward", 1,
+                       "one 768->10 forward on a 32 x 768 fp32 batch",
+                       "C oracle weight quantizer + numpy product, median of 50 after 1 untimed",
+                       higher_is_better=False)
 
 
 # ---------------------------------------------------------------------------
@@ -101,7 +281,9 @@ def bench_c2(torch, ca, args):
     def step():
         ca.hnlq_roundtrip(x, 4, 2, 1.0, packed_out=packed, decoded_out=out)
 
-    kernel_s, wall_s = gpu_time(torch, step, args.steps, args.warmup)
+    # the GPU needs ~20 launches of sustained load to leave its idle clock,
+    # whatever --warmup says: warm for C2_WARM_S seconds before timing
+    kernel_s, wall_s = gpu_time(torch, step, args.steps, args.warmup, C2_WARM_S)
 
     from oracle import oracle as O
     idx = torch.randint(0, n, (4096,), device=dev, generator=g)
@@ -111,7 +293,7 @@ def bench_c2(torch, ca, args):
           and np.array_equal(out[idx].cpu().numpy(), O.e8_decode(codes, 4, 2, 1.0)))
     if not ok:
         sys.exit("parity spot check FAILED: GPU codes differ from the oracle")
-    cpu = cpu_baseline(x[: args.cpu_sample].cpu().numpy()) if args.cpu_sample > 0 else None
+    cpu = cpu_c2(x.cpu().numpy(), 1 << 21) if args.cpu else None
     del x, packed, out
     return kernel_s, wall_s, cpu
 
@@ -173,6 +355,11 @@ def bench_c1(torch, ca, args):
         k2, w2 = gpu_time(torch, lambda: layer2(x), 200, 20)
     res["nondegenerate"] = {"workload": "Delta0 1.5, W ~ N(0,1)", "nonzero_weight_frac": round(nz, 3),
                             "us_per_forward_gpu": round(k2 * 1e6, 2), "us_per_forward_wall": round(w2 * 1e6, 2)}
+    if args.cpu:
+        with torch.no_grad():
+            beta = layer._beta().float().cpu().numpy()
+        res["cpu_baseline"] = cpu_c1(layer.weight.detach().cpu().numpy(), beta, x.cpu().numpy(),
+                                     layer.bias.detach().cpu().numpy())
     return res
 
 
@@ -231,10 +418,13 @@ def bench_c3(torch, ca, args):
 
     k, w = gpu_time(torch, step, 100, 3, 0.1)
     nbytes = 60 * n
-    return {"workload": "C3 2^22 Student-t(3) blocks clipped +-2, bf16 in, q16 M3, per-row beta, clamp 2",
-            "gblocks_per_s": round(n / k / 1e9, 3), "kernel_us": round(k * 1e6, 1),
-            "hbm_gbs": round(nbytes / k / 1e9, 1), "frac_hbm": round(nbytes / k / 1e9 / HBM_PEAK_GBS, 4),
-            "bytes_per_block": 60}
+    res = {"workload": "C3 2^22 Student-t(3) blocks clipped +-2, bf16 in, q16 M3, per-row beta, clamp 2",
+           "gblocks_per_s": round(n / k / 1e9, 3), "kernel_us": round(k * 1e6, 1),
+           "hbm_gbs": round(nbytes / k / 1e9, 1), "frac_hbm": round(nbytes / k / 1e9 / HBM_PEAK_GBS, 4),
+           "bytes_per_block": 60}
+    if args.cpu:
+        res["cpu_baseline"] = cpu_c3(x.float().cpu().numpy(), beta.cpu().numpy(), 128)
+    return res
 
 
 def graph_time(torch, fn, n_calls=20, reps=10):
@@ -266,6 +456,29 @@ def graph_time(torch, fn, n_calls=20, reps=10):
     return e0.elapsed_time(e1) / 1e3 / (reps * n_calls)
 
 
+def cold_time(torch, fn, flush, reps=25):
+    """Median GPU time of one call of fn with the caches cold: before each
+    call a 1 GiB buffer is written, which evicts the 256 MB Infinity Cache
+    (MALL) and the L2s, then HIP events bracket the call alone (the write
+    keeps the GPU busy while the host queues the call, so no host time
+    leaks into the interval)."""
+    fn()
+    torch.cuda.synchronize()
+    evs = []
+    for i in range(reps):
+        flush.fill_(float(i))
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        evs.append((e0, e1))
+    torch.cuda.synchronize()
+    return float(np.median([a.elapsed_time(b) for a, b in evs])) / 1e3
+
+
+C4_CODE_BYTES = 4096 * 512 * 2 * 2      # uint16 level words [4096, 512, 2]: the algorithmic weight bytes
+
+
 def bench_c4(torch, ca, args):
     g = torch.Generator(device="cuda").manual_seed(5)
     W = 0.02 * torch.randn((4096, 4096), device="cuda", generator=g)
@@ -276,10 +489,15 @@ def bench_c4(torch, ca, args):
     scale = torch.full((4096,), 0.02, device="cuda")
     del W
     res = {"workload": "C4 vLUT matmul 4096x4096 q4 M2 codes (8 MiB uint16 words; 16 MiB tiled prepared or "
-                       "decoded), "
-                       "fp16 activations, fp32 out; us_graph = per call replayed from a HIP graph, "
-                       "us_eager = per call from Python", "batches": {}}
+                       "decoded), fp16 activations, fp32 out; us_graph = per call replayed from a HIP graph "
+                       "(weights warm in the 256 MB MALL), us_cold = one call after a 1 GiB write evicted the "
+                       "caches (median of 25), us_eager = per call from Python",
+           "algorithmic_bytes": "8 MiB codes + B * 8 KiB fp16 activations + B * 16 KiB fp32 output "
+                                "(frac_hbm*); format_bytes counts the prepared format actually read",
+           "batches": {}}
     ws = torch.empty(64 * 4096 * 64, dtype=torch.float32, device="cuda")
+    flush = torch.empty(1 << 28, dtype=torch.float32, device="cuda")
+    words_host = words.cpu().numpy().astype(np.uint32) if args.cpu else None
     for B in (1, 8, 64):
         a = torch.randn((B, 4096), device="cuda", generator=g).to(torch.float16)
         row = {}
@@ -289,16 +507,25 @@ def bench_c4(torch, ca, args):
             fn = lambda: ca.vlut_matmul(wts, a, 4, scale=scale, method=m, workspace=ws)
             k_eager, _ = gpu_time(torch, fn, 50 if m == "lds" else 100, 5, 0.05)
             k = graph_time(torch, fn)
+            kc = cold_time(torch, fn, flush)
             wbytes = wts.data.numel() * 4 if isinstance(wts, ca.PreparedWords) else wts.numel() * wts.element_size()
-            nbytes = wbytes + B * 4096 * 2 + B * 4096 * 4
+            io_bytes = B * 4096 * 2 + B * 4096 * 4
+            nbytes = C4_CODE_BYTES + io_bytes
             flops = 2.0 * B * 4096 * 4096
             row[method] = {"tokens_per_s": round(B / k, 1), "us_graph": round(k * 1e6, 2),
-                           "us_eager": round(k_eager * 1e6, 2),
+                           "us_cold": round(kc * 1e6, 2), "us_eager": round(k_eager * 1e6, 2),
+                           "tokens_per_s_cold": round(B / kc, 1),
                            "gbs_algorithmic": round(nbytes / k / 1e9, 1),
                            "frac_hbm": round(nbytes / k / 1e9 / HBM_PEAK_GBS, 4),
+                           "frac_hbm_cold": round(nbytes / kc / 1e9 / HBM_PEAK_GBS, 4),
+                           "format_bytes": wbytes + io_bytes,
+                           "frac_hbm_format_cold": round((wbytes + io_bytes) / kc / 1e9 / HBM_PEAK_GBS, 4),
                            "dense_equiv_tflops": round(flops / k / 1e12, 2),
                            "frac_fp16_mfma": round(flops / k / 1e12 / FP16_MFMA_TFLOPS, 5)}
         res["batches"][str(B)] = row
+        if args.cpu:
+            row["cpu_baseline"] = cpu_c4(words_host, a.float().cpu().numpy())
+    del flush
     return res
 
 
@@ -332,6 +559,13 @@ def bench_c5(torch, ca, args):
                                                     "ms": round(kg * 1e3, 3), "ms_wall": round(wg * 1e3, 3),
                                                     "tflops": round(flops / kg / 1e12, 1),
                                                     "frac_bf16_mfma": round(flops / kg / 1e12 / BF16_MFMA_TFLOPS, 4)}}
+        if args.cpu:
+            with torch.no_grad():
+                beta = layer._beta().float().cpu().numpy()
+            res["shapes"][f"{fin}x{fout}"]["cpu_baseline"] = cpu_c5(
+                fin, fout, layer.weight.detach().cpu().numpy(), beta, x.detach().float().cpu().numpy(),
+                gy.float().cpu().numpy())
+        del cap, layer, x, gy, xs
     return res
 
 
@@ -342,8 +576,8 @@ def main():
     # the GPU takes tens of milliseconds of sustained load to reach its
     # steady clock: 200 untimed C2 steps are about 45 ms
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--cpu-sample", type=int, default=1 << 24,
-                    help="C2 blocks timed on the host CPU oracle (0 skips it)")
+    ap.add_argument("--no-cpu", dest="cpu", action="store_false",
+                    help="skip the host-CPU baselines (the C oracle on the host cores)")
     ap.add_argument("--only", default="c1,c2,c2codes,c2api,c3,c4,c5", help="comma list of workloads to run")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 512 MiB device copy (HBM counter calibration)")
@@ -389,8 +623,12 @@ def main():
             "ms_per_step": round(wall_s * 1e3, 4),
             "hbm_gbs": round(achieved, 1),
             "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile()},
+                         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(),
+                         "traffic_source": "stored: rocprofv3 PMC FETCH_SIZE + WRITE_SIZE of this kernel at this "
+                                           "size, calibrated on a device copy "
+                                           "(profiles/hnlq_roundtrip_c2_traffic.json), not measured in this run"},
             "kernel_us": round(kernel_s * 1e6, 2),
+            "warm_s": C2_WARM_S,
             "parity": "bit-exact vs oracle on 4096 sampled blocks",
             "cpu_baseline": cpu,
         })

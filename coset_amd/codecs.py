@@ -41,12 +41,32 @@ def word_dtype(q: int) -> torch.dtype:
 
 def _scale_args(beta, beta_row, blocks_per_row, n):
     if beta_row is not None:
+        br = on_gpu(beta_row).float().contiguous()
+        if br.numel() == 0:
+            raise ValueError("beta_row is empty")
         if blocks_per_row is None:
-            blocks_per_row = n // beta_row.numel()
-        return _lib.SCALE_LAYER, 1.0, beta_row.contiguous(), int(blocks_per_row)
+            blocks_per_row = n // br.numel()
+        if br.numel() * int(blocks_per_row) != n:
+            raise ValueError(f"beta_row holds {br.numel()} values for {blocks_per_row} blocks each, "
+                             f"but the input has {n} blocks")
+        return _lib.SCALE_LAYER, 1.0, br, int(blocks_per_row)
     if beta is None:
         return _lib.SCALE_NONE, 1.0, None, 0
     return _lib.SCALE_CODEC, float(beta), None, 0
+
+
+def _dither(dither, n):
+    """(dither tensor, stride): one [8] vector broadcast (stride 0) or one
+    row per block [n, 8] (stride 8); any other length is an error, as the
+    reference's broadcast x / beta + dither would raise."""
+    if dither is None:
+        return None, 0
+    d = on_gpu(dither).float().contiguous()
+    if d.numel() == 8:
+        return d, 0
+    if d.numel() == 8 * n:
+        return d, 8
+    raise ValueError(f"dither must hold 8 or {8 * n} values, got {d.numel()}")
 
 
 def hnlq_encode(x: torch.Tensor, q: int = 4, M: int = 2, beta: Optional[float] = 1.0, *,
@@ -63,11 +83,7 @@ def hnlq_encode(x: torch.Tensor, q: int = 4, M: int = 2, beta: Optional[float] =
     mode, b, brow, bpr = _scale_args(beta, beta_row, blocks_per_row, n)
     packed = torch.empty((n, M), dtype=word_dtype(q), device=xg.device)
     codes = torch.empty((n, M, 8), dtype=torch.float32, device=xg.device) if return_codes else None
-    d = None
-    ds = 0
-    if dither is not None:
-        d = on_gpu(dither).float().contiguous()
-        ds = 0 if d.numel() == 8 else 8
+    d, ds = _dither(dither, n)
     _lib.call("coset_e8_hnlq_encode", _lib.ptr(xg), _lib.dtype_code(xg.dtype), n, mode, b,
               _lib.ptr(brow), bpr, _lib.ptr(d), ds, int(q), int(M), _lib.ptr(packed),
               _lib.ptr(codes), _lib.stream_of(xg))

@@ -400,6 +400,40 @@ int coset_e8_qat_bwd_theta(const void* gWq, int g_dtype, const float* W, const v
                      "qat backward launch");
 }
 
+int64_t coset_colsum_workspace_floats(int64_t rows, int64_t cols)
+{
+    if (rows < 0 || cols < 0) return 0;
+    return coset::colsum_workspace_floats(rows, cols);
+}
+
+int coset_colsum(const void* g, int dtype, int64_t rows, int64_t cols, float* out, float* workspace,
+                 int64_t workspace_floats, void* stream)
+{
+    if (rows < 0 || cols < 0) return fail(COSET_EINVAL, "rows, cols must be >= 0");
+    if (dtype != COSET_F32 && dtype != COSET_BF16 && dtype != COSET_F16)
+        return fail(COSET_EUNSUPPORTED, "gradient dtype %d not supported (fp32, bf16, fp16)", dtype);
+    if (cols % 8) return fail(COSET_EINVAL, "cols must be a multiple of 8, got %lld", (long long)cols);
+    if (cols > 0 && (!out || (rows > 0 && !g))) return fail(COSET_EINVAL, "NULL buffer");
+    if (rows > 0 && !aligned(g, 16)) return fail(COSET_EINVAL, "g must be 16-byte aligned");
+    int64_t need = coset::colsum_workspace_floats(rows, cols);
+    if (cols > 0 && need > 0 && (!workspace || workspace_floats < need))
+        return fail(COSET_EINVAL, "workspace too small: %lld floats needed", (long long)need);
+    if ((rows + 63) / 64 > 65535) return fail(COSET_EINVAL, "too many rows");
+    return check_hip(coset::launch_colsum(g, dtype, rows, cols, out, workspace, (hipStream_t)stream),
+                     "column sum launch");
+}
+
+int coset_qat_stats_update(const float* W, int64_t tiles, int64_t tile_size, double momentum, float* sigma_ema,
+                           float* xmax_ema, void* stream)
+{
+    if (tiles < 0 || tile_size < 2) return fail(COSET_EINVAL, "tiles >= 0 and tile_size >= 2 required");
+    if (tiles > 0x7fffffff) return fail(COSET_EINVAL, "too many tiles");
+    if (tiles > 0 && (!W || !sigma_ema || !xmax_ema)) return fail(COSET_EINVAL, "NULL buffer");
+    if (tile_size == 8 && !aligned(W, 16)) return fail(COSET_EINVAL, "W must be 16-byte aligned");
+    return check_hip(coset::launch_qat_stats(W, tiles, tile_size, momentum, sigma_ema, xmax_ema, (hipStream_t)stream),
+                     "statistics launch");
+}
+
 int coset_vlut_build_one_sided(const float* queries, int64_t n_queries, int q, int legacy, float* vlut,
                                void* stream)
 {

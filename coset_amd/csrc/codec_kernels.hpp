@@ -42,7 +42,11 @@ __device__ __forceinline__ void theta_beta_terms(const ThetaBeta& tb, int64_t t,
     lo = fminf(lo, __fmul_rn(hi, 0.9f));
     *bmin = lo;
     *bmax = hi;
-    *sg = __fdiv_rn(1.f, __fadd_rn(1.f, expf(-tb.theta[t])));
+    // sigmoid = 1 / (1 + e) in fp32 with e = exp(-theta) rounded once to
+    // fp32 from a double-precision exp: the correctly rounded fp32 exp (but
+    // for double-rounding cases), which is what torch's CPU sigmoid gives on
+    // the reference's own layer goldens.
+    *sg = __fdiv_rn(1.f, __fadd_rn(1.f, (float)exp(-(double)tb.theta[t])));
 }
 
 __device__ __forceinline__ float theta_beta(const ThetaBeta& tb, int64_t t)
@@ -169,6 +173,11 @@ __device__ __forceinline__ void lds_barrier()
 
 // Backward of the QAT weight quantizer (qat.hip).
 // dbdt (nullable): also write dtheta[t] = dbeta[t] * dbdt[t].
+int64_t colsum_workspace_floats(int64_t rows, int64_t cols);
+hipError_t launch_colsum(const void* g, int dtype, int64_t rows, int64_t cols, float* out, float* workspace,
+                         hipStream_t s);
+hipError_t launch_qat_stats(const float* W, int64_t tiles, int64_t n, double momentum, float* sigma_ema,
+                            float* xmax_ema, hipStream_t s);
 hipError_t launch_qat_bwd(const void* g, int g_dtype, const float* W, const void* packed,
                           const float* beta, int64_t n_blocks, int64_t blocks_per_tile, float clip,
                           int q, int M, float* dW, float* dbeta, const float* dbdt, float* dtheta,

@@ -14,6 +14,8 @@
 // One workgroup per tile (row tiling: a tile is an output row of
 // blocks_per_tile 8-wide blocks) reduces dbeta with a wave reduction and one
 // LDS pass; block tiling (one block per tile) needs no reduction.
+#include <hip/hip_fp16.h>
+
 #include "codec_kernels.hpp"
 #include "tables.hpp"
 
@@ -180,6 +182,223 @@ static hipError_t launch_bwd_q(const QatBwdArgs& a, hipStream_t s)
         int64_t tiles = a.n_blocks / a.blocks_per_tile;
         hipLaunchKernelGGL(qat_bwd_tile_kernel<Q>, dim3((unsigned)tiles), dim3(256), 0, s, a);
     }
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Statistics update (HNLQLinearQAT._gather_stats, coset/core/layers.py:366-379)
+// over tiles of n contiguous weights (row tiling: a row; block tiling: one
+// 8-wide block):
+//   sigma = std(tile) + 1e-8,  xmax = max |tile| + 1e-8
+//   sigma_ema = sigma_ema * m + (1 - m) * sigma   (and xmax_ema likewise)
+// The standard deviation follows the reference's CPU arithmetic: the
+// unbiased variance accumulated in double, its double square root rounded
+// once to fp32; the rest are single fp32 operations in the reference's order
+// with the scalars rounded to fp32.  Two passes in double (mean, then the
+// squared deviations) keep the variance exact to ~1e-16 relative, so the
+// fp32 result matches a double-accumulating reduction in any order.
+struct StatsArgs {
+    const float* W;
+    int64_t tiles, n;           // tiles of n weights
+    float m, one_minus_m, eps;  // fp32 roundings of m, 1 - m, 1e-8
+    float* sigma_ema;
+    float* xmax_ema;
+};
+
+__device__ __forceinline__ void stats_write(const StatsArgs& a, int64_t t, double m2, float amax)
+{
+    float sd = (float)sqrt(m2 / (double)(a.n - 1));
+    float s1 = __fadd_rn(sd, a.eps);
+    float x1 = __fadd_rn(amax, a.eps);
+    a.sigma_ema[t] = __fadd_rn(__fmul_rn(a.sigma_ema[t], a.m), __fmul_rn(a.one_minus_m, s1));
+    a.xmax_ema[t] = __fadd_rn(__fmul_rn(a.xmax_ema[t], a.m), __fmul_rn(a.one_minus_m, x1));
+}
+
+// one workgroup (256 threads) per tile
+__global__ void __launch_bounds__(256) qat_stats_tile_kernel(StatsArgs a)
+{
+    const int64_t t = blockIdx.x;
+    const float* w = a.W + t * a.n;
+    __shared__ double s_d[4];
+    __shared__ float s_f[4];
+    double sum = 0.0;
+    float amax = 0.f;
+    for (int64_t i = threadIdx.x; i < a.n; i += blockDim.x) {
+        float v = w[i];
+        sum += (double)v;
+        amax = fmaxf(amax, fabsf(v));
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        sum += __shfl_down(sum, off, 64);
+        amax = fmaxf(amax, __shfl_down(amax, off, 64));
+    }
+    if ((threadIdx.x & 63) == 0) {
+        s_d[threadIdx.x >> 6] = sum;
+        s_f[threadIdx.x >> 6] = amax;
+    }
+    __syncthreads();
+    const double mean = ((s_d[0] + s_d[1]) + (s_d[2] + s_d[3])) / (double)a.n;
+    amax = fmaxf(fmaxf(s_f[0], s_f[1]), fmaxf(s_f[2], s_f[3]));
+    __syncthreads();
+    double m2 = 0.0;
+    for (int64_t i = threadIdx.x; i < a.n; i += blockDim.x) {
+        double d = (double)w[i] - mean;
+        m2 += d * d;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m2 += __shfl_down(m2, off, 64);
+    if ((threadIdx.x & 63) == 0) s_d[threadIdx.x >> 6] = m2;
+    __syncthreads();
+    if (threadIdx.x == 0) stats_write(a, t, (s_d[0] + s_d[1]) + (s_d[2] + s_d[3]), amax);
+}
+
+// one thread per 8-wide tile (block tiling)
+__global__ void __launch_bounds__(256) qat_stats_block_kernel(StatsArgs a)
+{
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= a.tiles) return;
+    const float4* p = reinterpret_cast<const float4*>(a.W + t * 8);
+    float4 u = p[0], v = p[1];
+    float x[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+    double sum = 0.0;
+    float amax = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        sum += (double)x[j];
+        amax = fmaxf(amax, fabsf(x[j]));
+    }
+    const double mean = sum / 8.0;
+    double m2 = 0.0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        double d = (double)x[j] - mean;
+        m2 += d * d;
+    }
+    stats_write(a, t, m2, amax);
+}
+
+// ---------------------------------------------------------------------------
+// Bias gradient of the layer's product y = x W_q^T + b (coset/core/layers.py:
+// 478): db[c] = sum_t g[t, c] over the tokens, accumulated in fp32 in a fixed
+// order whatever g's dtype (fp32, bf16 or fp16).  Stage 1: workgroups of 256
+// threads = 64 column threads (8 consecutive columns each: one 16-byte bf16
+// load or two fp32 loads) x 4 row threads, over a chunk of kColsumChunk rows,
+// write one fp32 partial per (chunk, column); stage 2 adds the chunks'
+// partials of a column in order.  Deterministic: no atomics.
+constexpr int kColsumChunk = 64;
+
+template <int DT>
+__device__ __forceinline__ void load8(const void* g, int64_t idx, float v[8])
+{
+    if (DT == DT_F32) {
+        const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(g) + idx);
+        float4 a = p[0], b = p[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+        uint4 u = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(g) + idx);
+        uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (DT == DT_BF16) {
+                v[2 * j] = __uint_as_float(w[j] << 16);
+                v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+            } else {
+                v[2 * j] = __half2float(__ushort_as_half((unsigned short)(w[j] & 0xffffu)));
+                v[2 * j + 1] = __half2float(__ushort_as_half((unsigned short)(w[j] >> 16)));
+            }
+        }
+    }
+}
+
+template <int DT>
+__global__ void __launch_bounds__(256) colsum_partial_kernel(const void* g, int64_t rows, int64_t cols,
+                                                             float* partial)
+{
+    const int64_t c8 = (int64_t)blockIdx.x * 64 + (threadIdx.x & 63);
+    const int rt = threadIdx.x >> 6;
+    const int64_t r0 = (int64_t)blockIdx.y * kColsumChunk;
+    const int64_t r1 = r0 + kColsumChunk < rows ? r0 + kColsumChunk : rows;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    const bool live = 8 * c8 < cols;
+    if (live) {
+        for (int64_t r = r0 + rt; r < r1; r += 4) {
+            float v[8];
+            load8<DT>(g, r * cols + 8 * c8, v);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[j] = __fadd_rn(acc[j], v[j]);
+        }
+    }
+    __shared__ float s[3][64][9];
+    if (rt > 0) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s[rt - 1][threadIdx.x & 63][j] = acc[j];
+    }
+    __syncthreads();
+    if (rt == 0 && live) {
+        float* out = partial + (int64_t)blockIdx.y * cols + 8 * c8;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int l = threadIdx.x & 63;
+            out[j] = __fadd_rn(__fadd_rn(acc[j], s[0][l][j]), __fadd_rn(s[1][l][j], s[2][l][j]));
+        }
+    }
+}
+
+__global__ void __launch_bounds__(256) colsum_final_kernel(const float* partial, int64_t chunks, int64_t cols,
+                                                           float* out)
+{
+    const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= cols) return;
+    float s = 0.f;
+    for (int64_t k = 0; k < chunks; ++k) s = __fadd_rn(s, partial[k * cols + c]);
+    out[c] = s;
+}
+
+int64_t colsum_workspace_floats(int64_t rows, int64_t cols)
+{
+    return ((rows + kColsumChunk - 1) / kColsumChunk) * cols;
+}
+
+hipError_t launch_colsum(const void* g, int dtype, int64_t rows, int64_t cols, float* out, float* workspace,
+                         hipStream_t s)
+{
+    if (cols == 0) return hipSuccess;
+    if (rows == 0) {
+        hipLaunchKernelGGL(colsum_final_kernel, dim3((unsigned)((cols + 255) / 256)), dim3(256), 0, s,
+                           (const float*)workspace, (int64_t)0, cols, out);
+        return hipGetLastError();
+    }
+    const int64_t chunks = (rows + kColsumChunk - 1) / kColsumChunk;
+    dim3 grid((unsigned)((cols / 8 + 63) / 64), (unsigned)chunks);
+    if (dtype == DT_F32)
+        hipLaunchKernelGGL(colsum_partial_kernel<DT_F32>, grid, dim3(256), 0, s, g, rows, cols, workspace);
+    else if (dtype == DT_BF16)
+        hipLaunchKernelGGL(colsum_partial_kernel<DT_BF16>, grid, dim3(256), 0, s, g, rows, cols, workspace);
+    else
+        hipLaunchKernelGGL(colsum_partial_kernel<DT_F16>, grid, dim3(256), 0, s, g, rows, cols, workspace);
+    hipLaunchKernelGGL(colsum_final_kernel, dim3((unsigned)((cols + 255) / 256)), dim3(256), 0, s,
+                       (const float*)workspace, chunks, cols, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_qat_stats(const float* W, int64_t tiles, int64_t n, double momentum, float* sigma_ema,
+                            float* xmax_ema, hipStream_t s)
+{
+    if (tiles == 0) return hipSuccess;
+    StatsArgs a{};
+    a.W = W;
+    a.tiles = tiles;
+    a.n = n;
+    a.m = (float)momentum;
+    a.one_minus_m = (float)(1.0 - momentum);
+    a.eps = 1e-8f;
+    a.sigma_ema = sigma_ema;
+    a.xmax_ema = xmax_ema;
+    if (n == 8)
+        hipLaunchKernelGGL(qat_stats_block_kernel, dim3((unsigned)((tiles + 255) / 256)), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL(qat_stats_tile_kernel, dim3((unsigned)tiles), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

@@ -283,6 +283,50 @@ class D4ThetaWeightQuant(torch.autograd.Function):
         return dW, dtheta.view(theta_shape), None, None, None, None, None, None, None, None
 
 
+def colsum(g2: torch.Tensor) -> torch.Tensor:
+    """sum over rows of a [rows, cols] fp32/bf16/fp16 tensor, accumulated in
+    fp32 in a fixed order (coset_colsum): the bias gradient of a product."""
+    g2 = g2.contiguous()
+    rows, cols = g2.shape
+    out = torch.empty(cols, dtype=torch.float32, device=g2.device)
+    need = int(_lib.load().coset_colsum_workspace_floats(rows, cols))
+    ws = torch.empty(max(need, 1), dtype=torch.float32, device=g2.device)
+    dt = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}[g2.dtype]
+    _lib.check("coset_colsum", _lib.fn("coset_colsum")(g2.data_ptr(), dt, rows, cols, out.data_ptr(), ws.data_ptr(),
+                                                       ws.numel(), _lib.stream_of(g2)))
+    return out
+
+
+class QATLinearFn(torch.autograd.Function):
+    """y = x W_q^T + b, the layer's F.linear (coset/core/layers.py:478): the
+    products run on hipBLASLt (torch.mm), the bias gradient is the fp32
+    column sum of the output gradient (coset_colsum) instead of a reduction
+    in the activation dtype, so a bf16 layer's fp32 bias gets an fp32-exact
+    sum of its gradient."""
+
+    @staticmethod
+    def forward(ctx, x, Wq, bias):
+        ctx.save_for_backward(x, Wq)
+        ctx.bias_dtype = None if bias is None else bias.dtype
+        return F.linear(x, Wq, None if bias is None else bias.to(x.dtype))
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, Wq = ctx.saved_tensors
+        g2 = gy.reshape(-1, gy.shape[-1])
+        dx = dW = db = None
+        if ctx.needs_input_grad[0]:
+            dx = (g2 @ Wq).reshape(x.shape)
+        if ctx.needs_input_grad[1]:
+            dW = g2.t() @ x.reshape(-1, x.shape[-1])
+        if ctx.bias_dtype is not None and ctx.needs_input_grad[2]:
+            if g2.shape[1] % 8 == 0 and g2.dtype in (torch.float32, torch.bfloat16, torch.float16):
+                db = colsum(g2).to(ctx.bias_dtype)
+            else:
+                db = g2.float().sum(0).to(ctx.bias_dtype)
+        return dx, dW, db
+
+
 class HNLQLinearQAT(nn.Module):
     """Hierarchical nested-lattice quantized linear layer with QAT cold start
     (coset/core/layers.py:166-658); same constructor, buffers, state_dict
@@ -399,7 +443,21 @@ class HNLQLinearQAT(nn.Module):
 
     # ------------------------------------------------------------------
     def _gather_stats(self, W_blocks):
-        """EMA of the unscaled weights' std and abs-max (layers.py:366-379)."""
+        """EMA of the unscaled weights' std and abs-max (layers.py:366-379).
+        On the GPU one kernel (coset_qat_stats_update) computes both
+        statistics and updates both buffers with the reference's CPU
+        arithmetic (variance in double)."""
+        if W_blocks.is_cuda and W_blocks.dtype == torch.float32 and self.sigma_ema.is_cuda:
+            Wc = W_blocks.detach().contiguous()
+            if self.tiling == "row":
+                tiles, size = self.out_features, self.blocks_per_row * self.block_size
+            else:
+                tiles, size = self.out_features * self.blocks_per_row, self.block_size
+            if self.sigma_ema.is_contiguous() and self.xmax_ema.is_contiguous() and size >= 2:
+                _lib.check("coset_qat_stats_update", _lib.fn("coset_qat_stats_update")(
+                    Wc.data_ptr(), tiles, size, float(self.ema_momentum), self.sigma_ema.data_ptr(),
+                    self.xmax_ema.data_ptr(), _lib.stream_of(Wc)))
+                return
         with torch.no_grad():
             m = self.ema_momentum
             if self.tiling == "row":
@@ -516,8 +574,10 @@ class HNLQLinearQAT(nn.Module):
         W_q = self._quantize_weights_as(wdt)
         if W_q.dtype != x.dtype:
             W_q = W_q.to(x.dtype)
-        b = self.bias.to(x.dtype) if self.bias is not None else None
-        x = F.linear(x, W_q, b)
+        if x.is_cuda:
+            x = QATLinearFn.apply(x, W_q, self.bias)
+        else:
+            x = F.linear(x, W_q, self.bias.to(x.dtype) if self.bias is not None else None)
         if self.quantize_activations and self.actq is not None:
             x = self.actq(x)
         return x
@@ -645,8 +705,14 @@ class CapturedQATStep:
     Semantics per ``step()`` are those of an eager step preceded by
     ``layer.zero_grad(set_to_none=True)``: the gradients of the layer's
     parameters and of the static input are overwritten, not accumulated, and
-    live in tensors owned by the graph (``param.grad`` after the first
-    step).  The device step counter advances inside the graph (the fused
+    live in tensors owned by the graph; every ``step()`` binds them to
+    ``param.grad`` (and ``x.grad``) again, so an optimizer loop that calls
+    ``opt.zero_grad()`` (which sets them to None) before ``step()`` and
+    ``opt.step()`` after it sees this step's gradients.  The graph reads the
+    parameters' storage: in-place updates (optimizer steps,
+    ``load_state_dict``) are seen by the next replay, while replacing a
+    parameter's storage (``load_weights``, ``load_from_linear``,
+    ``param.data = ...``) makes ``step()`` raise; capture again then.  The device step counter advances inside the graph (the fused
     kernel increments it); the host mirror of the counter and the
     every-``stat_update_interval``-steps EMA update of the weight statistics
     run eagerly, on the same stream, before the replay that reads them
@@ -689,6 +755,13 @@ class CapturedQATStep:
         with torch.cuda.graph(self.graph):
             self.y = self._run()
         layer._host_step = host_step
+        # the gradient tensors the graph writes, and the parameter storage it reads
+        self._grads = [(p, p.grad) for p in layer.parameters() if p.grad is not None]
+        self._x_grad = x.grad if x.requires_grad else None
+        self._storage = self._param_ptrs()
+
+    def _param_ptrs(self):
+        return [(name, p.data_ptr()) for name, p in self.layer.named_parameters()]
 
     def _zero_grads(self):
         self.layer.zero_grad(set_to_none=True)
@@ -711,16 +784,26 @@ class CapturedQATStep:
             raise RuntimeError("CapturedQATStep: quantization was switched since the capture; capture again")
         if grad_output is not None and self.grad_output is None:
             raise ValueError("CapturedQATStep: captured without a backward")
+        if self._param_ptrs() != self._storage:
+            raise RuntimeError("CapturedQATStep: a parameter's storage was replaced since the capture "
+                               "(load_weights / load_from_linear / .data assignment); capture again")
         with torch.no_grad():
             if x is not None:
                 self.x.copy_(x)
             if grad_output is not None:
                 self.grad_output.copy_(grad_output)
         if self._mode:
+            if L._host_step is None:       # after load_state_dict: mirror the loaded counter once
+                L._host_step = int(L.step_count)
             L._host_step += 1
             if L._host_step % L.stat_update_interval == 0:
                 L.gather_step_stats()
         self.graph.replay()
+        for p, g in self._grads:
+            if p.grad is not g:
+                p.grad = g
+        if self._x_grad is not None and self.x.grad is not self._x_grad:
+            self.x.grad = self._x_grad
         return self.y
 
 

@@ -98,10 +98,18 @@ class PackedLinear(nn.Module):
         # decoded once to 2 x_hat bytes where they fit (q = 4, M <= 2; q = 2, M <= 4), else cid | idx words
         fits = (self.q == 4 and self.M <= 2) or (self.q == 2 and self.M <= 4)
         self.prepared = vlut_prepare(words, self.q, legacy=False, layout="decoded" if fits else "tiled")
-        self.register_buffer("beta", tensors["beta"].to(words.device).float())
+        beta = tensors["beta"]
+        if beta.numel() != self.out_features:
+            raise ValueError(f"beta holds {beta.numel()} values, expected one per output row "
+                             f"({self.out_features})")
+        self.register_buffer("beta", beta.reshape(-1).to(words.device).float())
         bias = tensors.get("bias")
-        self.register_buffer("bias", None if bias is None else bias.to(words.device).float())
+        if bias is not None and bias.numel() != self.out_features:
+            raise ValueError(f"bias holds {bias.numel()} values, expected {self.out_features}")
         alpha = tensors.get("act_alpha")
+        if alpha is not None and ("act_bit_width" not in meta or alpha.numel() != 1):
+            raise ValueError("act_alpha needs one value and act_bit_width in the metadata")
+        self.register_buffer("bias", None if bias is None else bias.reshape(-1).to(words.device).float())
         self.register_buffer("act_alpha", None if alpha is None else alpha.to(words.device).float())
         self.act_qmax = 2 ** (int(meta["act_bit_width"]) - 1) - 1 if alpha is not None else 0
 

@@ -269,6 +269,10 @@ def vlut_matmul(words, act: torch.Tensor, q: int = 4, *, scale: Optional[torch.T
     s = None
     if scale is not None:
         s = on_gpu(scale).float().contiguous()
+        if s.numel() != rows:
+            raise ValueError(f"scale must hold one value per output row ({rows}), got {s.numel()}")
+    if scale_mode not in ("mul", "div"):
+        raise ValueError(f"scale_mode must be 'mul' or 'div', got {scale_mode!r}")
     out = torch.empty((B, rows), dtype=torch.float32, device=a.device)
     ws_n = workspace.numel() if workspace is not None else 0
     if bias is None and act_quant is None:

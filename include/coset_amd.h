@@ -29,6 +29,8 @@
  *                            unscale, clamp)       coset/core/layers.py:398-470
  *   coset_e8_qat_bwd         autograd of that chain through the straight-through
  *                            estimator             coset/core/layers.py:62-110, 428-463
+ *   coset_qat_stats_update   HNLQLinearQAT._gather_stats coset/core/layers.py:366-379
+ *   coset_colsum             bias gradient of the layer's F.linear  coset/core/layers.py:478
  *   coset_vlut_build_one_sided  vLUTManager.build_one_sided_vlut
  *                                                  coset/legacy/quant/vlut.py:72-117
  *   coset_vlut_lookup_dot    one-sided lookup sum  tests/legacy/test_one_sided_vlut_pytest.py:22-43
@@ -181,6 +183,28 @@ int coset_e8_qat_fwd_theta(const float* W, int64_t rows, int64_t cols, int64_t b
 int coset_e8_qat_bwd_theta(const void* gWq, int g_dtype, const float* W, const void* packed, const float* beta,
                            const float* dbeta_dtheta, int64_t rows, int64_t cols, int64_t blocks_per_tile,
                            float clip, int q, int M, float* dW, float* dbeta, float* dtheta, void* stream);
+
+/* Bias gradient of the layer's product (F.linear in HNLQLinearQAT.forward,
+ * coset/core/layers.py:478, whose autograd sums the output gradient over the
+ * tokens): out[c] = sum_t g[t, c] for g [rows, cols] (fp32, bf16 or fp16,
+ * cols % 8 == 0, 16-byte aligned), accumulated in fp32 in a fixed order
+ * (deterministic).  workspace: caller-owned fp32 scratch of
+ * coset_colsum_workspace_floats(rows, cols) floats. */
+int64_t coset_colsum_workspace_floats(int64_t rows, int64_t cols);
+int coset_colsum(const void* g, int dtype, int64_t rows, int64_t cols, float* out, float* workspace,
+                 int64_t workspace_floats, void* stream);
+
+/* The layer's periodic statistics update (HNLQLinearQAT._gather_stats,
+ * coset/core/layers.py:366-379, run every stat_update_interval steps at
+ * layers.py:408-413) over `tiles` tiles of tile_size contiguous fp32 weights
+ * (row tiling: tile_size = in_features; block tiling: 8):
+ *   sigma_ema[t] = sigma_ema[t] * m + (1 - m) * (std(tile) + 1e-8)
+ *   xmax_ema[t]  = xmax_ema[t]  * m + (1 - m) * (max |tile| + 1e-8)
+ * std unbiased; the reference's CPU arithmetic: variance in double, its
+ * square root rounded once to fp32, the EMA in fp32 with m and 1 - m rounded
+ * to fp32. */
+int coset_qat_stats_update(const float* W, int64_t tiles, int64_t tile_size, double momentum, float* sigma_ema,
+                           float* xmax_ema, void* stream);
 
 /* One-sided vLUTs (coset/legacy/quant/vlut.py:72-117): for each query
  * a[i, 0:8] writes vlut[i, idx] = <a, r(b_idx)> for all q^8 level words in

@@ -296,6 +296,43 @@ void or_build_one_sided_vlut(const float* a, int q, int legacy, float* vlut)
     }
 }
 
+void or_residual_table(int q, int legacy, int strided, float* R)
+{
+    uint32_t n = 1;
+    for (int j = 0; j < 8; ++j) n *= (uint32_t)q;
+    for (uint32_t i = 0; i < n; ++i) {
+        int32_t b[8];
+        or_unpack_index(i, q, b);
+        or_residual(b, q, legacy, strided, R + 8 * (size_t)i);
+    }
+}
+
+void or_vlut_onesided_accumulate(const uint32_t* words, int64_t rows, int64_t kb_total, int M, int q,
+                                 const float* R, const float* a, int64_t kb0, int64_t kb1, float* table,
+                                 double* acc)
+{
+    uint32_t n = 1;
+    for (int j = 0; j < 8; ++j) n *= (uint32_t)q;
+    for (int64_t k = kb0; k < kb1; ++k) {
+        const float* ak = a + 8 * k;
+        for (uint32_t i = 0; i < n; ++i) {
+            const float* r = R + 8 * (size_t)i;
+            float s = 0.0f;
+            for (int j = 0; j < 8; ++j) s += ak[j] * r[j];
+            table[i] = s;
+        }
+        for (int64_t o = 0; o < rows; ++o) {
+            const uint32_t* w = words + (o * kb_total + k) * M;
+            double v = 0.0, qm = 1.0;
+            for (int m = 0; m < M; ++m) {
+                v += qm * (double)table[w[m]];
+                qm *= q;
+            }
+            acc[o] += v;
+        }
+    }
+}
+
 void or_vlut_matmul(const uint32_t* words, const float* scale, int scale_mode,
                     const float* act, int64_t B, int64_t rows, int64_t K,
                     int q, int M, int legacy, float* out)

@@ -78,6 +78,21 @@ void or_vlut_matmul(const uint32_t* words, const float* scale, int scale_mode,
                     const float* act, int64_t B, int64_t rows, int64_t K,
                     int q, int M, int legacy, float* out);
 
+/* All q^8 residuals r(b_i) (or_residual) in lexicographic order: R [q^8, 8]. */
+void or_residual_table(int q, int legacy, int strided, float* R);
+
+/* The one-sided vLUT method of coset/legacy/quant/vlut.py:72-117 with the
+ * lookup sum of tests/legacy/test_one_sided_vlut_pytest.py:22-43, for one
+ * activation row a [K] over k-blocks [kb0, kb1) of level words
+ * [rows, kb_total, M]: per k-block it builds the query's table
+ * T[i] = <a[8k:8k+8], R[i]> (R from or_residual_table; table: q^8 floats of
+ * scratch) and adds sum_m q^m T[word[o, k, m]] to acc[o] (double).  The
+ * residuals do not depend on the query, so they are computed once, not per
+ * table as the reference's Python loop does.  CPU-baseline timing only. */
+void or_vlut_onesided_accumulate(const uint32_t* words, int64_t rows, int64_t kb_total, int M, int q,
+                                 const float* R, const float* a, int64_t kb0, int64_t kb1, float* table,
+                                 double* acc);
+
 /* coset/legacy/quant/functional.py:15-116 (encode with the overload loop,
  * the paper's Algorithm 1) for n 8-vectors: xs = x / beta (+ dither
  * [8] or [n, 8] by dither_stride 0 / 8), the chain y = Q(xs), xs = y / q

@@ -56,6 +56,10 @@ def lib():
         L.or_build_one_sided_vlut.argtypes = [_f32p, _int, _int, _f32p]
         L.or_vlut_matmul.argtypes = [_u32p, _f32p, _int, _f32p, _i64, _i64, _i64,
                                      _int, _int, _int, _f32p]
+        L.or_residual_table.argtypes = [_int, _int, _int, _f32p]
+        L.or_vlut_onesided_accumulate.argtypes = [_u32p, _i64, _i64, _int, _int, _f32p, _f32p, _i64, _i64,
+                                                  _f32p, np.ctypeslib.ndpointer(dtype=np.float64,
+                                                                                flags="C_CONTIGUOUS")]
         _u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
         L.or_legacy_encode.argtypes = [_f32p, _i64, _flt, _flt, _int, _int, ctypes.c_void_p, _i64, _int, _int,
                                        _i32p, _i32p, _u8p]
@@ -188,6 +192,27 @@ def vlut_matmul(words, scale, act, q, M, scale_mode=0, legacy=False):
     return out
 
 
+def residual_table(q, legacy=False, strided=True):
+    """r(b) for all q^8 level words, [q^8, 8] fp32 (or_residual per word)."""
+    R = np.empty((q ** 8, 8), np.float32)
+    lib().or_residual_table(int(q), int(legacy), int(strided), R)
+    return R
+
+
+def vlut_onesided_rows(words, R, a_row, q, kb0=0, kb1=None):
+    """sum over k-blocks [kb0, kb1) of the one-sided vLUT lookups for one
+    activation row a_row [K] (vlut.py:72-117 + the lookup sum of
+    test_one_sided_vlut_pytest.py:22-43): float64 [rows] partial sums."""
+    words = np.ascontiguousarray(words, np.uint32)
+    rows, kb, M = words.shape
+    kb1 = kb if kb1 is None else kb1
+    acc = np.zeros(rows, np.float64)
+    table = np.empty(q ** 8, np.float32)
+    lib().or_vlut_onesided_accumulate(words, rows, kb, M, int(q), R, _f32(a_row).reshape(-1), int(kb0), int(kb1),
+                                      table, acc)
+    return acc
+
+
 # --------------------------------------------------------------------------
 # beta pipeline and backward closed forms (float64 restatements; the layer
 # tolerances are 1e-3 relative so the float64 form is the stricter checker)
@@ -235,6 +260,66 @@ def layer_backward(gWq, W, qraw, beta_row, clip):
     dW = gQ * beta
     dbeta = (gQ * W).sum(axis=1) - (gm * Q / (beta * beta)).sum(axis=1)
     return dW, dbeta, mask
+
+
+def gather_stats(W_tiles, sigma_ema, xmax_ema, momentum=0.99):
+    """coset/core/layers.py:366-379 on [tiles, n] weights: the unbiased std
+    (variance in float64, its root rounded once to fp32, as torch's CPU
+    reduction), abs-max, + 1e-8, and the fp32 EMA with m and 1 - m rounded
+    to fp32.  Returns the new (sigma_ema, xmax_ema)."""
+    W = np.asarray(W_tiles, np.float32)
+    Wd = W.astype(np.float64)
+    n = W.shape[1]
+    mean = Wd.mean(axis=1, keepdims=True)
+    sd = np.sqrt(((Wd - mean) ** 2).sum(axis=1) / (n - 1)).astype(np.float32)
+    eps = np.float32(1e-8)
+    s1 = (sd + eps).astype(np.float32)
+    x1 = (np.abs(W).max(axis=1) + eps).astype(np.float32)
+    m, om = np.float32(momentum), np.float32(1.0 - momentum)
+    se = (np.asarray(sigma_ema, np.float32) * m).astype(np.float32) + (om * s1).astype(np.float32)
+    xe = (np.asarray(xmax_ema, np.float32) * m).astype(np.float32) + (om * x1).astype(np.float32)
+    return se.astype(np.float32), xe.astype(np.float32)
+
+
+def _lsq_parts(x, alpha, qmax):
+    """fp32 intermediates of LSQActivation.forward (coset/core/layers.py:
+    129-137) in the reference's operation order, with the straight-through
+    terms of ste_clip / ste_round (layers.py:20-26) kept: (x - x) and
+    (y - y) are +0 for finite values and turn a -0 result into +0."""
+    x = np.asarray(x, np.float32)
+    a = np.float32(np.float32(max(np.float32(alpha), np.float32(0))) + np.float32(1e-8))
+    with np.errstate(invalid="ignore"):
+        xc = ((x - x).astype(np.float32) + np.clip(x, -a, a).astype(np.float32)).astype(np.float32)
+        s = np.float32(a / np.float32(qmax))
+        y = (xc / s).astype(np.float32)
+        yq = ((y - y).astype(np.float32) + np.round(y).astype(np.float32)).astype(np.float32)
+    return a, s, xc, y, yq
+
+
+def lsq_forward(x, alpha, qmax):
+    """LSQActivation.forward: round(clamp(x, -a, a) / s) * s, a = relu(alpha)
+    + 1e-8, s = a / qmax (round half to even), fp32."""
+    _, s, _, _, yq = _lsq_parts(x, alpha, qmax)
+    return (yq * s).astype(np.float32)
+
+
+def lsq_backward(x, g, alpha, qmax):
+    """Autograd of lsq_forward: the STE terms pass g straight through the
+    clamp and the rounding, so dx = (g s) / s (fp32), and the clamp bound is
+    detached (no gradient to alpha through it); alpha's gradient comes from
+    s alone: dalpha = [alpha > 0] (sum g yq - sum (g s)((xc / s) / s)) / qmax,
+    the products in fp32 as autograd forms them, the sums in float64.
+    Returns (dx, dalpha, the sum of the terms' magnitudes / qmax)."""
+    g = np.asarray(g, np.float32)
+    a, s, xc, y, yq = _lsq_parts(x, alpha, qmax)
+    gs = (g * s).astype(np.float32)
+    dx = (gs / s).astype(np.float32)
+    t1 = (g * yq).astype(np.float32).astype(np.float64)
+    t2 = (gs * ((xc / s).astype(np.float32) / s).astype(np.float32)).astype(np.float32).astype(np.float64)
+    mag = (np.abs(t1).sum() + np.abs(t2).sum()) / qmax
+    if not np.float32(alpha) > 0:
+        return dx, 0.0, mag
+    return dx, float((t1.sum() - t2.sum()) / qmax), mag
 
 
 # --------------------------------------------------------------------------

@@ -14,7 +14,11 @@ coset/core/e8/layers.py:15-66), the legacy one-sided vLUT
 (coset/legacy/quant/vlut.py:72-117) and the legacy hierarchical encode /
 decode with the overload loop (coset/legacy/quant/functional.py:15-181).
 Only data is written (npz, no pickles); nothing here is needed at run time.
---only picks sections (projection, residual, codec, layer, vlut, legacy).
+--only picks sections (projection, residual, codec, layer, vlut, legacy,
+extra); "extra" writes layer_stats.npz (a layer run across its 256th step,
+coset/core/layers.py:366-379, 408-413), d4.npz (coset/core/d4/lattice.py:
+62-146 and the D4 layer of coset/core/d4/layers.py:14-68) and lsq.npz
+(LSQActivation, coset/core/layers.py:117-137).
 """
 from __future__ import annotations
 
@@ -95,6 +99,8 @@ def main():
     only = set(filter(None, args.only.split(",")))
     if only == {"legacy"}:
         return legacy_functional(args)
+    if only == {"extra"}:
+        return extra_goldens(args)
 
     sys.path.insert(0, args.reference)
     warnings.simplefilter("ignore")
@@ -231,6 +237,144 @@ def main():
             vl[f"q{q}_vlut{i}"] = _np(v)
     np.savez_compressed(os.path.join(args.out, "vlut_legacy.npz"), meta=meta, **vl)
     print("vlut")
+
+
+def _layer_record(out, name, layer, W, bias, x, g, extra=None):
+    """Inputs and outputs of one reference layer step (forward, backward) and
+    the beta it used."""
+    import torch
+    xt = torch.from_numpy(x).requires_grad_(True)
+    y = layer(xt)
+    (y * torch.from_numpy(g)).sum().backward()
+    with torch.no_grad():   # the bounds the step used (after its statistics update, if any)
+        bmin, bmax = layer._bounds()
+        beta = bmin + torch.sigmoid(layer.theta_beta) * (bmax - bmin)
+    rec = dict(W=W, bias=bias, x=x, g=g, y=_np(y), beta=_np(beta), beta_min=_np(bmin), beta_max=_np(bmax),
+               theta=_np(layer.theta_beta), dW=_np(layer.weight.grad), dtheta=_np(layer.theta_beta.grad),
+               dbias=_np(layer.bias.grad), dx=_np(xt.grad), Delta0=np.float64(layer.Delta0),
+               q=np.int64(layer.q), M=np.int64(layer.M), clip=np.float64(layer.weight_clip_value))
+    rec.update(extra or {})
+    for k, v in rec.items():
+        out[f"{name}_{k}"] = v
+
+
+def extra_goldens(args):
+    """Reference outputs for the statistics update, D4 and LSQ."""
+    sys.path.insert(0, args.reference)
+    warnings.simplefilter("ignore")
+    import torch
+    from coset.core.e8.layers import create_e8_hnlq_linear
+    from coset.core.d4.lattice import D4Lattice
+    from coset.core.d4.layers import create_d4_hnlq_linear
+    from coset.core.layers import LSQActivation
+
+    torch.set_num_threads(8)
+    meta = f"torch {torch.__version__}; generated by tests/golden/make_goldens.py --only extra"
+    rng = np.random.default_rng(20261203)
+
+    # ---- layer statistics: 255 forwards, then step 256 (the EMA update runs
+    # before the bounds, layers.py:408-413) with forward and backward
+    st = {}
+    stat_cases = [
+        ("row", 64, 16, dict(q=4, M=2, Delta0=1.5, tiling="row")),
+        ("c1", 768, 10, dict(q=4, M=2)),
+    ]
+    for name, fin, fout, kw in stat_cases:
+        torch.manual_seed(1)
+        layer = create_e8_hnlq_linear(fin, fout, **kw)
+        scale = 0.02 if name == "c1" else 1.0
+        W = (scale * rng.standard_normal((fout, fin)) * rng.uniform(0.3, 3.0, size=(fout, 1))
+             + 0.05 * scale * rng.standard_normal((fout, 1))).astype(np.float32)
+        layer.weight.data = torch.from_numpy(W.copy())
+        th = rng.uniform(-2, 2, size=layer.theta_beta.numel()).astype(np.float32)
+        layer.theta_beta.data = torch.from_numpy(th)
+        bias = (0.1 * rng.standard_normal(fout)).astype(np.float32)
+        layer.bias.data = torch.from_numpy(bias)
+        x = rng.standard_normal((16, fin)).astype(np.float32)
+        g = rng.standard_normal((16, fout)).astype(np.float32)
+        with torch.no_grad():
+            for _ in range(255):
+                layer(torch.from_numpy(x))
+        assert int(layer.step_count) == 255
+        sig0, xm0 = _np(layer.sigma_ema).copy(), _np(layer.xmax_ema).copy()
+        _layer_record(st, name, layer, W, bias, x, g)
+        assert int(layer.step_count) == 256
+        with torch.no_grad():
+            Wq = layer._quantize_weights()       # step 257: the statistics stay
+        st[f"{name}_sigma_ema_255"] = sig0
+        st[f"{name}_xmax_ema_255"] = xm0
+        st[f"{name}_sigma_ema"] = _np(layer.sigma_ema)
+        st[f"{name}_xmax_ema"] = _np(layer.xmax_ema)
+        st[f"{name}_Wq"] = _np(Wq)
+        print("stats", name, "sigma moved:", float(np.abs(st[f"{name}_sigma_ema"] - sig0).max()))
+    # block tiling: the reference's forward cannot run it (layers.py:459
+    # reshapes [out, bpr, 1] to [out, in]), so its _gather_stats is called on
+    # the blocks directly, twice (two EMA steps)
+    torch.manual_seed(1)
+    layer = create_e8_hnlq_linear(32, 8, q=4, M=2, Delta0=1.5, tiling="block")
+    W = (rng.standard_normal((8, 32)) * rng.uniform(0.3, 3.0, size=(8, 1))).astype(np.float32)
+    st["block_W"] = W
+    for i in range(2):
+        layer._gather_stats(torch.from_numpy(W).view(8, 4, 8))
+        st[f"block_sigma_ema_{i + 1}"] = _np(layer.sigma_ema).copy()
+        st[f"block_xmax_ema_{i + 1}"] = _np(layer.xmax_ema).copy()
+    np.savez_compressed(os.path.join(args.out, "layer_stats.npz"), meta=meta, **st)
+
+    # ---- D4: projection and g_x (random, ties, half-integers), layer steps
+    d4 = {}
+    lat = D4Lattice()
+    xs = np.concatenate([
+        rng.standard_normal((2048, 4)),
+        4.0 * rng.standard_normal((512, 4)),
+        rng.integers(-8, 9, size=(512, 4)) / 2.0,
+        rng.integers(-16, 17, size=(512, 4)) / 4.0,
+        np.round(rng.standard_normal((512, 4)) * 4) / 4 + rng.choice([0.0, 1e-7, -1e-7], size=(512, 4)),
+    ]).astype(np.float32)
+    xt = torch.from_numpy(xs)
+    d4["x"] = xs
+    d4["projection"] = _np(lat.projection(xt))
+    d4["g_x"] = _np(lat.g_x(xt))
+    d4_cases = [
+        ("d4def", 64, 16, dict(q=4, M=2), 0.02, None),
+        ("d4nd", 64, 16, dict(q=4, M=2, Delta0=1.5), 1.0, "uniform"),
+        ("d4clip", 32, 8, dict(q=4, M=2, Delta0=6.0, weight_clip_value=0.5), 1.0, "uniform"),
+    ]
+    for name, fin, fout, kw, wstd, theta in d4_cases:
+        torch.manual_seed(2)
+        layer = create_d4_hnlq_linear(fin, fout, **kw)
+        W = (wstd * rng.standard_normal((fout, fin))).astype(np.float32)
+        layer.weight.data = torch.from_numpy(W.copy())
+        if theta == "uniform":
+            layer.theta_beta.data = torch.from_numpy(
+                rng.uniform(-3, 3, size=layer.theta_beta.numel()).astype(np.float32))
+        bias = (0.1 * rng.standard_normal(fout)).astype(np.float32)
+        layer.bias.data = torch.from_numpy(bias)
+        x = rng.standard_normal((16, fin)).astype(np.float32)
+        g = rng.standard_normal((16, fout)).astype(np.float32)
+        _layer_record(d4, name, layer, W, bias, x, g)
+        with torch.no_grad():
+            layer.step_count.zero_()
+            d4[f"{name}_Wq"] = _np(layer._quantize_weights())
+        print("d4", name)
+    np.savez_compressed(os.path.join(args.out, "d4.npz"), meta=meta, **d4)
+
+    # ---- LSQ activation quantizer: forward and both gradients
+    lsq = {}
+    lsq_cases = [("b8_a1", 8, 1.0, 1.0), ("b8_a03", 8, 0.3, 1.0), ("b4_a2", 4, 2.0, 3.0),
+                 ("b8_neg", 8, -0.5, 1.0), ("b2_a1", 2, 1.0, 1.5)]
+    for name, bits, alpha, xs_scale in lsq_cases:
+        q = LSQActivation(bit_width=bits, init_alpha=alpha)
+        x = (xs_scale * rng.standard_normal((64, 48))).astype(np.float32)
+        x[0, :8] = np.array([0.0, -0.0, alpha, -alpha, 2 * alpha, -2 * alpha, alpha / 3, 1e-9], np.float32)
+        g = rng.standard_normal(x.shape).astype(np.float32)
+        xt = torch.from_numpy(x).requires_grad_(True)
+        y = q(xt)
+        (y * torch.from_numpy(g)).sum().backward()
+        for k, v in dict(x=x, g=g, y=_np(y), dx=_np(xt.grad), dalpha=_np(q.alpha.grad).reshape(1),
+                         alpha=np.array([alpha], np.float32), bits=np.int64(bits)).items():
+            lsq[f"{name}_{k}"] = v
+    np.savez_compressed(os.path.join(args.out, "lsq.npz"), meta=meta, **lsq)
+    print("lsq")
 
 
 def legacy_functional(args):

@@ -100,3 +100,60 @@ def test_captured_step_needs_gpu_tensors():
     L = coset_amd.create_e8_hnlq_linear(16, 8, device="cpu")
     with pytest.raises(ValueError):
         coset_amd.CapturedQATStep(L, torch.zeros(2, 16))
+
+
+@pytest.mark.gpu
+def test_captured_step_with_optimizer_zero_grad():
+    """opt.zero_grad() (set_to_none) + cap.step() + opt.step() updates the
+    parameters exactly as the same eager loop does."""
+    eager, cap_layer = _pair(128, 64, "row", interval=256)
+    gen = torch.Generator(device="cuda").manual_seed(21)
+    xs = [torch.randn(64, 128, device="cuda", generator=gen) for _ in range(4)]
+    gys = [torch.randn(64, 64, device="cuda", generator=gen) for _ in range(4)]
+    x_static = torch.zeros(64, 128, device="cuda", requires_grad=True)
+    cap = coset_amd.CapturedQATStep(cap_layer, x_static, torch.zeros(64, 64, device="cuda"))
+    opt_a = torch.optim.SGD(eager.parameters(), lr=0.05)
+    opt_b = torch.optim.SGD(cap_layer.parameters(), lr=0.05)
+    for i in range(4):
+        opt_a.zero_grad(set_to_none=True)
+        eager(xs[i]).backward(gys[i])
+        opt_a.step()
+        opt_b.zero_grad(set_to_none=True)
+        cap.step(xs[i], gys[i])
+        opt_b.step()
+        torch.cuda.synchronize()
+        print(f"optimizer step {i}", flush=True)
+        for name, pa, pb in (("weight", eager.weight, cap_layer.weight), ("theta", eager.theta_beta,
+                                                                          cap_layer.theta_beta),
+                             ("bias", eager.bias, cap_layer.bias)):
+            assert torch.equal(pa, pb), f"{name} differs after optimizer step {i}"
+    assert x_static.grad is not None
+
+
+@pytest.mark.gpu
+def test_captured_step_after_load_state_dict():
+    """load_state_dict copies in place: the next replay reads the loaded
+    values and the host counter mirror is re-read from the loaded buffer."""
+    src_layer, cap_layer = _pair(64, 16, "row", interval=256)
+    x = torch.randn(8, 64, device="cuda")
+    cap = coset_amd.CapturedQATStep(cap_layer, x.clone())
+    cap.step()
+    with torch.no_grad():
+        src_layer.weight.mul_(3.0)
+        src_layer.step_count.fill_(41)
+    cap_layer.load_state_dict(src_layer.state_dict())
+    y = cap.step(x).clone()
+    assert int(cap_layer.step_count) == 42 and cap_layer._host_step == 42
+    with torch.no_grad():
+        ya = src_layer(x)
+    assert torch.equal(y, ya)
+
+
+@pytest.mark.gpu
+def test_captured_step_refuses_replaced_weights():
+    _, L = _pair(64, 16, "row", interval=256)
+    cap = coset_amd.CapturedQATStep(L, torch.randn(8, 64, device="cuda"))
+    cap.step()
+    L.load_weights(torch.randn(16, 64))
+    with pytest.raises(RuntimeError):
+        cap.step()

@@ -409,3 +409,29 @@ def test_full_size_c3(ca):
     np.testing.assert_array_equal(host(W[sel.cuda()]), Wq)
     got = words(pk).reshape(rows, cols // 8, 3)[sel.numpy()]
     np.testing.assert_array_equal(got.reshape(-1, 3), O.pack_words(codes, 16).reshape(-1, 3))
+
+
+def test_input_lengths_are_checked():
+    """Lengths the kernels index by are validated on the host: a dither of
+    neither 8 nor 8 n values, a per-row beta that does not tile the blocks,
+    a vLUT scale or a packed layer's beta/bias of the wrong length."""
+    import coset_amd as ca
+    x = torch.randn(40, 8, device="cuda")
+    with pytest.raises(ValueError):
+        ca.hnlq_encode(x, 4, 2, 1.0, dither=torch.zeros(3, 8, device="cuda"))
+    ca.hnlq_encode(x, 4, 2, 1.0, dither=torch.zeros(40, 8, device="cuda"))
+    with pytest.raises(ValueError):
+        ca.hnlq_roundtrip(x, 4, 2, beta_row=torch.ones(3, device="cuda"), blocks_per_row=10)
+    with pytest.raises(ValueError):
+        ca.hnlq_decode(torch.zeros(40, 2, dtype=torch.uint16, device="cuda"), 4, 2,
+                       beta_row=torch.ones(7, device="cuda"))
+    words = torch.zeros(16, 4, 2, dtype=torch.uint16, device="cuda")
+    a = torch.randn(2, 32, device="cuda").half()
+    with pytest.raises(ValueError):
+        ca.vlut_matmul(words, a, 4, scale=torch.ones(15, device="cuda"))
+    tensors = {"words": words.cpu(), "beta": torch.ones(15)}
+    meta = {"q": 4, "M": 2, "in_features": 32, "out_features": 16}
+    with pytest.raises(ValueError):
+        ca.PackedLinear(tensors, meta)
+    with pytest.raises(ValueError):
+        ca.PackedLinear({"words": words.cpu(), "beta": torch.ones(16), "bias": torch.zeros(5)}, meta)

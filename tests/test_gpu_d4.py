@@ -140,3 +140,45 @@ def test_d4_layer_trains():
     assert torch.isfinite(loss) and int(layer.step_count) == 3
     with pytest.raises(ValueError):
         ca.create_d4_hnlq_linear(10, 4)
+
+
+@pytest.mark.parametrize("name,fin,fout,kw", [("d4def", 64, 16, dict(q=4, M=2)),
+                                              ("d4nd", 64, 16, dict(q=4, M=2, Delta0=1.5)),
+                                              ("d4clip", 32, 8, dict(q=4, M=2, Delta0=6.0, weight_clip_value=0.5))])
+def test_d4_layer_matches_reference_golden(golden, name, fin, fout, kw):
+    """create_d4_hnlq_linear against the reference's own D4 layer
+    (tests/golden/d4.npz): the kernel's beta and W_q bit-exact, outputs and
+    gradients elementwise within 1e-3 of the summands' magnitude; the
+    projection and g_x bit-exact on the golden blocks."""
+    import coset_amd as ca
+    from coset_amd.layers import d4_qat_fwd_theta
+    D = golden("d4")
+    g = lambda k: D[f"{name}_{k}"]
+    lat = ca.D4Lattice()
+    xt = torch.from_numpy(D["x"]).cuda()
+    assert np.array_equal(lat.projection(xt).cpu().numpy().view(np.int32), D["projection"].view(np.int32))
+    assert np.array_equal(lat.g_x(xt).cpu().numpy(), D["g_x"])
+    layer = ca.create_d4_hnlq_linear(fin, fout, **kw)
+    with torch.no_grad():
+        layer.weight.copy_(torch.from_numpy(g("W")))
+        layer.bias.copy_(torch.from_numpy(g("bias")))
+        layer.theta_beta.copy_(torch.from_numpy(g("theta")))
+    Wq_k, beta_k, _ = d4_qat_fwd_theta(layer.weight.detach().contiguous(), layer.theta_beta.detach(),
+                                       layer.sigma_ema, layer.xmax_ema, None,
+                                       (float(layer.Delta0), float(layer.eta), layer._ginv_f, int(layer.M)),
+                                       int(layer.q), float(layer.weight_clip_value), fin // 4, torch.float32)
+    np.testing.assert_array_equal(beta_k.cpu().numpy(), g("beta"))
+    np.testing.assert_array_equal(Wq_k.cpu().numpy(), g("Wq"))
+    x = torch.from_numpy(g("x")).cuda().requires_grad_(True)
+    y = layer(x)
+    (y * torch.from_numpy(g("g")).cuda()).sum().backward()
+    X, G, Wq = (g(k).astype(np.float64) for k in ("x", "g", "Wq"))
+
+    def close(a, b, mag):
+        assert (np.abs(np.asarray(a, np.float64) - b) <= 1e-3 * np.maximum(mag, np.abs(b))).all()
+    close(y.detach().cpu().numpy(), g("y"), np.abs(X) @ np.abs(Wq).T + np.abs(g("bias")))
+    close(layer.weight.grad.cpu().numpy(), g("dW"), np.abs(G).T @ np.abs(X))
+    close(x.grad.cpu().numpy(), g("dx"), np.abs(G) @ np.abs(Wq))
+    close(layer.bias.grad.cpu().numpy(), g("dbias"), np.abs(G).sum(axis=0))
+    dth = g("dtheta").astype(np.float64)
+    close(layer.theta_beta.grad.cpu().numpy(), dth, np.abs(dth) + 1e-3 * np.abs(dth).max())

@@ -144,3 +144,24 @@ def test_layer_with_activation_quantization():
     assert torch.equal(y, layer.actq(lin))
     y.sum().backward()
     assert layer.actq.alpha.grad is not None and torch.isfinite(layer.actq.alpha.grad)
+
+
+@pytest.mark.parametrize("name", ["b8_a1", "b8_a03", "b4_a2", "b8_neg", "b2_a1"])
+def test_lsq_matches_reference_golden(golden, name):
+    """LSQActivation against the reference module's own outputs
+    (tests/golden/lsq.npz): forward and dx bit for bit, dalpha within 1e-6
+    of the magnitude of its summands (summation order)."""
+    import numpy as np
+    import coset_amd as ca
+    from oracle import oracle as O
+    L = golden("lsq")
+    x, g = L[f"{name}_x"], L[f"{name}_g"]
+    alpha, bits = float(L[f"{name}_alpha"][0]), int(L[f"{name}_bits"])
+    m = ca.LSQActivation(bit_width=bits, init_alpha=alpha).cuda()
+    xg = torch.from_numpy(x).cuda().requires_grad_(True)
+    y = m(xg)
+    y.backward(torch.from_numpy(g).cuda())
+    assert np.array_equal(y.detach().cpu().numpy().view(np.int32), L[f"{name}_y"].view(np.int32))
+    assert np.array_equal(xg.grad.cpu().numpy().view(np.int32), L[f"{name}_dx"].view(np.int32))
+    _, _, mag = O.lsq_backward(x, g, alpha, m.qmax)
+    assert abs(m.alpha.grad.item() - float(L[f"{name}_dalpha"][0])) <= 1e-6 * mag

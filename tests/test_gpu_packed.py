@@ -105,3 +105,33 @@ def test_packed_layer_with_activation_quantizer(tmp_path):
     # across a rounding boundary to one step s
     assert d.max().item() <= s * 1.001 + 1e-5
     assert (d > 1e-5).float().mean().item() < 0.02
+
+
+def test_saved_words_and_served_output_match_oracle(tmp_path):
+    """f1 against the oracle: the file's level words are the oracle's codes
+    of the layer quantizer (coset/core/layers.py:428-463) at the saved beta,
+    packed as idx(b) = sum_j b_j q^(7-j); the served output equals the
+    oracle's one-sided lookup over those words (scale_mode 1: divide by
+    beta) plus bias, elementwise within 1e-3 of the summands' magnitude."""
+    import coset_amd as ca
+    from safetensors import safe_open
+    from oracle import oracle as O
+    layer = _layer(ca)
+    path = str(tmp_path / "o.safetensors")
+    ca.save_packed(layer, path)
+    with safe_open(path, framework="pt") as f:
+        words = f.get_tensor("words").numpy()
+        beta = f.get_tensor("beta").numpy()
+        bias = f.get_tensor("bias").numpy()
+    W = layer.weight.detach().cpu().numpy()
+    _, _, codes = O.layer_quant(W, beta, 4, 2, float(layer.weight_clip_value))
+    ref_words = O.pack_words(codes, 4).reshape(64, 32, 2)
+    np.testing.assert_array_equal(words.astype(np.uint32), ref_words)
+    pl = ca.load_packed(path)
+    x = torch.randn(7, 256, device="cuda").to(torch.bfloat16)
+    y = pl(x).cpu().numpy().astype(np.float64)
+    xf = x.float().cpu().numpy()
+    ref = O.vlut_matmul(ref_words, beta, xf, 4, 2, scale_mode=1) + bias
+    dec = O.e8_decode(codes, 4, 2, 1.0).reshape(64, 256) / beta[:, None]
+    mag = np.abs(xf).astype(np.float64) @ np.abs(dec).T.astype(np.float64) + np.abs(bias)
+    assert (np.abs(y - ref) <= 1e-3 * mag).all()
