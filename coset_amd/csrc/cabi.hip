@@ -6,6 +6,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "../../include/coset_amd.h"
@@ -14,9 +15,23 @@
 #include "tables.hpp"
 #include "vlut.hpp"
 
+// Scratch of coset_vlut_matmul_noalloc: the split-K partials of the vLUT
+// matmul's launch plan live in this fixed per-device array instead of a
+// caller workspace.  8 MiB per device (the whole 4096 x 4096 matmul at 64
+// tokens and 8 K splits fits), held until the process ends.  Host code never
+// uses the name itself (in host code it is a host-side stand-in, not a
+// device address): coset_init looks up each device's copy once with
+// hipGetSymbolAddress and the entry point passes that address to the kernels.
+constexpr int64_t kNoallocScratchFloats = (int64_t)2 << 20;
+static __device__ __align__(256) float scratch[kNoallocScratchFloats];
+
 namespace {
 
 thread_local std::string g_last_error;
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};   // per device: address of its `scratch`, set by coset_init
 
 int fail(int code, const char* fmt, ...)
 {
@@ -123,6 +138,17 @@ int coset_init(int device)
             const coset::DecodeTables* t = nullptr;
             if (rc == COSET_OK) rc = check_hip(coset::get_decode_tables(q, legacy, &t), "decode tables");
         }
+    // this device's copy of the no-allocation scratch array (looked up with
+    // the device current; each device holds its own copy at its own address)
+    const int dev = device >= 0 ? device : cur;
+    if (rc == COSET_OK && dev < kMaxDevices) {
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        if (!g_scratch_ptr[dev]) {
+            float* p = nullptr;
+            rc = check_hip(hipGetSymbolAddress((void**)&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+            if (rc == COSET_OK) g_scratch_ptr[dev] = p;
+        }
+    }
     if (device >= 0 && device != cur) (void)hipSetDevice(cur);
     return rc;
 }
@@ -608,7 +634,7 @@ int coset_vlut_prepare(const void* words, int64_t rows, int64_t kb, int M, int q
 static int vlut_matmul_impl(const void* words, int word_format, const float* scale, int scale_mode, const void* act,
                             int act_dtype, int64_t B, int64_t rows, int64_t K, int q, int M, int legacy, int method,
                             const float* bias, const float* lsq_alpha, int lsq_qmax, float* workspace,
-                            int64_t workspace_floats, float* out, void* stream)
+                            int64_t workspace_floats, float* out, void* stream, bool may_build = true)
 {
     int rc;
     if (lsq_alpha && lsq_qmax < 1) return fail(COSET_EINVAL, "lsq_qmax must be >= 1 (bit_width >= 2)");
@@ -655,7 +681,11 @@ static int vlut_matmul_impl(const void* words, int word_format, const float* sca
     p.lsq_alpha = lsq_alpha;
     p.lsq_qmax = lsq_qmax;
     const coset::DecodeTables* t = nullptr;
-    if ((rc = check_hip(coset::get_decode_tables(q, p.legacy, &t), "decode tables"))) return rc;
+    if (may_build) {
+        if ((rc = check_hip(coset::get_decode_tables(q, p.legacy, &t), "decode tables"))) return rc;
+    } else if (coset::find_decode_tables(q, p.legacy, &t) != hipSuccess) {
+        return fail(COSET_EINVAL, "decode tables not built on this device: call coset_init(device) first");
+    }
     if (t->n_coarse > coset::kMaxCoarseVlut) return fail(COSET_EUNSUPPORTED, "too many coarse points");
     return check_hip(coset::vlut_matmul(p, plan, (hipStream_t)stream), "vLUT matmul launch");
 }
@@ -667,6 +697,35 @@ int coset_vlut_matmul(const void* words, int word_format, const float* scale, in
     return vlut_matmul_impl(words, word_format, scale, scale_mode, act, act_dtype, B, rows, K, q, M, legacy, method,
                             nullptr, nullptr, 0, workspace, workspace_floats, out, stream);
 }
+
+int coset_vlut_matmul_noalloc(const void* words, int word_format, const float* scale, int scale_mode,
+                              const void* act, int act_dtype, int64_t B, int64_t rows, int64_t K, int q, int M,
+                              int legacy, int method, float* out, void* stream)
+{
+    int dev = 0;
+    int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
+    if (rc) return rc;
+    float* ws = nullptr;
+    if (dev < kMaxDevices) {
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        ws = g_scratch_ptr[dev];
+    }
+    if (!ws) return fail(COSET_EINVAL, "coset_vlut_matmul_noalloc: call coset_init(%d) on this device first", dev);
+    const int m = vlut_method(method, act_dtype, q, M);
+    if (m >= 0 && B > 0 && rows > 0 && K >= 8 && q >= 2 && q <= 4 && M >= 1 && M <= 4) {
+        const int64_t need = coset::vlut_workspace_floats(coset::vlut_plan(rows, B, K, q, M, m), B, rows);
+        if (need > kNoallocScratchFloats)
+            return fail(COSET_EINVAL,
+                        "coset_vlut_matmul_noalloc: B=%lld rows=%lld K=%lld needs %lld floats of scratch, more than "
+                        "the %lld (8 MiB) it holds; use coset_vlut_matmul with a workspace",
+                        (long long)B, (long long)rows, (long long)K, (long long)need,
+                        (long long)kNoallocScratchFloats);
+    }
+    return vlut_matmul_impl(words, word_format, scale, scale_mode, act, act_dtype, B, rows, K, q, M, legacy, method,
+                            nullptr, nullptr, 0, ws, kNoallocScratchFloats, out, stream, false);
+}
+
+int64_t coset_vlut_noalloc_scratch_floats(void) { return kNoallocScratchFloats; }
 
 int coset_vlut_linear(const void* words, int word_format, const float* scale, int scale_mode, const void* act,
                       int act_dtype, int64_t B, int64_t rows, int64_t K, int q, int M, int legacy, int method,

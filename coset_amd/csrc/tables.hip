@@ -16,6 +16,7 @@
 #include <algorithm>
 #include <array>
 #include <map>
+#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -130,6 +131,7 @@ struct Slot {
     std::once_flag once;
     DecodeTables t{};
     hipError_t err = hipSuccess;
+    std::atomic<bool> ready{false};   // set once the tables are built
 };
 
 std::mutex g_mu;
@@ -206,9 +208,25 @@ hipError_t get_decode_tables(int q, int legacy, const DecodeTables** out)
         if (!ref) ref = new Slot();
         s = ref;
     }
-    std::call_once(s->once, [&] { s->err = build(device, q, legacy, &s->t); });
+    std::call_once(s->once, [&] {
+        s->err = build(device, q, legacy, &s->t);
+        if (s->err == hipSuccess) s->ready.store(true, std::memory_order_release);
+    });
     if (s->err != hipSuccess) return s->err;
     *out = &s->t;
+    return hipSuccess;
+}
+
+hipError_t find_decode_tables(int q, int legacy, const DecodeTables** out)
+{
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) return e;
+    if (q != 2 && q != 4) return hipErrorInvalidValue;
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_slots.find((long)device * 64 + q * 2 + (legacy ? 1 : 0));
+    if (it == g_slots.end() || !it->second->ready.load(std::memory_order_acquire)) return hipErrorNotReady;
+    *out = &it->second->t;
     return hipSuccess;
 }
 

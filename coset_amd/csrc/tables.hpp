@@ -32,4 +32,9 @@ struct DecodeTables {
 // the current device; built on first use (blocking), then cached.
 hipError_t get_decode_tables(int q, int legacy, const DecodeTables** out);
 
+// The same tables only if they were already built on the current device
+// (coset_init or an earlier call): never builds or allocates; returns
+// hipErrorNotReady otherwise.
+hipError_t find_decode_tables(int q, int legacy, const DecodeTables** out);
+
 }  // namespace coset

@@ -257,6 +257,23 @@ int coset_vlut_matmul(const void* words, int word_format, const float* scale, in
                       int act_dtype, int64_t B, int64_t rows, int64_t K, int q, int M, int legacy, int method,
                       float* workspace, int64_t workspace_floats, float* out, void* stream);
 
+/* coset_vlut_matmul without a workspace argument, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  No counterpart in the reference (whose vLUT path
+ * is Python on the CPU).  It allocates nothing: the split-K partials go to a
+ * fixed per-device scratch array of coset_vlut_noalloc_scratch_floats()
+ * floats (8 MiB), whose address coset_init(device) looks up once per device;
+ * call coset_init on each device first (it also builds the decode tables,
+ * which this entry point never builds).  A launch plan needing more scratch
+ * is refused with COSET_EINVAL.  Every call on a device shares that
+ * device's array: calls that overlap on one GPU (two streams at once) race
+ * on it; calls on one stream are ordered and safe.  Nothing in the array
+ * needs to start at zero (each launch writes every partial it reads). */
+int64_t coset_vlut_noalloc_scratch_floats(void);
+int coset_vlut_matmul_noalloc(const void* words, int word_format, const float* scale, int scale_mode,
+                              const void* act, int act_dtype, int64_t B, int64_t rows, int64_t K, int q, int M,
+                              int legacy, int method, float* out, void* stream);
+
 /* D4 lattice operator over n_blocks fp32 [n, 4] blocks (coset/core/d4/lattice.py:62-146,
  * coset/core/base.py:134-176): COSET_OP_G_X, COSET_OP_PROJECT (closest point,
  * the reference's rule), COSET_OP_ENCODE_COORDS (round(G^-1 x) mod q),
