@@ -83,6 +83,7 @@ OPT_VLUT_SPLITS = 3
 OPT_FAST_PROJECTION = 4
 OPT_CODEC_PLAIN = 5
 OPT_CODEC_DYNAMIC = 6
+OPT_VLUT_DEEP = 7
 CODEC_AUTO, CODEC_GENERIC, CODEC_LUT = 0, 1, 2
 
 _lib = None
@@ -194,6 +195,11 @@ def set_codec_dynamic(enabled: bool) -> None:
 def set_vlut_decode(byte_tables: bool) -> None:
     """MFMA vLUT decode through byte tables (default) or integer digits."""
     call("coset_set_option", OPT_VLUT_DECODE, int(bool(byte_tables)))
+
+
+def set_vlut_deep(enabled: bool) -> None:
+    """vLUT matmuls above 32 tokens: the deep kernel (default) or the wide one."""
+    call("coset_set_option", OPT_VLUT_DEEP, int(bool(enabled)))
 
 
 def set_vlut_splits(splits: int) -> None:

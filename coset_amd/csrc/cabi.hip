@@ -121,6 +121,10 @@ int coset_set_option(int key, int value)
         if (value < 0) return fail(COSET_EINVAL, "vLUT splits %d < 0", value);
         coset::g_vlut_splits = value;
         return COSET_OK;
+    case COSET_OPT_VLUT_DEEP:
+        if (value < 0 || value > 1) return fail(COSET_EINVAL, "vLUT deep %d not in {0,1}", value);
+        coset::g_vlut_deep = value;
+        return COSET_OK;
     default: return fail(COSET_EINVAL, "unknown option %d", key);
     }
 }
@@ -659,7 +663,8 @@ static int vlut_matmul_impl(const void* words, int word_format, const float* sca
                     (long long)need);
     if (need > 0 && !workspace) return fail(COSET_EINVAL, "NULL workspace");
     if (word_format < 0 || word_format > 3) return fail(COSET_EINVAL, "word_format must be 0, 1, 2 or 3");
-    if (word_format == 3 && plan.kernel != coset::VK_MFMA_ROWS && plan.kernel != coset::VK_MFMA_WIDE)
+    if (word_format == 3 && plan.kernel != coset::VK_MFMA_ROWS && plan.kernel != coset::VK_MFMA_WIDE &&
+        plan.kernel != coset::VK_MFMA_DEEP)
         return fail(COSET_EUNSUPPORTED, "the decoded format runs on the matrix-core rows kernel only (fp16/bf16 activations)");
     if (word_format != 0 && !aligned(words, 16)) return fail(COSET_EINVAL, "prepared words must be 16-byte aligned");
     coset::VlutMatmulArgs p{};

@@ -88,6 +88,11 @@ struct CodecArgs {
     float* dbdt_out;         // nullable [tiles]: d beta / d theta at that beta
     int64_t* step_counter;   // nullable: incremented once per launch
     int fast_projection;     // encoders try project_fast first (set by the launcher)
+    // decode tables (tables.hpp, core rule; set by the launcher for q = 2, 4):
+    // the generic kernel then decodes a level as 2 r = 2 G b - q (2 c[cid])
+    // from the coarse-point id instead of running the projection
+    const uint16_t* dec_map;
+    const uint64_t* dec_coarse;
 };
 
 // One encoder level (core rule, contiguous distances): the projection's

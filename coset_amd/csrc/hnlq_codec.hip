@@ -14,33 +14,48 @@
 //   SCALE_LAYER  x_s = x * beta_row;    out = clamp(dec / beta_row, +-clip)
 //                                                                 (layers.py:431,455,463)
 #include "codec_kernels.hpp"
+#include "tables.hpp"
 
 namespace coset {
+
+// 2 r(b) of one level word through the decode tables (q = 2, 4):
+// 2 G b from the digits, minus q (2 c) for the word's coarse point.
+template <int Q>
+__device__ __forceinline__ void two_r_tables(uint32_t w, const uint16_t* map, const uint64_t* coarse, int out[8])
+{
+    w &= (Q == 2 ? 0xffu : 0xffffu);   // the map's bounds for any input word
+    int b[8];
+    unpack_word<Q>(w, Q, b);
+    const uint64_t c = coarse[map[w]];
+    out[0] = 4 * b[0] - 2 * b[1] + b[7];
+#pragma unroll
+    for (int j = 1; j < 6; ++j) out[j] = 2 * (b[j] - b[j + 1]) + b[7];
+    out[6] = 2 * b[6] + b[7];
+    out[7] = b[7];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) out[j] -= Q * (int)(int8_t)(uint8_t)(c >> (8 * j));
+}
+
+// Tiles whose theta-derived beta one workgroup of 256 blocks can touch when a
+// tile spans at least 64 blocks.
+constexpr int kWgTiles = 256 / 64 + 2;
 
 template <int Q, int MODE>
 __global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
 {
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i == 0 && a.step_counter) *a.step_counter += 1;
-    if (i >= a.n) return;
     const int q = Q > 0 ? Q : a.q;
     const float qf = (float)q;
     const int M = a.M;
 
-    float scale = 1.f;
-    if (a.scale_mode == SCALE_CODEC)
-        scale = a.beta;
-    else if (a.scale_mode == SCALE_LAYER)
-        scale = layer_scale(a, i);
-
-    float acc[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] = 0.f;
-
+    // the block's input is loaded first (clamped to the last block), so its
+    // latency overlaps the scale's loads below
+    float xl[8];
     if (MODE != MODE_DECODE) {
-        float xl[8];
+        const int64_t il = i < a.n ? i : a.n - 1;
         if (a.x_dtype == DT_BF16) {
-            uint4 v = reinterpret_cast<const uint4*>(a.x)[i];
+            uint4 v = reinterpret_cast<const uint4*>(a.x)[il];
             uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -48,11 +63,47 @@ __global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
                 xl[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
             }
         } else {
-            const float4* p = reinterpret_cast<const float4*>(a.x) + 2 * i;
+            const float4* p = reinterpret_cast<const float4*>(a.x) + 2 * il;
             float4 u = p[0], v = p[1];
             xl[0] = u.x; xl[1] = u.y; xl[2] = u.z; xl[3] = u.w;
             xl[4] = v.x; xl[5] = v.y; xl[6] = v.z; xl[7] = v.w;
         }
+    }
+
+    float scale = 1.f;
+    if (a.scale_mode == SCALE_LAYER && a.use_theta && a.blocks_per_row >= 64) {
+        // beta from theta once per tile the workgroup touches (not per block):
+        // the workgroup's blocks span tiles t0 .. t0 + kWgTiles - 1 at most
+        __shared__ float s_beta[kWgTiles];
+        const int64_t b0 = (int64_t)blockIdx.x * blockDim.x;
+        const int64_t t0 = b0 / a.blocks_per_row;
+        const int64_t t = t0 + threadIdx.x;
+        if (threadIdx.x < kWgTiles && t * a.blocks_per_row < a.n) {
+            float lo, hi, sg;
+            theta_beta_terms(a.tb, t, &lo, &hi, &sg);
+            const float span = __fsub_rn(hi, lo);
+            s_beta[threadIdx.x] = __fadd_rn(lo, __fmul_rn(sg, span));
+            const int64_t first = t * a.blocks_per_row;   // the workgroup holding it records beta
+            if (first >= b0 && first < b0 + blockDim.x) {
+                if (a.beta_out) a.beta_out[t] = s_beta[threadIdx.x];
+                if (a.dbdt_out) a.dbdt_out[t] = __fmul_rn(__fmul_rn(span, __fsub_rn(1.f, sg)), sg);
+            }
+        }
+        __syncthreads();
+        if (i < a.n) scale = s_beta[i / a.blocks_per_row - t0];
+    } else if (i < a.n) {
+        if (a.scale_mode == SCALE_CODEC)
+            scale = a.beta;
+        else if (a.scale_mode == SCALE_LAYER)
+            scale = layer_scale(a, i);
+    }
+    if (i >= a.n) return;
+
+    float acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+
+    if (MODE != MODE_DECODE) {
         if (a.scale_mode == SCALE_CODEC) {
             if (a.beta_is_pow2) {
 #pragma unroll
@@ -88,12 +139,21 @@ __global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
                 cp[1] = make_float4((float)b[4], (float)b[5], (float)b[6], (float)b[7]);
             }
             if (MODE == MODE_ROUNDTRIP) {
-                float gb[8], r[8];
-                lattice_point(b, gb);
-                if (a.strided)
-                    residual_from_point<false, true, Q>(gb, qf, r);
-                else
-                    residual_from_point<false, false, Q>(gb, qf, r);
+                float r[8];
+                if ((Q == 2 || Q == 4) && a.dec_map) {
+                    // exact: 2 r is an integer, r a half-integer
+                    int r2[8];
+                    two_r_tables<Q>(word, a.dec_map, a.dec_coarse, r2);
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) r[j] = 0.5f * (float)r2[j];
+                } else {
+                    float gb[8];
+                    lattice_point(b, gb);
+                    if (a.strided)
+                        residual_from_point<false, true, Q>(gb, qf, r);
+                    else
+                        residual_from_point<false, false, Q>(gb, qf, r);
+                }
 #pragma unroll
                 for (int j = 0; j < 8; ++j) acc[j] = __fadd_rn(acc[j], __fmul_rn(w, r[j]));
                 w = __fmul_rn(w, qf);
@@ -116,6 +176,14 @@ __global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
                     word = reinterpret_cast<const uint16_t*>(a.packed_in)[(size_t)i * M + m];
                 else
                     word = reinterpret_cast<const uint32_t*>(a.packed_in)[(size_t)i * M + m];
+                if ((Q == 2 || Q == 4) && a.dec_map) {
+                    int r2[8];
+                    two_r_tables<Q>(word, a.dec_map, a.dec_coarse, r2);
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) acc[j] = __fadd_rn(acc[j], __fmul_rn(w, 0.5f * (float)r2[j]));
+                    w = __fmul_rn(w, qf);
+                    continue;
+                }
                 int b[8];
                 unpack_word<Q>(word, q, b);
                 lattice_point(b, gb);
@@ -186,6 +254,15 @@ hipError_t launch_codec(const CodecArgs& args, int mode, hipStream_t s)
     bool lut = lut_path_supported(a, mode) &&
                (g_codec_path == 2 || (g_codec_path == 0 && a.n >= kLutMinBlocks));
     if (lut) return launch_codec_lut(a, mode, s);
+    if (g_codec_path == 0 && (a.q == 2 || a.q == 4) && mode != MODE_ENCODE) {
+        // layer-sized calls: the generic kernel decodes through the tables
+        // (one map and one coarse-point read per level, both L2-resident)
+        const DecodeTables* t = nullptr;
+        hipError_t e = get_decode_tables(a.q, 0, &t);
+        if (e != hipSuccess) return e;
+        a.dec_map = t->cid_map;
+        a.dec_coarse = t->coarse;
+    }
     return launch_codec_generic(a, mode, s);
 }
 

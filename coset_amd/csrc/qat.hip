@@ -345,14 +345,33 @@ __global__ void __launch_bounds__(256) colsum_partial_kernel(const void* g, int6
     }
 }
 
+// Stage 2: 64 columns per workgroup, the chunks split over 4 thread rows
+// (each sums its run of chunks with its loads in flight together), the 4
+// runs then added in order.
 __global__ void __launch_bounds__(256) colsum_final_kernel(const float* partial, int64_t chunks, int64_t cols,
                                                            float* out)
 {
-    const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= cols) return;
+    const int64_t c = (int64_t)blockIdx.x * 64 + (threadIdx.x & 63);
+    const int part = threadIdx.x >> 6;
+    const int64_t per = (chunks + 3) / 4;
+    const int64_t k0 = part * per, k1 = k0 + per < chunks ? k0 + per : chunks;
     float s = 0.f;
-    for (int64_t k = 0; k < chunks; ++k) s = __fadd_rn(s, partial[k * cols + c]);
-    out[c] = s;
+    if (c < cols) {
+        int64_t k = k0;
+        for (; k + 4 <= k1; k += 4) {
+            const float v0 = partial[k * cols + c], v1 = partial[(k + 1) * cols + c];
+            const float v2 = partial[(k + 2) * cols + c], v3 = partial[(k + 3) * cols + c];
+            s = __fadd_rn(__fadd_rn(__fadd_rn(__fadd_rn(s, v0), v1), v2), v3);
+        }
+        for (; k < k1; ++k) s = __fadd_rn(s, partial[k * cols + c]);
+    }
+    __shared__ float s_part[3][64];
+    if (part > 0) s_part[part - 1][threadIdx.x & 63] = s;
+    __syncthreads();
+    if (part == 0 && c < cols) {
+        const int l = threadIdx.x & 63;
+        out[c] = __fadd_rn(__fadd_rn(__fadd_rn(s, s_part[0][l]), s_part[1][l]), s_part[2][l]);
+    }
 }
 
 int64_t colsum_workspace_floats(int64_t rows, int64_t cols)
@@ -365,7 +384,7 @@ hipError_t launch_colsum(const void* g, int dtype, int64_t rows, int64_t cols, f
 {
     if (cols == 0) return hipSuccess;
     if (rows == 0) {
-        hipLaunchKernelGGL(colsum_final_kernel, dim3((unsigned)((cols + 255) / 256)), dim3(256), 0, s,
+        hipLaunchKernelGGL(colsum_final_kernel, dim3((unsigned)((cols + 63) / 64)), dim3(256), 0, s,
                            (const float*)workspace, (int64_t)0, cols, out);
         return hipGetLastError();
     }
@@ -377,7 +396,7 @@ hipError_t launch_colsum(const void* g, int dtype, int64_t rows, int64_t cols, f
         hipLaunchKernelGGL(colsum_partial_kernel<DT_BF16>, grid, dim3(256), 0, s, g, rows, cols, workspace);
     else
         hipLaunchKernelGGL(colsum_partial_kernel<DT_F16>, grid, dim3(256), 0, s, g, rows, cols, workspace);
-    hipLaunchKernelGGL(colsum_final_kernel, dim3((unsigned)((cols + 255) / 256)), dim3(256), 0, s,
+    hipLaunchKernelGGL(colsum_final_kernel, dim3((unsigned)((cols + 63) / 64)), dim3(256), 0, s,
                        (const float*)workspace, chunks, cols, out);
     return hipGetLastError();
 }

@@ -863,6 +863,164 @@ __global__ void __launch_bounds__(NW * 64) vlut_wide_kernel(VlutMatmulArgs p)
     }
 }
 
+// ---------------------------------------------------------------- MFMA deep kernel
+// Tile: 64 output rows x 64 tokens per workgroup of 8 waves; K split over
+// grid.y (partials [split][B][rows]) and, inside the workgroup, over the 8
+// waves.  Each wave owns all 4 row tiles of 16 rows (4 weight operands per
+// k-quad) and all 4 token tiles, so every activation operand read from LDS
+// feeds 4 MFMAs (the wide kernel's one-row-tile waves re-read all 64 tokens'
+// activations per 16 rows).  The workgroup issues every load of its K slice
+// up front -- activations (64 tokens x up to 1024 K, 128 KiB) into LDS, the
+// waves' weight pairs into registers -- then runs the products; the 8 waves'
+// partial tiles are summed in LDS in wave order, so a split writes one
+// partial (or, unsplit, the output) and the sums are deterministic.
+constexpr int kDeepRT = 4;                          // row tiles of 16 per wave
+constexpr int kDeepNW = 8;                          // waves per workgroup (split K)
+constexpr int kDeepRows = 16 * kDeepRT;             // 64 rows per workgroup
+constexpr int kDeepTokens = 64;
+constexpr int kDeepKqWave = 4;                      // at most 4 k-quads (128 K) per wave
+constexpr int kDeepKqWg = kDeepKqWave * kDeepNW;    // at most 32 k-quads (1024 K) per workgroup
+constexpr int kDeepStride = 32 * kDeepKqWg + 8;     // halves per token row in LDS (16-byte pad)
+
+template <int Q, int M, bool BF16, int FMT>
+__global__ void __launch_bounds__(kDeepNW * 64) vlut_deep_kernel(VlutMatmulArgs p)
+{
+    constexpr int WN = FMT == VLUT_DECODED ? 2 : M;  // uint32 per pair
+    constexpr int T = kDeepNW * 64;
+    constexpr int CH = 4 * kDeepKqWg;                // 16-byte activation chunks per token row
+    constexpr int AL = kDeepTokens * CH / T;         // activation loads per thread
+    static_assert(kDeepTokens * CH % T == 0, "whole activation loads per thread");
+    static_assert(kDeepNW * kDeepRows * kDeepTokens * 4 <= kDeepTokens * kDeepStride * 2,
+                  "the cross-wave sum fits in the activation buffer");
+    static_assert(kDeepStride * 2 % 16 == 0, "16-byte aligned token rows");
+    __shared__ __align__(16) uint16_t s_act[kDeepTokens * kDeepStride];
+    __shared__ uint64_t s_tab[FMT == VLUT_DECODED ? 1 : kSwarSlots];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4;
+    const int64_t kb_total = p.K / 8;
+    const int64_t kq_total = (kb_total + 3) / 4;
+    const int64_t kq_wg = (kq_total + gridDim.y - 1) / gridDim.y;   // <= kDeepKqWg (the plan's splits)
+    const int64_t kq_begin = blockIdx.y * kq_wg;
+    const int64_t kq_end = min(kq_total, kq_begin + kq_wg);
+    const int kqw = (int)((kq_wg + kDeepNW - 1) / kDeepNW);         // k-quads per wave, <= 4
+    const int64_t rb = (int64_t)blockIdx.x * kDeepRows;
+    const int64_t t_base = (int64_t)blockIdx.z * kDeepTokens;
+    const uint16_t* act = reinterpret_cast<const uint16_t*>(p.act);
+    const int bias = FMT == VLUT_DECODED ? kVlutDecodedBias : p.swar_bias;
+    const _Float16 f16_off = (_Float16)(1024 + bias);
+    const float f32_off = (float)bias;
+
+    // activations of the workgroup's K slice: chunk c = threadIdx.x + T i is
+    // (token c / CH, local k-block c % CH); outside the matrix or the slice it
+    // is zeroed through a mask (the load itself is unconditional, clamped)
+    uint4 av[AL];
+#pragma unroll
+    for (int i = 0; i < AL; ++i) {
+        const int c = threadIdx.x + T * i;
+        const int tok = c / CH, kbl = c % CH;
+        const int64_t kb = 4 * kq_begin + kbl;
+        const bool ok = t_base + tok < p.B && kb < kb_total && kq_begin + kbl / 4 < kq_end;
+        const uint4 v = *reinterpret_cast<const uint4*>(act + (ok ? (t_base + tok) * p.K + kb * 8 : 0));
+        uint32_t m;
+        __asm__("v_mov_b32 %0, %1" : "=v"(m) : "v"(ok ? ~0u : 0u));
+        av[i] = make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
+    }
+    // this wave's weight pairs: row tiles rt, k-quads kq_begin + wave * kqw + j
+    uint32_t w[kDeepRT][kDeepKqWave][WN];
+#pragma unroll
+    for (int rt = 0; rt < kDeepRT; ++rt) {
+        const int64_t r0 = rb + 16 * rt, row = r0 + (lane & 15);
+        const bool rows_ok = (FMT == VLUT_TILED || FMT == VLUT_DECODED) ? r0 < p.rows : row < p.rows;
+#pragma unroll
+        for (int j = 0; j < kDeepKqWave; ++j) {
+            const int64_t kq = kq_begin + (int64_t)wave * kqw + j;
+            const int64_t kb = 4 * kq + g;
+            const bool ok = rows_ok && j < kqw && kq < kq_end && kb < kb_total;
+            load_pair<Q, M, WN>(p, FMT, ok ? row : 0, ok ? kb : 0, kb_total, w[rt][j]);
+        }
+    }
+    if (FMT != VLUT_DECODED) {
+        for (int i = threadIdx.x; i < 512 + p.n_coarse; i += T) s_tab[i] = p.swar[i];
+    }
+#pragma unroll
+    for (int i = 0; i < AL; ++i) {
+        const int c = threadIdx.x + T * i;
+        *reinterpret_cast<uint4*>(&s_act[(c / CH) * kDeepStride + (c % CH) * 8]) = av[i];
+    }
+    __syncthreads();
+
+    float4_t acc[kDeepRT][4];
+#pragma unroll
+    for (int rt = 0; rt < kDeepRT; ++rt)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc[rt][s] = (float4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < kDeepKqWave; ++j) {
+        const int kql = wave * kqw + j;
+        if (j >= kqw || kq_begin + kql >= kq_end) break;   // wave-uniform
+        uint4 a[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+            a[s] = *reinterpret_cast<const uint4*>(&s_act[(16 * s + (lane & 15)) * kDeepStride + kql * 32 + 8 * g]);
+#pragma unroll
+        for (int rt = 0; rt < kDeepRT; ++rt) {
+            uint4 bw;
+            if constexpr (FMT == VLUT_DECODED)
+                bw = bytes_to_operand<BF16>(w[rt][j][0], w[rt][j][1 % WN], f16_off, f32_off);
+            else
+                bw = decode_pair_swar<Q, M, BF16>(s_tab, w[rt][j], f16_off, f32_off);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                if (BF16)
+                    acc[rt][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        __builtin_bit_cast(bf16x8_t, a[s]), __builtin_bit_cast(bf16x8_t, bw), acc[rt][s], 0, 0, 0);
+                else
+                    acc[rt][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        __builtin_bit_cast(half8_t, a[s]), __builtin_bit_cast(half8_t, bw), acc[rt][s], 0, 0, 0);
+            }
+        }
+    }
+
+    // the 8 waves' tiles summed in wave order through LDS (the activation
+    // buffer, no longer read), one 16-byte accumulator per (row tile, token
+    // tile) and lane: element i of acc[rt][s] in lane l is
+    // D[token 16 s + 4 (l / 16) + i][row 16 rt + l % 16]
+    __syncthreads();
+    float4* red = reinterpret_cast<float4*>(s_act);
+#pragma unroll
+    for (int rt = 0; rt < kDeepRT; ++rt)
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+            red[(wave * 16 + rt * 4 + s) * 64 + lane] =
+                make_float4(acc[rt][s][0], acc[rt][s][1], acc[rt][s][2], acc[rt][s][3]);
+    __syncthreads();
+    for (int e = threadIdx.x; e < 16 * 64; e += T) {
+        const int v4 = e >> 6, ln = e & 63;
+        float sum[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int wv = 0; wv < kDeepNW; ++wv) {
+            const float4 t = red[(wv * 16 + v4) * 64 + ln];
+            sum[0] += t.x;
+            sum[1] += t.y;
+            sum[2] += t.z;
+            sum[3] += t.w;
+        }
+        const int rt = v4 >> 2, s = v4 & 3;
+        const int64_t o = rb + 16 * rt + (ln & 15);
+        if (o >= p.rows) continue;
+        const float sc = p.scale ? (p.scale_mode == 0 ? p.scale[o] : 1.f / p.scale[o]) : 1.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int64_t tok = t_base + 16 * s + 4 * (ln >> 4) + i;
+            if (tok >= p.B) continue;
+            if (gridDim.y == 1)
+                p.out[tok * p.rows + o] = vlut_epilogue(sum[i] * 0.5f * sc, o, p.bias, p.lsq_alpha, p.lsq_qmax);
+            else
+                p.partial[((int64_t)blockIdx.y * p.B + tok) * p.rows + o] = sum[i];
+        }
+    }
+}
+
 // ---------------------------------------------------------------- reduce
 __global__ void __launch_bounds__(256) vlut_reduce_kernel(const float* partial, int splits, int64_t B,
                                                          int64_t rows, const float* scale, int scale_mode,
@@ -901,6 +1059,37 @@ __global__ void __launch_bounds__(256) vlut_reduce_sm_kernel(const float* partia
     for (int s = 0; s < splits; ++s) acc += partial[s * n + i];
     float sc = scale ? (scale_mode == 0 ? scale[o] : 1.f / scale[o]) : 1.f;
     out[i] = vlut_epilogue(acc * mult * sc, o, bias, lsq_alpha, lsq_qmax);
+}
+
+// The same with four consecutive outputs (one token, rows o..o+3; rows % 4
+// == 0) per thread: 16-byte loads of every split's partials and one 16-byte
+// store; each output's splits are still summed in order.
+__global__ void __launch_bounds__(256) vlut_reduce_sm4_kernel(const float* partial, int splits, int64_t B,
+                                                             int64_t rows, const float* scale, int scale_mode,
+                                                             float mult, const float* bias, const float* lsq_alpha,
+                                                             int lsq_qmax, float* out)
+{
+    const int64_t n4 = B * rows / 4;
+    const int64_t i4 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i4 >= n4) return;
+    const float4* p4 = reinterpret_cast<const float4*>(partial);
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < splits; ++s) {
+        const float4 v = p4[s * n4 + i4];
+        acc[0] += v.x;
+        acc[1] += v.y;
+        acc[2] += v.z;
+        acc[3] += v.w;
+    }
+    const int64_t o0 = (4 * i4) % rows;
+    float r[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t o = o0 + j;
+        const float sc = scale ? (scale_mode == 0 ? scale[o] : 1.f / scale[o]) : 1.f;
+        r[j] = vlut_epilogue(acc[j] * mult * sc, o, bias, lsq_alpha, lsq_qmax);
+    }
+    reinterpret_cast<float4*>(out)[i4] = make_float4(r[0], r[1], r[2], r[3]);
 }
 
 // ---------------------------------------------------------------- launchers
@@ -989,6 +1178,7 @@ hipError_t vlut_dot(const void* words, int64_t n, int M, int q, const float* vlu
 
 int g_vlut_swar = 1;
 int g_vlut_splits = 0;
+int g_vlut_deep = 1;
 
 namespace {
 
@@ -1018,6 +1208,18 @@ VlutPlan vlut_plan(int64_t rows, int64_t B, int64_t K, int q, int M, int method)
         return {VK_LDS, (int)std::max<int64_t>(1, std::min<int64_t>(want, kb))};
     }
     const bool swar = g_vlut_swar && ((q == 2 && M <= 4) || (q == 4 && M <= 2));
+    if (swar && B > 32 && g_vlut_deep) {
+        // 64-row, 64-token workgroups, at most 32 k-quads each: enough K
+        // splits for that, and more (down to one k-quad per workgroup) to
+        // fill the CUs
+        const int64_t kq_total = (kb + 3) / 4;
+        const int64_t groups = ((rows + kDeepRows - 1) / kDeepRows) * ((B + kDeepTokens - 1) / kDeepTokens);
+        const int64_t min_splits = (kq_total + kDeepKqWg - 1) / kDeepKqWg;
+        int64_t splits = g_vlut_splits > 0 ? g_vlut_splits
+                                           : std::max<int64_t>(1, device_cu_count() / std::max<int64_t>(1, groups));
+        splits = std::max(min_splits, std::min<int64_t>(splits, kq_total));
+        return {VK_MFMA_DEEP, (int)splits};
+    }
     if (swar && B > 32) {
         // 128-row, 64-token workgroups sharing the activations through LDS,
         // with K splits to fill the CUs (each keeping at least one stage)
@@ -1174,6 +1376,39 @@ hipError_t dispatch_wide(const VlutMatmulArgs& p, int splits, hipStream_t s)
     }
 }
 
+template <int Q, int M, bool BF16>
+void launch_deep_fmt(const VlutMatmulArgs& p, int splits, hipStream_t s)
+{
+    dim3 grid((unsigned)((p.rows + kDeepRows - 1) / kDeepRows), (unsigned)splits,
+              (unsigned)((p.B + kDeepTokens - 1) / kDeepTokens));
+#define COSET_DEEP(F) hipLaunchKernelGGL((vlut_deep_kernel<Q, M, BF16, F>), grid, dim3(kDeepNW * 64), 0, s, p)
+    switch (p.prepared) {
+    case VLUT_RAW: COSET_DEEP(VLUT_RAW); break;
+    case VLUT_PREPARED: COSET_DEEP(VLUT_PREPARED); break;
+    case VLUT_DECODED: COSET_DEEP(VLUT_DECODED); break;
+    default: COSET_DEEP(VLUT_TILED); break;
+    }
+#undef COSET_DEEP
+}
+
+template <int Q>
+hipError_t dispatch_deep(const VlutMatmulArgs& p, int splits, hipStream_t s)
+{
+    const bool bf = p.act_dtype == DT_BF16;
+    switch (p.M) {
+#define COSET_M(MM) \
+    case MM: \
+        if constexpr (Q == 2 || MM <= 2) { \
+            if (bf) launch_deep_fmt<Q, MM, true>(p, splits, s); else launch_deep_fmt<Q, MM, false>(p, splits, s); \
+            return hipGetLastError(); \
+        } \
+        return hipErrorInvalidValue;
+    COSET_M(1) COSET_M(2) COSET_M(3) COSET_M(4)
+#undef COSET_M
+    default: return hipErrorInvalidValue;
+    }
+}
+
 template <int Q>
 hipError_t dispatch_rows(const VlutMatmulArgs& p, int splits, hipStream_t s)
 {
@@ -1206,16 +1441,29 @@ hipError_t vlut_matmul(VlutMatmulArgs p, const VlutPlan& plan, hipStream_t s)
     p.swar = t->swar;
     p.swar_ok = p.M <= t->swar_max_m && g_vlut_swar;
     p.swar_bias = p.swar_ok ? t->swar_bias[p.M] : 0;
-    if (p.prepared == VLUT_DECODED && plan.kernel != VK_MFMA_ROWS && plan.kernel != VK_MFMA_WIDE)
+    if (p.prepared == VLUT_DECODED && plan.kernel != VK_MFMA_ROWS && plan.kernel != VK_MFMA_WIDE &&
+        plan.kernel != VK_MFMA_DEEP)
         return hipErrorInvalidValue;
-    if (plan.kernel == VK_MFMA_WIDE) {
+    if (plan.kernel == VK_MFMA_WIDE || plan.kernel == VK_MFMA_DEEP) {
         if (!p.swar_ok) return hipErrorInvalidValue;
-        e = p.q == 4 ? dispatch_wide<4>(p, splits, s) : dispatch_wide<2>(p, splits, s);
+        if (plan.kernel == VK_MFMA_DEEP) {
+            const int64_t kq_total = (p.K / 8 + 3) / 4;
+            if ((kq_total + splits - 1) / splits > kDeepKqWg) return hipErrorInvalidValue;
+            e = p.q == 4 ? dispatch_deep<4>(p, splits, s) : dispatch_deep<2>(p, splits, s);
+        } else {
+            e = p.q == 4 ? dispatch_wide<4>(p, splits, s) : dispatch_wide<2>(p, splits, s);
+        }
         if (e != hipSuccess || splits == 1) return e;
         const int64_t nw = p.B * p.rows;
-        hipLaunchKernelGGL(vlut_reduce_sm_kernel, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, s, p.partial,
-                           splits, p.B, p.rows, p.scale, p.scale_mode, 0.5f, p.bias, p.lsq_alpha, p.lsq_qmax,
-                           p.out);
+        const bool v4 = p.rows % 4 == 0 && ((uintptr_t)p.out % 16) == 0 && ((uintptr_t)p.partial % 16) == 0;
+        if (v4)
+            hipLaunchKernelGGL(vlut_reduce_sm4_kernel, dim3((unsigned)((nw / 4 + 255) / 256)), dim3(256), 0, s,
+                               p.partial, splits, p.B, p.rows, p.scale, p.scale_mode, 0.5f, p.bias, p.lsq_alpha,
+                               p.lsq_qmax, p.out);
+        else
+            hipLaunchKernelGGL(vlut_reduce_sm_kernel, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, s, p.partial,
+                               splits, p.B, p.rows, p.scale, p.scale_mode, 0.5f, p.bias, p.lsq_alpha, p.lsq_qmax,
+                               p.out);
         return hipGetLastError();
     }
     if (plan.kernel == VK_MFMA_ROWS) {

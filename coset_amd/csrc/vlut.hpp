@@ -48,6 +48,8 @@ struct VlutMatmulArgs {
 extern int g_vlut_swar;
 // > 0 forces the number of K splits (clamped to what the method allows)
 extern int g_vlut_splits;
+// 1 (default): batches above 32 tokens take the deep kernel, 0 the wide one
+extern int g_vlut_deep;
 
 // Index of level word m of (row, k-block kb) in a weight of format fmt.
 // (VLUT_DECODED: index of the pair's first uint32; m and M are ignored.)
@@ -67,7 +69,7 @@ __host__ __device__ inline int64_t vlut_prepared_words(int64_t rows, int64_t kb,
 
 // Launch plan of a matmul: kernel and K splits (splits > 1 needs a
 // workspace of splits * B * rows floats and a reduce launch).
-enum VlutKernel { VK_LDS = 0, VK_MFMA_TILE = 1, VK_MFMA_ROWS = 2, VK_MFMA_WIDE = 3 };
+enum VlutKernel { VK_LDS = 0, VK_MFMA_TILE = 1, VK_MFMA_ROWS = 2, VK_MFMA_WIDE = 3, VK_MFMA_DEEP = 4 };
 struct VlutPlan {
     int kernel;
     int splits;
@@ -78,7 +80,9 @@ VlutPlan vlut_plan(int64_t rows, int64_t B, int64_t K, int q, int M, int method)
 // kernel runs unsplit and writes the output itself.
 inline int64_t vlut_workspace_floats(const VlutPlan& plan, int64_t B, int64_t rows)
 {
-    if ((plan.kernel == VK_MFMA_ROWS || plan.kernel == VK_MFMA_WIDE) && plan.splits == 1) return 0;
+    if ((plan.kernel == VK_MFMA_ROWS || plan.kernel == VK_MFMA_WIDE || plan.kernel == VK_MFMA_DEEP) &&
+        plan.splits == 1)
+        return 0;
     return (int64_t)plan.splits * B * rows;
 }
 

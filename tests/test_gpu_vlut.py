@@ -186,23 +186,79 @@ def test_vlut_matmul_ragged_shapes(B, mfma_decode):
             close(out, ref, 1e-3)
 
 
+def _close_elem(out, ref, mag, rtol=1e-3):
+    """Elementwise |out - ref| <= rtol * mag, mag = |a| @ |W|^T (>= |ref|)."""
+    out, ref, mag = (np.asarray(t, np.float64) for t in (out, ref, mag))
+    bad = np.abs(out - ref) > rtol * np.maximum(mag, np.abs(ref))
+    assert not bad.any(), (int(bad.sum()), float(np.abs(out - ref)[bad].max()))
+
+
 def test_c4_full_size_equals_decoded_product():
     """C4: 4096 x 4096 weights ~ N(0, 0.02) encoded with beta = 0.02 (q4 M2),
-    fp16 activations at B = 1, 8, 64; both methods equal a @ decode^T."""
+    fp16 activations at B = 1, 8, 64; every weight format and both methods
+    against the oracle's lookup sum on 48 sampled rows (elementwise within
+    1e-3 of |a| @ |W|^T), and against a @ decode^T on all rows."""
     import coset_amd
     g = torch.Generator(device="cuda").manual_seed(5)
     W = 0.02 * torch.randn((4096, 4096), device="cuda", generator=g)
     words = coset_amd.hnlq_encode(W.reshape(-1, 8), 4, 2, 0.02).reshape(4096, 512, 2)
-    prepared = coset_amd.vlut_prepare(words, 4)
+    forms = {"words": words, "tiled": coset_amd.vlut_prepare(words, 4),
+             "decoded": coset_amd.vlut_prepare(words, 4, layout="decoded")}
     dec = coset_amd.hnlq_decode(words.reshape(-1, 2), 4, 2, 0.02).reshape(4096, 4096)
+    rows = np.arange(7, 4096, 85)
+    words_rows = words.cpu().numpy().astype(np.uint32)[rows]
     for B in (1, 8, 64):
         a = torch.randn((B, 4096), device="cuda", generator=g).to(torch.float16)
-        ref = (a.double() @ dec.double().T).float()
+        af = a.float().cpu().numpy()
+        ref_rows = O.vlut_matmul(words_rows, np.full(len(rows), 0.02, np.float32), af, 4, 2)
+        mag_rows = np.abs(af).astype(np.float64) @ np.abs(dec[rows].cpu().numpy().astype(np.float64)).T
+        ref = (a.double() @ dec.double().T)
+        mag = (a.double().abs() @ dec.double().abs().T)
         for method in ("lds", "mfma"):
-            for w in (words, prepared):
+            for name, w in forms.items():
+                if name == "decoded" and method == "lds":
+                    continue
+                print(f"C4 B={B} {method} {name}", flush=True)
                 out = coset_amd.vlut_matmul(w, a, 4, scale=torch.full((4096,), 0.02), method=method)
-                err = (out - ref).abs().max().item()
-                assert err <= 1e-3 * ref.abs().max().item(), (B, method, type(w).__name__, err)
+                _close_elem(out[:, rows].cpu().numpy(), ref_rows, mag_rows)
+                assert ((out.double() - ref).abs() <= 1e-3 * mag).all().item(), (B, method, name)
+
+
+@pytest.mark.parametrize("deep", [1, 0])
+@pytest.mark.parametrize("splits", [0, 1, 3, 8, 64])
+@pytest.mark.parametrize("B", [33, 64, 100])
+def test_wide_batch_kernels_vs_oracle(deep, splits, B):
+    """Batches above 32 tokens (the deep kernel, or the wide one) with ragged
+    rows and K, any forced K split, every weight format: against the
+    oracle's lookup sum, elementwise within 1e-3 of |a| @ |W|^T."""
+    import coset_amd as ca
+    from coset_amd import _lib
+    rng = np.random.default_rng(17 * B + splits)
+    rows, K = 200, 1064                    # rows % 64 != 0, K / 8 = 133 k-blocks (not a multiple of 4)
+    W = rng.standard_normal((rows, K)).astype(np.float32)
+    codes = O.e8_encode(W.reshape(-1, 8), 4, 2)
+    words_np = O.pack_words(codes, 4).reshape(rows, K // 8, 2)
+    words = torch.from_numpy(words_np.astype(np.int32)).to(torch.uint16).cuda()
+    a = torch.from_numpy(rng.standard_normal((B, K)).astype(np.float32)).to(torch.bfloat16)
+    af = a.float().numpy()
+    scale = rng.uniform(0.5, 2.0, rows).astype(np.float32)
+    ref = O.vlut_matmul(words_np, scale, af, 4, 2)
+    decw = O.e8_decode(codes, 4, 2).reshape(rows, K) * scale[:, None]
+    mag = np.abs(af).astype(np.float64) @ np.abs(decw).T.astype(np.float64)
+    forms = [words] + [ca.vlut_prepare(words, 4, layout=lay) for lay in ("rowmajor", "tiled", "decoded")]
+    try:
+        _lib.set_vlut_deep(bool(deep))
+        _lib.set_vlut_splits(splits)
+        outs = []
+        for w in forms:
+            out = ca.vlut_matmul(w, a.cuda(), 4, scale=torch.from_numpy(scale), method="mfma")
+            _close_elem(out.cpu().numpy(), ref, mag)
+            outs.append(out)
+    finally:
+        _lib.set_vlut_splits(0)
+        _lib.set_vlut_deep(True)
+    for o in outs[1:]:                     # the formats feed identical MFMA operands
+        assert torch.equal(o, outs[0])
 
 
 @pytest.mark.parametrize("q,M", [(4, 2), (4, 1), (2, 3), (2, 4)])
