@@ -164,6 +164,10 @@ extern int g_fast_projection;  // 1 (default): encoders use the fast projection 
 extern int g_codec_plain;      // 1 (default): the table kernel's fixed-format variant where it applies
 extern int g_codec_dynamic;    // 1 (default): the fixed-format kernel takes its tiles from a counter
 constexpr int64_t kLutMinBlocks = 1 << 20;  // below it the table staging does not pay (layer-sized calls)
+// n zeroed counters of the current device's counter ring (counters.hpp) for
+// one launch on stream s, or null under graph capture; the launch's last
+// workgroup must put them back to zero.
+unsigned* take_counters(hipStream_t s, uint32_t n);
 
 // Workgroup barrier that orders LDS only: waits for this wave's LDS
 // operations, not for its loads and stores in flight (__syncthreads would

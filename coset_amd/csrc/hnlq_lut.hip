@@ -16,10 +16,12 @@
 // the outputs.
 #include <algorithm>
 #include <map>
+#include <atomic>
 #include <mutex>
 #include <utility>
 
 #include "codec_kernels.hpp"
+#include "counters.hpp"
 #include "tables.hpp"
 
 namespace coset {
@@ -34,15 +36,13 @@ struct LutShape {
 
 constexpr int kLutThreads = 1024;
 
-// Tile counters of the dynamic schedule: one pair per (device, stream) --
-// [0] hands out tiles, [1] counts finished workgroups, and the workgroup that
-// finishes last puts both back to zero, so every call starts from zero.
-// Calls on one stream run one after another and so never share a pair while
-// it counts.  Zero-initialised when the code object is loaded.
-constexpr int kTileSlots = 64;
+// Tile counters of the dynamic schedule: a pair taken from the per-device
+// counter ring (counters.hpp) for each launch -- [0] hands out tiles, [1]
+// counts finished workgroups, and the workgroup that finishes last puts both
+// back to zero.
 constexpr int kTileBlocks = 2;        // blocks per thread in a dynamic tile
 constexpr int kTileBlocksDecode = 2;  // the decoder's, whole next tile ahead (1, 4, 8 measured slower)
-static __device__ __align__(256) unsigned g_tile_ctr[kTileSlots][2];
+static __device__ __align__(256) unsigned g_counter_ring[kCounterRing];
 
 
 // Copies the decode tables to LDS: the map (n_map uint4) and the byte or
@@ -703,44 +703,41 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
     schedule_stride<In>(n, load, body, pro);
 }
 
-namespace {
-
-// The counter pair of the current device for stream s, or null when all
-// kTileSlots pairs of the device are taken or s is capturing a graph (the
-// kernels then use the static schedule: a replayed graph may run beside
-// later calls on the stream it was captured from, so it must not share
-// that stream's pair).
-unsigned* tile_counters(hipStream_t s)
+// n counters of the current device's ring for one launch on stream s, or
+// null while s captures a graph (a replayed graph keeps the counters it was
+// captured with and may run beside later launches, so the kernels take their
+// static schedule instead) or when the ring cannot be reached.
+unsigned* take_counters(hipStream_t s, uint32_t n)
 {
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(s, &cap) != hipSuccess) {
         (void)hipGetLastError();  // the query's own error, not the launch's
         return nullptr;
     }
-    if (cap != hipStreamCaptureStatusNone) return nullptr;
+    if (cap != hipStreamCaptureStatusNone || n == 0 || n > kCounterRing) return nullptr;
+    constexpr int kDevices = 64;
     static std::mutex mu;
-    static std::map<std::pair<int, hipStream_t>, int> slot_of;
-    static unsigned* base[64] = {nullptr};
-    static int used[64] = {0};
+    static unsigned* base[kDevices] = {nullptr};
+    static std::atomic<uint64_t> cursor[kDevices];
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-    std::lock_guard<std::mutex> lock(mu);
-    if (!base[dev]) {
-        void* p = nullptr;
-        if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_tile_ctr)) != hipSuccess || !p) return nullptr;
-        base[dev] = static_cast<unsigned*>(p);
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kDevices) return nullptr;
+    unsigned* b;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        if (!base[dev]) {
+            void* p = nullptr;
+            if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_counter_ring)) != hipSuccess || !p) {
+                (void)hipGetLastError();
+                return nullptr;
+            }
+            base[dev] = static_cast<unsigned*>(p);
+        }
+        b = base[dev];
     }
-    auto it = slot_of.find({dev, s});
-    int slot;
-    if (it != slot_of.end()) {
-        slot = it->second;
-    } else {
-        if (used[dev] >= kTileSlots) return nullptr;
-        slot = used[dev]++;
-        slot_of[{dev, s}] = slot;
-    }
-    return base[dev] + 2 * slot;
+    return b + ring_take(cursor[dev], n, kCounterRing);
 }
+
+namespace {
 
 int cu_count()
 {
@@ -764,7 +761,7 @@ hipError_t launch_plain(const CodecArgs& a, int grid, const uint16_t* map, const
     if constexpr (MODE == MODE_ENCODE || Q == 2 || M <= 2) {
         const bool scaled = a.scale_mode == SCALE_CODEC && a.beta != 1.f;
         const bool codes = MODE != MODE_DECODE && a.codes_f32;
-        unsigned* tiles = g_codec_dynamic ? tile_counters(s) : nullptr;
+        unsigned* tiles = g_codec_dynamic ? take_counters(s, 2) : nullptr;
         // packed words are always written by the encoder, optional in the
         // round trip (e8_quantize asks for the decoded blocks only)
         const bool pk = MODE == MODE_ENCODE || (MODE == MODE_ROUNDTRIP && a.packed);

@@ -293,9 +293,9 @@ def test_roundtrip_with_float_codes(ca, path, beta, extra, dynamic):
 
 
 def test_dynamic_schedule_matches_static(ca):
-    """The fixed-format table kernel's dynamic tile schedule (per-stream
-    counter pair, reset by the last workgroup) against its static grid
-    stride: partial last tiles, fewer tiles than workgroups, calls repeated
+    """The fixed-format table kernel's dynamic tile schedule (a counter pair
+    from the per-device ring per launch, reset by the last workgroup) against
+    its static grid stride: partial last tiles, fewer tiles than workgroups, calls repeated
     on one stream and interleaved over three streams, all three modes."""
     from coset_amd import _lib
     _lib.require_gpu()
@@ -435,3 +435,40 @@ def test_input_lengths_are_checked():
         ca.PackedLinear(tensors, meta)
     with pytest.raises(ValueError):
         ca.PackedLinear({"words": words.cpu(), "beta": torch.ones(16), "bias": torch.zeros(5)}, meta)
+
+
+def test_dynamic_schedule_on_many_streams(ca):
+    """More streams than the old per-stream slot table held (64), each
+    launching concurrently with the others, and more launches than one lap
+    of the counter ring: every result equals the static schedule's."""
+    from coset_amd import _lib
+    _lib.require_gpu()
+    rng = np.random.default_rng(32)
+    x = dev(rng.standard_normal(((1 << 20) + 333, 8)).astype(np.float32))
+    try:
+        _lib.set_codec_path(2)
+        _lib.set_codec_dynamic(False)
+        _, ref = ca.hnlq_roundtrip(x, 4, 2, 1.0)
+        _lib.set_codec_dynamic(True)
+        torch.cuda.synchronize()
+        streams = [torch.cuda.Stream() for _ in range(80)]
+        outs = []
+        for s in streams:
+            with torch.cuda.stream(s):
+                outs.append(ca.hnlq_roundtrip(x, 4, 2, 1.0)[1])
+        torch.cuda.synchronize()
+        for i, o in enumerate(outs):
+            assert torch.equal(o, ref), i
+        # 8300 launches on one stream: past one lap of the 16384-counter ring
+        out = torch.empty_like(ref)
+        small = x[:4096]
+        _lib.set_codec_dynamic(False)
+        _, ref_small = ca.hnlq_roundtrip(small, 4, 2, 1.0)
+        _lib.set_codec_dynamic(True)
+        for _ in range(8300):
+            ca.hnlq_roundtrip(small, 4, 2, 1.0, decoded_out=out[:4096], want_packed=False)
+        torch.cuda.synchronize()
+        assert torch.equal(out[:4096], ref_small)
+    finally:
+        _lib.set_codec_dynamic(True)
+        _lib.set_codec_path(0)
