@@ -17,13 +17,18 @@
 //                          (8 + n_coarse floats instead of q^8 = 65536 at q = 4)
 //   vlut_mfma_kernel       same product by decoding 2 x_hat (exact in fp16/bf16)
 //                          into LDS and multiplying on the matrix cores
+//                          (for (q, M) whose byte tables would overflow)
 //   vlut_reduce_kernel     sums the split-K partials and applies s_o
+// The byte-table matrix-core kernels live in vlut_rows.hip (up to 32 tokens)
+// and vlut_wide.hip (wide and deep kernels, more tokens), with the helpers
+// they share in vlut_mfma.hpp.
 #include <algorithm>
 
 #include "codec_kernels.hpp"
 #include "tables.hpp"
 #include "vlut.hpp"
 #include "lsq.hpp"
+#include "vlut_mfma.hpp"
 
 namespace coset {
 
@@ -261,24 +266,6 @@ __global__ void __launch_bounds__(kVlutThreads) vlut_lds_kernel(VlutMatmulArgs p
 // minus (1024 + bias), exact as every value is an integer below 2048.
 // Decode (integer): 2x = sum_m q^m (2Gb - q (2c)) with the digits unpacked,
 // for the (q, M) whose bytes would overflow.
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
-typedef short bf16x4_t __attribute__((ext_vector_type(4)));
-typedef float float4_t __attribute__((ext_vector_type(4)));
-
-constexpr int kMfmaRows = 64;
-constexpr int kMfmaKB = 16;              // k-blocks per step
-constexpr int kMfmaK = kMfmaKB * 8;      // 128 K values per step
-constexpr int kMfmaLd = kMfmaK + 8;      // row pitch in halves (16-byte aligned, skews banks)
-constexpr int kMfmaMaxSteps = 4;         // steps per workgroup: its K range is <= 64 k-blocks
-constexpr int kSwarSlots = 512 + kMaxCoarseVlut;
-
-// two halves (bit patterns 0x64bb) from bytes k, k+1 of w
-__device__ __forceinline__ uint32_t bytes_to_f16_bits(uint32_t w, bool upper)
-{
-    return __builtin_amdgcn_perm(0x64646464u, w, upper ? 0x04030402u : 0x04010400u);
-}
-
 template <int Q, int M, bool BF16, bool SWAR, int NT>
 __global__ void __launch_bounds__(256) vlut_mfma_kernel(VlutMatmulArgs p)
 {
@@ -476,547 +463,6 @@ __global__ void __launch_bounds__(256) vlut_mfma_kernel(VlutMatmulArgs p)
                 int64_t tok = t_base + s * 16 + 4 * (lane >> 4) + i;
                 if (tok < p.B) p.partial[(tok * p.rows + row) * gridDim.y + blockIdx.y] = acc[s][i];
             }
-        }
-    }
-}
-
-// ---------------------------------------------------------------- MFMA rows kernel
-// Tile: 16 output rows per workgroup, K split over its 8 waves (and over
-// grid.y when the row tiles alone cannot fill the GPU), up to 16 * NTILE
-// tokens (grid.z beyond).  In each step lane l owns row l % 16 and k-block
-// 4 kq + l / 16: it decodes that pair's 2 x_hat through the byte tables
-// straight into its 8-half B operand of one 16x16x32 MFMA and loads
-// act[token][8 kb, 8 kb + 8) as its A operand, so neither goes through LDS.
-// Any assignment of K positions to (lane group, operand slot) works as long
-// as A and B use the same one, which holds since both come from the same kb.
-// In the tiled format a step's 64 word groups are one contiguous run.  The
-// waves' sums meet in LDS; with one K split the workgroup writes the output.
-typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-
-constexpr int kRowsWaves = 8;
-
-template <int Q, int M, int WN>
-__device__ __forceinline__ void load_pair(const VlutMatmulArgs& p, int fmt, int64_t row, int64_t kb, int64_t kb_total,
-                                          uint32_t w[WN])
-{
-    const int64_t i0 = vlut_word_index(fmt, row, kb, 0, kb_total, M);
-    if (fmt == VLUT_DECODED) {
-        const uint2 v = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint32_t*>(p.words) + i0);
-        w[0] = v.x;
-        w[1 % WN] = v.y;
-    } else if (fmt == VLUT_RAW) {
-        const uint16_t* src = reinterpret_cast<const uint16_t*>(p.words) + i0;
-        constexpr uint32_t kMask = Q == 2 ? 0xffu : 0xffffu;  // q^8 - 1: map bounds for any input
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-            const uint32_t x = src[m] & kMask;
-            w[m] = ((uint32_t)p.map[x] << 16) | x;
-        }
-    } else {
-        const uint32_t* src = reinterpret_cast<const uint32_t*>(p.words) + i0;
-        if (M == 2) {
-            const uint2 v = *reinterpret_cast<const uint2*>(src);
-            w[0] = v.x;
-            w[1 % M] = v.y;
-        } else if (M == 4) {
-            const uint4 v = *reinterpret_cast<const uint4*>(src);
-            w[0] = v.x;
-            w[1 % M] = v.y;
-            w[2 % M] = v.z;
-            w[3 % M] = v.w;
-        } else {
-#pragma unroll
-            for (int m = 0; m < M; ++m) w[m] = src[m];
-        }
-    }
-}
-
-// Eight biased bytes (x0: coordinates 0-3, x1: 4-7) minus the bias as 8
-// halves (fp16) or bf16 values, exact.
-template <bool BF16>
-__device__ __forceinline__ uint4 bytes_to_operand(uint32_t x0, uint32_t x1, _Float16 f16_off, float f32_off)
-{
-    uint32_t hv[4];
-    if (BF16) {
-        float f[8];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            f[j] = (float)((x0 >> (8 * j)) & 0xffu) - f32_off;
-            f[4 + j] = (float)((x1 >> (8 * j)) & 0xffu) - f32_off;
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            hv[j] = __builtin_amdgcn_perm(__float_as_uint(f[2 * j + 1]), __float_as_uint(f[2 * j]), 0x07060302u);
-    } else {
-        const uint32_t raw[4] = {bytes_to_f16_bits(x0, false), bytes_to_f16_bits(x0, true),
-                                 bytes_to_f16_bits(x1, false), bytes_to_f16_bits(x1, true)};
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            hv[j] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, raw[j]) - (half2_t){f16_off, f16_off});
-    }
-    return make_uint4(hv[0], hv[1], hv[2], hv[3]);
-}
-
-// 2 x_hat of one pair as 8 halves (fp16) or bf16 values, exact.
-template <int Q, int M, bool BF16>
-__device__ __forceinline__ uint4 decode_pair_swar(const uint64_t* s_tab, const uint32_t w[M], _Float16 f16_off,
-                                                  float f32_off)
-{
-    uint32_t x0 = 0u, x1 = 0u;
-#pragma unroll
-    for (int m = M - 1; m >= 0; --m) {
-        const uint32_t v = w[m];
-        const uint2 tl = *reinterpret_cast<const uint2*>(&s_tab[256 + (v & 0xffu)]);
-        const uint2 tc = *reinterpret_cast<const uint2*>(&s_tab[512 + (v >> 16)]);
-        uint32_t l0 = tl.x + tc.x, l1 = tl.y + tc.y;
-        if (Q != 2) {
-            const uint2 th = *reinterpret_cast<const uint2*>(&s_tab[(v >> 8) & 0xffu]);
-            l0 += th.x;
-            l1 += th.y;
-        }
-        x0 = x0 * Q + l0;
-        x1 = x1 * Q + l1;
-    }
-    return bytes_to_operand<BF16>(x0, x1, f16_off, f32_off);
-}
-
-// Output epilogue: + bias[o], then the LSQ activation quantizer (fp32, the
-// reference's order: the value F.linear(x, W, b) followed by actq,
-// coset/core/layers.py:472-484).
-__device__ __forceinline__ float vlut_epilogue(float y, int64_t o, const float* bias, const float* lsq_alpha,
-                                               int lsq_qmax)
-{
-    if (bias) y = __fadd_rn(y, bias[o]);
-    if (lsq_alpha) y = lsq_value(y, lsq_scale(lsq_alpha, lsq_qmax));
-    return y;
-}
-
-template <int Q, int M, bool BF16, int NTILE, int FMT>
-__global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulArgs p)
-{
-    constexpr int CH = 8 / NTILE;  // steps per prefetch chunk
-    __shared__ uint64_t s_tab[kSwarSlots];
-    __shared__ float s_red[kRowsWaves][NTILE * 4][64];
-
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4;
-    const int64_t kb_total = p.K / 8;
-    const int64_t kq_total = (kb_total + 3) / 4;
-    const int64_t kq_wg = (kq_total + gridDim.y - 1) / gridDim.y;
-    const int64_t kq_begin = blockIdx.y * kq_wg;
-    const int64_t kq_end = min(kq_total, kq_begin + kq_wg);
-    const int64_t kq_wave = (kq_end - kq_begin + kRowsWaves - 1) / kRowsWaves;
-    const int64_t w0 = kq_begin + wave * kq_wave;
-    const int64_t w1 = min(kq_end, w0 + kq_wave);
-    const int64_t r0 = (int64_t)blockIdx.x * 16;
-    const int64_t row = r0 + (lane & 15);
-    const int64_t t_base = (int64_t)blockIdx.z * 16 * NTILE;
-    const uint16_t* act = reinterpret_cast<const uint16_t*>(p.act);
-    const int bias = FMT == VLUT_DECODED ? kVlutDecodedBias : p.swar_bias;
-    const _Float16 f16_off = (_Float16)(1024 + bias);
-    const float f32_off = (float)bias;
-    constexpr int WN = FMT == VLUT_DECODED ? 2 : M;  // uint32 per pair
-
-    struct Chunk {
-        uint32_t w[CH][WN];
-        uint4 a[CH][NTILE];
-    };
-    auto load = [&](int64_t c0, Chunk& ck) {
-#pragma unroll
-        for (int st = 0; st < CH; ++st) {
-            const int64_t kq = c0 + st;
-            const int64_t kb = 4 * kq + g;
-            const bool kb_ok = kq < w1 && kb < kb_total;
-#pragma unroll
-            for (int m = 0; m < WN; ++m) ck.w[st][m] = 0u;
-            if (kb_ok && (FMT == VLUT_TILED || FMT == VLUT_DECODED || row < p.rows))
-                load_pair<Q, M, WN>(p, FMT, row, kb, kb_total, ck.w[st]);
-#pragma unroll
-            for (int s = 0; s < NTILE; ++s) {
-                const int64_t tok = t_base + 16 * s + (lane & 15);
-                ck.a[st][s] = make_uint4(0u, 0u, 0u, 0u);
-                if (kb_ok && tok < p.B) ck.a[st][s] = *reinterpret_cast<const uint4*>(act + tok * p.K + kb * 8);
-            }
-        }
-    };
-    float4_t acc[NTILE];
-#pragma unroll
-    for (int s = 0; s < NTILE; ++s) acc[s] = (float4_t){0.f, 0.f, 0.f, 0.f};
-    auto run = [&](const Chunk& ck) {
-#pragma unroll
-        for (int st = 0; st < CH; ++st) {
-            uint4 bw;
-            if constexpr (FMT == VLUT_DECODED)
-                bw = bytes_to_operand<BF16>(ck.w[st][0], ck.w[st][1 % WN], f16_off, f32_off);
-            else
-                bw = decode_pair_swar<Q, M, BF16>(s_tab, ck.w[st], f16_off, f32_off);
-#pragma unroll
-            for (int s = 0; s < NTILE; ++s) {
-                if (BF16)
-                    acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ck.a[st][s]),
-                                                                    __builtin_bit_cast(bf16x8_t, bw), acc[s], 0, 0, 0);
-                else
-                    acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, ck.a[st][s]),
-                                                                   __builtin_bit_cast(half8_t, bw), acc[s], 0, 0, 0);
-            }
-        }
-    };
-
-    Chunk c_a, c_b;
-    int64_t c0 = w0;
-    if (c0 < w1) load(c0, c_a);
-    // the tables are staged while the first chunk's loads are in flight
-    if constexpr (FMT != VLUT_DECODED) {
-        for (int i = threadIdx.x; i < 512 + p.n_coarse; i += blockDim.x) s_tab[i] = p.swar[i];
-        __syncthreads();
-    }
-    for (; c0 < w1; c0 += 2 * CH) {
-        const int64_t c1 = c0 + CH;
-        if (c1 < w1) load(c1, c_b);
-        run(c_a);
-        if (c1 >= w1) break;
-        const int64_t c2 = c1 + CH;
-        if (c2 < w1) load(c2, c_a);
-        run(c_b);
-    }
-
-    // D[token = 16 s + 4 (lane / 16) + i][row = lane % 16]; sum the waves
-#pragma unroll
-    for (int s = 0; s < NTILE; ++s)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s_red[wave][s * 4 + i][lane] = acc[s][i];
-    __syncthreads();
-    for (int e = threadIdx.x; e < NTILE * 256; e += blockDim.x) {
-        const int si = e >> 6, ln = e & 63;
-        float v = 0.f;
-#pragma unroll
-        for (int w = 0; w < kRowsWaves; ++w) v += s_red[w][si][ln];
-        const int64_t tok = t_base + 16 * (si >> 2) + 4 * (ln >> 4) + (si & 3);
-        const int64_t o = r0 + (ln & 15);
-        if (tok >= p.B || o >= p.rows) continue;
-        if (gridDim.y == 1) {
-            float sc = p.scale ? (p.scale_mode == 0 ? p.scale[o] : 1.f / p.scale[o]) : 1.f;
-            p.out[tok * p.rows + o] = vlut_epilogue(v * 0.5f * sc, o, p.bias, p.lsq_alpha, p.lsq_qmax);
-        } else {
-            p.partial[(tok * p.rows + o) * gridDim.y + blockIdx.y] = v;
-        }
-    }
-}
-
-// ---------------------------------------------------------------- MFMA wide kernel
-// Tile: 128 output rows (8 row tiles of 16, one per wave) x 64 tokens per
-// workgroup, K split over grid.y (partials [split][B][rows]), token tiles of
-// 64 over grid.z.  The activations of a stage (64 tokens x 128 K) are loaded
-// once per workgroup, two 16-byte loads per thread, and shared by the 8
-// waves through LDS (double-buffered, one LDS-only barrier per stage); each
-// wave decodes its own row tile's weight pairs into the B operand as the rows
-// kernel does and runs 4 MFMAs (one per 16-token tile) per k-quad.  Every
-// global load is unconditional (clamped; what lies outside the matrix or the
-// workgroup's K range has zero activations), so the waits before a stage
-// leave the next stage's loads in flight.
-constexpr int kWideRT = 1;                            // row tiles of 16 per wave
-constexpr int kWideNW = 8;                            // waves per workgroup
-constexpr int kWideRows = 16 * kWideRT * kWideNW;     // rows per workgroup
-constexpr int kWideTokens = 64;
-constexpr int kWideStageKq = 4;                       // k-quads (4 k-blocks of 8, 32 K) per stage
-constexpr int kWideActStride = 32 * kWideStageKq + 8; // halves per token row in LDS (16-byte pad)
-
-template <int Q, int M, bool BF16, int FMT, int RT, int NW>
-__global__ void __launch_bounds__(NW * 64) vlut_wide_kernel(VlutMatmulArgs p)
-{
-    constexpr int WN = FMT == VLUT_DECODED ? 2 : M;  // uint32 per pair
-    constexpr int T = NW * 64;                       // threads
-    constexpr int P = 4 * kWideStageKq;              // 16-byte k-block chunks per token and stage
-    constexpr int AL = kWideTokens * P / T;          // activation loads per thread and stage
-    static_assert(kWideTokens * P % T == 0, "whole activation loads per thread");
-    __shared__ uint64_t s_tab[FMT == VLUT_DECODED ? 1 : kSwarSlots];
-    __shared__ __align__(16) uint16_t s_act[2][kWideTokens][kWideActStride];
-
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4;
-    const int64_t kb_total = p.K / 8;
-    const int64_t kq_total = (kb_total + 3) / 4;
-    const int64_t kq_wg = (kq_total + gridDim.y - 1) / gridDim.y;
-    const int64_t kq_begin = blockIdx.y * kq_wg;
-    const int64_t kq_end = min(kq_total, kq_begin + kq_wg);
-    const int64_t rt0 = ((int64_t)blockIdx.x * NW + wave) * RT;  // first row tile of this wave
-    const int64_t t_base = (int64_t)blockIdx.z * kWideTokens;
-    const uint16_t* act = reinterpret_cast<const uint16_t*>(p.act);
-    const int bias = FMT == VLUT_DECODED ? kVlutDecodedBias : p.swar_bias;
-    const _Float16 f16_off = (_Float16)(1024 + bias);
-    const float f32_off = (float)bias;
-
-    // this thread's share of a stage's activations: chunks threadIdx.x + T i
-    // (token c / P, k-block c % P of the stage, 16 bytes each)
-    struct Act {
-        uint4 v[AL];
-    };
-    const int a_part = threadIdx.x % P;
-    auto load_act = [&](int64_t kq0, Act& ac) {
-#pragma unroll
-        for (int i = 0; i < AL; ++i) {
-            const int tok = (threadIdx.x + T * i) / P;
-            const int64_t kb = 4 * kq0 + a_part;
-            const bool ok = t_base + tok < p.B && kb < kb_total && kq0 + a_part / 4 < kq_end;
-            const uint4 v =
-                *reinterpret_cast<const uint4*>(act + (ok ? (t_base + tok) * p.K + kb * 8 : 0));
-            // zeroed through a mask the compiler cannot trace back to ok: a
-            // select would let it branch around the load, and the waits after
-            // a conditional load drain the queue
-            uint32_t m;
-            __asm__("v_mov_b32 %0, %1" : "=v"(m) : "v"(ok ? ~0u : 0u));
-            ac.v[i] = make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
-        }
-    };
-    struct W {
-        uint32_t w[RT][kWideStageKq][WN];
-    };
-    auto load_w = [&](int64_t kq0, W& ws) {
-#pragma unroll
-        for (int t = 0; t < RT; ++t) {
-            const int64_t r0 = (rt0 + t) * 16, row = r0 + (lane & 15);
-            // rows that hold weights (whole tiles in the tiled formats)
-            const bool rows_ok = (FMT == VLUT_TILED || FMT == VLUT_DECODED) ? r0 < p.rows : row < p.rows;
-#pragma unroll
-            for (int j = 0; j < kWideStageKq; ++j) {
-                const int64_t kb = 4 * (kq0 + j) + g;
-                const bool ok = rows_ok && kb < kb_total;
-                // outside the matrix: pair (0, 0) instead, under zero
-                // activations or an output that is not stored
-                load_pair<Q, M, WN>(p, FMT, ok ? row : 0, ok ? kb : 0, kb_total, ws.w[t][j]);
-            }
-        }
-    };
-    float4_t acc[RT][4];
-#pragma unroll
-    for (int t = 0; t < RT; ++t)
-#pragma unroll
-        for (int s = 0; s < 4; ++s) acc[t][s] = (float4_t){0.f, 0.f, 0.f, 0.f};
-
-    if (FMT != VLUT_DECODED) {
-        for (int i = threadIdx.x; i < 512 + p.n_coarse; i += blockDim.x) s_tab[i] = p.swar[i];
-    }
-    const int stages = (int)((kq_end - kq_begin + kWideStageKq - 1) / kWideStageKq);
-    W w_now, w_next;
-    Act a_next;
-    load_act(kq_begin, a_next);
-    load_w(kq_begin, w_now);
-    for (int st = 0; st < stages; ++st) {
-        const int64_t kq0 = kq_begin + (int64_t)st * kWideStageKq;
-        const int buf = st & 1;
-#pragma unroll
-        for (int i = 0; i < AL; ++i)
-            *reinterpret_cast<uint4*>(&s_act[buf][(threadIdx.x + T * i) / P][a_part * 8]) = a_next.v[i];
-        lds_barrier();
-        // the next stage's loads go out before this stage's products
-        const int64_t kq1 = st + 1 < stages ? kq0 + kWideStageKq : kq0;
-        load_act(kq1, a_next);
-        load_w(kq1, w_next);
-        __asm__ volatile("" ::: "memory");  // the loads stay ahead of the products
-        uint4 av_all[kWideStageKq][4];
-#pragma unroll
-        for (int j = 0; j < kWideStageKq; ++j)
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-                av_all[j][s] = *reinterpret_cast<const uint4*>(&s_act[buf][16 * s + (lane & 15)][(4 * j + g) * 8]);
-#pragma unroll
-        for (int j = 0; j < kWideStageKq; ++j) {
-#pragma unroll
-            for (int t = 0; t < RT; ++t) {
-                uint4 bw;
-                if constexpr (FMT == VLUT_DECODED)
-                    bw = bytes_to_operand<BF16>(w_now.w[t][j][0], w_now.w[t][j][1 % WN], f16_off, f32_off);
-                else
-                    bw = decode_pair_swar<Q, M, BF16>(s_tab, w_now.w[t][j], f16_off, f32_off);
-#pragma unroll
-                for (int s = 0; s < 4; ++s) {
-                    const uint4 av = av_all[j][s];
-                    if (BF16)
-                        acc[t][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            __builtin_bit_cast(bf16x8_t, av), __builtin_bit_cast(bf16x8_t, bw), acc[t][s], 0, 0, 0);
-                    else
-                        acc[t][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            __builtin_bit_cast(half8_t, av), __builtin_bit_cast(half8_t, bw), acc[t][s], 0, 0, 0);
-                }
-            }
-        }
-        w_now = w_next;
-    }
-
-    // D[token = 16 s + 4 (lane / 16) + i][row = lane % 16]
-#pragma unroll
-    for (int t = 0; t < RT; ++t) {
-        const int64_t o = (rt0 + t) * 16 + (lane & 15);
-        if (o >= p.rows) continue;
-        const float sc = p.scale ? (p.scale_mode == 0 ? p.scale[o] : 1.f / p.scale[o]) : 1.f;
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int64_t tok = t_base + 16 * s + 4 * g + i;
-                if (tok >= p.B) continue;
-                if (gridDim.y == 1)
-                    p.out[tok * p.rows + o] =
-                        vlut_epilogue(acc[t][s][i] * 0.5f * sc, o, p.bias, p.lsq_alpha, p.lsq_qmax);
-                else
-                    p.partial[((int64_t)blockIdx.y * p.B + tok) * p.rows + o] = acc[t][s][i];
-            }
-    }
-}
-
-// ---------------------------------------------------------------- MFMA deep kernel
-// Tile: 64 output rows x 64 tokens per workgroup of 8 waves; K split over
-// grid.y (partials [split][B][rows]) and, inside the workgroup, over the 8
-// waves.  Each wave owns all 4 row tiles of 16 rows (4 weight operands per
-// k-quad) and all 4 token tiles, so every activation operand read from LDS
-// feeds 4 MFMAs (the wide kernel's one-row-tile waves re-read all 64 tokens'
-// activations per 16 rows).  The workgroup issues every load of its K slice
-// up front -- activations (64 tokens x up to 1024 K, 128 KiB) into LDS, the
-// waves' weight pairs into registers -- then runs the products; the 8 waves'
-// partial tiles are summed in LDS in wave order, so a split writes one
-// partial (or, unsplit, the output) and the sums are deterministic.
-constexpr int kDeepRT = 4;                          // row tiles of 16 per wave
-constexpr int kDeepNW = 8;                          // waves per workgroup (split K)
-constexpr int kDeepRows = 16 * kDeepRT;             // 64 rows per workgroup
-constexpr int kDeepTokens = 64;
-constexpr int kDeepKqWave = 4;                      // at most 4 k-quads (128 K) per wave
-constexpr int kDeepKqWg = kDeepKqWave * kDeepNW;    // at most 32 k-quads (1024 K) per workgroup
-constexpr int kDeepStride = 32 * kDeepKqWg + 8;     // halves per token row in LDS (16-byte pad)
-
-template <int Q, int M, bool BF16, int FMT>
-__global__ void __launch_bounds__(kDeepNW * 64) vlut_deep_kernel(VlutMatmulArgs p)
-{
-    constexpr int WN = FMT == VLUT_DECODED ? 2 : M;  // uint32 per pair
-    constexpr int T = kDeepNW * 64;
-    constexpr int CH = 4 * kDeepKqWg;                // 16-byte activation chunks per token row
-    constexpr int AL = kDeepTokens * CH / T;         // activation loads per thread
-    static_assert(kDeepTokens * CH % T == 0, "whole activation loads per thread");
-    static_assert(kDeepNW * kDeepRows * kDeepTokens * 4 <= kDeepTokens * kDeepStride * 2,
-                  "the cross-wave sum fits in the activation buffer");
-    static_assert(kDeepStride * 2 % 16 == 0, "16-byte aligned token rows");
-    __shared__ __align__(16) uint16_t s_act[kDeepTokens * kDeepStride];
-    __shared__ uint64_t s_tab[FMT == VLUT_DECODED ? 1 : kSwarSlots];
-
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4;
-    const int64_t kb_total = p.K / 8;
-    const int64_t kq_total = (kb_total + 3) / 4;
-    const int64_t kq_wg = (kq_total + gridDim.y - 1) / gridDim.y;   // <= kDeepKqWg (the plan's splits)
-    const int64_t kq_begin = blockIdx.y * kq_wg;
-    const int64_t kq_end = min(kq_total, kq_begin + kq_wg);
-    const int kqw = (int)((kq_wg + kDeepNW - 1) / kDeepNW);         // k-quads per wave, <= 4
-    const int64_t rb = (int64_t)blockIdx.x * kDeepRows;
-    const int64_t t_base = (int64_t)blockIdx.z * kDeepTokens;
-    const uint16_t* act = reinterpret_cast<const uint16_t*>(p.act);
-    const int bias = FMT == VLUT_DECODED ? kVlutDecodedBias : p.swar_bias;
-    const _Float16 f16_off = (_Float16)(1024 + bias);
-    const float f32_off = (float)bias;
-
-    // activations of the workgroup's K slice: chunk c = threadIdx.x + T i is
-    // (token c / CH, local k-block c % CH); outside the matrix or the slice it
-    // is zeroed through a mask (the load itself is unconditional, clamped)
-    uint4 av[AL];
-#pragma unroll
-    for (int i = 0; i < AL; ++i) {
-        const int c = threadIdx.x + T * i;
-        const int tok = c / CH, kbl = c % CH;
-        const int64_t kb = 4 * kq_begin + kbl;
-        const bool ok = t_base + tok < p.B && kb < kb_total && kq_begin + kbl / 4 < kq_end;
-        const uint4 v = *reinterpret_cast<const uint4*>(act + (ok ? (t_base + tok) * p.K + kb * 8 : 0));
-        uint32_t m;
-        __asm__("v_mov_b32 %0, %1" : "=v"(m) : "v"(ok ? ~0u : 0u));
-        av[i] = make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
-    }
-    // this wave's weight pairs: row tiles rt, k-quads kq_begin + wave * kqw + j
-    uint32_t w[kDeepRT][kDeepKqWave][WN];
-#pragma unroll
-    for (int rt = 0; rt < kDeepRT; ++rt) {
-        const int64_t r0 = rb + 16 * rt, row = r0 + (lane & 15);
-        const bool rows_ok = (FMT == VLUT_TILED || FMT == VLUT_DECODED) ? r0 < p.rows : row < p.rows;
-#pragma unroll
-        for (int j = 0; j < kDeepKqWave; ++j) {
-            const int64_t kq = kq_begin + (int64_t)wave * kqw + j;
-            const int64_t kb = 4 * kq + g;
-            const bool ok = rows_ok && j < kqw && kq < kq_end && kb < kb_total;
-            load_pair<Q, M, WN>(p, FMT, ok ? row : 0, ok ? kb : 0, kb_total, w[rt][j]);
-        }
-    }
-    if (FMT != VLUT_DECODED) {
-        for (int i = threadIdx.x; i < 512 + p.n_coarse; i += T) s_tab[i] = p.swar[i];
-    }
-#pragma unroll
-    for (int i = 0; i < AL; ++i) {
-        const int c = threadIdx.x + T * i;
-        *reinterpret_cast<uint4*>(&s_act[(c / CH) * kDeepStride + (c % CH) * 8]) = av[i];
-    }
-    __syncthreads();
-
-    float4_t acc[kDeepRT][4];
-#pragma unroll
-    for (int rt = 0; rt < kDeepRT; ++rt)
-#pragma unroll
-        for (int s = 0; s < 4; ++s) acc[rt][s] = (float4_t){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < kDeepKqWave; ++j) {
-        const int kql = wave * kqw + j;
-        if (j >= kqw || kq_begin + kql >= kq_end) break;   // wave-uniform
-        uint4 a[4];
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-            a[s] = *reinterpret_cast<const uint4*>(&s_act[(16 * s + (lane & 15)) * kDeepStride + kql * 32 + 8 * g]);
-#pragma unroll
-        for (int rt = 0; rt < kDeepRT; ++rt) {
-            uint4 bw;
-            if constexpr (FMT == VLUT_DECODED)
-                bw = bytes_to_operand<BF16>(w[rt][j][0], w[rt][j][1 % WN], f16_off, f32_off);
-            else
-                bw = decode_pair_swar<Q, M, BF16>(s_tab, w[rt][j], f16_off, f32_off);
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                if (BF16)
-                    acc[rt][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        __builtin_bit_cast(bf16x8_t, a[s]), __builtin_bit_cast(bf16x8_t, bw), acc[rt][s], 0, 0, 0);
-                else
-                    acc[rt][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                        __builtin_bit_cast(half8_t, a[s]), __builtin_bit_cast(half8_t, bw), acc[rt][s], 0, 0, 0);
-            }
-        }
-    }
-
-    // the 8 waves' tiles summed in wave order through LDS (the activation
-    // buffer, no longer read), one 16-byte accumulator per (row tile, token
-    // tile) and lane: element i of acc[rt][s] in lane l is
-    // D[token 16 s + 4 (l / 16) + i][row 16 rt + l % 16]
-    __syncthreads();
-    float4* red = reinterpret_cast<float4*>(s_act);
-#pragma unroll
-    for (int rt = 0; rt < kDeepRT; ++rt)
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-            red[(wave * 16 + rt * 4 + s) * 64 + lane] =
-                make_float4(acc[rt][s][0], acc[rt][s][1], acc[rt][s][2], acc[rt][s][3]);
-    __syncthreads();
-    for (int e = threadIdx.x; e < 16 * 64; e += T) {
-        const int v4 = e >> 6, ln = e & 63;
-        float sum[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int wv = 0; wv < kDeepNW; ++wv) {
-            const float4 t = red[(wv * 16 + v4) * 64 + ln];
-            sum[0] += t.x;
-            sum[1] += t.y;
-            sum[2] += t.z;
-            sum[3] += t.w;
-        }
-        const int rt = v4 >> 2, s = v4 & 3;
-        const int64_t o = rb + 16 * rt + (ln & 15);
-        if (o >= p.rows) continue;
-        const float sc = p.scale ? (p.scale_mode == 0 ? p.scale[o] : 1.f / p.scale[o]) : 1.f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int64_t tok = t_base + 16 * s + 4 * (ln >> 4) + i;
-            if (tok >= p.B) continue;
-            if (gridDim.y == 1)
-                p.out[tok * p.rows + o] = vlut_epilogue(sum[i] * 0.5f * sc, o, p.bias, p.lsq_alpha, p.lsq_qmax);
-            else
-                p.partial[((int64_t)blockIdx.y * p.B + tok) * p.rows + o] = sum[i];
         }
     }
 }
@@ -1311,117 +757,6 @@ hipError_t vlut_prepare(const uint16_t* words, int64_t rows, int64_t kb, int M, 
     return hipGetLastError();
 }
 
-namespace {
-
-template <int Q, int M, bool BF16, int NTILE>
-void launch_rows_fmt(const VlutMatmulArgs& p, int splits, hipStream_t s)
-{
-    dim3 grid((unsigned)((p.rows + 15) / 16), (unsigned)splits, (unsigned)((p.B + 16 * NTILE - 1) / (16 * NTILE)));
-    switch (p.prepared) {
-    case VLUT_RAW: hipLaunchKernelGGL((vlut_rows_kernel<Q, M, BF16, NTILE, VLUT_RAW>), grid, dim3(kRowsWaves * 64), 0, s, p); break;
-    case VLUT_PREPARED: hipLaunchKernelGGL((vlut_rows_kernel<Q, M, BF16, NTILE, VLUT_PREPARED>), grid, dim3(kRowsWaves * 64), 0, s, p); break;
-    case VLUT_DECODED: hipLaunchKernelGGL((vlut_rows_kernel<Q, M, BF16, NTILE, VLUT_DECODED>), grid, dim3(kRowsWaves * 64), 0, s, p); break;
-    default: hipLaunchKernelGGL((vlut_rows_kernel<Q, M, BF16, NTILE, VLUT_TILED>), grid, dim3(kRowsWaves * 64), 0, s, p); break;
-    }
-}
-
-template <int Q, int M>
-hipError_t launch_rows(const VlutMatmulArgs& p, int splits, hipStream_t s)
-{
-    if constexpr (Q == 2 || M <= 2) {
-        const bool bf = p.act_dtype == DT_BF16;
-        if (p.B <= 16) {
-            if (bf) launch_rows_fmt<Q, M, true, 1>(p, splits, s); else launch_rows_fmt<Q, M, false, 1>(p, splits, s);
-        } else if (p.B <= 32) {
-            if (bf) launch_rows_fmt<Q, M, true, 2>(p, splits, s); else launch_rows_fmt<Q, M, false, 2>(p, splits, s);
-        } else {
-            if (bf) launch_rows_fmt<Q, M, true, 4>(p, splits, s); else launch_rows_fmt<Q, M, false, 4>(p, splits, s);
-        }
-        return hipGetLastError();
-    }
-    return hipErrorInvalidValue;
-}
-
-template <int Q, int M, bool BF16>
-void launch_wide_fmt(const VlutMatmulArgs& p, int splits, hipStream_t s)
-{
-    dim3 grid((unsigned)((p.rows + kWideRows - 1) / kWideRows), (unsigned)splits,
-              (unsigned)((p.B + kWideTokens - 1) / kWideTokens));
-#define COSET_WIDE(F) \
-    hipLaunchKernelGGL((vlut_wide_kernel<Q, M, BF16, F, kWideRT, kWideNW>), grid, dim3(kWideNW * 64), 0, s, p)
-    switch (p.prepared) {
-    case VLUT_RAW: COSET_WIDE(VLUT_RAW); break;
-    case VLUT_PREPARED: COSET_WIDE(VLUT_PREPARED); break;
-    case VLUT_DECODED: COSET_WIDE(VLUT_DECODED); break;
-    default: COSET_WIDE(VLUT_TILED); break;
-    }
-#undef COSET_WIDE
-}
-
-template <int Q>
-hipError_t dispatch_wide(const VlutMatmulArgs& p, int splits, hipStream_t s)
-{
-    const bool bf = p.act_dtype == DT_BF16;
-    switch (p.M) {
-#define COSET_M(MM) \
-    case MM: \
-        if constexpr (Q == 2 || MM <= 2) { \
-            if (bf) launch_wide_fmt<Q, MM, true>(p, splits, s); else launch_wide_fmt<Q, MM, false>(p, splits, s); \
-            return hipGetLastError(); \
-        } \
-        return hipErrorInvalidValue;
-    COSET_M(1) COSET_M(2) COSET_M(3) COSET_M(4)
-#undef COSET_M
-    default: return hipErrorInvalidValue;
-    }
-}
-
-template <int Q, int M, bool BF16>
-void launch_deep_fmt(const VlutMatmulArgs& p, int splits, hipStream_t s)
-{
-    dim3 grid((unsigned)((p.rows + kDeepRows - 1) / kDeepRows), (unsigned)splits,
-              (unsigned)((p.B + kDeepTokens - 1) / kDeepTokens));
-#define COSET_DEEP(F) hipLaunchKernelGGL((vlut_deep_kernel<Q, M, BF16, F>), grid, dim3(kDeepNW * 64), 0, s, p)
-    switch (p.prepared) {
-    case VLUT_RAW: COSET_DEEP(VLUT_RAW); break;
-    case VLUT_PREPARED: COSET_DEEP(VLUT_PREPARED); break;
-    case VLUT_DECODED: COSET_DEEP(VLUT_DECODED); break;
-    default: COSET_DEEP(VLUT_TILED); break;
-    }
-#undef COSET_DEEP
-}
-
-template <int Q>
-hipError_t dispatch_deep(const VlutMatmulArgs& p, int splits, hipStream_t s)
-{
-    const bool bf = p.act_dtype == DT_BF16;
-    switch (p.M) {
-#define COSET_M(MM) \
-    case MM: \
-        if constexpr (Q == 2 || MM <= 2) { \
-            if (bf) launch_deep_fmt<Q, MM, true>(p, splits, s); else launch_deep_fmt<Q, MM, false>(p, splits, s); \
-            return hipGetLastError(); \
-        } \
-        return hipErrorInvalidValue;
-    COSET_M(1) COSET_M(2) COSET_M(3) COSET_M(4)
-#undef COSET_M
-    default: return hipErrorInvalidValue;
-    }
-}
-
-template <int Q>
-hipError_t dispatch_rows(const VlutMatmulArgs& p, int splits, hipStream_t s)
-{
-    switch (p.M) {
-    case 1: return launch_rows<Q, 1>(p, splits, s);
-    case 2: return launch_rows<Q, 2>(p, splits, s);
-    case 3: return launch_rows<Q, 3>(p, splits, s);
-    case 4: return launch_rows<Q, 4>(p, splits, s);
-    default: return hipErrorInvalidValue;
-    }
-}
-
-}  // namespace
 
 hipError_t vlut_matmul(VlutMatmulArgs p, const VlutPlan& plan, hipStream_t s)
 {
@@ -1449,9 +784,9 @@ hipError_t vlut_matmul(VlutMatmulArgs p, const VlutPlan& plan, hipStream_t s)
         if (plan.kernel == VK_MFMA_DEEP) {
             const int64_t kq_total = (p.K / 8 + 3) / 4;
             if ((kq_total + splits - 1) / splits > kDeepKqWg) return hipErrorInvalidValue;
-            e = p.q == 4 ? dispatch_deep<4>(p, splits, s) : dispatch_deep<2>(p, splits, s);
+            e = vlut_launch_deep(p, splits, s);
         } else {
-            e = p.q == 4 ? dispatch_wide<4>(p, splits, s) : dispatch_wide<2>(p, splits, s);
+            e = vlut_launch_wide(p, splits, s);
         }
         if (e != hipSuccess || splits == 1) return e;
         const int64_t nw = p.B * p.rows;
@@ -1468,7 +803,7 @@ hipError_t vlut_matmul(VlutMatmulArgs p, const VlutPlan& plan, hipStream_t s)
     }
     if (plan.kernel == VK_MFMA_ROWS) {
         if (!p.swar_ok) return hipErrorInvalidValue;
-        e = p.q == 4 ? dispatch_rows<4>(p, splits, s) : dispatch_rows<2>(p, splits, s);
+        e = vlut_launch_rows(p, splits, s);
         if (e != hipSuccess || splits == 1) return e;
     } else {
         const int method = plan.kernel == VK_LDS ? VLUT_METHOD_LDS : VLUT_METHOD_MFMA;

@@ -1,0 +1,260 @@
+// vlut_rows.hip -- the matrix-core rows kernel of the vLUT matmul (batches
+// up to 32 tokens); the shared decode helpers are in vlut_mfma.hpp.
+#include "vlut_mfma.hpp"
+
+namespace coset {
+
+// ---------------------------------------------------------------- MFMA rows kernel
+// Tile: 16 output rows per workgroup, K split over its 8 waves (and over
+// grid.y when the row tiles alone cannot fill the GPU), up to 16 * NTILE
+// tokens (grid.z beyond).  In each step lane l owns row l % 16 and k-block
+// 4 kq + l / 16: it decodes that pair's 2 x_hat through the byte tables
+// straight into its 8-half B operand of one 16x16x32 MFMA, and takes
+// act[token][8 kb, 8 kb + 8) as its A operand.  Any assignment of K
+// positions to (lane group, operand slot) works as long as A and B use the
+// same one, which holds since both come from the same kb.  In the tiled
+// format a step's 64 word groups are one contiguous run.  The waves' sums
+// meet in LDS; with one K split the workgroup writes the output.
+// Activations: with TB = 0 every lane loads its A operand from global memory
+// (16 tokens x 64 bytes per wave load).  With TB > 0 (one 16-token tile, at
+// most TB tokens) each wave copies its chunk's K slice of every token into
+// LDS rows of its own with whole-row loads (two tokens x 512 bytes per wave
+// load) and reads its A operands from there: fewer, coalesced loads, and no
+// barrier, since no other wave touches those rows and a wave's LDS
+// operations complete in order.  A chunk's activation loads are issued ahead
+// of its weight loads.  The staged kernels take a wave's K range of at most
+// two chunks (kRowsStageKq k-quads) in one piece.
+constexpr int kRowsStageKq = 16;                             // k-quads of a wave's staged slice (two chunks)
+constexpr int kRowsStageRow = 4 * kRowsStageKq * 16 + 16;    // bytes per staged token row (64 k-blocks, 16-byte pad)
+
+template <int Q, int M, bool BF16, int NTILE, int FMT, int TB>
+__global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulArgs p)
+{
+    constexpr int CH = 8 / NTILE;  // steps per prefetch chunk
+    static_assert(TB == 0 || (NTILE == 1 && TB <= 16), "staged activations: one 16-token tile");
+    static_assert(TB == 0 || 2 * CH == kRowsStageKq, "a staged wave range is two chunks");
+    __shared__ uint64_t s_tab[FMT == VLUT_DECODED ? 1 : kSwarSlots];
+    __shared__ float s_red[kRowsWaves][NTILE * 4][64];
+    __shared__ __align__(16) unsigned char s_stage[TB == 0 ? 16 : kRowsWaves * TB * kRowsStageRow];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4;
+    const int64_t kb_total = p.K / 8;
+    const int64_t kq_total = (kb_total + 3) / 4;
+    const int64_t kq_wg = (kq_total + gridDim.y - 1) / gridDim.y;
+    const int64_t kq_begin = blockIdx.y * kq_wg;
+    const int64_t kq_end = min(kq_total, kq_begin + kq_wg);
+    const int64_t kq_wave = (kq_end - kq_begin + kRowsWaves - 1) / kRowsWaves;
+    const int64_t w0 = kq_begin + wave * kq_wave;
+    const int64_t w1 = min(kq_end, w0 + kq_wave);
+    const int64_t r0 = (int64_t)blockIdx.x * 16;
+    const int64_t row = r0 + (lane & 15);
+    const int64_t t_base = (int64_t)blockIdx.z * 16 * NTILE;
+    const uint16_t* act = reinterpret_cast<const uint16_t*>(p.act);
+    const int bias = FMT == VLUT_DECODED ? kVlutDecodedBias : p.swar_bias;
+    const _Float16 f16_off = (_Float16)(1024 + bias);
+    const float f32_off = (float)bias;
+    constexpr int WN = FMT == VLUT_DECODED ? 2 : M;  // uint32 per pair
+
+    struct Chunk {
+        uint32_t w[CH][WN];
+        uint4 a[TB == 0 ? CH : 1][NTILE];  // A operands (TB = 0), masked in run
+    };
+    // Every load is unconditional, with a clamped address where it lies
+    // outside the matrix, the wave's K range or the batch, and its value is
+    // masked where it is used: the number of loads issued after a chunk's is
+    // then the same on every path, so the wait for that chunk leaves the later
+    // loads in flight.  (Weights of an out-of-range k-block meet zero
+    // activations, and rows past the matrix are never written.)
+    auto load = [&](int64_t c0, Chunk& ck) {
+#pragma unroll
+        for (int st = 0; st < CH; ++st) {
+            const int64_t kq = c0 + st;
+            const int64_t kb = 4 * kq + g;
+            const bool ok = kq < w1 && kb < kb_total && (FMT == VLUT_TILED || FMT == VLUT_DECODED || row < p.rows);
+            load_pair<Q, M, WN>(p, FMT, ok ? row : r0, ok ? kb : 0, kb_total, ck.w[st]);
+            if constexpr (TB == 0) {
+#pragma unroll
+                for (int s = 0; s < NTILE; ++s) {
+                    const int64_t tok = t_base + 16 * s + (lane & 15);
+                    const bool oka = kq < w1 && kb < kb_total && tok < p.B;
+                    ck.a[st][s] = *reinterpret_cast<const uint4*>(act + (oka ? tok * p.K + kb * 8 : 0));
+                }
+            }
+        }
+    };
+    float4_t acc[NTILE];
+#pragma unroll
+    for (int s = 0; s < NTILE; ++s) acc[s] = (float4_t){0.f, 0.f, 0.f, 0.f};
+    auto run = [&](const Chunk& ck, int64_t c0) {
+#pragma unroll
+        for (int st = 0; st < CH; ++st) {
+            uint4 a[NTILE];
+            const int64_t kq = c0 + st, kb = 4 * kq + g;
+            if constexpr (TB > 0) {
+                // token lane % 16 (rows at or past the batch were not written: masked),
+                // local k-block 4 (kq - w0) + lane / 16 (zeros past the wave's range)
+                const int tok = lane & 15;
+                const int tr = tok < TB ? tok : TB - 1;
+                const uint4 v = *reinterpret_cast<const uint4*>(
+                    &s_stage[(wave * TB + tr) * kRowsStageRow + (4 * (int)(kq - w0) + g) * 16]);
+                a[0] = t_base + tok < p.B ? v : make_uint4(0u, 0u, 0u, 0u);
+            } else {
+#pragma unroll
+                for (int s = 0; s < NTILE; ++s) {
+                    const bool oka = kq < w1 && kb < kb_total && t_base + 16 * s + (lane & 15) < p.B;
+                    a[s] = oka ? ck.a[st][s] : make_uint4(0u, 0u, 0u, 0u);
+                }
+            }
+            uint4 bw;
+            if constexpr (FMT == VLUT_DECODED)
+                bw = bytes_to_operand<BF16>(ck.w[st][0], ck.w[st][1 % WN], f16_off, f32_off);
+            else
+                bw = decode_pair_swar<Q, M, BF16>(s_tab, ck.w[st], f16_off, f32_off);
+#pragma unroll
+            for (int s = 0; s < NTILE; ++s) {
+                if (BF16)
+                    acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a[s]),
+                                                                    __builtin_bit_cast(bf16x8_t, bw), acc[s], 0, 0, 0);
+                else
+                    acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a[s]),
+                                                                   __builtin_bit_cast(half8_t, bw), acc[s], 0, 0, 0);
+            }
+        }
+    };
+
+    Chunk c_a, c_b;
+    if constexpr (TB > 0) {
+        // the wave's K slice (at most two chunks, checked by the host) of every
+        // token, 16 bytes a lane and one load per token, then both chunks'
+        // weights; the activations go to the wave's LDS rows as they arrive
+        uint4 av[TB];
+#pragma unroll
+        for (int t = 0; t < TB; ++t) {
+            const int64_t kb = 4 * w0 + lane;
+            const bool ok = t_base + t < p.B && kb < 4 * w1 && kb < kb_total;
+            av[t] = *reinterpret_cast<const uint4*>(act + (ok ? (t_base + t) * p.K + kb * 8 : 0));
+        }
+        load(w0, c_a);
+        load(w0 + CH, c_b);
+#pragma unroll
+        for (int t = 0; t < TB; ++t) {
+            const int64_t kb = 4 * w0 + lane;
+            const bool ok = t_base + t < p.B && kb < 4 * w1 && kb < kb_total;
+            uint32_t m;
+            __asm__("v_mov_b32 %0, %1" : "=v"(m) : "v"(ok ? ~0u : 0u));
+            *reinterpret_cast<uint4*>(&s_stage[(wave * TB + t) * kRowsStageRow + lane * 16]) =
+                make_uint4(av[t].x & m, av[t].y & m, av[t].z & m, av[t].w & m);
+        }
+        if constexpr (FMT != VLUT_DECODED) {
+            for (int i = threadIdx.x; i < 512 + p.n_coarse; i += blockDim.x) s_tab[i] = p.swar[i];
+            __syncthreads();
+        }
+        run(c_a, w0);
+        run(c_b, w0 + CH);
+    } else {
+        // ping-pong over chunks; the chunk after the wave's last is loaded too
+        // (clamped and masked, never used), which keeps every load unconditional
+        int64_t c0 = w0;
+        load(c0, c_a);
+        // the tables are staged while the first chunk's loads are in flight
+        if constexpr (FMT != VLUT_DECODED) {
+            for (int i = threadIdx.x; i < 512 + p.n_coarse; i += blockDim.x) s_tab[i] = p.swar[i];
+            __syncthreads();
+        }
+        for (; c0 < w1; c0 += 2 * CH) {
+            const int64_t c1 = c0 + CH;
+            load(c1, c_b);
+            run(c_a, c0);
+            if (c1 >= w1) break;
+            load(c1 + CH, c_a);
+            run(c_b, c1);
+        }
+    }
+
+    // D[token = 16 s + 4 (lane / 16) + i][row = lane % 16]; sum the waves
+#pragma unroll
+    for (int s = 0; s < NTILE; ++s)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s_red[wave][s * 4 + i][lane] = acc[s][i];
+    __syncthreads();
+    for (int e = threadIdx.x; e < NTILE * 256; e += blockDim.x) {
+        const int si = e >> 6, ln = e & 63;
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < kRowsWaves; ++w) v += s_red[w][si][ln];
+        const int64_t tok = t_base + 16 * (si >> 2) + 4 * (ln >> 4) + (si & 3);
+        const int64_t o = r0 + (ln & 15);
+        if (tok >= p.B || o >= p.rows) continue;
+        if (gridDim.y == 1) {
+            float sc = p.scale ? (p.scale_mode == 0 ? p.scale[o] : 1.f / p.scale[o]) : 1.f;
+            p.out[tok * p.rows + o] = vlut_epilogue(v * 0.5f * sc, o, p.bias, p.lsq_alpha, p.lsq_qmax);
+        } else {
+            p.partial[(tok * p.rows + o) * gridDim.y + blockIdx.y] = v;
+        }
+    }
+}
+
+namespace {
+
+
+template <int Q, int M, bool BF16, int NTILE, int TB>
+void launch_rows_fmt(const VlutMatmulArgs& p, int splits, hipStream_t s)
+{
+    dim3 grid((unsigned)((p.rows + 15) / 16), (unsigned)splits, (unsigned)((p.B + 16 * NTILE - 1) / (16 * NTILE)));
+#define COSET_ROWS(F) hipLaunchKernelGGL((vlut_rows_kernel<Q, M, BF16, NTILE, F, TB>), grid, dim3(kRowsWaves * 64), 0, s, p)
+    switch (p.prepared) {
+    case VLUT_RAW: COSET_ROWS(VLUT_RAW); break;
+    case VLUT_PREPARED: COSET_ROWS(VLUT_PREPARED); break;
+    case VLUT_DECODED: COSET_ROWS(VLUT_DECODED); break;
+    default: COSET_ROWS(VLUT_TILED); break;
+    }
+#undef COSET_ROWS
+}
+
+template <int Q, int M>
+hipError_t launch_rows(const VlutMatmulArgs& p, int splits, hipStream_t s)
+{
+    if constexpr (Q == 2 || M <= 2) {
+        const bool bf = p.act_dtype == DT_BF16;
+        // the staged kernels take a wave's whole K range (at most kRowsStageKq k-quads) at once
+        const int64_t kq_total = (p.K / 8 + 3) / 4;
+        const int64_t kq_wg = (kq_total + splits - 1) / splits;
+        const bool staged = (kq_wg + kRowsWaves - 1) / kRowsWaves <= kRowsStageKq;
+        if (staged && p.B == 1) {  // staged activations, one token
+            if (bf) launch_rows_fmt<Q, M, true, 1, 1>(p, splits, s); else launch_rows_fmt<Q, M, false, 1, 1>(p, splits, s);
+        } else if (staged && p.B <= 8) {  // staged activations, up to 8 tokens
+            if (bf) launch_rows_fmt<Q, M, true, 1, 8>(p, splits, s); else launch_rows_fmt<Q, M, false, 1, 8>(p, splits, s);
+        } else if (staged && p.B <= 16) {  // staged activations, up to 16 tokens
+            if (bf) launch_rows_fmt<Q, M, true, 1, 16>(p, splits, s); else launch_rows_fmt<Q, M, false, 1, 16>(p, splits, s);
+        } else if (p.B <= 16) {
+            if (bf) launch_rows_fmt<Q, M, true, 1, 0>(p, splits, s); else launch_rows_fmt<Q, M, false, 1, 0>(p, splits, s);
+        } else if (p.B <= 32) {
+            if (bf) launch_rows_fmt<Q, M, true, 2, 0>(p, splits, s); else launch_rows_fmt<Q, M, false, 2, 0>(p, splits, s);
+        } else {
+            if (bf) launch_rows_fmt<Q, M, true, 4, 0>(p, splits, s); else launch_rows_fmt<Q, M, false, 4, 0>(p, splits, s);
+        }
+        return hipGetLastError();
+    }
+    return hipErrorInvalidValue;
+}
+
+template <int Q>
+hipError_t dispatch_rows(const VlutMatmulArgs& p, int splits, hipStream_t s)
+{
+    switch (p.M) {
+    case 1: return launch_rows<Q, 1>(p, splits, s);
+    case 2: return launch_rows<Q, 2>(p, splits, s);
+    case 3: return launch_rows<Q, 3>(p, splits, s);
+    case 4: return launch_rows<Q, 4>(p, splits, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+hipError_t vlut_launch_rows(const VlutMatmulArgs& p, int splits, hipStream_t s)
+{
+    return p.q == 4 ? dispatch_rows<4>(p, splits, s) : dispatch_rows<2>(p, splits, s);
+}
+
+}  // namespace coset

@@ -1,0 +1,393 @@
+// vlut_wide.hip -- the matrix-core wide and deep kernels of the vLUT matmul
+// (batches above 32 tokens); the shared decode helpers are in vlut_mfma.hpp.
+#include "vlut_mfma.hpp"
+
+namespace coset {
+
+// ---------------------------------------------------------------- MFMA wide kernel
+// Tile: 128 output rows (8 row tiles of 16, one per wave) x 64 tokens per
+// workgroup, K split over grid.y (partials [split][B][rows]), token tiles of
+// 64 over grid.z.  The activations of a stage (64 tokens x 128 K) are loaded
+// once per workgroup, two 16-byte loads per thread, and shared by the 8
+// waves through LDS (double-buffered, one LDS-only barrier per stage); each
+// wave decodes its own row tile's weight pairs into the B operand as the rows
+// kernel does and runs 4 MFMAs (one per 16-token tile) per k-quad.  Every
+// global load is unconditional (clamped; what lies outside the matrix or the
+// workgroup's K range has zero activations), so the waits before a stage
+// leave the next stage's loads in flight.
+
+template <int Q, int M, bool BF16, int FMT, int RT, int NW>
+__global__ void __launch_bounds__(NW * 64) vlut_wide_kernel(VlutMatmulArgs p)
+{
+    constexpr int WN = FMT == VLUT_DECODED ? 2 : M;  // uint32 per pair
+    constexpr int T = NW * 64;                       // threads
+    constexpr int P = 4 * kWideStageKq;              // 16-byte k-block chunks per token and stage
+    constexpr int AL = kWideTokens * P / T;          // activation loads per thread and stage
+    static_assert(kWideTokens * P % T == 0, "whole activation loads per thread");
+    __shared__ uint64_t s_tab[FMT == VLUT_DECODED ? 1 : kSwarSlots];
+    __shared__ __align__(16) uint16_t s_act[2][kWideTokens][kWideActStride];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4;
+    const int64_t kb_total = p.K / 8;
+    const int64_t kq_total = (kb_total + 3) / 4;
+    const int64_t kq_wg = (kq_total + gridDim.y - 1) / gridDim.y;
+    const int64_t kq_begin = blockIdx.y * kq_wg;
+    const int64_t kq_end = min(kq_total, kq_begin + kq_wg);
+    const int64_t rt0 = ((int64_t)blockIdx.x * NW + wave) * RT;  // first row tile of this wave
+    const int64_t t_base = (int64_t)blockIdx.z * kWideTokens;
+    const uint16_t* act = reinterpret_cast<const uint16_t*>(p.act);
+    const int bias = FMT == VLUT_DECODED ? kVlutDecodedBias : p.swar_bias;
+    const _Float16 f16_off = (_Float16)(1024 + bias);
+    const float f32_off = (float)bias;
+
+    // this thread's share of a stage's activations: chunks threadIdx.x + T i
+    // (token c / P, k-block c % P of the stage, 16 bytes each)
+    struct Act {
+        uint4 v[AL];
+    };
+    const int a_part = threadIdx.x % P;
+    auto load_act = [&](int64_t kq0, Act& ac) {
+#pragma unroll
+        for (int i = 0; i < AL; ++i) {
+            const int tok = (threadIdx.x + T * i) / P;
+            const int64_t kb = 4 * kq0 + a_part;
+            const bool ok = t_base + tok < p.B && kb < kb_total && kq0 + a_part / 4 < kq_end;
+            const uint4 v =
+                *reinterpret_cast<const uint4*>(act + (ok ? (t_base + tok) * p.K + kb * 8 : 0));
+            // zeroed through a mask the compiler cannot trace back to ok: a
+            // select would let it branch around the load, and the waits after
+            // a conditional load drain the queue
+            uint32_t m;
+            __asm__("v_mov_b32 %0, %1" : "=v"(m) : "v"(ok ? ~0u : 0u));
+            ac.v[i] = make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
+        }
+    };
+    struct W {
+        uint32_t w[RT][kWideStageKq][WN];
+    };
+    auto load_w = [&](int64_t kq0, W& ws) {
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+            const int64_t r0 = (rt0 + t) * 16, row = r0 + (lane & 15);
+            // rows that hold weights (whole tiles in the tiled formats)
+            const bool rows_ok = (FMT == VLUT_TILED || FMT == VLUT_DECODED) ? r0 < p.rows : row < p.rows;
+#pragma unroll
+            for (int j = 0; j < kWideStageKq; ++j) {
+                const int64_t kb = 4 * (kq0 + j) + g;
+                const bool ok = rows_ok && kb < kb_total;
+                // outside the matrix: pair (0, 0) instead, under zero
+                // activations or an output that is not stored
+                load_pair<Q, M, WN>(p, FMT, ok ? row : 0, ok ? kb : 0, kb_total, ws.w[t][j]);
+            }
+        }
+    };
+    float4_t acc[RT][4];
+#pragma unroll
+    for (int t = 0; t < RT; ++t)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc[t][s] = (float4_t){0.f, 0.f, 0.f, 0.f};
+
+    if (FMT != VLUT_DECODED) {
+        for (int i = threadIdx.x; i < 512 + p.n_coarse; i += blockDim.x) s_tab[i] = p.swar[i];
+    }
+    const int stages = (int)((kq_end - kq_begin + kWideStageKq - 1) / kWideStageKq);
+    W w_now, w_next;
+    Act a_next;
+    load_act(kq_begin, a_next);
+    load_w(kq_begin, w_now);
+    for (int st = 0; st < stages; ++st) {
+        const int64_t kq0 = kq_begin + (int64_t)st * kWideStageKq;
+        const int buf = st & 1;
+#pragma unroll
+        for (int i = 0; i < AL; ++i)
+            *reinterpret_cast<uint4*>(&s_act[buf][(threadIdx.x + T * i) / P][a_part * 8]) = a_next.v[i];
+        lds_barrier();
+        // the next stage's loads go out before this stage's products
+        const int64_t kq1 = st + 1 < stages ? kq0 + kWideStageKq : kq0;
+        load_act(kq1, a_next);
+        load_w(kq1, w_next);
+        __asm__ volatile("" ::: "memory");  // the loads stay ahead of the products
+        uint4 av_all[kWideStageKq][4];
+#pragma unroll
+        for (int j = 0; j < kWideStageKq; ++j)
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+                av_all[j][s] = *reinterpret_cast<const uint4*>(&s_act[buf][16 * s + (lane & 15)][(4 * j + g) * 8]);
+#pragma unroll
+        for (int j = 0; j < kWideStageKq; ++j) {
+#pragma unroll
+            for (int t = 0; t < RT; ++t) {
+                uint4 bw;
+                if constexpr (FMT == VLUT_DECODED)
+                    bw = bytes_to_operand<BF16>(w_now.w[t][j][0], w_now.w[t][j][1 % WN], f16_off, f32_off);
+                else
+                    bw = decode_pair_swar<Q, M, BF16>(s_tab, w_now.w[t][j], f16_off, f32_off);
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const uint4 av = av_all[j][s];
+                    if (BF16)
+                        acc[t][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            __builtin_bit_cast(bf16x8_t, av), __builtin_bit_cast(bf16x8_t, bw), acc[t][s], 0, 0, 0);
+                    else
+                        acc[t][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            __builtin_bit_cast(half8_t, av), __builtin_bit_cast(half8_t, bw), acc[t][s], 0, 0, 0);
+                }
+            }
+        }
+        w_now = w_next;
+    }
+
+    // D[token = 16 s + 4 (lane / 16) + i][row = lane % 16]
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+        const int64_t o = (rt0 + t) * 16 + (lane & 15);
+        if (o >= p.rows) continue;
+        const float sc = p.scale ? (p.scale_mode == 0 ? p.scale[o] : 1.f / p.scale[o]) : 1.f;
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int64_t tok = t_base + 16 * s + 4 * g + i;
+                if (tok >= p.B) continue;
+                if (gridDim.y == 1)
+                    p.out[tok * p.rows + o] =
+                        vlut_epilogue(acc[t][s][i] * 0.5f * sc, o, p.bias, p.lsq_alpha, p.lsq_qmax);
+                else
+                    p.partial[((int64_t)blockIdx.y * p.B + tok) * p.rows + o] = acc[t][s][i];
+            }
+    }
+}
+
+// ---------------------------------------------------------------- MFMA deep kernel
+// Tile: 64 output rows x 64 tokens per workgroup of 8 waves; K split over
+// grid.y (partials [split][B][rows]) and, inside the workgroup, over the 8
+// waves.  Each wave owns all 4 row tiles of 16 rows (4 weight operands per
+// k-quad) and all 4 token tiles, so every activation operand read from LDS
+// feeds 4 MFMAs (the wide kernel's one-row-tile waves re-read all 64 tokens'
+// activations per 16 rows).  The workgroup issues every load of its K slice
+// up front -- activations (64 tokens x up to 1024 K, 128 KiB) into LDS, the
+// waves' weight pairs into registers -- then runs the products; the 8 waves'
+// partial tiles are summed in LDS in wave order, so a split writes one
+// partial (or, unsplit, the output) and the sums are deterministic.
+
+template <int Q, int M, bool BF16, int FMT>
+__global__ void __launch_bounds__(kDeepNW * 64) vlut_deep_kernel(VlutMatmulArgs p)
+{
+    constexpr int WN = FMT == VLUT_DECODED ? 2 : M;  // uint32 per pair
+    constexpr int T = kDeepNW * 64;
+    constexpr int CH = 4 * kDeepKqWg;                // 16-byte activation chunks per token row
+    constexpr int AL = kDeepTokens * CH / T;         // activation loads per thread
+    static_assert(kDeepTokens * CH % T == 0, "whole activation loads per thread");
+    static_assert(kDeepNW * kDeepRows * kDeepTokens * 4 <= kDeepTokens * kDeepStride * 2,
+                  "the cross-wave sum fits in the activation buffer");
+    static_assert(kDeepStride * 2 % 16 == 0, "16-byte aligned token rows");
+    __shared__ __align__(16) uint16_t s_act[kDeepTokens * kDeepStride];
+    __shared__ uint64_t s_tab[FMT == VLUT_DECODED ? 1 : kSwarSlots];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4;
+    const int64_t kb_total = p.K / 8;
+    const int64_t kq_total = (kb_total + 3) / 4;
+    const int64_t kq_wg = (kq_total + gridDim.y - 1) / gridDim.y;   // <= kDeepKqWg (the plan's splits)
+    const int64_t kq_begin = blockIdx.y * kq_wg;
+    const int64_t kq_end = min(kq_total, kq_begin + kq_wg);
+    const int kqw = (int)((kq_wg + kDeepNW - 1) / kDeepNW);         // k-quads per wave, <= 4
+    const int64_t rb = (int64_t)blockIdx.x * kDeepRows;
+    const int64_t t_base = (int64_t)blockIdx.z * kDeepTokens;
+    const uint16_t* act = reinterpret_cast<const uint16_t*>(p.act);
+    const int bias = FMT == VLUT_DECODED ? kVlutDecodedBias : p.swar_bias;
+    const _Float16 f16_off = (_Float16)(1024 + bias);
+    const float f32_off = (float)bias;
+
+    // activations of the workgroup's K slice: chunk c = threadIdx.x + T i is
+    // (token c / CH, local k-block c % CH); outside the matrix or the slice it
+    // is zeroed through a mask (the load itself is unconditional, clamped)
+    uint4 av[AL];
+#pragma unroll
+    for (int i = 0; i < AL; ++i) {
+        const int c = threadIdx.x + T * i;
+        const int tok = c / CH, kbl = c % CH;
+        const int64_t kb = 4 * kq_begin + kbl;
+        const bool ok = t_base + tok < p.B && kb < kb_total && kq_begin + kbl / 4 < kq_end;
+        const uint4 v = *reinterpret_cast<const uint4*>(act + (ok ? (t_base + tok) * p.K + kb * 8 : 0));
+        uint32_t m;
+        __asm__("v_mov_b32 %0, %1" : "=v"(m) : "v"(ok ? ~0u : 0u));
+        av[i] = make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
+    }
+    // this wave's weight pairs: row tiles rt, k-quads kq_begin + wave * kqw + j
+    uint32_t w[kDeepRT][kDeepKqWave][WN];
+#pragma unroll
+    for (int rt = 0; rt < kDeepRT; ++rt) {
+        const int64_t r0 = rb + 16 * rt, row = r0 + (lane & 15);
+        const bool rows_ok = (FMT == VLUT_TILED || FMT == VLUT_DECODED) ? r0 < p.rows : row < p.rows;
+#pragma unroll
+        for (int j = 0; j < kDeepKqWave; ++j) {
+            const int64_t kq = kq_begin + (int64_t)wave * kqw + j;
+            const int64_t kb = 4 * kq + g;
+            const bool ok = rows_ok && j < kqw && kq < kq_end && kb < kb_total;
+            load_pair<Q, M, WN>(p, FMT, ok ? row : 0, ok ? kb : 0, kb_total, w[rt][j]);
+        }
+    }
+    if (FMT != VLUT_DECODED) {
+        for (int i = threadIdx.x; i < 512 + p.n_coarse; i += T) s_tab[i] = p.swar[i];
+    }
+#pragma unroll
+    for (int i = 0; i < AL; ++i) {
+        const int c = threadIdx.x + T * i;
+        *reinterpret_cast<uint4*>(&s_act[(c / CH) * kDeepStride + (c % CH) * 8]) = av[i];
+    }
+    __syncthreads();
+
+    float4_t acc[kDeepRT][4];
+#pragma unroll
+    for (int rt = 0; rt < kDeepRT; ++rt)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc[rt][s] = (float4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < kDeepKqWave; ++j) {
+        const int kql = wave * kqw + j;
+        if (j >= kqw || kq_begin + kql >= kq_end) break;   // wave-uniform
+        uint4 a[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+            a[s] = *reinterpret_cast<const uint4*>(&s_act[(16 * s + (lane & 15)) * kDeepStride + kql * 32 + 8 * g]);
+#pragma unroll
+        for (int rt = 0; rt < kDeepRT; ++rt) {
+            uint4 bw;
+            if constexpr (FMT == VLUT_DECODED)
+                bw = bytes_to_operand<BF16>(w[rt][j][0], w[rt][j][1 % WN], f16_off, f32_off);
+            else
+                bw = decode_pair_swar<Q, M, BF16>(s_tab, w[rt][j], f16_off, f32_off);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                if (BF16)
+                    acc[rt][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        __builtin_bit_cast(bf16x8_t, a[s]), __builtin_bit_cast(bf16x8_t, bw), acc[rt][s], 0, 0, 0);
+                else
+                    acc[rt][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        __builtin_bit_cast(half8_t, a[s]), __builtin_bit_cast(half8_t, bw), acc[rt][s], 0, 0, 0);
+            }
+        }
+    }
+
+    // the 8 waves' tiles summed in wave order through LDS (the activation
+    // buffer, no longer read), one 16-byte accumulator per (row tile, token
+    // tile) and lane: element i of acc[rt][s] in lane l is
+    // D[token 16 s + 4 (l / 16) + i][row 16 rt + l % 16]
+    __syncthreads();
+    float4* red = reinterpret_cast<float4*>(s_act);
+#pragma unroll
+    for (int rt = 0; rt < kDeepRT; ++rt)
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+            red[(wave * 16 + rt * 4 + s) * 64 + lane] =
+                make_float4(acc[rt][s][0], acc[rt][s][1], acc[rt][s][2], acc[rt][s][3]);
+    __syncthreads();
+    for (int e = threadIdx.x; e < 16 * 64; e += T) {
+        const int v4 = e >> 6, ln = e & 63;
+        float sum[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int wv = 0; wv < kDeepNW; ++wv) {
+            const float4 t = red[(wv * 16 + v4) * 64 + ln];
+            sum[0] += t.x;
+            sum[1] += t.y;
+            sum[2] += t.z;
+            sum[3] += t.w;
+        }
+        const int rt = v4 >> 2, s = v4 & 3;
+        const int64_t o = rb + 16 * rt + (ln & 15);
+        if (o >= p.rows) continue;
+        const float sc = p.scale ? (p.scale_mode == 0 ? p.scale[o] : 1.f / p.scale[o]) : 1.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int64_t tok = t_base + 16 * s + 4 * (ln >> 4) + i;
+            if (tok >= p.B) continue;
+            if (gridDim.y == 1)
+                p.out[tok * p.rows + o] = vlut_epilogue(sum[i] * 0.5f * sc, o, p.bias, p.lsq_alpha, p.lsq_qmax);
+            else
+                p.partial[((int64_t)blockIdx.y * p.B + tok) * p.rows + o] = sum[i];
+        }
+    }
+}
+
+namespace {
+
+template <int Q, int M, bool BF16>
+void launch_wide_fmt(const VlutMatmulArgs& p, int splits, hipStream_t s)
+{
+    dim3 grid((unsigned)((p.rows + kWideRows - 1) / kWideRows), (unsigned)splits,
+              (unsigned)((p.B + kWideTokens - 1) / kWideTokens));
+#define COSET_WIDE(F) \
+    hipLaunchKernelGGL((vlut_wide_kernel<Q, M, BF16, F, kWideRT, kWideNW>), grid, dim3(kWideNW * 64), 0, s, p)
+    switch (p.prepared) {
+    case VLUT_RAW: COSET_WIDE(VLUT_RAW); break;
+    case VLUT_PREPARED: COSET_WIDE(VLUT_PREPARED); break;
+    case VLUT_DECODED: COSET_WIDE(VLUT_DECODED); break;
+    default: COSET_WIDE(VLUT_TILED); break;
+    }
+#undef COSET_WIDE
+}
+
+template <int Q>
+hipError_t dispatch_wide(const VlutMatmulArgs& p, int splits, hipStream_t s)
+{
+    const bool bf = p.act_dtype == DT_BF16;
+    switch (p.M) {
+#define COSET_M(MM) \
+    case MM: \
+        if constexpr (Q == 2 || MM <= 2) { \
+            if (bf) launch_wide_fmt<Q, MM, true>(p, splits, s); else launch_wide_fmt<Q, MM, false>(p, splits, s); \
+            return hipGetLastError(); \
+        } \
+        return hipErrorInvalidValue;
+    COSET_M(1) COSET_M(2) COSET_M(3) COSET_M(4)
+#undef COSET_M
+    default: return hipErrorInvalidValue;
+    }
+}
+
+template <int Q, int M, bool BF16>
+void launch_deep_fmt(const VlutMatmulArgs& p, int splits, hipStream_t s)
+{
+    dim3 grid((unsigned)((p.rows + kDeepRows - 1) / kDeepRows), (unsigned)splits,
+              (unsigned)((p.B + kDeepTokens - 1) / kDeepTokens));
+#define COSET_DEEP(F) hipLaunchKernelGGL((vlut_deep_kernel<Q, M, BF16, F>), grid, dim3(kDeepNW * 64), 0, s, p)
+    switch (p.prepared) {
+    case VLUT_RAW: COSET_DEEP(VLUT_RAW); break;
+    case VLUT_PREPARED: COSET_DEEP(VLUT_PREPARED); break;
+    case VLUT_DECODED: COSET_DEEP(VLUT_DECODED); break;
+    default: COSET_DEEP(VLUT_TILED); break;
+    }
+#undef COSET_DEEP
+}
+
+template <int Q>
+hipError_t dispatch_deep(const VlutMatmulArgs& p, int splits, hipStream_t s)
+{
+    const bool bf = p.act_dtype == DT_BF16;
+    switch (p.M) {
+#define COSET_M(MM) \
+    case MM: \
+        if constexpr (Q == 2 || MM <= 2) { \
+            if (bf) launch_deep_fmt<Q, MM, true>(p, splits, s); else launch_deep_fmt<Q, MM, false>(p, splits, s); \
+            return hipGetLastError(); \
+        } \
+        return hipErrorInvalidValue;
+    COSET_M(1) COSET_M(2) COSET_M(3) COSET_M(4)
+#undef COSET_M
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+hipError_t vlut_launch_wide(const VlutMatmulArgs& p, int splits, hipStream_t s)
+{
+    return p.q == 4 ? dispatch_wide<4>(p, splits, s) : dispatch_wide<2>(p, splits, s);
+}
+
+hipError_t vlut_launch_deep(const VlutMatmulArgs& p, int splits, hipStream_t s)
+{
+    return p.q == 4 ? dispatch_deep<4>(p, splits, s) : dispatch_deep<2>(p, splits, s);
+}
+
+}  // namespace coset

@@ -164,6 +164,36 @@ def test_vlut_matmul_forced_splits(splits):
         _lib.set_vlut_splits(0)
 
 
+@pytest.mark.parametrize("B", [1, 2, 8, 9, 16])
+@pytest.mark.parametrize("K,splits", [(4096, 0), (4608, 1), (4608, 3)])
+def test_rows_kernel_staged_and_direct_activations(B, K, splits):
+    """Batches of one 16-token tile take the rows kernel with activations
+    staged in LDS (token bounds 1, 8, 16) when a wave's K range is at most
+    16 k-quads, and loaded straight into the A operands otherwise (K = 4608
+    in one split: 18 k-quads per wave); every weight format and both input
+    types against the oracle."""
+    import coset_amd
+    from coset_amd import _lib
+    rng = np.random.default_rng(2000 + B + K)
+    rows, q, M = 48, 4, 2
+    W = rng.standard_normal((rows, K)).astype(np.float32)
+    codes = O.e8_encode(W.reshape(-1, 8), q, M)
+    words_np = O.pack_words(codes, q).reshape(rows, K // 8, M)
+    words = torch.from_numpy(words_np.astype(np.int32)).to(torch.uint16).cuda()
+    scale = rng.uniform(0.5, 2.0, rows).astype(np.float32)
+    forms = [words] + [coset_amd.vlut_prepare(words, q, layout=lay) for lay in ("rowmajor", "tiled", "decoded")]
+    _lib.set_vlut_splits(splits)
+    try:
+        for dt in (torch.float16, torch.bfloat16):
+            a = torch.from_numpy(rng.standard_normal((B, K)).astype(np.float32)).to(dt)
+            ref = O.vlut_matmul(words_np, scale, a.float().numpy(), q, M)
+            for w in forms:
+                out = coset_amd.vlut_matmul(w, a.cuda(), q, scale=torch.from_numpy(scale), method="mfma")
+                close(out.cpu().numpy(), ref, 1e-3)
+    finally:
+        _lib.set_vlut_splits(0)
+
+
 @pytest.mark.parametrize("B", [1, 5, 17, 40, 70])
 def test_vlut_matmul_ragged_shapes(B, mfma_decode):
     """Rows and k-blocks that fill no tile (37 rows, 13 k-blocks), token
