@@ -40,7 +40,10 @@ __device__ __forceinline__ void two_r_tables(uint32_t w, const uint16_t* map, co
 // tile spans at least 64 blocks.
 constexpr int kWgTiles = 256 / 64 + 2;
 
-template <int Q, int MODE>
+// WGBETA: layer scaling with beta derived from theta and tiles of at least
+// 64 blocks -- the workgroup derives the beta of each tile it touches once,
+// in LDS, instead of every block deriving its own.
+template <int Q, int MODE, bool WGBETA>
 __global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
 {
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -49,11 +52,7 @@ __global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
     const float qf = (float)q;
     const int M = a.M;
 
-    // the block's input is loaded first (clamped to the last block), so its
-    // latency overlaps the scale's loads below
-    float xl[8];
-    if (MODE != MODE_DECODE) {
-        const int64_t il = i < a.n ? i : a.n - 1;
+    auto load_block = [&](int64_t il, float xl[8]) {
         if (a.x_dtype == DT_BF16) {
             uint4 v = reinterpret_cast<const uint4*>(a.x)[il];
             uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -68,12 +67,14 @@ __global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
             xl[0] = u.x; xl[1] = u.y; xl[2] = u.z; xl[3] = u.w;
             xl[4] = v.x; xl[5] = v.y; xl[6] = v.z; xl[7] = v.w;
         }
-    }
-
+    };
+    float xl[8];
     float scale = 1.f;
-    if (a.scale_mode == SCALE_LAYER && a.use_theta && a.blocks_per_row >= 64) {
-        // beta from theta once per tile the workgroup touches (not per block):
-        // the workgroup's blocks span tiles t0 .. t0 + kWgTiles - 1 at most
+    if constexpr (WGBETA) {
+        // the block's input is loaded first (clamped to the last block), so its
+        // latency overlaps the tile betas' derivation; the workgroup's blocks
+        // span tiles t0 .. t0 + kWgTiles - 1 at most
+        if (MODE != MODE_DECODE) load_block(i < a.n ? i : a.n - 1, xl);
         __shared__ float s_beta[kWgTiles];
         const int64_t b0 = (int64_t)blockIdx.x * blockDim.x;
         const int64_t t0 = b0 / a.blocks_per_row;
@@ -90,14 +91,16 @@ __global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
             }
         }
         __syncthreads();
-        if (i < a.n) scale = s_beta[i / a.blocks_per_row - t0];
-    } else if (i < a.n) {
+        if (i >= a.n) return;
+        scale = s_beta[i / a.blocks_per_row - t0];
+    } else {
+        if (i >= a.n) return;
         if (a.scale_mode == SCALE_CODEC)
             scale = a.beta;
         else if (a.scale_mode == SCALE_LAYER)
             scale = layer_scale(a, i);
+        if (MODE != MODE_DECODE) load_block(i, xl);
     }
-    if (i >= a.n) return;
 
     float acc[8];
 #pragma unroll
@@ -233,13 +236,19 @@ static hipError_t launch_mode(const CodecArgs& a, hipStream_t s)
 {
     dim3 block(256);
     dim3 grid((unsigned)((a.n + 255) / 256));
+    const bool wg_beta = a.scale_mode == SCALE_LAYER && a.use_theta && a.blocks_per_row >= 64;
+#define COSET_Q(QQ) \
+    if (wg_beta) hipLaunchKernelGGL((hnlq_codec_kernel<QQ, MODE, true>), grid, block, 0, s, a); \
+    else hipLaunchKernelGGL((hnlq_codec_kernel<QQ, MODE, false>), grid, block, 0, s, a); \
+    break;
     switch (a.q) {
-    case 2: hipLaunchKernelGGL((hnlq_codec_kernel<2, MODE>), grid, block, 0, s, a); break;
-    case 4: hipLaunchKernelGGL((hnlq_codec_kernel<4, MODE>), grid, block, 0, s, a); break;
-    case 8: hipLaunchKernelGGL((hnlq_codec_kernel<8, MODE>), grid, block, 0, s, a); break;
-    case 16: hipLaunchKernelGGL((hnlq_codec_kernel<16, MODE>), grid, block, 0, s, a); break;
-    default: hipLaunchKernelGGL((hnlq_codec_kernel<0, MODE>), grid, block, 0, s, a); break;
+    case 2: COSET_Q(2)
+    case 4: COSET_Q(4)
+    case 8: COSET_Q(8)
+    case 16: COSET_Q(16)
+    default: COSET_Q(0)
     }
+#undef COSET_Q
     return hipGetLastError();
 }
 
