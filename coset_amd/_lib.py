@@ -14,7 +14,7 @@ import torch
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_PKG, "libcoset_amd.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # mirrors of the enums in include/coset_amd.h
 OK, EINVAL, EUNSUPPORTED, EHIP = 0, -1, -2, -3
@@ -40,7 +40,8 @@ SIGNATURES = {
     "coset_e8_qat_bwd": [_vp, _int, _vp, _vp, _vp, _i64, _i64, _i64, _flt, _int, _int, _vp, _vp,
                          _vp],
     "coset_e8_qat_fwd_theta": [_vp, _i64, _i64, _i64, _vp, _vp, _vp, ctypes.c_double, ctypes.c_double,
-                               ctypes.c_double, _int, _flt, _int, _int, _vp, _int, _vp, _vp, _vp, _vp, _vp],
+                               ctypes.c_double, _int, _flt, _int, _int, _vp, _int, _vp, _vp, _vp, _vp, _vp,
+                               _vp, _vp],
     "coset_e8_qat_bwd_theta": [_vp, _int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _flt, _int, _int, _vp, _vp, _vp,
                                _vp],
     "coset_vlut_build_one_sided": [_vp, _i64, _int, _int, _vp, _vp],

@@ -373,10 +373,11 @@ int coset_e8_qat_fwd_theta(const float* W, int64_t rows, int64_t cols, int64_t b
                            const float* theta, const float* sigma_ema, const float* xmax_ema, double delta0,
                            double eta, double gamma_inv, int M_bounds, float clip, int q, int M, void* Wq,
                            int wq_dtype, void* packed, float* beta_out, float* dbeta_dtheta_out,
-                           int64_t* step_counter, void* stream)
+                           int64_t* step_counter, const float* bias, void* bias_out, void* stream)
 {
     int rc;
     if (rows < 0 || cols < 0 || cols % 8) return fail(COSET_EINVAL, "W must be [rows, 8k]");
+    if ((bias == nullptr) != (bias_out == nullptr)) return fail(COSET_EINVAL, "bias and bias_out go together");
     int64_t n = rows * (cols / 8);
     if ((rc = check_qm(q, M))) return rc;
     if (M_bounds < 1 || M_bounds > 16) return fail(COSET_EINVAL, "M_bounds=%d", M_bounds);
@@ -407,6 +408,9 @@ int coset_e8_qat_fwd_theta(const float* W, int64_t rows, int64_t cols, int64_t b
     a.beta_out = beta_out;
     a.dbdt_out = dbeta_dtheta_out;
     a.step_counter = step_counter;
+    a.aux_in = bias;
+    a.aux_out = bias_out;
+    a.aux_n = bias ? rows : 0;
     return check_hip(coset::launch_codec(a, coset::MODE_ROUNDTRIP, (hipStream_t)stream), "qat forward launch");
 }
 

@@ -93,6 +93,11 @@ struct CodecArgs {
     // from the coarse-point id instead of running the projection
     const uint16_t* dec_map;
     const uint64_t* dec_coarse;
+    // nullable: aux_out[i] = aux_in[i] in out_dtype for i < aux_n, written by
+    // the same launch (the layer's bias in the GEMM's dtype)
+    const float* aux_in;
+    void* aux_out;
+    int64_t aux_n;
 };
 
 // One encoder level (core rule, contiguous distances): the projection's

@@ -13,6 +13,8 @@
 //   SCALE_CODEC  x_s = x / beta;        out = dec * beta           (codecs.py:64,175)
 //   SCALE_LAYER  x_s = x * beta_row;    out = clamp(dec / beta_row, +-clip)
 //                                                                 (layers.py:431,455,463)
+#include <algorithm>
+
 #include "codec_kernels.hpp"
 #include "tables.hpp"
 
@@ -43,11 +45,29 @@ constexpr int kWgTiles = 256 / 64 + 2;
 // WGBETA: layer scaling with beta derived from theta and tiles of at least
 // 64 blocks -- the workgroup derives the beta of each tile it touches once,
 // in LDS, instead of every block deriving its own.
+// aux_out[i] = aux_in[i] in out_dtype (fp32 -> bf16 round to nearest even,
+// as torch's cast)
+__device__ __forceinline__ void aux_cast(const CodecArgs& a, int64_t i)
+{
+    const float v = a.aux_in[i];
+    if (a.out_dtype == DT_BF16)
+        reinterpret_cast<uint16_t*>(a.aux_out)[i] = f32_to_bf16(v);
+    else
+        reinterpret_cast<float*>(a.aux_out)[i] = v;
+}
+
+__global__ void __launch_bounds__(256) aux_cast_kernel(CodecArgs a)
+{
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < a.aux_n) aux_cast(a, i);
+}
+
 template <int Q, int MODE, bool WGBETA>
 __global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
 {
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i == 0 && a.step_counter) *a.step_counter += 1;
+    if (a.aux_out && i < a.aux_n) aux_cast(a, i);
     const int q = Q > 0 ? Q : a.q;
     const float qf = (float)q;
     const int M = a.M;
@@ -235,7 +255,7 @@ template <int MODE>
 static hipError_t launch_mode(const CodecArgs& a, hipStream_t s)
 {
     dim3 block(256);
-    dim3 grid((unsigned)((a.n + 255) / 256));
+    dim3 grid((unsigned)((std::max<int64_t>(a.n, a.aux_out ? a.aux_n : 0) + 255) / 256));
     const bool wg_beta = a.scale_mode == SCALE_LAYER && a.use_theta && a.blocks_per_row >= 64;
 #define COSET_Q(QQ) \
     if (wg_beta) hipLaunchKernelGGL((hnlq_codec_kernel<QQ, MODE, true>), grid, block, 0, s, a); \
@@ -257,11 +277,18 @@ int g_fast_projection = 1;
 
 hipError_t launch_codec(const CodecArgs& args, int mode, hipStream_t s)
 {
-    if (args.n == 0) return hipSuccess;
     CodecArgs a = args;
     a.fast_projection = g_fast_projection;
     bool lut = lut_path_supported(a, mode) &&
                (g_codec_path == 2 || (g_codec_path == 0 && a.n >= kLutMinBlocks));
+    if (a.aux_out && a.aux_n > 0 && (lut || a.n == 0)) {
+        // the table kernels take no side cast: it gets its own launch
+        hipLaunchKernelGGL(aux_cast_kernel, dim3((unsigned)((a.aux_n + 255) / 256)), dim3(256), 0, s, a);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        a.aux_out = nullptr;
+    }
+    if (a.n == 0) return hipSuccess;
     if (lut) return launch_codec_lut(a, mode, s);
     if (g_codec_path == 0 && (a.q == 2 || a.q == 4) && mode != MODE_ENCODE) {
         // layer-sized calls: the generic kernel decodes through the tables
@@ -277,7 +304,7 @@ hipError_t launch_codec(const CodecArgs& args, int mode, hipStream_t s)
 
 hipError_t launch_codec_generic(const CodecArgs& a, int mode, hipStream_t s)
 {
-    if (a.n == 0) return hipSuccess;
+    if (a.n == 0) return hipSuccess;  // (launch_codec has already done a side cast of an empty codec call)
     switch (mode) {
     case MODE_ENCODE: return launch_mode<MODE_ENCODE>(a, s);
     case MODE_DECODE: return launch_mode<MODE_DECODE>(a, s);

@@ -180,9 +180,11 @@ class E8WeightQuant(torch.autograd.Function):
         return dW, dbeta.view(beta_shape), None, None, None, None, None
 
 
-def qat_fwd_theta(Wc, theta, sigma, xmax, step_count, bounds, q, M, clip, blocks_per_tile, out_dtype):
+def qat_fwd_theta(Wc, theta, sigma, xmax, step_count, bounds, q, M, clip, blocks_per_tile, out_dtype, bias=None):
     """One coset_e8_qat_fwd_theta call: (W_q [rows, cols] in out_dtype,
-    level words [rows * cols / 8, M], beta [tiles], d beta / d theta [tiles])."""
+    level words [rows * cols / 8, M], beta [tiles], d beta / d theta [tiles],
+    and, given an fp32 bias [rows], that bias in out_dtype from the same
+    launch, else None)."""
     th = theta.contiguous()
     rows, cols = Wc.shape
     dev = Wc.device
@@ -190,13 +192,19 @@ def qat_fwd_theta(Wc, theta, sigma, xmax, step_count, bounds, q, M, clip, blocks
     packed = torch.empty((rows * (cols // 8), M), dtype=word_dtype(q), device=dev)
     beta = torch.empty(th.numel(), dtype=torch.float32, device=dev)
     dbdt = torch.empty_like(beta)
+    b_in = b_out = None
+    if bias is not None:
+        b_in = bias.detach().float().contiguous()
+        if b_in.numel() != rows:
+            raise ValueError(f"bias must hold {rows} values")
+        b_out = torch.empty(rows, dtype=out_dtype, device=dev)
     delta0, eta, ginv, m_bounds = bounds
     _lib.check("coset_e8_qat_fwd_theta", _lib.fn("coset_e8_qat_fwd_theta")(
         Wc.data_ptr(), rows, cols, blocks_per_tile, th.data_ptr(), sigma.contiguous().data_ptr(),
         xmax.contiguous().data_ptr(), delta0, eta, ginv, m_bounds, clip, q, M, Wq.data_ptr(),
         _lib.dtype_code(out_dtype), packed.data_ptr(), beta.data_ptr(), dbdt.data_ptr(),
-        _lib.ptr(step_count), _lib.stream_of(Wc)))
-    return Wq, packed, beta, dbdt
+        _lib.ptr(step_count), _lib.ptr(b_in), _lib.ptr(b_out), _lib.stream_of(Wc)))
+    return Wq, packed, beta, dbdt, b_out
 
 
 class E8ThetaWeightQuant(torch.autograd.Function):
@@ -208,16 +216,21 @@ class E8ThetaWeightQuant(torch.autograd.Function):
     do not affect this step's gradient."""
 
     @staticmethod
-    def forward(ctx, W, theta, sigma, xmax, step_count, bounds, q, M, clip, blocks_per_tile, out_dtype):
+    def forward(ctx, W, theta, sigma, xmax, step_count, bounds, q, M, clip, blocks_per_tile, out_dtype, bias=None):
         Wc = W.detach().contiguous()
-        Wq, packed, beta, dbdt = qat_fwd_theta(Wc, theta.detach(), sigma, xmax, step_count, bounds, q, M, clip,
-                                               blocks_per_tile, out_dtype)
+        Wq, packed, beta, dbdt, b_cast = qat_fwd_theta(Wc, theta.detach(), sigma, xmax, step_count, bounds, q, M,
+                                                       clip, blocks_per_tile, out_dtype, bias)
         ctx.save_for_backward(Wc, packed, beta, dbdt)
         ctx.cfg = (q, M, clip, blocks_per_tile, theta.shape)
-        return Wq
+        if b_cast is None:
+            return Wq
+        # the bias in the product's dtype rides along, not differentiable here:
+        # its gradient reaches the fp32 bias through QATLinearFn
+        ctx.mark_non_differentiable(b_cast)
+        return Wq, b_cast
 
     @staticmethod
-    def backward(ctx, g):
+    def backward(ctx, g, g_bias=None):
         Wc, packed, beta, dbdt = ctx.saved_tensors
         q, M, clip, bpt, theta_shape = ctx.cfg
         if g.dtype not in (torch.float32, torch.bfloat16):
@@ -231,7 +244,7 @@ class E8ThetaWeightQuant(torch.autograd.Function):
             g.data_ptr(), _lib.dtype_code(g.dtype), Wc.data_ptr(), packed.data_ptr(), beta.data_ptr(),
             dbdt.data_ptr(), rows, cols, bpt, clip, q, M, dW.data_ptr(), dbeta.data_ptr(), dtheta.data_ptr(),
             _lib.stream_of(Wc)))
-        return dW, dtheta.view(theta_shape), None, None, None, None, None, None, None, None, None
+        return dW, dtheta.view(theta_shape), None, None, None, None, None, None, None, None, None, None
 
 
 def d4_qat_fwd_theta(Wc, theta, sigma, xmax, step_count, bounds, q, clip, blocks_per_tile, out_dtype):
@@ -305,10 +318,14 @@ class QATLinearFn(torch.autograd.Function):
     sum of its gradient."""
 
     @staticmethod
-    def forward(ctx, x, Wq, bias):
+    def forward(ctx, x, Wq, bias, bias_cast=None):
+        """bias_cast (optional): bias already in x's dtype (the fused
+        quantizer writes it); the gradient still goes to bias."""
         ctx.save_for_backward(x, Wq)
         ctx.bias_dtype = None if bias is None else bias.dtype
-        return F.linear(x, Wq, None if bias is None else bias.to(x.dtype))
+        if bias is not None and bias_cast is None:
+            bias_cast = bias.to(x.dtype)
+        return F.linear(x, Wq, bias_cast)
 
     @staticmethod
     def backward(ctx, gy):
@@ -324,7 +341,7 @@ class QATLinearFn(torch.autograd.Function):
                 db = colsum(g2).to(ctx.bias_dtype)
             else:
                 db = g2.float().sum(0).to(ctx.bias_dtype)
-        return dx, dW, db
+        return dx, dW, db, None
 
 
 class HNLQLinearQAT(nn.Module):
@@ -519,11 +536,17 @@ class HNLQLinearQAT(nn.Module):
                 and self.lattice_type == "D4" and self.weight.is_cuda)
 
     def _quantize_weights_as(self, out_dtype: torch.dtype):
+        return self._quantize_weights_with_bias(out_dtype, False)[0]
+
+    def _quantize_weights_with_bias(self, out_dtype: torch.dtype, cast_bias: bool):
+        """(W_q in out_dtype, the bias in out_dtype written by the same fused
+        launch when cast_bias and the fused E8 path runs, else None)."""
         W = self.weight
         if not self.quantization_enabled:
             if self.enable_diagnostics:
                 self._weight_history.append(W.detach().clone())
-            return W
+            return W, None
+        b_cast = None
         fused = self._fused()
         fused_d4 = self._fused_d4()
         self._advance_step(device_increment=not (fused or fused_d4))
@@ -536,15 +559,17 @@ class HNLQLinearQAT(nn.Module):
             bpt = self.blocks_per_row if self.tiling == "row" else 1
             # one theta per tile: out_features entries for row tiling, so no slice is needed
             # the injected e8_quantize always encodes with M = 2 (codecs.py:245-254)
-            W_q = E8ThetaWeightQuant.apply(W, self.theta_beta, self.sigma_ema, self.xmax_ema, self.step_count,
+            out = E8ThetaWeightQuant.apply(W, self.theta_beta, self.sigma_ema, self.xmax_ema, self.step_count,
                                            (float(self.Delta0), float(self.eta), self._ginv_f, int(self.M)),
-                                           int(self.q), 2, float(self.weight_clip_value), int(bpt), out_dtype)
+                                           int(self.q), 2, float(self.weight_clip_value), int(bpt), out_dtype,
+                                           self.bias if cast_bias else None)
+            W_q, b_cast = out if isinstance(out, tuple) else (out, None)
         else:
             W_q = self._reference_composition(W, self._beta()).to(out_dtype)
         if self.enable_diagnostics:
             self._weight_history.append(W.detach().clone())
             self._quantization_errors.append(torch.norm(W - W_q.float()).item())
-        return W_q
+        return W_q, b_cast
 
     def _reference_composition(self, W, beta):
         """layers.py:428-463 around an arbitrary injected quantize_fn."""
@@ -571,11 +596,14 @@ class HNLQLinearQAT(nn.Module):
         wdt = x.dtype if x.dtype in (torch.bfloat16, torch.float16) else torch.float32
         if wdt == torch.float16:
             wdt = torch.float32
-        W_q = self._quantize_weights_as(wdt)
+        # a bf16 product takes the bias in bf16: the fused quantizer writes it
+        # in the same launch as W_q
+        cast_bias = x.is_cuda and self.bias is not None and wdt == torch.bfloat16 and x.dtype == wdt
+        W_q, b_cast = self._quantize_weights_with_bias(wdt, cast_bias)
         if W_q.dtype != x.dtype:
             W_q = W_q.to(x.dtype)
         if x.is_cuda:
-            x = QATLinearFn.apply(x, W_q, self.bias)
+            x = QATLinearFn.apply(x, W_q, self.bias, b_cast)
         else:
             x = F.linear(x, W_q, self.bias.to(x.dtype) if self.bias is not None else None)
         if self.quantize_activations and self.actq is not None:
@@ -672,7 +700,7 @@ class HNLQLinearQAT(nn.Module):
                 # the same quantization again, without advancing the step:
                 # its level words and beta reproduce W_q bit for bit
                 bpt = self.blocks_per_row if self.tiling == "row" else 1
-                _, packed, beta, _ = qat_fwd_theta(
+                _, packed, beta, _, _ = qat_fwd_theta(
                     self.weight.detach().contiguous(), self.theta_beta.detach(), self.sigma_ema, self.xmax_ema,
                     None, (float(self.Delta0), float(self.eta), self._ginv_f, int(self.M)), int(self.q), 2,
                     float(self.weight_clip_value), int(bpt), torch.float32)
@@ -697,8 +725,8 @@ class CapturedQATStep:
     given) captured once into a HIP graph and replayed by ``step()``.
 
     No counterpart in the reference, whose layer runs eagerly on the CPU.
-    An eager step issues about fifteen small launches from Python (bias cast,
-    the fused quantizer, hipBLASLt's products, the bias-gradient reduction),
+    An eager step issues about fifteen small launches from Python (the fused
+    quantizer, hipBLASLt's products, the backward and bias-gradient kernels),
     so at BERT shapes the host, not the GPU, sets its time; a replay issues
     them as one graph launch.
 

@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define COSET_ABI_VERSION 2
+#define COSET_ABI_VERSION 3
 
 enum {
     COSET_OK = 0,
@@ -172,12 +172,15 @@ int coset_e8_qat_bwd(const void* gWq, int g_dtype, const float* W, const void* p
  * (nullable, [tiles]) receive the beta used and (beta_max - beta_min) s (1 - s),
  * s = sigmoid(theta); step_counter (nullable, int64 device scalar: the layer's
  * step_count buffer) is incremented once.  M_bounds is the layer's M (the
- * bounds' q^M); M is the codec depth (2: e8_quantize, codecs.py:245-254). */
+ * bounds' q^M); M is the codec depth (2: e8_quantize, codecs.py:245-254).
+ * bias / bias_out (nullable, [rows]): the same launch also writes the
+ * layer's fp32 bias in wq_dtype (round to nearest even), the operand of the
+ * product that follows (layers.py:478), so no separate cast launch is needed. */
 int coset_e8_qat_fwd_theta(const float* W, int64_t rows, int64_t cols, int64_t blocks_per_tile,
                            const float* theta, const float* sigma_ema, const float* xmax_ema, double delta0,
                            double eta, double gamma_inv, int M_bounds, float clip, int q, int M, void* Wq,
                            int wq_dtype, void* packed, float* beta_out, float* dbeta_dtheta_out,
-                           int64_t* step_counter, void* stream);
+                           int64_t* step_counter, const float* bias, void* bias_out, void* stream);
 
 /* Backward of coset_e8_qat_fwd_theta: dW and dbeta as coset_e8_qat_bwd, plus
  * dtheta[t] = dbeta[t] * dbeta_dtheta[t] (the factor the forward recorded). */

@@ -40,7 +40,7 @@ def kernel_beta(layer):
     quantizer kernel with the layer's theta and statistics (no step)."""
     from coset_amd.layers import qat_fwd_theta
     bpt = layer.blocks_per_row if layer.tiling == "row" else 1
-    Wq, packed, beta, dbdt = qat_fwd_theta(
+    Wq, packed, beta, dbdt, _ = qat_fwd_theta(
         layer.weight.detach().contiguous(), layer.theta_beta.detach(), layer.sigma_ema, layer.xmax_ema, None,
         (float(layer.Delta0), float(layer.eta), layer._ginv_f, int(layer.M)), int(layer.q), 2,
         float(layer.weight_clip_value), int(bpt), torch.float32)
