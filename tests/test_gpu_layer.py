@@ -345,3 +345,30 @@ def test_colsum_is_exact_fp32_sum(dtype, rows, cols):
     mag = g.double().abs().sum(0)
     assert ((a.double() - ref).abs() <= 2 ** -17 * mag + 1e-30).all()
     assert a.shape == (cols,) and a.dtype == torch.float32
+
+
+@pytest.mark.parametrize("rows,cols", [(768, 768), (4096, 2048), (3, 8)])
+def test_fused_quantizer_writes_the_bias_cast(rows, cols):
+    """The quantizer launch also writes the fp32 bias in bf16, equal to
+    torch's cast (round to nearest even, NaN and infinities kept), on the
+    general kernel and on the table kernel's path (4096 x 2048 = 2^20
+    blocks: a side launch), with W_q unchanged by it."""
+    from coset_amd.layers import qat_fwd_theta
+    g = torch.Generator(device="cuda").manual_seed(rows + cols)
+    W = 0.02 * torch.randn((rows, cols), device="cuda", generator=g)
+    theta = torch.randn(rows, device="cuda", generator=g)
+    sigma = torch.full((rows,), 0.02, device="cuda")
+    xmax = torch.full((rows,), 0.08, device="cuda")
+    bias = torch.randn(rows, device="cuda", generator=g) * 10
+    bias[0] = float("inf")
+    if rows > 2:
+        bias[1] = float("nan")
+        bias[2] = 1.0 + 2 ** -8          # a tie: rounds to even
+    args = (W, theta, sigma, xmax, None, (1.5, 0.1, 1 / 12.0, 2), 4, 2, 2.0, cols // 8, torch.bfloat16)
+    Wq, packed, beta, dbdt, bc = qat_fwd_theta(*args, bias=bias)
+    Wq2, packed2, beta2, _, none = qat_fwd_theta(*args)
+    assert none is None and bc.dtype == torch.bfloat16 and bc.shape == (rows,)
+    ref = bias.to(torch.bfloat16)
+    assert torch.equal(bc.view(torch.int16)[~ref.isnan()], ref.view(torch.int16)[~ref.isnan()])
+    assert torch.equal(bc.isnan(), ref.isnan())
+    assert torch.equal(Wq, Wq2) and torch.equal(packed, packed2) and torch.equal(beta, beta2)
