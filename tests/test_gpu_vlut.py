@@ -1,7 +1,11 @@
 """vLUT kernels against the reference's legacy one-sided tables
-(tests/golden/vlut_legacy.npz), the oracle, and decode-then-dot.  Table
-entries and lookup sums within 1e-6 of the table's magnitude (8-term fp32
-dot products); matmul outputs within 1e-3 of the max magnitude."""
+(tests/golden/vlut_legacy.npz), the oracle, and decode-then-dot.
+
+Tolerances are elementwise and relative to the magnitude of the summands
+that make up each value: a table entry <a, r(b)> within 1e-6 of
+sum_j |a_j| |r_j(b)|, a lookup sum or matmul output within 1e-3 (fp32
+accumulate, the north star's bound) of sum_k sum_m q^m |<a_k, r(b_m)>|
+bounded by |a| @ (sum_m q^m |r(b_m)|)^T times the row's scale."""
 import numpy as np
 import pytest
 import torch
@@ -11,11 +15,38 @@ from oracle import oracle as O
 pytestmark = pytest.mark.gpu
 
 
-def close(a, b, tol):
-    a = np.asarray(a, np.float64)
-    b = np.asarray(b, np.float64)
-    scale = max(np.abs(b).max(), 1e-30)
-    assert np.abs(a - b).max() <= tol * scale, (np.abs(a - b).max(), scale)
+def close(a, b, mag, tol):
+    """Elementwise |a - b| <= tol * max(mag, |b|)."""
+    a, b, mag = (np.asarray(t, np.float64) for t in (a, b, mag))
+    bound = tol * np.maximum(mag, np.abs(b))
+    bad = np.abs(a - b) > bound
+    assert not bad.any(), (int(bad.sum()), float(np.abs(a - b)[bad].max()), float(bound[bad].min()))
+
+
+_RTABLES = {}
+
+
+def abs_residuals(q, legacy):
+    """|r(b)| for every level word of q (oracle residual table), float64."""
+    key = (q, bool(legacy))
+    if key not in _RTABLES:
+        _RTABLES[key] = np.abs(O.residual_table(q, legacy=legacy).astype(np.float64))
+    return _RTABLES[key]
+
+
+def matmul_mag(words_np, q, M, act, scale=None, scale_mode=0, legacy=False):
+    """Bound of the summands' magnitude of every vLUT matmul output:
+    |a| @ (sum_m q^m |r(b_m)|)^T, times |s_o| (or / |s_o| for scale_mode 1)."""
+    R = abs_residuals(q, legacy)
+    rows, kb, _ = words_np.shape
+    w = np.zeros((rows, kb, 8))
+    for m in range(M):
+        w += float(q) ** m * R[np.asarray(words_np[:, :, m], np.int64)]
+    mag = np.abs(np.asarray(act, np.float64)) @ w.reshape(rows, kb * 8).T
+    if scale is not None:
+        s = np.abs(np.asarray(scale, np.float64))
+        mag = mag * (s if scale_mode == 0 else 1.0 / s)[None, :]
+    return mag
 
 
 @pytest.mark.parametrize("q", [3, 4])
@@ -27,7 +58,8 @@ def test_legacy_one_sided_matches_reference(golden, q):
         a = torch.from_numpy(V[f"q{q}_a{i}"])
         v = mgr.build_one_sided_vlut(a)
         assert v.device.type == "cpu" and v.shape == (q ** 8,)
-        close(v.numpy(), V[f"q{q}_vlut{i}"], 1e-6)
+        close(v.numpy(), V[f"q{q}_vlut{i}"], abs_residuals(q, True) @ np.abs(V[f"q{q}_a{i}"].astype(np.float64)),
+              1e-6)
         assert mgr.build_one_sided_vlut(a) is v  # cached
 
 
@@ -37,10 +69,10 @@ def test_core_one_sided_matches_oracle():
     a = rng.standard_normal((3, 8)).astype(np.float32)
     for q in (2, 4):
         v = coset_amd.build_one_sided_vluts(torch.from_numpy(a), q, legacy=False).cpu().numpy()
+        R = O.e8_decode(O.unpack_words(np.arange(q ** 8), q).reshape(-1, 1, 8), q, 1).astype(np.float64)
         for i in range(3):
-            ref = np.array([np.dot(a[i].astype(np.float64), r) for r in
-                            O.e8_decode(O.unpack_words(np.arange(q ** 8), q).reshape(-1, 1, 8), q, 1)])
-            close(v[i], ref, 1e-6)
+            ref = R @ a[i].astype(np.float64)
+            close(v[i], ref, np.abs(R) @ np.abs(a[i].astype(np.float64)), 1e-6)
 
 
 def test_equal_sum_queries_get_their_own_tables():
@@ -60,8 +92,11 @@ def test_lookup_dot_equals_decode_then_dot():
     words = coset_amd.hnlq_encode(torch.from_numpy(x).cuda(), 4, 2, 1.0)
     vl = coset_amd.build_one_sided_vluts(torch.from_numpy(a).reshape(1, 8), 4, legacy=False)[0]
     got = coset_amd.vlut_dot(words, vl, 4).cpu().numpy()
-    dec = O.e8_decode(O.e8_encode(x, 4, 2), 4, 2)
-    close(got, dec.astype(np.float64) @ a.astype(np.float64), 1e-6)
+    codes = O.e8_encode(x, 4, 2)
+    dec = O.e8_decode(codes, 4, 2)
+    words_np = O.pack_words(codes, 4).reshape(-1, 1, 2)
+    mag = matmul_mag(words_np, 4, 2, a.reshape(1, 8))[0]
+    close(got, dec.astype(np.float64) @ a.astype(np.float64), mag, 1e-6)
 
 
 def test_reference_helpers():
@@ -111,10 +146,11 @@ def test_vlut_matmul_vs_oracle(method, B, adt, mfma_decode):
         for mode in ("mul", "div"):
             sm = 0 if mode == "mul" else 1
             ref = O.vlut_matmul(words_np, scale, a.float().numpy(), q, M, scale_mode=sm, legacy=legacy)
+            mag = matmul_mag(words_np, q, M, a.float().numpy(), scale, sm, legacy)
             for w in [words] + prepared:
                 out = coset_amd.vlut_matmul(w, a.cuda(), q, scale=torch.from_numpy(scale), scale_mode=mode,
                                             legacy=legacy, method=method).cpu().numpy()
-                close(out, ref, 1e-3)
+                close(out, ref, mag, 1e-3)
 
 
 @pytest.mark.parametrize("q,M", [(2, 1), (2, 2), (2, 3), (2, 4), (4, 1), (4, 3)])
@@ -134,11 +170,12 @@ def test_vlut_matmul_other_levels(q, M, B, mfma_decode):
     scale = np.ones(rows, np.float32)
     for legacy in (False, True):
         ref = O.vlut_matmul(words_np, scale, a.float().numpy(), q, M, scale_mode=0, legacy=legacy)
+        mag = matmul_mag(words_np, q, M, a.float().numpy(), legacy=legacy)
         prepared = [coset_amd.vlut_prepare(words, q, legacy=legacy, layout=lay) for lay in ("rowmajor", "tiled")]
         for method in ("lds", "mfma"):
             for w in [words] + prepared:
                 out = coset_amd.vlut_matmul(w, a.cuda(), q, legacy=legacy, method=method).cpu().numpy()
-                close(out, ref, 1e-3)
+                close(out, ref, mag, 1e-3)
 
 
 @pytest.mark.parametrize("splits", [1, 2, 5, 64])
@@ -155,11 +192,12 @@ def test_vlut_matmul_forced_splits(splits):
     words = torch.from_numpy(words_np.astype(np.int32)).to(torch.uint16).cuda()
     a = torch.from_numpy(rng.standard_normal((4, K)).astype(np.float32)).to(torch.float16)
     ref = O.vlut_matmul(words_np, np.ones(rows, np.float32), a.float().numpy(), q, M)
+    mag = matmul_mag(words_np, q, M, a.float().numpy())
     _lib.set_vlut_splits(splits)
     try:
         for method in ("lds", "mfma"):
             out = coset_amd.vlut_matmul(words, a.cuda(), q, method=method).cpu().numpy()
-            close(out, ref, 1e-3)
+            close(out, ref, mag, 1e-3)
     finally:
         _lib.set_vlut_splits(0)
 
@@ -187,9 +225,10 @@ def test_rows_kernel_staged_and_direct_activations(B, K, splits):
         for dt in (torch.float16, torch.bfloat16):
             a = torch.from_numpy(rng.standard_normal((B, K)).astype(np.float32)).to(dt)
             ref = O.vlut_matmul(words_np, scale, a.float().numpy(), q, M)
+            mag = matmul_mag(words_np, q, M, a.float().numpy(), scale)
             for w in forms:
                 out = coset_amd.vlut_matmul(w, a.cuda(), q, scale=torch.from_numpy(scale), method="mfma")
-                close(out.cpu().numpy(), ref, 1e-3)
+                close(out.cpu().numpy(), ref, mag, 1e-3)
     finally:
         _lib.set_vlut_splits(0)
 
@@ -207,13 +246,15 @@ def test_vlut_matmul_ragged_shapes(B, mfma_decode):
     words = torch.from_numpy(words_np.astype(np.int32)).to(torch.uint16).cuda()
     a = torch.from_numpy(rng.standard_normal((B, K)).astype(np.float32))
     scale = rng.uniform(0.5, 2.0, rows).astype(np.float32)
-    ref = O.vlut_matmul(words_np, scale, a.numpy().astype(np.float16).astype(np.float32), q, M)
+    a16 = a.numpy().astype(np.float16).astype(np.float32)
+    ref = O.vlut_matmul(words_np, scale, a16, q, M)
+    mag = matmul_mag(words_np, q, M, a16, scale)
     forms = [words] + [coset_amd.vlut_prepare(words, q, layout=lay) for lay in ("rowmajor", "tiled")]
     for w in forms:
         for method in ("lds", "mfma"):
             out = coset_amd.vlut_matmul(w, a.half().cuda(), q, scale=torch.from_numpy(scale),
                                         method=method).cpu().numpy()
-            close(out, ref, 1e-3)
+            close(out, ref, mag, 1e-3)
 
 
 def _close_elem(out, ref, mag, rtol=1e-3):
