@@ -165,10 +165,13 @@ __global__ void __launch_bounds__(NW * 64) vlut_wide_kernel(VlutMatmulArgs p)
 // k-quad) and all 4 token tiles, so every activation operand read from LDS
 // feeds 4 MFMAs (the wide kernel's one-row-tile waves re-read all 64 tokens'
 // activations per 16 rows).  The workgroup issues every load of its K slice
-// up front -- activations (64 tokens x up to 1024 K, 128 KiB) into LDS, the
-// waves' weight pairs into registers -- then runs the products; the 8 waves'
+// up front -- activations (64 tokens x up to 1024 K, 128 KiB) straight into
+// LDS, the waves' weight pairs into registers -- then runs the products; the 8 waves'
 // partial tiles are summed in LDS in wave order, so a split writes one
 // partial (or, unsplit, the output) and the sums are deterministic.
+
+// 16 zero bytes, the source of activation chunks outside the matrix
+static __device__ uint4 g_vlut_zero16;
 
 template <int Q, int M, bool BF16, int FMT>
 __global__ void __launch_bounds__(kDeepNW * 64) vlut_deep_kernel(VlutMatmulArgs p)
@@ -198,20 +201,22 @@ __global__ void __launch_bounds__(kDeepNW * 64) vlut_deep_kernel(VlutMatmulArgs 
     const _Float16 f16_off = (_Float16)(1024 + bias);
     const float f32_off = (float)bias;
 
-    // activations of the workgroup's K slice: chunk c = threadIdx.x + T i is
-    // (token c / CH, local k-block c % CH); outside the matrix or the slice it
-    // is zeroed through a mask (the load itself is unconditional, clamped)
-    uint4 av[AL];
+    // activations of the workgroup's K slice, loaded straight into LDS
+    // (global_load_lds, 16 bytes a lane: lane l's chunk lands 16 l bytes after
+    // the wave's base, which is uniform because a wave's 64 chunks c =
+    // threadIdx.x + T i lie in one token row, CH = 128 chunks long).  Chunk c
+    // is (token c / CH, local k-block c % CH); outside the matrix or the slice
+    // the lane reads 16 zero bytes instead.
+    static_assert(CH % 64 == 0 && T % 64 == 0, "a wave's chunks share one token row");
 #pragma unroll
     for (int i = 0; i < AL; ++i) {
         const int c = threadIdx.x + T * i;
+        const int c0 = c - lane;
         const int tok = c / CH, kbl = c % CH;
         const int64_t kb = 4 * kq_begin + kbl;
         const bool ok = t_base + tok < p.B && kb < kb_total && kq_begin + kbl / 4 < kq_end;
-        const uint4 v = *reinterpret_cast<const uint4*>(act + (ok ? (t_base + tok) * p.K + kb * 8 : 0));
-        uint32_t m;
-        __asm__("v_mov_b32 %0, %1" : "=v"(m) : "v"(ok ? ~0u : 0u));
-        av[i] = make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
+        const uint4* src = ok ? reinterpret_cast<const uint4*>(act + (t_base + tok) * p.K + kb * 8) : &g_vlut_zero16;
+        __builtin_amdgcn_global_load_lds(src, &s_act[(c0 / CH) * kDeepStride + (c0 % CH) * 8], 16, 0, 0);
     }
     // this wave's weight pairs: row tiles rt, k-quads kq_begin + wave * kqw + j
     uint32_t w[kDeepRT][kDeepKqWave][WN];
@@ -230,11 +235,8 @@ __global__ void __launch_bounds__(kDeepNW * 64) vlut_deep_kernel(VlutMatmulArgs 
     if (FMT != VLUT_DECODED) {
         for (int i = threadIdx.x; i < 512 + p.n_coarse; i += T) s_tab[i] = p.swar[i];
     }
-#pragma unroll
-    for (int i = 0; i < AL; ++i) {
-        const int c = threadIdx.x + T * i;
-        *reinterpret_cast<uint4*>(&s_act[(c / CH) * kDeepStride + (c % CH) * 8]) = av[i];
-    }
+    // the LDS writes of global_load_lds complete with the loads (vmcnt)
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
     float4_t acc[kDeepRT][4];
