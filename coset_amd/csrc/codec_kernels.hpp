@@ -110,7 +110,7 @@ __device__ __forceinline__ void encode_level(const float x[8], int fast, int q, 
     int c[8];
     bool ok = false;
     if (fast) {
-        ok = fast_rows(x, c, in_range);
+        ok = fast_rows<true>(x, c, in_range);  // condition (5) of e8_fast.hpp: tiny and zero coordinates stay fast
         // the rows stay computed here, ahead of the fallback branch: sunk past
         // it they would keep the argmax lane masks live across the fallback's
         // code

@@ -30,6 +30,20 @@
 // so the parity of sum floor x is that of sum rint x plus the number of
 // negative d0_i.
 // NaN or infinite inputs fail (1) or (4).
+//
+// Where (3) fails (a coordinate within 2^-20 of an integer: exact zeros, and
+// every coordinate of a block with max |x_i| < 2^-20) the D8 + 1/2 candidate's
+// rounding is the reference's tie rule, which the fast path does not restate.
+// The D8 candidate, which needs only (1) and (2), is still the answer when
+//   (5) 2 - sum |d0_i| - (|adj0| - 2 adj0 d0_k) > 2^-14:
+// every point of D8 + 1/2 -- the reference's candidate with or without its
+// parity adjustment -- has half-integer coordinates, so its squared distance
+// from x is at least sum (1/2 - |d0_i|)^2 = a + 2 - sum |d0_i| (as reals,
+// |d0_i| <= 1/2 under (2)), which exceeds the adjusted D8 distance by the
+// left side of (5); the evaluation and rounding bounds of (4) apply
+// unchanged.  Callers that take (5) (CLEAR_D8) accept such blocks with the
+// D8 rows; blocks with max |x_i| < 1/8, whose every level encodes to 0, are
+// among them.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -88,6 +102,7 @@ __host__ __device__ inline bool fast_in_range(const float x[8])
     return m < kFastMaxAbs;
 }
 
+template <bool CLEAR_D8 = false>
 __host__ __device__ inline bool fast_choose(const float x[8], FastChoice& c, bool in_range)
 {
     float d0[8], d1[8];
@@ -110,7 +125,7 @@ __host__ __device__ inline bool fast_choose(const float x[8], FastChoice& c, boo
             sa += fabsf(d0[i]);
         }
     }
-    bool ok = in_range && best0 < kFastTieLimit && best1 < kFastTieLimit;
+    const bool tie0 = best0 < kFastTieLimit, tie1 = best1 < kFastTieLimit;  // (2), (3)
 
     // first index of the largest |d| (torch.argmax)
     float xk0 = x[0], xk1 = x[0];
@@ -138,11 +153,18 @@ __host__ __device__ inline bool fast_choose(const float x[8], FastChoice& c, boo
     c.adj1 = odd1 ? ((tk1 >= 0.f && dk1 > 0.f) ? 1.f : -1.f) : 0.f;
 
     // b - a, with (d - adj)^2 - d^2 = adj^2 - 2 adj d and adj^2 = |adj|
-    const float diff =
-        (2.f - sa) + (fmaf(-2.f * c.adj1, ek1, fabsf(c.adj1)) - fmaf(-2.f * c.adj0, dk0, fabsf(c.adj0)));
+    const float base = 2.f - sa;
+    const float t0 = fmaf(-2.f * c.adj0, dk0, fabsf(c.adj0));
+    const float diff = base + (fmaf(-2.f * c.adj1, ek1, fabsf(c.adj1)) - t0);
     const bool pick0 = diff > kFastDistGap;
     c.pick0 = lanes_of(pick0);
-    return ok && (pick0 || diff < -kFastDistGap);
+    const bool decided = tie1 && (pick0 || diff < -kFastDistGap);
+    if constexpr (CLEAR_D8) {
+        // (5); it implies pick0: the adj1 term is >= 0 (ek1 in [-1/2, 1/2)),
+        // so diff >= base - t0 in rounded arithmetic too
+        return in_range && tie0 && (decided || base - t0 > kFastDistGap);
+    }
+    return in_range && tie0 && decided;
 }
 
 // The chosen candidate's worst coordinate, as a lane mask.
@@ -176,11 +198,13 @@ __host__ __device__ inline bool project_fast(const float x[8], float y[8])
 //   (G^-1 y)_7 = 2 Y_7 (+ 1 on the coset)
 // all exact in int32 under condition (1).  The adjustment enters the sums
 // through the single term j = k.  Returns false exactly when project_fast
-// does (in_range = fast_in_range(x)); rows are then unspecified.
+// does (in_range = fast_in_range(x)), or with CLEAR_D8 when neither (3) nor
+// (5) decides the block; rows are then unspecified.
+template <bool CLEAR_D8 = false>
 __host__ __device__ inline bool fast_rows(const float x[8], int rows[8], bool in_range)
 {
     FastChoice c;
-    const bool ok = fast_choose(x, c, in_range);
+    const bool ok = fast_choose<CLEAR_D8>(x, c, in_range);
     const bool pick0 = lane_in(c.pick0);
     const uint32_t adj = (uint32_t)(int)(pick0 ? c.adj0 : c.adj1);
     uint32_t Y[8];

@@ -4,9 +4,9 @@ encoder's project_fast and the decoders' project_dyadic.
 The header is compiled for the host (tests/fastpath/Makefile) and checked
 against the C oracle's projection: exhaustively for the rounding lemma it
 rests on (every float below 2^22), with a looser tie limit as the negative
-control that must fail, and bit for bit on blocks from seven input families
+control that must fail, and bit for bit on blocks from eight input families
 (Gaussian at eight scales, dyadic grids, near-ties, points on the boundary
-between the two D8 cosets, specials, uniform)."""
+between the two D8 cosets, specials, uniform, tiny and sparse blocks)."""
 import os
 import shutil
 import subprocess
@@ -44,13 +44,19 @@ def test_rounding_lemma_fails_at_the_tie(checker):
 
 
 def test_fast_projection_matches_oracle(checker):
+    """Both forms of the fast path: the strict one (conditions (1)-(4)) and
+    the generic encoder's, which also takes blocks that condition (5)
+    decides for the D8 candidate (tiny blocks, exact zeros)."""
     rc, out = run(checker, "blocks", "300000", "11")
     assert rc == 0, out
-    rates = {int(l.split()[1].rstrip(":")): float(l.split("(")[1].split("%")[0])
-             for l in out.splitlines() if l.startswith("family")}
-    assert len(rates) == 7
+    lines = [l for l in out.splitlines() if l.startswith("family")]
+    rates = {int(l.split()[1].rstrip(":")): float(l.split("(")[1].split("%")[0]) for l in lines}
+    rates5 = {int(l.split()[1].rstrip(":")): float(l.split("(")[3].split("%")[0]) for l in lines}
+    assert len(rates) == 8
     assert rates[6] > 99.0, out   # uniform box: almost always fast
     assert rates[4] > 10.0, out   # near coset boundaries: many decided, the rest fall back
+    assert all(rates5[f] >= rates[f] for f in rates), out
+    assert rates[7] < 20.0 and rates5[7] > 90.0, out   # tiny and sparse blocks: (5) decides them
 
 
 @pytest.mark.parametrize("q,n", [(2, 1 << 20), (4, 1 << 20), (8, 1 << 24), (16, 1000000)])

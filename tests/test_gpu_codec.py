@@ -261,6 +261,56 @@ def test_fast_projection_same_codes(ca, path, q, M):
     np.testing.assert_array_equal(outs[0], ref)
 
 
+def _tiny_and_sparse_blocks(rng, n):
+    """Blocks whose coordinates sit within 2^-20 of an integer: tiny blocks
+    (every level encodes to 0), exact and signed zeros, and zeros among
+    ordinary values -- the fast path's condition (3) fails on all of them."""
+    scales = np.array([0.12, 1e-2, 1e-4, 1e-6, 9.5e-7, 1e-9, 1e-20, 1e-38, 1e-44], dtype=np.float32)
+    tiny = np.clip(rng.standard_normal((n, 8)).astype(np.float32)
+                   * scales[rng.integers(0, len(scales), n)][:, None], -0.124, 0.124).astype(np.float32)
+    zeros = np.where(rng.random((n, 8)) < 0.5, np.float32(0.0), np.float32(-0.0)).astype(np.float32)
+    sparse = np.where(rng.random((n, 8)) < 0.6, np.float32(0.0),
+                      rng.standard_normal((n, 8)).astype(np.float32) * 3).astype(np.float32)
+    near = np.round(rng.standard_normal((n, 8)) * 4).astype(np.float32)
+    near += (rng.standard_normal((n, 8)) * 1e-7).astype(np.float32)
+    return np.concatenate([tiny, zeros, sparse, near]).astype(np.float32)
+
+
+@pytest.mark.parametrize("q,M", [(4, 2), (16, 3), (2, 4), (3, 2)])
+def test_tiny_and_sparse_blocks(ca, path, q, M):
+    """The encoders' fast path with condition (5) (tiny blocks and exact
+    zeros decided for the D8 candidate) gives the oracle's codes and decoded
+    values, the same as the reference operation sequence; in the codec and
+    in the layer convention (W * beta_row, the degenerate C5 setting of
+    W ~ N(0, 0.02) with a small beta among the rows)."""
+    from coset_amd import _lib
+    rng = np.random.default_rng(23 + q + M)
+    x = _tiny_and_sparse_blocks(rng, 3000)
+    xd = dev(x)
+    try:
+        outs = []
+        for fast in (True, False):
+            _lib.set_fast_projection(fast)
+            pk, out = ca.hnlq_roundtrip(xd, q, M, 1.0)
+            outs.append((words(pk), host(out)))
+    finally:
+        _lib.set_fast_projection(True)
+    codes = O.e8_encode(x, q, M)
+    np.testing.assert_array_equal(outs[0][0], O.pack_words(codes, q).reshape(outs[0][0].shape))
+    np.testing.assert_array_equal(outs[0][1].reshape(-1, 8), O.e8_decode(codes, q, M).reshape(-1, 8))
+    np.testing.assert_array_equal(outs[0][0], outs[1][0])
+    np.testing.assert_array_equal(outs[0][1], outs[1][1])
+
+    rows, cols = 64, 512
+    W = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+    W[::5, ::3] = 0.0
+    beta = np.exp(rng.uniform(np.log(1e-6), np.log(40.0), size=rows)).astype(np.float32)
+    Wq, qraw, lcodes = O.layer_quant(W, beta, q, M, 2.0)
+    pk, out = ca.hnlq_roundtrip(dev(W), q, M, beta_row=dev(beta), blocks_per_row=cols // 8, clip=2.0)
+    np.testing.assert_array_equal(host(out).reshape(rows, cols), Wq)
+    np.testing.assert_array_equal(words(pk), O.pack_words(lcodes, q).reshape(-1, M))
+
+
 @pytest.mark.parametrize("dynamic", [True, False])
 @pytest.mark.parametrize("beta,extra", [(1.0, 0), (0.25, 3), (0.3, 1), (1.0, 2)])
 def test_roundtrip_with_float_codes(ca, path, beta, extra, dynamic):
