@@ -16,6 +16,8 @@ The other BASELINE configurations are measured alongside under "extra":
   c4  vLUT matmul of 4096 x 4096 q4 M2 codes with fp16 activations, B = 1, 8, 64
       (core and legacy-Q residuals, tiled prepared and raw words, LDS-table method)
   c5  QAT linear forward + backward, BERT-base shapes, 4096 bf16 tokens
+  peaks  the spec peaks checked on the box: a 1 GiB device copy and a bf16
+      8192^3 GEMM through torch.mm
 The roofline object is the C2 codec kernel's (HIP events on its launch
 stream).  cpu_baseline is the C restatement of the reference algorithm
 (oracle/) on the host: every configuration is timed on all the host threads
@@ -86,6 +88,7 @@ def gpu_time(torch, fn, steps, warmup, warm_s=0.0):
 # duration of each C call, so a thread pool runs the chunks in parallel.
 # ---------------------------------------------------------------------------
 CPU_THREAD_CAP = 16            # one GPU's share of the box's cores
+CPU_REPS = 5                   # timed runs per figure (median), after one untimed run
 
 
 def cpu_model() -> str:
@@ -143,13 +146,14 @@ def cpu_c2(x_host: np.ndarray, one_thread_blocks: int):
     def tasks(xs):
         return [lambda c=xs[i:i + chunk]: O.e8_decode(O.e8_encode(c, 4, 2, 1.0), 4, 2, 1.0)
                 for i in range(0, xs.shape[0], chunk)]
-    t_all = _cpu_time(lambda: tasks(x_host), thr, 1)
+    t_all = _cpu_time(lambda: tasks(x_host), thr, CPU_REPS)
     xs1 = x_host[:one_thread_blocks]
-    t_one = _cpu_time(lambda: tasks(xs1), 1, 1)
+    t_one = _cpu_time(lambda: tasks(xs1), 1, CPU_REPS)
     return _cpu_record(n / t_all / 1e9, xs1.shape[0] / t_one / 1e9, "Gblocks/s", thr,
                        f"all {n} C2 blocks on {thr} threads ({t_all:.2f} s); the first {xs1.shape[0]} "
                        f"on one thread ({t_one:.2f} s)",
-                       "C oracle encode+decode in 2^20-block chunks, median of 1 run after 1 untimed run",
+                       f"C oracle encode+decode in 2^20-block chunks, median of {CPU_REPS} runs after 1 untimed "
+                       "run",
                        chunk_blocks=chunk)
 
 
@@ -164,13 +168,14 @@ def cpu_c3(x_host: np.ndarray, beta_host: np.ndarray, rows_one: int):
     def tasks(r1):
         return [lambda r=r: O.layer_quant(x_host[r:r + step], beta_host[r:r + step], 16, 3, 2.0)
                 for r in range(0, r1, step)]
-    t_all = _cpu_time(lambda: tasks(rows), thr, 1)
-    t_one = _cpu_time(lambda: tasks(rows_one), 1, 1)
+    t_all = _cpu_time(lambda: tasks(rows), thr, CPU_REPS)
+    t_one = _cpu_time(lambda: tasks(rows_one), 1, CPU_REPS)
     n_all, n_one = rows * cols // 8, rows_one * cols // 8
     return _cpu_record(n_all / t_all / 1e9, n_one / t_one / 1e9, "Gblocks/s", thr,
                        f"all {n_all} C3 blocks on {thr} threads ({t_all:.2f} s); {n_one} blocks "
                        f"({rows_one} rows) on one thread ({t_one:.2f} s)",
-                       "C oracle layer quantizer (fp32 upcast of the bf16 input) in 64-row chunks",
+                       f"C oracle layer quantizer (fp32 upcast of the bf16 input) in 64-row chunks, median of "
+                       f"{CPU_REPS} runs after 1 untimed run",
                        chunk_blocks=step * cols // 8)
 
 
@@ -191,13 +196,14 @@ def cpu_c4(words_host: np.ndarray, act_host: np.ndarray):
         return [lambda t=t, k0=k0: O.vlut_onesided_rows(words_host, R, act_host[t], 4, k0, min(kb, k0 + kstep))
                 for t in range(tokens) for k0 in range(0, kb, kstep)]
 
-    t_all = _cpu_time(lambda: tasks(B), thr, 1)
-    t_one = _cpu_time(lambda: [lambda: O.vlut_onesided_rows(words_host, R, act_host[0], 4)], 1, 1)
+    t_all = _cpu_time(lambda: tasks(B), thr, CPU_REPS)
+    t_one = _cpu_time(lambda: [lambda: O.vlut_onesided_rows(words_host, R, act_host[0], 4)], 1, CPU_REPS)
     return _cpu_record(B / t_all, 1 / t_one, "tokens/s", thr,
                        f"B={B}: all {B} tokens on {thr} threads ({t_all:.2f} s); one token on one thread "
                        f"({t_one:.2f} s)",
                        "C oracle one-sided vLUT (q^8 table per 8-wide activation block, residuals computed "
-                       "once) + lookup sum, fp32 tables, float64 row sums")
+                       f"once) + lookup sum, fp32 tables, float64 row sums, median of {CPU_REPS} runs after 1 "
+                       "untimed run")
 
 
 def cpu_c5(fin: int, fout: int, W: np.ndarray, beta: np.ndarray, x: np.ndarray, gy: np.ndarray):
@@ -236,15 +242,15 @@ def cpu_c5(fin: int, fout: int, W: np.ndarray, beta: np.ndarray, x: np.ndarray, 
         return float(np.median(ts))
     n_threads_before = torch.get_num_threads()
     try:
-        t_all = timed(thr, 3)
-        t_one = timed(1, 1)
+        t_all = timed(thr, CPU_REPS)
+        t_one = timed(1, CPU_REPS)
     finally:
         torch.set_num_threads(n_threads_before)
     return _cpu_record(4096 / t_all, 4096 / t_one, "tokens/s", thr,
                        f"{fin}x{fout}, 4096 fp32 tokens: {t_all * 1e3:.1f} ms per step on {thr} threads, "
                        f"{t_one * 1e3:.1f} ms on one",
                        "C oracle weight quantizer + torch CPU fp32 products + closed-form STE backward "
-                       "(numpy float64), median of 3 (all threads) / 1 (one thread) after 1 untimed step")
+                       f"(numpy float64), median of {CPU_REPS} steps after 1 untimed step")
 
 
 def cpu_c1(W: np.ndarray, beta: np.ndarray, x: np.ndarray, bias: np.ndarray):
@@ -476,6 +482,57 @@ def cold_time(torch, fn, flush, reps=25):
     return float(np.median([a.elapsed_time(b) for a, b in evs])) / 1e3
 
 
+def median_call_time(torch, fn, reps=25, warm_s=0.1):
+    """Median GPU seconds of single calls of fn (HIP events around each call,
+    all calls queued back to back), after warm_s seconds of untimed calls."""
+    t_warm = time.perf_counter()
+    while time.perf_counter() - t_warm < warm_s:
+        fn()
+        torch.cuda.synchronize()
+    evs = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        evs.append((e0, e1))
+    torch.cuda.synchronize()
+    return float(np.median([a.elapsed_time(b) for a, b in evs])) / 1e3
+
+
+def bench_peaks(torch, ca, args):
+    """The spec peaks checked on this GPU: a STREAM-like copy of 1 GiB (four
+    times the 256 MB Infinity Cache, so HBM serves it) through the runtime's
+    device copy, and a bf16 8192^3 GEMM through torch.mm (the BLAS library
+    torch is configured with, named in the record)."""
+    n = 1 << 28
+    src = torch.empty(n, dtype=torch.float32, device="cuda").normal_()
+    dst = torch.empty_like(src)
+    t_copy = median_call_time(torch, lambda: dst.copy_(src))
+    copy_gbs = 2 * n * 4 / t_copy / 1e9
+    del src, dst
+    torch.cuda.empty_cache()
+    g = torch.Generator(device="cuda").manual_seed(11)
+    s = 8192
+    a = torch.randn((s, s), device="cuda", generator=g).to(torch.bfloat16)
+    b = torch.randn((s, s), device="cuda", generator=g).to(torch.bfloat16)
+    c = torch.empty((s, s), device="cuda", dtype=torch.bfloat16)
+    t_mm = median_call_time(torch, lambda: torch.mm(a, b, out=c))
+    tflops = 2.0 * s ** 3 / t_mm / 1e12
+    del a, b, c
+    try:
+        blas = str(torch.backends.cuda.preferred_blas_library())
+    except Exception:   # older torch without the query
+        blas = "default"
+    return {"copy": {"bytes": 2 * n * 4, "us": round(t_copy * 1e6, 1), "gbs": round(copy_gbs, 1),
+                     "frac_of_spec": round(copy_gbs / HBM_PEAK_GBS, 4),
+                     "what": "1 GiB fp32 device-to-device copy (read + write), median of 25"},
+            "gemm_bf16": {"shape": [s, s, s], "us": round(t_mm * 1e6, 1), "tflops": round(tflops, 1),
+                          "frac_of_spec": round(tflops / BF16_MFMA_TFLOPS, 4), "blas": blas,
+                          "what": "torch.mm bf16 8192^3, fp32 accumulation, median of 25"},
+            "spec": {"hbm_gbs": HBM_PEAK_GBS, "bf16_mfma_tflops": BF16_MFMA_TFLOPS}}
+
+
 C4_CODE_BYTES = 4096 * 512 * 2 * 2      # uint16 level words [4096, 512, 2]: the algorithmic weight bytes
 
 
@@ -578,7 +635,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", dest="cpu", action="store_false",
                     help="skip the host-CPU baselines (the C oracle on the host cores)")
-    ap.add_argument("--only", default="c1,c2,c2codes,c2api,c3,c4,c5", help="comma list of workloads to run")
+    ap.add_argument("--only", default="c1,c2,c2codes,c2api,c3,c4,c5,peaks",
+                    help="comma list of workloads to run")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 512 MiB device copy (HBM counter calibration)")
     args = ap.parse_args()
@@ -606,7 +664,7 @@ def main():
     if "c2" in only:
         kernel_s, wall_s, cpu = bench_c2(torch, ca, args)
     for name, fn in (("c1", bench_c1), ("c2codes", bench_c2_codes), ("c2api", bench_c2_api), ("c3", bench_c3),
-                     ("c4", bench_c4), ("c5", bench_c5)):
+                     ("c4", bench_c4), ("c5", bench_c5), ("peaks", bench_peaks)):
         if name in only:
             extra[name] = fn(torch, ca, args)
             torch.cuda.empty_cache()
