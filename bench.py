@@ -543,6 +543,7 @@ def bench_c4(torch, ca, args):
     tiled = ca.vlut_prepare(words, 4)   # once per weight: cid << 16 | idx in fragment order, 16 MiB
     tiled_legacy = ca.vlut_prepare(words, 4, legacy=True)   # the reference vLUT's textbook-Q residuals
     decoded = ca.vlut_prepare(words, 4, layout="decoded")    # 2 x_hat bytes in fragment order, 16 MiB
+    pairs = ca.vlut_prepare(words, 4, layout="pairs")        # coordinate-pair ids in fragment order, 16 MiB
     scale = torch.full((4096,), 0.02, device="cuda")
     del W
     res = {"workload": "C4 vLUT matmul 4096x4096 q4 M2 codes (8 MiB uint16 words; 16 MiB tiled prepared or "
@@ -559,7 +560,7 @@ def bench_c4(torch, ca, args):
         a = torch.randn((B, 4096), device="cuda", generator=g).to(torch.float16)
         row = {}
         for method, wts in (("mfma", tiled), ("mfma_decoded", decoded), ("mfma_legacy_q", tiled_legacy),
-                            ("mfma_raw_words", words), ("lds", tiled)):
+                            ("mfma_raw_words", words), ("lds", pairs), ("lds_tiled", tiled)):
             m = "mfma" if method.startswith("mfma") else "lds"
             fn = lambda: ca.vlut_matmul(wts, a, 4, scale=scale, method=m, workspace=ws)
             k_eager, _ = gpu_time(torch, fn, 50 if m == "lds" else 100, 5, 0.05)

@@ -620,7 +620,7 @@ int coset_lsq_bwd(const void* x, const void* g, int dtype, int64_t n, const floa
 
 int64_t coset_vlut_prepared_words(int64_t rows, int64_t kb, int M, int word_format)
 {
-    if (rows < 0 || kb < 0 || M < 1 || word_format < 0 || word_format > 3) return 0;
+    if (rows < 0 || kb < 0 || M < 1 || word_format < 0 || word_format > 4) return 0;
     return coset::vlut_prepared_words(rows, kb, M, word_format);
 }
 
@@ -630,7 +630,7 @@ int coset_vlut_prepare(const void* words, int64_t rows, int64_t kb, int M, int q
     if (q != 2 && q != 4) return fail(COSET_EUNSUPPORTED, "vLUT prepare supports q = 2 or 4 (got %d)", q);
     if (rows < 0 || kb < 0 || M < 1 || M > 4) return fail(COSET_EINVAL, "bad shape rows=%lld kb=%lld M=%d",
                                                          (long long)rows, (long long)kb, M);
-    if (word_format < 1 || word_format > 3) return fail(COSET_EINVAL, "prepared word_format must be 1, 2 or 3");
+    if (word_format < 1 || word_format > 4) return fail(COSET_EINVAL, "prepared word_format must be 1, 2, 3 or 4");
     if (word_format == 3 && !((q == 4 && M <= 2) || (q == 2 && M <= 4)))
         return fail(COSET_EUNSUPPORTED, "decoded format needs |2 x_hat| <= 127: q = 4 with M <= 2 or q = 2 with M <= 4");
     if (rows * kb > 0 && (!words || !prepared)) return fail(COSET_EINVAL, "NULL buffer");
@@ -654,6 +654,11 @@ static int vlut_matmul_impl(const void* words, int word_format, const float* sca
     if (act_dtype != COSET_F32 && act_dtype != COSET_BF16 && act_dtype != COSET_F16)
         return fail(COSET_EINVAL, "activation dtype %d", act_dtype);
     if (scale_mode != 0 && scale_mode != 1) return fail(COSET_EINVAL, "scale_mode must be 0 or 1");
+    if (word_format == coset::VLUT_PAIRS) {  // read by the LDS-table method only
+        if (method == coset::VLUT_METHOD_MFMA)
+            return fail(COSET_EUNSUPPORTED, "the pairs format is read by the LDS-table method (1) only");
+        if (method == coset::VLUT_METHOD_AUTO) method = coset::VLUT_METHOD_LDS;
+    }
     int m = vlut_method(method, act_dtype, q, M);
     if (m < 0) return fail(COSET_EUNSUPPORTED, "MFMA method needs fp16/bf16 activations holding 2*x_hat exactly");
     if (m != coset::VLUT_METHOD_LDS && m != coset::VLUT_METHOD_MFMA) return fail(COSET_EINVAL, "unknown method %d", method);
@@ -666,7 +671,7 @@ static int vlut_matmul_impl(const void* words, int word_format, const float* sca
         return fail(COSET_EINVAL, "workspace holds %lld floats, needs %lld", (long long)workspace_floats,
                     (long long)need);
     if (need > 0 && !workspace) return fail(COSET_EINVAL, "NULL workspace");
-    if (word_format < 0 || word_format > 3) return fail(COSET_EINVAL, "word_format must be 0, 1, 2 or 3");
+    if (word_format < 0 || word_format > 4) return fail(COSET_EINVAL, "word_format must be 0, 1, 2, 3 or 4");
     if (word_format == 3 && plan.kernel != coset::VK_MFMA_ROWS && plan.kernel != coset::VK_MFMA_WIDE &&
         plan.kernel != coset::VK_MFMA_DEEP)
         return fail(COSET_EUNSUPPORTED, "the decoded format runs on the matrix-core rows kernel only (fp16/bf16 activations)");
@@ -720,7 +725,8 @@ int coset_vlut_matmul_noalloc(const void* words, int word_format, const float* s
         ws = g_scratch_ptr[dev];
     }
     if (!ws) return fail(COSET_EINVAL, "coset_vlut_matmul_noalloc: call coset_init(%d) on this device first", dev);
-    const int m = vlut_method(method, act_dtype, q, M);
+    const bool pairs_auto = word_format == coset::VLUT_PAIRS && method == coset::VLUT_METHOD_AUTO;
+    const int m = vlut_method(pairs_auto ? coset::VLUT_METHOD_LDS : method, act_dtype, q, M);
     if (m >= 0 && B > 0 && rows > 0 && K >= 8 && q >= 2 && q <= 4 && M >= 1 && M <= 4) {
         const int64_t need = coset::vlut_workspace_floats(coset::vlut_plan(rows, B, K, q, M, m), B, rows);
         if (need > kNoallocScratchFloats)

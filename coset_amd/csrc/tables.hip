@@ -6,7 +6,9 @@
 // tables store, per rule (core / legacy):
 //   cid_map[idx]  uint16 id of c(b)
 //   coarse[cid]   the 8 coordinates 2c as int8, packed in a uint64
-// so 2r = 2Gb - q*(2c) needs two small lookups instead of a projection.  They
+// so 2r = 2Gb - q*(2c) needs two small lookups instead of a projection,
+// plus the byte-lane form of the same sum (build_swar) and the coordinate
+// pairs of r with their ids per word (build_pairs, the LDS vLUT's tables).  They
 // are built once per device: a kernel evaluates c(b) for all q^8 words with
 // the same device projection the codec uses, the host assigns dense ids in
 // increasing key order, and the result is uploaded and kept for the life of
@@ -127,6 +129,37 @@ void build_swar(int q, uint32_t n, const std::vector<uint16_t>& map, const std::
     }
 }
 
+// Dense ids of the four coordinate pairs of 2r = U(b) - q (2c) over all
+// words, in increasing (2r_2p, 2r_2p+1) order per pair, and their values r.
+bool build_pairs(int q, uint32_t n, const std::vector<uint16_t>& map, const std::vector<uint64_t>& coarse,
+                 std::vector<uint32_t>& pair_map, std::vector<float2>& vals, int count[4])
+{
+    std::vector<std::array<int, 8>> r2(n);
+    for (uint32_t i = 0; i < n; ++i) {
+        int u[8];
+        two_gb(i, q, u);
+        for (int j = 0; j < 8; ++j) r2[i][j] = u[j] - q * (int)(int8_t)(uint8_t)(coarse[map[i]] >> (8 * j));
+    }
+    pair_map.assign(n, 0u);
+    vals.assign(4 * kPairSlots, make_float2(0.f, 0.f));
+    for (int p = 0; p < 4; ++p) {
+        std::vector<std::pair<int, int>> keys(n);
+        for (uint32_t i = 0; i < n; ++i) keys[i] = {r2[i][2 * p], r2[i][2 * p + 1]};
+        std::vector<std::pair<int, int>> uniq(keys);
+        std::sort(uniq.begin(), uniq.end());
+        uniq.erase(std::unique(uniq.begin(), uniq.end()), uniq.end());
+        if (uniq.size() > (size_t)kPairSlots) return false;
+        count[p] = (int)uniq.size();
+        for (size_t k = 0; k < uniq.size(); ++k)
+            vals[kPairSlots * p + k] = make_float2(0.5f * (float)uniq[k].first, 0.5f * (float)uniq[k].second);
+        for (uint32_t i = 0; i < n; ++i) {
+            const uint32_t id = (uint32_t)(std::lower_bound(uniq.begin(), uniq.end(), keys[i]) - uniq.begin());
+            pair_map[i] |= id << (8 * p);
+        }
+    }
+    return true;
+}
+
 struct Slot {
     std::once_flag once;
     DecodeTables t{};
@@ -149,6 +182,8 @@ hipError_t build(int device, int q, int legacy, DecodeTables* out)
     std::vector<uint32_t> keys(n);
     std::vector<uint16_t> map(n);
     std::vector<uint64_t> coarse, swar;
+    std::vector<uint32_t> pair_map;
+    std::vector<float2> pair_vals;
     if ((e = hipMalloc(&d_keys, n * sizeof(uint32_t))) != hipSuccess) goto done;
     if (legacy)
         hipLaunchKernelGGL(coarse_key_kernel<true>, dim3((n + 255) / 256), dim3(256), 0, nullptr, q, n, d_keys);
@@ -177,6 +212,10 @@ hipError_t build(int device, int q, int legacy, DecodeTables* out)
         }
     }
     build_swar(q, n, map, coarse, swar, &out->swar_max_m, out->swar_bias);
+    if (!build_pairs(q, n, map, coarse, pair_map, pair_vals, out->pair_count)) {
+        e = hipErrorInvalidValue;
+        goto done;
+    }
     out->q = q;
     out->n_codes = n;
     out->n_coarse = (int)coarse.size();
@@ -186,7 +225,15 @@ hipError_t build(int device, int q, int legacy, DecodeTables* out)
     if ((e = hipMemcpy((void*)out->cid_map, map.data(), n * sizeof(uint16_t), hipMemcpyHostToDevice)) != hipSuccess) goto done;
     if ((e = hipMemcpy((void*)out->swar, swar.data(), swar.size() * sizeof(uint64_t), hipMemcpyHostToDevice)) != hipSuccess)
         goto done;
-    e = hipMemcpy((void*)out->coarse, coarse.data(), coarse.size() * sizeof(uint64_t), hipMemcpyHostToDevice);
+    if ((e = hipMemcpy((void*)out->coarse, coarse.data(), coarse.size() * sizeof(uint64_t), hipMemcpyHostToDevice)) !=
+        hipSuccess)
+        goto done;
+    if ((e = hipMalloc((void**)&out->pair_map, n * sizeof(uint32_t))) != hipSuccess) goto done;
+    if ((e = hipMalloc((void**)&out->pair_vals, pair_vals.size() * sizeof(float2))) != hipSuccess) goto done;
+    if ((e = hipMemcpy((void*)out->pair_map, pair_map.data(), n * sizeof(uint32_t), hipMemcpyHostToDevice)) !=
+        hipSuccess)
+        goto done;
+    e = hipMemcpy((void*)out->pair_vals, pair_vals.data(), pair_vals.size() * sizeof(float2), hipMemcpyHostToDevice);
 done:
     if (d_keys) (void)hipFree(d_keys);
     if (cur != device) (void)hipSetDevice(cur);

@@ -7,6 +7,7 @@
 namespace coset {
 
 constexpr int kMaxCoarse = 1024;  // distinct coarse points c(b) per table (637 for q = 4)
+constexpr int kPairSlots = 72;    // distinct values of one coordinate pair of r (<= 70 for q = 4)
 
 struct DecodeTables {
     int q;
@@ -26,6 +27,15 @@ struct DecodeTables {
     const uint64_t* swar;     // [512 + n_coarse]
     int swar_max_m;           // largest M whose combined bytes stay < 256 (0: none)
     int swar_bias[5];         // byte offset of 2 x_hat after combining M levels
+    // Coordinate-pair form of r: the pairs (r_2p, r_2p+1), p = 0..3, take few
+    // distinct values (70, 68, 68, 55 for q = 4, core rule).
+    //   pair_map[idx]            byte p = id of the word's pair p
+    //   pair_vals[72 p + id]     that pair's two coordinates of r (zero past
+    //                            pair_count[p])
+    // so <a, r> = sum_p <(a_2p, a_2p+1), pair_vals[72 p + id_p]>.
+    const uint32_t* pair_map;   // [n_codes]
+    const float2* pair_vals;    // [4 * kPairSlots]
+    int pair_count[4];
 };
 
 // Tables of the core (legacy = 0) or legacy residual rule for q in {2, 4} on

@@ -12,13 +12,15 @@
 //   vlut_build_kernel      full one-sided tables, one thread per entry
 //   vlut_dot_kernel        sum_m q^m vLUT[idx_m] over encoded blocks
 //   vlut_lds_kernel        matmul out[t,o] = s_o sum_k sum_m q^m vLUT_{a_tk}[idx]
-//                          with per-(token, k-block) factorized tables in LDS:
-//                            vLUT_a[idx(b)] = sum_j b_j <a, g_j> - q <a, c(b)>
-//                          (8 + n_coarse floats instead of q^8 = 65536 at q = 4)
+//                          with per-(token, k-block) tables in LDS, factorized
+//                          over the coordinate pairs of r:
+//                            vLUT_a[idx(b)] = sum_p <(a_2p, a_2p+1), r_p(b)>
+//                          (289 floats instead of q^8 = 65536 at q = 4)
 //   vlut_mfma_kernel       same product by decoding 2 x_hat (exact in fp16/bf16)
 //                          into LDS and multiplying on the matrix cores
 //                          (for (q, M) whose byte tables would overflow)
-//   vlut_reduce_kernel     sums the split-K partials and applies s_o
+//   vlut_reduce_kernel     sums the split-K partials and applies s_o (the
+//                          _sm kernels: split-major partials, summed in order)
 // The byte-table matrix-core kernels live in vlut_rows.hip (up to 32 tokens)
 // and vlut_wide.hip (wide and deep kernels, more tokens), with the helpers
 // they share in vlut_mfma.hpp.
@@ -39,6 +41,21 @@ __device__ __forceinline__ float load_act(const void* p, int dt, int64_t i)
     uint16_t h = reinterpret_cast<const uint16_t*>(p)[i];
     if (dt == DT_BF16) return __uint_as_float((uint32_t)h << 16);
     return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// load_act in two steps, so the load can be issued ahead of others and
+// converted once they are in flight: the element's bits, then its value.
+__device__ __forceinline__ uint32_t load_act_bits(const void* p, int dt, int64_t i)
+{
+    if (dt == DT_F32) return reinterpret_cast<const uint32_t*>(p)[i];
+    return reinterpret_cast<const uint16_t*>(p)[i];
+}
+
+__device__ __forceinline__ float act_value(uint32_t bits, int dt)
+{
+    if (dt == DT_F32) return __uint_as_float(bits);
+    if (dt == DT_BF16) return __uint_as_float(bits << 16);
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
 }
 
 // 2 r(b) from the level word with the decode tables: U - q*(2c), U = 2Gb.
@@ -72,15 +89,22 @@ __device__ __forceinline__ void load_word(const VlutMatmulArgs& p, int64_t i, ui
 }
 
 // One thread per output word: the raw word of (row, kb, m) or, past the
-// matrix in the tiled format, the word 0 (which decodes to 0).
+// matrix in the tiled formats, the word 0 (which decodes to 0), stored as
+// cid << 16 | word, or as its pair ids (VLUT_PAIRS).
 __global__ void __launch_bounds__(256) vlut_prepare_kernel(const uint16_t* words, int64_t rows, int64_t kb_total,
                                                           int M, int fmt, int64_t n_out, const uint16_t* map,
-                                                          uint32_t mask, uint32_t* out)
+                                                          const uint32_t* pair_map, uint32_t mask, uint32_t* out)
 {
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n_out) return;
     uint32_t w = 0;
-    if (fmt == VLUT_TILED) {
+    if (fmt == VLUT_PAIRS) {  // [rows / 64][kb][M][64 rows]
+        const int64_t rest = i >> 6;
+        const int m = (int)(rest % M);
+        const int64_t kb = (rest / M) % kb_total;
+        const int64_t row = (rest / M / kb_total) * 64 + (i & 63);
+        if (row < rows) w = words[(row * kb_total + kb) * M + m];
+    } else if (fmt == VLUT_TILED) {
         const int m = (int)(i % M);
         const int64_t e = i / M;  // entry
         const int lane = (int)(e & 63);
@@ -93,7 +117,7 @@ __global__ void __launch_bounds__(256) vlut_prepare_kernel(const uint16_t* words
         w = words[i];
     }
     w &= mask;  // q^8 - 1: map bounds for any input
-    out[i] = ((uint32_t)map[w] << 16) | w;
+    out[i] = fmt == VLUT_PAIRS ? pair_map[w] : ((uint32_t)map[w] << 16) | w;
 }
 
 // ---------------------------------------------------------------- build
@@ -148,107 +172,169 @@ __global__ void __launch_bounds__(256) vlut_dot_kernel(const void* words, int wo
 }
 
 // ---------------------------------------------------------------- LDS vLUT matmul
-constexpr int kVlutThreads = 256;
-constexpr int kVlutRowsPerThread = 2;
-constexpr int kVlutMaxTables = 24;  // TT * KBW
-constexpr int kVlutTableFloats = kVlutMaxTables * (8 + kMaxCoarseVlut);
+// out[t, o] = s_o sum_k sum_m q^m <a_tk, r(b_okm)>, the inner products read
+// from per-(token, k-block) tables in LDS.  The coordinate pairs of r take
+// few values (tables.hpp: pair_vals), so one table is four sub-tables
+//   T[72 p + id] = a_2p r_2p(id) + a_2p+1 r_2p+1(id)     p = 0..3
+// (289 floats; 261 used at q = 4) and a level word costs four lookups:
+//   vLUT_a[idx(b)] = <a, r(b)> = sum_p T[72 p + id_p(b)].
+// Workgroup: 4 waves x 2 tiles of 64 rows (512 rows) x a K range (grid.y
+// splits) x TT tokens (grid.z); a lane owns one row of each of its wave's
+// tiles.  Every lookup instruction of a wave reads one sub-table (one token,
+// one k-block), 72 entries over the LDS banks, so its 64 lanes conflict only
+// where two ids 64 apart meet; lanes with the same id share the read.  The
+// K range runs in chunks of KB k-blocks: the chunk's activations and level
+// words are loaded (the words as pair ids; one 256-byte read per wave and
+// word in the pairs format), the activations staged and the tables built
+// while the word loads are in flight, then the tables are read.
+constexpr int kLdsWaves = 4;
+constexpr int kLdsTiles = 2;                          // 64-row tiles per wave
+constexpr int kLdsRows = kLdsWaves * kLdsTiles * 64;  // rows per workgroup
+constexpr int kLdsTable = 4 * kPairSlots + 1;         // floats per (token, k-block) table
 
-template <int Q, int M, int TT>
-__global__ void __launch_bounds__(kVlutThreads) vlut_lds_kernel(VlutMatmulArgs p)
+template <int TT>
+struct LdsChunk {
+    static constexpr int KB = TT >= 8 ? 4 : 8;  // k-blocks per chunk
+};
+
+// PAIRS: the weight is in the pairs format; otherwise the level words
+// (raw, row-major or tiled) are loaded first and their pair ids gathered
+// from pair_map after, each phase issued whole (no load waits behind a
+// per-word branch).
+template <int Q, int M, int TT, bool PAIRS>
+__global__ void __launch_bounds__(kLdsWaves * 64) vlut_lds_kernel(VlutMatmulArgs p)
 {
-    // grid.x: row chunks of 512 rows; grid.y: k splits; grid.z: token tiles.
-    // LDS holds, for TT tokens x KBW k-blocks, the factorized one-sided vLUT
-    //   T[t][k][j]     = <a_tk, g_j>      j < 8   (g_j: columns of G)
-    //   T[t][k][8 + c] = <a_tk, c>        c = coarse point id
-    // so vLUT_{a_tk}[idx(b)] = sum_j b_j T[j] - q T[8 + cid(b)].
-    __shared__ float s_tab[kVlutTableFloats];
-    __shared__ float s_act[kVlutMaxTables * 8];
-    __shared__ uint64_t s_coarse[kMaxCoarseVlut];
-    const int nc = p.n_coarse;
-    const int stride = 8 + nc;
-    const int kbw = p.kb_per_chunk;
-    const int t0 = blockIdx.z * TT;
-    const int nt = min(TT, (int)(p.B - t0));
+    constexpr int KB = LdsChunk<TT>::KB;
+    constexpr int NTAB = TT * KB;  // tables per chunk: token t, k-block j at t * KB + j
+    __shared__ float s_tab[NTAB * kLdsTable];
+    __shared__ float2 s_pv[4 * kPairSlots];
+    __shared__ float s_act[NTAB * 8];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t kb_total = p.K / 8;
-    const int64_t ks_len = (kb_total + gridDim.y - 1) / gridDim.y;
-    const int64_t k_begin = blockIdx.y * ks_len;
-    const int64_t k_end = min(kb_total, k_begin + ks_len);
-    const int64_t r0 = (int64_t)blockIdx.x * kVlutThreads * kVlutRowsPerThread;
-    for (int i = threadIdx.x; i < nc; i += kVlutThreads) s_coarse[i] = p.coarse[i];
+    const int64_t kb_wg = (kb_total + gridDim.y - 1) / gridDim.y;
+    const int64_t kb_begin = blockIdx.y * kb_wg;
+    const int64_t kb_end = min(kb_total, kb_begin + kb_wg);
+    const int64_t t0 = (int64_t)blockIdx.z * TT;
+    const int64_t row0 = (int64_t)blockIdx.x * kLdsRows + wave * (kLdsTiles * 64) + lane;  // the lane's first row
 
-    float acc[kVlutRowsPerThread][TT];
-#pragma unroll
-    for (int rr = 0; rr < kVlutRowsPerThread; ++rr)
-#pragma unroll
-        for (int t = 0; t < TT; ++t) acc[rr][t] = 0.f;
+    for (int i = threadIdx.x; i < 4 * kPairSlots; i += blockDim.x) s_pv[i] = p.pair_vals[i];
 
-    for (int64_t kc = k_begin; kc < k_end; kc += kbw) {
-        const int nk = (int)min((int64_t)kbw, k_end - kc);
-        __syncthreads();
-        for (int e = threadIdx.x; e < nt * nk * 8; e += kVlutThreads) {
-            int t = e / (nk * 8), rem = e - t * nk * 8;
-            s_act[t * kbw * 8 + rem] = load_act(p.act, p.act_dtype, (int64_t)(t0 + t) * p.K + kc * 8 + rem);
+    float acc[kLdsTiles][TT];
+#pragma unroll
+    for (int i = 0; i < kLdsTiles; ++i)
+#pragma unroll
+        for (int t = 0; t < TT; ++t) acc[i][t] = 0.f;
+
+    constexpr int kActPerThread = (NTAB * 8 + kLdsWaves * 64 - 1) / (kLdsWaves * 64);
+    for (int64_t kc = kb_begin; kc < kb_end; kc += KB) {
+        // the chunk's activations first: loads complete in order, so the
+        // LDS staging below then waits for these alone, with the level words
+        // still in flight through the table build
+        uint32_t av[kActPerThread];  // bits (0 outside the matrix and the range: the value 0 in every dtype)
+#pragma unroll
+        for (int u = 0; u < kActPerThread; ++u) {
+            const int e = threadIdx.x + u * kLdsWaves * 64;
+            const int t = e / (8 * KB), j = (e / 8) % KB;
+            const int64_t kb = kc + j;
+            const bool ok = e < NTAB * 8 && t0 + t < p.B && kb < kb_end;
+            // an index in the matrix for every lane, the bits dropped after
+            const int64_t ai = ok ? (t0 + t) * p.K + kb * 8 + (e % 8) : 0;
+            const uint32_t bits = load_act_bits(p.act, p.act_dtype, ai);
+            av[u] = ok ? bits : 0u;
         }
-        __syncthreads();
-        for (int e = threadIdx.x; e < nt * nk * stride; e += kVlutThreads) {
-            int t = e / (nk * stride);
-            int rem = e - t * nk * stride;
-            int k = rem / stride;
-            int j = rem - k * stride;
-            const float* av = s_act + (t * kbw + k) * 8;
-            float v;
-            if (j == 0) {
-                v = 2.f * av[0];
-            } else if (j < 7) {
-                v = av[j] - av[j - 1];
-            } else if (j == 7) {
-                v = 0.f;
+        // the chunk's level words; indices clamped into the matrix (those
+        // lanes' rows are never stored, their k-blocks have zero tables)
+        uint32_t pw[kLdsTiles][KB][M];
+        auto each_word = [&](auto&& f) {
 #pragma unroll
-                for (int i = 0; i < 8; ++i) v += av[i];
-                v *= 0.5f;
-            } else {
-                uint64_t c = s_coarse[j - 8];
-                v = 0.f;
+            for (int i = 0; i < kLdsTiles; ++i) {
+                const int64_t row = min(row0 + 64 * i, p.rows - 1);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) v = __fmaf_rn(av[i], (float)(int8_t)(uint8_t)(c >> (8 * i)), v);
-                v *= 0.5f;
+                for (int j = 0; j < KB; ++j) {
+                    const int64_t kb = min(kc + j, kb_total - 1);
+#pragma unroll
+                    for (int m = 0; m < M; ++m) f(pw[i][j][m], row, kb, m);
+                }
             }
-            s_tab[(t * kbw + k) * stride + j] = v;
+        };
+        if constexpr (PAIRS) {
+            const uint32_t* w32 = reinterpret_cast<const uint32_t*>(p.words);
+            each_word([&](uint32_t& w, int64_t row, int64_t kb, int m) {
+                w = w32[vlut_word_index(VLUT_PAIRS, row, kb, m, kb_total, M)];
+            });
+        } else {
+            if (p.prepared == VLUT_RAW) {
+                const uint16_t* w16 = reinterpret_cast<const uint16_t*>(p.words);
+                each_word([&](uint32_t& w, int64_t row, int64_t kb, int m) {
+                    w = w16[(row * kb_total + kb) * M + m];
+                });
+            } else {
+                const uint32_t* w32 = reinterpret_cast<const uint32_t*>(p.words);
+                const int fmt = p.prepared;
+                each_word([&](uint32_t& w, int64_t row, int64_t kb, int m) {
+                    w = w32[vlut_word_index(fmt, row, kb, m, kb_total, M)];
+                });
+            }
+            const uint32_t mask = Q == 2 ? 0xffu : 0xffffu;  // map bounds for any input
+            each_word([&](uint32_t& w, int64_t, int64_t, int) { w = p.pair_map[w & mask]; });
+        }
+        __syncthreads();  // the previous chunk's lookups are done with the tables
+#pragma unroll
+        for (int u = 0; u < kActPerThread; ++u) {
+            const int e = threadIdx.x + u * kLdsWaves * 64;
+            if (e < NTAB * 8) s_act[e] = act_value(av[u], p.act_dtype);
         }
         __syncthreads();
-        for (int k = 0; k < nk; ++k) {
+        for (int e = threadIdx.x; e < NTAB * kLdsTable; e += blockDim.x) {
+            const int tab = e / kLdsTable, slot = e - tab * kLdsTable;
+            float v = 0.f;
+            if (slot < 4 * kPairSlots) {
+                const float2 r = s_pv[slot];
+                const float* a = s_act + tab * 8 + 2 * (slot / kPairSlots);
+                v = __fmaf_rn(a[1], r.y, a[0] * r.x);
+            }
+            s_tab[e] = v;
+        }
+        __syncthreads();
 #pragma unroll
-            for (int rr = 0; rr < kVlutRowsPerThread; ++rr) {
-                int64_t row = r0 + threadIdx.x + rr * kVlutThreads;
-                if (row >= p.rows) continue;
+        for (int j = 0; j < KB; ++j) {
+#pragma unroll
+            for (int i = 0; i < kLdsTiles; ++i) {
                 float qm = 1.f;
 #pragma unroll
                 for (int m = 0; m < M; ++m) {
-                    uint32_t w, cid;
-                    load_word(p, vlut_word_index(p.prepared, row, kc + k, m, kb_total, M), &w, &cid);
-                    int b[8];
-                    unpack_word<Q>(w, Q, b);
+                    const uint32_t w = pw[i][j][m];
+                    // ids below the sub-table size for any input word
+                    const uint32_t id0 = min(w & 0xffu, kPairSlots - 1u);
+                    const uint32_t id1 = min((w >> 8) & 0xffu, kPairSlots - 1u) + kPairSlots;
+                    const uint32_t id2 = min((w >> 16) & 0xffu, kPairSlots - 1u) + 2 * kPairSlots;
+                    const uint32_t id3 = min(w >> 24, kPairSlots - 1u) + 3 * kPairSlots;
 #pragma unroll
                     for (int t = 0; t < TT; ++t) {
-                        if (t >= nt) break;
-                        const float* T = s_tab + (t * kbw + k) * stride;
-                        float sum = 0.f;
-#pragma unroll
-                        for (int j = 0; j < 8; ++j) sum = __fmaf_rn((float)b[j], T[j], sum);
-                        sum = __fmaf_rn(-(float)Q, T[8 + cid], sum);
-                        acc[rr][t] = __fmaf_rn(qm, sum, acc[rr][t]);
+                        const float* T = s_tab + (t * KB + j) * kLdsTable;
+                        const float v = (T[id0] + T[id1]) + (T[id2] + T[id3]);
+                        acc[i][t] = __fmaf_rn(qm, v, acc[i][t]);
                     }
                     qm *= (float)Q;
                 }
             }
         }
     }
+    // one store per (row, token): the output itself when the K range is
+    // whole, else the split's partial
 #pragma unroll
-    for (int rr = 0; rr < kVlutRowsPerThread; ++rr) {
-        int64_t row = r0 + threadIdx.x + rr * kVlutThreads;
+    for (int i = 0; i < kLdsTiles; ++i) {
+        const int64_t row = row0 + 64 * i;
         if (row >= p.rows) continue;
-        for (int t = 0; t < nt; ++t)
-            p.partial[((int64_t)(t0 + t) * p.rows + row) * gridDim.y + blockIdx.y] = acc[rr][t];
+        const float sc = gridDim.y > 1 || !p.scale ? 1.f : (p.scale_mode == 0 ? p.scale[row] : 1.f / p.scale[row]);
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+            if (t0 + t >= p.B) break;
+            if (gridDim.y == 1)
+                p.out[(t0 + t) * p.rows + row] = vlut_epilogue(acc[i][t] * sc, row, p.bias, p.lsq_alpha, p.lsq_qmax);
+            else
+                p.partial[((int64_t)blockIdx.y * p.B + t0 + t) * p.rows + row] = acc[i][t];
+        }
     }
 }
 
@@ -538,22 +624,83 @@ __global__ void __launch_bounds__(256) vlut_reduce_sm4_kernel(const float* parti
     reinterpret_cast<float4*>(out)[i4] = make_float4(r[0], r[1], r[2], r[3]);
 }
 
+// The same for many splits and few outputs (the LDS-table kernel at small
+// batches): a workgroup takes 16 output quads with 16 threads per quad, each
+// summing every 16th split in order; the 16 sums of a quad are added in a
+// fixed order through LDS, so the result is the same on every run.
+constexpr int kReduceGroups = 16;
+
+__global__ void __launch_bounds__(256) vlut_reduce_sm4g_kernel(const float* partial, int splits, int64_t B,
+                                                              int64_t rows, const float* scale, int scale_mode,
+                                                              float mult, const float* bias, const float* lsq_alpha,
+                                                              int lsq_qmax, float* out)
+{
+    __shared__ float4 s_sum[kReduceGroups][16 + 1];
+    const int quad = threadIdx.x & 15, g = threadIdx.x >> 4;
+    const int64_t n4 = B * rows / 4;
+    const int64_t i4 = (int64_t)blockIdx.x * 16 + quad;
+    const float4* p4 = reinterpret_cast<const float4*>(partial);
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (i4 < n4) {
+        for (int sp = g; sp < splits; sp += kReduceGroups) {
+            const float4 v = p4[sp * n4 + i4];
+            acc.x += v.x;
+            acc.y += v.y;
+            acc.z += v.z;
+            acc.w += v.w;
+        }
+    }
+    s_sum[g][quad] = acc;
+    __syncthreads();
+    if (g != 0 || i4 >= n4) return;
+    for (int k = 1; k < kReduceGroups; ++k) {
+        const float4 v = s_sum[k][quad];
+        acc.x += v.x;
+        acc.y += v.y;
+        acc.z += v.z;
+        acc.w += v.w;
+    }
+    const float a[4] = {acc.x, acc.y, acc.z, acc.w};
+    const int64_t o0 = (4 * i4) % rows;
+    float r[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t o = o0 + j;
+        const float sc = scale ? (scale_mode == 0 ? scale[o] : 1.f / scale[o]) : 1.f;
+        r[j] = vlut_epilogue(a[j] * mult * sc, o, bias, lsq_alpha, lsq_qmax);
+    }
+    reinterpret_cast<float4*>(out)[i4] = make_float4(r[0], r[1], r[2], r[3]);
+}
+
 // ---------------------------------------------------------------- launchers
 namespace {
 
-template <int Q, int M>
-hipError_t launch_lds(VlutMatmulArgs p, int splits, hipStream_t s)
+int lds_tokens(int64_t B)
 {
-    int TT = p.B >= 8 ? 8 : (p.B >= 4 ? 4 : (p.B >= 2 ? 2 : 1));
-    p.kb_per_chunk = std::max(1, kVlutMaxTables / TT);
-    dim3 grid((unsigned)((p.rows + kVlutThreads * kVlutRowsPerThread - 1) / (kVlutThreads * kVlutRowsPerThread)),
-              (unsigned)splits, (unsigned)((p.B + TT - 1) / TT));
+    return B >= 8 ? 8 : (B >= 4 ? 4 : (B >= 2 ? 2 : 1));
+}
+
+template <int Q, int M, bool PAIRS>
+void launch_lds_fmt(const VlutMatmulArgs& p, int splits, hipStream_t s)
+{
+    const int TT = lds_tokens(p.B);
+    dim3 grid((unsigned)((p.rows + kLdsRows - 1) / kLdsRows), (unsigned)splits, (unsigned)((p.B + TT - 1) / TT));
+    dim3 block(kLdsWaves * 64);
     switch (TT) {
-    case 8: hipLaunchKernelGGL((vlut_lds_kernel<Q, M, 8>), grid, dim3(kVlutThreads), 0, s, p); break;
-    case 4: hipLaunchKernelGGL((vlut_lds_kernel<Q, M, 4>), grid, dim3(kVlutThreads), 0, s, p); break;
-    case 2: hipLaunchKernelGGL((vlut_lds_kernel<Q, M, 2>), grid, dim3(kVlutThreads), 0, s, p); break;
-    default: hipLaunchKernelGGL((vlut_lds_kernel<Q, M, 1>), grid, dim3(kVlutThreads), 0, s, p); break;
+    case 8: hipLaunchKernelGGL((vlut_lds_kernel<Q, M, 8, PAIRS>), grid, block, 0, s, p); break;
+    case 4: hipLaunchKernelGGL((vlut_lds_kernel<Q, M, 4, PAIRS>), grid, block, 0, s, p); break;
+    case 2: hipLaunchKernelGGL((vlut_lds_kernel<Q, M, 2, PAIRS>), grid, block, 0, s, p); break;
+    default: hipLaunchKernelGGL((vlut_lds_kernel<Q, M, 1, PAIRS>), grid, block, 0, s, p); break;
     }
+}
+
+template <int Q, int M>
+hipError_t launch_lds(const VlutMatmulArgs& p, int splits, hipStream_t s)
+{
+    if (p.prepared == VLUT_PAIRS)
+        launch_lds_fmt<Q, M, true>(p, splits, s);
+    else
+        launch_lds_fmt<Q, M, false>(p, splits, s);
     return hipGetLastError();
 }
 
@@ -647,11 +794,13 @@ VlutPlan vlut_plan(int64_t rows, int64_t B, int64_t K, int q, int M, int method)
 {
     const int64_t kb = K / 8;
     if (method == VLUT_METHOD_LDS) {
-        int TT = B >= 8 ? 8 : (B >= 4 ? 4 : (B >= 2 ? 2 : 1));
-        int64_t row_chunks = (rows + kVlutThreads * kVlutRowsPerThread - 1) / (kVlutThreads * kVlutRowsPerThread);
-        int64_t tiles = (B + TT - 1) / TT;
-        int64_t want = g_vlut_splits > 0 ? g_vlut_splits : std::max<int64_t>(1, 256 / std::max<int64_t>(1, row_chunks * tiles));
-        return {VK_LDS, (int)std::max<int64_t>(1, std::min<int64_t>(want, kb))};
+        // 512-row, TT-token workgroups, with K splits for two per CU (each
+        // keeping at least one k-block)
+        const int TT = lds_tokens(B);
+        const int64_t groups = ((rows + kLdsRows - 1) / kLdsRows) * ((B + TT - 1) / TT);
+        int64_t splits = g_vlut_splits > 0 ? g_vlut_splits
+                                           : (2 * device_cu_count() + groups - 1) / std::max<int64_t>(1, groups);
+        return {VK_LDS, (int)std::max<int64_t>(1, std::min<int64_t>(splits, kb))};
     }
     const bool swar = g_vlut_swar && ((q == 2 && M <= 4) || (q == 4 && M <= 2));
     if (swar && B > 32 && g_vlut_deep) {
@@ -753,7 +902,7 @@ hipError_t vlut_prepare(const uint16_t* words, int64_t rows, int64_t kb, int M, 
         return hipGetLastError();
     }
     hipLaunchKernelGGL(vlut_prepare_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, words, rows, kb, M, fmt,
-                       n, t->cid_map, t->n_codes - 1u, prepared);
+                       n, t->cid_map, t->pair_map, t->n_codes - 1u, prepared);
     return hipGetLastError();
 }
 
@@ -776,12 +925,18 @@ hipError_t vlut_matmul(VlutMatmulArgs p, const VlutPlan& plan, hipStream_t s)
     p.swar = t->swar;
     p.swar_ok = p.M <= t->swar_max_m && g_vlut_swar;
     p.swar_bias = p.swar_ok ? t->swar_bias[p.M] : 0;
+    p.pair_map = t->pair_map;
+    p.pair_vals = t->pair_vals;
     if (p.prepared == VLUT_DECODED && plan.kernel != VK_MFMA_ROWS && plan.kernel != VK_MFMA_WIDE &&
         plan.kernel != VK_MFMA_DEEP)
         return hipErrorInvalidValue;
-    if (plan.kernel == VK_MFMA_WIDE || plan.kernel == VK_MFMA_DEEP) {
-        if (!p.swar_ok) return hipErrorInvalidValue;
-        if (plan.kernel == VK_MFMA_DEEP) {
+    if (p.prepared == VLUT_PAIRS && plan.kernel != VK_LDS) return hipErrorInvalidValue;
+    if (plan.kernel == VK_MFMA_WIDE || plan.kernel == VK_MFMA_DEEP || plan.kernel == VK_LDS) {
+        if (plan.kernel == VK_LDS) {
+            e = p.q == 4 ? dispatch_m<4>(p, VLUT_METHOD_LDS, splits, s) : dispatch_m<2>(p, VLUT_METHOD_LDS, splits, s);
+        } else if (!p.swar_ok) {
+            return hipErrorInvalidValue;
+        } else if (plan.kernel == VK_MFMA_DEEP) {
             const int64_t kq_total = (p.K / 8 + 3) / 4;
             if ((kq_total + splits - 1) / splits > kDeepKqWg) return hipErrorInvalidValue;
             e = vlut_launch_deep(p, splits, s);
@@ -789,15 +944,21 @@ hipError_t vlut_matmul(VlutMatmulArgs p, const VlutPlan& plan, hipStream_t s)
             e = vlut_launch_wide(p, splits, s);
         }
         if (e != hipSuccess || splits == 1) return e;
+        // split-major partials [splits, B, rows] of 2 x_hat products (MFMA) or of x_hat ones (LDS)
+        const float mult = plan.kernel == VK_LDS ? 1.f : 0.5f;
         const int64_t nw = p.B * p.rows;
         const bool v4 = p.rows % 4 == 0 && ((uintptr_t)p.out % 16) == 0 && ((uintptr_t)p.partial % 16) == 0;
-        if (v4)
+        if (v4 && plan.kernel == VK_LDS)
+            hipLaunchKernelGGL(vlut_reduce_sm4g_kernel, dim3((unsigned)((nw / 4 + 15) / 16)), dim3(256), 0, s,
+                               p.partial, splits, p.B, p.rows, p.scale, p.scale_mode, mult, p.bias, p.lsq_alpha,
+                               p.lsq_qmax, p.out);
+        else if (v4)
             hipLaunchKernelGGL(vlut_reduce_sm4_kernel, dim3((unsigned)((nw / 4 + 255) / 256)), dim3(256), 0, s,
-                               p.partial, splits, p.B, p.rows, p.scale, p.scale_mode, 0.5f, p.bias, p.lsq_alpha,
+                               p.partial, splits, p.B, p.rows, p.scale, p.scale_mode, mult, p.bias, p.lsq_alpha,
                                p.lsq_qmax, p.out);
         else
             hipLaunchKernelGGL(vlut_reduce_sm_kernel, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, s, p.partial,
-                               splits, p.B, p.rows, p.scale, p.scale_mode, 0.5f, p.bias, p.lsq_alpha, p.lsq_qmax,
+                               splits, p.B, p.rows, p.scale, p.scale_mode, mult, p.bias, p.lsq_alpha, p.lsq_qmax,
                                p.out);
         return hipGetLastError();
     }
@@ -806,14 +967,12 @@ hipError_t vlut_matmul(VlutMatmulArgs p, const VlutPlan& plan, hipStream_t s)
         e = vlut_launch_rows(p, splits, s);
         if (e != hipSuccess || splits == 1) return e;
     } else {
-        const int method = plan.kernel == VK_LDS ? VLUT_METHOD_LDS : VLUT_METHOD_MFMA;
-        e = p.q == 4 ? dispatch_m<4>(p, method, splits, s) : dispatch_m<2>(p, method, splits, s);
+        e = p.q == 4 ? dispatch_m<4>(p, VLUT_METHOD_MFMA, splits, s) : dispatch_m<2>(p, VLUT_METHOD_MFMA, splits, s);
         if (e != hipSuccess) return e;
     }
     int64_t n = p.B * p.rows;
-    float mult = plan.kernel == VK_LDS ? 1.f : 0.5f;
     hipLaunchKernelGGL(vlut_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p.partial, splits,
-                       p.B, p.rows, p.scale, p.scale_mode, mult, p.bias, p.lsq_alpha, p.lsq_qmax, p.out);
+                       p.B, p.rows, p.scale, p.scale_mode, 0.5f, p.bias, p.lsq_alpha, p.lsq_qmax, p.out);
     return hipGetLastError();
 }
 

@@ -14,12 +14,15 @@ enum VlutMethod { VLUT_METHOD_AUTO = 0, VLUT_METHOD_LDS = 1, VLUT_METHOD_MFMA = 
 // prepared uint32 (cid << 16 | idx), tiled prepared (matrix-core fragments).
 // VLUT_DECODED: per (row, k-block) pair the 8 bytes 2 x_hat + 128 of its
 // M-level decode (exact for the byte-table formats, |2 x_hat| <= 127), in the
-// tiled fragment order; two uint32 per pair.
-enum VlutFormat { VLUT_RAW = 0, VLUT_PREPARED = 1, VLUT_TILED = 2, VLUT_DECODED = 3 };
+// tiled fragment order; two uint32 per pair.  VLUT_PAIRS: each level word
+// replaced by its four coordinate-pair ids (pair_map, tables.hpp), laid out
+// [rows / 64][kb][M][64 rows] (rows padded to 64 with the ids of word 0):
+// the LDS-table kernel's format, one 256-byte read per wave and word.
+enum VlutFormat { VLUT_RAW = 0, VLUT_PREPARED = 1, VLUT_TILED = 2, VLUT_DECODED = 3, VLUT_PAIRS = 4 };
 constexpr int kVlutDecodedBias = 128;
 
 struct VlutMatmulArgs {
-    const void* words;   // [rows, K/8, M] (VLUT_RAW / VLUT_PREPARED) or tiles (VLUT_TILED)
+    const void* words;   // [rows, K/8, M] (VLUT_RAW / VLUT_PREPARED) or tiles (the other formats)
     int prepared;        // VlutFormat
     const float* scale;  // [rows] or null
     int scale_mode;      // 0: out *= scale[o]; 1: out /= scale[o]
@@ -27,7 +30,7 @@ struct VlutMatmulArgs {
     int act_dtype;
     int64_t B, rows, K;
     int q, M, legacy;
-    float* partial;      // [B, rows, splits] workspace
+    float* partial;      // split-K partials, [splits, B, rows] (the tile kernel: [B, rows, splits])
     float* out;          // [B, rows]
     // epilogue after the scale: + bias[o] (nullable), then the LSQ activation
     // quantizer with parameter *lsq_alpha and lsq_qmax (nullable alpha: none)
@@ -38,10 +41,11 @@ struct VlutMatmulArgs {
     const uint16_t* map;
     const uint64_t* coarse;
     int n_coarse;
-    int kb_per_chunk;
     const uint64_t* swar;  // byte tables of the MFMA decode (tables.hpp)
     int swar_ok;
     int swar_bias;
+    const uint32_t* pair_map;  // coordinate-pair ids and values (tables.hpp)
+    const float2* pair_vals;
 };
 
 // 0 forces the integer decode in the MFMA kernel (tests compare both)
@@ -55,6 +59,7 @@ extern int g_vlut_deep;
 // (VLUT_DECODED: index of the pair's first uint32; m and M are ignored.)
 __host__ __device__ inline int64_t vlut_word_index(int fmt, int64_t row, int64_t kb, int m, int64_t kb_total, int M)
 {
+    if (fmt == VLUT_PAIRS) return (((row >> 6) * kb_total + kb) * M + m) * 64 + (row & 63);
     if (fmt != VLUT_TILED && fmt != VLUT_DECODED) return (row * kb_total + kb) * M + m;
     const int64_t kq = (kb_total + 3) / 4;
     const int64_t entry = (((row >> 4) * kq + (kb >> 2)) * 64) + (row & 15) + 16 * (kb & 3);
@@ -63,6 +68,7 @@ __host__ __device__ inline int64_t vlut_word_index(int fmt, int64_t row, int64_t
 
 __host__ __device__ inline int64_t vlut_prepared_words(int64_t rows, int64_t kb, int M, int fmt)
 {
+    if (fmt == VLUT_PAIRS) return ((rows + 63) / 64) * 64 * kb * M;
     if (fmt != VLUT_TILED && fmt != VLUT_DECODED) return rows * kb * M;
     return ((rows + 15) / 16) * ((kb + 3) / 4) * 64 * (fmt == VLUT_DECODED ? 2 : M);
 }
@@ -80,7 +86,8 @@ VlutPlan vlut_plan(int64_t rows, int64_t B, int64_t K, int q, int M, int method)
 // kernel runs unsplit and writes the output itself.
 inline int64_t vlut_workspace_floats(const VlutPlan& plan, int64_t B, int64_t rows)
 {
-    if ((plan.kernel == VK_MFMA_ROWS || plan.kernel == VK_MFMA_WIDE || plan.kernel == VK_MFMA_DEEP) &&
+    if ((plan.kernel == VK_MFMA_ROWS || plan.kernel == VK_MFMA_WIDE || plan.kernel == VK_MFMA_DEEP ||
+         plan.kernel == VK_LDS) &&
         plan.splits == 1)
         return 0;
     return (int64_t)plan.splits * B * rows;
@@ -92,7 +99,8 @@ hipError_t vlut_matmul(VlutMatmulArgs p, const VlutPlan& plan, hipStream_t s);
 // prepared = cid(word) << 16 | word for raw words [rows, kb, M]: the
 // coarse-point id each level word decodes through, stored next to it so the
 // matmul needs no map lookup; fmt VLUT_PREPARED keeps the layout,
-// VLUT_TILED writes the fragment order (padding decodes to 0).
+// VLUT_TILED writes the fragment order (padding decodes to 0); VLUT_PAIRS
+// writes pair_map[word] in that order, VLUT_DECODED the M-level decode.
 hipError_t vlut_prepare(const uint16_t* words, int64_t rows, int64_t kb, int M, int q, int legacy, int fmt,
                         uint32_t* prepared, hipStream_t s);
 

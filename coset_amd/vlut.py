@@ -188,15 +188,17 @@ def vlut_dot(words: torch.Tensor, vlut: torch.Tensor, q: int) -> torch.Tensor:
 
 
 _METHODS = {"auto": 0, "lds": 1, "mfma": 2}
-_LAYOUTS = {"rowmajor": 1, "tiled": 2, "decoded": 3}
+_LAYOUTS = {"rowmajor": 1, "tiled": 2, "decoded": 3, "pairs": 4}
 
 
 @dataclass
 class PreparedWords:
     """Level words converted once for vlut_matmul (coset_vlut_prepare):
     uint32 cid << 16 | idx values, row-major or tiled in matrix-core fragment
-    order (16 rows x 4 k-blocks per 64-entry tile), or ("decoded") the
-    pairs' 2 x_hat as biased bytes in the tiled order."""
+    order (16 rows x 4 k-blocks per 64-entry tile), ("decoded") the
+    pairs' 2 x_hat as biased bytes in the tiled order, or ("pairs") each
+    level word's four coordinate-pair ids, [rows / 64][kb][M][64 rows], which
+    the LDS-table method reads without a map lookup."""
     data: torch.Tensor
     rows: int
     kb: int
@@ -214,8 +216,10 @@ def vlut_prepare(words: torch.Tensor, q: int = 4, legacy: bool = False, layout: 
     """uint16 level words [rows, K/8, M] -> PreparedWords, the weight format
     vlut_matmul reads without the coarse-id gather ("rowmajor", "tiled") or
     without any table lookup ("decoded": 8 bytes per pair, q = 4 with M <= 2
-    or q = 2 with M <= 4, fp16/bf16 activations).  Done once per weight;
-    ``legacy`` fixes the residual rule the matmul will use."""
+    or q = 2 with M <= 4, fp16/bf16 activations), or as the coordinate-pair
+    ids the LDS-table method looks up ("pairs": any activation dtype,
+    method "lds" or "auto").  Done once per weight; ``legacy`` fixes the
+    residual rule the matmul will use."""
     w = on_gpu(words).contiguous()
     if w.dtype != torch.uint16 or w.dim() != 3:
         raise ValueError("vlut_prepare takes uint16 level words [rows, K/8, M] (q <= 4)")
@@ -262,6 +266,10 @@ def vlut_matmul(words, act: torch.Tensor, q: int = 4, *, scale: Optional[torch.T
         raise ValueError(f"act must be [B, {8 * kb}]")
     B, K = a.shape
     m = _METHODS[method]
+    if fmt == _LAYOUTS["pairs"]:
+        if method == "mfma":
+            raise ValueError('the "pairs" layout is read by the lds method only')
+        m = _METHODS["lds"]
     dt = _lib.dtype_code(a.dtype)
     need = _lib.load().coset_vlut_workspace_floats(B, rows, K, int(q), int(M), dt, m)
     if need > 0 and (workspace is None or workspace.numel() < need):

@@ -238,9 +238,14 @@ int coset_vlut_lookup_dot(const void* words, int64_t n_blocks, int q, int M, con
  *      footprint of format 2 for M = 2, so the matmul reads no tables.
  *      q = 4 with M <= 2 or q = 2 with M <= 4 (|2 x_hat| <= 127); matrix-core
  *      method only.
+ *   4  pairs: each level word replaced by the ids of its residual's four
+ *      coordinate pairs (r_2p, r_2p+1), one byte each (at most 72 distinct
+ *      values per pair), the entries the LDS-table method looks up, laid out
+ *      [ceil(rows / 64)][kb][M][64 rows] (padding rows hold the ids of word
+ *      0, which decodes to 0); that method only (method 0 selects it).
  * coset_vlut_prepared_words gives the uint32 count of a format; prepare
- * (once per weight) converts format-0 words [rows, kb, M] into format 1, 2
- * or 3 for the core rule (legacy = 0) or the legacy one. */
+ * (once per weight) converts format-0 words [rows, kb, M] into format 1, 2,
+ * 3 or 4 for the core rule (legacy = 0) or the legacy one. */
 int64_t coset_vlut_prepared_words(int64_t rows, int64_t kb, int M, int word_format);
 int coset_vlut_prepare(const void* words, int64_t rows, int64_t kb, int M, int q, int legacy, int word_format,
                        uint32_t* prepared, void* stream);
@@ -249,11 +254,14 @@ int coset_vlut_prepare(const void* words, int64_t rows, int64_t kb, int M, int q
  * for level words of q in {2, 4}, M <= 4 in any word_format above (a
  * prepared format with the legacy flag it was prepared with), activations
  * [B, K] fp32/bf16/fp16, s_o = scale[o] (scale_mode 0), 1/scale[o] (1) or 1
- * (scale NULL).  method 1 keeps per-(token, k-block) factorized tables
- * <a, g_j>, <a, c> in LDS; method 2 decodes 2*x_hat and runs the product on
- * the matrix cores (fp16/bf16 activations holding 2*x_hat exactly); 0 picks 2
- * when it is exact.  workspace: caller-owned fp32 scratch of
- * coset_vlut_workspace_floats floats (0 is a valid size).
+ * (scale NULL).  method 1 keeps a per-(token, k-block) inner-product table in
+ * LDS, factorized over the coordinate pairs of r: <a, r(b)> = sum_p
+ * <(a_2p, a_2p+1), r_p(b)>, four lookups per level word (any activation
+ * dtype); method 2 decodes 2*x_hat and runs the product on the matrix cores
+ * (fp16/bf16 activations holding 2*x_hat exactly); 0 picks 2 when it is
+ * exact, and 1 for format 4.  workspace: caller-owned fp32 scratch of
+ * coset_vlut_workspace_floats floats (0 is a valid size; query with method 1
+ * for format 4).
  * The reference has no matmul routine; its placeholder QLinear._lut_matmul is
  * coset/legacy/nn/qlinear.py:272-281. */
 int64_t coset_vlut_workspace_floats(int64_t B, int64_t rows, int64_t K, int q, int M, int act_dtype, int method);

@@ -115,6 +115,12 @@ def test_reference_helpers():
     assert coset_amd.QuantizationConfig(lattice_type="E8", q=4, M=2).beta == 0.3
 
 
+def runs(method, w):
+    """Whether a weight form runs on a method: the pairs layout is read by
+    the LDS-table method only."""
+    return not (method == "mfma" and getattr(w, "layout", None) == "pairs")
+
+
 @pytest.fixture(params=["bytes", "integer"])
 def mfma_decode(request):
     """The MFMA kernel's two decoders: byte tables (default) and digits."""
@@ -142,12 +148,15 @@ def test_vlut_matmul_vs_oracle(method, B, adt, mfma_decode):
     words = torch.from_numpy(words_np.astype(np.int32)).to(torch.uint16).cuda()
     a = torch.from_numpy(rng.standard_normal((B, K)).astype(np.float32)).to(adt)
     for legacy in (False, True):
-        prepared = [coset_amd.vlut_prepare(words, q, legacy=legacy, layout=lay) for lay in ("rowmajor", "tiled")]
+        prepared = [coset_amd.vlut_prepare(words, q, legacy=legacy, layout=lay)
+                    for lay in ("rowmajor", "tiled", "pairs")]
         for mode in ("mul", "div"):
             sm = 0 if mode == "mul" else 1
             ref = O.vlut_matmul(words_np, scale, a.float().numpy(), q, M, scale_mode=sm, legacy=legacy)
             mag = matmul_mag(words_np, q, M, a.float().numpy(), scale, sm, legacy)
             for w in [words] + prepared:
+                if not runs(method, w):
+                    continue
                 out = coset_amd.vlut_matmul(w, a.cuda(), q, scale=torch.from_numpy(scale), scale_mode=mode,
                                             legacy=legacy, method=method).cpu().numpy()
                 close(out, ref, mag, 1e-3)
@@ -171,9 +180,12 @@ def test_vlut_matmul_other_levels(q, M, B, mfma_decode):
     for legacy in (False, True):
         ref = O.vlut_matmul(words_np, scale, a.float().numpy(), q, M, scale_mode=0, legacy=legacy)
         mag = matmul_mag(words_np, q, M, a.float().numpy(), legacy=legacy)
-        prepared = [coset_amd.vlut_prepare(words, q, legacy=legacy, layout=lay) for lay in ("rowmajor", "tiled")]
+        prepared = [coset_amd.vlut_prepare(words, q, legacy=legacy, layout=lay)
+                    for lay in ("rowmajor", "tiled", "pairs")]
         for method in ("lds", "mfma"):
             for w in [words] + prepared:
+                if not runs(method, w):
+                    continue
                 out = coset_amd.vlut_matmul(w, a.cuda(), q, legacy=legacy, method=method).cpu().numpy()
                 close(out, ref, mag, 1e-3)
 
@@ -193,10 +205,11 @@ def test_vlut_matmul_forced_splits(splits):
     a = torch.from_numpy(rng.standard_normal((4, K)).astype(np.float32)).to(torch.float16)
     ref = O.vlut_matmul(words_np, np.ones(rows, np.float32), a.float().numpy(), q, M)
     mag = matmul_mag(words_np, q, M, a.float().numpy())
+    pairs = coset_amd.vlut_prepare(words, q, layout="pairs")
     _lib.set_vlut_splits(splits)
     try:
-        for method in ("lds", "mfma"):
-            out = coset_amd.vlut_matmul(words, a.cuda(), q, method=method).cpu().numpy()
+        for method, w in (("lds", words), ("lds", pairs), ("mfma", words)):
+            out = coset_amd.vlut_matmul(w, a.cuda(), q, method=method).cpu().numpy()
             close(out, ref, mag, 1e-3)
     finally:
         _lib.set_vlut_splits(0)
@@ -249,12 +262,59 @@ def test_vlut_matmul_ragged_shapes(B, mfma_decode):
     a16 = a.numpy().astype(np.float16).astype(np.float32)
     ref = O.vlut_matmul(words_np, scale, a16, q, M)
     mag = matmul_mag(words_np, q, M, a16, scale)
-    forms = [words] + [coset_amd.vlut_prepare(words, q, layout=lay) for lay in ("rowmajor", "tiled")]
+    forms = [words] + [coset_amd.vlut_prepare(words, q, layout=lay) for lay in ("rowmajor", "tiled", "pairs")]
     for w in forms:
         for method in ("lds", "mfma"):
+            if not runs(method, w):
+                continue
             out = coset_amd.vlut_matmul(w, a.half().cuda(), q, scale=torch.from_numpy(scale),
                                         method=method).cpu().numpy()
             close(out, ref, mag, 1e-3)
+
+
+@pytest.mark.parametrize("q,M", [(4, 2), (4, 4), (2, 3)])
+@pytest.mark.parametrize("B", [1, 2, 4, 8, 11])
+def test_pairs_layout(q, M, B):
+    """The pairs layout: the LDS-table method with fp32 activations (the
+    method "auto" takes for them) against the oracle for token counts of
+    each token tiling, core and legacy rules; "auto" on the layout runs the
+    LDS-table method, "mfma" refuses it; the layout's words are the pair ids
+    the tables give every word."""
+    import coset_amd
+    rng = np.random.default_rng(300 + 10 * q + M + B)
+    rows, K = 530, 264                   # two 512-row workgroups, a partial k-quad
+    W = rng.standard_normal((rows, K)).astype(np.float32)
+    codes = O.e8_encode(W.reshape(-1, 8), q, M)
+    words_np = O.pack_words(codes, q).reshape(rows, K // 8, M)
+    words = torch.from_numpy(words_np.astype(np.int32)).to(torch.uint16).cuda()
+    a = torch.from_numpy(rng.standard_normal((B, K)).astype(np.float32))
+    scale = rng.uniform(0.5, 2.0, rows).astype(np.float32)
+    for legacy in (False, True):
+        pairs = coset_amd.vlut_prepare(words, q, legacy=legacy, layout="pairs")
+        ref = O.vlut_matmul(words_np, scale, a.numpy(), q, M, scale_mode=1, legacy=legacy)
+        mag = matmul_mag(words_np, q, M, a.numpy(), scale, 1, legacy)
+        for method in ("auto", "lds"):
+            out = coset_amd.vlut_matmul(pairs, a.cuda(), q, scale=torch.from_numpy(scale), scale_mode="div",
+                                        legacy=legacy, method=method).cpu().numpy()
+            close(out, ref, mag, 1e-3)
+        with pytest.raises(ValueError):
+            coset_amd.vlut_matmul(pairs, a.half().cuda(), q, legacy=legacy, method="mfma")
+    # every word's ids name pairs whose values are the word's residual; the
+    # layout is [rows / 64][kb][M][64 rows]
+    R = O.residual_table(q, legacy=False, strided=True)
+    kb = K // 8
+    ids = coset_amd.vlut_prepare(words, q, layout="pairs").data.cpu().numpy().astype(np.uint32)
+    ids = ids.reshape(-1, kb, M, 64).transpose(0, 3, 1, 2).reshape(-1, kb, M)
+    assert ids.shape[0] == -(-rows // 64) * 64
+    ids = ids[:rows].reshape(-1)
+    idx = words_np.astype(np.int64).reshape(-1)
+    for p_ in range(4):
+        pid = (ids >> (8 * p_)) & 0xff
+        key = R[idx, 2 * p_] * 64 + R[idx, 2 * p_ + 1]      # the pair's value, as one number
+        assert pid.max() < 72
+        # one id per distinct value and one value per id
+        pairs_seen = np.unique(np.stack([pid, key]), axis=1)
+        assert len(np.unique(pairs_seen[0])) == pairs_seen.shape[1] == len(np.unique(pairs_seen[1]))
 
 
 def _close_elem(out, ref, mag, rtol=1e-3):
@@ -274,7 +334,8 @@ def test_c4_full_size_equals_decoded_product():
     W = 0.02 * torch.randn((4096, 4096), device="cuda", generator=g)
     words = coset_amd.hnlq_encode(W.reshape(-1, 8), 4, 2, 0.02).reshape(4096, 512, 2)
     forms = {"words": words, "tiled": coset_amd.vlut_prepare(words, 4),
-             "decoded": coset_amd.vlut_prepare(words, 4, layout="decoded")}
+             "decoded": coset_amd.vlut_prepare(words, 4, layout="decoded"),
+             "pairs": coset_amd.vlut_prepare(words, 4, layout="pairs")}
     dec = coset_amd.hnlq_decode(words.reshape(-1, 2), 4, 2, 0.02).reshape(4096, 4096)
     rows = np.arange(7, 4096, 85)
     words_rows = words.cpu().numpy().astype(np.uint32)[rows]
@@ -287,7 +348,7 @@ def test_c4_full_size_equals_decoded_product():
         mag = (a.double().abs() @ dec.double().abs().T)
         for method in ("lds", "mfma"):
             for name, w in forms.items():
-                if name == "decoded" and method == "lds":
+                if (name == "decoded" and method == "lds") or not runs(method, w):
                     continue
                 print(f"C4 B={B} {method} {name}", flush=True)
                 out = coset_amd.vlut_matmul(w, a, 4, scale=torch.full((4096,), 0.02), method=method)

@@ -69,12 +69,13 @@ def test_noalloc_refuses_plans_beyond_its_scratch():
     _lib.require_gpu()
     lib = _lib.load()
     cap = lib.coset_vlut_noalloc_scratch_floats()
-    # the LDS-table method at a large batch needs more partials than the array holds
+    # the matrix-core method at a large batch (the deep kernel, four K splits at
+    # least) needs more partials than the array holds
     B, rows, K = 4096, 4096, 4096
-    need = lib.coset_vlut_workspace_floats(B, rows, K, 4, 2, _lib.F16, 1)
+    need = lib.coset_vlut_workspace_floats(B, rows, K, 4, 2, _lib.F16, 2)
     assert need > cap, need
     dummy = torch.empty(16, dtype=torch.float32, device="cuda")
     rc = lib.coset_vlut_matmul_noalloc(dummy.data_ptr(), 0, None, 0, dummy.data_ptr(), _lib.F16, B, rows, K, 4, 2, 0,
-                                       1, dummy.data_ptr(), _lib.stream_of(dummy))
+                                       2, dummy.data_ptr(), _lib.stream_of(dummy))
     assert rc == _lib.EINVAL
     assert b"scratch" in lib.coset_last_error()
