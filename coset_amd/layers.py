@@ -225,12 +225,17 @@ class E8ThetaWeightQuant(torch.autograd.Function):
         if b_cast is None:
             return Wq
         # the bias in the product's dtype rides along, not differentiable here:
-        # its gradient reaches the fp32 bias through QATLinearFn
+        # its gradient reaches the fp32 bias through QATLinearFn.  Unused
+        # gradients stay None (autograd would otherwise fill a zero tensor
+        # for b_cast on every backward: one more launch per step)
         ctx.mark_non_differentiable(b_cast)
+        ctx.set_materialize_grads(False)
         return Wq, b_cast
 
     @staticmethod
     def backward(ctx, g, g_bias=None):
+        if g is None:
+            return (None,) * 12
         Wc, packed, beta, dbdt = ctx.saved_tensors
         q, M, clip, bpt, theta_shape = ctx.cfg
         if g.dtype not in (torch.float32, torch.bfloat16):
