@@ -301,18 +301,47 @@ class D4ThetaWeightQuant(torch.autograd.Function):
         return dW, dtheta.view(theta_shape), None, None, None, None, None, None, None, None
 
 
-def colsum(g2: torch.Tensor) -> torch.Tensor:
-    """sum over rows of a [rows, cols] fp32/bf16/fp16 tensor, accumulated in
-    fp32 in a fixed order (coset_colsum): the bias gradient of a product."""
-    g2 = g2.contiguous()
+def _colsum_buffers(g2: torch.Tensor):
+    """The output and workspace of colsum(g2), allocated on the current stream."""
     rows, cols = g2.shape
     out = torch.empty(cols, dtype=torch.float32, device=g2.device)
     need = int(_lib.load().coset_colsum_workspace_floats(rows, cols))
     ws = torch.empty(max(need, 1), dtype=torch.float32, device=g2.device)
+    return out, ws
+
+
+def _colsum_into(g2: torch.Tensor, out: torch.Tensor, ws: torch.Tensor) -> None:
+    """coset_colsum of a contiguous g2 into out, on the current stream."""
+    rows, cols = g2.shape
     dt = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}[g2.dtype]
     _lib.check("coset_colsum", _lib.fn("coset_colsum")(g2.data_ptr(), dt, rows, cols, out.data_ptr(), ws.data_ptr(),
                                                        ws.numel(), _lib.stream_of(g2)))
+
+
+def colsum(g2: torch.Tensor) -> torch.Tensor:
+    """sum over rows of a [rows, cols] fp32/bf16/fp16 tensor, accumulated in
+    fp32 in a fixed order (coset_colsum): the bias gradient of a product."""
+    g2 = g2.contiguous()
+    out, ws = _colsum_buffers(g2)
+    _colsum_into(g2, out, ws)
     return out
+
+
+_AUX_STREAMS: Dict[int, "torch.cuda.Stream"] = {}
+# > 0 while CapturedQATStep warms up and captures: the backward then forks
+# its independent products onto a second stream (graph branches).  Eager
+# steps stay on one stream, where the host's launch time is the limit and
+# the fork and join would only add to it.
+_OVERLAP_BACKWARD = [0]
+
+
+def _aux_stream(device: torch.device) -> "torch.cuda.Stream":
+    """A second stream per device (default priority) for the backward's
+    products that do not depend on each other."""
+    s = _AUX_STREAMS.get(device.index)
+    if s is None:
+        s = _AUX_STREAMS[device.index] = torch.cuda.Stream(device=device)
+    return s
 
 
 class QATLinearFn(torch.autograd.Function):
@@ -337,6 +366,37 @@ class QATLinearFn(torch.autograd.Function):
         x, Wq = ctx.saved_tensors
         g2 = gy.reshape(-1, gy.shape[-1])
         dx = dW = db = None
+        need_dx, need_dw = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        fast_db = (ctx.bias_dtype is not None and ctx.needs_input_grad[2] and g2.shape[1] % 8 == 0
+                   and g2.dtype in (torch.float32, torch.bfloat16, torch.float16))
+        overlap = g2.is_cuda and (_OVERLAP_BACKWARD[0] > 0 or torch.cuda.is_current_stream_capturing())
+        if overlap and need_dw and (need_dx or fast_db) and g2.dtype == Wq.dtype == x.dtype:
+            # dX and the bias gradient on a second stream while dW runs on
+            # this one: the dW product alone leaves CUs idle at these shapes
+            # (one 128 x 128 tile per CU or fewer).  Outputs are allocated here, on the
+            # current stream, before the fork; the join comes before they
+            # are returned.  Under graph capture the two streams become two
+            # branches of the graph.
+            g2 = g2.contiguous()
+            main = torch.cuda.current_stream(g2.device)
+            aux = _aux_stream(g2.device)
+            dx2 = torch.empty((g2.shape[0], Wq.shape[1]), dtype=g2.dtype, device=g2.device) if need_dx else None
+            cs = _colsum_buffers(g2) if fast_db else None
+            aux.wait_stream(main)
+            with torch.cuda.stream(aux):
+                if need_dx:
+                    torch.mm(g2, Wq, out=dx2)
+                if fast_db:
+                    _colsum_into(g2, *cs)
+            dW = g2.t() @ x.reshape(-1, x.shape[-1])
+            main.wait_stream(aux)
+            if need_dx:
+                dx = dx2.reshape(x.shape)
+            if fast_db:
+                db = cs[0].to(ctx.bias_dtype)
+            elif ctx.bias_dtype is not None and ctx.needs_input_grad[2]:
+                db = g2.float().sum(0).to(ctx.bias_dtype)
+            return dx, dW, db, None
         if ctx.needs_input_grad[0]:
             dx = (g2 @ Wq).reshape(x.shape)
         if ctx.needs_input_grad[1]:
@@ -772,21 +832,25 @@ class CapturedQATStep:
         host_step = layer._host_step
         saved = {name: b.clone() for name, b in layer.named_buffers()}
 
-        side = torch.cuda.Stream(device=x.device)
-        side.wait_stream(torch.cuda.current_stream(x.device))
-        with torch.cuda.stream(side):
-            for _ in range(max(1, int(warmup))):
-                self._zero_grads()
-                self._run()
-        torch.cuda.current_stream(x.device).wait_stream(side)
-        with torch.no_grad():
-            for name, b in layer.named_buffers():
-                b.copy_(saved[name])
-        self._zero_grads()
+        _OVERLAP_BACKWARD[0] += 1   # warm-up and capture take the same (two-stream) backward
+        try:
+            side = torch.cuda.Stream(device=x.device)
+            side.wait_stream(torch.cuda.current_stream(x.device))
+            with torch.cuda.stream(side):
+                for _ in range(max(1, int(warmup))):
+                    self._zero_grads()
+                    self._run()
+            torch.cuda.current_stream(x.device).wait_stream(side)
+            with torch.no_grad():
+                for name, b in layer.named_buffers():
+                    b.copy_(saved[name])
+            self._zero_grads()
 
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
-            self.y = self._run()
+            self.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.graph):
+                self.y = self._run()
+        finally:
+            _OVERLAP_BACKWARD[0] -= 1
         layer._host_step = host_step
         # the gradient tensors the graph writes, and the parameter storage it reads
         self._grads = [(p, p.grad) for p in layer.parameters() if p.grad is not None]

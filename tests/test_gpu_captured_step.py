@@ -27,10 +27,14 @@ def _grads(L, x):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("tiling", ["row", "block"])
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_captured_step_matches_eager_steps(tiling, dtype):
-    fin, fout, tokens, steps = 256, 384, 512, 7
+@pytest.mark.parametrize("tiling,dtype,fin,fout,tokens", [
+    ("row", torch.bfloat16, 256, 384, 512), ("block", torch.bfloat16, 256, 384, 512),
+    ("row", torch.float32, 256, 384, 512), ("block", torch.float32, 256, 384, 512),
+    # a BERT-base shape: the captured backward runs dX and the bias gradient on a
+    # second stream beside dW, the eager one on one stream
+    ("row", torch.bfloat16, 768, 3072, 4096)])
+def test_captured_step_matches_eager_steps(tiling, dtype, fin, fout, tokens):
+    steps = 7
     eager, cap_layer = _pair(fin, fout, tiling, interval=3)
     gen = torch.Generator(device="cuda").manual_seed(5)
     xs = [torch.randn(tokens, fin, device="cuda", generator=gen).to(dtype) for _ in range(steps)]
