@@ -64,6 +64,28 @@ def test_noalloc_matches_workspace_entry_point(layout):
         _lib.set_vlut_splits(0)
 
 
+@pytest.mark.parametrize("layout", ["pairs", "tiled"])
+def test_noalloc_lds_table_method(layout):
+    """The LDS-table method (fp32 activations) through both entry points: its
+    split-major partials in the scratch, then a smaller call."""
+    import coset_amd as ca
+    from coset_amd import _lib
+    _lib.require_gpu()
+    lib = _lib.load()
+    torch.manual_seed(13)
+    rows, K = 1024, 2048
+    W = torch.randn(rows * K // 8, 8, device="cuda")
+    words = ca.hnlq_encode(W, 4, 2, 1.0).reshape(rows, K // 8, 2)
+    prep = ca.vlut_prepare(words, 4, layout=layout)
+    scale = torch.rand(rows, device="cuda") + 0.5
+    for B in (8, 3):
+        print(f"noalloc lds layout={layout} B={B}", flush=True)
+        a = torch.randn(B, K, device="cuda")
+        need, ref, out = _call_both(lib, _lib, prep.data, prep.word_format, a, scale, rows, K, method=1)
+        assert torch.equal(out, ref), (layout, B)
+        assert need > 0, "a K split: the call exercises the scratch"
+
+
 def test_noalloc_refuses_plans_beyond_its_scratch():
     from coset_amd import _lib
     _lib.require_gpu()
