@@ -272,41 +272,54 @@ __global__ void __launch_bounds__(kDeepNW * 64) vlut_deep_kernel(VlutMatmulArgs 
     }
 
     // the 8 waves' tiles summed in wave order through LDS (the activation
-    // buffer, no longer read), one 16-byte accumulator per (row tile, token
-    // tile) and lane: element i of acc[rt][s] in lane l is
-    // D[token 16 s + 4 (l / 16) + i][row 16 rt + l % 16]
+    // buffer, no longer read).  Element i of acc[rt][s] in lane l is
+    // D[token 16 s + 4 (l / 16) + i][row 16 rt + l % 16]; a wave stores it
+    // at red[((wave * 16 + rt * 4 + s) * 4 + i) * 64 + l], where rows
+    // 4 r .. 4 r + 3 of a row tile and token are 4 consecutive floats
     __syncthreads();
-    float4* red = reinterpret_cast<float4*>(s_act);
+    float* red = reinterpret_cast<float*>(s_act);
 #pragma unroll
     for (int rt = 0; rt < kDeepRT; ++rt)
 #pragma unroll
         for (int s = 0; s < 4; ++s)
-            red[(wave * 16 + rt * 4 + s) * 64 + lane] =
-                make_float4(acc[rt][s][0], acc[rt][s][1], acc[rt][s][2], acc[rt][s][3]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) red[((wave * 16 + rt * 4 + s) * 4 + i) * 64 + lane] = acc[rt][s][i];
     __syncthreads();
-    for (int e = threadIdx.x; e < 16 * 64; e += T) {
-        const int v4 = e >> 6, ln = e & 63;
+    // thread e: token t = e / 16 of the tile and its rows 4 (e % 16) .. + 3,
+    // so 16 threads write one token's 64 rows as 16-byte stores
+    for (int e = threadIdx.x; e < kDeepTokens * (kDeepRows / 4); e += T) {
+        const int t = e >> 4, q = e & 15;
+        const int s = t >> 4, g = (t >> 2) & 3, i = t & 3;
+        const int rt = q >> 2, r4 = 4 * (q & 3);
         float sum[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int wv = 0; wv < kDeepNW; ++wv) {
-            const float4 t = red[(wv * 16 + v4) * 64 + ln];
-            sum[0] += t.x;
-            sum[1] += t.y;
-            sum[2] += t.z;
-            sum[3] += t.w;
+            const float4 v = *reinterpret_cast<const float4*>(&red[((wv * 16 + rt * 4 + s) * 4 + i) * 64 + 16 * g + r4]);
+            sum[0] += v.x;
+            sum[1] += v.y;
+            sum[2] += v.z;
+            sum[3] += v.w;
         }
-        const int rt = v4 >> 2, s = v4 & 3;
-        const int64_t o = rb + 16 * rt + (ln & 15);
-        if (o >= p.rows) continue;
-        const float sc = p.scale ? (p.scale_mode == 0 ? p.scale[o] : 1.f / p.scale[o]) : 1.f;
+        const int64_t tok = t_base + t, o0 = rb + 16 * rt + r4;
+        if (tok >= p.B || o0 >= p.rows) continue;
+        float* dst;
+        if (gridDim.y == 1) {
+            dst = p.out + tok * p.rows + o0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int64_t tok = t_base + 16 * s + 4 * (ln >> 4) + i;
-            if (tok >= p.B) continue;
-            if (gridDim.y == 1)
-                p.out[tok * p.rows + o] = vlut_epilogue(sum[i] * 0.5f * sc, o, p.bias, p.lsq_alpha, p.lsq_qmax);
-            else
-                p.partial[((int64_t)blockIdx.y * p.B + tok) * p.rows + o] = sum[i];
+            for (int k = 0; k < 4; ++k) {
+                const int64_t o = o0 + k < p.rows ? o0 + k : p.rows - 1;
+                const float sc = p.scale ? (p.scale_mode == 0 ? p.scale[o] : 1.f / p.scale[o]) : 1.f;
+                sum[k] = vlut_epilogue(sum[k] * 0.5f * sc, o, p.bias, p.lsq_alpha, p.lsq_qmax);
+            }
+        } else {
+            dst = p.partial + ((int64_t)blockIdx.y * p.B + tok) * p.rows + o0;
+        }
+        if (o0 + 3 < p.rows && ((uintptr_t)dst & 15) == 0) {
+            *reinterpret_cast<float4*>(dst) = make_float4(sum[0], sum[1], sum[2], sum[3]);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (o0 + k < p.rows) dst[k] = sum[k];
         }
     }
 }
