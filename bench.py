@@ -547,10 +547,10 @@ def bench_c4(torch, ca, args):
     scale = torch.full((4096,), 0.02, device="cuda")
     del W
     res = {"workload": "C4 vLUT matmul 4096x4096 q4 M2 codes (8 MiB uint16 words; 16 MiB tiled prepared or "
-                       "decoded), fp16 activations, fp32 out; us_graph = per call replayed from a HIP graph "
+                       "decoded), fp16 activations (fp32_act_*: the same values in fp32), fp32 out; us_graph = per call replayed from a HIP graph "
                        "(weights warm in the 256 MB MALL), us_cold = one call after a 1 GiB write evicted the "
                        "caches (median of 25), us_eager = per call from Python",
-           "algorithmic_bytes": "8 MiB codes + B * 8 KiB fp16 activations + B * 16 KiB fp32 output "
+           "algorithmic_bytes": "8 MiB codes + B * 8 KiB fp16 (16 KiB fp32) activations + B * 16 KiB fp32 output "
                                 "(frac_hbm*); format_bytes counts the prepared format actually read",
            "batches": {}}
     ws = torch.empty(64 * 4096 * 64, dtype=torch.float32, device="cuda")
@@ -558,16 +558,19 @@ def bench_c4(torch, ca, args):
     words_host = words.cpu().numpy().astype(np.uint32) if args.cpu else None
     for B in (1, 8, 64):
         a = torch.randn((B, 4096), device="cuda", generator=g).to(torch.float16)
+        a32 = a.float()   # the same values as fp32 activations (the matrix cores take them as three bf16 planes)
         row = {}
         for method, wts in (("mfma", tiled), ("mfma_decoded", decoded), ("mfma_legacy_q", tiled_legacy),
-                            ("mfma_raw_words", words), ("lds", pairs), ("lds_tiled", tiled)):
-            m = "mfma" if method.startswith("mfma") else "lds"
-            fn = lambda: ca.vlut_matmul(wts, a, 4, scale=scale, method=m, workspace=ws)
+                            ("mfma_raw_words", words), ("lds", pairs), ("lds_tiled", tiled),
+                            ("fp32_act_mfma_decoded", decoded), ("fp32_act_lds", pairs)):
+            m = "lds" if method.endswith("lds") or method == "lds_tiled" else "mfma"
+            act = a32 if method.startswith("fp32") else a
+            fn = lambda: ca.vlut_matmul(wts, act, 4, scale=scale, method=m, workspace=ws)
             k_eager, _ = gpu_time(torch, fn, 50 if m == "lds" else 100, 5, 0.05)
             k = graph_time(torch, fn)
             kc = cold_time(torch, fn, flush)
             wbytes = wts.data.numel() * 4 if isinstance(wts, ca.PreparedWords) else wts.numel() * wts.element_size()
-            io_bytes = B * 4096 * 2 + B * 4096 * 4
+            io_bytes = B * 4096 * act.element_size() + B * 4096 * 4
             nbytes = C4_CODE_BYTES + io_bytes
             flops = 2.0 * B * 4096 * 4096
             row[method] = {"tokens_per_s": round(B / k, 1), "us_graph": round(k * 1e6, 2),

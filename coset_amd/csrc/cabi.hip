@@ -495,20 +495,32 @@ int coset_vlut_lookup_dot(const void* words, int64_t n_blocks, int q, int M, con
 static int vlut_method(int method, int act_dtype, int q, int M)
 {
     // the MFMA path multiplies 2*x_hat held exactly in fp16 (|v| < 2048)
-    // or bf16 (|v| < 256); max |2x_hat| <= 12 q^M at q <= 4
+    // or bf16 (|v| < 256); max |2x_hat| <= 12 q^M at q <= 4.  fp32
+    // activations run on it as three exact bf16 planes.
     int64_t qm = 1;
     for (int i = 0; i < M; ++i) qm *= q;
     bool exact = (act_dtype == COSET_F16 && 12 * qm < 2048) || (act_dtype == COSET_BF16 && 12 * qm < 256);
-    if (method == coset::VLUT_METHOD_MFMA && !exact) return -1;
-    if (method == coset::VLUT_METHOD_AUTO) return exact ? coset::VLUT_METHOD_MFMA : coset::VLUT_METHOD_LDS;
+    bool split = act_dtype == COSET_F32 && 12 * qm < 256;
+    if (method == coset::VLUT_METHOD_MFMA || method == coset::VLUT_METHOD_AUTO) {
+        if (exact) return coset::VLUT_METHOD_MFMA;
+        if (split) return coset::VLUT_METHOD_MFMA_SPLIT;
+        return method == coset::VLUT_METHOD_MFMA ? -1 : coset::VLUT_METHOD_LDS;
+    }
     return method;
+}
+
+// Workspace floats of a matmul under resolved method m.
+static int64_t vlut_method_workspace(int m, int64_t B, int64_t rows, int64_t K, int q, int M)
+{
+    if (m == coset::VLUT_METHOD_MFMA_SPLIT) return coset::vlut_split_workspace_floats(B, rows, K, q, M);
+    return coset::vlut_workspace_floats(coset::vlut_plan(rows, B, K, q, M, m), B, rows);
 }
 
 int64_t coset_vlut_workspace_floats(int64_t B, int64_t rows, int64_t K, int q, int M, int act_dtype, int method)
 {
     int m = vlut_method(method, act_dtype, q, M);
     if (m < 0 || B < 0 || rows < 0 || K < 8) return 0;
-    return coset::vlut_workspace_floats(coset::vlut_plan(rows, B, K, q, M, m), B, rows);
+    return vlut_method_workspace(m, B, rows, K, q, M);
 }
 
 int coset_d4_lattice_op(int op, const float* in, int64_t n_blocks, int q, float* out, void* stream)
@@ -659,14 +671,17 @@ static int vlut_matmul_impl(const void* words, int word_format, const float* sca
             return fail(COSET_EUNSUPPORTED, "the pairs format is read by the LDS-table method (1) only");
         if (method == coset::VLUT_METHOD_AUTO) method = coset::VLUT_METHOD_LDS;
     }
+    if (method < coset::VLUT_METHOD_AUTO || method > coset::VLUT_METHOD_MFMA)
+        return fail(COSET_EINVAL, "unknown method %d", method);
     int m = vlut_method(method, act_dtype, q, M);
-    if (m < 0) return fail(COSET_EUNSUPPORTED, "MFMA method needs fp16/bf16 activations holding 2*x_hat exactly");
-    if (m != coset::VLUT_METHOD_LDS && m != coset::VLUT_METHOD_MFMA) return fail(COSET_EINVAL, "unknown method %d", method);
+    if (m < 0) return fail(COSET_EUNSUPPORTED, "MFMA method needs activations holding 2*x_hat exactly (q^M too large)");
     if (B == 0 || rows == 0) return COSET_OK;
     if (!words || !act || !out) return fail(COSET_EINVAL, "NULL buffer");
     if (!aligned(act, 16) || !aligned(words, 4)) return fail(COSET_EINVAL, "act must be 16-byte aligned, words 4-byte");
-    const coset::VlutPlan plan = coset::vlut_plan(rows, B, K, q, M, m);
-    const int64_t need = coset::vlut_workspace_floats(plan, B, rows);
+    const bool split = m == coset::VLUT_METHOD_MFMA_SPLIT;
+    // the split path's inner product: 3B bf16 tokens on the matrix cores
+    const coset::VlutPlan plan = coset::vlut_plan(rows, split ? 3 * B : B, K, q, M, split ? coset::VLUT_METHOD_MFMA : m);
+    const int64_t need = vlut_method_workspace(m, B, rows, K, q, M);
     if (workspace_floats < need)
         return fail(COSET_EINVAL, "workspace holds %lld floats, needs %lld", (long long)workspace_floats,
                     (long long)need);
@@ -701,6 +716,7 @@ static int vlut_matmul_impl(const void* words, int word_format, const float* sca
         return fail(COSET_EINVAL, "decode tables not built on this device: call coset_init(device) first");
     }
     if (t->n_coarse > coset::kMaxCoarseVlut) return fail(COSET_EUNSUPPORTED, "too many coarse points");
+    if (split) return check_hip(coset::vlut_matmul_split(p, workspace, (hipStream_t)stream), "vLUT matmul launch");
     return check_hip(coset::vlut_matmul(p, plan, (hipStream_t)stream), "vLUT matmul launch");
 }
 
@@ -728,7 +744,7 @@ int coset_vlut_matmul_noalloc(const void* words, int word_format, const float* s
     const bool pairs_auto = word_format == coset::VLUT_PAIRS && method == coset::VLUT_METHOD_AUTO;
     const int m = vlut_method(pairs_auto ? coset::VLUT_METHOD_LDS : method, act_dtype, q, M);
     if (m >= 0 && B > 0 && rows > 0 && K >= 8 && q >= 2 && q <= 4 && M >= 1 && M <= 4) {
-        const int64_t need = coset::vlut_workspace_floats(coset::vlut_plan(rows, B, K, q, M, m), B, rows);
+        const int64_t need = vlut_method_workspace(m, B, rows, K, q, M);
         if (need > kNoallocScratchFloats)
             return fail(COSET_EINVAL,
                         "coset_vlut_matmul_noalloc: B=%lld rows=%lld K=%lld needs %lld floats of scratch, more than "

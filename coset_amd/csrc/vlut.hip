@@ -907,6 +907,95 @@ hipError_t vlut_prepare(const uint16_t* words, int64_t rows, int64_t kb, int M, 
 }
 
 
+// One fp32 activation per thread (four a thread): the three bf16 planes of
+// the exact split a = h1 + h2 + h3, h1 the top 16 bits of a, h2 those of
+// a - h1, h3 those of a - h1 - h2.  Each difference is exact (it keeps the
+// bits the truncation dropped), and a - h1 - h2 has at most 8 significant
+// bits, so h3 holds it exactly (for |a| above the bf16 subnormal range,
+// ~1e-33).  Infinities go to h1 whole, a NaN to h1 as a quiet NaN, with
+// h2 = h3 = 0, so the products see the value itself.
+__device__ __forceinline__ void split3(float a, uint16_t& h1, uint16_t& h2, uint16_t& h3)
+{
+    const uint32_t u = __float_as_uint(a);
+    if ((u & 0x7f800000u) == 0x7f800000u) {
+        h1 = (u & 0x007fffffu) ? (uint16_t)0x7fc0u : (uint16_t)(u >> 16);
+        h2 = h3 = 0;
+        return;
+    }
+    h1 = (uint16_t)(u >> 16);
+    const float r1 = __fsub_rn(a, __uint_as_float((uint32_t)h1 << 16));
+    h2 = (uint16_t)(__float_as_uint(r1) >> 16);
+    const float r2 = __fsub_rn(r1, __uint_as_float((uint32_t)h2 << 16));
+    h3 = (uint16_t)(__float_as_uint(r2) >> 16);
+}
+
+__global__ void __launch_bounds__(256) vlut_split_kernel(const float* __restrict__ act, int64_t n4,
+                                                        uint16_t* __restrict__ planes, int64_t plane)
+{
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n4) return;
+    const float4 v = reinterpret_cast<const float4*>(act)[i];
+    const float a[4] = {v.x, v.y, v.z, v.w};
+    uint16_t h[3][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) split3(a[j], h[0][j], h[1][j], h[2][j]);
+#pragma unroll
+    for (int p = 0; p < 3; ++p)
+        *reinterpret_cast<uint2*>(planes + p * plane + 4 * i) =
+            make_uint2((uint32_t)h[p][0] | ((uint32_t)h[p][1] << 16), (uint32_t)h[p][2] | ((uint32_t)h[p][3] << 16));
+}
+
+// out[b, o] = epilogue((y[b, o] + y[B + b, o]) + y[2B + b, o]) over the three
+// planes' scaled outputs y [3B, rows]
+__global__ void __launch_bounds__(256) vlut_split_sum_kernel(const float* __restrict__ y, int64_t B, int64_t rows,
+                                                            const float* bias, const float* lsq_alpha, int lsq_qmax,
+                                                            float* __restrict__ out)
+{
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t n = B * rows;
+    if (i >= n) return;
+    const float v = __fadd_rn(__fadd_rn(y[i], y[n + i]), y[2 * n + i]);
+    out[i] = vlut_epilogue(v, i % rows, bias, lsq_alpha, lsq_qmax);
+}
+
+namespace {
+
+constexpr int64_t align64(int64_t n) { return (n + 63) / 64 * 64; }
+
+}  // namespace
+
+int64_t vlut_split_workspace_floats(int64_t B, int64_t rows, int64_t K, int q, int M)
+{
+    const int64_t planes = align64(3 * B * K / 2), outs = align64(3 * B * rows);
+    return planes + outs + vlut_workspace_floats(vlut_plan(rows, 3 * B, K, q, M, VLUT_METHOD_MFMA), 3 * B, rows);
+}
+
+hipError_t vlut_matmul_split(VlutMatmulArgs p, float* workspace, hipStream_t s)
+{
+    if (p.B == 0 || p.rows == 0) return hipSuccess;
+    const int64_t B = p.B, n = B * p.K;
+    uint16_t* planes = reinterpret_cast<uint16_t*>(workspace);
+    float* y = workspace + align64(3 * B * p.K / 2);
+    float* inner = y + align64(3 * B * p.rows);
+    hipLaunchKernelGGL(vlut_split_kernel, dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, s,
+                       static_cast<const float*>(p.act), n / 4, planes, n);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    VlutMatmulArgs q = p;
+    q.act = planes;
+    q.act_dtype = DT_BF16;
+    q.B = 3 * B;
+    q.out = y;
+    q.partial = inner;
+    q.bias = nullptr;
+    q.lsq_alpha = nullptr;
+    e = vlut_matmul(q, vlut_plan(p.rows, 3 * B, p.K, p.q, p.M, VLUT_METHOD_MFMA), s);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(vlut_split_sum_kernel, dim3((unsigned)((B * p.rows + 255) / 256)), dim3(256), 0, s, y, B,
+                       p.rows, p.bias, p.lsq_alpha, p.lsq_qmax, p.out);
+    return hipGetLastError();
+}
+
 hipError_t vlut_matmul(VlutMatmulArgs p, const VlutPlan& plan, hipStream_t s)
 {
     if (p.B == 0 || p.rows == 0) return hipSuccess;

@@ -8,7 +8,9 @@ namespace coset {
 
 constexpr int kMaxCoarseVlut = 640;  // LDS table slots for <a, c> (637 at q = 4)
 
-enum VlutMethod { VLUT_METHOD_AUTO = 0, VLUT_METHOD_LDS = 1, VLUT_METHOD_MFMA = 2 };
+// VLUT_METHOD_MFMA_SPLIT is internal: method MFMA with fp32 activations,
+// each split exactly into three bf16 planes that run on the matrix cores
+enum VlutMethod { VLUT_METHOD_AUTO = 0, VLUT_METHOD_LDS = 1, VLUT_METHOD_MFMA = 2, VLUT_METHOD_MFMA_SPLIT = 3 };
 
 // Weight formats (include/coset_amd.h): raw uint16 words, row-major
 // prepared uint32 (cid << 16 | idx), tiled prepared (matrix-core fragments).
@@ -96,6 +98,13 @@ inline int64_t vlut_workspace_floats(const VlutPlan& plan, int64_t B, int64_t ro
 hipError_t vlut_build(const float* a, int64_t n_queries, int q, int legacy, float* vlut, hipStream_t s);
 hipError_t vlut_dot(const void* words, int64_t n, int M, int q, const float* vlut, float* out, hipStream_t s);
 hipError_t vlut_matmul(VlutMatmulArgs p, const VlutPlan& plan, hipStream_t s);
+// fp32 activations on the matrix cores: a = h1 + h2 + h3 with each h the
+// bf16 truncation of what the previous ones leave (exact: 3 x 8 significant
+// bits), the three planes multiplied as 3B tokens of bf16 and summed per
+// output.  The workspace holds the planes, the planes' outputs and the inner
+// product's own partials.
+int64_t vlut_split_workspace_floats(int64_t B, int64_t rows, int64_t K, int q, int M);
+hipError_t vlut_matmul_split(VlutMatmulArgs p, float* workspace, hipStream_t s);
 // prepared = cid(word) << 16 | word for raw words [rows, kb, M]: the
 // coarse-point id each level word decodes through, stored next to it so the
 // matmul needs no map lookup; fmt VLUT_PREPARED keeps the layout,

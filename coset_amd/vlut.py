@@ -247,6 +247,10 @@ def vlut_matmul(words, act: torch.Tensor, q: int = 4, *, scale: Optional[torch.T
     convention).  With the core rule (legacy=False) the result equals
     act @ (e8_decode(codes) * s)^T.
 
+    method: "lds" (per-token inner-product tables in LDS), "mfma" (decoded
+    weights on the matrix cores; fp32 activations run as three exact bf16
+    planes) or "auto" (mfma wherever 2 x_hat is exact in the operand type).
+
     Epilogue, fused into the output write (coset_vlut_linear): ``bias``
     [rows] is added, then ``act_quant = (alpha, qmax)`` applies the LSQ
     activation quantizer with that parameter (inference: no gradient).

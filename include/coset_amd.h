@@ -258,7 +258,9 @@ int coset_vlut_prepare(const void* words, int64_t rows, int64_t kb, int M, int q
  * LDS, factorized over the coordinate pairs of r: <a, r(b)> = sum_p
  * <(a_2p, a_2p+1), r_p(b)>, four lookups per level word (any activation
  * dtype); method 2 decodes 2*x_hat and runs the product on the matrix cores
- * (fp16/bf16 activations holding 2*x_hat exactly); 0 picks 2 when it is
+ * (fp16/bf16 activations holding 2*x_hat exactly; fp32 activations as three
+ * bf16 planes, a = h1 + h2 + h3 exactly, multiplied as 3B tokens and summed
+ * per output, where bf16 holds 2*x_hat exactly); 0 picks 2 when it is
  * exact, and 1 for format 4.  workspace: caller-owned fp32 scratch of
  * coset_vlut_workspace_floats floats (0 is a valid size; query with method 1
  * for format 4).

@@ -135,8 +135,6 @@ def mfma_decode(request):
 @pytest.mark.parametrize("adt", [torch.float16, torch.bfloat16, torch.float32])
 def test_vlut_matmul_vs_oracle(method, B, adt, mfma_decode):
     import coset_amd
-    if method == "mfma" and adt == torch.float32:
-        pytest.skip("MFMA path takes fp16/bf16 activations")
     if method == "lds" and mfma_decode == "integer":
         pytest.skip("decoder choice applies to the MFMA path")
     rng = np.random.default_rng(B)
@@ -188,6 +186,91 @@ def test_vlut_matmul_other_levels(q, M, B, mfma_decode):
                     continue
                 out = coset_amd.vlut_matmul(w, a.cuda(), q, legacy=legacy, method=method).cpu().numpy()
                 close(out, ref, mag, 1e-3)
+
+
+@pytest.mark.parametrize("q,M", [(4, 2), (4, 1), (2, 3), (2, 4)])
+@pytest.mark.parametrize("B", [1, 5, 11, 40])
+def test_fp32_activations_on_matrix_cores(q, M, B):
+    """fp32 activations on the MFMA method: each value split exactly into
+    three bf16 planes (3B tokens), the planes' products summed per output;
+    against the oracle's lookup sum (elementwise 1e-3 of the summands'
+    magnitude), every weight format, both rules, with the bias + LSQ epilogue
+    applied after the sum, and "auto" taking the same path."""
+    import coset_amd
+    rng = np.random.default_rng(7 * B + q + M)
+    rows, K = 72, 136                        # 17 k-blocks
+    W = rng.standard_normal((rows, K)).astype(np.float32)
+    codes = O.e8_encode(W.reshape(-1, 8), q, M)
+    words_np = O.pack_words(codes, q).reshape(rows, K // 8, M)
+    words = torch.from_numpy(words_np.astype(np.int32)).to(torch.uint16).cuda()
+    # magnitudes over 60 binades, so the low planes carry real bits
+    a_np = (rng.standard_normal((B, K)) * np.exp2(rng.integers(-30, 30, (B, K)))).astype(np.float32)
+    a = torch.from_numpy(a_np).cuda()
+    scale = rng.uniform(0.5, 2.0, rows).astype(np.float32)
+    for legacy in (False, True):
+        ref = O.vlut_matmul(words_np, scale, a_np, q, M, legacy=legacy)
+        mag = matmul_mag(words_np, q, M, a_np, scale, 0, legacy)
+        forms = [words] + [coset_amd.vlut_prepare(words, q, legacy=legacy, layout=lay)
+                           for lay in ("rowmajor", "tiled", "decoded")]
+        for w in forms:
+            for method in ("mfma", "auto"):
+                out = coset_amd.vlut_matmul(w, a, q, scale=torch.from_numpy(scale), legacy=legacy, method=method)
+                close(out.cpu().numpy(), ref, mag, 1e-3)
+    # epilogue after the three planes' sum: bias, then the LSQ kernel's quantizer
+    sc, bias = torch.from_numpy(scale).cuda(), torch.from_numpy(rng.standard_normal(rows).astype(np.float32)).cuda()
+    m = coset_amd.LSQActivation(bit_width=6, init_alpha=3.0).cuda()
+    plain = coset_amd.vlut_matmul(words, a, q, scale=sc, method="mfma")
+    only_bias = coset_amd.vlut_matmul(words, a, q, scale=sc, bias=bias, method="mfma")
+    fused = coset_amd.vlut_matmul(words, a, q, scale=sc, bias=bias, act_quant=(m.alpha, m.qmax), method="mfma")
+    assert torch.equal(only_bias, plain + bias)
+    with torch.no_grad():
+        assert torch.equal(fused, m(plain + bias))
+
+
+def test_fp32_split_special_values():
+    """Infinities and NaN in fp32 activations reach the products whole (the
+    planes after them hold 0): an output is finite exactly where the oracle's
+    fp32 table sum is (which of NaN and +-inf a non-finite output takes can
+    differ: the matrix-core method multiplies the decoded weight, the tables
+    multiply each level's residual), a NaN activation makes its token's
+    outputs NaN, and finite outputs agree with the oracle."""
+    import coset_amd
+    rng = np.random.default_rng(31)
+    rows, K, q, M = 48, 64, 4, 2
+    W = rng.standard_normal((rows, K)).astype(np.float32)
+    codes = O.e8_encode(W.reshape(-1, 8), q, M)
+    words_np = O.pack_words(codes, q).reshape(rows, K // 8, M)
+    words = torch.from_numpy(words_np.astype(np.int32)).to(torch.uint16).cuda()
+    a_np = rng.standard_normal((6, K)).astype(np.float32)
+    a_np[1, 3] = np.inf
+    a_np[2, 10] = -np.inf
+    a_np[3, 20] = np.nan
+    a_np[4, 5], a_np[4, 40] = np.inf, -np.inf
+    a_np[5] *= np.float32(1e30)
+    ref = O.vlut_matmul(words_np, np.ones(rows, np.float32), a_np, q, M)
+    out = coset_amd.vlut_matmul(words, torch.from_numpy(a_np).cuda(), q, method="mfma").cpu().numpy()
+    fin = np.isfinite(ref)
+    assert np.array_equal(np.isfinite(out), fin)
+    assert np.isnan(out[3]).all() and not fin[1:5].any() and fin[[0, 5]].all()
+    mag = matmul_mag(words_np, q, M, np.where(np.isfinite(a_np), a_np, 0))
+    close(out[fin], ref[fin], mag[fin], 1e-3)
+
+
+def test_fp32_mfma_needs_exact_operands():
+    """q = 4, M = 3 decodes beyond what bf16 holds exactly: method "mfma"
+    refuses fp32 activations there, "auto" takes the LDS-table method."""
+    import coset_amd
+    rng = np.random.default_rng(2)
+    rows, K, q, M = 16, 32, 4, 3
+    codes = O.e8_encode(rng.standard_normal((rows * K // 8, 8)).astype(np.float32), q, M)
+    words_np = O.pack_words(codes, q).reshape(rows, K // 8, M)
+    words = torch.from_numpy(words_np.astype(np.int32)).to(torch.uint16).cuda()
+    a_np = rng.standard_normal((3, K)).astype(np.float32)
+    with pytest.raises(Exception):
+        coset_amd.vlut_matmul(words, torch.from_numpy(a_np).cuda(), q, method="mfma")
+    out = coset_amd.vlut_matmul(words, torch.from_numpy(a_np).cuda(), q, method="auto").cpu().numpy()
+    close(out, O.vlut_matmul(words_np, np.ones(rows, np.float32), a_np, q, M),
+          matmul_mag(words_np, q, M, a_np), 1e-3)
 
 
 @pytest.mark.parametrize("splits", [1, 2, 5, 64])
@@ -423,5 +506,7 @@ def test_decoded_format_rejects_what_it_cannot_hold():
     with pytest.raises(Exception):
         ca.vlut_prepare(words, 4, layout="decoded")      # q = 4, M = 3 overflows a byte
     dec = ca.vlut_prepare(torch.zeros(16, 4, 2, dtype=torch.uint16, device="cuda"), 4, layout="decoded")
+    a = torch.randn(2, 32, device="cuda")
     with pytest.raises(Exception):
-        ca.vlut_matmul(dec, torch.randn(2, 32, device="cuda"))   # fp32 activations: no matrix-core path
+        ca.vlut_matmul(dec, a, method="lds")                 # the LDS-table method reads no decoded bytes
+    assert torch.equal(ca.vlut_matmul(dec, a), torch.zeros(2, 16, device="cuda"))   # fp32: the three-plane path
