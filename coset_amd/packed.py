@@ -118,8 +118,8 @@ class PackedLinear(nn.Module):
         in the matmul's epilogue."""
         lead = x.shape[:-1]
         a = x.reshape(-1, self.in_features)
-        if a.dtype not in (torch.float16, torch.bfloat16):
-            a = a.to(torch.bfloat16)
+        if a.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+            a = a.float()   # fp32 runs on the matrix cores as three exact bf16 planes
         aq = None if self.act_alpha is None else (self.act_alpha, self.act_qmax)
         y = vlut_matmul(self.prepared, a, scale=self.beta, scale_mode="div", bias=self.bias, act_quant=aq)
         return y.reshape(*lead, self.out_features)

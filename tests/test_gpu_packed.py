@@ -30,7 +30,7 @@ def test_save_load_serves_the_layer(tmp_path):
     # decode(words) / beta is the layer's W_q bit for bit (nothing clipped)
     torch.testing.assert_close(pl.dequantized_weight(), W_q.float(), rtol=0, atol=0)
     x = torch.randn(5, 3, 256, device="cuda")
-    for dt in (torch.float16, torch.bfloat16):
+    for dt in (torch.float16, torch.bfloat16, torch.float32):
         xa = x.to(dt)
         y = pl(xa)
         ref = F.linear(xa.float(), W_q.float(), layer.bias.float())
