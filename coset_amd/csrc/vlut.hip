@@ -180,9 +180,12 @@ __global__ void __launch_bounds__(256) vlut_dot_kernel(const void* words, int wo
 //   vLUT_a[idx(b)] = <a, r(b)> = sum_p T[72 p + id_p(b)].
 // Workgroup: 4 waves x 2 tiles of 64 rows (512 rows) x a K range (grid.y
 // splits) x TT tokens (grid.z); a lane owns one row of each of its wave's
-// tiles.  Every lookup instruction of a wave reads one sub-table (one token,
-// one k-block), 72 entries over the LDS banks, so its 64 lanes conflict only
-// where two ids 64 apart meet; lanes with the same id share the read.  The
+// tiles.  The tables of a k-block are interleaved in planes of VW = min(TT,
+// 4) tokens, entry-major (plane h: T[(72 p + id) VW + c] for token h VW + c),
+// so one lookup instruction reads an entry for VW tokens at once (16 bytes a
+// lane at VW = 4, with consecutive ids 16 bytes apart over the banks): a
+// quarter of the gather instructions of one table per token, the same bytes.
+// Lanes with the same id share the read.  The
 // K range runs in chunks of KB k-blocks: the chunk's activations and level
 // words are loaded (the words as pair ids; one 256-byte read per wave and
 // word in the pairs format), the activations staged and the tables built
@@ -191,6 +194,18 @@ constexpr int kLdsWaves = 4;
 constexpr int kLdsTiles = 2;                          // 64-row tiles per wave
 constexpr int kLdsRows = kLdsWaves * kLdsTiles * 64;  // rows per workgroup
 constexpr int kLdsTable = 4 * kPairSlots + 1;         // floats per (token, k-block) table
+
+// 1, 2 or 4 consecutive table entries (one per token) as one LDS read
+template <int N>
+struct LdsVec {
+    typedef float type __attribute__((ext_vector_type(N)));
+    static __device__ __forceinline__ float at(const type& v, int c) { return v[c]; }
+};
+template <>
+struct LdsVec<1> {
+    typedef float type;
+    static __device__ __forceinline__ float at(const type& v, int) { return v; }
+};
 
 template <int TT>
 struct LdsChunk {
@@ -205,8 +220,10 @@ template <int Q, int M, int TT, bool PAIRS>
 __global__ void __launch_bounds__(kLdsWaves * 64) vlut_lds_kernel(VlutMatmulArgs p)
 {
     constexpr int KB = LdsChunk<TT>::KB;
-    constexpr int NTAB = TT * KB;  // tables per chunk: token t, k-block j at t * KB + j
-    __shared__ float s_tab[NTAB * kLdsTable];
+    constexpr int NTAB = TT * KB;  // tables per chunk; s_act holds token t, k-block j at t * KB + j
+    constexpr int VW = TT < 4 ? TT : 4;  // tokens per lookup
+    using vecw_t = typename LdsVec<VW>::type;
+    __shared__ __align__(16) float s_tab[NTAB * kLdsTable];
     __shared__ float2 s_pv[4 * kPairSlots];
     __shared__ float s_act[NTAB * 8];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -285,12 +302,16 @@ __global__ void __launch_bounds__(kLdsWaves * 64) vlut_lds_kernel(VlutMatmulArgs
             if (e < NTAB * 8) s_act[e] = act_value(av[u], p.act_dtype);
         }
         __syncthreads();
+        // table entry e: token c = e % VW of plane h, slot, k-block j, at
+        // ((j (TT / VW) + h) kLdsTable + slot) VW + c
         for (int e = threadIdx.x; e < NTAB * kLdsTable; e += blockDim.x) {
-            const int tab = e / kLdsTable, slot = e - tab * kLdsTable;
+            const int c = e % VW, rest = e / VW;
+            const int jh = rest / kLdsTable, slot = rest - jh * kLdsTable;
+            const int j = jh / (TT / VW), t = (jh % (TT / VW)) * VW + c;
             float v = 0.f;
             if (slot < 4 * kPairSlots) {
                 const float2 r = s_pv[slot];
-                const float* a = s_act + tab * 8 + 2 * (slot / kPairSlots);
+                const float* a = s_act + (t * KB + j) * 8 + 2 * (slot / kPairSlots);
                 v = __fmaf_rn(a[1], r.y, a[0] * r.x);
             }
             s_tab[e] = v;
@@ -310,10 +331,18 @@ __global__ void __launch_bounds__(kLdsWaves * 64) vlut_lds_kernel(VlutMatmulArgs
                     const uint32_t id2 = min((w >> 16) & 0xffu, kPairSlots - 1u) + 2 * kPairSlots;
                     const uint32_t id3 = min(w >> 24, kPairSlots - 1u) + 3 * kPairSlots;
 #pragma unroll
-                    for (int t = 0; t < TT; ++t) {
-                        const float* T = s_tab + (t * KB + j) * kLdsTable;
-                        const float v = (T[id0] + T[id1]) + (T[id2] + T[id3]);
-                        acc[i][t] = __fmaf_rn(qm, v, acc[i][t]);
+                    for (int h = 0; h < TT / VW; ++h) {
+                        const float* T = s_tab + (j * (TT / VW) + h) * kLdsTable * VW;
+                        const vecw_t x0 = *reinterpret_cast<const vecw_t*>(T + id0 * VW);
+                        const vecw_t x1 = *reinterpret_cast<const vecw_t*>(T + id1 * VW);
+                        const vecw_t x2 = *reinterpret_cast<const vecw_t*>(T + id2 * VW);
+                        const vecw_t x3 = *reinterpret_cast<const vecw_t*>(T + id3 * VW);
+#pragma unroll
+                        for (int c = 0; c < VW; ++c) {
+                            const float v = (LdsVec<VW>::at(x0, c) + LdsVec<VW>::at(x1, c)) +
+                                            (LdsVec<VW>::at(x2, c) + LdsVec<VW>::at(x3, c));
+                            acc[i][h * VW + c] = __fmaf_rn(qm, v, acc[i][h * VW + c]);
+                        }
                     }
                     qm *= (float)Q;
                 }
