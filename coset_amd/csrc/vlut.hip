@@ -200,11 +200,13 @@ template <int N>
 struct LdsVec {
     typedef float type __attribute__((ext_vector_type(N)));
     static __device__ __forceinline__ float at(const type& v, int c) { return v[c]; }
+    static __device__ __forceinline__ void set(type& v, int c, float x) { v[c] = x; }
 };
 template <>
 struct LdsVec<1> {
     typedef float type;
     static __device__ __forceinline__ float at(const type& v, int) { return v; }
+    static __device__ __forceinline__ void set(type& v, int, float x) { v = x; }
 };
 
 template <int TT>
@@ -225,7 +227,7 @@ __global__ void __launch_bounds__(kLdsWaves * 64) vlut_lds_kernel(VlutMatmulArgs
     using vecw_t = typename LdsVec<VW>::type;
     __shared__ __align__(16) float s_tab[NTAB * kLdsTable];
     __shared__ float2 s_pv[4 * kPairSlots];
-    __shared__ float s_act[NTAB * 8];
+    __shared__ __align__(8) float s_act[NTAB * 8];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t kb_total = p.K / 8;
     const int64_t kb_wg = (kb_total + gridDim.y - 1) / gridDim.y;
@@ -302,19 +304,31 @@ __global__ void __launch_bounds__(kLdsWaves * 64) vlut_lds_kernel(VlutMatmulArgs
             if (e < NTAB * 8) s_act[e] = act_value(av[u], p.act_dtype);
         }
         __syncthreads();
-        // table entry e: token c = e % VW of plane h, slot, k-block j, at
-        // ((j (TT / VW) + h) kLdsTable + slot) VW + c
-        for (int e = threadIdx.x; e < NTAB * kLdsTable; e += blockDim.x) {
-            const int c = e % VW, rest = e / VW;
-            const int jh = rest / kLdsTable, slot = rest - jh * kLdsTable;
-            const int j = jh / (TT / VW), t = (jh % (TT / VW)) * VW + c;
-            float v = 0.f;
-            if (slot < 4 * kPairSlots) {
-                const float2 r = s_pv[slot];
-                const float* a = s_act + (t * KB + j) * 8 + 2 * (slot / kPairSlots);
-                v = __fmaf_rn(a[1], r.y, a[0] * r.x);
+        // table item it = jh kLdsTable + slot: the VW entries of plane h of
+        // k-block j (jh = j (TT / VW) + h) at that slot, tokens h VW + c, at
+        // (jh kLdsTable + slot) VW + c.  A thread's items step by the
+        // workgroup size, so (jh, slot) advance without a division.
+        static_assert(kLdsWaves * 64 < kLdsTable, "one wrap of the slot per step");
+        {
+            int jh = 0, slot = threadIdx.x;
+            for (int it = threadIdx.x; it < (NTAB / VW) * kLdsTable; it += kLdsWaves * 64) {
+                const int j = jh / (TT / VW), h = jh % (TT / VW);
+                const int pp = (slot >= kPairSlots) + (slot >= 2 * kPairSlots) + (slot >= 3 * kPairSlots);
+                const bool live = slot < 4 * kPairSlots;
+                const float2 r = s_pv[live ? slot : 0];
+                vecw_t v;
+#pragma unroll
+                for (int c = 0; c < VW; ++c) {
+                    const float2 a = *reinterpret_cast<const float2*>(s_act + ((h * VW + c) * KB + j) * 8 + 2 * pp);
+                    LdsVec<VW>::set(v, c, live ? __fmaf_rn(a.y, r.y, a.x * r.x) : 0.f);
+                }
+                *reinterpret_cast<vecw_t*>(s_tab + it * VW) = v;
+                slot += kLdsWaves * 64;
+                if (slot >= kLdsTable) {
+                    slot -= kLdsTable;
+                    ++jh;
+                }
             }
-            s_tab[e] = v;
         }
         __syncthreads();
 #pragma unroll
