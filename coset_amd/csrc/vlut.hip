@@ -178,7 +178,7 @@ __global__ void __launch_bounds__(256) vlut_dot_kernel(const void* words, int wo
 //   T[72 p + id] = a_2p r_2p(id) + a_2p+1 r_2p+1(id)     p = 0..3
 // (289 floats; 261 used at q = 4) and a level word costs four lookups:
 //   vLUT_a[idx(b)] = <a, r(b)> = sum_p T[72 p + id_p(b)].
-// Workgroup: 4 waves x 2 tiles of 64 rows (512 rows) x a K range (grid.y
+// Workgroup: 4 waves x 2 or 4 tiles of 64 rows (512 or 1024 rows) x a K range (grid.y
 // splits) x TT tokens (grid.z); a lane owns one row of each of its wave's
 // tiles.  The tables of a k-block are interleaved in planes of VW = min(TT,
 // 4) tokens, entry-major (plane h: T[(72 p + id) VW + c] for token h VW + c),
@@ -191,8 +191,11 @@ __global__ void __launch_bounds__(256) vlut_dot_kernel(const void* words, int wo
 // word in the pairs format), the activations staged and the tables built
 // while the word loads are in flight, then the tables are read.
 constexpr int kLdsWaves = 4;
-constexpr int kLdsTiles = 2;                          // 64-row tiles per wave
-constexpr int kLdsRows = kLdsWaves * kLdsTiles * 64;  // rows per workgroup
+// 64-row tiles per wave: 2 (512 rows per workgroup), or 4 (1024 rows) from
+// 32 tokens on, where each table built serves twice the rows -- the builds,
+// one per (row group, token, k-block), take more time than the lookups there
+__host__ __device__ constexpr int lds_tiles(int64_t B) { return B >= 32 ? 4 : 2; }
+__host__ __device__ constexpr int64_t lds_rows(int64_t B) { return kLdsWaves * lds_tiles(B) * 64; }
 constexpr int kLdsTable = 4 * kPairSlots + 1;         // floats per (token, k-block) table
 
 // 1, 2 or 4 consecutive table entries (one per token) as one LDS read
@@ -218,9 +221,10 @@ struct LdsChunk {
 // (raw, row-major or tiled) are loaded first and their pair ids gathered
 // from pair_map after, each phase issued whole (no load waits behind a
 // per-word branch).
-template <int Q, int M, int TT, bool PAIRS>
+template <int Q, int M, int TT, int kLdsTiles, bool PAIRS>
 __global__ void __launch_bounds__(kLdsWaves * 64) vlut_lds_kernel(VlutMatmulArgs p)
 {
+    constexpr int kLdsRows = kLdsWaves * kLdsTiles * 64;  // rows per workgroup
     constexpr int KB = LdsChunk<TT>::KB;
     constexpr int NTAB = TT * KB;  // tables per chunk; s_act holds token t, k-block j at t * KB + j
     constexpr int VW = TT < 4 ? TT : 4;  // tokens per lookup
@@ -727,13 +731,18 @@ template <int Q, int M, bool PAIRS>
 void launch_lds_fmt(const VlutMatmulArgs& p, int splits, hipStream_t s)
 {
     const int TT = lds_tokens(p.B);
-    dim3 grid((unsigned)((p.rows + kLdsRows - 1) / kLdsRows), (unsigned)splits, (unsigned)((p.B + TT - 1) / TT));
+    const int64_t rows_wg = lds_rows(p.B);
+    dim3 grid((unsigned)((p.rows + rows_wg - 1) / rows_wg), (unsigned)splits, (unsigned)((p.B + TT - 1) / TT));
     dim3 block(kLdsWaves * 64);
+    if (lds_tiles(p.B) == 4) {   // B >= 32: TT = 8
+        hipLaunchKernelGGL((vlut_lds_kernel<Q, M, 8, 4, PAIRS>), grid, block, 0, s, p);
+        return;
+    }
     switch (TT) {
-    case 8: hipLaunchKernelGGL((vlut_lds_kernel<Q, M, 8, PAIRS>), grid, block, 0, s, p); break;
-    case 4: hipLaunchKernelGGL((vlut_lds_kernel<Q, M, 4, PAIRS>), grid, block, 0, s, p); break;
-    case 2: hipLaunchKernelGGL((vlut_lds_kernel<Q, M, 2, PAIRS>), grid, block, 0, s, p); break;
-    default: hipLaunchKernelGGL((vlut_lds_kernel<Q, M, 1, PAIRS>), grid, block, 0, s, p); break;
+    case 8: hipLaunchKernelGGL((vlut_lds_kernel<Q, M, 8, 2, PAIRS>), grid, block, 0, s, p); break;
+    case 4: hipLaunchKernelGGL((vlut_lds_kernel<Q, M, 4, 2, PAIRS>), grid, block, 0, s, p); break;
+    case 2: hipLaunchKernelGGL((vlut_lds_kernel<Q, M, 2, 2, PAIRS>), grid, block, 0, s, p); break;
+    default: hipLaunchKernelGGL((vlut_lds_kernel<Q, M, 1, 2, PAIRS>), grid, block, 0, s, p); break;
     }
 }
 
@@ -837,10 +846,10 @@ VlutPlan vlut_plan(int64_t rows, int64_t B, int64_t K, int q, int M, int method)
 {
     const int64_t kb = K / 8;
     if (method == VLUT_METHOD_LDS) {
-        // 512-row, TT-token workgroups, with K splits for two per CU (each
-        // keeping at least one k-block)
+        // 512- or 1024-row, TT-token workgroups, with K splits for two per
+        // CU (each keeping at least one k-block)
         const int TT = lds_tokens(B);
-        const int64_t groups = ((rows + kLdsRows - 1) / kLdsRows) * ((B + TT - 1) / TT);
+        const int64_t groups = ((rows + lds_rows(B) - 1) / lds_rows(B)) * ((B + TT - 1) / TT);
         int64_t splits = g_vlut_splits > 0 ? g_vlut_splits
                                            : (2 * device_cu_count() + groups - 1) / std::max<int64_t>(1, groups);
         return {VK_LDS, (int)std::max<int64_t>(1, std::min<int64_t>(splits, kb))};
