@@ -671,6 +671,44 @@ __global__ void __launch_bounds__(256) vlut_reduce_sm4_kernel(const float* parti
     reinterpret_cast<float4*>(out)[i4] = make_float4(r[0], r[1], r[2], r[3]);
 }
 
+// The same for three planes of nb tokens (B = 3 nb, rows % 4 == 0): each
+// plane's splits are summed and scaled as above, then the planes are added
+// in order and the epilogue applied; out is [nb, rows].
+__global__ void __launch_bounds__(256) vlut_reduce_planes4_kernel(const float* partial, int splits, int64_t nb,
+                                                                 int64_t rows, const float* scale, int scale_mode,
+                                                                 float mult, const float* bias,
+                                                                 const float* lsq_alpha, int lsq_qmax, float* out)
+{
+    const int64_t m4 = nb * rows / 4, n4 = 3 * m4;
+    const int64_t i4 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i4 >= m4) return;
+    const float4* p4 = reinterpret_cast<const float4*>(partial);
+    const int64_t o0 = (4 * i4) % rows;
+    float y[3][4];
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl) {
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int s = 0; s < splits; ++s) {
+            const float4 v = p4[s * n4 + pl * m4 + i4];
+            acc[0] += v.x;
+            acc[1] += v.y;
+            acc[2] += v.z;
+            acc[3] += v.w;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t o = o0 + j;
+            const float sc = scale ? (scale_mode == 0 ? scale[o] : 1.f / scale[o]) : 1.f;
+            y[pl][j] = acc[j] * mult * sc;
+        }
+    }
+    float r[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        r[j] = vlut_epilogue(__fadd_rn(__fadd_rn(y[0][j], y[1][j]), y[2][j]), o0 + j, bias, lsq_alpha, lsq_qmax);
+    reinterpret_cast<float4*>(out)[i4] = make_float4(r[0], r[1], r[2], r[3]);
+}
+
 // The same for many splits and few outputs (the LDS-table kernel at small
 // batches): a workgroup takes 16 output quads with 16 threads per quad, each
 // summing every 16th split in order; the 16 sums of a quad are added in a
@@ -959,28 +997,7 @@ hipError_t vlut_prepare(const uint16_t* words, int64_t rows, int64_t kb, int M, 
 }
 
 
-// One fp32 activation per thread (four a thread): the three bf16 planes of
-// the exact split a = h1 + h2 + h3, h1 the top 16 bits of a, h2 those of
-// a - h1, h3 those of a - h1 - h2.  Each difference is exact (it keeps the
-// bits the truncation dropped), and a - h1 - h2 has at most 8 significant
-// bits, so h3 holds it exactly (for |a| above the bf16 subnormal range,
-// ~1e-33).  Infinities go to h1 whole, a NaN to h1 as a quiet NaN, with
-// h2 = h3 = 0, so the products see the value itself.
-__device__ __forceinline__ void split3(float a, uint16_t& h1, uint16_t& h2, uint16_t& h3)
-{
-    const uint32_t u = __float_as_uint(a);
-    if ((u & 0x7f800000u) == 0x7f800000u) {
-        h1 = (u & 0x007fffffu) ? (uint16_t)0x7fc0u : (uint16_t)(u >> 16);
-        h2 = h3 = 0;
-        return;
-    }
-    h1 = (uint16_t)(u >> 16);
-    const float r1 = __fsub_rn(a, __uint_as_float((uint32_t)h1 << 16));
-    h2 = (uint16_t)(__float_as_uint(r1) >> 16);
-    const float r2 = __fsub_rn(r1, __uint_as_float((uint32_t)h2 << 16));
-    h3 = (uint16_t)(__float_as_uint(r2) >> 16);
-}
-
+// One fp32 activation per thread (four a thread), split by split3 (vlut_mfma.hpp).
 __global__ void __launch_bounds__(256) vlut_split_kernel(const float* __restrict__ act, int64_t n4,
                                                         uint16_t* __restrict__ planes, int64_t plane)
 {
@@ -1029,19 +1046,35 @@ hipError_t vlut_matmul_split(VlutMatmulArgs p, float* workspace, hipStream_t s)
     uint16_t* planes = reinterpret_cast<uint16_t*>(workspace);
     float* y = workspace + align64(3 * B * p.K / 2);
     float* inner = y + align64(3 * B * p.rows);
+    VlutMatmulArgs q = p;
+    q.act_dtype = DT_BF16;
+    q.B = 3 * B;
+    q.partial = inner;
+    const VlutPlan plan = vlut_plan(p.rows, 3 * B, p.K, p.q, p.M, VLUT_METHOD_MFMA);
+    // the plane sum goes into the plan's last kernel where that kernel holds
+    // all three planes of an output: the rows kernel with one split and one
+    // token tile, or the reduce of a split wide / deep kernel; a staged rows
+    // kernel also splits the fp32 activations itself
+    const bool v4 = p.rows % 4 == 0 && ((uintptr_t)p.out % 16) == 0 && ((uintptr_t)inner % 16) == 0;
+    const bool rows1 = plan.kernel == VK_MFMA_ROWS && plan.splits == 1;
+    if (rows1 && 3 * B <= 15 && vlut_rows_staged(p.K, 1)) {
+        q.planes_b = B;
+        q.act_planes = 1;   // q.act stays the fp32 activations
+        return vlut_matmul(q, plan, s);
+    }
     hipLaunchKernelGGL(vlut_split_kernel, dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, s,
                        static_cast<const float*>(p.act), n / 4, planes, n);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    VlutMatmulArgs q = p;
     q.act = planes;
-    q.act_dtype = DT_BF16;
-    q.B = 3 * B;
+    if ((rows1 && 3 * B <= 64) || ((plan.kernel == VK_MFMA_WIDE || plan.kernel == VK_MFMA_DEEP) && plan.splits > 1 && v4)) {
+        q.planes_b = B;
+        return vlut_matmul(q, plan, s);
+    }
     q.out = y;
-    q.partial = inner;
     q.bias = nullptr;
     q.lsq_alpha = nullptr;
-    e = vlut_matmul(q, vlut_plan(p.rows, 3 * B, p.K, p.q, p.M, VLUT_METHOD_MFMA), s);
+    e = vlut_matmul(q, plan, s);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(vlut_split_sum_kernel, dim3((unsigned)((B * p.rows + 255) / 256)), dim3(256), 0, s, y, B,
                        p.rows, p.bias, p.lsq_alpha, p.lsq_qmax, p.out);
@@ -1089,7 +1122,12 @@ hipError_t vlut_matmul(VlutMatmulArgs p, const VlutPlan& plan, hipStream_t s)
         const float mult = plan.kernel == VK_LDS ? 1.f : 0.5f;
         const int64_t nw = p.B * p.rows;
         const bool v4 = p.rows % 4 == 0 && ((uintptr_t)p.out % 16) == 0 && ((uintptr_t)p.partial % 16) == 0;
-        if (v4 && plan.kernel == VK_LDS)
+        if (p.planes_b > 0) {
+            if (!v4 || plan.kernel == VK_LDS || p.B != 3 * p.planes_b) return hipErrorInvalidValue;
+            hipLaunchKernelGGL(vlut_reduce_planes4_kernel, dim3((unsigned)((p.planes_b * p.rows / 4 + 255) / 256)),
+                               dim3(256), 0, s, p.partial, splits, p.planes_b, p.rows, p.scale, p.scale_mode, mult,
+                               p.bias, p.lsq_alpha, p.lsq_qmax, p.out);
+        } else if (v4 && plan.kernel == VK_LDS)
             hipLaunchKernelGGL(vlut_reduce_sm4g_kernel, dim3((unsigned)((nw / 4 + 15) / 16)), dim3(256), 0, s,
                                p.partial, splits, p.B, p.rows, p.scale, p.scale_mode, mult, p.bias, p.lsq_alpha,
                                p.lsq_qmax, p.out);

@@ -39,6 +39,16 @@ struct VlutMatmulArgs {
     const float* bias;
     const float* lsq_alpha;
     int lsq_qmax;
+    // > 0: act holds three planes of planes_b tokens each (B = 3 planes_b,
+    // the fp32 activations' exact bf16 planes); out is [planes_b, rows] and
+    // each output adds its three planes' scaled products in plane order
+    // before the bias / LSQ epilogue.  Set by vlut_matmul_split only, for
+    // plans whose last kernel holds all three planes of an output.
+    int64_t planes_b;
+    // with planes_b: 1 when act is the fp32 activations [planes_b, K]
+    // themselves, which the rows kernel's staging splits into the planes
+    // (staged rows plans only), 0 when act holds the bf16 planes
+    int act_planes;
     // filled by the launcher
     const uint16_t* map;
     const uint64_t* coarse;

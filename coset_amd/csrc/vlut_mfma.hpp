@@ -117,6 +117,27 @@ __device__ __forceinline__ uint4 decode_pair_swar(const uint64_t* s_tab, const u
     return bytes_to_operand<BF16>(x0, x1, f16_off, f32_off);
 }
 
+// The three bf16 planes of the exact split a = h1 + h2 + h3, h1 the top 16 bits of a, h2 those of
+// a - h1, h3 those of a - h1 - h2.  Each difference is exact (it keeps the
+// bits the truncation dropped), and a - h1 - h2 has at most 8 significant
+// bits, so h3 holds it exactly (for |a| above the bf16 subnormal range,
+// ~1e-33).  Infinities go to h1 whole, a NaN to h1 as a quiet NaN, with
+// h2 = h3 = 0, so the products see the value itself.
+__device__ __forceinline__ void split3(float a, uint16_t& h1, uint16_t& h2, uint16_t& h3)
+{
+    const uint32_t u = __float_as_uint(a);
+    if ((u & 0x7f800000u) == 0x7f800000u) {
+        h1 = (u & 0x007fffffu) ? (uint16_t)0x7fc0u : (uint16_t)(u >> 16);
+        h2 = h3 = 0;
+        return;
+    }
+    h1 = (uint16_t)(u >> 16);
+    const float r1 = __fsub_rn(a, __uint_as_float((uint32_t)h1 << 16));
+    h2 = (uint16_t)(__float_as_uint(r1) >> 16);
+    const float r2 = __fsub_rn(r1, __uint_as_float((uint32_t)h2 << 16));
+    h3 = (uint16_t)(__float_as_uint(r2) >> 16);
+}
+
 // Output epilogue: + bias[o], then the LSQ activation quantizer (fp32, the
 // reference's order: the value F.linear(x, W, b) followed by actq,
 // coset/core/layers.py:472-484).
@@ -147,6 +168,10 @@ constexpr int kDeepStride = 32 * kDeepKqWg + 8;     // halves per token row in L
 // tables must cover M).  The wide and deep kernels with splits > 1 write
 // split-major partials and leave the reduce to the caller.
 hipError_t vlut_launch_rows(const VlutMatmulArgs& p, int splits, hipStream_t s);
+// The rows kernel stages its activations in LDS (a wave's K range of at most
+// two chunks) for this K and split count; with act_planes set and B <= 16
+// it then splits fp32 activations into their planes itself.
+bool vlut_rows_staged(int64_t K, int splits);
 hipError_t vlut_launch_wide(const VlutMatmulArgs& p, int splits, hipStream_t s);
 hipError_t vlut_launch_deep(const VlutMatmulArgs& p, int splits, hipStream_t s);
 

@@ -27,11 +27,16 @@ namespace coset {
 constexpr int kRowsStageKq = 16;                             // k-quads of a wave's staged slice (two chunks)
 constexpr int kRowsStageRow = 4 * kRowsStageKq * 16 + 16;    // bytes per staged token row (64 k-blocks, 16-byte pad)
 
-template <int Q, int M, bool BF16, int NTILE, int FMT, int TB>
+// SPLIT (staged, bf16): act is fp32 [planes_b, K] and the staging writes
+// each token's three bf16 planes (split3) to token rows b, planes_b + b and
+// 2 planes_b + b, so the kernel multiplies the planes as 3 planes_b tokens
+// without a separate split launch.
+template <int Q, int M, bool BF16, int NTILE, int FMT, int TB, bool SPLIT = false>
 __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulArgs p)
 {
     constexpr int CH = 8 / NTILE;  // steps per prefetch chunk
     static_assert(TB == 0 || (NTILE == 1 && TB <= 16), "staged activations: one 16-token tile");
+    static_assert(!SPLIT || (TB > 0 && BF16), "the split staging writes bf16 token rows");
     static_assert(TB == 0 || 2 * CH == kRowsStageKq, "a staged wave range is two chunks");
     __shared__ uint64_t s_tab[FMT == VLUT_DECODED ? 1 : kSwarSlots];
     __shared__ float s_red[kRowsWaves][NTILE * 4][64];
@@ -123,7 +128,49 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulAr
     };
 
     Chunk c_a, c_b;
-    if constexpr (TB > 0) {
+    if constexpr (SPLIT) {
+        // each fp32 token's K slice, 32 bytes a lane, then both chunks'
+        // weights; the three planes of a lane's 8 values go to the token's
+        // three rows (3 planes_b <= TB, checked by the host)
+        constexpr int NB = TB / 3;
+        const float* act32 = static_cast<const float*>(p.act);
+        const int64_t nb = p.planes_b;
+        float4 av[NB][2];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int64_t kb = 4 * w0 + lane;
+            const bool ok = b < nb && kb < 4 * w1 && kb < kb_total;
+            const float4* src = reinterpret_cast<const float4*>(act32 + (ok ? b * p.K + kb * 8 : 0));
+            av[b][0] = src[0];
+            av[b][1] = src[1];
+        }
+        load(w0, c_a);
+        load(w0 + CH, c_b);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            if (b >= nb) break;   // uniform
+            const int64_t kb = 4 * w0 + lane;
+            const bool ok = kb < 4 * w1 && kb < kb_total;
+            const float v[8] = {av[b][0].x, av[b][0].y, av[b][0].z, av[b][0].w,
+                                av[b][1].x, av[b][1].y, av[b][1].z, av[b][1].w};
+            uint16_t h[3][8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) split3(ok ? v[j] : 0.f, h[0][j], h[1][j], h[2][j]);
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl)
+                *reinterpret_cast<uint4*>(&s_stage[(wave * TB + pl * (int)nb + b) * kRowsStageRow + lane * 16]) =
+                    make_uint4((uint32_t)h[pl][0] | ((uint32_t)h[pl][1] << 16),
+                               (uint32_t)h[pl][2] | ((uint32_t)h[pl][3] << 16),
+                               (uint32_t)h[pl][4] | ((uint32_t)h[pl][5] << 16),
+                               (uint32_t)h[pl][6] | ((uint32_t)h[pl][7] << 16));
+        }
+        if constexpr (FMT != VLUT_DECODED) {
+            for (int i = threadIdx.x; i < 512 + p.n_coarse; i += blockDim.x) s_tab[i] = p.swar[i];
+            __syncthreads();
+        }
+        run(c_a, w0);
+        run(c_b, w0 + CH);
+    } else if constexpr (TB > 0) {
         // the wave's K slice (at most two chunks, checked by the host) of every
         // token, 16 bytes a lane and one load per token, then both chunks'
         // weights; the activations go to the wave's LDS rows as they arrive
@@ -177,6 +224,30 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulAr
 #pragma unroll
         for (int i = 0; i < 4; ++i) s_red[wave][s * 4 + i][lane] = acc[s][i];
     __syncthreads();
+    if (p.planes_b > 0) {
+        // one split and one token tile (t_base = 0) hold all three planes:
+        // output (b, o) sums each plane's waves as below, scales it, adds the
+        // planes in order and takes the epilogue
+        const int64_t nb = p.planes_b;
+        for (int e = threadIdx.x; e < nb * 16; e += blockDim.x) {
+            const int64_t b = e >> 4, o = r0 + (e & 15);
+            if (o >= p.rows) continue;
+            const float sc = p.scale ? (p.scale_mode == 0 ? p.scale[o] : 1.f / p.scale[o]) : 1.f;
+            float y[3];
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl) {
+                const int t = (int)(pl * nb + b);
+                const int si = 4 * (t >> 4) + (t & 3), ln = 16 * ((t >> 2) & 3) + (e & 15);
+                float v = 0.f;
+#pragma unroll
+                for (int w = 0; w < kRowsWaves; ++w) v += s_red[w][si][ln];
+                y[pl] = v * 0.5f * sc;
+            }
+            p.out[b * p.rows + o] =
+                vlut_epilogue(__fadd_rn(__fadd_rn(y[0], y[1]), y[2]), o, p.bias, p.lsq_alpha, p.lsq_qmax);
+        }
+        return;
+    }
     for (int e = threadIdx.x; e < NTILE * 256; e += blockDim.x) {
         const int si = e >> 6, ln = e & 63;
         float v = 0.f;
@@ -197,11 +268,12 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulAr
 namespace {
 
 
-template <int Q, int M, bool BF16, int NTILE, int TB>
+template <int Q, int M, bool BF16, int NTILE, int TB, bool SPLIT = false>
 void launch_rows_fmt(const VlutMatmulArgs& p, int splits, hipStream_t s)
 {
     dim3 grid((unsigned)((p.rows + 15) / 16), (unsigned)splits, (unsigned)((p.B + 16 * NTILE - 1) / (16 * NTILE)));
-#define COSET_ROWS(F) hipLaunchKernelGGL((vlut_rows_kernel<Q, M, BF16, NTILE, F, TB>), grid, dim3(kRowsWaves * 64), 0, s, p)
+#define COSET_ROWS(F) \
+    hipLaunchKernelGGL((vlut_rows_kernel<Q, M, BF16, NTILE, F, TB, SPLIT>), grid, dim3(kRowsWaves * 64), 0, s, p)
     switch (p.prepared) {
     case VLUT_RAW: COSET_ROWS(VLUT_RAW); break;
     case VLUT_PREPARED: COSET_ROWS(VLUT_PREPARED); break;
@@ -217,10 +289,13 @@ hipError_t launch_rows(const VlutMatmulArgs& p, int splits, hipStream_t s)
     if constexpr (Q == 2 || M <= 2) {
         const bool bf = p.act_dtype == DT_BF16;
         // the staged kernels take a wave's whole K range (at most kRowsStageKq k-quads) at once
-        const int64_t kq_total = (p.K / 8 + 3) / 4;
-        const int64_t kq_wg = (kq_total + splits - 1) / splits;
-        const bool staged = (kq_wg + kRowsWaves - 1) / kRowsWaves <= kRowsStageKq;
-        if (staged && p.B == 1) {  // staged activations, one token
+        const bool staged = vlut_rows_staged(p.K, splits);
+        if (p.act_planes) {   // fp32 activations split by the staging: one tile, one split
+            if (!staged || splits != 1 || p.planes_b <= 0 || p.B != 3 * p.planes_b || p.B > 15)
+                return hipErrorInvalidValue;
+            if (p.B <= 6) launch_rows_fmt<Q, M, true, 1, 8, true>(p, splits, s);
+            else launch_rows_fmt<Q, M, true, 1, 16, true>(p, splits, s);
+        } else if (staged && p.B == 1) {  // staged activations, one token
             if (bf) launch_rows_fmt<Q, M, true, 1, 1>(p, splits, s); else launch_rows_fmt<Q, M, false, 1, 1>(p, splits, s);
         } else if (staged && p.B <= 8) {  // staged activations, up to 8 tokens
             if (bf) launch_rows_fmt<Q, M, true, 1, 8>(p, splits, s); else launch_rows_fmt<Q, M, false, 1, 8>(p, splits, s);
@@ -251,6 +326,13 @@ hipError_t dispatch_rows(const VlutMatmulArgs& p, int splits, hipStream_t s)
 }
 
 }  // namespace
+
+bool vlut_rows_staged(int64_t K, int splits)
+{
+    const int64_t kq_total = (K / 8 + 3) / 4;
+    const int64_t kq_wg = (kq_total + splits - 1) / splits;
+    return (kq_wg + kRowsWaves - 1) / kRowsWaves <= kRowsStageKq;
+}
 
 hipError_t vlut_launch_rows(const VlutMatmulArgs& p, int splits, hipStream_t s)
 {

@@ -227,13 +227,16 @@ def test_fp32_activations_on_matrix_cores(q, M, B):
         assert torch.equal(fused, m(plain + bias))
 
 
-def test_fp32_split_special_values():
+@pytest.mark.parametrize("n_tok", [6, 5])
+def test_fp32_split_special_values(n_tok):
     """Infinities and NaN in fp32 activations reach the products whole (the
     planes after them hold 0): an output is finite exactly where the oracle's
     fp32 table sum is (which of NaN and +-inf a non-finite output takes can
     differ: the matrix-core method multiplies the decoded weight, the tables
     multiply each level's residual), a NaN activation makes its token's
-    outputs NaN, and finite outputs agree with the oracle."""
+    outputs NaN, and finite outputs agree with the oracle.  Five tokens take
+    the rows kernel that splits the activations in its staging, six the
+    separate split launch."""
     import coset_amd
     rng = np.random.default_rng(31)
     rows, K, q, M = 48, 64, 4, 2
@@ -247,13 +250,52 @@ def test_fp32_split_special_values():
     a_np[3, 20] = np.nan
     a_np[4, 5], a_np[4, 40] = np.inf, -np.inf
     a_np[5] *= np.float32(1e30)
+    a_np = np.ascontiguousarray(a_np[:n_tok])
     ref = O.vlut_matmul(words_np, np.ones(rows, np.float32), a_np, q, M)
     out = coset_amd.vlut_matmul(words, torch.from_numpy(a_np).cuda(), q, method="mfma").cpu().numpy()
     fin = np.isfinite(ref)
     assert np.array_equal(np.isfinite(out), fin)
-    assert np.isnan(out[3]).all() and not fin[1:5].any() and fin[[0, 5]].all()
+    assert np.isnan(out[3]).all() and not fin[1:5].any() and fin[0].all() and fin[5:].all()
     mag = matmul_mag(words_np, q, M, np.where(np.isfinite(a_np), a_np, 0))
     close(out[fin], ref[fin], mag[fin], 1e-3)
+
+
+def _split3_np(a):
+    """The exact three-plane split of finite fp32 values (h1 = a truncated to
+    bf16, h2 = (a - h1) truncated, h3 = (a - h1 - h2) truncated), as uint16
+    planes [3, ...]."""
+    a = np.asarray(a, np.float32)
+    hs, r = [], a
+    for _ in range(3):
+        h = (r.view(np.uint32) >> 16).astype(np.uint16)
+        hs.append(h)
+        r = (r - (h.astype(np.uint32) << 16).view(np.float32)).astype(np.float32)
+    return np.stack(hs)
+
+
+@pytest.mark.parametrize("B,rows,K", [(1, 80, 256), (8, 80, 256), (21, 64, 512), (40, 128, 4096), (40, 72, 136)])
+def test_fp32_plane_sum_is_the_planes_products(B, rows, K):
+    """The fp32 path adds each output's three plane products in the last
+    kernel of its plan (the rows kernel, or the reduce of a split deep
+    kernel; other plans through a separate sum): bit for bit
+    ((y_1 + y_2) + y_3) + bias of the three bf16 planes run as 3B tokens of
+    their own, for the raw words and the decoded format."""
+    import coset_amd
+    rng = np.random.default_rng(B * 1000 + rows + K)
+    q, M = 4, 2
+    W = rng.standard_normal((rows, K)).astype(np.float32)
+    words_np = O.pack_words(O.e8_encode(W.reshape(-1, 8), q, M), q).reshape(rows, K // 8, M)
+    words = torch.from_numpy(words_np.astype(np.int32)).to(torch.uint16).cuda()
+    a_np = (rng.standard_normal((B, K)) * np.exp2(rng.integers(-20, 20, (B, K)))).astype(np.float32)
+    planes = _split3_np(a_np).reshape(3 * B, K)
+    p_bf = torch.from_numpy(planes.view(np.int16)).cuda().view(torch.bfloat16)
+    sc = torch.from_numpy(rng.uniform(0.5, 2.0, rows).astype(np.float32)).cuda()
+    bias = torch.from_numpy(rng.standard_normal(rows).astype(np.float32)).cuda()
+    for w in (words, coset_amd.vlut_prepare(words, q, layout="decoded")):
+        y = coset_amd.vlut_matmul(w, p_bf, q, scale=sc, method="mfma")
+        want = ((y[:B] + y[B:2 * B]) + y[2 * B:]) + bias
+        got = coset_amd.vlut_matmul(w, torch.from_numpy(a_np).cuda(), q, scale=sc, bias=bias, method="mfma")
+        assert torch.equal(got, want)
 
 
 def test_fp32_mfma_needs_exact_operands():
