@@ -62,7 +62,11 @@ __global__ void __launch_bounds__(256) aux_cast_kernel(CodecArgs a)
     if (i < a.aux_n) aux_cast(a, i);
 }
 
-template <int Q, int MODE, bool WGBETA>
+// MM > 0: the level count fixed at compile time (the layer quantizer's M = 2
+// round trip through the decode tables): every level is encoded first, then
+// the levels' table reads are issued together, so a block waits for one
+// round of map reads and one of coarse-point reads instead of one per level.
+template <int Q, int MODE, bool WGBETA, int MM = 0>
 __global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
 {
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -70,7 +74,7 @@ __global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
     if (a.aux_out && i < a.aux_n) aux_cast(a, i);
     const int q = Q > 0 ? Q : a.q;
     const float qf = (float)q;
-    const int M = a.M;
+    const int M = MM > 0 ? MM : a.M;
 
     auto load_block = [&](int64_t il, float xl[8]) {
         if (a.x_dtype == DT_BF16) {
@@ -145,6 +149,48 @@ __global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
                 xl[j] = __fadd_rn(xl[j], a.dither[a.dither_stride * i + j]);
         }
 
+        if constexpr (MM > 0 && MODE == MODE_ROUNDTRIP && (Q == 2 || Q == 4)) {
+            uint32_t words[MM];
+#pragma unroll
+            for (int m = 0; m < MM; ++m) {
+                int b[8];
+                encode_level<Q>(xl, a.fast_projection, q, b);
+                words[m] = pack_word<Q>(b, q);
+                if (a.packed) reinterpret_cast<uint16_t*>(a.packed)[(size_t)i * MM + m] = (uint16_t)words[m];
+                if (a.codes_f32) {
+                    float4* cp = reinterpret_cast<float4*>(a.codes_f32 + ((size_t)i * MM + m) * 8);
+                    cp[0] = make_float4((float)b[0], (float)b[1], (float)b[2], (float)b[3]);
+                    cp[1] = make_float4((float)b[4], (float)b[5], (float)b[6], (float)b[7]);
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) xl[j] = div_q<Q>(xl[j], qf);
+            }
+            // 2 r of each level as two_r_tables computes it, the table reads first
+            constexpr uint32_t kMask = Q == 2 ? 0xffu : 0xffffu;
+            uint16_t cid[MM];
+            uint64_t cc[MM];
+#pragma unroll
+            for (int m = 0; m < MM; ++m) cid[m] = a.dec_map[words[m] & kMask];
+#pragma unroll
+            for (int m = 0; m < MM; ++m) cc[m] = a.dec_coarse[cid[m]];
+            float w = 1.f;
+#pragma unroll
+            for (int m = 0; m < MM; ++m) {
+                int b[8], r2[8];
+                unpack_word<Q>(words[m] & kMask, Q, b);
+                r2[0] = 4 * b[0] - 2 * b[1] + b[7];
+#pragma unroll
+                for (int j = 1; j < 6; ++j) r2[j] = 2 * (b[j] - b[j + 1]) + b[7];
+                r2[6] = 2 * b[6] + b[7];
+                r2[7] = b[7];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float r = 0.5f * (float)(r2[j] - Q * (int)(int8_t)(uint8_t)(cc[m] >> (8 * j)));
+                    acc[j] = __fadd_rn(acc[j], __fmul_rn(w, r));
+                }
+                w = __fmul_rn(w, qf);
+            }
+        } else {
         float w = 1.f;
         for (int m = 0; m < M; ++m) {
             int b[8];
@@ -183,6 +229,7 @@ __global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) xl[j] = div_q<Q>(xl[j], qf);
+        }
         }
     } else {
         float w = 1.f;
@@ -258,7 +305,9 @@ static hipError_t launch_mode(const CodecArgs& a, hipStream_t s)
     dim3 grid((unsigned)((std::max<int64_t>(a.n, a.aux_out ? a.aux_n : 0) + 255) / 256));
     const bool wg_beta = a.scale_mode == SCALE_LAYER && a.use_theta && a.blocks_per_row >= 64;
 #define COSET_Q(QQ) \
-    if (wg_beta) hipLaunchKernelGGL((hnlq_codec_kernel<QQ, MODE, true>), grid, block, 0, s, a); \
+    if (wg_beta && MODE == MODE_ROUNDTRIP && (QQ == 2 || QQ == 4) && a.M == 2 && a.dec_map) \
+        hipLaunchKernelGGL((hnlq_codec_kernel<QQ, MODE, true, 2>), grid, block, 0, s, a); \
+    else if (wg_beta) hipLaunchKernelGGL((hnlq_codec_kernel<QQ, MODE, true>), grid, block, 0, s, a); \
     else hipLaunchKernelGGL((hnlq_codec_kernel<QQ, MODE, false>), grid, block, 0, s, a); \
     break;
     switch (a.q) {
