@@ -671,6 +671,40 @@ __global__ void __launch_bounds__(256) vlut_reduce_sm4_kernel(const float* parti
     reinterpret_cast<float4*>(out)[i4] = make_float4(r[0], r[1], r[2], r[3]);
 }
 
+// The same sums for the deep kernel's partials with workgroup (x, y) taking
+// the 64 rows of row group x for tokens 16 y .. 16 y + 15, one quad a
+// thread: x runs on the XCD whose workgroups wrote that row group's
+// partials (both grids deal workgroups to the 8 XCDs by x mod 8 when there
+// are a multiple of 8 row groups), so its reads hit that XCD's L2.
+__global__ void __launch_bounds__(256) vlut_reduce_rg4_kernel(const float* partial, int splits, int64_t B,
+                                                             int64_t rows, const float* scale, int scale_mode,
+                                                             float mult, const float* bias, const float* lsq_alpha,
+                                                             int lsq_qmax, float* out)
+{
+    const int64_t rq = rows / 4, n4 = B * rq;
+    const int64_t qd = (int64_t)blockIdx.x * 16 + (threadIdx.x & 15);
+    const int64_t tok = (int64_t)blockIdx.y * 16 + (threadIdx.x >> 4);
+    if (qd >= rq || tok >= B) return;
+    const float4* p4 = reinterpret_cast<const float4*>(partial);
+    const int64_t i4 = tok * rq + qd, o0 = 4 * qd;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < splits; ++s) {
+        const float4 v = p4[s * n4 + i4];
+        acc[0] += v.x;
+        acc[1] += v.y;
+        acc[2] += v.z;
+        acc[3] += v.w;
+    }
+    float r[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t o = o0 + j;
+        const float sc = scale ? (scale_mode == 0 ? scale[o] : 1.f / scale[o]) : 1.f;
+        r[j] = vlut_epilogue(acc[j] * mult * sc, o, bias, lsq_alpha, lsq_qmax);
+    }
+    reinterpret_cast<float4*>(out)[i4] = make_float4(r[0], r[1], r[2], r[3]);
+}
+
 // The same for three planes of nb tokens (B = 3 nb, rows % 4 == 0): each
 // plane's splits are summed and scaled as above, then the planes are added
 // in order and the epilogue applied; out is [nb, rows].
@@ -679,11 +713,14 @@ __global__ void __launch_bounds__(256) vlut_reduce_planes4_kernel(const float* p
                                                                  float mult, const float* bias,
                                                                  const float* lsq_alpha, int lsq_qmax, float* out)
 {
-    const int64_t m4 = nb * rows / 4, n4 = 3 * m4;
-    const int64_t i4 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i4 >= m4) return;
+    // workgroup (x, y): row group x (64 rows) of tokens 16 y .. 16 y + 15, as
+    // in vlut_reduce_rg4_kernel
+    const int64_t rq = rows / 4, m4 = nb * rq, n4 = 3 * m4;
+    const int64_t qd = (int64_t)blockIdx.x * 16 + (threadIdx.x & 15);
+    const int64_t tok = (int64_t)blockIdx.y * 16 + (threadIdx.x >> 4);
+    if (qd >= rq || tok >= nb) return;
     const float4* p4 = reinterpret_cast<const float4*>(partial);
-    const int64_t o0 = (4 * i4) % rows;
+    const int64_t i4 = tok * rq + qd, o0 = 4 * qd;
     float y[3][4];
 #pragma unroll
     for (int pl = 0; pl < 3; ++pl) {
@@ -1124,9 +1161,13 @@ hipError_t vlut_matmul(VlutMatmulArgs p, const VlutPlan& plan, hipStream_t s)
         const bool v4 = p.rows % 4 == 0 && ((uintptr_t)p.out % 16) == 0 && ((uintptr_t)p.partial % 16) == 0;
         if (p.planes_b > 0) {
             if (!v4 || plan.kernel == VK_LDS || p.B != 3 * p.planes_b) return hipErrorInvalidValue;
-            hipLaunchKernelGGL(vlut_reduce_planes4_kernel, dim3((unsigned)((p.planes_b * p.rows / 4 + 255) / 256)),
-                               dim3(256), 0, s, p.partial, splits, p.planes_b, p.rows, p.scale, p.scale_mode, mult,
+            hipLaunchKernelGGL(vlut_reduce_planes4_kernel,
+                               dim3((unsigned)((p.rows + 63) / 64), (unsigned)((p.planes_b + 15) / 16)), dim3(256), 0, s, p.partial, splits, p.planes_b, p.rows, p.scale, p.scale_mode, mult,
                                p.bias, p.lsq_alpha, p.lsq_qmax, p.out);
+        } else if (v4 && plan.kernel == VK_MFMA_DEEP) {
+            hipLaunchKernelGGL(vlut_reduce_rg4_kernel, dim3((unsigned)((p.rows + 63) / 64), (unsigned)((p.B + 15) / 16)),
+                               dim3(256), 0, s, p.partial, splits, p.B, p.rows, p.scale, p.scale_mode, mult, p.bias,
+                               p.lsq_alpha, p.lsq_qmax, p.out);
         } else if (v4 && plan.kernel == VK_LDS)
             hipLaunchKernelGGL(vlut_reduce_sm4g_kernel, dim3((unsigned)((nw / 4 + 15) / 16)), dim3(256), 0, s,
                                p.partial, splits, p.B, p.rows, p.scale, p.scale_mode, mult, p.bias, p.lsq_alpha,
