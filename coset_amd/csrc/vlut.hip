@@ -755,15 +755,27 @@ constexpr int kReduceGroups = 16;
 __global__ void __launch_bounds__(256) vlut_reduce_sm4g_kernel(const float* partial, int splits, int64_t B,
                                                               int64_t rows, const float* scale, int scale_mode,
                                                               float mult, const float* bias, const float* lsq_alpha,
-                                                              int lsq_qmax, float* out)
+                                                              int lsq_qmax, float* out, int64_t rg_rows)
 {
     __shared__ float4 s_sum[kReduceGroups][16 + 1];
     const int quad = threadIdx.x & 15, g = threadIdx.x >> 4;
     const int64_t n4 = B * rows / 4;
-    const int64_t i4 = (int64_t)blockIdx.x * 16 + quad;
+    // rg_rows > 0: workgroup (x, y) takes 16 quads of token y in row group
+    // x % groups (chunk x / groups), so it runs on the XCD whose workgroups
+    // wrote that row group's partials (the LDS-table kernel's workgroup x
+    // takes rows rg_rows x ..; both grids deal workgroups to the 8 XCDs by
+    // linear id mod 8); rg_rows = 0: the 16 quads 16 x .. of the flat order
+    int64_t i4 = (int64_t)blockIdx.x * 16 + quad;
+    bool live = i4 < n4;
+    if (rg_rows > 0) {
+        const int64_t groups = (rows + rg_rows - 1) / rg_rows;
+        const int64_t rg = blockIdx.x % groups, q = (blockIdx.x / groups) * 16 + quad;
+        live = q < rg_rows / 4 && rg * (rg_rows / 4) + q < rows / 4;
+        i4 = (int64_t)blockIdx.y * (rows / 4) + rg * (rg_rows / 4) + q;
+    }
     const float4* p4 = reinterpret_cast<const float4*>(partial);
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (i4 < n4) {
+    if (live) {
         for (int sp = g; sp < splits; sp += kReduceGroups) {
             const float4 v = p4[sp * n4 + i4];
             acc.x += v.x;
@@ -774,7 +786,7 @@ __global__ void __launch_bounds__(256) vlut_reduce_sm4g_kernel(const float* part
     }
     s_sum[g][quad] = acc;
     __syncthreads();
-    if (g != 0 || i4 >= n4) return;
+    if (g != 0 || !live) return;
     for (int k = 1; k < kReduceGroups; ++k) {
         const float4 v = s_sum[k][quad];
         acc.x += v.x;
@@ -1169,9 +1181,17 @@ hipError_t vlut_matmul(VlutMatmulArgs p, const VlutPlan& plan, hipStream_t s)
                                dim3(256), 0, s, p.partial, splits, p.B, p.rows, p.scale, p.scale_mode, mult, p.bias,
                                p.lsq_alpha, p.lsq_qmax, p.out);
         } else if (v4 && plan.kernel == VK_LDS)
-            hipLaunchKernelGGL(vlut_reduce_sm4g_kernel, dim3((unsigned)((nw / 4 + 15) / 16)), dim3(256), 0, s,
-                               p.partial, splits, p.B, p.rows, p.scale, p.scale_mode, mult, p.bias, p.lsq_alpha,
-                               p.lsq_qmax, p.out);
+        {
+            const int64_t rg = lds_rows(p.B), groups = (p.rows + rg - 1) / rg;
+            if (p.B <= 65535 && groups * (rg / 64) <= 0x7fffffff)
+                hipLaunchKernelGGL(vlut_reduce_sm4g_kernel, dim3((unsigned)(groups * (rg / 64)), (unsigned)p.B),
+                                   dim3(256), 0, s, p.partial, splits, p.B, p.rows, p.scale, p.scale_mode, mult,
+                                   p.bias, p.lsq_alpha, p.lsq_qmax, p.out, rg);
+            else
+                hipLaunchKernelGGL(vlut_reduce_sm4g_kernel, dim3((unsigned)((nw / 4 + 15) / 16)), dim3(256), 0, s,
+                                   p.partial, splits, p.B, p.rows, p.scale, p.scale_mode, mult, p.bias, p.lsq_alpha,
+                                   p.lsq_qmax, p.out, (int64_t)0);
+        }
         else if (v4)
             hipLaunchKernelGGL(vlut_reduce_sm4_kernel, dim3((unsigned)((nw / 4 + 255) / 256)), dim3(256), 0, s,
                                p.partial, splits, p.B, p.rows, p.scale, p.scale_mode, mult, p.bias, p.lsq_alpha,
