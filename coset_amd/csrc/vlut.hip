@@ -1183,7 +1183,8 @@ hipError_t vlut_matmul(VlutMatmulArgs p, const VlutPlan& plan, hipStream_t s)
         } else if (v4 && plan.kernel == VK_LDS)
         {
             const int64_t rg = lds_rows(p.B), groups = (p.rows + rg - 1) / rg;
-            if (p.B <= 65535 && groups * (rg / 64) <= 0x7fffffff)
+            // by row group where the kernel put all of a row group's splits on one XCD
+            if (groups % 8 == 0 && p.B <= 65535 && groups * (rg / 64) <= 0x7fffffff)
                 hipLaunchKernelGGL(vlut_reduce_sm4g_kernel, dim3((unsigned)(groups * (rg / 64)), (unsigned)p.B),
                                    dim3(256), 0, s, p.partial, splits, p.B, p.rows, p.scale, p.scale_mode, mult,
                                    p.bias, p.lsq_alpha, p.lsq_qmax, p.out, rg);
