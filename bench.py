@@ -92,14 +92,24 @@ CPU_REPS = 5                   # timed runs per figure (median), after one untim
 
 
 def cpu_model() -> str:
+    """The host CPU as /proc/cpuinfo names it (model name, family/model/stepping,
+    clock) plus the logical CPUs online and those this process may use."""
+    info = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if not line.strip():
+                    break    # the first processor's fields are enough
+                k, _, v = line.partition(":")
+                info.setdefault(k.strip(), v.strip())
     except OSError:
         pass
-    return "unknown"
+    name = info.get("model name", "unknown")
+    fms = "family {} model {} stepping {}".format(info.get("cpu family", "?"), info.get("model", "?"),
+                                                  info.get("stepping", "?"))
+    mhz = info.get("cpu MHz")
+    return "{} ({}{}), {} logical CPUs online, {} usable by this process".format(
+        name, fms, f", {float(mhz):.0f} MHz" if mhz else "", os.cpu_count(), len(os.sched_getaffinity(0)))
 
 
 def cpu_threads() -> int:

@@ -169,10 +169,18 @@ extern int g_fast_projection;  // 1 (default): encoders use the fast projection 
 extern int g_codec_plain;      // 1 (default): the table kernel's fixed-format variant where it applies
 extern int g_codec_dynamic;    // 1 (default): the fixed-format kernel takes its tiles from a counter
 constexpr int64_t kLutMinBlocks = 1 << 20;  // below it the table staging does not pay (layer-sized calls)
-// n zeroed counters of the current device's counter ring (counters.hpp) for
-// one launch on stream s, or null under graph capture; the launch's last
-// workgroup must put them back to zero.
-unsigned* take_counters(hipStream_t s, uint32_t n);
+// A zeroed counter pair of the current device's counter ring (counters.hpp)
+// for one launch on stream s, held until the launch's last workgroup puts the
+// pair back to zero and stores 1 to *release; pair is null (static schedule)
+// under graph capture or while every slot is held.
+struct TileCounters {
+    unsigned* pair;     // [0] hands out tiles, [1] counts finished workgroups
+    unsigned* release;  // the slot's release flag (host memory, device address)
+    int64_t slot;
+};
+TileCounters take_counters(hipStream_t s);
+// Hands back the slot of a launch that failed to start.
+void return_counters(const TileCounters& tc);
 
 // Workgroup barrier that orders LDS only: waits for this wave's LDS
 // operations, not for its loads and stores in flight (__syncthreads would

@@ -1,36 +1,55 @@
 // counters.hpp -- host-side bookkeeping of the per-device counter ring.
 //
-// Kernels that hand out work dynamically (the codec's tile schedule) keep
-// their counters in a device array of kCounterRing unsigned counters,
-// zero-initialised when the code object is loaded.  Each launch takes the
-// next run of n consecutive counters from a host-side cursor, and the
-// launch's last workgroup puts them back to zero, so every launch starts
-// from zero without a memset.  Consecutive launches use different counters,
-// so launches on different streams never share counters unless both run at
-// the same time and kCounterRing / n launches were issued between them (at
-// n = 2: 8192 launches while one is still running).  Plain C++ (no HIP), so
-// the bookkeeping is unit-tested on the CPU.
+// Kernels that hand out work dynamically (the codec's tile schedule) take a
+// pair of counters per launch from a device array of kCounterSlots pairs,
+// zero-initialised when the code object is loaded.  The launch's last
+// workgroup puts its pair back to zero and then sets the slot's release flag
+// to 1; the flags live in host-visible memory, so the host reads them.  A
+// slot is handed to a launch only while its flag reads 1, i.e. once every
+// earlier launch that held it has finished, whatever order streams and
+// event waits give the launches: two launches never share a pair, however
+// long one of them is held back.  When every slot is held (kCounterSlots
+// launches in flight), the launch takes its static schedule instead.
+// Plain C++ (no HIP), so the bookkeeping is unit-tested on the CPU.
 #pragma once
 
-#include <atomic>
+#include <mutex>
 #include <stdint.h>
 
 namespace coset {
 
-constexpr uint32_t kCounterRing = 1u << 14;  // counters per device (64 KiB)
+constexpr uint32_t kCounterSlots = 1u << 13;    // counter pairs per device
+constexpr uint32_t kCounterRing = 2 * kCounterSlots;  // counters per device (64 KiB)
 
-// Offset of a run of n consecutive counters (1 <= n <= ring) for one launch.
-// A run never crosses the end of the ring: when it would, it starts over at
-// offset 0 (the counters skipped stay zero).  Thread-safe.
-inline uint32_t ring_take(std::atomic<uint64_t>& cursor, uint32_t n, uint32_t ring)
+struct CounterRing {
+    std::mutex mu;
+    uint32_t cursor = 0;          // next slot to try
+    uint32_t slots = kCounterSlots;
+    uint32_t* release = nullptr;  // [slots]: 1 = free, 0 = held by a launch (written by the GPU)
+};
+
+// A free slot for one launch, its flag set to 0 (held), or -1 when every
+// slot is held.  Slots are tried in ring order from the one after the last
+// handed out, so a slot is reused as late as possible.  Thread-safe.
+inline int64_t ring_acquire(CounterRing& r)
 {
-    uint64_t cur = cursor.load(std::memory_order_relaxed);
-    for (;;) {
-        const uint64_t start = cur % ring;
-        const uint64_t skip = start + n > ring ? ring - start : 0;
-        if (cursor.compare_exchange_weak(cur, cur + skip + n, std::memory_order_relaxed))
-            return (uint32_t)((cur + skip) % ring);
+    std::lock_guard<std::mutex> lock(r.mu);
+    for (uint32_t i = 0; i < r.slots; ++i) {
+        const uint32_t s = (r.cursor + i) % r.slots;
+        if (__atomic_load_n(&r.release[s], __ATOMIC_ACQUIRE) == 1u) {
+            __atomic_store_n(&r.release[s], 0u, __ATOMIC_RELAXED);
+            r.cursor = (s + 1) % r.slots;
+            return s;
+        }
     }
+    return -1;
+}
+
+// Hands a slot back from the host: the launch that took it never ran (its
+// launch call failed).  A kernel that ran releases its slot itself.
+inline void ring_release(CounterRing& r, int64_t s)
+{
+    __atomic_store_n(&r.release[s], 1u, __ATOMIC_RELEASE);
 }
 
 }  // namespace coset

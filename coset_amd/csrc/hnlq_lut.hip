@@ -39,7 +39,7 @@ constexpr int kLutThreads = 1024;
 // Tile counters of the dynamic schedule: a pair taken from the per-device
 // counter ring (counters.hpp) for each launch -- [0] hands out tiles, [1]
 // counts finished workgroups, and the workgroup that finishes last puts both
-// back to zero.
+// back to zero and then releases the slot to the host.
 constexpr int kTileBlocks = 2;        // blocks per thread in a dynamic tile
 constexpr int kTileBlocksDecode = 2;  // the decoder's, whole next tile ahead (1, 4, 8 measured slower)
 static __device__ __align__(256) unsigned g_counter_ring[kCounterRing];
@@ -134,8 +134,9 @@ __device__ __forceinline__ void schedule_stride(int64_t n, Load& load, Body& bod
 // compiler rewrites a uniform-address atomicAdd into a wave reduction that
 // waits for its result at once) two tiles ahead and publishes them through
 // LDS behind an LDS-only barrier; when a workgroup has seen its last tile it
-// counts itself done, and the last one resets the pair for the next call on
-// the stream.
+// counts itself done, and the last one resets the pair and then sets the
+// slot's release flag (host memory, system scope): only after that does the
+// host hand the pair to another launch.
 __device__ __forceinline__ void tiles_first_two(unsigned* tiles, unsigned* s_tile, int64_t& t0, int64_t& t1)
 {
     if (threadIdx.x == 0) {
@@ -147,20 +148,23 @@ __device__ __forceinline__ void tiles_first_two(unsigned* tiles, unsigned* s_til
     t1 = s_tile[3];
 }
 
-__device__ __forceinline__ void tiles_done(unsigned* tiles)
+__device__ __forceinline__ void tiles_done(unsigned* tiles, unsigned* release)
 {
     if (threadIdx.x == 0 && atomicAdd(tiles + 1, 1u) == gridDim.x - 1) {
         atomicExch(tiles, 0u);
         atomicExch(tiles + 1, 0u);
+        __threadfence_system();
+        __hip_atomic_store(release, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
     }
 }
 
 // Dynamic tiles of KT x blockDim.x consecutive blocks (KT per thread,
 // blockDim.x apart) with one block ahead; one LDS barrier per tile.
 template <int KT, typename In, typename Load, typename Body>
-__device__ __forceinline__ void schedule_tiles(int64_t n, unsigned* tiles, unsigned* s_tile, Load& load, Body& body)
+__device__ __forceinline__ void schedule_tiles(int64_t n, TileCounters tc, unsigned* s_tile, Load& load, Body& body)
 {
     static_assert(KT % 2 == 0 || KT == 1, "register sets alternate per block");
+    unsigned* tiles = tc.pair;
     const int64_t last = n - 1;
     const int64_t ntiles = (n + KT * (int64_t)blockDim.x - 1) / (KT * (int64_t)blockDim.x);
     auto blk = [&](int64_t t, int j) {
@@ -209,15 +213,16 @@ __device__ __forceinline__ void schedule_tiles(int64_t n, unsigned* tiles, unsig
             }
         }
     }
-    tiles_done(tiles);
+    tiles_done(tiles, tc.release);
 }
 
 // Dynamic tiles of KD blocks per thread with all of the next tile's inputs
 // in flight while the current tile is processed (inputs of a few bytes).
 template <int KD, typename In, typename Load, typename Body, typename Pro>
-__device__ __forceinline__ void schedule_tiles_whole(int64_t n, unsigned* tiles, unsigned* s_tile, Load& load,
+__device__ __forceinline__ void schedule_tiles_whole(int64_t n, TileCounters tc, unsigned* s_tile, Load& load,
                                                      Body& body, Pro& pro)
 {
+    unsigned* tiles = tc.pair;
     const int64_t last = n - 1;
     const int64_t ntiles = (n + KD * (int64_t)blockDim.x - 1) / (KD * (int64_t)blockDim.x);
     auto blk = [&](int64_t t, int j) {
@@ -255,7 +260,7 @@ __device__ __forceinline__ void schedule_tiles_whole(int64_t n, unsigned* tiles,
             t1 = t3;
         }
     }
-    tiles_done(tiles);
+    tiles_done(tiles, tc.release);
 }
 
 // SWAR: each level's 2r comes from three byte tables (tables.hpp) added as
@@ -545,7 +550,7 @@ __device__ __forceinline__ uint32_t encode_level_word(const float xl[8], bool in
 template <int Q, int M, int MODE, bool SCALED, bool CODES, bool PK>
 __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, const uint16_t* __restrict__ g_map,
                                                               const uint64_t* __restrict__ g_tab, int n_coarse,
-                                                              int swar_bias, unsigned* tiles)
+                                                              int swar_bias, TileCounters tc)
 {
     constexpr int NC = LutShape<Q>::kCodes;
     __shared__ __align__(16) uint16_t s_map[NC];
@@ -686,55 +691,99 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
 
     // every store of a body is unconditional (see the schedules above)
     if constexpr (MODE == MODE_DECODE) {
-        if (tiles) {
-            schedule_tiles_whole<kTileBlocksDecode, In>(n, tiles, s_tile, load, body, pro);
+        if (tc.pair) {
+            schedule_tiles_whole<kTileBlocksDecode, In>(n, tc, s_tile, load, body, pro);
             return;
         }
     }
     if constexpr (MODE != MODE_DECODE) {
-        if (tiles) {
+        if (tc.pair) {
             // one block per thread and tile when the float codes are written
             // (e8_encode 290 -> 278 us at 2^24 blocks; two blocks measured
             // faster for the others, A/B on one box)
-            schedule_tiles<CODES ? 1 : kTileBlocks, In>(n, tiles, s_tile, load, body);
+            schedule_tiles<CODES ? 1 : kTileBlocks, In>(n, tc, s_tile, load, body);
             return;
         }
     }
     schedule_stride<In>(n, load, body, pro);
 }
 
-// n counters of the current device's ring for one launch on stream s, or
-// null while s captures a graph (a replayed graph keeps the counters it was
-// captured with and may run beside later launches, so the kernels take their
-// static schedule instead) or when the ring cannot be reached.
-unsigned* take_counters(hipStream_t s, uint32_t n)
+namespace {
+
+// Per-device counter rings: the pairs' device address, the release flags
+// (coherent host memory, and their device address) and the host bookkeeping.
+constexpr int kRingDevices = 64;
+std::mutex g_ring_mu;
+unsigned* g_ring_pairs[kRingDevices] = {nullptr};
+unsigned* g_ring_release_dev[kRingDevices] = {nullptr};
+CounterRing* g_ring[kRingDevices] = {nullptr};
+
+CounterRing* device_ring(int dev)
 {
+    std::lock_guard<std::mutex> lock(g_ring_mu);
+    if (!g_ring[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_counter_ring)) != hipSuccess || !p) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        // the kernels write the flags with system-scope stores; every slot starts free
+        void* h = nullptr;
+        if (hipHostMalloc(&h, kCounterSlots * sizeof(uint32_t), hipHostMallocCoherent) != hipSuccess || !h) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        void* hd = nullptr;
+        if (hipHostGetDevicePointer(&hd, h, 0) != hipSuccess || !hd) {
+            (void)hipGetLastError();
+            (void)hipHostFree(h);
+            return nullptr;
+        }
+        uint32_t* flags = static_cast<uint32_t*>(h);
+        for (uint32_t i = 0; i < kCounterSlots; ++i) flags[i] = 1u;
+        CounterRing* r = new CounterRing;
+        r->release = flags;
+        g_ring_pairs[dev] = static_cast<unsigned*>(p);
+        g_ring_release_dev[dev] = static_cast<unsigned*>(hd);
+        g_ring[dev] = r;
+    }
+    return g_ring[dev];
+}
+
+}  // namespace
+
+// A counter pair of the current device's ring for one launch on stream s
+// (counters.hpp), or none (pair null: the static schedule) while s captures a
+// graph (a replayed graph keeps the counters it was captured with and may
+// run beside later launches), while every slot is held by a launch still in
+// flight, or when the ring cannot be set up.
+TileCounters take_counters(hipStream_t s)
+{
+    const TileCounters none{nullptr, nullptr, -1};
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(s, &cap) != hipSuccess) {
         (void)hipGetLastError();  // the query's own error, not the launch's
-        return nullptr;
+        return none;
     }
-    if (cap != hipStreamCaptureStatusNone || n == 0 || n > kCounterRing) return nullptr;
-    constexpr int kDevices = 64;
-    static std::mutex mu;
-    static unsigned* base[kDevices] = {nullptr};
-    static std::atomic<uint64_t> cursor[kDevices];
+    if (cap != hipStreamCaptureStatusNone) return none;
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kDevices) return nullptr;
-    unsigned* b;
-    {
-        std::lock_guard<std::mutex> lock(mu);
-        if (!base[dev]) {
-            void* p = nullptr;
-            if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_counter_ring)) != hipSuccess || !p) {
-                (void)hipGetLastError();
-                return nullptr;
-            }
-            base[dev] = static_cast<unsigned*>(p);
-        }
-        b = base[dev];
-    }
-    return b + ring_take(cursor[dev], n, kCounterRing);
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kRingDevices) return none;
+    CounterRing* r = device_ring(dev);
+    if (!r) return none;
+    const int64_t slot = ring_acquire(*r);
+    if (slot < 0) return none;
+    return TileCounters{g_ring_pairs[dev] + 2 * slot, g_ring_release_dev[dev] + slot, slot};
+}
+
+// Hands back the slot of a launch that failed to start (its kernel never
+// releases it); call on the device the slot was taken on.
+void return_counters(const TileCounters& tc)
+{
+    if (!tc.pair || tc.slot < 0) return;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kRingDevices) return;
+    CounterRing* r = g_ring[dev];
+    if (r) ring_release(*r, tc.slot);
 }
 
 namespace {
@@ -761,7 +810,7 @@ hipError_t launch_plain(const CodecArgs& a, int grid, const uint16_t* map, const
     if constexpr (MODE == MODE_ENCODE || Q == 2 || M <= 2) {
         const bool scaled = a.scale_mode == SCALE_CODEC && a.beta != 1.f;
         const bool codes = MODE != MODE_DECODE && a.codes_f32;
-        unsigned* tiles = g_codec_dynamic ? take_counters(s, 2) : nullptr;
+        const TileCounters tiles = g_codec_dynamic ? take_counters(s) : TileCounters{nullptr, nullptr, -1};
         // packed words are always written by the encoder, optional in the
         // round trip (e8_quantize asks for the decoded blocks only)
         const bool pk = MODE == MODE_ENCODE || (MODE == MODE_ROUNDTRIP && a.packed);
@@ -790,7 +839,9 @@ hipError_t launch_plain(const CodecArgs& a, int grid, const uint16_t* map, const
             }
         }
 #undef COSET_PLAIN
-        return hipGetLastError();
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return_counters(tiles);
+        return e;
     }
     return hipErrorInvalidValue;
 }

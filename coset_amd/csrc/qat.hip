@@ -214,6 +214,13 @@ __device__ __forceinline__ void stats_write(const StatsArgs& a, int64_t t, doubl
     a.xmax_ema[t] = __fadd_rn(__fmul_rn(a.xmax_ema[t], a.m), __fmul_rn(a.one_minus_m, x1));
 }
 
+// max(a, b) that returns a NaN operand (the reference's Tensor.amax
+// propagates NaN; fmaxf would drop it)
+__device__ __forceinline__ float max_nan(float a, float b)
+{
+    return (b > a || b != b) ? b : a;
+}
+
 // one workgroup (256 threads) per tile
 __global__ void __launch_bounds__(256) qat_stats_tile_kernel(StatsArgs a)
 {
@@ -226,12 +233,12 @@ __global__ void __launch_bounds__(256) qat_stats_tile_kernel(StatsArgs a)
     for (int64_t i = threadIdx.x; i < a.n; i += blockDim.x) {
         float v = w[i];
         sum += (double)v;
-        amax = fmaxf(amax, fabsf(v));
+        amax = max_nan(amax, fabsf(v));
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
         sum += __shfl_down(sum, off, 64);
-        amax = fmaxf(amax, __shfl_down(amax, off, 64));
+        amax = max_nan(amax, __shfl_down(amax, off, 64));
     }
     if ((threadIdx.x & 63) == 0) {
         s_d[threadIdx.x >> 6] = sum;
@@ -239,7 +246,7 @@ __global__ void __launch_bounds__(256) qat_stats_tile_kernel(StatsArgs a)
     }
     __syncthreads();
     const double mean = ((s_d[0] + s_d[1]) + (s_d[2] + s_d[3])) / (double)a.n;
-    amax = fmaxf(fmaxf(s_f[0], s_f[1]), fmaxf(s_f[2], s_f[3]));
+    amax = max_nan(max_nan(s_f[0], s_f[1]), max_nan(s_f[2], s_f[3]));
     __syncthreads();
     double m2 = 0.0;
     for (int64_t i = threadIdx.x; i < a.n; i += blockDim.x) {
@@ -266,7 +273,7 @@ __global__ void __launch_bounds__(256) qat_stats_block_kernel(StatsArgs a)
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         sum += (double)x[j];
-        amax = fmaxf(amax, fabsf(x[j]));
+        amax = max_nan(amax, fabsf(x[j]));
     }
     const double mean = sum / 8.0;
     double m2 = 0.0;

@@ -82,8 +82,12 @@ def load_packed(path: str, device: Optional[torch.device] = None) -> "PackedLine
 
 class PackedLinear(nn.Module):
     """y = x @ (decode(words) / beta)^T + bias through the vLUT matmul, with
-    the words prepared once (decoded to bytes in fragment order).  x: [..., in] fp16 or
-    bf16 (fp32 is cast to bf16: 2 x_hat is exact in both) -> fp32."""
+    the words prepared once (decoded to bytes in fragment order).  x: [..., in]
+    fp16 or bf16, or fp32 (run on the matrix cores as three exact bf16 planes
+    where the decoded format applies, else by the LDS-table method) -> fp32.
+
+    Only the prepared weight is resident on the GPU; the raw level words stay
+    in host memory (``words``), read by ``dequantized_weight()`` alone."""
 
     def __init__(self, tensors: Dict[str, torch.Tensor], meta: Dict[str, object],
                  device: Optional[torch.device] = None):
@@ -94,7 +98,7 @@ class PackedLinear(nn.Module):
         words = on_gpu(tensors["words"]) if device is None else tensors["words"].to(device)
         if words.shape != (self.out_features, self.in_features // 8, self.M):
             raise ValueError(f"words shape {tuple(words.shape)} does not match the metadata")
-        self.words = words
+        self.words = words.cpu()   # host copy: the GPU keeps only the prepared format
         # decoded once to 2 x_hat bytes where they fit (q = 4, M <= 2; q = 2, M <= 4), else cid | idx words
         fits = (self.q == 4 and self.M <= 2) or (self.q == 2 and self.M <= 4)
         self.prepared = vlut_prepare(words, self.q, legacy=False, layout="decoded" if fits else "tiled")
@@ -126,5 +130,6 @@ class PackedLinear(nn.Module):
 
     def dequantized_weight(self) -> torch.Tensor:
         """decode(words) / beta, [out, in] fp32 (no clamp)."""
-        dec = hnlq_decode(self.words.reshape(-1, self.M), self.q, self.M, None)
+        words = self.words.to(self.beta.device)
+        dec = hnlq_decode(words.reshape(-1, self.M), self.q, self.M, None)
         return dec.reshape(self.out_features, self.in_features) / self.beta.view(-1, 1)

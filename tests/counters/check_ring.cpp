@@ -1,4 +1,8 @@
 // CPU unit test of the counter-ring bookkeeping (coset_amd/csrc/counters.hpp).
+// A "launch" takes a slot with ring_acquire and its kernel's last workgroup
+// releases it; here the release is ring_release, called when the simulated
+// launch finishes.
+#include <atomic>
 #include <cstdio>
 #include <thread>
 #include <vector>
@@ -8,59 +12,134 @@
 static int fails = 0;
 #define CHECK(c) do { if (!(c)) { std::printf("FAIL %s:%d %s\n", __FILE__, __LINE__, #c); ++fails; } } while (0)
 
+using coset::CounterRing;
+using coset::ring_acquire;
+using coset::ring_release;
+
+struct Ring {
+    std::vector<uint32_t> flags;
+    CounterRing r;
+    explicit Ring(uint32_t slots) : flags(slots, 1u)
+    {
+        r.slots = slots;
+        r.release = flags.data();
+    }
+};
+
+// The earlier scheme: slots handed out by a cursor alone, whether or not the
+// previous holder has finished.  The held-back check below must catch it.
+static int64_t acquire_by_cursor(CounterRing& r)
+{
+    const uint32_t s = r.cursor;
+    r.cursor = (s + 1) % r.slots;
+    r.release[s] = 0u;
+    return s;
+}
+
+// One launch held back (never finishing) while `others` launches start and
+// finish one after another; returns how many of them were handed its slot.
+template <typename Acquire>
+static int held_back_sharing(uint32_t slots, int others, Acquire acquire)
+{
+    Ring ring(slots);
+    const int64_t held = acquire(ring.r);
+    int shared = 0;
+    for (int i = 0; i < others; ++i) {
+        const int64_t s = acquire(ring.r);
+        if (s == held) ++shared;
+        if (s >= 0) ring_release(ring.r, s);
+    }
+    return shared;
+}
+
 int main()
 {
-    using coset::ring_take;
-    // sequential runs are consecutive, wrap at the end and never cross it
+    // launches that finish in order take the slots in ring order
     {
-        std::atomic<uint64_t> cur{0};
-        const uint32_t ring = 10;
-        uint32_t want[] = {0, 3, 6, 0, 3, 6, 0};
-        for (uint32_t w : want) CHECK(ring_take(cur, 3, ring) == w);
-        std::atomic<uint64_t> c2{0};
-        for (int i = 0; i < 100; ++i) {
-            const uint32_t n = 1 + (uint32_t)(i * 7 % 10);
-            const uint32_t o = ring_take(c2, n, ring);
-            CHECK(o + n <= ring);
+        Ring ring(5);
+        for (int i = 0; i < 12; ++i) {
+            const int64_t s = ring_acquire(ring.r);
+            CHECK(s == i % 5);
+            ring_release(ring.r, s);
         }
-        std::atomic<uint64_t> c3{0};
-        for (int i = 0; i < 5; ++i) CHECK(ring_take(c3, ring, ring) == 0);   // the whole ring each time
     }
-    // concurrent takers: within one lap of the ring no two runs overlap
+    // a held-back launch keeps its slot through many laps of the ring, at the
+    // real ring size and a tiny one; a cursor-only scheme hands it out again
     {
-        const uint32_t ring = coset::kCounterRing, n = 2;
-        const int threads = 8, per = 256;   // 8 * 256 * 2 = 4096 < ring: one lap
-        std::atomic<uint64_t> cur{0};
-        std::vector<std::vector<uint32_t>> got(threads);
+        CHECK(held_back_sharing(coset::kCounterSlots, 3 * (int)coset::kCounterSlots, ring_acquire) == 0);
+        CHECK(held_back_sharing(3, 100, ring_acquire) == 0);
+        CHECK(held_back_sharing(coset::kCounterSlots, 3 * (int)coset::kCounterSlots, acquire_by_cursor) == 3);
+        CHECK(held_back_sharing(3, 100, acquire_by_cursor) == 33);
+    }
+    // released late, the slot is handed out again within one lap
+    {
+        Ring ring(4);
+        const int64_t held = ring_acquire(ring.r);
+        for (int i = 0; i < 10; ++i) ring_release(ring.r, ring_acquire(ring.r));
+        ring_release(ring.r, held);
+        bool back = false;
+        for (int i = 0; i < 4 && !back; ++i) {
+            const int64_t s = ring_acquire(ring.r);
+            back = s == held;
+            ring_release(ring.r, s);
+        }
+        CHECK(back);
+    }
+    // every slot held: no slot (the static schedule); one released: that one
+    {
+        Ring ring(6);
+        std::vector<int> seen(6, 0);
+        for (int i = 0; i < 6; ++i) {
+            const int64_t s = ring_acquire(ring.r);
+            CHECK(s >= 0 && s < 6);
+            if (s >= 0 && s < 6) ++seen[s];
+        }
+        for (int c : seen) CHECK(c == 1);
+        CHECK(ring_acquire(ring.r) == -1);
+        ring_release(ring.r, 4);
+        CHECK(ring_acquire(ring.r) == 4);
+        CHECK(ring_acquire(ring.r) == -1);
+    }
+    // concurrent launches that finish out of order: no slot is ever held by
+    // two launches at once
+    {
+        Ring ring(64);
+        std::vector<std::atomic<int>> owner(64);
+        for (auto& o : owner) o.store(0);
+        std::atomic<int> doubles{0}, none{0};
         std::vector<std::thread> ts;
-        for (int t = 0; t < threads; ++t)
+        for (int t = 0; t < 8; ++t)
             ts.emplace_back([&, t] {
-                for (int i = 0; i < per; ++i) got[t].push_back(ring_take(cur, n, ring));
+                std::vector<int64_t> mine;
+                for (int i = 0; i < 20000; ++i) {
+                    const int64_t s = ring_acquire(ring.r);
+                    if (s < 0) {
+                        ++none;
+                    } else {
+                        if (owner[s].exchange(t + 1) != 0) ++doubles;
+                        mine.push_back(s);
+                    }
+                    // finish a pseudo-random earlier launch of this thread, or hold on
+                    const size_t k = (size_t)((i * 2654435761u + t) % 7);
+                    if (!mine.empty() && k < 4) {
+                        const size_t j = (size_t)((i * 40503u) % mine.size());
+                        const int64_t f = mine[j];
+                        mine.erase(mine.begin() + (long)j);
+                        owner[f].store(0);
+                        ring_release(ring.r, f);
+                    }
+                }
+                for (int64_t f : mine) {
+                    owner[f].store(0);
+                    ring_release(ring.r, f);
+                }
             });
         for (auto& th : ts) th.join();
-        std::vector<int> use(ring, 0);
-        for (auto& g : got)
-            for (uint32_t o : g) {
-                CHECK(o + n <= ring);
-                for (uint32_t j = 0; j < n; ++j) ++use[o + j];
-            }
-        int twice = 0, once = 0;
-        for (int u : use) {
-            twice += u > 1;
-            once += u == 1;
-        }
-        CHECK(twice == 0);
-        CHECK(once == threads * per * (int)n);
-    }
-    // runs of different sizes over many laps stay inside the ring
-    {
-        std::atomic<uint64_t> cur{0};
-        const uint32_t ring = coset::kCounterRing;
-        for (int i = 0; i < 100000; ++i) {
-            const uint32_t n = 1 + (uint32_t)((i * 2654435761u) % 300);
-            const uint32_t o = ring_take(cur, n, ring);
-            CHECK(o + n <= ring);
-        }
+        CHECK(doubles.load() == 0);
+        int held = 0;
+        for (uint32_t f : ring.flags) held += f != 1u;
+        CHECK(held == 0);
+        std::printf("concurrent: %d acquisitions found every slot held\n", none.load());
     }
     std::printf("%s (%d failures)\n", fails ? "FAILED" : "ok", fails);
     return fails ? 1 : 0;

@@ -509,7 +509,7 @@ def test_dynamic_schedule_on_many_streams(ca):
         torch.cuda.synchronize()
         for i, o in enumerate(outs):
             assert torch.equal(o, ref), i
-        # 8300 launches on one stream: past one lap of the 16384-counter ring
+        # 8300 launches on one stream: past one lap of the ring's 8192 counter pairs
         out = torch.empty_like(ref)
         small = x[:4096]
         _lib.set_codec_dynamic(False)
@@ -519,6 +519,46 @@ def test_dynamic_schedule_on_many_streams(ca):
             ca.hnlq_roundtrip(small, 4, 2, 1.0, decoded_out=out[:4096], want_packed=False)
         torch.cuda.synchronize()
         assert torch.equal(out[:4096], ref_small)
+    finally:
+        _lib.set_codec_dynamic(True)
+        _lib.set_codec_path(0)
+
+
+def test_dynamic_schedule_held_back_launch(ca):
+    """A launch queued behind other work on its stream while more than one
+    lap of the counter ring's launches start and finish on another stream,
+    the last of them large enough to run beside it: the held-back launch
+    keeps its counter pair until it has finished, so both results equal the
+    static schedule's."""
+    from coset_amd import _lib
+    _lib.require_gpu()
+    rng = np.random.default_rng(33)
+    x = dev(rng.standard_normal(((1 << 21) + 77, 8)).astype(np.float32))
+    small = x[:2048]
+    try:
+        _lib.set_codec_path(2)
+        _lib.set_codec_dynamic(False)
+        _, ref = ca.hnlq_roundtrip(x, 4, 2, 1.0)
+        _, ref_small = ca.hnlq_roundtrip(small, 4, 2, 1.0)
+        _lib.set_codec_dynamic(True)
+        torch.cuda.synchronize()
+        sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+        busy = torch.empty(1 << 26, device="cuda")
+        out_a = torch.empty_like(ref)
+        out_b = torch.empty_like(ref)
+        out_s = torch.empty_like(ref_small)
+        with torch.cuda.stream(sa):
+            for i in range(40):            # ~10 ms of fills ahead of the held-back launch
+                busy.fill_(float(i))
+            ca.hnlq_roundtrip(x, 4, 2, 1.0, decoded_out=out_a, want_packed=False)
+        with torch.cuda.stream(sb):
+            for _ in range(8200):
+                ca.hnlq_roundtrip(small, 4, 2, 1.0, decoded_out=out_s, want_packed=False)
+            ca.hnlq_roundtrip(x, 4, 2, 1.0, decoded_out=out_b, want_packed=False)
+        torch.cuda.synchronize()
+        assert torch.equal(out_a, ref)
+        assert torch.equal(out_b, ref)
+        assert torch.equal(out_s, ref_small)
     finally:
         _lib.set_codec_dynamic(True)
         _lib.set_codec_path(0)

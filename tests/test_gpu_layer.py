@@ -328,6 +328,41 @@ def test_block_tiling_statistics_match_reference(golden):
         np.testing.assert_array_equal(layer.xmax_ema.cpu().numpy(), S[f"block_xmax_ema_{i}"])
 
 
+@pytest.mark.parametrize("tiling", ["row", "block"])
+def test_statistics_propagate_non_finite_weights(tiling):
+    """A NaN weight in one tile and an infinite one in another: the
+    statistics kernel's EMA buffers equal the reference's composition
+    (coset/core/layers.py:366-379: W.std() + 1e-8 and W.abs().amax() + 1e-8,
+    then the EMA) computed by torch on the CPU, NaN where it is NaN -- amax
+    propagates NaN, which a plain fmax would drop."""
+    import coset_amd
+    torch.manual_seed(5)
+    fout, fin = 6, 64
+    layer = coset_amd.create_e8_hnlq_linear(fin, fout, q=4, M=2, Delta0=1.5, tiling=tiling)
+    W = torch.randn(fout, fin) * 0.3
+    W[1, 17] = float("nan")
+    W[3, 40] = float("inf")
+    W[4, 2] = -float("inf")
+    blocks = W.view(fout, fin // 8, 8)
+    layer._gather_stats(blocks.cuda())
+    m = layer.ema_momentum
+    if tiling == "row":
+        sigma = blocks.std(dim=(1, 2)) + 1e-8
+        xmax = blocks.abs().amax(dim=(1, 2)) + 1e-8
+    else:
+        sigma = blocks.std(dim=2).reshape(-1) + 1e-8
+        xmax = blocks.abs().amax(dim=2).reshape(-1) + 1e-8
+    ones = torch.ones_like(sigma)
+    want_s = ones.mul(m).add((1 - m) * sigma)
+    want_x = ones.mul(m).add((1 - m) * xmax)
+    assert torch.isnan(want_x).any() and torch.isinf(want_x).any()
+    # finite entries: torch's CPU std may round its last bit differently from
+    # the kernel's double-precision variance (bit parity is pinned on the
+    # reference's own statistics in layer_stats.npz); NaN and inf exactly
+    torch.testing.assert_close(layer.sigma_ema.cpu(), want_s, rtol=1e-6, atol=0, equal_nan=True)
+    torch.testing.assert_close(layer.xmax_ema.cpu(), want_x, rtol=0, atol=0, equal_nan=True)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("rows,cols", [(4096, 768), (4096, 3072), (1, 8), (65, 24), (0, 16), (130, 40)])
 def test_colsum_is_exact_fp32_sum(dtype, rows, cols):

@@ -298,6 +298,43 @@ def test_fp32_plane_sum_is_the_planes_products(B, rows, K):
         assert torch.equal(got, want)
 
 
+@pytest.mark.parametrize("deep", [1, 0])
+@pytest.mark.parametrize("splits", [3, 8, 64])
+@pytest.mark.parametrize("B,rows,K", [(40, 128, 4096), (40, 72, 136)])
+def test_fp32_plane_sum_on_split_wide_and_deep_kernels(deep, splits, B, rows, K):
+    """fp32 activations on a forced K split of the deep kernel and of the
+    wide one (set_vlut_deep(False)): the split-major partials reach the fused
+    three-plane reduce with the indexing each kernel writes, so the output is
+    bit for bit ((y_1 + y_2) + y_3) + bias of the planes run as 3B tokens
+    under the same plan."""
+    import coset_amd
+    from coset_amd import _lib
+    rng = np.random.default_rng(B * 7 + rows + K + splits)
+    q, M = 4, 2
+    W = rng.standard_normal((rows, K)).astype(np.float32)
+    words_np = O.pack_words(O.e8_encode(W.reshape(-1, 8), q, M), q).reshape(rows, K // 8, M)
+    words = torch.from_numpy(words_np.astype(np.int32)).to(torch.uint16).cuda()
+    a_np = (rng.standard_normal((B, K)) * np.exp2(rng.integers(-20, 20, (B, K)))).astype(np.float32)
+    planes = _split3_np(a_np).reshape(3 * B, K)
+    p_bf = torch.from_numpy(planes.view(np.int16)).cuda().view(torch.bfloat16)
+    sc = torch.from_numpy(rng.uniform(0.5, 2.0, rows).astype(np.float32)).cuda()
+    bias = torch.from_numpy(rng.standard_normal(rows).astype(np.float32)).cuda()
+    try:
+        _lib.set_vlut_deep(bool(deep))
+        _lib.set_vlut_splits(splits)
+        for w in (words, coset_amd.vlut_prepare(words, q, layout="decoded")):
+            y = coset_amd.vlut_matmul(w, p_bf, q, scale=sc, method="mfma")
+            want = ((y[:B] + y[B:2 * B]) + y[2 * B:]) + bias
+            got = coset_amd.vlut_matmul(w, torch.from_numpy(a_np).cuda(), q, scale=sc, bias=bias, method="mfma")
+            assert torch.equal(got, want)
+            ref = O.vlut_matmul(words_np, sc.cpu().numpy(), a_np, q, M) + bias.cpu().numpy()
+            _close_elem(got.cpu().numpy(), ref,
+                        matmul_mag(words_np, q, M, a_np, sc.cpu().numpy()) + np.abs(bias.cpu().numpy()))
+    finally:
+        _lib.set_vlut_splits(0)
+        _lib.set_vlut_deep(True)
+
+
 def test_fp32_mfma_needs_exact_operands():
     """q = 4, M = 3 decodes beyond what bf16 holds exactly: method "mfma"
     refuses fp32 activations there, "auto" takes the LDS-table method."""

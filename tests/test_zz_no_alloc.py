@@ -96,8 +96,14 @@ def test_noalloc_refuses_plans_beyond_its_scratch():
     B, rows, K = 4096, 4096, 4096
     need = lib.coset_vlut_workspace_floats(B, rows, K, 4, 2, _lib.F16, 2)
     assert need > cap, need
-    dummy = torch.empty(16, dtype=torch.float32, device="cuda")
-    rc = lib.coset_vlut_matmul_noalloc(dummy.data_ptr(), 0, None, 0, dummy.data_ptr(), _lib.F16, B, rows, K, 4, 2, 0,
-                                       2, dummy.data_ptr(), _lib.stream_of(dummy))
+    # buffers of the plan's real sizes (8 MiB words, 32 MiB fp16 activations,
+    # 64 MiB fp32 output): should the size check ever regress, the call runs
+    # in bounds and fails the return-code assert instead of faulting
+    words = torch.zeros(rows, K // 8, 2, dtype=torch.uint16, device="cuda")
+    act = torch.zeros(B, K, dtype=torch.float16, device="cuda")
+    out = torch.empty(B, rows, dtype=torch.float32, device="cuda")
+    rc = lib.coset_vlut_matmul_noalloc(words.data_ptr(), 0, None, 0, act.data_ptr(), _lib.F16, B, rows, K, 4, 2, 0,
+                                       2, out.data_ptr(), _lib.stream_of(out))
+    torch.cuda.synchronize()
     assert rc == _lib.EINVAL
     assert b"scratch" in lib.coset_last_error()
