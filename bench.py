@@ -28,6 +28,7 @@ under extra.<config>.cpu_baseline.
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import os
 import sys
@@ -314,6 +315,34 @@ def bench_c2(torch, ca, args):
     return kernel_s, wall_s, cpu
 
 
+def bench_c2_stream(torch, ca, args):
+    """The ceiling of C2's access pattern: the C2 kernel itself (same grid,
+    tile schedule, loads and stores) with the lattice arithmetic taken out
+    (coset_probe_c2_stream: out = x, packed = a word folded from x), with and
+    without its decode-table staging, timed as C2 is."""
+    from coset_amd import _lib
+    lib = _lib.load()
+    dev = torch.device("cuda")
+    n = C2_BLOCKS
+    g = torch.Generator(device=dev).manual_seed(2)
+    x = torch.randn((n, 8), device=dev, generator=g, dtype=torch.float32)
+    packed = torch.empty((n, 2), dtype=torch.uint16, device=dev)
+    out = torch.empty((n, 8), dtype=torch.float32, device=dev)
+    res = {"workload": "C2's kernel (2^24 blocks, 68 B/block) with no lattice arithmetic: its streaming ceiling",
+           "bytes_per_block": C2_BYTES_PER_BLOCK}
+    for name, staged in (("staged", 1), ("unstaged", 0)):
+        def step():
+            _lib.check("coset_probe_c2_stream", lib.coset_probe_c2_stream(
+                x.data_ptr(), n, packed.data_ptr(), out.data_ptr(), staged, _lib.stream_of(x)))
+        k, _ = gpu_time(torch, step, args.steps, args.warmup, C2_WARM_S)
+        res[name] = {"kernel_us": round(k * 1e6, 2), "hbm_gbs": round(C2_BYTES_PER_BLOCK * n / k / 1e9, 1),
+                     "frac_hbm": round(C2_BYTES_PER_BLOCK * n / k / 1e9 / HBM_PEAK_GBS, 4)}
+    if not torch.equal(out, x):
+        sys.exit("c2 stream probe: out != x")
+    del x, packed, out
+    return res
+
+
 def bench_c2_api(torch, ca, args):
     """The C2 blocks through each codec entry point on its own: the
     reference signatures (e8_encode with its float code tensor [N, 2, 8],
@@ -492,6 +521,42 @@ def cold_time(torch, fn, flush, reps=25):
     return float(np.median([a.elapsed_time(b) for a, b in evs])) / 1e3
 
 
+STREAM_BYTES = 512 << 20   # rotation footprint of stream_time: twice the 256 MB Infinity Cache
+
+
+def stream_time(torch, fns, reps=5):
+    """Per-call GPU time of calls that each read their own copy of the data:
+    fns[i] uses copy i, and the copies together (STREAM_BYTES) are twice the
+    256 MB Infinity Cache, so every call finds its weights evicted from the
+    L2s and the MALL by the calls between and streams them from HBM.  The
+    calls are replayed from a HIP graph (no host launch cost, no events
+    between calls), as a serving step over many layers would run them."""
+    for f in fns:
+        f()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        graph.capture_begin()
+        for f in fns:
+            f()
+        graph.capture_end()
+    torch.cuda.current_stream().wait_stream(side)
+    graph.replay()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1) / 1e3 / len(fns))
+    del graph
+    return float(np.median(ts))
+
+
 def median_call_time(torch, fn, reps=25, warm_s=0.1):
     """Median GPU seconds of single calls of fn (HIP events around each call,
     all calls queued back to back), after warm_s seconds of untimed calls."""
@@ -546,6 +611,41 @@ def bench_peaks(torch, ca, args):
 C4_CODE_BYTES = 4096 * 512 * 2 * 2      # uint16 level words [4096, 512, 2]: the algorithmic weight bytes
 
 
+def c4_floors(torch, ca, flush, fmt_bytes):
+    """What a C4 call cannot beat, measured the way the calls are: the two
+    HIP events of a cold call with nothing between them, an empty launch of
+    the rows kernel's shape (256 workgroups of 512 threads) and of the deep
+    kernel's (256 of 512 with 132 KiB of LDS), and a pure read of each weight
+    format's bytes at the rows kernel's shape (cold, graph-replayed, and
+    streamed from HBM over rotating copies)."""
+    from coset_amd import _lib
+    lib = _lib.load()
+    sink = torch.empty(1 << 16, dtype=torch.int32, device="cuda")
+    st = lambda: _lib.stream_of(sink)
+
+    def empty(grid, threads, lds):
+        return lambda: _lib.check("coset_probe_empty", lib.coset_probe_empty(grid, threads, lds, sink.data_ptr(), st()))
+
+    res = {"events_only_us_cold": round(cold_time(torch, lambda: None, flush) * 1e6, 2)}
+    for name, fn in (("empty_rows_shape", empty(256, 512, 0)), ("empty_deep_shape", empty(256, 512, 135168))):
+        res[name] = {"us_cold": round(cold_time(torch, fn, flush) * 1e6, 2),
+                     "us_graph": round(graph_time(torch, lambda: (fn(), sink)[1]) * 1e6, 2)}
+    for fmt, nbytes in fmt_bytes.items():
+        nb = (nbytes + 15) // 16 * 16
+        copies = max(2, -(-STREAM_BYTES // nb))
+        bufs = [torch.empty(nb // 4, dtype=torch.int32, device="cuda").random_() for _ in range(copies)]
+
+        def rd(buf):
+            return lambda: _lib.check("coset_probe_read", lib.coset_probe_read(buf.data_ptr(), nb, 256, 512,
+                                                                               sink.data_ptr(), st()))
+        f0 = rd(bufs[0])
+        res["read_" + fmt] = {"bytes": nb, "us_cold": round(cold_time(torch, f0, flush) * 1e6, 2),
+                              "us_graph": round(graph_time(torch, lambda: (f0(), sink)[1]) * 1e6, 2),
+                              "us_stream": round(stream_time(torch, [rd(b_) for b_ in bufs]) * 1e6, 2)}
+        del bufs
+    return res
+
+
 def bench_c4(torch, ca, args):
     g = torch.Generator(device="cuda").manual_seed(5)
     W = 0.02 * torch.randn((4096, 4096), device="cuda", generator=g)
@@ -554,23 +654,40 @@ def bench_c4(torch, ca, args):
     tiled_legacy = ca.vlut_prepare(words, 4, legacy=True)   # the reference vLUT's textbook-Q residuals
     decoded = ca.vlut_prepare(words, 4, layout="decoded")    # 2 x_hat bytes in fragment order, 16 MiB
     pairs = ca.vlut_prepare(words, 4, layout="pairs")        # coordinate-pair ids in fragment order, 16 MiB
+    decoded6 = ca.vlut_prepare(words, 4, layout="decoded6")  # the same decode in 6 bytes per pair, 12 MiB
     scale = torch.full((4096,), 0.02, device="cuda")
     del W
     res = {"workload": "C4 vLUT matmul 4096x4096 q4 M2 codes (8 MiB uint16 words; 16 MiB tiled prepared or "
-                       "decoded), fp16 activations (fp32_act_*: the same values in fp32), fp32 out; us_graph = per call replayed from a HIP graph "
-                       "(weights warm in the 256 MB MALL), us_cold = one call after a 1 GiB write evicted the "
-                       "caches (median of 25), us_eager = per call from Python",
+                       "decoded, 12 MiB decoded6), fp16 activations (fp32_act_*: the same values in fp32), fp32 out; us_graph = per call replayed from a HIP graph "
+                       "(weights warm in the 256 MB MALL), us_stream = per call replayed from a HIP graph over "
+                       "copies of the weights twice the MALL's size (each call streams its weights from HBM), "
+                       "us_cold = one call between two HIP events after a 1 GiB write evicted the "
+                       "caches (median of 25; includes the events' own cost, floors.events_only_us_cold), "
+                       "us_eager = per call from Python",
            "algorithmic_bytes": "8 MiB codes + B * 8 KiB fp16 (16 KiB fp32) activations + B * 16 KiB fp32 output "
                                 "(frac_hbm*); format_bytes counts the prepared format actually read",
            "batches": {}}
     ws = torch.empty(64 * 4096 * 64, dtype=torch.float32, device="cuda")
     flush = torch.empty(1 << 28, dtype=torch.float32, device="cuda")
+    wbytes_of = lambda wts: (wts.data.numel() * 4 if isinstance(wts, ca.PreparedWords)
+                             else wts.numel() * wts.element_size())
+    res["floors"] = c4_floors(torch, ca, flush, {"raw_words": wbytes_of(words), "decoded6": wbytes_of(decoded6),
+                                                  "decoded": wbytes_of(decoded)})
+    # the formats streamed from HBM: copies whose total is STREAM_BYTES
+    stream_sets = {}
+    for key, wts in (("mfma_decoded6", decoded6), ("mfma_decoded", decoded), ("mfma_raw_words", words)):
+        n = max(2, -(-STREAM_BYTES // wbytes_of(wts)))
+        if isinstance(wts, ca.PreparedWords):
+            stream_sets[key] = [wts] + [dataclasses.replace(wts, data=wts.data.clone()) for _ in range(n - 1)]
+        else:
+            stream_sets[key] = [wts] + [wts.clone() for _ in range(n - 1)]
     words_host = words.cpu().numpy().astype(np.uint32) if args.cpu else None
     for B in (1, 8, 64):
         a = torch.randn((B, 4096), device="cuda", generator=g).to(torch.float16)
         a32 = a.float()   # the same values as fp32 activations (the matrix cores take them as three bf16 planes)
         row = {}
-        for method, wts in (("mfma", tiled), ("mfma_decoded", decoded), ("mfma_legacy_q", tiled_legacy),
+        for method, wts in (("mfma_decoded6", decoded6), ("mfma", tiled), ("mfma_decoded", decoded),
+                            ("mfma_legacy_q", tiled_legacy),
                             ("mfma_raw_words", words), ("lds", pairs), ("lds_tiled", tiled),
                             ("fp32_act_mfma_decoded", decoded), ("fp32_act_lds", pairs)):
             m = "lds" if method.endswith("lds") or method == "lds_tiled" else "mfma"
@@ -579,24 +696,32 @@ def bench_c4(torch, ca, args):
             k_eager, _ = gpu_time(torch, fn, 50 if m == "lds" else 100, 5, 0.05)
             k = graph_time(torch, fn)
             kc = cold_time(torch, fn, flush)
-            wbytes = wts.data.numel() * 4 if isinstance(wts, ca.PreparedWords) else wts.numel() * wts.element_size()
+            wbytes = wbytes_of(wts)
             io_bytes = B * 4096 * act.element_size() + B * 4096 * 4
             nbytes = C4_CODE_BYTES + io_bytes
             flops = 2.0 * B * 4096 * 4096
-            row[method] = {"tokens_per_s": round(B / k, 1), "us_graph": round(k * 1e6, 2),
-                           "us_cold": round(kc * 1e6, 2), "us_eager": round(k_eager * 1e6, 2),
-                           "tokens_per_s_cold": round(B / kc, 1),
-                           "gbs_algorithmic": round(nbytes / k / 1e9, 1),
-                           "frac_hbm": round(nbytes / k / 1e9 / HBM_PEAK_GBS, 4),
-                           "frac_hbm_cold": round(nbytes / kc / 1e9 / HBM_PEAK_GBS, 4),
-                           "format_bytes": wbytes + io_bytes,
-                           "frac_hbm_format_cold": round((wbytes + io_bytes) / kc / 1e9 / HBM_PEAK_GBS, 4),
-                           "dense_equiv_tflops": round(flops / k / 1e12, 2),
-                           "frac_fp16_mfma": round(flops / k / 1e12 / FP16_MFMA_TFLOPS, 5)}
+            r = {"tokens_per_s": round(B / k, 1), "us_graph": round(k * 1e6, 2),
+                 "us_cold": round(kc * 1e6, 2), "us_eager": round(k_eager * 1e6, 2),
+                 "tokens_per_s_cold": round(B / kc, 1),
+                 "gbs_algorithmic": round(nbytes / k / 1e9, 1),
+                 "frac_hbm": round(nbytes / k / 1e9 / HBM_PEAK_GBS, 4),
+                 "frac_hbm_cold": round(nbytes / kc / 1e9 / HBM_PEAK_GBS, 4),
+                 "format_bytes": wbytes + io_bytes,
+                 "frac_hbm_format_cold": round((wbytes + io_bytes) / kc / 1e9 / HBM_PEAK_GBS, 4),
+                 "dense_equiv_tflops": round(flops / k / 1e12, 2),
+                 "frac_fp16_mfma": round(flops / k / 1e12 / FP16_MFMA_TFLOPS, 5)}
+            if method in stream_sets:
+                fns = [(lambda w_=w_: ca.vlut_matmul(w_, act, 4, scale=scale, method=m, workspace=ws))
+                       for w_ in stream_sets[method]]
+                ks = stream_time(torch, fns)
+                r.update({"us_stream": round(ks * 1e6, 2), "tokens_per_s_stream": round(B / ks, 1),
+                          "frac_hbm_stream": round(nbytes / ks / 1e9 / HBM_PEAK_GBS, 4),
+                          "frac_hbm_format_stream": round((wbytes + io_bytes) / ks / 1e9 / HBM_PEAK_GBS, 4)})
+            row[method] = r
         res["batches"][str(B)] = row
         if args.cpu:
             row["cpu_baseline"] = cpu_c4(words_host, a.float().cpu().numpy())
-    del flush
+    del flush, stream_sets
     return res
 
 
@@ -649,7 +774,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", dest="cpu", action="store_false",
                     help="skip the host-CPU baselines (the C oracle on the host cores)")
-    ap.add_argument("--only", default="c1,c2,c2codes,c2api,c3,c4,c5,peaks",
+    ap.add_argument("--only", default="c1,c2,c2stream,c2codes,c2api,c3,c4,c5,peaks",
                     help="comma list of workloads to run")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 512 MiB device copy (HBM counter calibration)")
@@ -677,8 +802,9 @@ def main():
     cpu = None
     if "c2" in only:
         kernel_s, wall_s, cpu = bench_c2(torch, ca, args)
-    for name, fn in (("c1", bench_c1), ("c2codes", bench_c2_codes), ("c2api", bench_c2_api), ("c3", bench_c3),
-                     ("c4", bench_c4), ("c5", bench_c5), ("peaks", bench_peaks)):
+    for name, fn in (("c1", bench_c1), ("c2stream", bench_c2_stream), ("c2codes", bench_c2_codes),
+                     ("c2api", bench_c2_api), ("c3", bench_c3), ("c4", bench_c4), ("c5", bench_c5),
+                     ("peaks", bench_peaks)):
         if name in only:
             extra[name] = fn(torch, ca, args)
             torch.cuda.empty_cache()
@@ -704,8 +830,81 @@ def main():
             "parity": "bit-exact vs oracle on 4096 sampled blocks",
             "cpu_baseline": cpu,
         })
+    if kernel_s is not None and "c2stream" in extra:
+        extra["c2stream"]["c2_frac_of_ceiling"] = round(extra["c2stream"]["staged"]["kernel_us"] / (kernel_s * 1e6), 4)
+    # the detailed record first (one line), then the record the driver reads:
+    # the same top-level fields with one compact object per configuration
     rec["extra"] = extra
     print(json.dumps(rec), flush=True)
+    rec["extra"] = summarize(extra)
+    rec["detail"] = "the line above holds every figure of this run"
+    print(json.dumps(rec), flush=True)
+
+
+def _pick(d, *path):
+    for k in path:
+        if not isinstance(d, dict) or k not in d:
+            return None
+        d = d[k]
+    return d
+
+
+def summarize(extra):
+    """One compact object per configuration: time, fraction of its roofline,
+    the C4 cold and HBM-streamed times, and the CPU baseline's value."""
+    out = {}
+    c1 = extra.get("c1")
+    if c1:
+        out["c1"] = {"us_graph": _pick(c1, "graph", "us_per_forward_gpu"), "us_eager": c1.get("us_per_forward_gpu"),
+                     "us_nondegenerate": _pick(c1, "nondegenerate", "us_per_forward_gpu"),
+                     "cpu_us": _pick(c1, "cpu_baseline", "value")}
+    c2s = extra.get("c2stream")
+    if c2s:
+        out["c2stream"] = {"us": _pick(c2s, "staged", "kernel_us"), "frac_hbm": _pick(c2s, "staged", "frac_hbm"),
+                           "us_unstaged": _pick(c2s, "unstaged", "kernel_us"),
+                           "c2_frac_of_ceiling": c2s.get("c2_frac_of_ceiling")}
+    c2c = extra.get("c2codes")
+    if c2c:
+        out["c2codes"] = {"us": c2c.get("kernel_us"), "frac_hbm": c2c.get("frac_hbm")}
+    c2a = extra.get("c2api")
+    if c2a:
+        out["c2api_us"] = {k: v.get("kernel_us") for k, v in c2a.get("calls", {}).items()}
+    c3 = extra.get("c3")
+    if c3:
+        out["c3"] = {"us": c3.get("kernel_us"), "gbs": c3.get("hbm_gbs"), "frac_hbm": c3.get("frac_hbm"),
+                     "cpu_gblocks_s": _pick(c3, "cpu_baseline", "value")}
+    c4 = extra.get("c4")
+    if c4:
+        o4 = {}
+        for B, row in c4.get("batches", {}).items():
+            best = min((v for k, v in row.items() if isinstance(v, dict) and "us_graph" in v
+                        and not k.startswith("fp32") and k != "mfma_legacy_q"), key=lambda v: v.get("us_graph", 1e9))
+            name = [k for k, v in row.items() if v is best][0]
+            o4["B" + B] = {"method": name, "us_graph": best.get("us_graph"), "us_stream": best.get("us_stream"),
+                           "us_cold": best.get("us_cold"), "frac_hbm": best.get("frac_hbm"),
+                           "frac_hbm_stream": best.get("frac_hbm_stream"), "frac_hbm_cold": best.get("frac_hbm_cold"),
+                           "lds_us_graph": _pick(row, "lds", "us_graph"),
+                           "cpu_tokens_s": _pick(row, "cpu_baseline", "value")}
+            for k in ("mfma_decoded", "mfma_decoded6", "mfma_raw_words"):
+                if k in row and row[k] is not best:
+                    o4["B" + B][k] = {f: row[k].get(f) for f in ("us_graph", "us_stream", "us_cold")}
+        fl = c4.get("floors", {})
+        o4["floors"] = {"events_only_us_cold": fl.get("events_only_us_cold"),
+                        "empty_us_cold": _pick(fl, "empty_rows_shape", "us_cold"),
+                        "empty_us_graph": _pick(fl, "empty_rows_shape", "us_graph")}
+        for k, v in fl.items():
+            if k.startswith("read_"):
+                o4["floors"][k] = {f: v.get(f) for f in ("us_cold", "us_graph", "us_stream")}
+        out["c4"] = o4
+    c5 = extra.get("c5")
+    if c5:
+        out["c5"] = {k: {"ms_graph": _pick(v, "graph", "ms"), "frac_mfma": _pick(v, "graph", "frac_bf16_mfma"),
+                         "ms_eager": v.get("ms"), "cpu_tokens_s": _pick(v, "cpu_baseline", "value")}
+                     for k, v in c5.get("shapes", {}).items()}
+    pk = extra.get("peaks")
+    if pk:
+        out["peaks"] = {"copy_gbs": _pick(pk, "copy", "gbs"), "gemm_bf16_tflops": _pick(pk, "gemm_bf16", "tflops")}
+    return out
 
 
 if __name__ == "__main__":

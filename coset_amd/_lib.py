@@ -65,6 +65,9 @@ SIGNATURES = {
     "coset_colsum": [_vp, _int, _i64, _i64, _vp, _vp, _i64, _vp],
     "coset_vlut_matmul_noalloc": [_vp, _int, _vp, _int, _vp, _int, _i64, _i64, _i64, _int, _int, _int, _int, _vp,
                                   _vp],
+    "coset_probe_empty": [_int, _int, _int, _vp, _vp],
+    "coset_probe_read": [_vp, _i64, _int, _int, _vp, _vp],
+    "coset_probe_c2_stream": [_vp, _i64, _vp, _vp, _int, _vp],
     "coset_init": [_int],
     "coset_set_option": [_int, _int],
 }

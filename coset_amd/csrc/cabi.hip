@@ -12,6 +12,7 @@
 #include "../../include/coset_amd.h"
 #include "codec_kernels.hpp"
 #include "legacy.hpp"
+#include "probes.hpp"
 #include "tables.hpp"
 #include "vlut.hpp"
 
@@ -632,7 +633,7 @@ int coset_lsq_bwd(const void* x, const void* g, int dtype, int64_t n, const floa
 
 int64_t coset_vlut_prepared_words(int64_t rows, int64_t kb, int M, int word_format)
 {
-    if (rows < 0 || kb < 0 || M < 1 || word_format < 0 || word_format > 4) return 0;
+    if (rows < 0 || kb < 0 || M < 1 || word_format < 0 || word_format > 5) return 0;
     return coset::vlut_prepared_words(rows, kb, M, word_format);
 }
 
@@ -642,9 +643,16 @@ int coset_vlut_prepare(const void* words, int64_t rows, int64_t kb, int M, int q
     if (q != 2 && q != 4) return fail(COSET_EUNSUPPORTED, "vLUT prepare supports q = 2 or 4 (got %d)", q);
     if (rows < 0 || kb < 0 || M < 1 || M > 4) return fail(COSET_EINVAL, "bad shape rows=%lld kb=%lld M=%d",
                                                          (long long)rows, (long long)kb, M);
-    if (word_format < 1 || word_format > 4) return fail(COSET_EINVAL, "prepared word_format must be 1, 2, 3 or 4");
+    if (word_format < 1 || word_format > 5) return fail(COSET_EINVAL, "prepared word_format must be 1, 2, 3, 4 or 5");
     if (word_format == 3 && !((q == 4 && M <= 2) || (q == 2 && M <= 4)))
         return fail(COSET_EUNSUPPORTED, "decoded format needs |2 x_hat| <= 127: q = 4 with M <= 2 or q = 2 with M <= 4");
+    if (word_format == 5) {
+        const coset::DecodeTables* t = nullptr;
+        int rc = check_hip(coset::get_decode_tables(q, legacy ? 1 : 0, &t), "decode tables");
+        if (rc) return rc;
+        if (coset::decoded6_offset(*t, M) < 0)
+            return fail(COSET_EUNSUPPORTED, "the 6-byte decoded format does not hold 2 x_hat at q = %d, M = %d", q, M);
+    }
     if (rows * kb > 0 && (!words || !prepared)) return fail(COSET_EINVAL, "NULL buffer");
     if (!aligned(prepared, 16)) return fail(COSET_EINVAL, "prepared must be 16-byte aligned");
     return check_hip(coset::vlut_prepare((const uint16_t*)words, rows, kb, M, q, legacy ? 1 : 0, word_format, prepared,
@@ -686,10 +694,12 @@ static int vlut_matmul_impl(const void* words, int word_format, const float* sca
         return fail(COSET_EINVAL, "workspace holds %lld floats, needs %lld", (long long)workspace_floats,
                     (long long)need);
     if (need > 0 && !workspace) return fail(COSET_EINVAL, "NULL workspace");
-    if (word_format < 0 || word_format > 4) return fail(COSET_EINVAL, "word_format must be 0, 1, 2, 3 or 4");
+    if (word_format < 0 || word_format > 5) return fail(COSET_EINVAL, "word_format must be 0, 1, 2, 3, 4 or 5");
     if (word_format == 3 && plan.kernel != coset::VK_MFMA_ROWS && plan.kernel != coset::VK_MFMA_WIDE &&
         plan.kernel != coset::VK_MFMA_DEEP)
         return fail(COSET_EUNSUPPORTED, "the decoded format runs on the matrix-core rows kernel only (fp16/bf16 activations)");
+    if (word_format == 5 && plan.kernel != coset::VK_MFMA_ROWS && plan.kernel != coset::VK_MFMA_DEEP)
+        return fail(COSET_EUNSUPPORTED, "the 6-byte decoded format runs on the matrix-core rows and deep kernels only");
     if (word_format != 0 && !aligned(words, 16)) return fail(COSET_EINVAL, "prepared words must be 16-byte aligned");
     coset::VlutMatmulArgs p{};
     p.words = words;
@@ -778,6 +788,39 @@ int coset_e8_lattice_op(int op, int legacy, const float* in, int64_t n_blocks, i
     if (op == COSET_OP_ENCODE_COORDS && q < 1) return fail(COSET_EINVAL, "q must be positive");
     return check_hip(coset::launch_lattice_op(op, legacy, in, n_blocks, q, out, (hipStream_t)stream),
                      "lattice op launch");
+}
+
+// ---------------------------------------------------------------- measurement probes
+
+int coset_probe_empty(int grid, int threads, int lds_bytes, uint32_t* out, void* stream)
+{
+    if (grid < 1 || grid > (1 << 24) || threads < 64 || threads > 1024 || threads % 64)
+        return fail(COSET_EINVAL, "grid in [1, 2^24] and threads a multiple of 64 in [64, 1024] required");
+    if (lds_bytes < 0 || lds_bytes > 160 * 1024) return fail(COSET_EINVAL, "lds_bytes outside [0, 160 KiB]");
+    if (!out) return fail(COSET_EINVAL, "NULL buffer");
+    return check_hip(coset::launch_probe_empty(grid, threads, lds_bytes, out, (hipStream_t)stream), "probe launch");
+}
+
+int coset_probe_read(const void* src, int64_t bytes, int grid, int threads, uint32_t* out, void* stream)
+{
+    if (grid < 1 || grid > (1 << 24) || threads < 64 || threads > 1024 || threads % 64)
+        return fail(COSET_EINVAL, "grid in [1, 2^24] and threads a multiple of 64 in [64, 1024] required");
+    if (bytes < 16 || bytes % 16) return fail(COSET_EINVAL, "bytes must be a positive multiple of 16");
+    if (!src || !out) return fail(COSET_EINVAL, "NULL buffer");
+    if (!aligned(src, 16)) return fail(COSET_EINVAL, "src must be 16-byte aligned");
+    if (coset::probe_read_loads(bytes, grid, threads) < 0)
+        return fail(COSET_EINVAL, "more than 32 loads per thread: use a larger grid");
+    return check_hip(coset::launch_probe_read(src, bytes, grid, threads, out, (hipStream_t)stream), "probe launch");
+}
+
+int coset_probe_c2_stream(const float* x, int64_t n_blocks, uint32_t* packed, float* out, int staged, void* stream)
+{
+    if (n_blocks < 1) return fail(COSET_EINVAL, "n_blocks must be positive");
+    if (!x || !packed || !out) return fail(COSET_EINVAL, "NULL buffer");
+    if (!aligned(x, 16) || !aligned(out, 16) || !aligned(packed, 4))
+        return fail(COSET_EINVAL, "x and out must be 16-byte aligned, packed 4-byte aligned");
+    return check_hip(coset::launch_c2_stream_probe(x, n_blocks, packed, out, staged, (hipStream_t)stream),
+                     "probe launch");
 }
 
 }  // extern "C"

@@ -22,6 +22,7 @@
 
 #include "codec_kernels.hpp"
 #include "counters.hpp"
+#include "probes.hpp"
 #include "tables.hpp"
 
 namespace coset {
@@ -547,7 +548,12 @@ __device__ __forceinline__ uint32_t encode_level_word(const float xl[8], bool in
     return pack_word<Q>(b, Q);
 }
 
-template <int Q, int M, int MODE, bool SCALED, bool CODES, bool PK>
+// PROBE (measurement, the round trip only): 0 is the codec; 1 keeps the
+// launch, table staging, tile schedule, loads and stores but writes each
+// block's input back out and a word folded from its bits, with no lattice
+// arithmetic -- the streaming ceiling of this kernel's access pattern; 2 is
+// 1 without the table staging.
+template <int Q, int M, int MODE, bool SCALED, bool CODES, bool PK, int PROBE = 0>
 __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, const uint16_t* __restrict__ g_map,
                                                               const uint64_t* __restrict__ g_tab, int n_coarse,
                                                               int swar_bias, TileCounters tc)
@@ -566,7 +572,8 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
     // (an LDS-only barrier: the loads stay in flight), 2.5 us sooner per
     // launch at 2^24 blocks; the round trip stages them first (measured
     // faster that way on the same box).
-    if constexpr (MODE == MODE_ROUNDTRIP) {
+    static_assert(PROBE == 0 || (MODE == MODE_ROUNDTRIP && M == 2 && PK && !CODES && !SCALED), "probe: C2's outputs");
+    if constexpr (MODE == MODE_ROUNDTRIP && PROBE != 2) {
         stage();
         __syncthreads();
     }
@@ -603,6 +610,15 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
         }
     };
     auto body = [&](int64_t i, const In& in) {
+        if constexpr (PROBE != 0) {
+            const uint32_t f = __float_as_uint(in.u.x) ^ __float_as_uint(in.u.y) ^ __float_as_uint(in.u.z) ^
+                               __float_as_uint(in.u.w) ^ __float_as_uint(in.v.x) ^ __float_as_uint(in.v.y) ^
+                               __float_as_uint(in.v.z) ^ __float_as_uint(in.v.w);
+            *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(a.packed) + (size_t)i * 2) = f;
+            const float o[8] = {in.u.x, in.u.y, in.u.z, in.u.w, in.v.x, in.v.y, in.v.z, in.v.w};
+            store_out_wave(static_cast<float*>(a.out), n, i, o, s_stage[threadIdx.x >> 6]);
+            return;
+        }
         float xl[8] = {in.u.x, in.u.y, in.u.z, in.u.w, in.v.x, in.v.y, in.v.z, in.v.w};
         uint64_t pack = MODE == MODE_DECODE ? in.w : 0;
         if (MODE != MODE_DECODE && SCALED) {
@@ -890,6 +906,33 @@ hipError_t launch_q(const CodecArgs& a, const DecodeTables* t, hipStream_t s)
 }
 
 }  // namespace
+
+hipError_t launch_c2_stream_probe(const float* x, int64_t n, uint32_t* packed, float* out, int staged, hipStream_t s)
+{
+    CodecArgs a{};
+    a.x = x;
+    a.x_dtype = DT_F32;
+    a.n = n;
+    a.q = 4;
+    a.M = 2;
+    a.packed = packed;
+    a.out = out;
+    a.out_dtype = DT_F32;
+    const DecodeTables* t = nullptr;
+    hipError_t e = get_decode_tables(4, 0, &t);
+    if (e != hipSuccess) return e;
+    const int grid = (int)std::min<int64_t>((n + kLutThreads - 1) / kLutThreads, (int64_t)cu_count());
+    const TileCounters tiles = g_codec_dynamic ? take_counters(s) : TileCounters{nullptr, nullptr, -1};
+    if (staged)
+        hipLaunchKernelGGL((hnlq_plain_kernel<4, 2, MODE_ROUNDTRIP, false, false, true, 1>), dim3(grid),
+                           dim3(kLutThreads), 0, s, a, t->cid_map, t->swar, t->n_coarse, t->swar_bias[2], tiles);
+    else
+        hipLaunchKernelGGL((hnlq_plain_kernel<4, 2, MODE_ROUNDTRIP, false, false, true, 2>), dim3(grid),
+                           dim3(kLutThreads), 0, s, a, t->cid_map, t->swar, t->n_coarse, t->swar_bias[2], tiles);
+    e = hipGetLastError();
+    if (e != hipSuccess) return_counters(tiles);
+    return e;
+}
 
 bool lut_path_supported(const CodecArgs& a, int mode)
 {

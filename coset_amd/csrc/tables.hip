@@ -74,7 +74,7 @@ uint64_t pack_bytes(const int v[8], int bias)
 
 // Byte tables of the SWAR decode and the levels they can combine.
 void build_swar(int q, uint32_t n, const std::vector<uint16_t>& map, const std::vector<uint64_t>& coarse,
-                std::vector<uint64_t>& swar, int* max_m, int bias[5])
+                std::vector<uint64_t>& swar, int* max_m, int bias[5], int r2_min[8], int r2_max[8])
 {
     int hi[256][8], lo[256][8];
     std::vector<std::array<int, 8>> cc(coarse.size());
@@ -99,10 +99,19 @@ void build_swar(int q, uint32_t n, const std::vector<uint16_t>& map, const std::
             max_c = std::max(max_c, cc[c][j]);
         }
     int r_max = -1 << 20;  // largest coordinate of 2r over all words
+    for (int j = 0; j < 8; ++j) {
+        r2_min[j] = 1 << 20;
+        r2_max[j] = -(1 << 20);
+    }
     for (uint32_t i = 0; i < n; ++i) {
         int u[8];
         two_gb(i, q, u);
-        for (int j = 0; j < 8; ++j) r_max = std::max(r_max, u[j] + cc[map[i]][j]);
+        for (int j = 0; j < 8; ++j) {
+            const int v = u[j] + cc[map[i]][j];
+            r_max = std::max(r_max, v);
+            r2_min[j] = std::min(r2_min[j], v);
+            r2_max[j] = std::max(r2_max[j], v);
+        }
     }
     const int b_hi = -min_hi, b_lo = -min_lo, b_c = -min_c, b_l = b_hi + b_lo + b_c;
     swar.resize(512 + coarse.size());
@@ -211,7 +220,7 @@ hipError_t build(int device, int q, int legacy, DecodeTables* out)
             coarse[c] = packed;
         }
     }
-    build_swar(q, n, map, coarse, swar, &out->swar_max_m, out->swar_bias);
+    build_swar(q, n, map, coarse, swar, &out->swar_max_m, out->swar_bias, out->r2_min, out->r2_max);
     if (!build_pairs(q, n, map, coarse, pair_map, pair_vals, out->pair_count)) {
         e = hipErrorInvalidValue;
         goto done;

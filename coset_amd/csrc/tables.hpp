@@ -36,7 +36,30 @@ struct DecodeTables {
     const uint32_t* pair_map;   // [n_codes]
     const float2* pair_vals;    // [4 * kPairSlots]
     int pair_count[4];
+    // smallest and largest coordinate j of 2r over all words
+    int r2_min[8], r2_max[8];
 };
+
+// Field offset of the 6-byte decoded weight format (vlut.hpp) for M levels of
+// these tables: every coordinate of 2 x_hat = sum_m q^m 2r_m stored as
+// floor(2 x_hat / 2) + off (6 bits; 5 bits for coordinate 7) with the common
+// parity in one bit.  -1 when the range does not fit.
+inline int decoded6_offset(const DecodeTables& t, int M)
+{
+    long lo[8], hi[8], qm = 1;
+    for (int j = 0; j < 8; ++j) lo[j] = hi[j] = 0;
+    for (int m = 0; m < M; ++m, qm *= t.q)
+        for (int j = 0; j < 8; ++j) {
+            lo[j] += qm * t.r2_min[j];
+            hi[j] += qm * t.r2_max[j];
+        }
+    auto fl2 = [](long v) { return v >= 0 ? v / 2 : -((-v + 1) / 2); };  // floor(v / 2)
+    long off = 0;
+    for (int j = 0; j < 8; ++j) off = off > -fl2(lo[j]) ? off : -fl2(lo[j]);
+    for (int j = 0; j < 8; ++j)
+        if (fl2(hi[j]) + off > (j < 7 ? 63 : 31)) return -1;
+    return (int)off;
+}
 
 // Tables of the core (legacy = 0) or legacy residual rule for q in {2, 4} on
 // the current device; built on first use (blocking), then cached.

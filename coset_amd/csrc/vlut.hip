@@ -992,13 +992,15 @@ __global__ void __launch_bounds__(256) vlut_prepare_decoded_kernel(const uint16_
                                                                   const uint16_t* map, const uint64_t* coarse,
                                                                   uint32_t mask, uint32_t* out)
 {
+    // pair e: [row tile][k-quad pair][lane][k-quad % 2] (vlut.hpp)
     const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (e >= n_pairs) return;
-    const int lane = (int)(e & 63);
-    const int64_t tile = e >> 6;
-    const int64_t kq = (kb_total + 3) / 4;
-    const int64_t row = (tile / kq) * 16 + (lane & 15);
-    const int64_t kb = (tile % kq) * 4 + (lane >> 4);
+    const int half = (int)(e & 1);
+    const int lane = (int)((e >> 1) & 63);
+    const int64_t tile = e >> 7;
+    const int64_t kq2 = ((kb_total + 3) / 4 + 1) / 2;
+    const int64_t row = (tile / kq2) * 16 + (lane & 15);
+    const int64_t kb = ((tile % kq2) * 2 + half) * 4 + (lane >> 4);
     int acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     if (row < rows && kb < kb_total) {
         int qm = 1;
@@ -1020,6 +1022,60 @@ __global__ void __launch_bounds__(256) vlut_prepare_decoded_kernel(const uint16_
     out[2 * e + 1] = hi;
 }
 
+// VLUT_DECODED6 (vlut.hpp): one thread per (row tile, chunk, lane) writes
+// the lane's 8 pairs as 12 words.
+template <int Q>
+__global__ void __launch_bounds__(256) vlut_prepare_decoded6_kernel(const uint16_t* words, int64_t rows,
+                                                                   int64_t kb_total, int M, int64_t n_lanes,
+                                                                   const uint16_t* map, const uint64_t* coarse,
+                                                                   uint32_t mask, int off, uint32_t* out)
+{
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n_lanes) return;
+    const int lane = (int)(e & 63);
+    const int64_t chunks = ((kb_total + 3) / 4 + kD6Steps - 1) / kD6Steps;
+    const int64_t rt = (e >> 6) / chunks, ch = (e >> 6) % chunks;
+    const int64_t row = rt * 16 + (lane & 15);
+    uint32_t w[kD6Words];
+#pragma unroll
+    for (int i = 0; i < kD6Words; ++i) w[i] = 0u;
+    for (int st = 0; st < kD6Steps; ++st) {
+        const int64_t kb = (ch * kD6Steps + st) * 4 + (lane >> 4);
+        int acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (row < rows && kb < kb_total) {
+            int qm = 1;
+            for (int m = 0; m < M; ++m) {
+                int r2[8];
+                two_r_lut<Q>(words[(row * kb_total + kb) * M + m] & mask, map, coarse, r2);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[j] += qm * r2[j];
+                qm *= Q;
+            }
+        }
+        // fields f_j = floor(2 x_hat_j / 2) + off and the parity p (shared by
+        // the 8: x_hat is in E8), laid out as d6_bytes (vlut_mfma.hpp) reads them
+        uint32_t f[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) f[j] = (uint32_t)((acc[j] >> 1) + off);
+        const uint32_t v7 = f[7] | ((uint32_t)(acc[0] & 1) << 5);
+        const uint32_t top[6] = {f[6] & 3u, (f[6] >> 2) & 3u, (f[6] >> 4) & 3u, v7 & 3u, (v7 >> 2) & 3u, v7 >> 4};
+        uint64_t v = 0;
+#pragma unroll
+        for (int i = 0; i < 6; ++i) v |= (uint64_t)(f[i] | (top[i] << 6)) << (8 * i);
+        const int b0 = 48 * st;  // bit offset in the lane's 384 bits
+#pragma unroll
+        for (int i = 0; i < kD6Words; ++i) {
+            const int lo = 32 * i;
+            if (lo + 32 <= b0 || lo >= b0 + 48) continue;
+            w[i] |= lo >= b0 ? (uint32_t)(v >> (lo - b0)) : (uint32_t)(v << (b0 - lo));
+        }
+    }
+    uint4* dst = reinterpret_cast<uint4*>(out + e * kD6Words);
+    dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    dst[2] = make_uint4(w[8], w[9], w[10], w[11]);
+}
+
 hipError_t vlut_prepare(const uint16_t* words, int64_t rows, int64_t kb, int M, int q, int legacy, int fmt,
                         uint32_t* prepared, hipStream_t s)
 {
@@ -1028,6 +1084,19 @@ hipError_t vlut_prepare(const uint16_t* words, int64_t rows, int64_t kb, int M, 
     const DecodeTables* t = nullptr;
     hipError_t e = get_decode_tables(q, legacy, &t);
     if (e != hipSuccess) return e;
+    if (fmt == VLUT_DECODED6) {
+        const int off = decoded6_offset(*t, M);
+        if (off < 0 || (q != 2 && q != 4)) return hipErrorInvalidValue;  // fields would overflow
+        const int64_t lanes = n / kD6Words;
+        const dim3 grid((unsigned)((lanes + 255) / 256)), block(256);
+        if (q == 4)
+            hipLaunchKernelGGL(vlut_prepare_decoded6_kernel<4>, grid, block, 0, s, words, rows, kb, M, lanes,
+                               t->cid_map, t->coarse, t->n_codes - 1u, off, prepared);
+        else
+            hipLaunchKernelGGL(vlut_prepare_decoded6_kernel<2>, grid, block, 0, s, words, rows, kb, M, lanes,
+                               t->cid_map, t->coarse, t->n_codes - 1u, off, prepared);
+        return hipGetLastError();
+    }
     if (fmt == VLUT_DECODED) {
         if (M > t->swar_max_m || (q != 2 && q != 4)) return hipErrorInvalidValue;  // bytes would overflow
         const int64_t pairs = n / 2;
@@ -1153,6 +1222,12 @@ hipError_t vlut_matmul(VlutMatmulArgs p, const VlutPlan& plan, hipStream_t s)
     if (p.prepared == VLUT_DECODED && plan.kernel != VK_MFMA_ROWS && plan.kernel != VK_MFMA_WIDE &&
         plan.kernel != VK_MFMA_DEEP)
         return hipErrorInvalidValue;
+    if (p.prepared == VLUT_DECODED6) {
+        // the rows and deep kernels read the 6-byte format
+        const int off = decoded6_offset(*t, p.M);
+        if (off < 0 || (plan.kernel != VK_MFMA_ROWS && plan.kernel != VK_MFMA_DEEP)) return hipErrorInvalidValue;
+        p.d6_bias = 2 * off;
+    }
     if (p.prepared == VLUT_PAIRS && plan.kernel != VK_LDS) return hipErrorInvalidValue;
     if (plan.kernel == VK_MFMA_WIDE || plan.kernel == VK_MFMA_DEEP || plan.kernel == VK_LDS) {
         if (plan.kernel == VK_LDS) {

@@ -94,6 +94,35 @@ __device__ __forceinline__ uint4 bytes_to_operand(uint32_t x0, uint32_t x1, _Flo
     return make_uint4(hv[0], hv[1], hv[2], hv[3]);
 }
 
+// One pair of the 6-byte format (vlut.hpp) from its 48 bits (lo: bits 0-31,
+// hi: bits 32-47 in its low half; the upper half is ignored) as the bytes
+// 2 x_hat + 2 off (x0: coordinates 0-3, x1: 4-7).  Fields 0-5 are the low 6
+// bits of the six bytes; the bytes' top two bits carry field 6 (bytes 0-2)
+// and v7 = field 7 | parity << 5 (bytes 3-5), each gathered into 6
+// contiguous bits by one multiply (the three 2-bit pieces land 2 bits apart
+// and the cross terms fall elsewhere: no carries).  Then 2 f + p per byte
+// (at most 2 * 63 + 1).
+__device__ __forceinline__ void d6_bytes(uint32_t lo, uint32_t hi, uint32_t& x0, uint32_t& x1)
+{
+    const uint32_t f6 = __builtin_amdgcn_ubfe((lo & 0x00c0c0c0u) * 4161u, 18, 6);
+    const uint32_t y = __builtin_amdgcn_alignbit(hi, lo, 30);   // lo bits 30-31, then hi
+    const uint32_t v7 = __builtin_amdgcn_ubfe((y & 0x00030303u) * 4161u, 12, 6);
+    const uint32_t pm = (v7 >> 5) * 0x01010101u;
+    const uint32_t b1 = (hi & 0x3f3fu) | (f6 << 16) | ((v7 & 31u) << 24);
+    x0 = ((lo & 0x3f3f3f3fu) << 1) + pm;
+    x1 = (b1 << 1) + pm;
+}
+
+// Pair j (0..7) of a lane's 6-byte chunk w[12] (384 bits, pair j at bit 48 j).
+__device__ __forceinline__ void d6_pair(const uint32_t* w, int j, uint32_t& x0, uint32_t& x1)
+{
+    const int i = 3 * (j >> 1);
+    if (j & 1)
+        d6_bytes(__builtin_amdgcn_alignbit(w[i + 2], w[i + 1], 16), w[i + 2] >> 16, x0, x1);
+    else
+        d6_bytes(w[i], w[i + 1], x0, x1);
+}
+
 // 2 x_hat of one pair as 8 halves (fp16) or bf16 values, exact.
 template <int Q, int M, bool BF16>
 __device__ __forceinline__ uint4 decode_pair_swar(const uint64_t* s_tab, const uint32_t w[M], _Float16 f16_off,
@@ -136,6 +165,15 @@ __device__ __forceinline__ void split3(float a, uint16_t& h1, uint16_t& h2, uint
     h2 = (uint16_t)(__float_as_uint(r1) >> 16);
     const float r2 = __fsub_rn(r1, __uint_as_float((uint32_t)h2 << 16));
     h3 = (uint16_t)(__float_as_uint(r2) >> 16);
+}
+
+// The same with bias[o] already loaded (b; used where bias is non-null).
+__device__ __forceinline__ float vlut_epilogue_b(float y, float b, const float* bias, const float* lsq_alpha,
+                                                 int lsq_qmax)
+{
+    if (bias) y = __fadd_rn(y, b);
+    if (lsq_alpha) y = lsq_value(y, lsq_scale(lsq_alpha, lsq_qmax));
+    return y;
 }
 
 // Output epilogue: + bias[o], then the LSQ activation quantizer (fp32, the

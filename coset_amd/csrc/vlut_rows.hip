@@ -38,30 +38,44 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulAr
     static_assert(TB == 0 || (NTILE == 1 && TB <= 16), "staged activations: one 16-token tile");
     static_assert(!SPLIT || (TB > 0 && BF16), "the split staging writes bf16 token rows");
     static_assert(TB == 0 || 2 * CH == kRowsStageKq, "a staged wave range is two chunks");
-    __shared__ uint64_t s_tab[FMT == VLUT_DECODED ? 1 : kSwarSlots];
+    constexpr bool DEC = FMT == VLUT_DECODED || FMT == VLUT_DECODED6;  // no table reads
+    __shared__ uint64_t s_tab[DEC ? 1 : kSwarSlots];
     __shared__ float s_red[kRowsWaves][NTILE * 4][64];
     __shared__ __align__(16) unsigned char s_stage[TB == 0 ? 16 : kRowsWaves * TB * kRowsStageRow];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4;
     const int64_t kb_total = p.K / 8;
     const int64_t kq_total = (kb_total + 3) / 4;
-    const int64_t kq_wg = (kq_total + gridDim.y - 1) / gridDim.y;
+    // split and wave ranges start on an even k-quad (the 8-byte decoded format
+    // keeps a lane's two k-quads 2i, 2i + 1 together; every format aligns the
+    // same way, so they sum in the same order) or, for the 6-byte format, on
+    // a chunk of 8 k-quads
+    constexpr int64_t KA = FMT == VLUT_DECODED6 ? kD6Steps : 2;
+    const int64_t kq_wg = ((kq_total + gridDim.y - 1) / gridDim.y + KA - 1) / KA * KA;
     const int64_t kq_begin = blockIdx.y * kq_wg;
     const int64_t kq_end = min(kq_total, kq_begin + kq_wg);
-    const int64_t kq_wave = (kq_end - kq_begin + kRowsWaves - 1) / kRowsWaves;
+    const int64_t kq_wave = ((kq_end - kq_begin + kRowsWaves - 1) / kRowsWaves + KA - 1) / KA * KA;
     const int64_t w0 = kq_begin + wave * kq_wave;
     const int64_t w1 = min(kq_end, w0 + kq_wave);
     const int64_t r0 = (int64_t)blockIdx.x * 16;
     const int64_t row = r0 + (lane & 15);
     const int64_t t_base = (int64_t)blockIdx.z * 16 * NTILE;
     const uint16_t* act = reinterpret_cast<const uint16_t*>(p.act);
-    const int bias = FMT == VLUT_DECODED ? kVlutDecodedBias : p.swar_bias;
+    const int bias = FMT == VLUT_DECODED ? kVlutDecodedBias : FMT == VLUT_DECODED6 ? p.d6_bias : p.swar_bias;
     const _Float16 f16_off = (_Float16)(1024 + bias);
     const float f32_off = (float)bias;
     constexpr int WN = FMT == VLUT_DECODED ? 2 : M;  // uint32 per pair
+    constexpr int W6 = FMT == VLUT_DECODED6 ? CH * kD6Words / kD6Steps : 1;  // 6-byte format: uint32 per lane and chunk
+    static_assert(FMT != VLUT_DECODED6 || (CH * kD6Words) % kD6Steps == 0, "whole words per chunk");
+    // the epilogue's per-row scale and bias, loaded with the first loads: a
+    // thread's outputs all lie in row r0 + threadIdx.x % 16
+    const int64_t o_ep = min(r0 + (int64_t)(threadIdx.x & 15), p.rows - 1);
+    const float sc_ep = p.scale ? (p.scale_mode == 0 ? p.scale[o_ep] : 1.f / p.scale[o_ep]) : 1.f;
+    const float bias_ep = p.bias ? p.bias[o_ep] : 0.f;
 
     struct Chunk {
-        uint32_t w[CH][WN];
+        uint32_t w[FMT == VLUT_DECODED6 ? 1 : CH][WN];
+        uint32_t w6[W6];                   // 6-byte format: the lane's steps of the chunk
         uint4 a[TB == 0 ? CH : 1][NTILE];  // A operands (TB = 0), masked in run
     };
     // Every load is unconditional, with a clamped address where it lies
@@ -71,12 +85,48 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulAr
     // loads in flight.  (Weights of an out-of-range k-block meet zero
     // activations, and rows past the matrix are never written.)
     auto load = [&](int64_t c0, Chunk& ck) {
+        if constexpr (FMT == VLUT_DECODED6) {
+            // steps c0 .. c0 + CH - 1 of one chunk (c0 is a multiple of CH and the
+            // wave's range starts on a chunk); past the wave's range, chunk 0
+            const bool ok = c0 < w1;
+            const uint32_t* src = reinterpret_cast<const uint32_t*>(p.words) +
+                                  vlut_word_index(FMT, ok ? row : r0, ok ? 4 * c0 + g : g, 0, kb_total, M) +
+                                  (ok ? (c0 % kD6Steps) * kD6Words / kD6Steps : 0);
+            if constexpr (W6 == 12) {
+                const uint4 v0 = reinterpret_cast<const uint4*>(src)[0], v1 = reinterpret_cast<const uint4*>(src)[1],
+                            v2 = reinterpret_cast<const uint4*>(src)[2];
+                const uint32_t v[12] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w, v2.x, v2.y, v2.z, v2.w};
+#pragma unroll
+                for (int i = 0; i < 12; ++i) ck.w6[i] = v[i];
+            } else if constexpr (W6 == 6) {
+                const uint4 v0 = *reinterpret_cast<const uint4*>(src);  // 24-byte offsets: 8-byte aligned
+                const uint2 v1 = *reinterpret_cast<const uint2*>(src + 4);
+                ck.w6[0] = v0.x; ck.w6[1] = v0.y; ck.w6[2] = v0.z; ck.w6[3] = v0.w; ck.w6[4] = v1.x; ck.w6[5] = v1.y;
+            } else {
+#pragma unroll
+                for (int i = 0; i < W6; ++i) ck.w6[i] = src[i];
+            }
+        }
 #pragma unroll
         for (int st = 0; st < CH; ++st) {
             const int64_t kq = c0 + st;
             const int64_t kb = 4 * kq + g;
-            const bool ok = kq < w1 && kb < kb_total && (FMT == VLUT_TILED || FMT == VLUT_DECODED || row < p.rows);
-            load_pair<Q, M, WN>(p, FMT, ok ? row : r0, ok ? kb : 0, kb_total, ck.w[st]);
+            const bool ok = kq < w1 && kb < kb_total && (FMT == VLUT_TILED || DEC || row < p.rows);
+            if constexpr (FMT == VLUT_DECODED && CH % 2 == 0) {
+                // steps st, st + 1 (k-quads 2i, 2i + 1: c0 is even) in one 16-byte load;
+                // the second may lie past the range (padding or masked activations)
+                if (st % 2 == 0) {
+                    const uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint32_t*>(p.words) +
+                                                                    vlut_word_index(FMT, ok ? row : r0, ok ? kb : 0,
+                                                                                    0, kb_total, M));
+                    ck.w[st][0] = v.x;
+                    ck.w[st][1 % WN] = v.y;
+                    ck.w[st + 1][0] = v.z;
+                    ck.w[st + 1][1 % WN] = v.w;
+                }
+            } else if constexpr (FMT != VLUT_DECODED6) {
+                load_pair<Q, M, WN>(p, FMT, ok ? row : r0, ok ? kb : 0, kb_total, ck.w[st]);
+            }
             if constexpr (TB == 0) {
 #pragma unroll
                 for (int s = 0; s < NTILE; ++s) {
@@ -111,10 +161,20 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulAr
                 }
             }
             uint4 bw;
-            if constexpr (FMT == VLUT_DECODED)
+            if constexpr (FMT == VLUT_DECODED6) {
+                // step st of the loaded words: pair (c0 + st) % 8 of the chunk, i.e.
+                // pair st of the CH loaded (CH divides 8)
+                uint32_t x0, x1;
+                uint32_t w12[12];
+#pragma unroll
+                for (int i = 0; i < 12; ++i) w12[i] = i < W6 ? ck.w6[i] : 0u;
+                d6_pair(w12, st, x0, x1);
+                bw = bytes_to_operand<BF16>(x0, x1, f16_off, f32_off);
+            } else if constexpr (FMT == VLUT_DECODED) {
                 bw = bytes_to_operand<BF16>(ck.w[st][0], ck.w[st][1 % WN], f16_off, f32_off);
-            else
+            } else {
                 bw = decode_pair_swar<Q, M, BF16>(s_tab, ck.w[st], f16_off, f32_off);
+            }
 #pragma unroll
             for (int s = 0; s < NTILE; ++s) {
                 if (BF16)
@@ -164,7 +224,7 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulAr
                                (uint32_t)h[pl][4] | ((uint32_t)h[pl][5] << 16),
                                (uint32_t)h[pl][6] | ((uint32_t)h[pl][7] << 16));
         }
-        if constexpr (FMT != VLUT_DECODED) {
+        if constexpr (!DEC) {
             for (int i = threadIdx.x; i < 512 + p.n_coarse; i += blockDim.x) s_tab[i] = p.swar[i];
             __syncthreads();
         }
@@ -192,7 +252,7 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulAr
             *reinterpret_cast<uint4*>(&s_stage[(wave * TB + t) * kRowsStageRow + lane * 16]) =
                 make_uint4(av[t].x & m, av[t].y & m, av[t].z & m, av[t].w & m);
         }
-        if constexpr (FMT != VLUT_DECODED) {
+        if constexpr (!DEC) {
             for (int i = threadIdx.x; i < 512 + p.n_coarse; i += blockDim.x) s_tab[i] = p.swar[i];
             __syncthreads();
         }
@@ -204,7 +264,7 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulAr
         int64_t c0 = w0;
         load(c0, c_a);
         // the tables are staged while the first chunk's loads are in flight
-        if constexpr (FMT != VLUT_DECODED) {
+        if constexpr (!DEC) {
             for (int i = threadIdx.x; i < 512 + p.n_coarse; i += blockDim.x) s_tab[i] = p.swar[i];
             __syncthreads();
         }
@@ -232,7 +292,7 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulAr
         for (int e = threadIdx.x; e < nb * 16; e += blockDim.x) {
             const int64_t b = e >> 4, o = r0 + (e & 15);
             if (o >= p.rows) continue;
-            const float sc = p.scale ? (p.scale_mode == 0 ? p.scale[o] : 1.f / p.scale[o]) : 1.f;
+            const float sc = sc_ep;
             float y[3];
 #pragma unroll
             for (int pl = 0; pl < 3; ++pl) {
@@ -244,7 +304,7 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulAr
                 y[pl] = v * 0.5f * sc;
             }
             p.out[b * p.rows + o] =
-                vlut_epilogue(__fadd_rn(__fadd_rn(y[0], y[1]), y[2]), o, p.bias, p.lsq_alpha, p.lsq_qmax);
+                vlut_epilogue_b(__fadd_rn(__fadd_rn(y[0], y[1]), y[2]), bias_ep, p.bias, p.lsq_alpha, p.lsq_qmax);
         }
         return;
     }
@@ -257,8 +317,7 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulAr
         const int64_t o = r0 + (ln & 15);
         if (tok >= p.B || o >= p.rows) continue;
         if (gridDim.y == 1) {
-            float sc = p.scale ? (p.scale_mode == 0 ? p.scale[o] : 1.f / p.scale[o]) : 1.f;
-            p.out[tok * p.rows + o] = vlut_epilogue(v * 0.5f * sc, o, p.bias, p.lsq_alpha, p.lsq_qmax);
+            p.out[tok * p.rows + o] = vlut_epilogue_b(v * 0.5f * sc_ep, bias_ep, p.bias, p.lsq_alpha, p.lsq_qmax);
         } else {
             p.partial[(tok * p.rows + o) * gridDim.y + blockIdx.y] = v;
         }
@@ -278,6 +337,7 @@ void launch_rows_fmt(const VlutMatmulArgs& p, int splits, hipStream_t s)
     case VLUT_RAW: COSET_ROWS(VLUT_RAW); break;
     case VLUT_PREPARED: COSET_ROWS(VLUT_PREPARED); break;
     case VLUT_DECODED: COSET_ROWS(VLUT_DECODED); break;
+    case VLUT_DECODED6: COSET_ROWS(VLUT_DECODED6); break;
     default: COSET_ROWS(VLUT_TILED); break;
     }
 #undef COSET_ROWS

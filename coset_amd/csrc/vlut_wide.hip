@@ -177,6 +177,8 @@ template <int Q, int M, bool BF16, int FMT>
 __global__ void __launch_bounds__(kDeepNW * 64) vlut_deep_kernel(VlutMatmulArgs p)
 {
     constexpr int WN = FMT == VLUT_DECODED ? 2 : M;  // uint32 per pair
+    constexpr bool D6 = FMT == VLUT_DECODED6;
+    constexpr bool DEC = FMT == VLUT_DECODED || D6;   // no table reads
     constexpr int T = kDeepNW * 64;
     constexpr int CH = 4 * kDeepKqWg;                // 16-byte activation chunks per token row
     constexpr int AL = kDeepTokens * CH / T;         // activation loads per thread
@@ -185,19 +187,25 @@ __global__ void __launch_bounds__(kDeepNW * 64) vlut_deep_kernel(VlutMatmulArgs 
                   "the cross-wave sum fits in the activation buffer");
     static_assert(kDeepStride * 2 % 16 == 0, "16-byte aligned token rows");
     __shared__ __align__(16) uint16_t s_act[kDeepTokens * kDeepStride];
-    __shared__ uint64_t s_tab[FMT == VLUT_DECODED ? 1 : kSwarSlots];
+    __shared__ uint64_t s_tab[DEC ? 1 : kSwarSlots];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4;
     const int64_t kb_total = p.K / 8;
     const int64_t kq_total = (kb_total + 3) / 4;
-    const int64_t kq_wg = (kq_total + gridDim.y - 1) / gridDim.y;   // <= kDeepKqWg (the plan's splits)
+    // <= kDeepKqWg (the plan's splits); the 6-byte format's slices start on a
+    // chunk of 8 k-quads and every wave takes half a chunk (4 k-quads); the
+    // others' slices are whole multiples of 16 k-quads, so every wave's range
+    // starts on an even k-quad (the 8-byte decoded format's 16-byte loads)
+    constexpr int64_t KA = D6 ? kD6Steps : 2 * kDeepNW;
+    const int64_t kq_wg = ((kq_total + gridDim.y - 1) / gridDim.y + KA - 1) / KA * KA;
     const int64_t kq_begin = blockIdx.y * kq_wg;
     const int64_t kq_end = min(kq_total, kq_begin + kq_wg);
-    const int kqw = (int)((kq_wg + kDeepNW - 1) / kDeepNW);         // k-quads per wave, <= 4
+    const int kqw = D6 ? kDeepKqWave : (int)((kq_wg + kDeepNW - 1) / kDeepNW);   // k-quads per wave, <= 4
+    static_assert(!D6 || 2 * kDeepKqWave == kD6Steps, "a wave's k-quads are half a chunk");
     const int64_t rb = (int64_t)blockIdx.x * kDeepRows;
     const int64_t t_base = (int64_t)blockIdx.z * kDeepTokens;
     const uint16_t* act = reinterpret_cast<const uint16_t*>(p.act);
-    const int bias = FMT == VLUT_DECODED ? kVlutDecodedBias : p.swar_bias;
+    const int bias = FMT == VLUT_DECODED ? kVlutDecodedBias : D6 ? p.d6_bias : p.swar_bias;
     const _Float16 f16_off = (_Float16)(1024 + bias);
     const float f32_off = (float)bias;
 
@@ -219,20 +227,52 @@ __global__ void __launch_bounds__(kDeepNW * 64) vlut_deep_kernel(VlutMatmulArgs 
         __builtin_amdgcn_global_load_lds(src, &s_act[(c0 / CH) * kDeepStride + (c0 % CH) * 8], 16, 0, 0);
     }
     // this wave's weight pairs: row tiles rt, k-quads kq_begin + wave * kqw + j
-    uint32_t w[kDeepRT][kDeepKqWave][WN];
+    uint32_t w[D6 ? 1 : kDeepRT][D6 ? 1 : kDeepKqWave][WN];
+    uint32_t w6[D6 ? kDeepRT : 1][kD6Words];   // 6-byte format: half a chunk per row tile (words 0-5)
 #pragma unroll
     for (int rt = 0; rt < kDeepRT; ++rt) {
         const int64_t r0 = rb + 16 * rt, row = r0 + (lane & 15);
-        const bool rows_ok = (FMT == VLUT_TILED || FMT == VLUT_DECODED) ? r0 < p.rows : row < p.rows;
+        const bool rows_ok = (FMT == VLUT_TILED || DEC) ? r0 < p.rows : row < p.rows;
+        if constexpr (D6) {
+            // k-quads kq0 .. kq0 + 3: the first or second half of a chunk (outside
+            // the matrix or the slice: the first half of row tile 0's chunk 0)
+            const int64_t kq0 = kq_begin + (int64_t)wave * kDeepKqWave;
+            const bool ok = rows_ok && kq0 < kq_end;
+            const uint32_t* src = reinterpret_cast<const uint32_t*>(p.words) +
+                                  vlut_word_index(FMT, ok ? row : (lane & 15), ok ? 4 * kq0 + g : g, 0, kb_total, M) +
+                                  (ok ? (kq0 % kD6Steps) * kD6Words / kD6Steps : 0);
+            const uint4 v0 = *reinterpret_cast<const uint4*>(src);   // 24-byte halves: 8-byte aligned
+            const uint2 v1 = *reinterpret_cast<const uint2*>(src + 4);
+            w6[rt][0] = v0.x; w6[rt][1] = v0.y; w6[rt][2] = v0.z; w6[rt][3] = v0.w; w6[rt][4] = v1.x; w6[rt][5] = v1.y;
 #pragma unroll
-        for (int j = 0; j < kDeepKqWave; ++j) {
-            const int64_t kq = kq_begin + (int64_t)wave * kqw + j;
-            const int64_t kb = 4 * kq + g;
-            const bool ok = rows_ok && j < kqw && kq < kq_end && kb < kb_total;
-            load_pair<Q, M, WN>(p, FMT, ok ? row : 0, ok ? kb : 0, kb_total, w[rt][j]);
+            for (int i = 6; i < kD6Words; ++i) w6[rt][i] = 0u;
+        } else if constexpr (FMT == VLUT_DECODED) {
+            // k-quads j, j + 1 of the wave (kq_begin and kqw are even) in one
+            // 16-byte load; past the range, pair (0, 0) under zero activations
+#pragma unroll
+            for (int j = 0; j < kDeepKqWave; j += 2) {
+                const int64_t kq = kq_begin + (int64_t)wave * kqw + j;
+                const int64_t kb = 4 * kq + g;
+                const bool ok = rows_ok && j < kqw && kq < kq_end && kb < kb_total;
+                const uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint32_t*>(p.words) +
+                                                                vlut_word_index(FMT, ok ? row : 0, ok ? kb : 0, 0,
+                                                                                kb_total, M));
+                w[rt][j][0] = v.x;
+                w[rt][j][1 % WN] = v.y;
+                w[rt][j + 1][0] = v.z;
+                w[rt][j + 1][1 % WN] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < kDeepKqWave; ++j) {
+                const int64_t kq = kq_begin + (int64_t)wave * kqw + j;
+                const int64_t kb = 4 * kq + g;
+                const bool ok = rows_ok && j < kqw && kq < kq_end && kb < kb_total;
+                load_pair<Q, M, WN>(p, FMT, ok ? row : 0, ok ? kb : 0, kb_total, w[rt][j]);
+            }
         }
     }
-    if (FMT != VLUT_DECODED) {
+    if (!DEC) {
         for (int i = threadIdx.x; i < 512 + p.n_coarse; i += T) s_tab[i] = p.swar[i];
     }
     // the LDS writes of global_load_lds complete with the loads (vmcnt)
@@ -255,10 +295,15 @@ __global__ void __launch_bounds__(kDeepNW * 64) vlut_deep_kernel(VlutMatmulArgs 
 #pragma unroll
         for (int rt = 0; rt < kDeepRT; ++rt) {
             uint4 bw;
-            if constexpr (FMT == VLUT_DECODED)
+            if constexpr (D6) {
+                uint32_t x0, x1;
+                d6_pair(w6[rt], j, x0, x1);
+                bw = bytes_to_operand<BF16>(x0, x1, f16_off, f32_off);
+            } else if constexpr (FMT == VLUT_DECODED) {
                 bw = bytes_to_operand<BF16>(w[rt][j][0], w[rt][j][1 % WN], f16_off, f32_off);
-            else
+            } else {
                 bw = decode_pair_swar<Q, M, BF16>(s_tab, w[rt][j], f16_off, f32_off);
+            }
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
                 if (BF16)
@@ -370,6 +415,7 @@ void launch_deep_fmt(const VlutMatmulArgs& p, int splits, hipStream_t s)
     case VLUT_RAW: COSET_DEEP(VLUT_RAW); break;
     case VLUT_PREPARED: COSET_DEEP(VLUT_PREPARED); break;
     case VLUT_DECODED: COSET_DEEP(VLUT_DECODED); break;
+    case VLUT_DECODED6: COSET_DEEP(VLUT_DECODED6); break;
     default: COSET_DEEP(VLUT_TILED); break;
     }
 #undef COSET_DEEP

@@ -188,7 +188,7 @@ def vlut_dot(words: torch.Tensor, vlut: torch.Tensor, q: int) -> torch.Tensor:
 
 
 _METHODS = {"auto": 0, "lds": 1, "mfma": 2}
-_LAYOUTS = {"rowmajor": 1, "tiled": 2, "decoded": 3, "pairs": 4}
+_LAYOUTS = {"rowmajor": 1, "tiled": 2, "decoded": 3, "pairs": 4, "decoded6": 5}
 
 
 @dataclass
@@ -196,9 +196,11 @@ class PreparedWords:
     """Level words converted once for vlut_matmul (coset_vlut_prepare):
     uint32 cid << 16 | idx values, row-major or tiled in matrix-core fragment
     order (16 rows x 4 k-blocks per 64-entry tile), ("decoded") the
-    pairs' 2 x_hat as biased bytes in the tiled order, or ("pairs") each
-    level word's four coordinate-pair ids, [rows / 64][kb][M][64 rows], which
-    the LDS-table method reads without a map lookup."""
+    pairs' 2 x_hat as biased bytes in the tiled order, ("decoded6") the same
+    decode in 6 bytes per pair (one parity bit and eight 6-bit fields,
+    chunks of 8 k-quads per lane), or ("pairs") each level word's four
+    coordinate-pair ids, [rows / 64][kb][M][64 rows], which the LDS-table
+    method reads without a map lookup."""
     data: torch.Tensor
     rows: int
     kb: int
@@ -216,7 +218,8 @@ def vlut_prepare(words: torch.Tensor, q: int = 4, legacy: bool = False, layout: 
     """uint16 level words [rows, K/8, M] -> PreparedWords, the weight format
     vlut_matmul reads without the coarse-id gather ("rowmajor", "tiled") or
     without any table lookup ("decoded": 8 bytes per pair, q = 4 with M <= 2
-    or q = 2 with M <= 4, fp16/bf16 activations), or as the coordinate-pair
+    or q = 2 with M <= 4; "decoded6": 6 bytes per pair where the decode's
+    range fits, e.g. q = 4 with M <= 2; both on the matrix cores), or as the coordinate-pair
     ids the LDS-table method looks up ("pairs": any activation dtype,
     method "lds" or "auto").  Done once per weight; ``legacy`` fixes the
     residual rule the matmul will use."""

@@ -243,9 +243,21 @@ int coset_vlut_lookup_dot(const void* words, int64_t n_blocks, int q, int M, con
  *      values per pair), the entries the LDS-table method looks up, laid out
  *      [ceil(rows / 64)][kb][M][64 rows] (padding rows hold the ids of word
  *      0, which decodes to 0); that method only (method 0 selects it).
+ *   5  decoded6: the decode of format 3 in 6 bytes per pair (12.6 MB at
+ *      4096 x 4096 against 16.8 MB).  2 x_hat lies in E8, so its coordinates
+ *      share one parity p: coordinate j is stored as the 6-bit field
+ *      f_j = floor(2 x_hat_j / 2) + off (f_7 < 32), off = 18 for q = 4, M = 2
+ *      (core or legacy rule; other q, M where the ranges fit, else the
+ *      prepare call returns COSET_EUNSUPPORTED).  Byte i (0-5) of a pair
+ *      holds f_i in bits 0-5; bits 6-7 of bytes 0-2 hold f_6 (2 bits each,
+ *      low first) and those of bytes 3-5 hold f_7 | p << 5.  Layout: [ceil(rows / 16)][ceil(kb / 32)][64
+ *      lanes][8 pairs x 6 bytes]: lane row % 16 + 16 (kb % 4), pair
+ *      (kb / 4) % 8, so a lane reads a chunk of 8 k-quads as three 16-byte
+ *      loads; padding holds x_hat = 0.  Matrix-core method, rows (B <= 32)
+ *      and deep (B > 32) kernels.
  * coset_vlut_prepared_words gives the uint32 count of a format; prepare
  * (once per weight) converts format-0 words [rows, kb, M] into format 1, 2,
- * 3 or 4 for the core rule (legacy = 0) or the legacy one. */
+ * 3, 4 or 5 for the core rule (legacy = 0) or the legacy one. */
 int64_t coset_vlut_prepared_words(int64_t rows, int64_t kb, int M, int word_format);
 int coset_vlut_prepare(const void* words, int64_t rows, int64_t kb, int M, int q, int legacy, int word_format,
                        uint32_t* prepared, void* stream);
@@ -287,6 +299,23 @@ int64_t coset_vlut_noalloc_scratch_floats(void);
 int coset_vlut_matmul_noalloc(const void* words, int word_format, const float* scale, int scale_mode,
                               const void* act, int act_dtype, int64_t B, int64_t rows, int64_t K, int q, int M,
                               int legacy, int method, float* out, void* stream);
+
+/* Measurement probes (no counterpart in the reference: the floors bench.py
+ * sets the kernels above against).
+ *   coset_probe_empty: a launch of grid x threads with lds_bytes of LDS that
+ *     does no work (out is never written) -- the cost of one launch.
+ *   coset_probe_read: reads `bytes` (a multiple of 16) from src into
+ *     registers at that launch shape, every load issued before any is used,
+ *     and writes one uint32 per workgroup to out[grid] -- the floor of a
+ *     kernel that reads a weight format of that size.
+ *   coset_probe_c2_stream: the C2 round trip's kernel (coset_e8_hnlq_roundtrip
+ *     at q = 4, M = 2, fp32, no scale) with its launch, tile schedule, loads
+ *     and stores but no lattice arithmetic: out = x, packed[i] = the XOR of
+ *     block i's eight words (staged != 0: with its decode-table staging) --
+ *     the streaming ceiling of that access pattern. */
+int coset_probe_empty(int grid, int threads, int lds_bytes, uint32_t* out, void* stream);
+int coset_probe_read(const void* src, int64_t bytes, int grid, int threads, uint32_t* out, void* stream);
+int coset_probe_c2_stream(const float* x, int64_t n_blocks, uint32_t* packed, float* out, int staged, void* stream);
 
 /* D4 lattice operator over n_blocks fp32 [n, 4] blocks (coset/core/d4/lattice.py:62-146,
  * coset/core/base.py:134-176): COSET_OP_G_X, COSET_OP_PROJECT (closest point,
