@@ -63,6 +63,8 @@ SIGNATURES = {
     "coset_lsq_bwd": [_vp, _vp, _int, _i64, _vp, _int, _vp, _vp, _vp, _i64, _vp],
     "coset_qat_stats_update": [_vp, _i64, _i64, ctypes.c_double, _vp, _vp, _vp],
     "coset_colsum": [_vp, _int, _i64, _i64, _vp, _vp, _i64, _vp],
+    "coset_gemm_tn_supported": [_i64, _i64, _i64],
+    "coset_gemm_tn": [_vp, _i64, _vp, _i64, _vp, _i64, _int, _i64, _i64, _i64, _vp, _i64, _vp],
     "coset_vlut_matmul_noalloc": [_vp, _int, _vp, _int, _vp, _int, _i64, _i64, _i64, _int, _int, _int, _int, _vp,
                                   _vp],
     "coset_probe_empty": [_int, _int, _int, _vp, _vp],
@@ -78,6 +80,7 @@ SIZE_QUERIES = {
     "coset_vlut_prepared_words": [_i64, _i64, _int, _int],
     "coset_lsq_workspace_floats": [_i64],
     "coset_colsum_workspace_floats": [_i64, _i64],
+    "coset_gemm_tn_workspace_floats": [_i64, _i64, _i64],
     "coset_vlut_noalloc_scratch_floats": [],
 }
 

@@ -36,6 +36,14 @@ HIPCC_FLAGS = [
 ]
 
 
+# per-source extra flags: the TN GEMM keeps its staging registers in
+# registers (at one wave per SIMD the compiler would otherwise move them to
+# LDS, beside the kernel's own 96 KiB of stage buffers)
+EXTRA_FLAGS = {
+    "gemm_tn.hip": ["-mllvm", "-disable-promote-alloca-to-lds"],
+}
+
+
 def hipcc() -> str:
     for c in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if c and os.path.exists(c):
@@ -65,7 +73,8 @@ def build(verbose: bool = False, jobs: int = 0) -> str:
     objs = [os.path.join(OBJ_DIR, os.path.basename(s)[:-4] + ".o") for s in srcs]
     jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 4)), 16)
     with ThreadPoolExecutor(jobs) as ex:
-        rcs = list(ex.map(lambda so: _run([cc, *HIPCC_FLAGS, *inc, "-c", "-o", so[1], so[0]], verbose),
+        rcs = list(ex.map(lambda so: _run([cc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(os.path.basename(so[0]), []), *inc,
+                                           "-c", "-o", so[1], so[0]], verbose),
                           zip(srcs, objs)))
     bad = [s for s, rc in zip(srcs, rcs) if rc != 0]
     if bad:

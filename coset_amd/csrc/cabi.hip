@@ -11,6 +11,7 @@
 
 #include "../../include/coset_amd.h"
 #include "codec_kernels.hpp"
+#include "gemm.hpp"
 #include "legacy.hpp"
 #include "probes.hpp"
 #include "tables.hpp"
@@ -456,6 +457,42 @@ int coset_colsum(const void* g, int dtype, int64_t rows, int64_t cols, float* ou
     if ((rows + 63) / 64 > 65535) return fail(COSET_EINVAL, "too many rows");
     return check_hip(coset::launch_colsum(g, dtype, rows, cols, out, workspace, (hipStream_t)stream),
                      "column sum launch");
+}
+
+int coset_gemm_tn_supported(int64_t M, int64_t N, int64_t K)
+{
+    return coset::gemm_tn_plan(M, N, K).tile > 0 ? 1 : 0;
+}
+
+int64_t coset_gemm_tn_workspace_floats(int64_t M, int64_t N, int64_t K)
+{
+    return coset::gemm_tn_workspace_floats(coset::gemm_tn_plan(M, N, K), M, N);
+}
+
+int coset_gemm_tn(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int out_dtype,
+                  int64_t M, int64_t N, int64_t K, float* workspace, int64_t workspace_floats, void* stream)
+{
+    if (M < 0 || N < 0 || K < 0) return fail(COSET_EINVAL, "M, N, K must be >= 0");
+    if (out_dtype != COSET_F32 && out_dtype != COSET_BF16)
+        return fail(COSET_EUNSUPPORTED, "output dtype %d not supported (fp32, bf16)", out_dtype);
+    const coset::GemmTnPlan plan = coset::gemm_tn_plan(M, N, K);
+    if (plan.tile == 0)
+        return fail(COSET_EUNSUPPORTED,
+                    "shape M=%lld N=%lld K=%lld not taken: M, N multiples of 64, at most 256 tiles of 64 x 64, "
+                    "K = 256 s m (s a power of two, m in 4, 8, 16, 32)",
+                    (long long)M, (long long)N, (long long)K);
+    if (!A || !B || !C) return fail(COSET_EINVAL, "NULL buffer");
+    if (!aligned(A, 16) || !aligned(B, 16) || !aligned(C, 16)) return fail(COSET_EINVAL, "buffers must be 16-byte aligned");
+    if (lda < M || ldb < N || ldc < N || lda % 8 || ldb % 8 || ldc % 8)
+        return fail(COSET_EINVAL, "leading dimensions must cover the rows and be multiples of 8");
+    const int64_t need = coset::gemm_tn_workspace_floats(plan, M, N);
+    if (need > 0 && (!workspace || workspace_floats < need))
+        return fail(COSET_EINVAL, "workspace too small: %lld floats needed", (long long)need);
+    if (need > 0 && !aligned(workspace, 16)) return fail(COSET_EINVAL, "workspace must be 16-byte aligned");
+    return check_hip(coset::gemm_tn_bf16(static_cast<const uint16_t*>(A), lda, static_cast<const uint16_t*>(B), ldb, C,
+                                         ldc, out_dtype, M, N, K, plan, need > 0 ? workspace : nullptr,
+                                         (hipStream_t)stream),
+                     "gemm_tn launch");
 }
 
 int coset_qat_stats_update(const float* W, int64_t tiles, int64_t tile_size, double momentum, float* sigma_ema,

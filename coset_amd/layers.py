@@ -327,6 +327,52 @@ def colsum(g2: torch.Tensor) -> torch.Tensor:
     return out
 
 
+# 1: the weight gradient gy^T x runs on coset_gemm_tn where the shape and
+# dtypes allow it (bf16, M and N multiples of 64, tokens a multiple of 128),
+# 0: always on torch.mm (hipBLASLt)
+_GEMM_TN = [1]
+
+
+def set_gemm_tn(enabled: bool) -> None:
+    """Route the layer's weight-gradient product to coset_gemm_tn (default)
+    or to torch.mm."""
+    _GEMM_TN[0] = 1 if enabled else 0
+
+
+def gemm_tn(a: torch.Tensor, b: torch.Tensor, out_dtype: Optional[torch.dtype] = None) -> Optional[torch.Tensor]:
+    """a^T b for bf16 a [K, M] and b [K, N] on the GPU (coset_gemm_tn: fp32
+    accumulation in a fixed order, output bf16 rounded to nearest even or
+    fp32).  None where the kernel does not take the shape or dtypes."""
+    if out_dtype is None:
+        out_dtype = a.dtype
+    if (a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16 or out_dtype not in (torch.bfloat16, torch.float32)
+            or a.dim() != 2 or b.dim() != 2 or a.shape[0] != b.shape[0] or not a.is_cuda or b.device != a.device):
+        return None
+    K, M = a.shape
+    N = b.shape[1]
+    lib = _lib.load()
+    if not lib.coset_gemm_tn_supported(M, N, K):
+        return None
+    a = a.contiguous()
+    b = b.contiguous()
+    out = torch.empty((M, N), dtype=out_dtype, device=a.device)
+    need = int(lib.coset_gemm_tn_workspace_floats(M, N, K))
+    ws = torch.empty(max(need, 4), dtype=torch.float32, device=a.device)
+    _lib.check("coset_gemm_tn", lib.coset_gemm_tn(a.data_ptr(), M, b.data_ptr(), N, out.data_ptr(), N,
+                                                 _lib.BF16 if out_dtype == torch.bfloat16 else _lib.F32, M, N, K,
+                                                 ws.data_ptr(), need, _lib.stream_of(a)))
+    return out
+
+
+def _weight_grad(g2: torch.Tensor, x2: torch.Tensor) -> torch.Tensor:
+    """dW_q = g2^T x2: coset_gemm_tn where it applies, else torch.mm."""
+    if _GEMM_TN[0] and g2.is_cuda:
+        out = gemm_tn(g2, x2)
+        if out is not None:
+            return out
+    return g2.t() @ x2
+
+
 _AUX_STREAMS: Dict[int, "torch.cuda.Stream"] = {}
 # > 0 while CapturedQATStep warms up and captures: the backward then forks
 # its independent products onto a second stream (graph branches).  Eager
@@ -346,7 +392,8 @@ def _aux_stream(device: torch.device) -> "torch.cuda.Stream":
 
 class QATLinearFn(torch.autograd.Function):
     """y = x W_q^T + b, the layer's F.linear (coset/core/layers.py:478): the
-    products run on hipBLASLt (torch.mm), the bias gradient is the fp32
+    weight gradient runs on coset_gemm_tn where it applies (bf16), the other
+    products on hipBLASLt (torch.mm), the bias gradient is the fp32
     column sum of the output gradient (coset_colsum) instead of a reduction
     in the activation dtype, so a bf16 layer's fp32 bias gets an fp32-exact
     sum of its gradient."""
@@ -388,7 +435,7 @@ class QATLinearFn(torch.autograd.Function):
                     torch.mm(g2, Wq, out=dx2)
                 if fast_db:
                     _colsum_into(g2, *cs)
-            dW = g2.t() @ x.reshape(-1, x.shape[-1])
+            dW = _weight_grad(g2, x.reshape(-1, x.shape[-1]))
             main.wait_stream(aux)
             if need_dx:
                 dx = dx2.reshape(x.shape)
@@ -400,7 +447,7 @@ class QATLinearFn(torch.autograd.Function):
         if ctx.needs_input_grad[0]:
             dx = (g2 @ Wq).reshape(x.shape)
         if ctx.needs_input_grad[1]:
-            dW = g2.t() @ x.reshape(-1, x.shape[-1])
+            dW = _weight_grad(g2, x.reshape(-1, x.shape[-1]))
         if ctx.bias_dtype is not None and ctx.needs_input_grad[2]:
             if g2.shape[1] % 8 == 0 and g2.dtype in (torch.float32, torch.bfloat16, torch.float16):
                 db = colsum(g2).to(ctx.bias_dtype)

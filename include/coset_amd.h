@@ -31,6 +31,7 @@
  *                            estimator             coset/core/layers.py:62-110, 428-463
  *   coset_qat_stats_update   HNLQLinearQAT._gather_stats coset/core/layers.py:366-379
  *   coset_colsum             bias gradient of the layer's F.linear  coset/core/layers.py:478
+ *   coset_gemm_tn            weight gradient of the layer's F.linear coset/core/layers.py:478
  *   coset_vlut_build_one_sided  vLUTManager.build_one_sided_vlut
  *                                                  coset/legacy/quant/vlut.py:72-117
  *   coset_vlut_lookup_dot    one-sided lookup sum  tests/legacy/test_one_sided_vlut_pytest.py:22-43
@@ -197,6 +198,25 @@ int coset_e8_qat_bwd_theta(const void* gWq, int g_dtype, const float* W, const v
 int64_t coset_colsum_workspace_floats(int64_t rows, int64_t cols);
 int coset_colsum(const void* g, int dtype, int64_t rows, int64_t cols, float* out, float* workspace,
                  int64_t workspace_floats, void* stream);
+
+/* Weight gradient of the layer's product (F.linear in HNLQLinearQAT.forward,
+ * coset/core/layers.py:478, whose autograd forms grad_weight = gy^T x):
+ * C[M, N] = A^T B for A = gy [K, M] and B = x [K, N], bf16, row-major with
+ * leading dimensions lda, ldb (elements), accumulated in fp32 in a fixed
+ * order (deterministic); C [M, N] (leading dimension ldc) in fp32
+ * (out_dtype COSET_F32) or bf16 rounded to nearest even (COSET_BF16).  Shapes
+ * the kernel takes (coset_gemm_tn_supported returns 1 for them): M and N
+ * multiples of 64 with (M / 64) (N / 64) <= 256, and K = 256 s m for a power
+ * of two s (the K splits the launch plan picks) and m in {4, 8, 16, 32}
+ * (e.g. K = 1024 .. 8192 in powers of two); others return
+ * COSET_EUNSUPPORTED -- larger products are the library GEMM's.  Buffers 16-byte aligned, lda, ldb, ldc multiples of 8.
+ * workspace: caller-owned fp32 scratch of coset_gemm_tn_workspace_floats(M,
+ * N, K) floats (the split-K partials; 0 when the launch plan has none, and
+ * workspace may then be NULL). */
+int coset_gemm_tn_supported(int64_t M, int64_t N, int64_t K);
+int64_t coset_gemm_tn_workspace_floats(int64_t M, int64_t N, int64_t K);
+int coset_gemm_tn(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int out_dtype,
+                  int64_t M, int64_t N, int64_t K, float* workspace, int64_t workspace_floats, void* stream);
 
 /* The layer's periodic statistics update (HNLQLinearQAT._gather_stats,
  * coset/core/layers.py:366-379, run every stat_update_interval steps at
