@@ -501,17 +501,39 @@ def graph_time(torch, fn, n_calls=20, reps=10):
     return e0.elapsed_time(e1) / 1e3 / (reps * n_calls)
 
 
+class CacheFlush:
+    """Evicts the L2s and the 256 MB Infinity Cache (MALL) by reading a
+    1 GiB buffer (coset_probe_read: every byte loaded, one word per
+    workgroup written).  A read leaves the caches holding clean lines, so the
+    call timed next is not charged for writing back someone else's dirty
+    data (a 1 GiB write as the flush added about 3 us to a C4 call)."""
+
+    def __init__(self, torch):
+        from coset_amd import _lib
+        self._lib = _lib
+        self.lib = _lib.load()
+        self.buf = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+        self.sink = torch.empty(8192, dtype=torch.int32, device="cuda")
+
+    def __call__(self):
+        # 8192 workgroups of 512 threads, 16 loads of 16 bytes a thread
+        self._lib.check("coset_probe_read", self.lib.coset_probe_read(
+            self.buf.data_ptr(), self.buf.numel() * 4, 8192, 512, self.sink.data_ptr(),
+            self._lib.stream_of(self.sink)))
+
+
 def cold_time(torch, fn, flush, reps=25):
     """Median GPU time of one call of fn with the caches cold: before each
-    call a 1 GiB buffer is written, which evicts the 256 MB Infinity Cache
-    (MALL) and the L2s, then HIP events bracket the call alone (the write
-    keeps the GPU busy while the host queues the call, so no host time
-    leaks into the interval)."""
+    call flush() evicts the L2s and the MALL, then HIP events bracket the
+    call alone (the flush keeps the GPU busy while the host queues the call,
+    so no host time leaks into the interval).  The interval includes the
+    event pair's own cost after a flush, about 5 us on this part
+    (c4 floors.events_only_us_cold, subtracted in the *_cold_net figures)."""
     fn()
     torch.cuda.synchronize()
     evs = []
     for i in range(reps):
-        flush.fill_(float(i))
+        flush()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         fn()
@@ -661,17 +683,18 @@ def bench_c4(torch, ca, args):
                        "decoded, 12 MiB decoded6), fp16 activations (fp32_act_*: the same values in fp32), fp32 out; us_graph = per call replayed from a HIP graph "
                        "(weights warm in the 256 MB MALL), us_stream = per call replayed from a HIP graph over "
                        "copies of the weights twice the MALL's size (each call streams its weights from HBM), "
-                       "us_cold = one call between two HIP events after a 1 GiB write evicted the "
-                       "caches (median of 25; includes the events' own cost, floors.events_only_us_cold), "
+                       "us_cold = one call between two HIP events after a 1 GiB read evicted the "
+                       "caches (median of 25; includes the events' own cost, floors.events_only_us_cold, "
+                       "which us_cold_net subtracts), "
                        "us_eager = per call from Python",
            "algorithmic_bytes": "8 MiB codes + B * 8 KiB fp16 (16 KiB fp32) activations + B * 16 KiB fp32 output "
                                 "(frac_hbm*); format_bytes counts the prepared format actually read",
            "batches": {}}
     ws = torch.empty(64 * 4096 * 64, dtype=torch.float32, device="cuda")
-    flush = torch.empty(1 << 28, dtype=torch.float32, device="cuda")
+    flush = CacheFlush(torch)
     wbytes_of = lambda wts: (wts.data.numel() * 4 if isinstance(wts, ca.PreparedWords)
                              else wts.numel() * wts.element_size())
-    res["floors"] = c4_floors(torch, ca, flush, {"raw_words": wbytes_of(words), "decoded6": wbytes_of(decoded6),
+    floors = res["floors"] = c4_floors(torch, ca, flush, {"raw_words": wbytes_of(words), "decoded6": wbytes_of(decoded6),
                                                   "decoded": wbytes_of(decoded)})
     # the formats streamed from HBM: copies whose total is STREAM_BYTES
     stream_sets = {}
@@ -700,8 +723,11 @@ def bench_c4(torch, ca, args):
             io_bytes = B * 4096 * act.element_size() + B * 4096 * 4
             nbytes = C4_CODE_BYTES + io_bytes
             flops = 2.0 * B * 4096 * 4096
+            kcn = max(kc - floors["events_only_us_cold"] * 1e-6, 1e-9)   # the call alone, cold
             r = {"tokens_per_s": round(B / k, 1), "us_graph": round(k * 1e6, 2),
-                 "us_cold": round(kc * 1e6, 2), "us_eager": round(k_eager * 1e6, 2),
+                 "us_cold": round(kc * 1e6, 2), "us_cold_net": round(kcn * 1e6, 2),
+                 "frac_hbm_cold_net": round(nbytes / kcn / 1e9 / HBM_PEAK_GBS, 4),
+                 "us_eager": round(k_eager * 1e6, 2),
                  "tokens_per_s_cold": round(B / kc, 1),
                  "gbs_algorithmic": round(nbytes / k / 1e9, 1),
                  "frac_hbm": round(nbytes / k / 1e9 / HBM_PEAK_GBS, 4),
@@ -833,12 +859,20 @@ def main():
     if kernel_s is not None and "c2stream" in extra:
         extra["c2stream"]["c2_frac_of_ceiling"] = round(extra["c2stream"]["staged"]["kernel_us"] / (kernel_s * 1e6), 4)
     # the detailed record first (one line), then the record the driver reads:
-    # the same top-level fields with one compact object per configuration
+    # the same top-level fields, short, with one compact entry per
+    # configuration, so that the whole line fits the driver's 2000-character
+    # tail of the output
     rec["extra"] = extra
     print(json.dumps(rec), flush=True)
+    if rec.get("cpu_baseline"):
+        cb = rec["cpu_baseline"]
+        rec["cpu_baseline"] = {"value": round(cb["value"], 5), "unit": cb["unit"], "cores": cb["cores"],
+                               "kind": cb["kind"], "sample": "all 2^24 C2 blocks, C oracle, 2^20-block chunks"}
+    if rec.get("roofline"):
+        rec["roofline"]["traffic_source"] = "stored PMC (profiles/hnlq_roundtrip_c2_traffic.json)"
+    rec["config"] = {"workload": "C2 bulk E8 HNLQ encode->decode", "blocks": C2_BLOCKS, "q": 4, "M": 2, "beta": 1.0}
     rec["extra"] = summarize(extra)
-    rec["detail"] = "the line above holds every figure of this run"
-    print(json.dumps(rec), flush=True)
+    print(json.dumps(rec, separators=(",", ":")), flush=True)
 
 
 def _pick(d, *path):
@@ -849,61 +883,63 @@ def _pick(d, *path):
     return d
 
 
+def _r(x, nd=3):
+    """x to nd significant digits (None stays None)."""
+    if x is None:
+        return None
+    if x == 0:
+        return 0
+    return float(f"{x:.{nd}g}")
+
+
 def summarize(extra):
-    """One compact object per configuration: time, fraction of its roofline,
-    the C4 cold and HBM-streamed times, and the CPU baseline's value."""
+    """One compact entry per configuration (times in us unless the key says
+    ms; f = fraction of the config's roofline; cpu = the CPU baseline's value
+    in the config's unit).  The legend key spells out the C4 and C5 lists."""
     out = {}
     c1 = extra.get("c1")
     if c1:
-        out["c1"] = {"us_graph": _pick(c1, "graph", "us_per_forward_gpu"), "us_eager": c1.get("us_per_forward_gpu"),
-                     "us_nondegenerate": _pick(c1, "nondegenerate", "us_per_forward_gpu"),
-                     "cpu_us": _pick(c1, "cpu_baseline", "value")}
+        out["c1"] = {"us_graph": _r(_pick(c1, "graph", "us_per_forward_gpu")), "us": _r(c1.get("us_per_forward_gpu")),
+                     "cpu_us": _r(_pick(c1, "cpu_baseline", "value"))}
     c2s = extra.get("c2stream")
     if c2s:
-        out["c2stream"] = {"us": _pick(c2s, "staged", "kernel_us"), "frac_hbm": _pick(c2s, "staged", "frac_hbm"),
-                           "us_unstaged": _pick(c2s, "unstaged", "kernel_us"),
-                           "c2_frac_of_ceiling": c2s.get("c2_frac_of_ceiling")}
+        out["c2stream"] = {"us": _r(_pick(c2s, "staged", "kernel_us"), 4), "f": _r(_pick(c2s, "staged", "frac_hbm")),
+                           "c2_of_ceiling": _r(c2s.get("c2_frac_of_ceiling"))}
     c2c = extra.get("c2codes")
     if c2c:
-        out["c2codes"] = {"us": c2c.get("kernel_us"), "frac_hbm": c2c.get("frac_hbm")}
+        out["c2codes"] = {"us": _r(c2c.get("kernel_us"), 4), "f": _r(c2c.get("frac_hbm"))}
     c2a = extra.get("c2api")
     if c2a:
-        out["c2api_us"] = {k: v.get("kernel_us") for k, v in c2a.get("calls", {}).items()}
+        out["c2api_us"] = {k: _r(v.get("kernel_us"), 4) for k, v in c2a.get("calls", {}).items()}
     c3 = extra.get("c3")
     if c3:
-        out["c3"] = {"us": c3.get("kernel_us"), "gbs": c3.get("hbm_gbs"), "frac_hbm": c3.get("frac_hbm"),
-                     "cpu_gblocks_s": _pick(c3, "cpu_baseline", "value")}
+        out["c3"] = {"us": _r(c3.get("kernel_us"), 4), "f": _r(c3.get("frac_hbm")),
+                     "cpu_gblocks_s": _r(_pick(c3, "cpu_baseline", "value"))}
     c4 = extra.get("c4")
     if c4:
-        o4 = {}
+        o4 = {"legend": "B: [method, us_graph, us_stream, us_cold_net, f_graph, f_stream, cpu tokens/s, lds us_graph]"}
         for B, row in c4.get("batches", {}).items():
-            best = min((v for k, v in row.items() if isinstance(v, dict) and "us_graph" in v
-                        and not k.startswith("fp32") and k != "mfma_legacy_q"), key=lambda v: v.get("us_graph", 1e9))
-            name = [k for k, v in row.items() if v is best][0]
-            o4["B" + B] = {"method": name, "us_graph": best.get("us_graph"), "us_stream": best.get("us_stream"),
-                           "us_cold": best.get("us_cold"), "frac_hbm": best.get("frac_hbm"),
-                           "frac_hbm_stream": best.get("frac_hbm_stream"), "frac_hbm_cold": best.get("frac_hbm_cold"),
-                           "lds_us_graph": _pick(row, "lds", "us_graph"),
-                           "cpu_tokens_s": _pick(row, "cpu_baseline", "value")}
-            for k in ("mfma_decoded", "mfma_decoded6", "mfma_raw_words"):
-                if k in row and row[k] is not best:
-                    o4["B" + B][k] = {f: row[k].get(f) for f in ("us_graph", "us_stream", "us_cold")}
+            cands = [(k, v) for k, v in row.items() if isinstance(v, dict) and "us_graph" in v
+                     and not k.startswith("fp32") and k != "mfma_legacy_q"]
+            name, best = min(cands, key=lambda kv: kv[1].get("us_graph", 1e9))
+            o4[B] = [name, _r(best.get("us_graph")), _r(best.get("us_stream")), _r(best.get("us_cold_net")),
+                     _r(best.get("frac_hbm")), _r(best.get("frac_hbm_stream")),
+                     _r(_pick(row, "cpu_baseline", "value")), _r(_pick(row, "lds", "us_graph"))]
         fl = c4.get("floors", {})
-        o4["floors"] = {"events_only_us_cold": fl.get("events_only_us_cold"),
-                        "empty_us_cold": _pick(fl, "empty_rows_shape", "us_cold"),
-                        "empty_us_graph": _pick(fl, "empty_rows_shape", "us_graph")}
-        for k, v in fl.items():
-            if k.startswith("read_"):
-                o4["floors"][k] = {f: v.get(f) for f in ("us_cold", "us_graph", "us_stream")}
+        o4["floors_us"] = {"events_cold": _r(fl.get("events_only_us_cold")),
+                           "empty_graph": _r(_pick(fl, "empty_rows_shape", "us_graph")),
+                           "read_raw_stream": _r(_pick(fl, "read_raw_words", "us_stream")),
+                           "read_decoded_stream": _r(_pick(fl, "read_decoded", "us_stream"))}
         out["c4"] = o4
     c5 = extra.get("c5")
     if c5:
-        out["c5"] = {k: {"ms_graph": _pick(v, "graph", "ms"), "frac_mfma": _pick(v, "graph", "frac_bf16_mfma"),
-                         "ms_eager": v.get("ms"), "cpu_tokens_s": _pick(v, "cpu_baseline", "value")}
-                     for k, v in c5.get("shapes", {}).items()}
+        out["c5"] = {"legend": "[ms_graph, f_mfma, ms_eager, cpu tokens/s]"}
+        for k, v in c5.get("shapes", {}).items():
+            out["c5"][k] = [_r(_pick(v, "graph", "ms")), _r(_pick(v, "graph", "frac_bf16_mfma")), _r(v.get("ms")),
+                            _r(_pick(v, "cpu_baseline", "value"))]
     pk = extra.get("peaks")
     if pk:
-        out["peaks"] = {"copy_gbs": _pick(pk, "copy", "gbs"), "gemm_bf16_tflops": _pick(pk, "gemm_bf16", "tflops")}
+        out["peaks"] = {"copy_gbs": _r(_pick(pk, "copy", "gbs"), 4), "gemm_bf16_tflops": _r(_pick(pk, "gemm_bf16", "tflops"), 4)}
     return out
 
 

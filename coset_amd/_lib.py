@@ -64,7 +64,7 @@ SIGNATURES = {
     "coset_qat_stats_update": [_vp, _i64, _i64, ctypes.c_double, _vp, _vp, _vp],
     "coset_colsum": [_vp, _int, _i64, _i64, _vp, _vp, _i64, _vp],
     "coset_gemm_tn_supported": [_i64, _i64, _i64],
-    "coset_gemm_tn": [_vp, _i64, _vp, _i64, _vp, _i64, _int, _i64, _i64, _i64, _vp, _i64, _vp],
+    "coset_gemm_tn": [_vp, _i64, _vp, _i64, _vp, _i64, _int, _i64, _i64, _i64, _vp, _vp, _i64, _vp],
     "coset_vlut_matmul_noalloc": [_vp, _int, _vp, _int, _vp, _int, _i64, _i64, _i64, _int, _int, _int, _int, _vp,
                                   _vp],
     "coset_probe_empty": [_int, _int, _int, _vp, _vp],

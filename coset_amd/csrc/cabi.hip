@@ -470,7 +470,8 @@ int64_t coset_gemm_tn_workspace_floats(int64_t M, int64_t N, int64_t K)
 }
 
 int coset_gemm_tn(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int out_dtype,
-                  int64_t M, int64_t N, int64_t K, float* workspace, int64_t workspace_floats, void* stream)
+                  int64_t M, int64_t N, int64_t K, float* colsum, float* workspace, int64_t workspace_floats,
+                  void* stream)
 {
     if (M < 0 || N < 0 || K < 0) return fail(COSET_EINVAL, "M, N, K must be >= 0");
     if (out_dtype != COSET_F32 && out_dtype != COSET_BF16)
@@ -489,8 +490,9 @@ int coset_gemm_tn(const void* A, int64_t lda, const void* B, int64_t ldb, void* 
     if (need > 0 && (!workspace || workspace_floats < need))
         return fail(COSET_EINVAL, "workspace too small: %lld floats needed", (long long)need);
     if (need > 0 && !aligned(workspace, 16)) return fail(COSET_EINVAL, "workspace must be 16-byte aligned");
+    if (colsum && !aligned(colsum, 16)) return fail(COSET_EINVAL, "colsum must be 16-byte aligned");
     return check_hip(coset::gemm_tn_bf16(static_cast<const uint16_t*>(A), lda, static_cast<const uint16_t*>(B), ldb, C,
-                                         ldc, out_dtype, M, N, K, plan, need > 0 ? workspace : nullptr,
+                                         ldc, out_dtype, M, N, K, plan, need > 0 ? workspace : nullptr, colsum,
                                          (hipStream_t)stream),
                      "gemm_tn launch");
 }

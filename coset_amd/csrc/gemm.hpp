@@ -24,12 +24,13 @@ struct GemmTnPlan {
 // The plan for this shape: M, N multiples of 64 with at most 256 tiles of 64 x 64,
 // K = 256 * splits * my for my in {4, 8, 16, 32}.
 GemmTnPlan gemm_tn_plan(int64_t M, int64_t N, int64_t K);
-// fp32 workspace the plan needs (splits x M x N, or 0)
+// fp32 workspace the plan needs (splits x (M x N + M), or 0)
 int64_t gemm_tn_workspace_floats(const GemmTnPlan& p, int64_t M, int64_t N);
 
 // out_dtype: 0 fp32, 1 bf16 (round to nearest even).  ldc in elements.
+// colsum (nullable): also colsum[m] = sum_k A[k, m] in fp32 (fixed order).
 hipError_t gemm_tn_bf16(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t ldb, void* C, int64_t ldc,
                         int out_dtype, int64_t M, int64_t N, int64_t K, const GemmTnPlan& plan, float* workspace,
-                        hipStream_t s);
+                        float* colsum, hipStream_t s);
 
 }  // namespace coset

@@ -39,6 +39,7 @@ namespace coset {
 namespace {
 
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef short s16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8_gt __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
@@ -99,11 +100,17 @@ __device__ __forceinline__ void store8(void* C, int64_t idx, const float v[8])
 // OUT: 0 fp32 C, 1 bf16 C (one K split, C with leading dimension ldc), 2 the
 // fp32 partial tile of split blockIdx.y at C + blockIdx.y * M * ldc.  MY: the
 // 32-token slices of each wave (the split's K range is kTnWaves * MY * 32).
-template <int OUT, int MY>
+// CS: also the column sums of A, colsum[m] = sum_k A[k, m] (the bias
+// gradient when A is the output gradient), by one workgroup per tile row (tn
+// == tm % tiles_n) with four more MFMAs per slice against an all-ones
+// operand; fp32 to colsum (one split) or split blockIdx.y's partial to
+// colsum + blockIdx.y * M.
+template <int OUT, int MY, bool CS>
 __global__ void __launch_bounds__(kTnWaves * 64) gemm_tn_kernel(const uint16_t* __restrict__ A, int64_t lda,
                                                                 const uint16_t* __restrict__ B, int64_t ldb,
                                                                 void* __restrict__ C, int64_t ldc, int64_t M,
-                                                                int tiles_n, int xcd_m, int xcd_n)
+                                                                int tiles_n, int xcd_m, int xcd_n,
+                                                                float* __restrict__ colsum)
 {
     __shared__ __align__(16) char lds[kTnLds];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -124,6 +131,7 @@ __global__ void __launch_bounds__(kTnWaves * 64) gemm_tn_kernel(const uint16_t* 
         tn = blockIdx.x % tiles_n;
     }
     const int64_t m0 = (int64_t)tm * kTnTile, n0 = (int64_t)tn * kTnTile;
+    const bool do_cs = CS && tn == tm % tiles_n;   // uniform
     // this wave's slices: k = (blockIdx.y * kTnWaves * MY + wave + i * kTnWaves) * 32, i < MY
     const int64_t k_wave = ((int64_t)blockIdx.y * kTnWaves * MY + wave) * kTnSlice;
 
@@ -150,11 +158,14 @@ __global__ void __launch_bounds__(kTnWaves * 64) gemm_tn_kernel(const uint16_t* 
         }
     };
 
-    f32x4_t acc[kTnMt][kTnMt];
+    f32x4_t acc[kTnMt][kTnMt], acs[kTnMt];
 #pragma unroll
-    for (int i = 0; i < kTnMt; ++i)
+    for (int i = 0; i < kTnMt; ++i) {
+        acs[i] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < kTnMt; ++j) acc[i][j] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    }
+    const bf16x8_gt ones = __builtin_bit_cast(bf16x8_gt, (s16x8_t)(short)0x3f80);   // eight bf16 1.0
 
     // two transposing reads per operand tile: rows (tokens) 8 g + r / 4 and 4
     // more, columns 16 i + 4 (r % 4)
@@ -173,6 +184,7 @@ __global__ void __launch_bounds__(kTnWaves * 64) gemm_tn_kernel(const uint16_t* 
         for (int i = 0; i < kTnMt; ++i) {
             const bf16x8_gt av =
                 __builtin_bit_cast(bf16x8_gt, __builtin_shufflevector(a[i][0], a[i][1], 0, 1, 2, 3, 4, 5, 6, 7));
+            if (do_cs) acs[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, ones, acs[i], 0, 0, 0);
 #pragma unroll
             for (int j = 0; j < kTnMt; ++j) {
                 const bf16x8_gt bv =
@@ -229,17 +241,47 @@ __global__ void __launch_bounds__(kTnWaves * 64) gemm_tn_kernel(const uint16_t* 
         }
         __syncthreads();
     }
+    if (do_cs) {
+        // D[row 4 g + e][every column] = that row's sum over the wave's tokens:
+        // lanes of column 0 hand them to LDS, then the waves' sums in wave order
+        if (r == 0) {
+#pragma unroll
+            for (int i = 0; i < kTnMt; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) red[wave * kTnTile + 16 * i + 4 * g + e] = acs[i][e];
+        }
+        __syncthreads();
+        if (tid < kTnTile) {
+            float v = red[tid];
+#pragma unroll
+            for (int w = 1; w < kTnWaves; ++w) v += red[w * kTnTile + tid];
+            colsum[(OUT == 2 ? (int64_t)blockIdx.y * M : 0) + m0 + tid] = v;
+        }
+    }
 }
 
 // C = sum over splits of the fp32 partials [splits, M, N], in split order;
-// 8 consecutive outputs per thread (N % 8 == 0)
+// 8 consecutive outputs per thread (N % 8 == 0).  With colsum: the threads
+// past C also sum the column sums' partials [splits, M] (after the tiles'
+// partials in the workspace) into colsum.
 template <int OUT>
 __global__ void __launch_bounds__(256) gemm_tn_reduce_kernel(const float* __restrict__ part, int splits, int64_t M,
-                                                             int64_t N, void* __restrict__ C, int64_t ldc)
+                                                             int64_t N, void* __restrict__ C, int64_t ldc,
+                                                             float* __restrict__ colsum)
 {
     const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
     const int64_t mn = M * N;
-    if (i >= mn) return;
+    if (i >= mn) {
+        const int64_t m = i - mn;
+        if (!colsum || m >= M) return;
+        const float* cp = part + splits * mn;
+        for (int q = 0; q < 8; ++q) {
+            float v = cp[m + q];
+            for (int sp = 1; sp < splits; ++sp) v += cp[sp * M + m + q];
+            colsum[m + q] = v;
+        }
+        return;
+    }
     float v[8];
     for (int s = 0; s < splits; ++s) {
         const float4* src = reinterpret_cast<const float4*>(part + s * mn + i);
@@ -251,33 +293,46 @@ __global__ void __launch_bounds__(256) gemm_tn_reduce_kernel(const float* __rest
     store8<OUT>(C, (i / N) * ldc + i % N, v);
 }
 
-template <int MY>
+template <int MY, bool CS>
 hipError_t launch_tn(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t ldb, void* C, int64_t ldc,
-                     int out_bf16, int64_t M, int64_t N, const GemmTnPlan& plan, float* partial, hipStream_t s)
+                     int out_bf16, int64_t M, int64_t N, const GemmTnPlan& plan, float* partial, float* colsum,
+                     hipStream_t s)
 {
     const int tiles_n = (int)(N / kTnTile);
     const dim3 grid((unsigned)((M / kTnTile) * tiles_n), (unsigned)plan.splits);
     const dim3 block(kTnWaves * 64);
     if (plan.splits == 1) {
         if (out_bf16)
-            hipLaunchKernelGGL((gemm_tn_kernel<1, MY>), grid, block, 0, s, A, lda, B, ldb, C, ldc, M, tiles_n,
-                               plan.xcd_m, plan.xcd_n);
+            hipLaunchKernelGGL((gemm_tn_kernel<1, MY, CS>), grid, block, 0, s, A, lda, B, ldb, C, ldc, M, tiles_n,
+                               plan.xcd_m, plan.xcd_n, colsum);
         else
-            hipLaunchKernelGGL((gemm_tn_kernel<0, MY>), grid, block, 0, s, A, lda, B, ldb, C, ldc, M, tiles_n,
-                               plan.xcd_m, plan.xcd_n);
+            hipLaunchKernelGGL((gemm_tn_kernel<0, MY, CS>), grid, block, 0, s, A, lda, B, ldb, C, ldc, M, tiles_n,
+                               plan.xcd_m, plan.xcd_n, colsum);
         return hipGetLastError();
     }
-    hipLaunchKernelGGL((gemm_tn_kernel<2, MY>), grid, block, 0, s, A, lda, B, ldb, (void*)partial, N, M, tiles_n,
-                       plan.xcd_m, plan.xcd_n);
+    // split partials: the tiles' [splits, M, N], then the column sums' [splits, M]
+    hipLaunchKernelGGL((gemm_tn_kernel<2, MY, CS>), grid, block, 0, s, A, lda, B, ldb, (void*)partial, N, M, tiles_n,
+                       plan.xcd_m, plan.xcd_n, partial + (int64_t)plan.splits * M * N);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int64_t threads = M * N / 8;
+    const int64_t threads = (M * N + (CS ? M : 0)) / 8;
     const dim3 rgrid((unsigned)((threads + 255) / 256));
     if (out_bf16)
-        hipLaunchKernelGGL((gemm_tn_reduce_kernel<1>), rgrid, dim3(256), 0, s, partial, plan.splits, M, N, C, ldc);
+        hipLaunchKernelGGL((gemm_tn_reduce_kernel<1>), rgrid, dim3(256), 0, s, partial, plan.splits, M, N, C, ldc,
+                           CS ? colsum : nullptr);
     else
-        hipLaunchKernelGGL((gemm_tn_reduce_kernel<0>), rgrid, dim3(256), 0, s, partial, plan.splits, M, N, C, ldc);
+        hipLaunchKernelGGL((gemm_tn_reduce_kernel<0>), rgrid, dim3(256), 0, s, partial, plan.splits, M, N, C, ldc,
+                           CS ? colsum : nullptr);
     return hipGetLastError();
+}
+
+template <int MY>
+hipError_t launch_tn_cs(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t ldb, void* C, int64_t ldc,
+                        int out_bf16, int64_t M, int64_t N, const GemmTnPlan& plan, float* partial, float* colsum,
+                        hipStream_t s)
+{
+    return colsum ? launch_tn<MY, true>(A, lda, B, ldb, C, ldc, out_bf16, M, N, plan, partial, colsum, s)
+                  : launch_tn<MY, false>(A, lda, B, ldb, C, ldc, out_bf16, M, N, plan, partial, nullptr, s);
 }
 
 }  // namespace
@@ -327,21 +382,21 @@ GemmTnPlan gemm_tn_plan(int64_t M, int64_t N, int64_t K)
 
 int64_t gemm_tn_workspace_floats(const GemmTnPlan& p, int64_t M, int64_t N)
 {
-    return p.tile > 0 && p.splits > 1 ? (int64_t)p.splits * M * N : 0;
+    return p.tile > 0 && p.splits > 1 ? (int64_t)p.splits * (M * N + M) : 0;
 }
 
 hipError_t gemm_tn_bf16(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t ldb, void* C, int64_t ldc,
                         int out_dtype, int64_t M, int64_t N, int64_t K, const GemmTnPlan& plan, float* workspace,
-                        hipStream_t s)
+                        float* colsum, hipStream_t s)
 {
     const int ob = out_dtype == 1;
     if (plan.tile != kTnTile || (plan.splits > 1 && !workspace)) return hipErrorInvalidValue;
     (void)K;   // the plan's slice count fixes the K range of each launch
     switch (plan.my) {
-    case 4: return launch_tn<4>(A, lda, B, ldb, C, ldc, ob, M, N, plan, workspace, s);
-    case 8: return launch_tn<8>(A, lda, B, ldb, C, ldc, ob, M, N, plan, workspace, s);
-    case 16: return launch_tn<16>(A, lda, B, ldb, C, ldc, ob, M, N, plan, workspace, s);
-    case 32: return launch_tn<32>(A, lda, B, ldb, C, ldc, ob, M, N, plan, workspace, s);
+    case 4: return launch_tn_cs<4>(A, lda, B, ldb, C, ldc, ob, M, N, plan, workspace, colsum, s);
+    case 8: return launch_tn_cs<8>(A, lda, B, ldb, C, ldc, ob, M, N, plan, workspace, colsum, s);
+    case 16: return launch_tn_cs<16>(A, lda, B, ldb, C, ldc, ob, M, N, plan, workspace, colsum, s);
+    case 32: return launch_tn_cs<32>(A, lda, B, ldb, C, ldc, ob, M, N, plan, workspace, colsum, s);
     default: return hipErrorInvalidValue;
     }
 }

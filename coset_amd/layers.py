@@ -328,9 +328,16 @@ def colsum(g2: torch.Tensor) -> torch.Tensor:
 
 
 # 1: the weight gradient gy^T x runs on coset_gemm_tn where the shape and
-# dtypes allow it (bf16, M and N multiples of 64, tokens a multiple of 128),
-# 0: always on torch.mm (hipBLASLt)
+# dtypes allow it (coset_gemm_tn_supported, bf16), 0: always on torch.mm
+# (hipBLASLt)
 _GEMM_TN = [1]
+# 1: where coset_gemm_tn runs the weight gradient of a step on one stream
+# (eager), the bias gradient's column sums come from the same pass, one launch
+# fewer; 0: from coset_colsum.  A step that forks its backward over two
+# streams (CapturedQATStep) keeps coset_colsum beside dX on the second
+# stream: fused into dW the sums lengthened the 768x768 graph step (4096
+# tokens) from 59.2 to 63.7 us
+_FUSE_BIAS_GRAD = [1]
 
 
 def set_gemm_tn(enabled: bool) -> None:
@@ -339,10 +346,13 @@ def set_gemm_tn(enabled: bool) -> None:
     _GEMM_TN[0] = 1 if enabled else 0
 
 
-def gemm_tn(a: torch.Tensor, b: torch.Tensor, out_dtype: Optional[torch.dtype] = None) -> Optional[torch.Tensor]:
+def gemm_tn(a: torch.Tensor, b: torch.Tensor, out_dtype: Optional[torch.dtype] = None,
+            colsum: Optional[torch.Tensor] = None) -> Optional[torch.Tensor]:
     """a^T b for bf16 a [K, M] and b [K, N] on the GPU (coset_gemm_tn: fp32
     accumulation in a fixed order, output bf16 rounded to nearest even or
-    fp32).  None where the kernel does not take the shape or dtypes."""
+    fp32); colsum (optional fp32 [M]) also receives the column sums of a in
+    the same pass.  None where the kernel does not take the shape or dtypes
+    (colsum then untouched)."""
     if out_dtype is None:
         out_dtype = a.dtype
     if (a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16 or out_dtype not in (torch.bfloat16, torch.float32)
@@ -353,6 +363,8 @@ def gemm_tn(a: torch.Tensor, b: torch.Tensor, out_dtype: Optional[torch.dtype] =
     lib = _lib.load()
     if not lib.coset_gemm_tn_supported(M, N, K):
         return None
+    if colsum is not None and (colsum.dtype != torch.float32 or colsum.numel() != M or not colsum.is_contiguous()):
+        raise ValueError("colsum must be a contiguous fp32 tensor of M elements")
     a = a.contiguous()
     b = b.contiguous()
     out = torch.empty((M, N), dtype=out_dtype, device=a.device)
@@ -360,16 +372,28 @@ def gemm_tn(a: torch.Tensor, b: torch.Tensor, out_dtype: Optional[torch.dtype] =
     ws = torch.empty(max(need, 4), dtype=torch.float32, device=a.device)
     _lib.check("coset_gemm_tn", lib.coset_gemm_tn(a.data_ptr(), M, b.data_ptr(), N, out.data_ptr(), N,
                                                  _lib.BF16 if out_dtype == torch.bfloat16 else _lib.F32, M, N, K,
-                                                 ws.data_ptr(), need, _lib.stream_of(a)))
+                                                 0 if colsum is None else colsum.data_ptr(), ws.data_ptr(), need,
+                                                 _lib.stream_of(a)))
     return out
 
 
-def _weight_grad(g2: torch.Tensor, x2: torch.Tensor) -> torch.Tensor:
-    """dW_q = g2^T x2: coset_gemm_tn where it applies, else torch.mm."""
-    if _GEMM_TN[0] and g2.is_cuda:
-        out = gemm_tn(g2, x2)
+def _gemm_tn_takes(g2: torch.Tensor, x2: torch.Tensor) -> bool:
+    """Whether _weight_grad runs g2^T x2 on coset_gemm_tn."""
+    return (_GEMM_TN[0] == 1 and g2.is_cuda and g2.dtype == x2.dtype == torch.bfloat16 and g2.dim() == 2
+            and x2.dim() == 2 and g2.shape[0] == x2.shape[0]
+            and bool(_lib.load().coset_gemm_tn_supported(g2.shape[1], x2.shape[1], g2.shape[0])))
+
+
+def _weight_grad(g2: torch.Tensor, x2: torch.Tensor, colsum: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """dW_q = g2^T x2: coset_gemm_tn where it applies (with colsum: also the
+    fp32 column sums of g2, the bias gradient, in the same pass), else
+    torch.mm (colsum must then be None)."""
+    if _gemm_tn_takes(g2, x2):
+        out = gemm_tn(g2, x2, colsum=colsum)
         if out is not None:
             return out
+    if colsum is not None:
+        raise RuntimeError("column sums requested where coset_gemm_tn does not run")
     return g2.t() @ x2
 
 
@@ -392,11 +416,11 @@ def _aux_stream(device: torch.device) -> "torch.cuda.Stream":
 
 class QATLinearFn(torch.autograd.Function):
     """y = x W_q^T + b, the layer's F.linear (coset/core/layers.py:478): the
-    weight gradient runs on coset_gemm_tn where it applies (bf16), the other
-    products on hipBLASLt (torch.mm), the bias gradient is the fp32
-    column sum of the output gradient (coset_colsum) instead of a reduction
-    in the activation dtype, so a bf16 layer's fp32 bias gets an fp32-exact
-    sum of its gradient."""
+    weight gradient runs on coset_gemm_tn where it applies (bf16), with the
+    bias gradient's column sums in the same pass, the other products on
+    hipBLASLt (torch.mm); elsewhere the bias gradient is the fp32 column sum
+    of the output gradient (coset_colsum).  Either way a bf16 layer's fp32
+    bias gets an fp32 sum of its gradient, not a reduction in bf16."""
 
     @staticmethod
     def forward(ctx, x, Wq, bias, bias_cast=None):
@@ -417,12 +441,14 @@ class QATLinearFn(torch.autograd.Function):
         fast_db = (ctx.bias_dtype is not None and ctx.needs_input_grad[2] and g2.shape[1] % 8 == 0
                    and g2.dtype in (torch.float32, torch.bfloat16, torch.float16))
         overlap = g2.is_cuda and (_OVERLAP_BACKWARD[0] > 0 or torch.cuda.is_current_stream_capturing())
+        x2 = x.reshape(-1, x.shape[-1])
         if overlap and need_dw and (need_dx or fast_db) and g2.dtype == Wq.dtype == x.dtype:
             # dX and the bias gradient on a second stream while dW runs on
-            # this one: the dW product alone leaves CUs idle at these shapes
-            # (one 128 x 128 tile per CU or fewer).  Outputs are allocated here, on the
-            # current stream, before the fork; the join comes before they
-            # are returned.  Under graph capture the two streams become two
+            # this one: the dW product alone
+            # leaves CUs idle at these shapes (one 64 x 64 or 128 x 128 tile
+            # per CU or fewer).  Outputs are allocated here, on the current
+            # stream, before the fork; the join comes before they are
+            # returned.  Under graph capture the two streams become two
             # branches of the graph.
             g2 = g2.contiguous()
             main = torch.cuda.current_stream(g2.device)
@@ -435,7 +461,7 @@ class QATLinearFn(torch.autograd.Function):
                     torch.mm(g2, Wq, out=dx2)
                 if fast_db:
                     _colsum_into(g2, *cs)
-            dW = _weight_grad(g2, x.reshape(-1, x.shape[-1]))
+            dW = _weight_grad(g2, x2)
             main.wait_stream(aux)
             if need_dx:
                 dx = dx2.reshape(x.shape)
@@ -443,6 +469,16 @@ class QATLinearFn(torch.autograd.Function):
                 db = cs[0].to(ctx.bias_dtype)
             elif ctx.bias_dtype is not None and ctx.needs_input_grad[2]:
                 db = g2.float().sum(0).to(ctx.bias_dtype)
+            return dx, dW, db, None
+        # one stream: the bias gradient in the weight-gradient kernel's pass
+        # where that kernel runs (bf16), the column sums of gy with gy^T x
+        if (_FUSE_BIAS_GRAD[0] == 1 and fast_db and need_dw and g2.dtype == torch.bfloat16 and g2.is_contiguous()
+                and _gemm_tn_takes(g2, x2)):
+            dbf = torch.empty(g2.shape[1], dtype=torch.float32, device=g2.device)
+            dW = _weight_grad(g2, x2, colsum=dbf)
+            db = dbf.to(ctx.bias_dtype)
+            if need_dx:
+                dx = (g2 @ Wq).reshape(x.shape)
             return dx, dW, db, None
         if ctx.needs_input_grad[0]:
             dx = (g2 @ Wq).reshape(x.shape)

@@ -209,14 +209,18 @@ int coset_colsum(const void* g, int dtype, int64_t rows, int64_t cols, float* ou
  * multiples of 64 with (M / 64) (N / 64) <= 256, and K = 256 s m for a power
  * of two s (the K splits the launch plan picks) and m in {4, 8, 16, 32}
  * (e.g. K = 1024 .. 8192 in powers of two); others return
- * COSET_EUNSUPPORTED -- larger products are the library GEMM's.  Buffers 16-byte aligned, lda, ldb, ldc multiples of 8.
- * workspace: caller-owned fp32 scratch of coset_gemm_tn_workspace_floats(M,
- * N, K) floats (the split-K partials; 0 when the launch plan has none, and
- * workspace may then be NULL). */
+ * COSET_EUNSUPPORTED -- larger products are the library GEMM's.  Buffers
+ * 16-byte aligned, lda, ldb, ldc multiples of 8.  colsum (nullable): also
+ * colsum[m] = sum_k A[k, m], fp32, fixed order -- with A = gy, the bias
+ * gradient of the same F.linear, in the same pass.  workspace: caller-owned
+ * fp32 scratch of coset_gemm_tn_workspace_floats(M, N, K) floats (the split-K
+ * partials; 0 when the launch plan has none, and workspace may then be
+ * NULL). */
 int coset_gemm_tn_supported(int64_t M, int64_t N, int64_t K);
 int64_t coset_gemm_tn_workspace_floats(int64_t M, int64_t N, int64_t K);
 int coset_gemm_tn(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int out_dtype,
-                  int64_t M, int64_t N, int64_t K, float* workspace, int64_t workspace_floats, void* stream);
+                  int64_t M, int64_t N, int64_t K, float* colsum, float* workspace, int64_t workspace_floats,
+                  void* stream);
 
 /* The layer's periodic statistics update (HNLQLinearQAT._gather_stats,
  * coset/core/layers.py:366-379, run every stat_update_interval steps at

@@ -31,15 +31,15 @@ def _workspace(M, N, K):
     return torch.full((max(need, 4),), float("nan"), dtype=torch.float32, device="cuda"), need
 
 
-def _tn(a, b, out_dtype):
+def _tn(a, b, out_dtype, colsum=None):
     lib = _lib.load()
     K, M = a.shape
     N = b.shape[1]
     out = torch.full((M, N), float("nan"), dtype=out_dtype, device="cuda")
     ws, need = _workspace(M, N, K)
     rc = lib.coset_gemm_tn(a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0), out.data_ptr(), out.stride(0),
-                           _lib.BF16 if out_dtype == torch.bfloat16 else _lib.F32, M, N, K, ws.data_ptr(), need,
-                           _lib.stream_of(a))
+                           _lib.BF16 if out_dtype == torch.bfloat16 else _lib.F32, M, N, K,
+                           0 if colsum is None else colsum.data_ptr(), ws.data_ptr(), need, _lib.stream_of(a))
     _lib.check("coset_gemm_tn", rc)
     torch.cuda.synchronize()
     return out
@@ -60,8 +60,11 @@ def test_integer_operands_exact(M, N, K):
     a, b, exact = _int_operands(K, M, N, seed=M + N + K)
     c32 = _tn(a, b, torch.float32)
     assert torch.equal(c32.double(), exact), "fp32 output differs from the exact integer product"
-    c16 = _tn(a, b, torch.bfloat16)
+    cs = torch.full((M,), float("nan"), dtype=torch.float32, device="cuda")
+    c16 = _tn(a, b, torch.bfloat16, colsum=cs)
     assert torch.equal(c16, exact.float().to(torch.bfloat16)), "bf16 output is not the RNE of the exact product"
+    # the column sums of A (the bias gradient when A = gy), exact integers too
+    assert torch.equal(cs.double(), a.double().sum(0)), "column sums differ"
 
 
 @pytest.mark.parametrize("M,N,K", [(768, 768, 4096), (512, 512, 4096)])
@@ -93,7 +96,7 @@ def test_strided_operands():
         out = torch.full((M, N + 16), float("nan"), dtype=torch.float32, device="cuda")
         ws, need = _workspace(M, N, K)
         rc = lib.coset_gemm_tn(a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0), out.data_ptr(), out.stride(0),
-                               _lib.F32, M, N, K, ws.data_ptr(), need, _lib.stream_of(a))
+                               _lib.F32, M, N, K, 0, ws.data_ptr(), need, _lib.stream_of(a))
         _lib.check("coset_gemm_tn", rc)
         torch.cuda.synchronize()
         assert torch.equal(out[:, :N].double(), exact)
@@ -105,12 +108,12 @@ def test_workspace_refusals():
     lib = _lib.load()
     M, N, K = 512, 512, 4096
     need = int(lib.coset_gemm_tn_workspace_floats(M, N, K))
-    assert need == 4 * M * N   # 64 tiles: four K splits
+    assert need == 4 * (M * N + M)   # 64 tiles: four K splits (tiles' and column sums' partials)
     a = torch.zeros((K, M), dtype=torch.bfloat16, device="cuda")
     out = torch.zeros((M, N), dtype=torch.bfloat16, device="cuda")
     ws = torch.zeros(need, dtype=torch.float32, device="cuda")
     for ptr, n in ((0, 0), (ws.data_ptr(), need - 1)):
-        rc = lib.coset_gemm_tn(a.data_ptr(), M, a.data_ptr(), N, out.data_ptr(), N, _lib.BF16, M, N, K, ptr, n,
+        rc = lib.coset_gemm_tn(a.data_ptr(), M, a.data_ptr(), N, out.data_ptr(), N, _lib.BF16, M, N, K, 0, ptr, n,
                                _lib.stream_of(a))
         assert rc == -1, rc
     assert int(lib.coset_gemm_tn_workspace_floats(768, 768, 4096)) == 0   # 144 tiles: no split
@@ -128,8 +131,9 @@ def test_unsupported_shapes_refused():
 
 
 def test_layer_weight_grad_matches_torch():
-    """The layer's weight gradient through QATLinearFn equals torch.mm's
-    within bf16 rounding, with the kernel on and off."""
+    """The layer's weight and bias gradients through QATLinearFn, with the
+    kernel on (bias gradient fused into its pass) and off (torch.mm and
+    coset_colsum): dW within bf16 rounding, db within the fp32 sum bound."""
     print("gemm_tn layer weight grad", flush=True)
     torch.manual_seed(7)
     import coset_amd as ca
@@ -146,6 +150,7 @@ def test_layer_weight_grad_matches_torch():
             y = layer(x)
             y.backward(gy)
             grads[on] = layer.weight.grad.clone()
+            grads[(on, "b")] = layer.bias.grad.clone()
         finally:
             layers.set_gemm_tn(True)
     # the straight-through backward passes dW_q through (times the clamp
@@ -156,3 +161,7 @@ def test_layer_weight_grad_matches_torch():
     mag = gy.float().abs().t() @ x.float().abs()
     assert (d <= 2.0 ** -7 * grads[False].abs() + 2.0 ** -16 * mag).all()
     assert (d == 0).float().mean() > 0.5, "most weights should see the same bf16 value"
+    db_ref = gy.double().sum(0)
+    bmag = gy.double().abs().sum(0)
+    for on in (True, False):
+        assert ((grads[(on, "b")].double() - db_ref).abs() <= 2.0 ** -16 * bmag).all()
