@@ -3,9 +3,15 @@
 
 Tolerances are elementwise and relative to the magnitude of the summands
 that make up each value: a table entry <a, r(b)> within 1e-6 of
-sum_j |a_j| |r_j(b)|, a lookup sum or matmul output within 1e-3 (fp32
-accumulate, the north star's bound) of sum_k sum_m q^m |<a_k, r(b_m)>|
-bounded by |a| @ (sum_m q^m |r(b_m)|)^T times the row's scale."""
+sum_j |a_j| |r_j(b)|; a lookup sum or matmul output within RTOL[method] of
+sum_k sum_m q^m |<a_k, r(b_m)>|, bounded by |a| @ (sum_m q^m |r(b_m)|)^T
+times the row's scale.  On the matrix cores every product a x 2 x_hat is
+exact (both exact in the operand type) and only the fp32 sums round; the
+oracle's own sum of fp32 8-term table entries over at most ~1,100 terms
+errs by at most ~1,100 ulp of the magnitude, so 2^-14 holds with margin at
+the tests' sizes (typical errors are ~2^-20).  The LDS-table method rounds
+its pair-table entries once more (2^-12).  The north star's bound, 1e-3,
+is far looser than either."""
 import numpy as np
 import pytest
 import torch
@@ -13,6 +19,9 @@ import torch
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
+
+
+RTOL = {"mfma": 2.0 ** -14, "lds": 2.0 ** -12, "auto": 2.0 ** -12}
 
 
 def close(a, b, mag, tol):
@@ -157,7 +166,7 @@ def test_vlut_matmul_vs_oracle(method, B, adt, mfma_decode):
                     continue
                 out = coset_amd.vlut_matmul(w, a.cuda(), q, scale=torch.from_numpy(scale), scale_mode=mode,
                                             legacy=legacy, method=method).cpu().numpy()
-                close(out, ref, mag, 1e-3)
+                close(out, ref, mag, RTOL[method])
 
 
 @pytest.mark.parametrize("q,M", [(2, 1), (2, 2), (2, 3), (2, 4), (4, 1), (4, 3)])
@@ -185,7 +194,7 @@ def test_vlut_matmul_other_levels(q, M, B, mfma_decode):
                 if not runs(method, w):
                     continue
                 out = coset_amd.vlut_matmul(w, a.cuda(), q, legacy=legacy, method=method).cpu().numpy()
-                close(out, ref, mag, 1e-3)
+                close(out, ref, mag, RTOL[method])
 
 
 @pytest.mark.parametrize("q,M", [(4, 2), (4, 1), (2, 3), (2, 4)])
@@ -193,7 +202,7 @@ def test_vlut_matmul_other_levels(q, M, B, mfma_decode):
 def test_fp32_activations_on_matrix_cores(q, M, B):
     """fp32 activations on the MFMA method: each value split exactly into
     three bf16 planes (3B tokens), the planes' products summed per output;
-    against the oracle's lookup sum (elementwise 1e-3 of the summands'
+    against the oracle's lookup sum (elementwise RTOL of the summands'
     magnitude), every weight format, both rules, with the bias + LSQ epilogue
     applied after the sum, and "auto" taking the same path."""
     import coset_amd
@@ -215,7 +224,7 @@ def test_fp32_activations_on_matrix_cores(q, M, B):
         for w in forms:
             for method in ("mfma", "auto"):
                 out = coset_amd.vlut_matmul(w, a, q, scale=torch.from_numpy(scale), legacy=legacy, method=method)
-                close(out.cpu().numpy(), ref, mag, 1e-3)
+                close(out.cpu().numpy(), ref, mag, RTOL["mfma"])   # "auto" takes the matrix cores here
     # epilogue after the three planes' sum: bias, then the LSQ kernel's quantizer
     sc, bias = torch.from_numpy(scale).cuda(), torch.from_numpy(rng.standard_normal(rows).astype(np.float32)).cuda()
     m = coset_amd.LSQActivation(bit_width=6, init_alpha=3.0).cuda()
@@ -257,7 +266,7 @@ def test_fp32_split_special_values(n_tok):
     assert np.array_equal(np.isfinite(out), fin)
     assert np.isnan(out[3]).all() and not fin[1:5].any() and fin[0].all() and fin[5:].all()
     mag = matmul_mag(words_np, q, M, np.where(np.isfinite(a_np), a_np, 0))
-    close(out[fin], ref[fin], mag[fin], 1e-3)
+    close(out[fin], ref[fin], mag[fin], RTOL["mfma"])
 
 
 def _split3_np(a):
@@ -349,7 +358,7 @@ def test_fp32_mfma_needs_exact_operands():
         coset_amd.vlut_matmul(words, torch.from_numpy(a_np).cuda(), q, method="mfma")
     out = coset_amd.vlut_matmul(words, torch.from_numpy(a_np).cuda(), q, method="auto").cpu().numpy()
     close(out, O.vlut_matmul(words_np, np.ones(rows, np.float32), a_np, q, M),
-          matmul_mag(words_np, q, M, a_np), 1e-3)
+          matmul_mag(words_np, q, M, a_np), RTOL["auto"])
 
 
 @pytest.mark.parametrize("splits", [1, 2, 5, 64])
@@ -372,7 +381,7 @@ def test_vlut_matmul_forced_splits(splits):
     try:
         for method, w in (("lds", words), ("lds", pairs), ("mfma", words)):
             out = coset_amd.vlut_matmul(w, a.cuda(), q, method=method).cpu().numpy()
-            close(out, ref, mag, 1e-3)
+            close(out, ref, mag, RTOL[method])
     finally:
         _lib.set_vlut_splits(0)
 
@@ -403,7 +412,7 @@ def test_rows_kernel_staged_and_direct_activations(B, K, splits):
             mag = matmul_mag(words_np, q, M, a.float().numpy(), scale)
             for w in forms:
                 out = coset_amd.vlut_matmul(w, a.cuda(), q, scale=torch.from_numpy(scale), method="mfma")
-                close(out.cpu().numpy(), ref, mag, 1e-3)
+                close(out.cpu().numpy(), ref, mag, RTOL["mfma"])
     finally:
         _lib.set_vlut_splits(0)
 
@@ -431,7 +440,7 @@ def test_vlut_matmul_ragged_shapes(B, mfma_decode):
                 continue
             out = coset_amd.vlut_matmul(w, a.half().cuda(), q, scale=torch.from_numpy(scale),
                                         method=method).cpu().numpy()
-            close(out, ref, mag, 1e-3)
+            close(out, ref, mag, RTOL[method])
 
 
 @pytest.mark.parametrize("q,M", [(4, 2), (4, 4), (2, 3)])
@@ -458,7 +467,7 @@ def test_pairs_layout(q, M, B):
         for method in ("auto", "lds"):
             out = coset_amd.vlut_matmul(pairs, a.cuda(), q, scale=torch.from_numpy(scale), scale_mode="div",
                                         legacy=legacy, method=method).cpu().numpy()
-            close(out, ref, mag, 1e-3)
+            close(out, ref, mag, RTOL[method])
         with pytest.raises(ValueError):
             coset_amd.vlut_matmul(pairs, a.half().cuda(), q, legacy=legacy, method="mfma")
     # every word's ids name pairs whose values are the word's residual; the
@@ -540,7 +549,7 @@ def test_c4_full_size_equals_decoded_product():
 def test_wide_batch_kernels_vs_oracle(deep, splits, B):
     """Batches above 32 tokens (the deep kernel, or the wide one) with ragged
     rows and K, any forced K split, every weight format: against the
-    oracle's lookup sum, elementwise within 1e-3 of |a| @ |W|^T."""
+    oracle's lookup sum, elementwise within RTOL of |a| @ |W|^T."""
     import coset_amd as ca
     from coset_amd import _lib
     rng = np.random.default_rng(17 * B + splits)
@@ -562,7 +571,7 @@ def test_wide_batch_kernels_vs_oracle(deep, splits, B):
         outs = []
         for w in forms:
             out = ca.vlut_matmul(w, a.cuda(), 4, scale=torch.from_numpy(scale), method="mfma")
-            _close_elem(out.cpu().numpy(), ref, mag)
+            _close_elem(out.cpu().numpy(), ref, mag, RTOL["mfma"])
             outs.append(out)
     finally:
         _lib.set_vlut_splits(0)
@@ -592,7 +601,8 @@ def test_decoded_format_equals_tiled(q, M, dt, B):
     assert torch.equal(y2, y3)
     W = ca.hnlq_decode(words.reshape(-1, M), q, M, None).reshape(rows, K) * scale.view(-1, 1)
     ref = a.float() @ W.t()
-    assert (y3 - ref).abs().max().item() <= 1e-3 * max(1.0, ref.abs().max().item())
+    mag = a.float().abs() @ W.abs().t()
+    assert ((y3 - ref).abs() <= RTOL["mfma"] * mag).all()
 
 
 def _unpack_decoded6(data, rows, kb):
@@ -654,7 +664,7 @@ def test_decoded6_format_holds_the_decode(legacy):
 def test_decoded6_matmul_vs_oracle(q, M, dt, B, splits):
     """Format 5 on the rows (B <= 32) and deep (B > 32) kernels, ragged rows
     and K (partial chunks), natural and forced K splits: elementwise against
-    the oracle's lookup sum within 1e-3 of the summands' magnitude, and within
+    the oracle's lookup sum within RTOL of the summands' magnitude, and within
     2^-16 of it against the 8-byte decoded format (the same exact operands,
     the waves' K ranges aligned to chunks)."""
     import coset_amd as ca
@@ -677,7 +687,7 @@ def test_decoded6_matmul_vs_oracle(q, M, dt, B, splits):
         y8 = ca.vlut_matmul(d8, a.cuda(), q, scale=torch.from_numpy(scale), method="mfma")
     finally:
         _lib.set_vlut_splits(0)
-    _close_elem(y6.cpu().numpy(), ref, mag)
+    _close_elem(y6.cpu().numpy(), ref, mag, RTOL["mfma"])
     _close_elem(y6.cpu().numpy(), y8.cpu().numpy(), mag, 2.0 ** -16)
 
 
