@@ -59,6 +59,39 @@ def test_fast_projection_matches_oracle(checker):
     assert rates[7] < 20.0 and rates5[7] > 90.0, out   # tiny and sparse blocks: (5) decides them
 
 
+def test_condition5_fails_without_its_d8_term(tmp_path):
+    """Negative control of condition (5): with the D8 candidate's adjustment
+    term dropped (2 - sum |d0_i| > 2^-14 alone), the bound no longer holds
+    and the checker must find blocks whose rows differ from the oracle's.
+    The mutated header is a copy built here; the library's is untouched."""
+    if shutil.which("hipcc") is None and not os.path.exists("/opt/rocm/bin/hipcc"):
+        pytest.skip("hipcc not available")
+    src = os.path.join(HERE, "..", "..", "coset_amd", "csrc", "e8_fast.hpp")
+    text = open(src).read()
+    term = "(decided || base - t0 > kFastDistGap)"
+    assert text.count(term) == 1, "condition (5) moved: update this negative control"
+    inc = tmp_path / "inc"
+    inc.mkdir()
+    (inc / "e8_fast.hpp").write_text(text.replace(term, "(decided || base > kFastDistGap)"))
+    for name in os.listdir(os.path.dirname(src)):
+        if name.endswith(".hpp") and name != "e8_fast.hpp":
+            shutil.copy(os.path.join(os.path.dirname(src), name), inc / name)
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    oracle = os.path.join(HERE, "..", "..", "oracle", "e8_oracle.c")
+    exe = tmp_path / "check_mutated"
+    subprocess.run(["gcc", "-O2", "-fPIC", "-std=c99", "-ffp-contract=off", "-fno-fast-math", "-c", "-o",
+                    str(tmp_path / "o.o"), oracle], check=True, capture_output=True)
+    subprocess.run([hipcc, "-O2", "-std=c++17", "-ffp-contract=off", "--offload-arch=gfx950", f"-I{inc}", "-c",
+                    "-o", str(tmp_path / "c.o"), os.path.join(HERE, "check_fastpath.hip")], check=True,
+                   capture_output=True)
+    subprocess.run([hipcc, "--offload-arch=gfx950", "-o", str(exe), str(tmp_path / "c.o"), str(tmp_path / "o.o"),
+                    "-lpthread", "-lm"], check=True, capture_output=True)
+    rc, out = run(str(exe), "blocks", "300000", "11")
+    assert rc == 1, out
+    bad = [l for l in out.splitlines() if l.startswith("family") and not l.endswith("row mismatches 0")]
+    assert len(bad) >= 3, out   # several families hit blocks where the dropped term matters
+
+
 @pytest.mark.parametrize("q,n", [(2, 1 << 20), (4, 1 << 20), (8, 1 << 24), (16, 1000000)])
 def test_dyadic_projection_matches_oracle(checker, q, n):
     """The decoders' exact projection of G b / q for q = 2^k: every code for
