@@ -600,8 +600,10 @@ def median_call_time(torch, fn, reps=25, warm_s=0.1):
 def bench_peaks(torch, ca, args):
     """The spec peaks checked on this GPU: a STREAM-like copy of 1 GiB (four
     times the 256 MB Infinity Cache, so HBM serves it) through the runtime's
-    device copy, and a bf16 8192^3 GEMM through torch.mm (the BLAS library
-    torch is configured with, named in the record)."""
+    device copy, a bf16 8192^3 GEMM through torch.mm (the BLAS library torch
+    is configured with, named in the record), and the sustained VALU issue
+    rate (coset_probe_valu: fp32 FMA and compare + select chains, wave
+    instructions per SIMD per us) the VALU-bound C3 kernel is set against."""
     n = 1 << 28
     src = torch.empty(n, dtype=torch.float32, device="cuda").normal_()
     dst = torch.empty_like(src)
@@ -621,12 +623,27 @@ def bench_peaks(torch, ca, args):
         blas = str(torch.backends.cuda.preferred_blas_library())
     except Exception:   # older torch without the query
         blas = "default"
+    # VALU issue rate: coset_probe_valu's eight independent chains per thread,
+    # 1024 workgroups of 8 waves (8 per SIMD), 2000 iterations
+    from coset_amd import _lib
+    lib = _lib.load()
+    grid, iters = 1024, 2000
+    vout = torch.empty(grid * 512, dtype=torch.float32, device="cuda")
+    valu = {}
+    for kind, name, per_iter in ((0, "fp32_fma", 64), (1, "cmp_select", 128)):
+        fn = lambda: _lib.check("coset_probe_valu", lib.coset_probe_valu(kind, grid, iters, vout.data_ptr(),
+                                                                         _lib.stream_of(vout)))
+        t = median_call_time(torch, fn, reps=9, warm_s=0.05)
+        rate = grid * 8 * iters * per_iter / 1024 / (t * 1e6)
+        valu[name] = {"us": round(t * 1e6, 1), "wave_instr_per_simd_per_us": round(rate, 1)}
+    del vout
     return {"copy": {"bytes": 2 * n * 4, "us": round(t_copy * 1e6, 1), "gbs": round(copy_gbs, 1),
                      "frac_of_spec": round(copy_gbs / HBM_PEAK_GBS, 4),
                      "what": "1 GiB fp32 device-to-device copy (read + write), median of 25"},
             "gemm_bf16": {"shape": [s, s, s], "us": round(t_mm * 1e6, 1), "tflops": round(tflops, 1),
                           "frac_of_spec": round(tflops / BF16_MFMA_TFLOPS, 4), "blas": blas,
                           "what": "torch.mm bf16 8192^3, fp32 accumulation, median of 25"},
+            "valu": valu,
             "spec": {"hbm_gbs": HBM_PEAK_GBS, "bf16_mfma_tflops": BF16_MFMA_TFLOPS}}
 
 
@@ -939,7 +956,8 @@ def summarize(extra):
                             _r(_pick(v, "cpu_baseline", "value"))]
     pk = extra.get("peaks")
     if pk:
-        out["peaks"] = {"copy_gbs": _r(_pick(pk, "copy", "gbs"), 4), "gemm_bf16_tflops": _r(_pick(pk, "gemm_bf16", "tflops"), 4)}
+        out["peaks"] = {"copy_gbs": _r(_pick(pk, "copy", "gbs"), 4), "gemm_bf16_tflops": _r(_pick(pk, "gemm_bf16", "tflops"), 4),
+                        "valu_fma_per_simd_us": _r(_pick(pk, "valu", "fp32_fma", "wave_instr_per_simd_per_us"))}
     return out
 
 

@@ -70,6 +70,7 @@ SIGNATURES = {
     "coset_probe_empty": [_int, _int, _int, _vp, _vp],
     "coset_probe_read": [_vp, _i64, _int, _int, _vp, _vp],
     "coset_probe_c2_stream": [_vp, _i64, _vp, _vp, _int, _vp],
+    "coset_probe_valu": [_int, _int, _int, _vp, _vp],
     "coset_init": [_int],
     "coset_set_option": [_int, _int],
 }

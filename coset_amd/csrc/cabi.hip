@@ -852,6 +852,14 @@ int coset_probe_read(const void* src, int64_t bytes, int grid, int threads, uint
     return check_hip(coset::launch_probe_read(src, bytes, grid, threads, out, (hipStream_t)stream), "probe launch");
 }
 
+int coset_probe_valu(int kind, int grid, int iters, float* out, void* stream)
+{
+    if (kind != 0 && kind != 1) return fail(COSET_EINVAL, "kind must be 0 (fp32 FMA) or 1 (compare + select)");
+    if (grid < 1 || grid > (1 << 20) || iters < 1) return fail(COSET_EINVAL, "grid in [1, 2^20], iters >= 1 required");
+    if (!out) return fail(COSET_EINVAL, "NULL buffer");
+    return check_hip(coset::launch_probe_valu(kind, grid, iters, out, (hipStream_t)stream), "probe launch");
+}
+
 int coset_probe_c2_stream(const float* x, int64_t n_blocks, uint32_t* packed, float* out, int staged, void* stream)
 {
     if (n_blocks < 1) return fail(COSET_EINVAL, "n_blocks must be positive");

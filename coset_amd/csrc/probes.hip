@@ -5,7 +5,10 @@
 //   read:  a stream of `bytes` from HBM into registers, L 16-byte loads per
 //          thread all issued before any is used, one uint32 per workgroup
 //          written (so the loads are live) -- the floor of a kernel that
-//          reads a weight format of that size with that launch shape.
+//          reads a weight format of that size with that launch shape;
+//   valu:  eight independent VALU chains per thread, 8 waves per workgroup
+//          -- the sustained VALU issue rate the arithmetic-bound kernels
+//          (C3) are set against.
 // The C2 streaming probe (the codec kernel's own access pattern) is a
 // variant of that kernel, in hnlq_lut.hip.
 #include <hip/hip_runtime.h>
@@ -42,6 +45,41 @@ __global__ void probe_read_kernel(const uint4* __restrict__ src, int64_t n16, ui
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) x ^= __shfl_xor(x, off, 64);
     if (threadIdx.x == 0) out[blockIdx.x] = x;
+}
+
+// KIND 0: 64 v_fma_f32 per iteration (8 steps x 8 chains), 1: 64 compares
+// and 64 selects; the empty asm keeps each step's eight operations in place
+template <int KIND>
+__global__ void __launch_bounds__(512) probe_valu_kernel(float* out, int iters, float s)
+{
+    const float t0 = (float)threadIdx.x * 1e-3f;
+    float a0 = t0, a1 = t0 + 1.f, a2 = t0 + 2.f, a3 = t0 + 3.f, a4 = t0 + 4.f, a5 = t0 + 5.f, a6 = t0 + 6.f,
+          a7 = t0 + 7.f;
+    for (int i = 0; i < iters; ++i) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (KIND == 0) {
+                a0 = __builtin_fmaf(a0, s, 1.f); a1 = __builtin_fmaf(a1, s, 1.f);
+                a2 = __builtin_fmaf(a2, s, 1.f); a3 = __builtin_fmaf(a3, s, 1.f);
+                a4 = __builtin_fmaf(a4, s, 1.f); a5 = __builtin_fmaf(a5, s, 1.f);
+                a6 = __builtin_fmaf(a6, s, 1.f); a7 = __builtin_fmaf(a7, s, 1.f);
+            } else {
+                a0 = a0 > s ? a1 : a2; a1 = a1 > s ? a2 : a3; a2 = a2 > s ? a3 : a4; a3 = a3 > s ? a4 : a5;
+                a4 = a4 > s ? a5 : a6; a5 = a5 > s ? a6 : a7; a6 = a6 > s ? a7 : a0; a7 = a7 > s ? a0 : a1;
+            }
+            __asm__ volatile("" ::: "memory");
+        }
+    }
+    out[(int64_t)blockIdx.x * blockDim.x + threadIdx.x] = a0 + a1 + a2 + a3 + a4 + a5 + a6 + a7;
+}
+
+hipError_t launch_probe_valu(int kind, int grid, int iters, float* out, hipStream_t s)
+{
+    if (kind == 0)
+        hipLaunchKernelGGL(probe_valu_kernel<0>, dim3(grid), dim3(512), 0, s, out, iters, 0.999f);
+    else
+        hipLaunchKernelGGL(probe_valu_kernel<1>, dim3(grid), dim3(512), 0, s, out, iters, 0.999f);
+    return hipGetLastError();
 }
 
 hipError_t launch_probe_empty(int grid, int threads, int lds_bytes, uint32_t* out, hipStream_t s)

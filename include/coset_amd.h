@@ -336,10 +336,17 @@ int coset_vlut_matmul_noalloc(const void* words, int word_format, const float* s
  *     at q = 4, M = 2, fp32, no scale) with its launch, tile schedule, loads
  *     and stores but no lattice arithmetic: out = x, packed[i] = the XOR of
  *     block i's eight words (staged != 0: with its decode-table staging) --
- *     the streaming ceiling of that access pattern. */
+ *     the streaming ceiling of that access pattern.
+ *   coset_probe_valu: `grid` 512-thread workgroups whose waves each run
+ *     `iters` x 8 steps of eight independent VALU chains -- kind 0 fp32 FMA
+ *     (64 v_fma_f32 per iteration), 1 compare + select (64 v_cmp_lt_f32 and
+ *     64 v_cndmask_b32) -- and write one float per thread to out[grid * 512]:
+ *     the sustained VALU issue rate of this part (wave instructions per SIMD
+ *     per second = waves x instructions per wave / SIMDs / time). */
 int coset_probe_empty(int grid, int threads, int lds_bytes, uint32_t* out, void* stream);
 int coset_probe_read(const void* src, int64_t bytes, int grid, int threads, uint32_t* out, void* stream);
 int coset_probe_c2_stream(const float* x, int64_t n_blocks, uint32_t* packed, float* out, int staged, void* stream);
+int coset_probe_valu(int kind, int grid, int iters, float* out, void* stream);
 
 /* D4 lattice operator over n_blocks fp32 [n, 4] blocks (coset/core/d4/lattice.py:62-146,
  * coset/core/base.py:134-176): COSET_OP_G_X, COSET_OP_PROJECT (closest point,
