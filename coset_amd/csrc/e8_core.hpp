@@ -275,6 +275,36 @@ __device__ __forceinline__ void residual_from_point(const float gb[8], float qf,
     for (int i = 0; i < 8; ++i) r[i] = __fsub_rn(gb[i], __fmul_rn(qf, c[i]));
 }
 
+// One level's core-rule residual from its digits: residual_dyadic for
+// q = 8, 16, 32 (the same values in fewer operations), else the lattice
+// point and residual_from_point.
+template <bool STRIDED, int Q>
+__device__ __forceinline__ void level_residual(const int b[8], float qf, float r[8])
+{
+    if constexpr (Q == 8 || Q == 16 || Q == 32) {
+        residual_dyadic<Q>(b, r);
+    } else {
+        float gb[8];
+        lattice_point(b, gb);
+        residual_from_point<false, STRIDED, Q>(gb, qf, r);
+    }
+}
+
+// acc += w r for one level.  With q = 2^k, w = q^m and r a half-integer of
+// the residual's range, w r is exact, so one fused operation rounds the sum
+// as the reference's multiply and add do; other q keep the two operations.
+template <int Q>
+__device__ __forceinline__ void add_level(float acc[8], float w, const float r[8])
+{
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        if constexpr (Q > 0 && (Q & (Q - 1)) == 0)
+            acc[j] = __fmaf_rn(w, r[j], acc[j]);
+        else
+            acc[j] = __fadd_rn(acc[j], __fmul_rn(w, r[j]));
+    }
+}
+
 __device__ __forceinline__ float bf16_to_f32(uint16_t h)
 {
     return __uint_as_float(((uint32_t)h) << 16);

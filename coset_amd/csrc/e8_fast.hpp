@@ -292,4 +292,113 @@ __host__ __device__ inline void project_dyadic(const float x[8], float y[8])
     }
 }
 
+// The decoders' residual of one level, r = G b - q P(G b / q)
+// (coset/core/e8/codecs.py:164-166, core rule), for q = 8, 16, 32 straight
+// from the digits b_j in [0, q), in fewer operations than project_dyadic.
+//
+// z = G b / q = Z / (2q) with Z = 2 G b an integer: Z_0 = 4 b_0 - 2 b_1 + b_7,
+// Z_i = 2 (b_i - b_i+1) + b_7 (i = 1..5), Z_6 = 2 b_6 + b_7, Z_7 = b_7, so
+// -2q < Z_i < 5q and -1 < z_i < 5/2.  On this grid (steps of 1/(2q)):
+//  - custom_round's ties are z in {-1/2, 1/2, 3/2} for the D8 candidate and
+//    z - 1/2 in {-1/2, 1/2, 3/2} for D8 + 1/2, all of magnitude below 2,
+//    where it rounds toward zero (its 2^-23 nudge is exact there); so the D8
+//    candidate is f0 = trunc(z + copysign(1/2 - 1/(4q), z)) and the D8 + 1/2
+//    candidate's integer part is f1 = floor(z) but z - 1 for the integers
+//    z >= 1, i.e. floor(z - 1/(4q)) for z > 0 and floor(z + 1/(4q)) for z <= 0;
+//  - with d0 = z - f0 in [-1/2, 1/2] and d1 = z - 1/2 - f1, |d1_i| =
+//    1/2 - |d0_i| exactly, so the first argmax of |d1| (torch.argmax) is the
+//    first argmin of |d0|, and the squared distances of the two adjusted
+//    candidates differ by b - a = 2 - sum |d0_i| + corr1 - corr0 with
+//    corr = (d_k - adj)^2 - d_k^2 = |adj| - 2 adj d_k (d_k the worst
+//    coordinate's difference, adj the core g_x step).
+// Every value is a small multiple of 1/(2q): sums, products and the
+// comparison are exact in fp32, which makes the reference's comparison of
+// correctly rounded norms the exact test b - a > 0 (ties to D8 + 1/2), under
+// both of its distance rules.  The argmax, the g_x step and the tie rules are
+// the reference's, as in project_dyadic; the CPU checker compares r with the
+// oracle's for every code at q = 8 and q = 16 (all 2^32) and a sample at 32.
+template <int Q>
+__host__ __device__ inline void residual_dyadic(const int b[8], float r[8])
+{
+    static_assert(Q == 8 || Q == 16 || Q == 32, "the grid bounds above are those of q = 8, 16, 32");
+    constexpr float kInv = 1.f / (float)(2 * Q);          // z = Z kInv, exact
+    constexpr float kRound = 0.5f - 1.f / (float)(4 * Q); // toward zero on ties, nearest elsewhere
+    constexpr float kNudge = 1.f / (float)(4 * Q);        // below the grid step
+    // nz = -Z in fp32: Z = 0 converts to +0, so copysignf(c, nz) takes the
+    // sign of -Z and of z <= 0 for zero, as the rules above need
+    float nz[8];
+    int nb7 = -b[7];
+#if defined(__HIP_DEVICE_COMPILE__)
+    asm volatile("" : "+v"(nb7));  // each coordinate is then one shift-and-add after the difference
+#endif
+    nz[0] = (float)(((b[1] - 2 * b[0]) << 1) + nb7);
+#pragma unroll
+    for (int i = 1; i < 6; ++i) nz[i] = (float)(((b[i + 1] - b[i]) << 1) + nb7);
+    nz[6] = (float)(b[6] * -2 + nb7);
+    nz[7] = (float)nb7;
+
+    // g0 = -f0 = trunc(-z + copysign(1/2 - 1/(4q), -z)) (trunc is odd), so
+    // no negated copysign is needed; the parity of sum f0 is that of sum g0
+    float g0[8], f1[8], d0[8];
+    float s0, s1, sa, best, least;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        g0[i] = truncf(fmaf(nz[i], kInv, copysignf(kRound, nz[i])));
+        d0[i] = fmaf(nz[i], -kInv, g0[i]);
+        f1[i] = floorf(fmaf(nz[i], -kInv, copysignf(kNudge, nz[i])));
+        const float ad = fabsf(d0[i]);
+        s0 = i == 0 ? g0[0] : s0 + g0[i];
+        s1 = i == 0 ? f1[0] : s1 + f1[i];
+        sa = i == 0 ? ad : sa + ad;
+        best = i == 0 ? ad : fmaxf(best, ad);
+        least = i == 0 ? ad : fminf(least, ad);
+    }
+    // first index of the largest |d0| (D8) and of the smallest (D8 + 1/2),
+    // and -Z at each
+    lanes_t first0[8], first1[8], seen0 = 0ull, seen1 = 0ull;
+    float nk0 = nz[0], nk1 = nz[0];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float ad = fabsf(d0[i]);
+        const lanes_t h0 = lanes_of(ad == best), h1 = lanes_of(ad == least);
+        first0[i] = h0 & ~seen0;
+        first1[i] = h1 & ~seen1;
+        seen0 |= h0;
+        seen1 |= h1;
+        nk0 = lane_in(first0[i]) ? nz[i] : nk0;
+        nk1 = lane_in(first1[i]) ? nz[i] : nk1;
+    }
+    // the worst coordinates' differences, recomputed from z_k (same operations)
+    const float dk0 = fmaf(nk0, -kInv, truncf(fmaf(nk0, kInv, copysignf(kRound, nk0))));
+    const float tk1 = fmaf(nk1, -kInv, -0.5f);
+    const float dk1 = tk1 - floorf(fmaf(nk1, -kInv, copysignf(kNudge, nk1)));
+    // core g_x: an odd sum moves the worst coordinate by +1 when t_k >= 0 and
+    // d_k > 0 (t = z for D8, z - 1/2 for D8 + 1/2), by -1 otherwise
+    const bool odd0 = ((int)s0 & 1) != 0, odd1 = ((int)s1 & 1) != 0;
+    const float adj0 = odd0 ? ((nk0 <= 0.f && dk0 > 0.f) ? 1.f : -1.f) : 0.f;
+    const float adj1 = odd1 ? ((tk1 >= 0.f && dk1 > 0.f) ? 1.f : -1.f) : 0.f;
+    const float diff = (2.f - sa) + (fmaf(-2.f * adj1, dk1, fabsf(adj1)) - fmaf(-2.f * adj0, dk0, fabsf(adj0)));
+    const bool pick0 = diff > 0.f;  // a < b; ties go to D8 + 1/2
+    const lanes_t p0 = lanes_of(pick0);
+    // r = G b - q y with y = f0 (+ adj0 at k0) or f1 + 1/2 (+ adj1 at k1):
+    // r_i = (-nz_i / 2 + c_i) + q g0_i or (...) - q f1_i, c_i = -q (1/2 if
+    // D8 + 1/2) - q adj at the moved coordinate; every term and partial sum
+    // is exact, and -nz_i / 2 + c_i is +0 (not -0) where it is zero, as the
+    // reference's G b - q c is
+    const float c_off = pick0 ? 0.f : -0.5f * (float)Q;
+    float c_at = c_off - (float)Q * (pick0 ? adj0 : adj1);
+#if defined(__HIP_DEVICE_COMPILE__)
+    // keep c_at a value of its own, so that each coordinate selects between
+    // two registers (one operation) rather than subtracting a selected term
+    asm volatile("" : "+v"(c_at));
+#endif
+    const float qs = pick0 ? (float)Q : -(float)Q;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const lanes_t at = (p0 & first0[i]) | (~p0 & first1[i]);
+        const float g = fmaf(nz[i], -0.5f, lane_in(at) ? c_at : c_off);
+        r[i] = fmaf(qs, pick0 ? g0[i] : f1[i], g);
+    }
+}
+
 }  // namespace coset

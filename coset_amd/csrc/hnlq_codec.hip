@@ -215,16 +215,15 @@ __global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
                     two_r_tables<Q>(word, a.dec_map, a.dec_coarse, r2);
 #pragma unroll
                     for (int j = 0; j < 8; ++j) r[j] = 0.5f * (float)r2[j];
+                } else if constexpr (Q == 8 || Q == 16 || Q == 32) {
+                    residual_dyadic<Q>(b, r);  // both distance rules agree on this grid
                 } else {
-                    float gb[8];
-                    lattice_point(b, gb);
                     if (a.strided)
-                        residual_from_point<false, true, Q>(gb, qf, r);
+                        level_residual<true, Q>(b, qf, r);
                     else
-                        residual_from_point<false, false, Q>(gb, qf, r);
+                        level_residual<false, Q>(b, qf, r);
                 }
-#pragma unroll
-                for (int j = 0; j < 8; ++j) acc[j] = __fadd_rn(acc[j], __fmul_rn(w, r[j]));
+                add_level<Q>(acc, w, r);
                 w = __fmul_rn(w, qf);
             }
 #pragma unroll
@@ -256,14 +255,19 @@ __global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
                 }
                 int b[8];
                 unpack_word<Q>(word, q, b);
+                if constexpr (Q == 8 || Q == 16 || Q == 32) {
+                    residual_dyadic<Q>(b, r);
+                    add_level<Q>(acc, w, r);
+                    w = __fmul_rn(w, qf);
+                    continue;
+                }
                 lattice_point(b, gb);
             }
             if (a.strided)
                 residual_from_point<false, true, Q>(gb, qf, r);
             else
                 residual_from_point<false, false, Q>(gb, qf, r);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) acc[j] = __fadd_rn(acc[j], __fmul_rn(w, r[j]));
+            add_level<Q>(acc, w, r);
             w = __fmul_rn(w, qf);
         }
     }

@@ -83,15 +83,13 @@ __device__ __forceinline__ void decode_q(const QatBwdArgs& a, int64_t blk, float
             uint32_t w = word_bytes(q) == 2 ? reinterpret_cast<const uint16_t*>(a.packed)[blk * a.M + m]
                                             : reinterpret_cast<const uint32_t*>(a.packed)[blk * a.M + m];
             int b[8];
-            float gb[8], r[8];
+            float r[8];
             unpack_word<Q>(w, q, b);
-            lattice_point(b, gb);
-            if (a.strided)
-                residual_from_point<false, true, Q>(gb, qf, r);
+            if (Q == 8 || Q == 16 || Q == 32 || !a.strided)  // both rules agree on the dyadic grid
+                level_residual<false, Q>(b, qf, r);
             else
-                residual_from_point<false, false, Q>(gb, qf, r);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) acc[j] = __fadd_rn(acc[j], __fmul_rn(wf, r[j]));
+                level_residual<true, Q>(b, qf, r);
+            add_level<Q>(acc, wf, r);
             wf = __fmul_rn(wf, qf);
         }
 #pragma unroll

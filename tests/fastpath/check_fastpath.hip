@@ -19,6 +19,11 @@
 //                                   code for q^8 <= N, else N random codes
 //                                   plus every code with digits in
 //                                   {0, 1, q/2 - 1, q/2, q - 1}
+//   check_fastpath fastres q N [T]  the same residual through
+//                                   residual_dyadic<q> (q = 8, 16, 32) on T
+//                                   threads: every code for q^8 <= N (all
+//                                   2^32 at q = 16 with N = 4294967296),
+//                                   else the structured codes and N random
 #include <math.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -249,6 +254,93 @@ static int residual_check(const int32_t b[8], int q, long* bad)
     return 0;
 }
 
+// residual_dyadic<Q> (the decoders' fast residual straight from the digits)
+// against the oracle under both distance rules, bit for bit
+template <int Q>
+static long fast_residual_check(const int32_t b[8], long* shown)
+{
+    float r[8], ref0[8], ref1[8];
+    int bi[8];
+    for (int i = 0; i < 8; ++i) bi[i] = b[i];
+    coset::residual_dyadic<Q>(bi, r);
+    or_residual(b, Q, 0, 0, ref0);
+    or_residual(b, Q, 0, 1, ref1);
+    if (memcmp(r, ref0, sizeof r) == 0 && memcmp(r, ref1, sizeof r) == 0) return 0;
+    if (*shown < 5) {
+        ++*shown;
+        printf("mismatch q=%d b=", Q);
+        for (int i = 0; i < 8; ++i) printf("%d ", b[i]);
+        printf(" r=");
+        for (int i = 0; i < 8; ++i) printf("%g ", r[i]);
+        printf(" ref=");
+        for (int i = 0; i < 8; ++i) printf("%g ", ref0[i]);
+        printf("\n");
+    }
+    return 1;
+}
+
+// every code for q^8 <= n (threads over the leading digit pairs), else the
+// 5^8 structured codes and n random ones
+template <int Q>
+static int fast_residual(long n, int threads)
+{
+    long total = 1;
+    for (int i = 0; i < 8; ++i) total *= Q;
+    std::atomic<long> bad{0}, checked{0}, shown{0};
+    if (total <= n) {
+        std::atomic<int> next{0};
+        auto work = [&]() {
+            long my_bad = 0, my_checked = 0, my_shown = 0;
+            for (;;) {
+                const int hi = next.fetch_add(1);
+                if (hi >= Q * Q) break;
+                int32_t b[8];
+                b[0] = hi / Q;
+                b[1] = hi % Q;
+                long rest = total / (Q * Q);
+                for (long idx = 0; idx < rest; ++idx) {
+                    long v = idx;
+                    for (int j = 7; j >= 2; --j) {
+                        b[j] = (int32_t)(v % Q);
+                        v /= Q;
+                    }
+                    my_bad += fast_residual_check<Q>(b, &my_shown);
+                }
+                my_checked += rest;
+            }
+            bad += my_bad;
+            checked += my_checked;
+            shown += my_shown;
+        };
+        std::vector<std::thread> pool;
+        for (int t = 0; t < threads; ++t) pool.emplace_back(work);
+        for (auto& t : pool) t.join();
+    } else {
+        long my_shown = 0, b_ = 0, c_ = 0;
+        int32_t b[8];
+        const int pick[5] = {0, 1, Q / 2 - 1, Q / 2, Q - 1};
+        for (long idx = 0; idx < 390625; ++idx) {  // 5^8
+            long v = idx;
+            for (int j = 7; j >= 0; --j) {
+                b[j] = pick[v % 5];
+                v /= 5;
+            }
+            b_ += fast_residual_check<Q>(b, &my_shown);
+            ++c_;
+        }
+        std::mt19937_64 g(4321 + Q);
+        for (long it = 0; it < n; ++it) {
+            for (int j = 0; j < 8; ++j) b[j] = (int32_t)(g() % (uint64_t)Q);
+            b_ += fast_residual_check<Q>(b, &my_shown);
+            ++c_;
+        }
+        bad += b_;
+        checked += c_;
+    }
+    printf("fast residual q=%d: %ld codes, mismatches %ld\n", Q, checked.load(), bad.load());
+    return bad ? 1 : 0;
+}
+
 static int dyadic(int q, long n)
 {
     long total = 1, bad = 0, checked = 0;
@@ -289,9 +381,19 @@ static int dyadic(int q, long n)
 int main(int argc, char** argv)
 {
     if (argc >= 4 && !strcmp(argv[1], "dyadic")) return dyadic(atoi(argv[2]), atol(argv[3]));
+    if (argc >= 4 && !strcmp(argv[1], "fastres")) {
+        const int q = atoi(argv[2]);
+        const long n = atol(argv[3]);
+        const int th = argc >= 5 ? atoi(argv[4]) : 1;
+        if (q == 8) return fast_residual<8>(n, th);
+        if (q == 16) return fast_residual<16>(n, th);
+        if (q == 32) return fast_residual<32>(n, th);
+        fprintf(stderr, "fastres: q must be 8, 16 or 32\n");
+        return 2;
+    }
     // an optional second argument replaces the tie limit (a looser one must fail)
     if (argc >= 2 && !strcmp(argv[1], "lemma")) return lemma(argc >= 3 ? strtof(argv[2], nullptr) : coset::kFastTieLimit);
     if (argc >= 4 && !strcmp(argv[1], "blocks")) return blocks(atol(argv[2]), (unsigned)atoi(argv[3]));
-    fprintf(stderr, "usage: %s lemma [limit] | blocks N seed | dyadic q N\n", argv[0]);
+    fprintf(stderr, "usage: %s lemma [limit] | blocks N seed | dyadic q N | fastres q N [threads]\n", argv[0]);
     return 2;
 }

@@ -1,5 +1,6 @@
 """CPU checks of the fast projections (coset_amd/csrc/e8_fast.hpp): the
-encoder's project_fast and the decoders' project_dyadic.
+encoder's project_fast, the decoders' project_dyadic and their short
+residual residual_dyadic (with a negative control that must fail).
 
 The header is compiled for the host (tests/fastpath/Makefile) and checked
 against the C oracle's projection: exhaustively for the rounding lemma it
@@ -100,3 +101,46 @@ def test_dyadic_projection_matches_oracle(checker, q, n):
     rc, out = run(checker, "dyadic", str(q), str(n))
     assert rc == 0, out
     assert " mismatches 0" in out, out
+
+
+@pytest.mark.parametrize("q,n", [(8, 1 << 24), (16, 1 << 21), (32, 1 << 20)])
+def test_fast_residual_matches_oracle(checker, q, n):
+    """The decoders' short residual residual_dyadic<q> (straight from the
+    digits, |d1| = 1/2 - |d0|, b - a = 2 - sum |d0| + corrections): every
+    code at q = 8, the structured codes and a random sample at q = 16 and
+    32, bit for bit against the oracle's residual under both distance rules.
+    (Every one of the 2^32 codes at q = 16 is checked by
+    `check_fastpath fastres 16 4294967296 <threads>`, about ten minutes on
+    eight cores.)"""
+    rc, out = run(checker, "fastres", str(q), str(n), str(min(8, os.cpu_count() or 1)))
+    assert rc == 0, out
+    assert " mismatches 0" in out, out
+
+
+def test_fast_residual_fails_without_its_integer_tie_rule(tmp_path):
+    """Negative control of residual_dyadic: without the nudge that sends the
+    D8 + 1/2 candidate of a positive integer z to z - 1 (custom_round's tie
+    toward zero at z - 1/2), the checker must report mismatches.  The
+    mutated header is a copy built here; the library's is untouched."""
+    if shutil.which("hipcc") is None and not os.path.exists("/opt/rocm/bin/hipcc"):
+        pytest.skip("hipcc not available")
+    src = os.path.join(HERE, "..", "..", "coset_amd", "csrc", "e8_fast.hpp")
+    text = open(src).read()
+    term = "constexpr float kNudge = 1.f / (float)(4 * Q);"
+    assert text.count(term) == 1, "residual_dyadic's nudge moved: update this negative control"
+    inc = tmp_path / "inc"
+    inc.mkdir()
+    (inc / "e8_fast.hpp").write_text(text.replace(term, "constexpr float kNudge = 0.f;"))
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    oracle = os.path.join(HERE, "..", "..", "oracle", "e8_oracle.c")
+    exe = tmp_path / "check_mutated"
+    subprocess.run(["gcc", "-O2", "-fPIC", "-std=c99", "-ffp-contract=off", "-fno-fast-math", "-c", "-o",
+                    str(tmp_path / "o.o"), oracle], check=True, capture_output=True)
+    subprocess.run([hipcc, "-O2", "-std=c++17", "-ffp-contract=off", "--offload-arch=gfx950", f"-I{inc}", "-c",
+                    "-o", str(tmp_path / "c.o"), os.path.join(HERE, "check_fastpath.hip")], check=True,
+                   capture_output=True)
+    subprocess.run([hipcc, "--offload-arch=gfx950", "-o", str(exe), str(tmp_path / "c.o"), str(tmp_path / "o.o"),
+                    "-lpthread", "-lm"], check=True, capture_output=True)
+    rc, out = run(str(exe), "fastres", "8", str(1 << 24), "4")
+    assert rc == 1, out
+    assert " mismatches 0" not in out, out

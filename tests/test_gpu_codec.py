@@ -114,6 +114,34 @@ def test_q16_decode_sample(ca, golden):
     cfg = ca.LatticeConfig(lattice_type="E8", q=16, M=1)
     r = ca.e8_decode(dev(R["b_q16"].astype(np.float32).reshape(-1, 1, 8)), cfg)
     np.testing.assert_array_equal(host(r), R["r_q16"])
+    # the same codes as packed words go through the short dyadic residual
+    w = torch.from_numpy(O.pack_words(R["b_q16"].astype(np.int64).reshape(-1, 1, 8), 16).astype(np.int64))
+    rw = ca.hnlq_decode(w.to(ca.word_dtype(16)).cuda().reshape(-1, 1), 16, 1, 1.0)
+    np.testing.assert_array_equal(host(rw), R["r_q16"])
+
+
+@pytest.mark.parametrize("q,n", [(8, 8 ** 8), (16, 1 << 22)])
+def test_dyadic_residual_word_decode(ca, q, n):
+    """Packed-word decodes at q = 8, 16 take the short dyadic residual
+    (residual_dyadic: the CPU checker compares it with the oracle for every
+    code at q = 8 and 16); here on the GPU: every q = 8 code and 2^22 random
+    q = 16 codes, decoded from packed words, equal the decode of the same
+    digits given as float codes (the exact projection path), and a sample
+    equals the oracle, over two levels with beta = 0.5."""
+    g = torch.Generator(device="cuda").manual_seed(q)
+    if q == 8:
+        words = torch.arange(n, device="cuda", dtype=torch.int64)
+    else:
+        words = torch.randint(0, 1 << 32, (n,), device="cuda", generator=g, dtype=torch.int64)
+    w2 = torch.stack([words, words.flip(0)], 1)                       # two levels per block
+    digits = torch.stack([(w2 >> (4 * (7 - j) if q == 16 else 3 * (7 - j))) & (q - 1) for j in range(8)], -1)
+    out_w = ca.hnlq_decode(w2.to(ca.word_dtype(q)), q, 2, 0.5)
+    cfg = ca.LatticeConfig(lattice_type="E8", q=q, M=2, beta=0.5)
+    out_f = ca.e8_decode(digits.float(), cfg)
+    assert torch.equal(out_w.reshape(-1, 8), out_f.reshape(-1, 8))
+    sel = torch.randint(0, n, (20000,), device="cuda", generator=g)
+    want = O.e8_decode(host(digits[sel]).astype(np.int64), q, 2, beta=0.5)
+    np.testing.assert_array_equal(host(out_w.reshape(-1, 8)[sel]), want.reshape(-1, 8))
 
 
 @pytest.mark.parametrize("n", [0, 1, 2, 255, 257, 1000])
