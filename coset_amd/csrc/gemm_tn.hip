@@ -39,7 +39,6 @@ namespace coset {
 namespace {
 
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
-typedef short s16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8_gt __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
@@ -97,14 +96,50 @@ __device__ __forceinline__ void store8(void* C, int64_t idx, const float v[8])
     }
 }
 
+// Column sums of one 64-column block of A over one split's K range (kRows
+// tokens from k0), for the workgroups past the tiles: thread t sums column
+// chunk t % 8 (8 columns, one 16-byte load per token) over the tokens
+// t / 8, t / 8 + 64, ... in order, 8 loads in flight; then the 64 row groups'
+// sums of each column are added in group order.  Deterministic; fp32.
+template <int MY>
+__device__ __forceinline__ void tn_colsum_block(const uint16_t* __restrict__ A, int64_t lda, int64_t m0, int64_t k0,
+                                                float* __restrict__ out, char* lds)
+{
+    constexpr int kRows = kTnWaves * MY * kTnSlice;
+    constexpr int kIter = kRows / 64;
+    const int tid = threadIdx.x, c = tid & 7, rg = tid >> 3;
+    const uint16_t* p = A + (k0 + rg) * lda + m0 + 8 * c;
+    float s[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) s[q] = 0.f;
+#pragma unroll 8
+    for (int it = 0; it < kIter; ++it) {
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(p + (int64_t)it * 64 * lda);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            s[2 * q] += __uint_as_float(v[q] << 16);
+            s[2 * q + 1] += __uint_as_float(v[q] & 0xffff0000u);
+        }
+    }
+    float* red = reinterpret_cast<float*>(lds);   // [64 row groups][64 columns]
+#pragma unroll
+    for (int q = 0; q < 8; ++q) red[rg * kTnTile + 8 * c + q] = s[q];
+    __syncthreads();
+    if (tid < kTnTile) {
+        float v = red[tid];
+        for (int grp = 1; grp < 64; ++grp) v += red[grp * kTnTile + tid];
+        out[m0 + tid] = v;
+    }
+}
+
 // OUT: 0 fp32 C, 1 bf16 C (one K split, C with leading dimension ldc), 2 the
 // fp32 partial tile of split blockIdx.y at C + blockIdx.y * M * ldc.  MY: the
 // 32-token slices of each wave (the split's K range is kTnWaves * MY * 32).
 // CS: also the column sums of A, colsum[m] = sum_k A[k, m] (the bias
-// gradient when A is the output gradient), by one workgroup per tile row (tn
-// == tm % tiles_n) with four more MFMAs per slice against an all-ones
-// operand; fp32 to colsum (one split) or split blockIdx.y's partial to
-// colsum + blockIdx.y * M.
+// gradient when A is the output gradient), by M / 64 more workgroups past the
+// tiles, one per 64-column block and split (tn_colsum_block); they run beside
+// the tiles on CUs the tiles leave free.  fp32 to colsum (one split) or split
+// blockIdx.y's partial to colsum + blockIdx.y * M.
 template <int OUT, int MY, bool CS>
 __global__ void __launch_bounds__(kTnWaves * 64) gemm_tn_kernel(const uint16_t* __restrict__ A, int64_t lda,
                                                                 const uint16_t* __restrict__ B, int64_t ldb,
@@ -117,6 +152,14 @@ __global__ void __launch_bounds__(kTnWaves * 64) gemm_tn_kernel(const uint16_t* 
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, r = lane & 15;
 
+    if (CS && (int64_t)blockIdx.x >= (M / kTnTile) * tiles_n) {
+        const int64_t cb = (int64_t)blockIdx.x - (M / kTnTile) * tiles_n;
+        // past the blocks: padding that keeps the grid a multiple of 8
+        if (cb < M / kTnTile)
+            tn_colsum_block<MY>(A, lda, cb * kTnTile, (int64_t)blockIdx.y * kTnWaves * MY * kTnSlice,
+                                colsum + (OUT == 2 ? (int64_t)blockIdx.y * M : 0), lds);
+        return;
+    }
     int tm, tn;
     if (xcd_m > 0) {
         // workgroup b runs on XCD b % 8 (tiles % 8 == 0, so every split's
@@ -131,7 +174,6 @@ __global__ void __launch_bounds__(kTnWaves * 64) gemm_tn_kernel(const uint16_t* 
         tn = blockIdx.x % tiles_n;
     }
     const int64_t m0 = (int64_t)tm * kTnTile, n0 = (int64_t)tn * kTnTile;
-    const bool do_cs = CS && tn == tm % tiles_n;   // uniform
     // this wave's slices: k = (blockIdx.y * kTnWaves * MY + wave + i * kTnWaves) * 32, i < MY
     const int64_t k_wave = ((int64_t)blockIdx.y * kTnWaves * MY + wave) * kTnSlice;
 
@@ -158,14 +200,11 @@ __global__ void __launch_bounds__(kTnWaves * 64) gemm_tn_kernel(const uint16_t* 
         }
     };
 
-    f32x4_t acc[kTnMt][kTnMt], acs[kTnMt];
+    f32x4_t acc[kTnMt][kTnMt];
 #pragma unroll
-    for (int i = 0; i < kTnMt; ++i) {
-        acs[i] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < kTnMt; ++i)
 #pragma unroll
         for (int j = 0; j < kTnMt; ++j) acc[i][j] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-    }
-    const bf16x8_gt ones = __builtin_bit_cast(bf16x8_gt, (s16x8_t)(short)0x3f80);   // eight bf16 1.0
 
     // two transposing reads per operand tile: rows (tokens) 8 g + r / 4 and 4
     // more, columns 16 i + 4 (r % 4)
@@ -184,7 +223,6 @@ __global__ void __launch_bounds__(kTnWaves * 64) gemm_tn_kernel(const uint16_t* 
         for (int i = 0; i < kTnMt; ++i) {
             const bf16x8_gt av =
                 __builtin_bit_cast(bf16x8_gt, __builtin_shufflevector(a[i][0], a[i][1], 0, 1, 2, 3, 4, 5, 6, 7));
-            if (do_cs) acs[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, ones, acs[i], 0, 0, 0);
 #pragma unroll
             for (int j = 0; j < kTnMt; ++j) {
                 const bf16x8_gt bv =
@@ -241,23 +279,6 @@ __global__ void __launch_bounds__(kTnWaves * 64) gemm_tn_kernel(const uint16_t* 
         }
         __syncthreads();
     }
-    if (do_cs) {
-        // D[row 4 g + e][every column] = that row's sum over the wave's tokens:
-        // lanes of column 0 hand them to LDS, then the waves' sums in wave order
-        if (r == 0) {
-#pragma unroll
-            for (int i = 0; i < kTnMt; ++i)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) red[wave * kTnTile + 16 * i + 4 * g + e] = acs[i][e];
-        }
-        __syncthreads();
-        if (tid < kTnTile) {
-            float v = red[tid];
-#pragma unroll
-            for (int w = 1; w < kTnWaves; ++w) v += red[w * kTnTile + tid];
-            colsum[(OUT == 2 ? (int64_t)blockIdx.y * M : 0) + m0 + tid] = v;
-        }
-    }
 }
 
 // C = sum over splits of the fp32 partials [splits, M, N], in split order;
@@ -299,7 +320,10 @@ hipError_t launch_tn(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t 
                      hipStream_t s)
 {
     const int tiles_n = (int)(N / kTnTile);
-    const dim3 grid((unsigned)((M / kTnTile) * tiles_n), (unsigned)plan.splits);
+    // the column-sum workgroups, padded to a multiple of 8 so that every
+    // split's tiles keep their XCDs
+    const int64_t cs_wg = CS ? (M / kTnTile + 7) / 8 * 8 : 0;
+    const dim3 grid((unsigned)((M / kTnTile) * tiles_n + cs_wg), (unsigned)plan.splits);
     const dim3 block(kTnWaves * 64);
     if (plan.splits == 1) {
         if (out_bf16)

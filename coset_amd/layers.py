@@ -331,12 +331,11 @@ def colsum(g2: torch.Tensor) -> torch.Tensor:
 # dtypes allow it (coset_gemm_tn_supported, bf16), 0: always on torch.mm
 # (hipBLASLt)
 _GEMM_TN = [1]
-# 1: where coset_gemm_tn runs the weight gradient of a step on one stream
-# (eager), the bias gradient's column sums come from the same pass, one launch
-# fewer; 0: from coset_colsum.  A step that forks its backward over two
-# streams (CapturedQATStep) keeps coset_colsum beside dX on the second
-# stream: fused into dW the sums lengthened the 768x768 graph step (4096
-# tokens) from 59.2 to 63.7 us
+# 1: where coset_gemm_tn runs the weight gradient of a step, the bias
+# gradient's column sums come from the same launch (workgroups of their own
+# beside the product's tiles), so a step that forks its backward over two
+# streams (CapturedQATStep) leaves only dX on the second stream; 0: from
+# coset_colsum (beside dX on the second stream, or after dW on one stream)
 _FUSE_BIAS_GRAD = [1]
 
 
@@ -443,30 +442,33 @@ class QATLinearFn(torch.autograd.Function):
         overlap = g2.is_cuda and (_OVERLAP_BACKWARD[0] > 0 or torch.cuda.is_current_stream_capturing())
         x2 = x.reshape(-1, x.shape[-1])
         if overlap and need_dw and (need_dx or fast_db) and g2.dtype == Wq.dtype == x.dtype:
-            # dX and the bias gradient on a second stream while dW runs on
-            # this one: the dW product alone
-            # leaves CUs idle at these shapes (one 64 x 64 or 128 x 128 tile
-            # per CU or fewer).  Outputs are allocated here, on the current
-            # stream, before the fork; the join comes before they are
+            # dX (and the bias gradient where coset_gemm_tn does not take it)
+            # on a second stream while dW runs on this one: the dW product
+            # alone leaves CUs idle at these shapes (one 64 x 64 or 128 x 128
+            # tile per CU or fewer).  Outputs are allocated here, on the
+            # current stream, before the fork; the join comes before they are
             # returned.  Under graph capture the two streams become two
             # branches of the graph.
             g2 = g2.contiguous()
+            fuse = (_FUSE_BIAS_GRAD[0] == 1 and fast_db and g2.dtype == torch.bfloat16
+                    and _gemm_tn_takes(g2, x2))
             main = torch.cuda.current_stream(g2.device)
             aux = _aux_stream(g2.device)
             dx2 = torch.empty((g2.shape[0], Wq.shape[1]), dtype=g2.dtype, device=g2.device) if need_dx else None
-            cs = _colsum_buffers(g2) if fast_db else None
+            cs = _colsum_buffers(g2) if fast_db and not fuse else None
+            dbf = torch.empty(g2.shape[1], dtype=torch.float32, device=g2.device) if fuse else None
             aux.wait_stream(main)
             with torch.cuda.stream(aux):
                 if need_dx:
                     torch.mm(g2, Wq, out=dx2)
-                if fast_db:
+                if cs is not None:
                     _colsum_into(g2, *cs)
-            dW = _weight_grad(g2, x2)
+            dW = _weight_grad(g2, x2, colsum=dbf)
             main.wait_stream(aux)
             if need_dx:
                 dx = dx2.reshape(x.shape)
             if fast_db:
-                db = cs[0].to(ctx.bias_dtype)
+                db = (dbf if fuse else cs[0]).to(ctx.bias_dtype)
             elif ctx.bias_dtype is not None and ctx.needs_input_grad[2]:
                 db = g2.float().sum(0).to(ctx.bias_dtype)
             return dx, dW, db, None
