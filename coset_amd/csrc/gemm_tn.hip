@@ -47,7 +47,7 @@ typedef __attribute__((address_space(3))) char lds_char_t;
 
 constexpr int kTnTile = 64;     // output rows and columns per workgroup
 constexpr int kTnWaves = 8;     // waves per workgroup
-constexpr int kTnD = 2;         // slices in flight per wave
+constexpr int kTnD = 1;         // slices in flight per wave, in registers while the previous one is multiplied from LDS
 constexpr int kTnSlice = 32;    // tokens per slice (one MFMA K step)
 
 // LDS row pitch (bytes) of a 64-wide operand slice: 128 bytes + 32, so the
