@@ -498,8 +498,11 @@ __device__ __forceinline__ void store_out_wave(float* out, int64_t n, int64_t i,
 // bits: level 0), 64 bytes a block, through the wave's 1 KiB LDS slice as
 // in store_out_wave: a quarter of the wave at a time writes its blocks'
 // codes there and the whole wave reads them back 16 bytes a lane, so each
-// of the four stores writes 16 consecutive blocks (1 KiB).
-template <int Q>
+// of the four stores writes 16 consecutive blocks (1 KiB).  NT: the stores
+// are non-temporal (measured faster for the encoder, whose only other output
+// is the packed words, and slower beside the decoded-block stores of the
+// round trip).
+template <int Q, bool NT>
 __device__ __forceinline__ void store_codes_wave(float* codes, int64_t n, int64_t i, uint32_t words, uint4* st)
 {
     uint32_t e[4][4];  // e[chunk][dword]: chunk c = level c / 2, coordinates 4 (c % 2) ..
@@ -527,7 +530,11 @@ __device__ __forceinline__ void store_codes_wave(float* codes, int64_t n, int64_
         const uint4 v = st[lane];
         __asm__ volatile("" ::: "memory");
         const uint32_t q = min(16 * h + (lane >> 2), lim);
-        *reinterpret_cast<uint4*>(dst + (q * 64u + (lane & 3) * 16u)) = v;  // 32-bit lane offset
+        char* p = dst + (q * 64u + (lane & 3) * 16u);  // 32-bit lane offset
+        if constexpr (NT)
+            store_nt(p, __builtin_bit_cast(float4, v));
+        else
+            *reinterpret_cast<uint4*>(p) = v;
     }
 }
 
@@ -686,7 +693,7 @@ __global__ void __launch_bounds__(kLutThreads) hnlq_plain_kernel(CodecArgs a, co
             }
         }
         if (MODE != MODE_DECODE && CODES && M == 2)
-            store_codes_wave<Q>(a.codes_f32, n, i, (uint32_t)pack, reinterpret_cast<uint4*>(s_stage[threadIdx.x >> 6]));
+            store_codes_wave<Q, MODE == MODE_ENCODE>(a.codes_f32, n, i, (uint32_t)pack, reinterpret_cast<uint4*>(s_stage[threadIdx.x >> 6]));
         if (MODE != MODE_DECODE && PK) {
             uint16_t* pw = reinterpret_cast<uint16_t*>(a.packed) + (size_t)i * M;
             if (M == 1) {
