@@ -6,6 +6,7 @@
 
 #include "e8_core.hpp"
 #include "e8_fast.hpp"
+#include "fastdiv.hpp"
 
 namespace coset {
 
@@ -98,6 +99,9 @@ struct CodecArgs {
     const float* aux_in;
     void* aux_out;
     int64_t aux_n;
+    // SCALE_LAYER: floor(block / blocks_per_row) for blocks < 2^32 (set by
+    // the launcher for the layer round-trip kernel)
+    U32Div row_div;
 };
 
 // One encoder level (core rule, contiguous distances): the projection's

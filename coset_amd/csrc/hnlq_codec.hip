@@ -302,6 +302,148 @@ __global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
     }
 }
 
+// The layer quantizer's round trip with stored per-row betas (SCALE_LAYER:
+// HNLQLinearQAT._quantize_weights, coset/core/layers.py:428-463) for
+// q = 8, 16 and M <= 4, with the level count and input dtype fixed at
+// compile time, so a block runs straight through without the generic
+// kernel's per-call branches and the register copies at their joins:
+//  - the block's row from the launcher's 32-bit multiplier (blocks < 2^32);
+//  - x * beta, then per level the encoder (the fast projection first, its
+//    range checked once) and the level's residual straight from its digits
+//    (residual_dyadic);
+//  - dec / beta from one correctly rounded reciprocal per block and one or
+//    two residual corrections (div_by_recip: one where the decoded sums stay
+//    within its checked half-integer range), clamped by one med3.  That takes
+//    |beta| in [2^-64, 2^64] -- the decoded sums are half-integers below 2^46
+//    here, so every quantity stays normal -- and clip > 0 (the launcher's
+//    condition); the sums are finite, so no quotient is NaN.  Other betas
+//    (zero, tiny, huge, non-finite) take the IEEE divide and torch.clamp's NaN
+//    rule, as the generic kernel does for every block.
+template <int Q, int M, bool XBF16>
+__global__ void __launch_bounds__(256) hnlq_layer_rt_kernel(CodecArgs a)
+{
+    static_assert(Q == 8 || Q == 16, "residual_dyadic's q within the codec's q <= 16");
+    static_assert(M >= 1 && M <= 4, "level words stored as one vector");
+    constexpr int kSteps = Q == 8 || M <= 3 ? 1 : 2;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i == 0 && a.step_counter) *a.step_counter += 1;
+    if (i >= a.n) return;
+    const float beta = a.beta_row[u32div((uint32_t)i, a.row_div)];
+    float xl[8];
+    if constexpr (XBF16) {
+        const uint4 v = reinterpret_cast<const uint4*>(a.x)[i];
+        const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            xl[2 * j] = __uint_as_float(u[j] << 16);
+            xl[2 * j + 1] = __uint_as_float(u[j] & 0xffff0000u);
+        }
+    } else {
+        const float4* p = reinterpret_cast<const float4*>(a.x) + 2 * i;
+        const float4 u = p[0], v = p[1];
+        xl[0] = u.x; xl[1] = u.y; xl[2] = u.z; xl[3] = u.w;
+        xl[4] = v.x; xl[5] = v.y; xl[6] = v.z; xl[7] = v.w;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xl[j] = __fmul_rn(xl[j], beta);
+
+    float acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+    uint32_t* pw = a.packed ? reinterpret_cast<uint32_t*>(a.packed) + (size_t)i * M : nullptr;
+    // the fast projection's range condition holds at every level once it
+    // holds for the first: each level's input is the last one divided by q
+    const bool in_range = fast_in_range(xl);
+    float w = 1.f;
+#pragma unroll 1
+    for (int m = 0;; ++m) {
+        int b[8];
+        encode_level<Q>(xl, 1, Q, b, in_range);
+        if (pw) pw[m] = pack_word<Q>(b, Q);
+        float r[8];
+        residual_dyadic<Q>(b, r);
+        add_level<Q>(acc, w, r);
+        if (m + 1 == M) break;
+        w = __fmul_rn(w, (float)Q);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xl[j] = div_q<Q>(xl[j], (float)Q);
+    }
+    if (!a.out) return;
+
+    float o[8];
+    const float ab = fabsf(beta);
+    if (ab >= 0x1p-64f && ab <= 0x1p64f) {
+        const float y = __fdiv_rn(1.f, beta);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            o[j] = __builtin_amdgcn_fmed3f(div_by_recip<kSteps>(acc[j], beta, y), -a.clip, a.clip);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float v = __fdiv_rn(acc[j], beta);
+            o[j] = fminf(fmaxf(v, -a.clip), a.clip);
+            if (v != v) o[j] = v;  // torch.clamp propagates NaN
+        }
+    }
+    if (a.out_dtype == DT_BF16) {
+        uint4 v;
+        v.x = f32_to_bf16(o[0]) | ((uint32_t)f32_to_bf16(o[1]) << 16);
+        v.y = f32_to_bf16(o[2]) | ((uint32_t)f32_to_bf16(o[3]) << 16);
+        v.z = f32_to_bf16(o[4]) | ((uint32_t)f32_to_bf16(o[5]) << 16);
+        v.w = f32_to_bf16(o[6]) | ((uint32_t)f32_to_bf16(o[7]) << 16);
+        reinterpret_cast<uint4*>(a.out)[i] = v;
+    } else {
+        float4* p = reinterpret_cast<float4*>(a.out) + 2 * i;
+        p[0] = make_float4(o[0], o[1], o[2], o[3]);
+        p[1] = make_float4(o[4], o[5], o[6], o[7]);
+    }
+}
+
+// Calls the layer round-trip kernel takes (its static_asserts, the domain of
+// its division and row index; it always tries the fast projection first);
+// g_codec_plain = 0 keeps them on the generic kernel.
+static bool layer_rt_supported(const CodecArgs& a, int mode)
+{
+    return g_codec_plain && a.fast_projection && mode == MODE_ROUNDTRIP && a.scale_mode == SCALE_LAYER && !a.use_theta && a.beta_row &&
+           (a.q == 8 || a.q == 16) && a.M >= 1 && a.M <= 4 && !a.dither && !a.codes_f32 &&
+           (a.x_dtype == DT_F32 || a.x_dtype == DT_BF16) && (a.out_dtype == DT_F32 || a.out_dtype == DT_BF16) &&
+           a.clip > 0.f && a.n <= (int64_t)0xffffffffLL && a.blocks_per_row >= 1 &&
+           a.blocks_per_row <= (int64_t)0xffffffffLL;
+}
+
+static hipError_t launch_layer_rt(const CodecArgs& args, hipStream_t s)
+{
+    CodecArgs a = args;
+    if (a.aux_out && a.aux_n > 0) {
+        hipLaunchKernelGGL(aux_cast_kernel, dim3((unsigned)((a.aux_n + 255) / 256)), dim3(256), 0, s, a);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        a.aux_out = nullptr;
+    }
+    a.row_div = u32div_of((uint32_t)a.blocks_per_row);
+    const dim3 grid((unsigned)((a.n + 255) / 256)), block(256);
+    const bool bf = a.x_dtype == DT_BF16;
+#define COSET_LAYER(QQ, MM)                                                                        \
+    if (bf) hipLaunchKernelGGL((hnlq_layer_rt_kernel<QQ, MM, true>), grid, block, 0, s, a);       \
+    else hipLaunchKernelGGL((hnlq_layer_rt_kernel<QQ, MM, false>), grid, block, 0, s, a);         \
+    break;
+#define COSET_LAYER_Q(QQ)                     \
+    switch (a.M) {                            \
+    case 1: COSET_LAYER(QQ, 1)                \
+    case 2: COSET_LAYER(QQ, 2)                \
+    case 3: COSET_LAYER(QQ, 3)                \
+    default: COSET_LAYER(QQ, 4)               \
+    }                                         \
+    break;
+    switch (a.q) {
+    case 8: COSET_LAYER_Q(8)
+    default: COSET_LAYER_Q(16)
+    }
+#undef COSET_LAYER_Q
+#undef COSET_LAYER
+    return hipGetLastError();
+}
+
 template <int MODE>
 static hipError_t launch_mode(const CodecArgs& a, hipStream_t s)
 {
@@ -358,6 +500,7 @@ hipError_t launch_codec(const CodecArgs& args, int mode, hipStream_t s)
 hipError_t launch_codec_generic(const CodecArgs& a, int mode, hipStream_t s)
 {
     if (a.n == 0) return hipSuccess;  // (launch_codec has already done a side cast of an empty codec call)
+    if (layer_rt_supported(a, mode)) return launch_layer_rt(a, s);
     switch (mode) {
     case MODE_ENCODE: return launch_mode<MODE_ENCODE>(a, s);
     case MODE_DECODE: return launch_mode<MODE_DECODE>(a, s);

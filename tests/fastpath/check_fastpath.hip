@@ -23,7 +23,19 @@
 //                                   residual_dyadic<q> (q = 8, 16, 32) on T
 //                                   threads: every code for q^8 <= N (all
 //                                   2^32 at q = 16 with N = 4294967296),
-//                                   else the structured codes and N random
+//                                   else the structured codes and N random;
+//                                   also that no residual coordinate
+//                                   exceeds 3q/2 in magnitude
+//   check_fastpath divq S K [T]     div_by_recip<S>(a, b, RN(1/b)) against
+//                                   the IEEE quotient a / b for every b
+//                                   significand in [1, 2) and a = k / 2,
+//                                   k = 0 .. K (signs of a and b varied),
+//                                   plus, for S >= 2, random a of any
+//                                   exponent in the helper's domain
+//   check_fastpath u32div N         u32div against n / d: every d < 2^16 and
+//                                   N random d, each with the n next to its
+//                                   multiples, the ends of the range and
+//                                   random n
 #include <math.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -36,6 +48,7 @@
 #include <vector>
 
 #include "e8_fast.hpp"
+#include "fastdiv.hpp"
 
 extern "C" {
 float or_custom_round(float x);
@@ -265,7 +278,9 @@ static long fast_residual_check(const int32_t b[8], long* shown)
     coset::residual_dyadic<Q>(bi, r);
     or_residual(b, Q, 0, 0, ref0);
     or_residual(b, Q, 0, 1, ref1);
-    if (memcmp(r, ref0, sizeof r) == 0 && memcmp(r, ref1, sizeof r) == 0) return 0;
+    bool in_bound = true;  // |r_i| <= 3q/2 (div_by_recip's domain rests on it)
+    for (int i = 0; i < 8; ++i) in_bound = in_bound && fabsf(r[i]) <= 1.5f * (float)Q;
+    if (in_bound && memcmp(r, ref0, sizeof r) == 0 && memcmp(r, ref1, sizeof r) == 0) return 0;
     if (*shown < 5) {
         ++*shown;
         printf("mismatch q=%d b=", Q);
@@ -341,6 +356,105 @@ static int fast_residual(long n, int threads)
     return bad ? 1 : 0;
 }
 
+// div_by_recip<S> against the IEEE quotient: every significand of b in
+// [1, 2) (the quotient's rounding does not depend on b's exponent in the
+// helper's domain), a = k / 2 for k = 0 .. K with the four sign pairs on
+// every 16th b, and for S >= 2 eight random a per b with exponents from
+// 2^-1 to 2^46 and b scaled by 2^-64 .. 2^64
+template <int S>
+static int divq(long K, int threads)
+{
+    std::atomic<long> bad{0}, checked{0}, shown{0};
+    std::atomic<long> next{0};
+    constexpr long kChunk = 1 << 12;
+    auto work = [&]() {
+        long my_bad = 0, my_checked = 0;
+        std::mt19937_64 g;
+        for (;;) {
+            const long s0 = next.fetch_add(kChunk);
+            if (s0 >= (1L << 23)) break;
+            g.seed(977 + s0);
+            for (long sig = s0; sig < s0 + kChunk; ++sig) {
+                const float b = from_bits(0x3f800000u | (uint32_t)sig);
+                volatile float one = 1.f;
+                const float y = one / b;
+                auto check = [&](float a, float bb, float yy) {
+                    const float got = coset::div_by_recip<S>(a, bb, yy);
+                    volatile float va = a, vb = bb;
+                    const float want = va / vb;
+                    ++my_checked;
+                    if (to_bits(got) != to_bits(want)) {
+                        ++my_bad;
+                        if (shown.fetch_add(1) < 5)
+                            printf("mismatch S=%d a=%a b=%a got=%a want=%a\n", S, a, bb, got, want);
+                    }
+                };
+                for (long k = 0; k <= K; ++k) {
+                    const float a = 0.5f * (float)k;
+                    check(a, b, y);
+                    if ((sig & 15) == 0 && k > 0) {
+                        check(-a, b, y);
+                        check(a, -b, -y);
+                        check(-a, -b, -y);
+                    }
+                }
+                if (S >= 2) {
+                    for (int t = 0; t < 8; ++t) {
+                        const uint64_t h = g();
+                        const int ea = (int)(h % 48) - 1, eb = (int)((h >> 8) % 129) - 64;
+                        const float a = ldexpf(from_bits(0x3f800000u | (uint32_t)(h >> 40 & 0x7fffff)), ea);
+                        const float bb = ldexpf(b, eb), yy = ldexpf(y, -eb);
+                        check((h >> 63) ? -a : a, bb, yy);
+                    }
+                }
+            }
+        }
+        bad += my_bad;
+        checked += my_checked;
+    };
+    std::vector<std::thread> pool;
+    for (int t = 0; t < threads; ++t) pool.emplace_back(work);
+    for (auto& t : pool) t.join();
+    printf("divq S=%d K=%ld: %ld quotients, mismatches %ld\n", S, K, checked.load(), bad.load());
+    return bad ? 1 : 0;
+}
+
+static int u32div_check(long n_random)
+{
+    std::mt19937_64 g(2024);
+    long bad = 0, checked = 0;
+    auto one = [&](uint32_t d) {
+        const coset::U32Div dv = coset::u32div_of(d);
+        auto at = [&](uint32_t n) {
+            ++checked;
+            if (coset::u32div(n, dv) != n / d) {
+                if (++bad <= 5) printf("mismatch n=%u d=%u got=%u\n", n, d, coset::u32div(n, dv));
+            }
+        };
+        at(0u);
+        at(0xffffffffu);
+        at(0xffffffffu - 1u);
+        for (int t = 0; t < 16; ++t) {
+            const uint64_t k = g() % (0xffffffffull / d + 1);
+            const uint64_t m = k * d;
+            if (m > 0) at((uint32_t)(m - 1));
+            if (m <= 0xffffffffull) at((uint32_t)m);
+            if (m + 1 <= 0xffffffffull) at((uint32_t)(m + 1));
+            at((uint32_t)g());
+        }
+    };
+    for (uint32_t d = 1; d < (1u << 16); ++d) one(d);
+    for (int k = 16; k < 32; ++k) {
+        one(1u << k);
+        one((1u << k) - 1u);
+        one((1u << k) + 1u);
+    }
+    one(0xffffffffu);
+    for (long t = 0; t < n_random; ++t) one(((uint32_t)g() >> (g() % 32)) | 1u);
+    printf("u32div: %ld quotients, mismatches %ld\n", checked, bad);
+    return bad ? 1 : 0;
+}
+
 static int dyadic(int q, long n)
 {
     long total = 1, bad = 0, checked = 0;
@@ -391,9 +505,20 @@ int main(int argc, char** argv)
         fprintf(stderr, "fastres: q must be 8, 16 or 32\n");
         return 2;
     }
+    if (argc >= 3 && !strcmp(argv[1], "u32div")) return u32div_check(atol(argv[2]));
+    if (argc >= 4 && !strcmp(argv[1], "divq")) {
+        const int steps = atoi(argv[2]);
+        const long k = atol(argv[3]);
+        const int th = argc >= 5 ? atoi(argv[4]) : 1;
+        if (steps == 0) return divq<0>(k, th);
+        if (steps == 1) return divq<1>(k, th);
+        if (steps == 2) return divq<2>(k, th);
+        fprintf(stderr, "divq: steps must be 0, 1 or 2\n");
+        return 2;
+    }
     // an optional second argument replaces the tie limit (a looser one must fail)
     if (argc >= 2 && !strcmp(argv[1], "lemma")) return lemma(argc >= 3 ? strtof(argv[2], nullptr) : coset::kFastTieLimit);
     if (argc >= 4 && !strcmp(argv[1], "blocks")) return blocks(atol(argv[2]), (unsigned)atoi(argv[3]));
-    fprintf(stderr, "usage: %s lemma [limit] | blocks N seed | dyadic q N | fastres q N [threads]\n", argv[0]);
+    fprintf(stderr, "usage: %s lemma [limit] | blocks N seed | dyadic q N | fastres q N [threads] | divq steps K [threads] | u32div N\n", argv[0]);
     return 2;
 }

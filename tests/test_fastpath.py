@@ -16,6 +16,8 @@ import pytest
 
 HERE = os.path.join(os.path.dirname(__file__), "fastpath")
 EXE = os.path.join(HERE, "_build", "check_fastpath")
+# the library headers the mutated copies do not replace (fastdiv.hpp)
+CSRC = os.path.join(HERE, "..", "..", "coset_amd", "csrc")
 
 
 @pytest.fixture(scope="module")
@@ -82,7 +84,7 @@ def test_condition5_fails_without_its_d8_term(tmp_path):
     exe = tmp_path / "check_mutated"
     subprocess.run(["gcc", "-O2", "-fPIC", "-std=c99", "-ffp-contract=off", "-fno-fast-math", "-c", "-o",
                     str(tmp_path / "o.o"), oracle], check=True, capture_output=True)
-    subprocess.run([hipcc, "-O2", "-std=c++17", "-ffp-contract=off", "--offload-arch=gfx950", f"-I{inc}", "-c",
+    subprocess.run([hipcc, "-O2", "-std=c++17", "-ffp-contract=off", "--offload-arch=gfx950", f"-I{inc}", f"-I{CSRC}", "-c",
                     "-o", str(tmp_path / "c.o"), os.path.join(HERE, "check_fastpath.hip")], check=True,
                    capture_output=True)
     subprocess.run([hipcc, "--offload-arch=gfx950", "-o", str(exe), str(tmp_path / "c.o"), str(tmp_path / "o.o"),
@@ -136,7 +138,7 @@ def test_fast_residual_fails_without_its_integer_tie_rule(tmp_path):
     exe = tmp_path / "check_mutated"
     subprocess.run(["gcc", "-O2", "-fPIC", "-std=c99", "-ffp-contract=off", "-fno-fast-math", "-c", "-o",
                     str(tmp_path / "o.o"), oracle], check=True, capture_output=True)
-    subprocess.run([hipcc, "-O2", "-std=c++17", "-ffp-contract=off", "--offload-arch=gfx950", f"-I{inc}", "-c",
+    subprocess.run([hipcc, "-O2", "-std=c++17", "-ffp-contract=off", "--offload-arch=gfx950", f"-I{inc}", f"-I{CSRC}", "-c",
                     "-o", str(tmp_path / "c.o"), os.path.join(HERE, "check_fastpath.hip")], check=True,
                    capture_output=True)
     subprocess.run([hipcc, "--offload-arch=gfx950", "-o", str(exe), str(tmp_path / "c.o"), str(tmp_path / "o.o"),
@@ -144,3 +146,37 @@ def test_fast_residual_fails_without_its_integer_tie_rule(tmp_path):
     rc, out = run(str(exe), "fastres", "8", str(1 << 24), "4")
     assert rc == 1, out
     assert " mismatches 0" not in out, out
+
+
+@pytest.mark.parametrize("steps,k", [(1, 256), (2, 256)])
+def test_division_by_reciprocal(checker, steps, k):
+    """div_by_recip (the layer round trip's dec / beta from one reciprocal per
+    block) against the IEEE quotient: every significand of b in [1, 2) with
+    a = 0, 1/2, .., 128 (and the four sign pairs on every 16th b), plus, with
+    two corrections, random a and b over the helper's whole exponent domain.
+    (The single correction's range that the kernel relies on, every
+    half-integer up to 16384, is checked by `check_fastpath divq 1 32768
+    <threads>`, about a minute on eight cores.)"""
+    rc, out = run(checker, "divq", str(steps), str(k), str(min(8, os.cpu_count() or 1)))
+    assert rc == 0, out
+    assert " mismatches 0" in out, out
+
+
+def test_division_by_reciprocal_fails_without_its_correction(checker):
+    """Negative control: the bare product RN(a RN(1/b)) is not the correctly
+    rounded quotient, so the checker must find mismatches without the
+    correction step."""
+    rc, out = run(checker, "divq", "0", "16", str(min(8, os.cpu_count() or 1)))
+    assert rc == 1, out
+    assert " mismatches 0" not in out, out
+
+
+def test_row_index_by_multiplier(checker):
+    """u32div (the layer round trip's row of a block, floor(i / blocks_per_row)
+    from a host-computed multiplier) against integer division: every divisor
+    below 2^16, powers of two and their neighbours, 2^32 - 1 and random
+    divisors, at the numerators next to their multiples, the range's ends and
+    random ones."""
+    rc, out = run(checker, "u32div", "100000")
+    assert rc == 0, out
+    assert " mismatches 0" in out, out

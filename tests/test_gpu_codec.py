@@ -506,6 +506,67 @@ def test_full_size_c3(ca):
     np.testing.assert_array_equal(got.reshape(-1, 3), O.pack_words(codes, 16).reshape(-1, 3))
 
 
+@pytest.mark.parametrize("q", [8, 16])
+def test_layer_roundtrip_kernel_matches_generic(ca, q):
+    """The layer round-trip kernel (SCALE_LAYER with stored per-row betas,
+    q = 8, 16, M <= 4: one reciprocal per block and div_by_recip for
+    dec / beta, med3 clamp) bit for bit against the generic kernel
+    (set_codec_plain(False)): every M, fp32 and bf16 inputs and outputs,
+    rows of 1, 7, 96 and 512 blocks, block counts that end inside a
+    workgroup, betas log-uniform over 1e-3 .. 1e3 with the division's edge
+    cases (2^-64 and 2^64 and the floats just outside, 0, negative,
+    subnormal, huge, inf, NaN), clips of 2, inf and 1e-3; the fp32 outputs
+    of finite rows also against the oracle on a sample."""
+    from coset_amd import _lib
+    rng = np.random.default_rng(40 + q)
+    specials = np.array([2.0 ** -64, 2.0 ** 64, np.nextafter(np.float32(2.0 ** -64), np.float32(0)),
+                         np.nextafter(np.float32(2.0 ** 64), np.float32(np.inf)), 0.0, -1.5, 1e-40, 3e38,
+                         np.inf, np.nan, -np.inf, 1e-20, 1e20, -2.0 ** -64], dtype=np.float32)
+    checked = 0
+    try:
+        for bpr, rows in ((1, 3621), (7, 517), (96, 37), (512, 7)):
+            n = bpr * rows
+            beta = np.exp(rng.uniform(np.log(1e-3), np.log(1e3), rows)).astype(np.float32)
+            k = min(rows // 2, len(specials))
+            beta[rng.choice(rows, k, replace=False)] = specials[:k] if rows > 40 else specials[rng.choice(len(specials), k, replace=False)]
+            x = (rng.standard_normal((n, 8)) * rng.choice([0.05, 1.0, 30.0], (n, 1))).astype(np.float32)
+            x[rng.choice(n, 3, replace=False)] = 0.0
+            xd = dev(x)
+            bd = dev(beta)
+            for M in (1, 2, 3, 4):
+                for xdt in (torch.float32, torch.bfloat16):
+                    for clip in (2.0, float("inf"), 1e-3):
+                        odt = torch.bfloat16 if (M + bpr) % 2 else torch.float32
+                        res = []
+                        for plain in (True, False):
+                            _lib.set_codec_plain(plain)
+                            pk, out = ca.hnlq_roundtrip(xd.to(xdt), q, M, beta_row=bd, blocks_per_row=bpr,
+                                                        clip=clip, out_dtype=odt)
+                            res.append((words(pk), host(out.view(torch.int32 if odt == torch.float32 else torch.int16))))
+                        case = f"q={q} M={M} bpr={bpr} x={xdt} out={odt} clip={clip}"
+                        np.testing.assert_array_equal(res[0][0], res[1][0], err_msg=case)
+                        np.testing.assert_array_equal(res[0][1], res[1][1], err_msg=case)
+                        checked += 1
+                        if odt == torch.float32 and xdt == torch.float32 and clip == 2.0:
+                            # rows whose scaled blocks stay below 2^20 (the reference's fp32
+                            # encode_coords is exact there; far beyond it the digits leave
+                            # int32 here and the oracle's doubles, and torch's own matmul
+                            # rounds): the 2^-64 rows among them
+                            big = np.abs(x.reshape(rows, -1).astype(np.float64)).max(1) * np.abs(beta)
+                            ok = np.isfinite(beta) & (beta != 0) & (big < 2.0 ** 20)
+                            sel = np.concatenate([np.flatnonzero(ok & (np.abs(beta) < 1e-10))[:2],
+                                                  np.flatnonzero(ok & (np.abs(beta) >= 1e-10))[:4]])
+                            xs = x.reshape(rows, bpr * 8)[sel]
+                            Wq, _, codes = O.layer_quant(xs, beta[sel], q, M, 2.0)
+                            got = res[0][1].view(np.float32).reshape(rows, bpr * 8)[sel]
+                            np.testing.assert_array_equal(got, Wq, err_msg=case)
+                            gw = res[0][0].reshape(rows, bpr, M)[sel].reshape(-1, M)
+                            np.testing.assert_array_equal(gw, O.pack_words(codes, q).reshape(-1, M), err_msg=case)
+    finally:
+        _lib.set_codec_plain(True)
+    assert checked == 4 * 4 * 2 * 3
+
+
 def test_input_lengths_are_checked():
     """Lengths the kernels index by are validated on the host: a dither of
     neither 8 nor 8 n values, a per-row beta that does not tile the blocks,
