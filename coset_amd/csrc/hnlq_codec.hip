@@ -347,26 +347,30 @@ __global__ void __launch_bounds__(256) hnlq_layer_rt_kernel(CodecArgs a)
 #pragma unroll
     for (int j = 0; j < 8; ++j) xl[j] = __fmul_rn(xl[j], beta);
 
-    float acc[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] = 0.f;
     uint32_t* pw = a.packed ? reinterpret_cast<uint32_t*>(a.packed) + (size_t)i * M : nullptr;
     // the fast projection's range condition holds at every level once it
     // holds for the first: each level's input is the last one divided by q
     const bool in_range = fast_in_range(xl);
+    // level 0 starts the sum: 0 + 1 r = r, as residual_dyadic never returns -0
+    float acc[8];
+    {
+        int b[8];
+        encode_level<Q>(xl, 1, Q, b, in_range);
+        if (pw) pw[0] = pack_word<Q>(b, Q);
+        residual_dyadic<Q>(b, acc);
+    }
     float w = 1.f;
 #pragma unroll 1
-    for (int m = 0;; ++m) {
+    for (int m = 1; m < M; ++m) {
+        w = __fmul_rn(w, (float)Q);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xl[j] = div_q<Q>(xl[j], (float)Q);
         int b[8];
         encode_level<Q>(xl, 1, Q, b, in_range);
         if (pw) pw[m] = pack_word<Q>(b, Q);
         float r[8];
         residual_dyadic<Q>(b, r);
         add_level<Q>(acc, w, r);
-        if (m + 1 == M) break;
-        w = __fmul_rn(w, (float)Q);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) xl[j] = div_q<Q>(xl[j], (float)Q);
     }
     if (!a.out) return;
 

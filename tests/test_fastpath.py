@@ -156,7 +156,7 @@ def test_division_by_reciprocal(checker, steps, k):
     two corrections, random a and b over the helper's whole exponent domain.
     (The single correction's range that the kernel relies on, every
     half-integer up to 16384, is checked by `check_fastpath divq 1 32768
-    <threads>`, about a minute on eight cores.)"""
+    <threads>`, about six minutes on eight cores.)"""
     rc, out = run(checker, "divq", str(steps), str(k), str(min(8, os.cpu_count() or 1)))
     assert rc == 0, out
     assert " mismatches 0" in out, out
