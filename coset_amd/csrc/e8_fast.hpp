@@ -401,4 +401,101 @@ __host__ __device__ inline void residual_dyadic(const int b[8], float r[8])
     }
 }
 
+// The same residual in integers, from a table of per-coordinate quantities
+// (the layer round-trip kernel, q = 8, 16).  Everything residual_dyadic
+// derives for coordinate i is a function of Z_i alone, an integer in
+// [-2(q-1), 5(q-1)], so a 7q-entry table indexed by Z + 2q holds it:
+//   f0 = the nearest integer to z = Z / 2q, ties toward zero (g0 = -f0);
+//   D0 = 2q d0 = Z - 2q f0, in [-q, q];
+//   f1 = floor(z - 1/(4q)) for Z > 0, floor(z + 1/(4q)) for Z <= 0, i.e.
+//        floor((Z - 1) / 2q) and floor(Z / 2q);
+//   D1 = 2q d1 = Z - q - 2q f1, with |D1| = q - |D0|;
+//   c0 = [Z >= 0 and D0 > 0], c1 = [Z >= q and D1 > 0]: the direction of
+//        the g_x step at the worst coordinate (nk0 <= 0 and dk0 > 0, tk1 >= 0
+//        and dk1 > 0 above).
+// Entry words, laid out so that the maximum of word + (7 - i) << 24 over the
+// eight coordinates is the first index of the largest |D| with that
+// coordinate's own low fields, and the plain sum of the eight words holds the
+// sums without carries between fields:
+//   x = |D0| << 27 | (f0 & 1) << 21 | |D0| << 13 | c0 << 9 | (D0 + q)
+//   y = |D1| << 27 | (f1 & 1) << 21 |              c1 << 9 | (D1 + q)
+//   z = (D0 + q) | (D1 + q) << 16
+// (sums over eight coordinates: D + q <= 2q each, at most 16q = 256 in bits
+// 0-8; c counts <= 8 in bits 9-12; sum |D0| <= 8q = 128 in bits 13-20; the
+// parity count's low bit at 21, its carries in bits 22 and up, unused).  The
+// largest |D1| is the smallest |D0|, so y's maximum is the first argmin of
+// |d0| as above, and in units of 1/(2q) the comparison is the integer
+//   4q - sum |D0| + (2q |adj1| - 2 adj1 D1_k1) - (2q |adj0| - 2 adj0 D0_k0) > 0.
+template <int Q>
+__host__ __device__ inline uint4 dyadic_table_entry(int Z)
+{
+    const int f0 = Z >= 0 ? (Z + Q - 1) / (2 * Q) : -((Q - 1 - Z) / (2 * Q));
+    const int d0 = Z - 2 * Q * f0;
+    const int f1 = Z > 0 ? (Z - 1) / (2 * Q) : -((2 * Q - 1 - Z) / (2 * Q));
+    const int d1 = Z - Q - 2 * Q * f1;
+    const uint32_t a0 = (uint32_t)(d0 < 0 ? -d0 : d0), a1 = (uint32_t)(d1 < 0 ? -d1 : d1);
+    const uint32_t c0 = Z >= 0 && d0 > 0, c1 = Z >= Q && d1 > 0;
+    uint4 e;
+    e.x = a0 << 27 | (uint32_t)(f0 & 1) << 21 | a0 << 13 | c0 << 9 | (uint32_t)(d0 + Q);
+    e.y = a1 << 27 | (uint32_t)(f1 & 1) << 21 | c1 << 9 | (uint32_t)(d1 + Q);
+    e.z = (uint32_t)(d0 + Q) | (uint32_t)(d1 + Q) << 16;
+    e.w = 0u;
+    return e;
+}
+
+__host__ __device__ inline int mad24(int a, int b, int c)
+{
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __mul24(a, b) + c;  // one v_mad_i32_i24
+#else
+    return a * b + c;
+#endif
+}
+
+// One level of the sum 2 x_hat = sum_m q^m (2 r_m), in integers: adds
+// (2 r_i + q) << shift to acc2[i] (FIRST: sets it), where 2 r is twice the
+// residual residual_dyadic<Q>(b) returns and tab the 7q-entry table above
+// (tab[Z + 2q] = dyadic_table_entry<Q>(Z)).  The caller subtracts
+// q sum_m q^m once at the end.
+template <int Q, bool FIRST>
+__host__ __device__ inline void dyadic_level_acc(const int b[8], const uint4* tab, int shift, int acc2[8])
+{
+    static_assert(Q == 8 || Q == 16, "the table fields hold q <= 16");
+    const uint4* t7 = tab + (b[7] + 2 * Q);  // Z_i = 2 (..) + b_7
+    uint4 e[8];
+    e[0] = t7[2 * (2 * b[0] - b[1])];
+#pragma unroll
+    for (int i = 1; i < 6; ++i) e[i] = t7[2 * (b[i] - b[i + 1])];
+    e[6] = t7[2 * b[6]];
+    e[7] = t7[0];
+    uint32_t kx[8], ky[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        kx[i] = e[i].x + ((uint32_t)(7 - i) << 24);
+        ky[i] = e[i].y + ((uint32_t)(7 - i) << 24);
+    }
+    uint32_t mx = kx[0], my = ky[0], sx = kx[0], sy = ky[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) {
+        mx = mx > kx[i] ? mx : kx[i];
+        my = my > ky[i] ? my : ky[i];
+        sx += kx[i];
+        sy += ky[i];
+    }
+    const int sa = (int)((sx >> 13) & 0xffu);
+    const int adj0 = (sx >> 21) & 1u ? (((mx >> 9) & 1u) ? 1 : -1) : 0;
+    const int adj1 = (sy >> 21) & 1u ? (((my >> 9) & 1u) ? 1 : -1) : 0;
+    const int dk0 = (int)(mx & 0x1ffu) - Q, dk1 = (int)(my & 0x1ffu) - Q;
+    const int diff = 4 * Q - sa + (2 * Q * (adj1 != 0) - 2 * adj1 * dk1) - (2 * Q * (adj0 != 0) - 2 * adj0 * dk0);
+    const bool pick0 = diff > 0;  // ties go to D8 + 1/2
+    const uint32_t sel = pick0 ? 0u : 16u;
+    const uint32_t mk = 1u << (7u - ((pick0 ? mx : my) >> 24 & 7u));  // the moved coordinate
+    const int t = -2 * Q * (pick0 ? adj0 : adj1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int v = mad24((int)((mk >> i) & 1u), t, (int)((e[i].z >> sel) & 0xffffu));
+        acc2[i] = FIRST ? v << shift : (v << shift) + acc2[i];
+    }
+}
+
 }  // namespace coset

@@ -309,8 +309,9 @@ __global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
 // kernel's per-call branches and the register copies at their joins:
 //  - the block's row from the launcher's 32-bit multiplier (blocks < 2^32);
 //  - x * beta, then per level the encoder (the fast projection first, its
-//    range checked once) and the level's residual straight from its digits
-//    (residual_dyadic);
+//    range checked once) and the level's residual from its digits through
+//    the workgroup's LDS table of per-coordinate quantities
+//    (dyadic_level_acc: residual_dyadic's values, summed in integers);
 //  - dec / beta from one correctly rounded reciprocal per block and one or
 //    two residual corrections (div_by_recip: one where the decoded sums stay
 //    within its checked half-integer range), clamped by one med3.  That takes
@@ -325,6 +326,13 @@ __global__ void __launch_bounds__(256) hnlq_layer_rt_kernel(CodecArgs a)
     static_assert(Q == 8 || Q == 16, "residual_dyadic's q within the codec's q <= 16");
     static_assert(M >= 1 && M <= 4, "level words stored as one vector");
     constexpr int kSteps = Q == 8 || M <= 3 ? 1 : 2;
+    constexpr int kLog2Q = Q == 8 ? 3 : 4;
+    constexpr int kOff = Q * (Q == 8 ? (M == 1 ? 1 : M == 2 ? 9 : M == 3 ? 73 : 585)
+                                     : (M == 1 ? 1 : M == 2 ? 17 : M == 3 ? 273 : 4369));  // q sum_m q^m
+    // the decode table of dyadic_level_acc, one entry per Z + 2q
+    __shared__ uint4 s_tab[7 * Q];
+    if (threadIdx.x < 7 * Q) s_tab[threadIdx.x] = dyadic_table_entry<Q>((int)threadIdx.x - 2 * Q);
+    __syncthreads();
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i == 0 && a.step_counter) *a.step_counter += 1;
     if (i >= a.n) return;
@@ -351,27 +359,27 @@ __global__ void __launch_bounds__(256) hnlq_layer_rt_kernel(CodecArgs a)
     // the fast projection's range condition holds at every level once it
     // holds for the first: each level's input is the last one divided by q
     const bool in_range = fast_in_range(xl);
-    // level 0 starts the sum: 0 + 1 r = r, as residual_dyadic never returns -0
-    float acc[8];
+    // 2 x_hat = sum_m q^m (2 r_m) in integers (the float sum of the levels
+    // is exact on these half-integers, so its value is the same)
+    int acc2[8];
     {
         int b[8];
         encode_level<Q>(xl, 1, Q, b, in_range);
         if (pw) pw[0] = pack_word<Q>(b, Q);
-        residual_dyadic<Q>(b, acc);
+        dyadic_level_acc<Q, true>(b, s_tab, 0, acc2);
     }
-    float w = 1.f;
 #pragma unroll 1
     for (int m = 1; m < M; ++m) {
-        w = __fmul_rn(w, (float)Q);
 #pragma unroll
         for (int j = 0; j < 8; ++j) xl[j] = div_q<Q>(xl[j], (float)Q);
         int b[8];
         encode_level<Q>(xl, 1, Q, b, in_range);
         if (pw) pw[m] = pack_word<Q>(b, Q);
-        float r[8];
-        residual_dyadic<Q>(b, r);
-        add_level<Q>(acc, w, r);
+        dyadic_level_acc<Q, false>(b, s_tab, m * kLog2Q, acc2);
     }
+    float acc[8];  // +0 where the sum is zero, as the float sum of the levels
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.5f * (float)(acc2[j] - kOff);
     if (!a.out) return;
 
     float o[8];

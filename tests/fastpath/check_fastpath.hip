@@ -26,6 +26,9 @@
 //                                   else the structured codes and N random;
 //                                   also that no residual coordinate
 //                                   exceeds 3q/2 in magnitude
+//   check_fastpath tabres q N [T]   the same residual through the integer
+//                                   table form dyadic_level_acc<q> (q = 8,
+//                                   16), codes as for fastres
 //   check_fastpath divq S K [T]     div_by_recip<S>(a, b, RN(1/b)) against
 //                                   the IEEE quotient a / b for every b
 //                                   significand in [1, 2) and a = k / 2,
@@ -269,13 +272,25 @@ static int residual_check(const int32_t b[8], int q, long* bad)
 
 // residual_dyadic<Q> (the decoders' fast residual straight from the digits)
 // against the oracle under both distance rules, bit for bit
-template <int Q>
+// TABLE: the residual from dyadic_level_acc (one level, shift 0) instead
+template <int Q, bool TABLE = false>
 static long fast_residual_check(const int32_t b[8], long* shown)
 {
     float r[8], ref0[8], ref1[8];
     int bi[8];
     for (int i = 0; i < 8; ++i) bi[i] = b[i];
-    coset::residual_dyadic<Q>(bi, r);
+    if constexpr (TABLE) {
+        static const std::vector<uint4> tab = [] {
+            std::vector<uint4> t(7 * Q);
+            for (int z = -2 * Q; z < 5 * Q; ++z) t[z + 2 * Q] = coset::dyadic_table_entry<Q>(z);
+            return t;
+        }();
+        int acc2[8];
+        coset::dyadic_level_acc<Q, true>(bi, tab.data(), 0, acc2);
+        for (int i = 0; i < 8; ++i) r[i] = 0.5f * (float)(acc2[i] - Q);
+    } else {
+        coset::residual_dyadic<Q>(bi, r);
+    }
     or_residual(b, Q, 0, 0, ref0);
     or_residual(b, Q, 0, 1, ref1);
     bool in_bound = true;  // |r_i| <= 3q/2 (div_by_recip's domain rests on it)
@@ -296,7 +311,7 @@ static long fast_residual_check(const int32_t b[8], long* shown)
 
 // every code for q^8 <= n (threads over the leading digit pairs), else the
 // 5^8 structured codes and n random ones
-template <int Q>
+template <int Q, bool TABLE = false>
 static int fast_residual(long n, int threads)
 {
     long total = 1;
@@ -319,7 +334,7 @@ static int fast_residual(long n, int threads)
                         b[j] = (int32_t)(v % Q);
                         v /= Q;
                     }
-                    my_bad += fast_residual_check<Q>(b, &my_shown);
+                    my_bad += fast_residual_check<Q, TABLE>(b, &my_shown);
                 }
                 my_checked += rest;
             }
@@ -340,19 +355,20 @@ static int fast_residual(long n, int threads)
                 b[j] = pick[v % 5];
                 v /= 5;
             }
-            b_ += fast_residual_check<Q>(b, &my_shown);
+            b_ += fast_residual_check<Q, TABLE>(b, &my_shown);
             ++c_;
         }
         std::mt19937_64 g(4321 + Q);
         for (long it = 0; it < n; ++it) {
             for (int j = 0; j < 8; ++j) b[j] = (int32_t)(g() % (uint64_t)Q);
-            b_ += fast_residual_check<Q>(b, &my_shown);
+            b_ += fast_residual_check<Q, TABLE>(b, &my_shown);
             ++c_;
         }
         bad += b_;
         checked += c_;
     }
-    printf("fast residual q=%d: %ld codes, mismatches %ld\n", Q, checked.load(), bad.load());
+    printf("%s residual q=%d: %ld codes, mismatches %ld\n", TABLE ? "table" : "fast", Q, checked.load(),
+           bad.load());
     return bad ? 1 : 0;
 }
 
@@ -495,6 +511,15 @@ static int dyadic(int q, long n)
 int main(int argc, char** argv)
 {
     if (argc >= 4 && !strcmp(argv[1], "dyadic")) return dyadic(atoi(argv[2]), atol(argv[3]));
+    if (argc >= 4 && !strcmp(argv[1], "tabres")) {
+        const int q = atoi(argv[2]);
+        const long n = atol(argv[3]);
+        const int th = argc >= 5 ? atoi(argv[4]) : 1;
+        if (q == 8) return fast_residual<8, true>(n, th);
+        if (q == 16) return fast_residual<16, true>(n, th);
+        fprintf(stderr, "tabres: q must be 8 or 16\n");
+        return 2;
+    }
     if (argc >= 4 && !strcmp(argv[1], "fastres")) {
         const int q = atoi(argv[2]);
         const long n = atol(argv[3]);
@@ -519,6 +544,6 @@ int main(int argc, char** argv)
     // an optional second argument replaces the tie limit (a looser one must fail)
     if (argc >= 2 && !strcmp(argv[1], "lemma")) return lemma(argc >= 3 ? strtof(argv[2], nullptr) : coset::kFastTieLimit);
     if (argc >= 4 && !strcmp(argv[1], "blocks")) return blocks(atol(argv[2]), (unsigned)atoi(argv[3]));
-    fprintf(stderr, "usage: %s lemma [limit] | blocks N seed | dyadic q N | fastres q N [threads] | divq steps K [threads] | u32div N\n", argv[0]);
+    fprintf(stderr, "usage: %s lemma [limit] | blocks N seed | dyadic q N | fastres q N [threads] | tabres q N [threads] | divq steps K [threads] | u32div N\n", argv[0]);
     return 2;
 }

@@ -119,6 +119,49 @@ def test_fast_residual_matches_oracle(checker, q, n):
     assert " mismatches 0" in out, out
 
 
+@pytest.mark.parametrize("q,n", [(8, 1 << 24), (16, 1 << 21)])
+def test_table_residual_matches_oracle(checker, q, n):
+    """The layer kernel's integer decode dyadic_level_acc<q> (per-coordinate
+    table, first-index argmax/argmin as maxima of packed keys, sums and
+    parities as one add): every code at q = 8, the structured codes and a
+    random sample at q = 16, twice the residual bit for bit against the
+    oracle's under both distance rules.  (All 2^32 codes at q = 16:
+    `check_fastpath tabres 16 4294967296 <threads>`, about ten minutes on
+    eight cores.)"""
+    rc, out = run(checker, "tabres", str(q), str(n), str(min(8, os.cpu_count() or 1)))
+    assert rc == 0, out
+    assert " mismatches 0" in out, out
+
+
+def test_table_residual_fails_with_a_wrong_gx_direction(tmp_path):
+    """Negative control of the table decode: with the D8 + 1/2 candidate's g_x
+    direction taken from the sign of d1 alone (without z >= 1/2), the
+    checker must report mismatches.  The mutated header is a copy built
+    here."""
+    if shutil.which("hipcc") is None and not os.path.exists("/opt/rocm/bin/hipcc"):
+        pytest.skip("hipcc not available")
+    src = os.path.join(HERE, "..", "..", "coset_amd", "csrc", "e8_fast.hpp")
+    text = open(src).read()
+    term = "c1 = Z >= Q && d1 > 0;"
+    assert text.count(term) == 1, "the table's c1 rule moved: update this negative control"
+    inc = tmp_path / "inc"
+    inc.mkdir()
+    (inc / "e8_fast.hpp").write_text(text.replace(term, "c1 = d1 > 0;"))
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    oracle = os.path.join(HERE, "..", "..", "oracle", "e8_oracle.c")
+    exe = tmp_path / "check_mutated"
+    subprocess.run(["gcc", "-O2", "-fPIC", "-std=c99", "-ffp-contract=off", "-fno-fast-math", "-c", "-o",
+                    str(tmp_path / "o.o"), oracle], check=True, capture_output=True)
+    subprocess.run([hipcc, "-O2", "-std=c++17", "-ffp-contract=off", "--offload-arch=gfx950", f"-I{inc}", f"-I{CSRC}",
+                    "-c", "-o", str(tmp_path / "c.o"), os.path.join(HERE, "check_fastpath.hip")], check=True,
+                   capture_output=True)
+    subprocess.run([hipcc, "--offload-arch=gfx950", "-o", str(exe), str(tmp_path / "c.o"), str(tmp_path / "o.o"),
+                    "-lpthread", "-lm"], check=True, capture_output=True)
+    rc, out = run(str(exe), "tabres", "8", str(1 << 24), "4")
+    assert rc == 1, out
+    assert " mismatches 0" not in out, out
+
+
 def test_fast_residual_fails_without_its_integer_tie_rule(tmp_path):
     """Negative control of residual_dyadic: without the nudge that sends the
     D8 + 1/2 candidate of a positive integer z to z - 1 (custom_round's tie
