@@ -92,6 +92,7 @@ OPT_FAST_PROJECTION = 4
 OPT_CODEC_PLAIN = 5
 OPT_CODEC_DYNAMIC = 6
 OPT_VLUT_DEEP = 7
+OPT_GEMM_TN_TILE = 8
 CODEC_AUTO, CODEC_GENERIC, CODEC_LUT = 0, 1, 2
 
 _lib = None
@@ -208,6 +209,12 @@ def set_vlut_decode(byte_tables: bool) -> None:
 def set_vlut_deep(enabled: bool) -> None:
     """vLUT matmuls above 32 tokens: the deep kernel (default) or the wide one."""
     call("coset_set_option", OPT_VLUT_DEEP, int(bool(enabled)))
+
+
+def set_gemm_tn_tile(tile: int) -> None:
+    """coset_gemm_tn's output tiles: 0 the plan's choice (64 x 64 where they
+    fit, else 96 x 96), 64 or 96 only that size."""
+    call("coset_set_option", OPT_GEMM_TN_TILE, int(tile))
 
 
 def set_vlut_splits(splits: int) -> None:

@@ -127,6 +127,10 @@ int coset_set_option(int key, int value)
         if (value < 0 || value > 1) return fail(COSET_EINVAL, "vLUT deep %d not in {0,1}", value);
         coset::g_vlut_deep = value;
         return COSET_OK;
+    case COSET_OPT_GEMM_TN_TILE:
+        if (value != 0 && value != 64 && value != 96) return fail(COSET_EINVAL, "gemm_tn tile %d not in {0,64,96}", value);
+        coset::g_gemm_tn_tile = value;
+        return COSET_OK;
     default: return fail(COSET_EINVAL, "unknown option %d", key);
     }
 }

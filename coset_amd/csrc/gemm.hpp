@@ -21,9 +21,12 @@ struct GemmTnPlan {
     int my;
 };
 
-// The plan for this shape: M, N multiples of 64 with at most 256 tiles of 64 x 64,
-// K = 256 * splits * my for my in {4, 8, 16, 32}.
+// The plan for this shape: tiles of 64 x 64 (M, N multiples of 64, at most 256
+// tiles) where they fit, else of 96 x 96 (multiples of 96, at most 256
+// tiles), K = 256 * splits * my for my in {4, 8, 16, 32}.
 GemmTnPlan gemm_tn_plan(int64_t M, int64_t N, int64_t K);
+// 0 (default): the plan's choice of tile; 64 or 96: only that tile size
+extern int g_gemm_tn_tile;
 // fp32 workspace the plan needs (splits x (M x N + M), or 0)
 int64_t gemm_tn_workspace_floats(const GemmTnPlan& p, int64_t M, int64_t N);
 

@@ -45,23 +45,30 @@ typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
 typedef __attribute__((address_space(3))) char lds_char_t;
 
-constexpr int kTnTile = 64;     // output rows and columns per workgroup
 constexpr int kTnWaves = 8;     // waves per workgroup
 constexpr int kTnD = 1;         // slices in flight per wave, in registers while the previous one is multiplied from LDS
 constexpr int kTnSlice = 32;    // tokens per slice (one MFMA K step)
+constexpr int kTnCsCols = 64;   // columns of A per column-sum workgroup
 
-// LDS row pitch (bytes) of a 64-wide operand slice: 128 bytes + 32, so the
+// The layout of one output tile size T (64 or 96 rows and columns per
+// workgroup).  LDS row pitch of a T-wide operand slice: 2T bytes + 32, so the
 // four 32-byte row pieces one 16-lane group of a transposing read touches
-// (rows k..k+3) fall in distinct bank windows
-constexpr int kTnPitch = 2 * kTnTile + 32;
-constexpr int kTnWaveLds = 2 * kTnSlice * kTnPitch;              // A and B slices of one wave
-constexpr int kTnLds = kTnWaves * kTnWaveLds;                    // 80 KiB
-constexpr int kTnCh = kTnTile / 8;                               // 16-byte chunks per row
-constexpr int kTnLoads = kTnSlice * kTnCh / 64;                  // loads per lane, slice and operand
-constexpr int kTnMt = kTnTile / 16;                              // MFMA tiles per dimension
-constexpr int kTnRp = kTnTile + 4;                               // epilogue row pitch (floats)
-constexpr int kTnHt = 2;                                         // row tiles per epilogue pass
-static_assert(kTnWaves * 16 * kTnHt * kTnRp * 4 <= kTnLds, "epilogue fits the slices");
+// (rows k..k+3: offsets 0, P, 2P, 3P mod 256 = 0, 160, 64, 224 for T = 64 and
+// 0, 224, 192, 160 for T = 96) fall in distinct bank windows.
+template <int T>
+struct TnShape {
+    static_assert(T == 64 || T == 96, "tile sizes of the kernel");
+    static constexpr int kPitch = 2 * T + 32;
+    static constexpr int kWaveLds = 2 * kTnSlice * kPitch;     // A and B slices of one wave
+    static constexpr int kLds = kTnWaves * kWaveLds;           // 80 KiB (T = 64), 112 KiB (T = 96)
+    static constexpr int kCh = T / 8;                          // 16-byte chunks per row
+    static constexpr int kLoads = kTnSlice * kCh / 64;         // loads per lane, slice and operand
+    static constexpr int kMt = T / 16;                         // MFMA tiles per dimension
+    static constexpr int kRp = T + 4;                          // epilogue row pitch (floats)
+    static constexpr int kHt = 2;                              // row tiles per epilogue pass
+    static_assert(kTnWaves * 16 * kHt * kRp * 4 <= kLds, "epilogue fits the slices");
+    static_assert(kMt % kHt == 0, "whole epilogue passes");
+};
 
 // f(s0 + I, integral_constant<I>) for I = 0, 1, ...: the register slot of each
 // step is a compile-time index
@@ -96,19 +103,22 @@ __device__ __forceinline__ void store8(void* C, int64_t idx, const float v[8])
     }
 }
 
-// Column sums of one 64-column block of A over one split's K range (kRows
-// tokens from k0), for the workgroups past the tiles: thread t sums column
+// Column sums of one 64-column block of A (cols <= 64 of them, M being a
+// multiple of 32) over one split's K range (kRows tokens from k0), for the
+// workgroups past the tiles: thread t sums column
 // chunk t % 8 (8 columns, one 16-byte load per token) over the tokens
 // t / 8, t / 8 + 64, ... in order, 8 loads in flight; then the 64 row groups'
 // sums of each column are added in group order.  Deterministic; fp32.
 template <int MY>
-__device__ __forceinline__ void tn_colsum_block(const uint16_t* __restrict__ A, int64_t lda, int64_t m0, int64_t k0,
-                                                float* __restrict__ out, char* lds)
+__device__ __forceinline__ void tn_colsum_block(const uint16_t* __restrict__ A, int64_t lda, int64_t m0, int cols,
+                                                int64_t k0, float* __restrict__ out, char* lds)
 {
     constexpr int kRows = kTnWaves * MY * kTnSlice;
     constexpr int kIter = kRows / 64;
     const int tid = threadIdx.x, c = tid & 7, rg = tid >> 3;
-    const uint16_t* p = A + (k0 + rg) * lda + m0 + 8 * c;
+    // a last block of cols < 64 columns: the chunks past it re-read chunk 0
+    // (inside the matrix) and their sums are not used
+    const uint16_t* p = A + (k0 + rg) * lda + m0 + (8 * c < cols ? 8 * c : 0);
     float s[8];
 #pragma unroll
     for (int q = 0; q < 8; ++q) s[q] = 0.f;
@@ -123,11 +133,11 @@ __device__ __forceinline__ void tn_colsum_block(const uint16_t* __restrict__ A, 
     }
     float* red = reinterpret_cast<float*>(lds);   // [64 row groups][64 columns]
 #pragma unroll
-    for (int q = 0; q < 8; ++q) red[rg * kTnTile + 8 * c + q] = s[q];
+    for (int q = 0; q < 8; ++q) red[rg * kTnCsCols + 8 * c + q] = s[q];
     __syncthreads();
-    if (tid < kTnTile) {
+    if (tid < cols) {
         float v = red[tid];
-        for (int grp = 1; grp < 64; ++grp) v += red[grp * kTnTile + tid];
+        for (int grp = 1; grp < 64; ++grp) v += red[grp * kTnCsCols + tid];
         out[m0 + tid] = v;
     }
 }
@@ -140,23 +150,24 @@ __device__ __forceinline__ void tn_colsum_block(const uint16_t* __restrict__ A, 
 // tiles, one per 64-column block and split (tn_colsum_block); they run beside
 // the tiles on CUs the tiles leave free.  fp32 to colsum (one split) or split
 // blockIdx.y's partial to colsum + blockIdx.y * M.
-template <int OUT, int MY, bool CS>
+template <int T, int OUT, int MY, bool CS>
 __global__ void __launch_bounds__(kTnWaves * 64) gemm_tn_kernel(const uint16_t* __restrict__ A, int64_t lda,
                                                                 const uint16_t* __restrict__ B, int64_t ldb,
                                                                 void* __restrict__ C, int64_t ldc, int64_t M,
                                                                 int tiles_n, int xcd_m, int xcd_n,
                                                                 float* __restrict__ colsum)
 {
-    __shared__ __align__(16) char lds[kTnLds];
+    using S = TnShape<T>;
+    __shared__ __align__(16) char lds[S::kLds];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, r = lane & 15;
 
-    if (CS && (int64_t)blockIdx.x >= (M / kTnTile) * tiles_n) {
-        const int64_t cb = (int64_t)blockIdx.x - (M / kTnTile) * tiles_n;
+    if (CS && (int64_t)blockIdx.x >= (M / T) * tiles_n) {
+        const int64_t cb = (int64_t)blockIdx.x - (M / T) * tiles_n;
         // past the blocks: padding that keeps the grid a multiple of 8
-        if (cb < M / kTnTile)
-            tn_colsum_block<MY>(A, lda, cb * kTnTile, (int64_t)blockIdx.y * kTnWaves * MY * kTnSlice,
+        if (cb * kTnCsCols < M)
+            tn_colsum_block<MY>(A, lda, cb * kTnCsCols, (int)std::min<int64_t>(kTnCsCols, M - cb * kTnCsCols), (int64_t)blockIdx.y * kTnWaves * MY * kTnSlice,
                                 colsum + (OUT == 2 ? (int64_t)blockIdx.y * M : 0), lds);
         return;
     }
@@ -173,58 +184,58 @@ __global__ void __launch_bounds__(kTnWaves * 64) gemm_tn_kernel(const uint16_t* 
         tm = blockIdx.x / tiles_n;
         tn = blockIdx.x % tiles_n;
     }
-    const int64_t m0 = (int64_t)tm * kTnTile, n0 = (int64_t)tn * kTnTile;
+    const int64_t m0 = (int64_t)tm * T, n0 = (int64_t)tn * T;
     // this wave's slices: k = (blockIdx.y * kTnWaves * MY + wave + i * kTnWaves) * 32, i < MY
     const int64_t k_wave = ((int64_t)blockIdx.y * kTnWaves * MY + wave) * kTnSlice;
 
-    // a slice is 32 rows of 128 bytes per operand: chunk e = j * 64 + lane is
-    // row e / 8, 16-byte piece e % 8 (a wave load covers 8 whole rows)
-    u32x4_t ra[kTnD][kTnLoads], rb[kTnD][kTnLoads];
-    auto gload = [&](int i, u32x4_t (&xa)[kTnLoads], u32x4_t (&xb)[kTnLoads]) __attribute__((always_inline)) {
+    // a slice is 32 rows of 2T bytes per operand: chunk e = j * 64 + lane is
+    // row e / (T / 8), 16-byte piece e % (T / 8)
+    u32x4_t ra[kTnD][S::kLoads], rb[kTnD][S::kLoads];
+    auto gload = [&](int i, u32x4_t (&xa)[S::kLoads], u32x4_t (&xb)[S::kLoads]) __attribute__((always_inline)) {
         const int ii = i < MY ? i : MY - 1;   // past the last slice: repeat it (loaded, never used)
         const int64_t k0 = k_wave + (int64_t)ii * kTnWaves * kTnSlice;
 #pragma unroll
-        for (int j = 0; j < kTnLoads; ++j) {
-            const int e = j * 64 + lane, row = e / kTnCh, c = e % kTnCh;
+        for (int j = 0; j < S::kLoads; ++j) {
+            const int e = j * 64 + lane, row = e / S::kCh, c = e % S::kCh;
             xa[j] = *reinterpret_cast<const u32x4_t*>(A + (k0 + row) * lda + m0 + 8 * c);
             xb[j] = *reinterpret_cast<const u32x4_t*>(B + (k0 + row) * ldb + n0 + 8 * c);
         }
     };
-    char* wl = lds + wave * kTnWaveLds;
-    auto swrite = [&](const u32x4_t (&xa)[kTnLoads], const u32x4_t (&xb)[kTnLoads]) __attribute__((always_inline)) {
+    char* wl = lds + wave * S::kWaveLds;
+    auto swrite = [&](const u32x4_t (&xa)[S::kLoads], const u32x4_t (&xb)[S::kLoads]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int j = 0; j < kTnLoads; ++j) {
-            const int e = j * 64 + lane, row = e / kTnCh, c = e % kTnCh;
-            *reinterpret_cast<u32x4_t*>(wl + row * kTnPitch + 16 * c) = xa[j];
-            *reinterpret_cast<u32x4_t*>(wl + (kTnSlice + row) * kTnPitch + 16 * c) = xb[j];
+        for (int j = 0; j < S::kLoads; ++j) {
+            const int e = j * 64 + lane, row = e / S::kCh, c = e % S::kCh;
+            *reinterpret_cast<u32x4_t*>(wl + row * S::kPitch + 16 * c) = xa[j];
+            *reinterpret_cast<u32x4_t*>(wl + (kTnSlice + row) * S::kPitch + 16 * c) = xb[j];
         }
     };
 
-    f32x4_t acc[kTnMt][kTnMt];
+    f32x4_t acc[S::kMt][S::kMt];
 #pragma unroll
-    for (int i = 0; i < kTnMt; ++i)
+    for (int i = 0; i < S::kMt; ++i)
 #pragma unroll
-        for (int j = 0; j < kTnMt; ++j) acc[i][j] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < S::kMt; ++j) acc[i][j] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
 
     // two transposing reads per operand tile: rows (tokens) 8 g + r / 4 and 4
     // more, columns 16 i + 4 (r % 4)
-    const lds_char_t* rbase = (const lds_char_t*)wl + (8 * g + (r >> 2)) * kTnPitch + 8 * (r & 3);
+    const lds_char_t* rbase = (const lds_char_t*)wl + (8 * g + (r >> 2)) * S::kPitch + 8 * (r & 3);
     auto compute = [&]() __attribute__((always_inline)) {
-        s16x4_t a[kTnMt][2], b[kTnMt][2];
+        s16x4_t a[S::kMt][2], b[S::kMt][2];
 #pragma unroll
-        for (int i = 0; i < kTnMt; ++i)
+        for (int i = 0; i < S::kMt; ++i)
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                a[i][h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(rbase + h * 4 * kTnPitch + 32 * i));
+                a[i][h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(rbase + h * 4 * S::kPitch + 32 * i));
                 b[i][h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (lds_s16x4_t*)(rbase + (kTnSlice + h * 4) * kTnPitch + 32 * i));
+                    (lds_s16x4_t*)(rbase + (kTnSlice + h * 4) * S::kPitch + 32 * i));
             }
 #pragma unroll
-        for (int i = 0; i < kTnMt; ++i) {
+        for (int i = 0; i < S::kMt; ++i) {
             const bf16x8_gt av =
                 __builtin_bit_cast(bf16x8_gt, __builtin_shufflevector(a[i][0], a[i][1], 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
-            for (int j = 0; j < kTnMt; ++j) {
+            for (int j = 0; j < S::kMt; ++j) {
                 const bf16x8_gt bv =
                     __builtin_bit_cast(bf16x8_gt, __builtin_shufflevector(b[j][0], b[j][1], 0, 1, 2, 3, 4, 5, 6, 7));
                 acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc[i][j], 0, 0, 0);
@@ -249,27 +260,27 @@ __global__ void __launch_bounds__(kTnWaves * 64) gemm_tn_kernel(const uint16_t* 
     for (int i0 = 0; i0 < MY; i0 += kTnD) unroll_steps(step, i0, std::make_integer_sequence<int, kTnD>{});
     __syncthreads();
 
-    // epilogue: the waves' tiles meet in LDS (kTnHt row tiles at a time) and
+    // epilogue: the waves' tiles meet in LDS (S::kHt row tiles at a time) and
     // each output is the sum of the waves' values in wave order
     float* red = reinterpret_cast<float*>(lds);
     void* out = OUT == 2 ? static_cast<void*>(static_cast<float*>(C) + (int64_t)blockIdx.y * M * ldc) : C;
-    for (int i0 = 0; i0 < kTnMt; i0 += kTnHt) {
+    for (int i0 = 0; i0 < S::kMt; i0 += S::kHt) {
         // D[row 4 g + e][column r] of tile (i, j) -> red[wave][16 (i - i0) + 4 g + e][16 j + r]
 #pragma unroll
-        for (int i = 0; i < kTnHt; ++i)
+        for (int i = 0; i < S::kHt; ++i)
 #pragma unroll
-            for (int j = 0; j < kTnMt; ++j)
+            for (int j = 0; j < S::kMt; ++j)
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    red[(wave * 16 * kTnHt + 16 * i + 4 * g + e) * kTnRp + 16 * j + r] = acc[i0 + i][j][e];
+                    red[(wave * 16 * S::kHt + 16 * i + 4 * g + e) * S::kRp + 16 * j + r] = acc[i0 + i][j][e];
         __syncthreads();
-        constexpr int kChunks = 16 * kTnHt * kTnCh;   // 8 consecutive columns each
+        constexpr int kChunks = 16 * S::kHt * S::kCh;   // 8 consecutive columns each
         for (int idx = tid; idx < kChunks; idx += kTnWaves * 64) {
-            const int row = idx / kTnCh, c = idx % kTnCh;
+            const int row = idx / S::kCh, c = idx % S::kCh;
             float v[8];
 #pragma unroll
             for (int w = 0; w < kTnWaves; ++w) {
-                const float4* src = reinterpret_cast<const float4*>(&red[(w * 16 * kTnHt + row) * kTnRp + 8 * c]);
+                const float4* src = reinterpret_cast<const float4*>(&red[(w * 16 * S::kHt + row) * S::kRp + 8 * c]);
                 const float4 x0 = src[0], x1 = src[1];
                 const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
@@ -314,28 +325,28 @@ __global__ void __launch_bounds__(256) gemm_tn_reduce_kernel(const float* __rest
     store8<OUT>(C, (i / N) * ldc + i % N, v);
 }
 
-template <int MY, bool CS>
+template <int T, int MY, bool CS>
 hipError_t launch_tn(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t ldb, void* C, int64_t ldc,
                      int out_bf16, int64_t M, int64_t N, const GemmTnPlan& plan, float* partial, float* colsum,
                      hipStream_t s)
 {
-    const int tiles_n = (int)(N / kTnTile);
+    const int tiles_n = (int)(N / T);
     // the column-sum workgroups, padded to a multiple of 8 so that every
     // split's tiles keep their XCDs
-    const int64_t cs_wg = CS ? (M / kTnTile + 7) / 8 * 8 : 0;
-    const dim3 grid((unsigned)((M / kTnTile) * tiles_n + cs_wg), (unsigned)plan.splits);
+    const int64_t cs_wg = CS ? ((M + kTnCsCols - 1) / kTnCsCols + 7) / 8 * 8 : 0;
+    const dim3 grid((unsigned)((M / T) * tiles_n + cs_wg), (unsigned)plan.splits);
     const dim3 block(kTnWaves * 64);
     if (plan.splits == 1) {
         if (out_bf16)
-            hipLaunchKernelGGL((gemm_tn_kernel<1, MY, CS>), grid, block, 0, s, A, lda, B, ldb, C, ldc, M, tiles_n,
+            hipLaunchKernelGGL((gemm_tn_kernel<T, 1, MY, CS>), grid, block, 0, s, A, lda, B, ldb, C, ldc, M, tiles_n,
                                plan.xcd_m, plan.xcd_n, colsum);
         else
-            hipLaunchKernelGGL((gemm_tn_kernel<0, MY, CS>), grid, block, 0, s, A, lda, B, ldb, C, ldc, M, tiles_n,
+            hipLaunchKernelGGL((gemm_tn_kernel<T, 0, MY, CS>), grid, block, 0, s, A, lda, B, ldb, C, ldc, M, tiles_n,
                                plan.xcd_m, plan.xcd_n, colsum);
         return hipGetLastError();
     }
     // split partials: the tiles' [splits, M, N], then the column sums' [splits, M]
-    hipLaunchKernelGGL((gemm_tn_kernel<2, MY, CS>), grid, block, 0, s, A, lda, B, ldb, (void*)partial, N, M, tiles_n,
+    hipLaunchKernelGGL((gemm_tn_kernel<T, 2, MY, CS>), grid, block, 0, s, A, lda, B, ldb, (void*)partial, N, M, tiles_n,
                        plan.xcd_m, plan.xcd_n, partial + (int64_t)plan.splits * M * N);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -350,24 +361,26 @@ hipError_t launch_tn(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t 
     return hipGetLastError();
 }
 
-template <int MY>
+template <int T, int MY>
 hipError_t launch_tn_cs(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t ldb, void* C, int64_t ldc,
                         int out_bf16, int64_t M, int64_t N, const GemmTnPlan& plan, float* partial, float* colsum,
                         hipStream_t s)
 {
-    return colsum ? launch_tn<MY, true>(A, lda, B, ldb, C, ldc, out_bf16, M, N, plan, partial, colsum, s)
-                  : launch_tn<MY, false>(A, lda, B, ldb, C, ldc, out_bf16, M, N, plan, partial, nullptr, s);
+    return colsum ? launch_tn<T, MY, true>(A, lda, B, ldb, C, ldc, out_bf16, M, N, plan, partial, colsum, s)
+                  : launch_tn<T, MY, false>(A, lda, B, ldb, C, ldc, out_bf16, M, N, plan, partial, nullptr, s);
 }
 
 }  // namespace
 
-GemmTnPlan gemm_tn_plan(int64_t M, int64_t N, int64_t K)
+namespace {
+
+GemmTnPlan plan_for_tile(int64_t M, int64_t N, int64_t K, int T)
 {
     GemmTnPlan p{0, 1, 0, 0, 0};
-    if (M <= 0 || N <= 0 || K <= 0 || M % kTnTile || N % kTnTile) return p;
+    if (M <= 0 || N <= 0 || K <= 0 || M % T || N % T) return p;
     // one round of workgroups (one per CU of MI355X's 256): larger grids are
     // left to the library GEMM, which covers them with larger tiles
-    const int64_t tiles = (M / kTnTile) * (N / kTnTile);
+    const int64_t tiles = (M / T) * (N / T);
     if (tiles > 256) return p;
     // K splits while the tiles leave most CUs idle; each wave then takes MY
     // slices, MY one of the compiled counts
@@ -382,11 +395,11 @@ GemmTnPlan gemm_tn_plan(int64_t M, int64_t N, int64_t K)
         }
     }
     if (p.my == 0) return p;
-    p.tile = kTnTile;
+    p.tile = T;
     p.splits = splits;
     // XCD blocks: 8 blocks of tiles / 8 tiles, the most compact shape (fewest
     // operand panels per block) that tiles the grid
-    const int64_t tm = M / kTnTile, tn = N / kTnTile;
+    const int64_t tm = M / T, tn = N / T;
     if (tiles % 8 == 0) {
         const int64_t per = tiles / 8;
         int64_t best = -1;
@@ -404,6 +417,20 @@ GemmTnPlan gemm_tn_plan(int64_t M, int64_t N, int64_t K)
     return p;
 }
 
+}  // namespace
+
+int g_gemm_tn_tile = 0;
+
+GemmTnPlan gemm_tn_plan(int64_t M, int64_t N, int64_t K)
+{
+    // 64 x 64 tiles where they fit in one round, else 96 x 96 (products of up
+    // to 256 tiles of 96, such as the 3072-wide layers' 768 x 3072 dW: 576
+    // tiles of 64); g_gemm_tn_tile forces one of them
+    if (g_gemm_tn_tile == 64 || g_gemm_tn_tile == 96) return plan_for_tile(M, N, K, g_gemm_tn_tile);
+    const GemmTnPlan p = plan_for_tile(M, N, K, 64);
+    return p.tile > 0 ? p : plan_for_tile(M, N, K, 96);
+}
+
 int64_t gemm_tn_workspace_floats(const GemmTnPlan& p, int64_t M, int64_t N)
 {
     return p.tile > 0 && p.splits > 1 ? (int64_t)p.splits * (M * N + M) : 0;
@@ -414,15 +441,21 @@ hipError_t gemm_tn_bf16(const uint16_t* A, int64_t lda, const uint16_t* B, int64
                         float* colsum, hipStream_t s)
 {
     const int ob = out_dtype == 1;
-    if (plan.tile != kTnTile || (plan.splits > 1 && !workspace)) return hipErrorInvalidValue;
+    if ((plan.tile != 64 && plan.tile != 96) || (plan.splits > 1 && !workspace)) return hipErrorInvalidValue;
     (void)K;   // the plan's slice count fixes the K range of each launch
-    switch (plan.my) {
-    case 4: return launch_tn_cs<4>(A, lda, B, ldb, C, ldc, ob, M, N, plan, workspace, colsum, s);
-    case 8: return launch_tn_cs<8>(A, lda, B, ldb, C, ldc, ob, M, N, plan, workspace, colsum, s);
-    case 16: return launch_tn_cs<16>(A, lda, B, ldb, C, ldc, ob, M, N, plan, workspace, colsum, s);
-    case 32: return launch_tn_cs<32>(A, lda, B, ldb, C, ldc, ob, M, N, plan, workspace, colsum, s);
-    default: return hipErrorInvalidValue;
+#define COSET_TN(TT)                                                                                        \
+    switch (plan.my) {                                                                                      \
+    case 4: return launch_tn_cs<TT, 4>(A, lda, B, ldb, C, ldc, ob, M, N, plan, workspace, colsum, s);      \
+    case 8: return launch_tn_cs<TT, 8>(A, lda, B, ldb, C, ldc, ob, M, N, plan, workspace, colsum, s);      \
+    case 16: return launch_tn_cs<TT, 16>(A, lda, B, ldb, C, ldc, ob, M, N, plan, workspace, colsum, s);    \
+    case 32: return launch_tn_cs<TT, 32>(A, lda, B, ldb, C, ldc, ob, M, N, plan, workspace, colsum, s);    \
+    default: return hipErrorInvalidValue;                                                                   \
     }
+    if (plan.tile == 96) {
+        COSET_TN(96)
+    }
+    COSET_TN(64)
+#undef COSET_TN
 }
 
 }  // namespace coset

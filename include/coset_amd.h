@@ -82,7 +82,8 @@ enum {
     COSET_OPT_FAST_PROJECTION = 4, /* encoders: 1 fast projection where provably exact (default), 0 never */
     COSET_OPT_CODEC_PLAIN = 5,     /* table kernel: 1 fixed-format variant for fp32, beta = 2^k calls (default), 0 never */
     COSET_OPT_CODEC_DYNAMIC = 6,   /* fixed-format table kernel: 1 tiles from a counter run per launch (default), 0 grid stride */
-    COSET_OPT_VLUT_DEEP = 7        /* vLUT matmul above 32 tokens: 1 the 64-row deep kernel (default), 0 the 128-row wide one */
+    COSET_OPT_VLUT_DEEP = 7,       /* vLUT matmul above 32 tokens: 1 the 64-row deep kernel (default), 0 the 128-row wide one */
+    COSET_OPT_GEMM_TN_TILE = 8     /* coset_gemm_tn output tiles: 0 64 x 64 where they fit, else 96 x 96 (default); 64 or 96 only that size */
 };
 
 int coset_abi_version(void);
@@ -206,10 +207,12 @@ int coset_colsum(const void* g, int dtype, int64_t rows, int64_t cols, float* ou
  * order (deterministic); C [M, N] (leading dimension ldc) in fp32
  * (out_dtype COSET_F32) or bf16 rounded to nearest even (COSET_BF16).  Shapes
  * the kernel takes (coset_gemm_tn_supported returns 1 for them): M and N
- * multiples of 64 with (M / 64) (N / 64) <= 256, and K = 256 s m for a power
- * of two s (the K splits the launch plan picks) and m in {4, 8, 16, 32}
- * (e.g. K = 1024 .. 8192 in powers of two); others return
- * COSET_EUNSUPPORTED -- larger products are the library GEMM's.  Buffers
+ * multiples of 64 with (M / 64) (N / 64) <= 256 (64 x 64 output tiles), or
+ * else multiples of 96 with (M / 96) (N / 96) <= 256 (96 x 96 tiles), and
+ * K = 256 s m for a power of two s (the K splits the launch plan picks) and
+ * m in {4, 8, 16, 32} (e.g. K = 1024 .. 8192 in powers of two); others
+ * return COSET_EUNSUPPORTED -- larger products are the library GEMM's
+ * (COSET_OPT_GEMM_TN_TILE restricts the plan to one tile size).  Buffers
  * 16-byte aligned, lda, ldb, ldc multiples of 8.  colsum (nullable): also
  * colsum[m] = sum_k A[k, m], fp32, fixed order -- with A = gy, the bias
  * gradient of the same F.linear, in the same pass.  workspace: caller-owned

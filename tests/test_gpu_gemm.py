@@ -16,15 +16,28 @@ from coset_amd import _lib, layers
 
 pytestmark = pytest.mark.gpu
 
+# (M, N, K, tile): tile 0 is the plan's own choice, 64 or 96 forced
 SHAPES = [
-    (768, 768, 4096),    # C5 768 -> 768: 144 tiles, one split, XCD blocks 3 x 6
-    (512, 512, 4096),    # 64 tiles: 4 K splits and the ordered reduce
-    (2048, 512, 2048),   # 256 tiles, one split
-    (1024, 1024, 1024),  # 256 tiles, 4 slices per wave
-    (64, 64, 8192),      # one tile: 8 K splits
-    (192, 320, 2048),    # 15 tiles: no XCD blocks, 2 K splits
-    (128, 64, 4096),     # 2 tiles: 4 K splits
+    (768, 768, 4096, 0),     # C5 768 -> 768: 144 tiles of 64 x 64, one split, XCD blocks 3 x 6
+    (768, 768, 4096, 96),    # the same on 64 tiles of 96 x 96, 4 K splits and the ordered reduce
+    (3072, 768, 4096, 0),    # C5 768 -> 3072: 256 tiles of 96 x 96, one split, XCD blocks 4 x 8
+    (768, 3072, 4096, 0),    # C5 3072 -> 768: the transposed grid
+    (512, 512, 4096, 0),     # 64 tiles of 64 x 64: 4 K splits
+    (2048, 512, 2048, 0),    # 256 tiles, one split
+    (1024, 1024, 1024, 0),   # 256 tiles, 4 slices per wave
+    (64, 64, 8192, 0),       # one tile: 8 K splits
+    (192, 320, 2048, 0),     # 15 tiles: no XCD blocks, 2 K splits
+    (128, 64, 4096, 0),      # 2 tiles: 4 K splits
+    (96, 96, 8192, 0),       # one 96 x 96 tile: 8 K splits
+    (288, 480, 2048, 96),    # 15 tiles of 96 x 96: no XCD blocks, 2 K splits
 ]
+
+
+@pytest.fixture
+def tile():
+    yield
+    _lib.set_gemm_tn_tile(0)
+
 
 def _workspace(M, N, K):
     need = int(_lib.load().coset_gemm_tn_workspace_floats(M, N, K))
@@ -53,9 +66,10 @@ def _int_operands(K, M, N, seed):
     return a, b, exact
 
 
-@pytest.mark.parametrize("M,N,K", SHAPES)
-def test_integer_operands_exact(M, N, K):
-    print(f"gemm_tn exact M={M} N={N} K={K}", flush=True)
+@pytest.mark.parametrize("M,N,K,T", SHAPES)
+def test_integer_operands_exact(M, N, K, T, tile):
+    print(f"gemm_tn exact M={M} N={N} K={K} tile={T}", flush=True)
+    _lib.set_gemm_tn_tile(T)
     assert _lib.load().coset_gemm_tn_supported(M, N, K) == 1
     a, b, exact = _int_operands(K, M, N, seed=M + N + K)
     c32 = _tn(a, b, torch.float32)
@@ -67,9 +81,11 @@ def test_integer_operands_exact(M, N, K):
     assert torch.equal(cs.double(), a.double().sum(0)), "column sums differ"
 
 
-@pytest.mark.parametrize("M,N,K", [(768, 768, 4096), (512, 512, 4096)])
-def test_gaussian_operands_within_fp32_bound(M, N, K):
-    print(f"gemm_tn gaussian M={M} N={N} K={K}", flush=True)
+@pytest.mark.parametrize("M,N,K,T", [(768, 768, 4096, 0), (768, 768, 4096, 96), (512, 512, 4096, 0),
+                                     (3072, 768, 4096, 0)])
+def test_gaussian_operands_within_fp32_bound(M, N, K, T, tile):
+    print(f"gemm_tn gaussian M={M} N={N} K={K} tile={T}", flush=True)
+    _lib.set_gemm_tn_tile(T)
     g = torch.Generator(device="cuda").manual_seed(9)
     a = torch.randn((K, M), device="cuda", generator=g).to(torch.bfloat16)
     b = torch.randn((K, N), device="cuda", generator=g).to(torch.bfloat16)
@@ -88,7 +104,8 @@ def test_gaussian_operands_within_fp32_bound(M, N, K):
 def test_strided_operands():
     """Leading dimensions wider than the matrix (views into wider buffers)."""
     print("gemm_tn strided", flush=True)
-    for K, M, N in ((1024, 128, 192), (4096, 64, 128)):   # one split; 4 splits and the reduce
+    # one split; 4 splits and the reduce; 96 x 96 tiles with 2 splits
+    for K, M, N in ((1024, 128, 192), (4096, 64, 128), (2048, 192, 288)):
         a_full, b_full, _ = _int_operands(K, M + 32, N + 64, seed=3)
         a, b = a_full[:, 16:16 + M], b_full[:, 8:8 + N]
         exact = a.double().t() @ b.double()
@@ -103,7 +120,7 @@ def test_strided_operands():
         assert torch.isnan(out[:, N:]).all(), "wrote past the output columns"
 
 
-def test_workspace_refusals():
+def test_workspace_refusals(tile):
     """A split plan without (enough) workspace is refused before any launch."""
     lib = _lib.load()
     M, N, K = 512, 512, 4096
@@ -116,16 +133,25 @@ def test_workspace_refusals():
         rc = lib.coset_gemm_tn(a.data_ptr(), M, a.data_ptr(), N, out.data_ptr(), N, _lib.BF16, M, N, K, 0, ptr, n,
                                _lib.stream_of(a))
         assert rc == -1, rc
-    assert int(lib.coset_gemm_tn_workspace_floats(768, 768, 4096)) == 0   # 144 tiles: no split
+    assert int(lib.coset_gemm_tn_workspace_floats(768, 768, 4096)) == 0     # 144 tiles of 64: no split
+    assert int(lib.coset_gemm_tn_workspace_floats(3072, 768, 4096)) == 0    # 256 tiles of 96: no split
+    _lib.set_gemm_tn_tile(96)
+    assert int(lib.coset_gemm_tn_workspace_floats(768, 768, 4096)) == 4 * (768 * 768 + 768)   # 64 tiles of 96
 
 
-def test_unsupported_shapes_refused():
+def test_unsupported_shapes_refused(tile):
     lib = _lib.load()
     # not multiples of 64, K not 256 * 2^s * {4, 8, 16, 32}, more than 256
-    # tiles (the C5 3072-wide layers: the library GEMM takes those)
+    # tiles of either size (the library GEMM takes those)
     for M, N, K in ((770, 768, 4096), (768, 768, 4000), (768, 10, 4096), (0, 768, 4096), (768, 768, 768),
-                    (3072, 768, 4096), (768, 3072, 4096)):
+                    (3072, 3072, 4096), (1536, 1920, 4096)):
         assert lib.coset_gemm_tn_supported(M, N, K) == 0, (M, N, K)
+    # the 3072-wide C5 layers: 256 tiles of 96 x 96, 576 of 64 x 64
+    assert lib.coset_gemm_tn_supported(3072, 768, 4096) == 1
+    _lib.set_gemm_tn_tile(64)
+    assert lib.coset_gemm_tn_supported(3072, 768, 4096) == 0
+    _lib.set_gemm_tn_tile(96)
+    assert lib.coset_gemm_tn_supported(512, 512, 4096) == 0
     a = torch.zeros((4000, 768), dtype=torch.bfloat16, device="cuda")
     assert layers.gemm_tn(a, a) is None
 
