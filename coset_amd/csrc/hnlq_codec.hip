@@ -302,8 +302,8 @@ __global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
     }
 }
 
-// The layer quantizer's round trip with stored per-row betas (SCALE_LAYER:
-// HNLQLinearQAT._quantize_weights, coset/core/layers.py:428-463) for
+// The layer quantizer's round trip with per-row betas, stored or derived from
+// theta (SCALE_LAYER: HNLQLinearQAT._quantize_weights, coset/core/layers.py:428-463) for
 // q = 8, 16 and M <= 4, with the level count and input dtype fixed at
 // compile time, so a block runs straight through without the generic
 // kernel's per-call branches and the register copies at their joins:
@@ -320,7 +320,7 @@ __global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
 //    condition); the sums are finite, so no quotient is NaN.  Other betas
 //    (zero, tiny, huge, non-finite) take the IEEE divide and torch.clamp's NaN
 //    rule, as the generic kernel does for every block.
-template <int Q, int M, bool XBF16>
+template <int Q, int M, bool XBF16, bool THETA>
 __global__ void __launch_bounds__(256) hnlq_layer_rt_kernel(CodecArgs a)
 {
     static_assert(Q == 8 || Q == 16, "residual_dyadic's q within the codec's q <= 16");
@@ -332,11 +332,34 @@ __global__ void __launch_bounds__(256) hnlq_layer_rt_kernel(CodecArgs a)
     // the decode table of dyadic_level_acc, one entry per Z + 2q
     __shared__ uint4 s_tab[7 * Q];
     if (threadIdx.x < 7 * Q) s_tab[threadIdx.x] = dyadic_table_entry<Q>((int)threadIdx.x - 2 * Q);
+    // THETA: the betas of the rows this workgroup's blocks span (rows of at
+    // least 64 blocks: kWgTiles of them at most), derived from theta once
+    // per row as the generic kernel does, and recorded with d beta / d theta
+    // by the workgroup holding the row's first block
+    __shared__ float s_beta[THETA ? kWgTiles : 1];
+    const int64_t b0 = (int64_t)blockIdx.x * blockDim.x;
+    uint32_t t0 = 0;
+    if constexpr (THETA) {
+        t0 = u32div((uint32_t)b0, a.row_div);
+        const int64_t t = (int64_t)t0 + threadIdx.x;
+        if (threadIdx.x < kWgTiles && t * a.blocks_per_row < a.n) {
+            float lo, hi, sg;
+            theta_beta_terms(a.tb, t, &lo, &hi, &sg);
+            const float span = __fsub_rn(hi, lo);
+            s_beta[threadIdx.x] = __fadd_rn(lo, __fmul_rn(sg, span));
+            const int64_t first = t * a.blocks_per_row;
+            if (first >= b0 && first < b0 + blockDim.x) {
+                if (a.beta_out) a.beta_out[t] = s_beta[threadIdx.x];
+                if (a.dbdt_out) a.dbdt_out[t] = __fmul_rn(__fmul_rn(span, __fsub_rn(1.f, sg)), sg);
+            }
+        }
+    }
     __syncthreads();
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t i = b0 + threadIdx.x;
     if (i == 0 && a.step_counter) *a.step_counter += 1;
     if (i >= a.n) return;
-    const float beta = a.beta_row[u32div((uint32_t)i, a.row_div)];
+    const uint32_t row = u32div((uint32_t)i, a.row_div);
+    const float beta = THETA ? s_beta[row - t0] : a.beta_row[row];
     float xl[8];
     if constexpr (XBF16) {
         const uint4 v = reinterpret_cast<const uint4*>(a.x)[i];
@@ -416,7 +439,10 @@ __global__ void __launch_bounds__(256) hnlq_layer_rt_kernel(CodecArgs a)
 // g_codec_plain = 0 keeps them on the generic kernel.
 static bool layer_rt_supported(const CodecArgs& a, int mode)
 {
-    return g_codec_plain && a.fast_projection && mode == MODE_ROUNDTRIP && a.scale_mode == SCALE_LAYER && !a.use_theta && a.beta_row &&
+    // betas stored per row, or derived from theta per row of at least 64
+    // blocks (fp32 weights: the layer quantizer's input)
+    const bool betas = a.use_theta ? a.blocks_per_row >= 64 && a.x_dtype == DT_F32 : a.beta_row != nullptr;
+    return g_codec_plain && a.fast_projection && mode == MODE_ROUNDTRIP && a.scale_mode == SCALE_LAYER && betas &&
            (a.q == 8 || a.q == 16) && a.M >= 1 && a.M <= 4 && !a.dither && !a.codes_f32 &&
            (a.x_dtype == DT_F32 || a.x_dtype == DT_BF16) && (a.out_dtype == DT_F32 || a.out_dtype == DT_BF16) &&
            a.clip > 0.f && a.n <= (int64_t)0xffffffffLL && a.blocks_per_row >= 1 &&
@@ -435,9 +461,10 @@ static hipError_t launch_layer_rt(const CodecArgs& args, hipStream_t s)
     a.row_div = u32div_of((uint32_t)a.blocks_per_row);
     const dim3 grid((unsigned)((a.n + 255) / 256)), block(256);
     const bool bf = a.x_dtype == DT_BF16;
-#define COSET_LAYER(QQ, MM)                                                                        \
-    if (bf) hipLaunchKernelGGL((hnlq_layer_rt_kernel<QQ, MM, true>), grid, block, 0, s, a);       \
-    else hipLaunchKernelGGL((hnlq_layer_rt_kernel<QQ, MM, false>), grid, block, 0, s, a);         \
+#define COSET_LAYER(QQ, MM)                                                                          \
+    if (a.use_theta) hipLaunchKernelGGL((hnlq_layer_rt_kernel<QQ, MM, false, true>), grid, block, 0, s, a); \
+    else if (bf) hipLaunchKernelGGL((hnlq_layer_rt_kernel<QQ, MM, true, false>), grid, block, 0, s, a);     \
+    else hipLaunchKernelGGL((hnlq_layer_rt_kernel<QQ, MM, false, false>), grid, block, 0, s, a);            \
     break;
 #define COSET_LAYER_Q(QQ)                     \
     switch (a.M) {                            \

@@ -407,3 +407,42 @@ def test_fused_quantizer_writes_the_bias_cast(rows, cols):
     assert torch.equal(bc.view(torch.int16)[~ref.isnan()], ref.view(torch.int16)[~ref.isnan()])
     assert torch.equal(bc.isnan(), ref.isnan())
     assert torch.equal(Wq, Wq2) and torch.equal(packed, packed2) and torch.equal(beta, beta2)
+
+
+@pytest.mark.parametrize("q,M", [(8, 2), (16, 2), (16, 3), (16, 4)])
+def test_theta_quantizer_layer_kernel_matches_generic(q, M):
+    """The fused quantizer with beta from theta at q = 8, 16 on the layer
+    round-trip kernel (betas derived once per row in the workgroup, the table
+    decode, dec / beta from one reciprocal) against the generic kernel
+    (set_codec_plain(False)), bit for bit: W_q in fp32 and bf16, the level
+    words, beta, d beta / d theta, the step counter and the bias cast; rows
+    of 64 (the least the per-workgroup betas take), 96 and 384 blocks, and a
+    row count that ends inside a workgroup."""
+    from coset_amd import _lib
+    from coset_amd.layers import qat_fwd_theta
+    for rows, cols in ((37, 512), (768, 768), (96, 3072)):
+        g = torch.Generator(device="cuda").manual_seed(rows * 7 + cols + q + M)
+        W = 0.02 * torch.randn((rows, cols), device="cuda", generator=g)
+        W[0, :8] = 0.0
+        theta = 3 * torch.randn(rows, device="cuda", generator=g)
+        sigma = 0.02 * (0.5 + torch.rand(rows, device="cuda", generator=g))
+        xmax = 4 * sigma
+        bias = torch.randn(rows, device="cuda", generator=g)
+        for odt in (torch.float32, torch.bfloat16):
+            res = []
+            for plain in (True, False):
+                _lib.set_codec_plain(plain)
+                try:
+                    sc = torch.zeros((), dtype=torch.int64, device="cuda")
+                    out = qat_fwd_theta(W, theta, sigma, xmax, sc, (1.5, 0.1, 1 / 12.0, M), q, M, 2.0, cols // 8, odt,
+                                        bias=bias)
+                    res.append([t.clone() for t in out] + [sc.clone()])
+                finally:
+                    _lib.set_codec_plain(True)
+            case = f"q={q} M={M} rows={rows} cols={cols} {odt}"
+            for a, b in zip(res[0], res[1]):
+                if a.dtype in (torch.float32, torch.bfloat16):
+                    a, b = a.view(torch.int32 if a.dtype == torch.float32 else torch.int16), \
+                        b.view(torch.int32 if b.dtype == torch.float32 else torch.int16)
+                assert torch.equal(a, b), case
+            assert int(res[0][-1]) == 1, case
