@@ -498,4 +498,15 @@ __host__ __device__ inline void dyadic_level_acc(const int b[8], const uint4* ta
     }
 }
 
+// residual_dyadic<Q>(b) through the table (the same values, +0 for zero): for
+// the decoders whose levels accumulate in fp32.
+template <int Q>
+__host__ __device__ inline void residual_table(const int b[8], const uint4* tab, float r[8])
+{
+    int r2[8];
+    dyadic_level_acc<Q, true>(b, tab, 0, r2);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = 0.5f * (float)(r2[i] - Q);
+}
+
 }  // namespace coset

@@ -72,6 +72,13 @@ __global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i == 0 && a.step_counter) *a.step_counter += 1;
     if (a.aux_out && i < a.aux_n) aux_cast(a, i);
+    // q = 8, 16: the decode table of residual_table, one entry per Z + 2q
+    constexpr bool kRtab = (Q == 8 || Q == 16) && MODE != MODE_ENCODE;
+    __shared__ uint4 s_rtab[kRtab ? 7 * Q : 1];
+    if constexpr (kRtab) {
+        if (threadIdx.x < 7 * Q) s_rtab[threadIdx.x] = dyadic_table_entry<Q>((int)threadIdx.x - 2 * Q);
+        __syncthreads();
+    }
     const int q = Q > 0 ? Q : a.q;
     const float qf = (float)q;
     const int M = MM > 0 ? MM : a.M;
@@ -215,8 +222,8 @@ __global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
                     two_r_tables<Q>(word, a.dec_map, a.dec_coarse, r2);
 #pragma unroll
                     for (int j = 0; j < 8; ++j) r[j] = 0.5f * (float)r2[j];
-                } else if constexpr (Q == 8 || Q == 16 || Q == 32) {
-                    residual_dyadic<Q>(b, r);  // both distance rules agree on this grid
+                } else if constexpr (kRtab) {
+                    residual_table<Q>(b, s_rtab, r);  // both distance rules agree on this grid
                 } else {
                     if (a.strided)
                         level_residual<true, Q>(b, qf, r);
@@ -255,8 +262,8 @@ __global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
                 }
                 int b[8];
                 unpack_word<Q>(word, q, b);
-                if constexpr (Q == 8 || Q == 16 || Q == 32) {
-                    residual_dyadic<Q>(b, r);
+                if constexpr (kRtab) {
+                    residual_table<Q>(b, s_rtab, r);
                     add_level<Q>(acc, w, r);
                     w = __fmul_rn(w, qf);
                     continue;

@@ -46,9 +46,26 @@ __device__ __forceinline__ void write_dtheta(const QatBwdArgs& a, int64_t t, flo
     if (a.dbdt) a.dtheta[t] = __fmul_rn(dbeta, a.dbdt[t]);
 }
 
+// q = 8, 16: each workgroup's decode table of residual_table (built at the
+// kernel's start), else unused
+template <int Q>
+struct BwdTab {
+    static constexpr bool kOn = Q == 8 || Q == 16;
+    static constexpr int kEntries = kOn ? 7 * Q : 1;
+};
+
+template <int Q>
+__device__ __forceinline__ void build_bwd_tab(uint4* tab)
+{
+    if constexpr (BwdTab<Q>::kOn) {
+        if (threadIdx.x < 7 * Q) tab[threadIdx.x] = dyadic_table_entry<Q>((int)threadIdx.x - 2 * Q);
+        __syncthreads();
+    }
+}
+
 // Unscaled quantized block Q = sum_m q^m r_m from packed words.
 template <int Q>
-__device__ __forceinline__ void decode_q(const QatBwdArgs& a, int64_t blk, float out[8])
+__device__ __forceinline__ void decode_q(const QatBwdArgs& a, int64_t blk, const uint4* tab, float out[8])
 {
     const int q = Q > 0 ? Q : a.q;
     const float qf = (float)q;
@@ -85,7 +102,9 @@ __device__ __forceinline__ void decode_q(const QatBwdArgs& a, int64_t blk, float
             int b[8];
             float r[8];
             unpack_word<Q>(w, q, b);
-            if (Q == 8 || Q == 16 || Q == 32 || !a.strided)  // both rules agree on the dyadic grid
+            if constexpr (BwdTab<Q>::kOn)  // both rules agree on the dyadic grid
+                residual_table<Q>(b, tab, r);
+            else if (!a.strided)
                 level_residual<false, Q>(b, qf, r);
             else
                 level_residual<true, Q>(b, qf, r);
@@ -99,10 +118,10 @@ __device__ __forceinline__ void decode_q(const QatBwdArgs& a, int64_t blk, float
 
 // Gradients of one block; returns its dbeta contribution.
 template <int Q>
-__device__ __forceinline__ float block_grad(const QatBwdArgs& a, int64_t blk, float beta)
+__device__ __forceinline__ float block_grad(const QatBwdArgs& a, int64_t blk, float beta, const uint4* tab)
 {
     float Qv[8], g[8], w[8];
-    decode_q<Q>(a, blk, Qv);
+    decode_q<Q>(a, blk, tab, Qv);
     if (a.g_dtype == DT_BF16) {
         uint4 v = reinterpret_cast<const uint4*>(a.g)[blk];
         uint32_t u[4] = {v.x, v.y, v.z, v.w};
@@ -143,11 +162,14 @@ __device__ __forceinline__ float block_grad(const QatBwdArgs& a, int64_t blk, fl
 template <int Q>
 __global__ void __launch_bounds__(256) qat_bwd_tile_kernel(QatBwdArgs a)
 {
+    __shared__ uint4 s_tab[BwdTab<Q>::kEntries];
+    build_bwd_tab<Q>(s_tab);
     const int64_t tile = blockIdx.x;
     const float beta = a.beta[tile];
     const int64_t b0 = tile * a.blocks_per_tile;
     float part = 0.f;
-    for (int64_t k = threadIdx.x; k < a.blocks_per_tile; k += blockDim.x) part += block_grad<Q>(a, b0 + k, beta);
+    for (int64_t k = threadIdx.x; k < a.blocks_per_tile; k += blockDim.x)
+        part += block_grad<Q>(a, b0 + k, beta, s_tab);
     // wave reduction, then across the 4 waves
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) part += __shfl_down(part, off, 64);
@@ -164,9 +186,11 @@ __global__ void __launch_bounds__(256) qat_bwd_tile_kernel(QatBwdArgs a)
 template <int Q>
 __global__ void __launch_bounds__(256) qat_bwd_block_kernel(QatBwdArgs a)
 {
+    __shared__ uint4 s_tab[BwdTab<Q>::kEntries];
+    build_bwd_tab<Q>(s_tab);
     int64_t blk = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (blk >= a.n_blocks) return;
-    float db = block_grad<Q>(a, blk, a.beta[blk]);
+    float db = block_grad<Q>(a, blk, a.beta[blk], s_tab);
     a.dbeta[blk] = db;
     write_dtheta(a, blk, db);
 }
