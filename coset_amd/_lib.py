@@ -42,6 +42,8 @@ SIGNATURES = {
     "coset_e8_qat_fwd_theta": [_vp, _i64, _i64, _i64, _vp, _vp, _vp, ctypes.c_double, ctypes.c_double,
                                ctypes.c_double, _int, _flt, _int, _int, _vp, _int, _vp, _vp, _vp, _vp, _vp,
                                _vp, _vp],
+    "coset_e8_qat_head_fwd": [_vp, _i64, _i64, _vp, _vp, _vp, ctypes.c_double, ctypes.c_double, ctypes.c_double,
+                              _int, _flt, _int, _vp, _i64, _vp, _vp, _vp, _vp],
     "coset_e8_qat_bwd_theta": [_vp, _int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _flt, _int, _int, _vp, _vp, _vp,
                                _vp],
     "coset_vlut_build_one_sided": [_vp, _i64, _int, _int, _vp, _vp],

@@ -420,6 +420,27 @@ int coset_e8_qat_fwd_theta(const float* W, int64_t rows, int64_t cols, int64_t b
     return check_hip(coset::launch_codec(a, coset::MODE_ROUNDTRIP, (hipStream_t)stream), "qat forward launch");
 }
 
+int coset_e8_qat_head_fwd(const float* W, int64_t rows, int64_t cols, const float* theta, const float* sigma_ema,
+                          const float* xmax_ema, double delta0, double eta, double gamma_inv, int M_bounds, float clip,
+                          int q, const float* x, int64_t tokens, const float* bias, float* y, int64_t* step_counter,
+                          void* stream)
+{
+    if (rows < 0 || tokens < 0) return fail(COSET_EINVAL, "negative size");
+    if (q != 2 && q != 4) return fail(COSET_EUNSUPPORTED, "the fused layer forward takes q = 2, 4, got %d", q);
+    if (cols <= 0 || cols % 8 || cols > 8192) return fail(COSET_EUNSUPPORTED, "cols=%lld: 8k <= 8192", (long long)cols);
+    if (tokens > 64) return fail(COSET_EUNSUPPORTED, "tokens=%lld > 64", (long long)tokens);
+    if (M_bounds < 1 || M_bounds > 16) return fail(COSET_EINVAL, "M_bounds=%d", M_bounds);
+    if (rows == 0 || tokens == 0) return COSET_OK;
+    if (!W || !theta || !sigma_ema || !xmax_ema || !x || !y) return fail(COSET_EINVAL, "NULL buffer");
+    if (!aligned(W, 16) || !aligned(x, 16)) return fail(COSET_EINVAL, "W and x must be 16-byte aligned");
+    if (!(clip >= 0.f)) return fail(COSET_EINVAL, "clip must be >= 0");
+    if (!(delta0 > 0) || !(eta > 0) || !(gamma_inv > 0)) return fail(COSET_EINVAL, "delta0, eta, gamma_inv must be positive");
+    const coset::ThetaBeta tb = make_theta_beta(theta, sigma_ema, xmax_ema, delta0, eta, gamma_inv, q, M_bounds);
+    return check_hip(coset::launch_qat_head(W, rows, cols, tb, clip, q, x, (int)tokens, bias, y, step_counter,
+                                            (hipStream_t)stream),
+                     "qat head forward launch");
+}
+
 int coset_e8_qat_bwd_theta(const void* gWq, int g_dtype, const float* W, const void* packed, const float* beta,
                            const float* dbeta_dtheta, int64_t rows, int64_t cols, int64_t blocks_per_tile,
                            float clip, int q, int M, float* dW, float* dbeta, float* dtheta, void* stream)

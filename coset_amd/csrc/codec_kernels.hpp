@@ -165,6 +165,12 @@ __device__ __forceinline__ float layer_scale(const CodecArgs& a, int64_t block)
 // n, the generic kernel (hnlq_codec.hip) otherwise.  codec_path overrides
 // the choice: 0 automatic, 1 always generic, 2 table kernel when supported.
 hipError_t launch_codec(const CodecArgs& a, int mode, hipStream_t s);
+// The forward of a small QAT layer (hnlq_codec.hip): W [rows, cols] fp32
+// with one theta per row, q = 2 or 4, M = 2; x [tokens, cols] fp32 (tokens
+// <= 64, cols <= 8192, cols % 8 == 0); y [tokens, rows] fp32.
+hipError_t launch_qat_head(const float* W, int64_t rows, int64_t cols, const ThetaBeta& tb, float clip, int q,
+                           const float* x, int tokens, const float* bias, float* y, int64_t* step_counter,
+                           hipStream_t s);
 hipError_t launch_codec_generic(const CodecArgs& a, int mode, hipStream_t s);
 bool lut_path_supported(const CodecArgs& a, int mode);
 hipError_t launch_codec_lut(const CodecArgs& a, int mode, hipStream_t s);

@@ -490,6 +490,144 @@ static hipError_t launch_layer_rt(const CodecArgs& args, hipStream_t s)
     return hipGetLastError();
 }
 
+// The forward of a small QAT layer in one launch (the layer's F.linear after
+// its fused quantizer, coset/core/layers.py:428-484, under no_grad): workgroup
+// o derives row o's beta from theta, quantizes the row into LDS with the
+// quantizer's own operations (x * beta, two levels encoded, each decoded
+// through the tables, sum, / beta, clamp: the W_q values the quantizer
+// writes), then computes y[t, o] = sum_k x[t, k] W_q[o, k] + bias[o] for the
+// tokens, each as the sum of 256 / P fixed-order partial sums (P the tokens
+// rounded up to a power of two) added in order.  fp32 throughout.
+constexpr int kHeadMaxCols = 8192;
+constexpr int kHeadMaxTokens = 64;
+
+struct HeadArgs {
+    const float* W;          // [rows, cols]
+    int64_t cols;
+    ThetaBeta tb;            // one theta per row
+    float clip;
+    const float* x;          // [tokens, cols]
+    int tokens, tpt;         // tpt: threads per token (256 / P)
+    const float* bias;       // nullable [rows]
+    float* y;                // [tokens, rows]
+    int64_t rows;
+    int64_t* step_counter;   // nullable: incremented once per launch
+    const uint16_t* map;     // decode tables
+    const uint64_t* coarse;
+    int fast;
+};
+
+template <int Q>
+__global__ void __launch_bounds__(256) qat_head_fwd_kernel(HeadArgs h)
+{
+    __shared__ __align__(16) float s_wq[kHeadMaxCols];
+    __shared__ float s_part[256];
+    __shared__ float s_beta;
+    const int64_t o = blockIdx.x;
+    const int tid = threadIdx.x;
+    if (tid == 0) {
+        float lo, hi, sg;
+        theta_beta_terms(h.tb, o, &lo, &hi, &sg);
+        s_beta = __fadd_rn(lo, __fmul_rn(sg, __fsub_rn(hi, lo)));
+        if (o == 0 && h.step_counter) *h.step_counter += 1;
+    }
+    __syncthreads();
+    const float scale = s_beta;
+    const float qf = (float)Q;
+    for (int64_t j = tid; j < h.cols / 8; j += blockDim.x) {
+        const float4* p = reinterpret_cast<const float4*>(h.W + o * h.cols) + 2 * j;
+        const float4 u = p[0], v = p[1];
+        float xl[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xl[e] = __fmul_rn(xl[e], scale);
+        uint32_t words[2];
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+            int b[8];
+            encode_level<Q>(xl, h.fast, Q, b);
+            words[m] = pack_word<Q>(b, Q);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xl[e] = div_q<Q>(xl[e], qf);
+        }
+        float acc[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+        float w = 1.f;
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+            int r2[8];
+            two_r_tables<Q>(words[m], h.map, h.coarse, r2);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[e] = __fadd_rn(acc[e], __fmul_rn(w, 0.5f * (float)r2[e]));
+            w = __fmul_rn(w, qf);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float q = __fdiv_rn(acc[e], scale);
+            float c = fminf(fmaxf(q, -h.clip), h.clip);
+            if (q != q) c = q;  // torch.clamp propagates NaN
+            s_wq[8 * j + e] = c;
+        }
+    }
+    __syncthreads();
+    // token t = tid / tpt sums the columns 4 (part + tpt i) .. + 3 in order
+    const int t = tid / h.tpt, part = tid % h.tpt;
+    float sum = 0.f;
+    if (t < h.tokens) {
+        const float* xr = h.x + (int64_t)t * h.cols;
+        for (int64_t k = 4 * part; k < h.cols; k += 4 * h.tpt) {
+            const float4 xv = *reinterpret_cast<const float4*>(xr + k);
+            const float4 wv = *reinterpret_cast<const float4*>(s_wq + k);
+            sum = __fmaf_rn(xv.x, wv.x, sum);
+            sum = __fmaf_rn(xv.y, wv.y, sum);
+            sum = __fmaf_rn(xv.z, wv.z, sum);
+            sum = __fmaf_rn(xv.w, wv.w, sum);
+        }
+    }
+    s_part[tid] = sum;
+    __syncthreads();
+    if (tid < h.tokens) {
+        float v = s_part[tid * h.tpt];
+        for (int i = 1; i < h.tpt; ++i) v = __fadd_rn(v, s_part[tid * h.tpt + i]);
+        if (h.bias) v = __fadd_rn(v, h.bias[o]);
+        h.y[(int64_t)tid * h.rows + o] = v;
+    }
+}
+
+hipError_t launch_qat_head(const float* W, int64_t rows, int64_t cols, const ThetaBeta& tb, float clip, int q,
+                           const float* x, int tokens, const float* bias, float* y, int64_t* step_counter,
+                           hipStream_t s)
+{
+    if (rows <= 0 || tokens <= 0) return hipSuccess;
+    if ((q != 2 && q != 4) || cols <= 0 || cols % 8 || cols > kHeadMaxCols || tokens > kHeadMaxTokens)
+        return hipErrorInvalidValue;
+    const DecodeTables* t = nullptr;
+    hipError_t e = get_decode_tables(q, 0, &t);
+    if (e != hipSuccess) return e;
+    HeadArgs h{};
+    h.W = W;
+    h.cols = cols;
+    h.tb = tb;
+    h.clip = clip;
+    h.x = x;
+    h.tokens = tokens;
+    int p2 = 1;
+    while (p2 < tokens) p2 *= 2;
+    h.tpt = 256 / p2;
+    h.bias = bias;
+    h.y = y;
+    h.rows = rows;
+    h.step_counter = step_counter;
+    h.map = t->cid_map;
+    h.coarse = t->coarse;
+    h.fast = g_fast_projection;
+    if (q == 4)
+        hipLaunchKernelGGL(qat_head_fwd_kernel<4>, dim3((unsigned)rows), dim3(256), 0, s, h);
+    else
+        hipLaunchKernelGGL(qat_head_fwd_kernel<2>, dim3((unsigned)rows), dim3(256), 0, s, h);
+    return hipGetLastError();
+}
+
 template <int MODE>
 static hipError_t launch_mode(const CodecArgs& a, hipStream_t s)
 {

@@ -396,6 +396,17 @@ def _weight_grad(g2: torch.Tensor, x2: torch.Tensor, colsum: Optional[torch.Tens
     return g2.t() @ x2
 
 
+# 1: no-grad forwards of small fp32 batches run as one fused launch
+# (coset_e8_qat_head_fwd); 0: the quantizer and F.linear as two launches
+_HEAD_FWD = [1]
+
+
+def set_head_forward(enabled: bool) -> None:
+    """Run no-grad forwards of up to 64 fp32 tokens as one launch (default)
+    or as the quantizer followed by F.linear."""
+    _HEAD_FWD[0] = 1 if enabled else 0
+
+
 _AUX_STREAMS: Dict[int, "torch.cuda.Stream"] = {}
 # > 0 while CapturedQATStep warms up and captures: the backward then forks
 # its independent products onto a second stream (graph branches).  Eager
@@ -740,9 +751,41 @@ class HNLQLinearQAT(nn.Module):
         """coset/core/layers.py:398-470 (fp32 W_q)."""
         return self._quantize_weights_as(torch.float32)
 
+    def _head_takes(self, x) -> bool:
+        """Whether forward() runs as one fused launch (coset_e8_qat_head_fwd):
+        a no-grad forward of at most 64 fp32 tokens through the fused E8
+        quantizer with row tiling and q = 2, 4."""
+        if not (_HEAD_FWD[0] == 1 and x.is_cuda and x.dtype == torch.float32 and self.quantization_enabled
+                and self._fused() and self.tiling == "row" and self.q in (2, 4) and not self.enable_diagnostics
+                and x.shape[-1] == self.in_features and self.in_features <= 8192 and x.numel() > 0
+                and x.numel() // self.in_features <= 64):
+            return False
+        params = (self.weight, self.theta_beta) + ((self.bias,) if self.bias is not None else ())
+        return not torch.is_grad_enabled() or not (x.requires_grad or any(p.requires_grad for p in params))
+
+    def _head_forward(self, x):
+        """y = x W_q^T + bias with W_q quantized in the same launch."""
+        self._advance_step(device_increment=False)   # the kernel increments step_count
+        x2 = x.reshape(-1, self.in_features).contiguous()
+        y = torch.empty((x2.shape[0], self.out_features), dtype=torch.float32, device=x.device)
+        W = self.weight.detach().contiguous()
+        _lib.call("coset_e8_qat_head_fwd", W.data_ptr(), self.out_features, self.in_features,
+                  self.theta_beta.detach().contiguous().data_ptr(), self.sigma_ema.data_ptr(),
+                  self.xmax_ema.data_ptr(), float(self.Delta0), float(self.eta), self._ginv_f, int(self.M),
+                  float(self.weight_clip_value), int(self.q), x2.data_ptr(), x2.shape[0],
+                  None if self.bias is None else self.bias.detach().data_ptr(), y.data_ptr(),
+                  self.step_count.data_ptr(), _lib.stream_of(x2))
+        y = y.reshape(*x.shape[:-1], self.out_features)
+        if self.quantize_activations and self.actq is not None:
+            y = self.actq(y)
+        return y
+
     def forward(self, x):
         """F.linear(x, W_q, bias) (layers.py:472-484); W_q is produced in the
-        activation dtype (float32 or bfloat16) for the GEMM."""
+        activation dtype (float32 or bfloat16) for the GEMM.  No-grad forwards
+        of up to 64 fp32 tokens run as one launch (quantizer and product)."""
+        if self._head_takes(x):
+            return self._head_forward(x)
         wdt = x.dtype if x.dtype in (torch.bfloat16, torch.float16) else torch.float32
         if wdt == torch.float16:
             wdt = torch.float32

@@ -27,6 +27,8 @@
  *                            legacy E8Lattice.g_x/Q coset/legacy/lattices/e8.py:41-103
  *   coset_e8_qat_fwd         HNLQLinearQAT._quantize_weights (scale, STE quantize,
  *                            unscale, clamp)       coset/core/layers.py:398-470
+ *   coset_e8_qat_head_fwd    HNLQLinearQAT.forward of a small layer under no_grad
+ *                            (quantizer + F.linear) coset/core/layers.py:428-484
  *   coset_e8_qat_bwd         autograd of that chain through the straight-through
  *                            estimator             coset/core/layers.py:62-110, 428-463
  *   coset_qat_stats_update   HNLQLinearQAT._gather_stats coset/core/layers.py:366-379
@@ -184,6 +186,19 @@ int coset_e8_qat_fwd_theta(const float* W, int64_t rows, int64_t cols, int64_t b
                            double eta, double gamma_inv, int M_bounds, float clip, int q, int M, void* Wq,
                            int wq_dtype, void* packed, float* beta_out, float* dbeta_dtheta_out,
                            int64_t* step_counter, const float* bias, void* bias_out, void* stream);
+
+/* The forward of a small QAT layer in one launch: HNLQLinearQAT.forward
+ * (coset/core/layers.py:472-484) with its fused quantizer
+ * (coset_e8_qat_fwd_theta, row tiling: one theta per row, M = 2, q = 2 or 4)
+ * and F.linear, y [tokens, rows] = x [tokens, cols] W_q^T + bias, fp32, for
+ * inference-sized batches (tokens <= 64, cols % 8 == 0 and <= 8192; others
+ * return COSET_EUNSUPPORTED).  W_q is the quantizer's, bit for bit; the
+ * products are fp32 in a fixed order.  step_counter (nullable) is
+ * incremented once; bias nullable. */
+int coset_e8_qat_head_fwd(const float* W, int64_t rows, int64_t cols, const float* theta, const float* sigma_ema,
+                          const float* xmax_ema, double delta0, double eta, double gamma_inv, int M_bounds, float clip,
+                          int q, const float* x, int64_t tokens, const float* bias, float* y, int64_t* step_counter,
+                          void* stream);
 
 /* Backward of coset_e8_qat_fwd_theta: dW and dbeta as coset_e8_qat_bwd, plus
  * dtheta[t] = dbeta[t] * dbeta_dtheta[t] (the factor the forward recorded). */

@@ -446,3 +446,68 @@ def test_theta_quantizer_layer_kernel_matches_generic(q, M):
                         b.view(torch.int32 if b.dtype == torch.float32 else torch.int16)
                 assert torch.equal(a, b), case
             assert int(res[0][-1]) == 1, case
+
+
+@pytest.mark.parametrize("fin,fout,q,kw,wstd", [(768, 10, 4, dict(theta_init_value=0.0), 0.02),
+                                                (768, 10, 4, dict(Delta0=1.5), 1.0),
+                                                (512, 96, 2, dict(Delta0=1.5), 1.0),
+                                                (2048, 33, 4, dict(Delta0=1.5, weight_clip_value=0.5), 1.0)])
+def test_head_forward_matches_two_launch_path(fin, fout, q, kw, wstd):
+    """A no-grad forward of up to 64 fp32 tokens in one launch
+    (coset_e8_qat_head_fwd: the quantizer's W_q bit for bit, then fp32
+    products in a fixed order) against the quantizer followed by F.linear
+    (set_head_forward(False)): outputs within the fp32 accumulation bound of
+    the products' magnitude, the same step counter, and token counts 1, 7, 32,
+    64 and a 3-D input.  A forward that needs gradients takes the two-launch
+    path."""
+    import coset_amd as ca
+    from coset_amd import layers as L
+    torch.manual_seed(fin + fout)
+    layer = ca.create_e8_hnlq_linear(fin, fout, q=q, M=2, **kw)
+    with torch.no_grad():
+        layer.weight.normal_(0.0, wstd)
+        layer.bias.normal_(0.0, 0.1)
+        layer.theta_beta.uniform_(-2.0, 2.0)
+    for shape in ((1, fin), (7, fin), (32, fin), (64, fin), (2, 16, fin)):
+        x = torch.randn(shape, device="cuda")
+        outs, steps = [], []
+        for fused in (True, False):
+            L.set_head_forward(fused)
+            try:
+                s0 = int(layer.step_count)
+                with torch.no_grad():
+                    outs.append(layer(x))
+                steps.append(int(layer.step_count) - s0)
+            finally:
+                L.set_head_forward(True)
+        with torch.no_grad():
+            Wq = layer._quantize_weights()
+        mag = (x.reshape(-1, fin).abs().double() @ Wq.abs().double().t()).reshape(outs[1].shape) + 1e-30
+        assert steps == [1, 1], shape
+        assert outs[0].shape == outs[1].shape == (*shape[:-1], fout)
+        # two fp32 sums of fin products in different orders: each within
+        # fin 2^-24 of the products' magnitude
+        assert ((outs[0].double() - outs[1].double()).abs() <= fin * 2.0 ** -23 * mag + 1e-7).all(), shape
+    # gradients needed: the two-launch path (autograd through QATLinearFn)
+    x = torch.randn(8, fin, device="cuda", requires_grad=True)
+    assert not layer._head_takes(x)
+    y = layer(x)
+    assert y.grad_fn is not None
+
+
+def test_head_forward_refuses_unsupported_sizes():
+    """More than 64 tokens, columns past 8192 or not a multiple of 8, q
+    outside {2, 4}: COSET_EUNSUPPORTED or EINVAL before any launch."""
+    from coset_amd import _lib
+    lib = _lib.load()
+    W = torch.zeros((4, 64), device="cuda")
+    x = torch.zeros((65, 64), device="cuda")
+    y = torch.zeros((65, 4), device="cuda")
+    t = torch.zeros(4, device="cuda")
+    args = lambda tokens, cols, q: (W.data_ptr(), 4, cols, t.data_ptr(), t.data_ptr(), t.data_ptr(), 1.5, 0.1,
+                                    1 / 12.0, 2, 2.0, q, x.data_ptr(), tokens, None, y.data_ptr(), None,
+                                    _lib.stream_of(x))
+    assert lib.coset_e8_qat_head_fwd(*args(65, 64, 4)) != 0
+    assert lib.coset_e8_qat_head_fwd(*args(8, 8200, 4)) != 0
+    assert lib.coset_e8_qat_head_fwd(*args(8, 60, 4)) != 0
+    assert lib.coset_e8_qat_head_fwd(*args(8, 64, 8)) != 0
