@@ -402,9 +402,12 @@ __host__ __device__ inline void residual_dyadic(const int b[8], float r[8])
 }
 
 // The same residual in integers, from a table of per-coordinate quantities
-// (the layer round-trip kernel, q = 8, 16).  Everything residual_dyadic
-// derives for coordinate i is a function of Z_i alone, an integer in
-// [-2(q-1), 5(q-1)], so a 7q-entry table indexed by Z + 2q holds it:
+// (the layer round-trip kernel at q = 8, 16, the QAT backward at q = 2, 4,
+// 8, 16; the grid argument above holds for q = 2 and 4 as well, and the CPU
+// checker compares every code of q = 2, 4, 8 and 16 with the oracle's
+// residual).  Everything residual_dyadic derives for coordinate i is a
+// function of Z_i alone, an integer in [-2(q-1), 5(q-1)], so a 7q-entry
+// table indexed by Z + 2q holds it:
 //   f0 = the nearest integer to z = Z / 2q, ties toward zero (g0 = -f0);
 //   D0 = 2q d0 = Z - 2q f0, in [-q, q];
 //   f1 = floor(z - 1/(4q)) for Z > 0, floor(z + 1/(4q)) for Z <= 0, i.e.
@@ -460,7 +463,7 @@ __host__ __device__ inline int mad24(int a, int b, int c)
 template <int Q, bool FIRST>
 __host__ __device__ inline void dyadic_level_acc(const int b[8], const uint4* tab, int shift, int acc2[8])
 {
-    static_assert(Q == 8 || Q == 16, "the table fields hold q <= 16");
+    static_assert(Q == 2 || Q == 4 || Q == 8 || Q == 16, "the table fields hold q <= 16");
     const uint4* t7 = tab + (b[7] + 2 * Q);  // Z_i = 2 (..) + b_7
     uint4 e[8];
     e[0] = t7[2 * (2 * b[0] - b[1])];

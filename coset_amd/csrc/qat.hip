@@ -8,8 +8,9 @@
 //   dW     = gq * beta                         STE identity, then mul backward
 //   dbeta  = sum_tile( gq * W ) + sum_tile( -(g*m) * ((Q/beta)/beta) )
 // The forward kernel (hnlq_codec / hnlq_lut, SCALE_LAYER) saves the packed
-// level words; here Q is re-decoded from them (tables for q = 2, 4,
-// projections otherwise), so the backward reads g, W and 0.5 B/weight of codes.
+// level words; here Q is re-decoded from them (for q = 2, 4, 8, 16 through a
+// per-coordinate table in LDS, projections otherwise), so the backward reads
+// g, W and 0.5 B/weight of codes and makes no dependent global loads.
 //
 // One workgroup per tile (row tiling: a tile is an output row of
 // blocks_per_tile 8-wide blocks) reduces dbeta with a wave reduction and one
@@ -31,8 +32,6 @@ struct QatBwdArgs {
     int64_t blocks_per_tile;
     float clip;
     int q, M, strided;
-    const uint16_t* map;   // decode tables (q = 2, 4) or null
-    const uint64_t* coarse;
     float* dW;             // [rows, cols]
     float* dbeta;          // [n_tiles]
     const float* dbdt;     // [n_tiles] d beta / d theta, or null
@@ -46,11 +45,11 @@ __device__ __forceinline__ void write_dtheta(const QatBwdArgs& a, int64_t t, flo
     if (a.dbdt) a.dtheta[t] = __fmul_rn(dbeta, a.dbdt[t]);
 }
 
-// q = 8, 16: each workgroup's decode table of residual_table (built at the
-// kernel's start), else unused
+// q = 2, 4, 8, 16: each workgroup's table of dyadic_table_entry, one entry
+// per Z + 2q (built at the kernel's start), else unused
 template <int Q>
 struct BwdTab {
-    static constexpr bool kOn = Q == 8 || Q == 16;
+    static constexpr bool kOn = Q == 2 || Q == 4 || Q == 8 || Q == 16;
     static constexpr int kEntries = kOn ? 7 * Q : 1;
 };
 
@@ -69,28 +68,23 @@ __device__ __forceinline__ void decode_q(const QatBwdArgs& a, int64_t blk, const
 {
     const int q = Q > 0 ? Q : a.q;
     const float qf = (float)q;
-    if (Q == 2 || Q == 4) {
+    if constexpr (Q == 2 || Q == 4) {
+        // 2 Q = sum_m q^m (2 r_m) in integers: dyadic_level_acc adds
+        // q^m (2 r_m + q); q sum_m q^m comes off at the end
+        constexpr int kLog2Q = Q == 2 ? 1 : 2;
         int acc2[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc2[j] = 0;
-        int wq = 1;
+        int off = 0;
         for (int m = 0; m < a.M; ++m) {
-            uint32_t w = reinterpret_cast<const uint16_t*>(a.packed)[blk * a.M + m] & (Q == 2 ? 0xffu : 0xffffu);
+            const uint32_t w = reinterpret_cast<const uint16_t*>(a.packed)[blk * a.M + m] & (Q == 2 ? 0xffu : 0xffffu);
             int b[8];
             unpack_word<Q>(w, q, b);
-            int u[8];
-            u[0] = 4 * b[0] - 2 * b[1] + b[7];
-#pragma unroll
-            for (int j = 1; j < 6; ++j) u[j] = 2 * (b[j] - b[j + 1]) + b[7];
-            u[6] = 2 * b[6] + b[7];
-            u[7] = b[7];
-            uint64_t c = a.coarse[a.map[w]];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) acc2[j] += wq * (u[j] - Q * (int)(int8_t)(uint8_t)(c >> (8 * j)));
-            wq *= Q;
+            dyadic_level_acc<Q, false>(b, tab, m * kLog2Q, acc2);
+            off += Q << (m * kLog2Q);
         }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) out[j] = __fmul_rn((float)acc2[j], 0.5f);
+        for (int j = 0; j < 8; ++j) out[j] = __fmul_rn((float)(acc2[j] - off), 0.5f);
     } else {
         float acc[8];
 #pragma unroll
@@ -472,15 +466,9 @@ hipError_t launch_qat_bwd(const void* g, int g_dtype, const float* W, const void
     a.strided = n_blocks > 1;
     a.dW = dW;
     a.dbeta = dbeta;
-    if (q == 2 || q == 4) {
-        const DecodeTables* t = nullptr;
-        hipError_t e = get_decode_tables(q, 0, &t);
-        if (e != hipSuccess) return e;
-        a.map = t->cid_map;
-        a.coarse = t->coarse;
-        return q == 4 ? launch_bwd_q<4>(a, s) : launch_bwd_q<2>(a, s);
-    }
     switch (q) {
+    case 2: return launch_bwd_q<2>(a, s);
+    case 4: return launch_bwd_q<4>(a, s);
     case 8: return launch_bwd_q<8>(a, s);
     case 16: return launch_bwd_q<16>(a, s);
     default: return launch_bwd_q<0>(a, s);

@@ -27,8 +27,8 @@
 //                                   also that no residual coordinate
 //                                   exceeds 3q/2 in magnitude
 //   check_fastpath tabres q N [T]   the same residual through the integer
-//                                   table form dyadic_level_acc<q> (q = 8,
-//                                   16), codes as for fastres
+//                                   table form dyadic_level_acc<q> (q = 2,
+//                                   4, 8, 16), codes as for fastres
 //   check_fastpath divq S K [T]     div_by_recip<S>(a, b, RN(1/b)) against
 //                                   the IEEE quotient a / b for every b
 //                                   significand in [1, 2) and a = k / 2,
@@ -515,9 +515,11 @@ int main(int argc, char** argv)
         const int q = atoi(argv[2]);
         const long n = atol(argv[3]);
         const int th = argc >= 5 ? atoi(argv[4]) : 1;
+        if (q == 2) return fast_residual<2, true>(n, th);
+        if (q == 4) return fast_residual<4, true>(n, th);
         if (q == 8) return fast_residual<8, true>(n, th);
         if (q == 16) return fast_residual<16, true>(n, th);
-        fprintf(stderr, "tabres: q must be 8 or 16\n");
+        fprintf(stderr, "tabres: q must be 2, 4, 8 or 16\n");
         return 2;
     }
     if (argc >= 4 && !strcmp(argv[1], "fastres")) {

@@ -119,13 +119,14 @@ def test_fast_residual_matches_oracle(checker, q, n):
     assert " mismatches 0" in out, out
 
 
-@pytest.mark.parametrize("q,n", [(8, 1 << 24), (16, 1 << 21)])
+@pytest.mark.parametrize("q,n", [(2, 1 << 8), (4, 1 << 16), (8, 1 << 24), (16, 1 << 21)])
 def test_table_residual_matches_oracle(checker, q, n):
-    """The layer kernel's integer decode dyadic_level_acc<q> (per-coordinate
-    table, first-index argmax/argmin as maxima of packed keys, sums and
-    parities as one add): every code at q = 8, the structured codes and a
-    random sample at q = 16, twice the residual bit for bit against the
-    oracle's under both distance rules.  (All 2^32 codes at q = 16:
+    """The integer decode dyadic_level_acc<q> of the layer round-trip kernel
+    and the QAT backward (per-coordinate table, first-index argmax/argmin as
+    maxima of packed keys, sums and parities as one add): every code at
+    q = 2, 4 and 8, the structured codes and a random sample at q = 16,
+    twice the residual bit for bit against the oracle's under both distance
+    rules.  (All 2^32 codes at q = 16:
     `check_fastpath tabres 16 4294967296 <threads>`, about ten minutes on
     eight cores.)"""
     rc, out = run(checker, "tabres", str(q), str(n), str(min(8, os.cpu_count() or 1)))

@@ -89,7 +89,8 @@ def test_layer_matches_reference(golden, name, fin, fout, kw):
 
 
 @pytest.mark.parametrize("tiling", ["row", "block"])
-@pytest.mark.parametrize("q,gdt", [(4, torch.float32), (4, torch.bfloat16), (8, torch.float32), (16, torch.float32), (3, torch.float32)])
+@pytest.mark.parametrize("q,gdt", [(2, torch.float32), (4, torch.float32), (4, torch.bfloat16), (8, torch.float32),
+                                   (16, torch.float32), (3, torch.float32)])
 def test_weight_quant_kernels_vs_oracle(tiling, q, gdt):
     """coset_e8_qat_fwd/bwd against the oracle's quantizer and closed-form
     backward, with the clamp active on part of the weights."""
