@@ -787,9 +787,11 @@ def bench_c5(torch, ca, args):
 
         k, w = gpu_time(torch, step, 100, 3, 0.1)
         flops = 6.0 * 4096 * fin * fout
-        # the same step captured once into a HIP graph and replayed
+        # the same step captured once into a HIP graph and replayed, with the
+        # dense products' library solutions chosen by timing whole replays
+        # (torch's default selection or TunableOp's)
         xs = x.detach().clone().requires_grad_(True)
-        cap = ca.CapturedQATStep(layer, xs, gy.clone())
+        cap = ca.CapturedQATStep(layer, xs, gy.clone(), tune_gemms=True)
         kg, wg = gpu_time(torch, cap.step, 100, 3, 0.1)
         res["shapes"][f"{fin}x{fout}"] = {"tokens_per_s": round(4096 / k, 1), "ms": round(k * 1e3, 3),
                                           "tflops": round(flops / k / 1e12, 1),
@@ -797,7 +799,8 @@ def bench_c5(torch, ca, args):
                                           "graph": {"tokens_per_s": round(4096 / kg, 1),
                                                     "ms": round(kg * 1e3, 3), "ms_wall": round(wg * 1e3, 3),
                                                     "tflops": round(flops / kg / 1e12, 1),
-                                                    "frac_bf16_mfma": round(flops / kg / 1e12 / BF16_MFMA_TFLOPS, 4)}}
+                                                    "frac_bf16_mfma": round(flops / kg / 1e12 / BF16_MFMA_TFLOPS, 4),
+                                                    "gemm_selection": cap.gemm_selection, "tune_us": cap.tune_us}}
         if args.cpu:
             with torch.no_grad():
                 beta = layer._beta().float().cpu().numpy()
@@ -950,10 +953,10 @@ def summarize(extra):
         out["c4"] = o4
     c5 = extra.get("c5")
     if c5:
-        out["c5"] = {"legend": "[ms_graph, f_mfma, ms_eager, cpu tokens/s]"}
+        out["c5"] = {"legend": "[ms_graph, f_mfma, ms_eager, cpu tokens/s, gemm selection]"}
         for k, v in c5.get("shapes", {}).items():
             out["c5"][k] = [_r(_pick(v, "graph", "ms")), _r(_pick(v, "graph", "frac_bf16_mfma")), _r(v.get("ms")),
-                            _r(_pick(v, "cpu_baseline", "value"))]
+                            _r(_pick(v, "cpu_baseline", "value")), _pick(v, "graph", "gemm_selection")]
     pk = extra.get("peaks")
     if pk:
         out["peaks"] = {"copy_gbs": _r(_pick(pk, "copy", "gbs"), 4), "gemm_bf16_tflops": _r(_pick(pk, "gemm_bf16", "tflops"), 4),

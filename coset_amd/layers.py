@@ -943,10 +943,23 @@ class CapturedQATStep:
     capture; ``step()`` raises instead of replaying a stale graph.  The
     warm-up runs that torch needs before capture leave the layer's buffers
     and counters as they were.
+
+    ``tune_gemms=True`` also captures the step with the dense products
+    (forward and input gradient; the weight gradient is the library's own
+    kernel) chosen by PyTorch-ROCm's TunableOp (``torch.cuda.tunable``: each
+    product shape benchmarked over the hipBLASLt and rocBLAS solutions during
+    the warm-up), times a few replays of both graphs and keeps the faster one
+    (``gemm_selection``: "default" or "tunableop"; ``tune_us``: the timed
+    replay of each).  A product that is fastest alone is not always fastest
+    in the step, where the weight gradient runs beside it, hence the timing
+    of whole replays.  TunableOp's enable and tuning flags are restored
+    afterwards; its table of tuned shapes stays in the process.  Products of
+    other solutions round differently: the step's output and input gradient
+    then match an eager step to the products' rounding, not bit for bit.
     """
 
     def __init__(self, layer: HNLQLinearQAT, x: torch.Tensor, grad_output: Optional[torch.Tensor] = None,
-                 warmup: int = 3):
+                 warmup: int = 3, tune_gemms: bool = False):
         if not x.is_cuda or not layer.weight.is_cuda:
             raise ValueError("CapturedQATStep needs the layer and its input on a GPU")
         if layer.enable_diagnostics:
@@ -962,6 +975,46 @@ class CapturedQATStep:
 
         _OVERLAP_BACKWARD[0] += 1   # warm-up and capture take the same (two-stream) backward
         try:
+            cands = [self._capture(warmup, saved, False)]
+            if tune_gemms:
+                cands.append(self._capture(warmup, saved, True))
+        finally:
+            _OVERLAP_BACKWARD[0] -= 1
+        self.gemm_selection = "default"
+        self.tune_us = None
+        best = 0
+        if len(cands) > 1:
+            times = self._time_replays([c[0] for c in cands], saved)
+            self.tune_us = {"default": round(times[0], 2), "tunableop": round(times[1], 2)}
+            best = 1 if times[1] < times[0] else 0
+            self.gemm_selection = ("default", "tunableop")[best]
+        self.graph, self.y, self._grads, self._x_grad = cands[best]
+        del cands
+        layer._host_step = host_step
+        # the winner's gradient tensors are the parameters' (and the input's) grads
+        for p, g in self._grads:
+            p.grad = g
+        if self._x_grad is not None:
+            self.x.grad = self._x_grad
+        self._storage = self._param_ptrs()
+
+    def _restore_buffers(self, saved):
+        with torch.no_grad():
+            for name, b in self.layer.named_buffers():
+                b.copy_(saved[name])
+
+    def _capture(self, warmup, saved, tuned):
+        """Warm-up steps on a side stream (with ``tuned``: under TunableOp,
+        tuning each new product shape), the layer's buffers restored, then
+        the capture.  Returns the graph, its output, the (parameter, grad)
+        pairs and the input's grad it writes."""
+        x = self.x
+        tun = torch.cuda.tunable
+        prev = (tun.is_enabled(), tun.tuning_is_enabled()) if tuned else None
+        try:
+            if tuned:
+                tun.enable(True)
+                tun.tuning_enable(True)
             side = torch.cuda.Stream(device=x.device)
             side.wait_stream(torch.cuda.current_stream(x.device))
             with torch.cuda.stream(side):
@@ -969,21 +1022,42 @@ class CapturedQATStep:
                     self._zero_grads()
                     self._run()
             torch.cuda.current_stream(x.device).wait_stream(side)
-            with torch.no_grad():
-                for name, b in layer.named_buffers():
-                    b.copy_(saved[name])
+            self._restore_buffers(saved)
             self._zero_grads()
-
-            self.graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(self.graph):
-                self.y = self._run()
+            if tuned:
+                tun.tuning_enable(False)   # the capture only looks the tuned solutions up
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                y = self._run()
         finally:
-            _OVERLAP_BACKWARD[0] -= 1
-        layer._host_step = host_step
-        # the gradient tensors the graph writes, and the parameter storage it reads
-        self._grads = [(p, p.grad) for p in layer.parameters() if p.grad is not None]
-        self._x_grad = x.grad if x.requires_grad else None
-        self._storage = self._param_ptrs()
+            if tuned:
+                tun.tuning_enable(prev[1])
+                tun.enable(prev[0])
+        grads = [(p, p.grad) for p in self.layer.parameters() if p.grad is not None]
+        return graph, y, grads, (x.grad if x.requires_grad else None)
+
+    def _time_replays(self, graphs, saved, rounds: int = 9, reps: int = 10):
+        """Median time (us) of one replay of each graph, the graphs timed in
+        turn after a few untimed replays each; the layer's buffers (the device
+        step counter among them) are restored afterwards."""
+        stream = torch.cuda.current_stream(self.x.device)
+        for g in graphs:
+            for _ in range(reps):
+                g.replay()
+        ts = [[] for _ in graphs]
+        for _ in range(rounds):
+            for k, g in enumerate(graphs):
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for _ in range(reps):
+                    g.replay()
+                e1.record(stream)
+                e1.synchronize()
+                ts[k].append(e0.elapsed_time(e1) * 1e3 / reps)
+        self._restore_buffers(saved)
+        stream.synchronize()
+        return [sorted(t)[len(t) // 2] for t in ts]
 
     def _param_ptrs(self):
         return [(name, p.data_ptr()) for name, p in self.layer.named_parameters()]

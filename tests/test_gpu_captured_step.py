@@ -74,6 +74,62 @@ def test_captured_step_matches_eager_steps(tiling, dtype, fin, fout, tokens):
 
 
 @pytest.mark.gpu
+def test_captured_step_tuned_gemms():
+    """tune_gemms: the graph kept (torch's default products or TunableOp's)
+    gives the eager step's weight, theta and bias gradients bit for bit (the
+    library's own kernels), and its output and input gradient within the
+    rounding of a bf16 product summed in another order (bit for bit when the
+    default selection is kept); TunableOp's flags are as they were."""
+    tun = torch.cuda.tunable
+    flags = (tun.is_enabled(), tun.tuning_is_enabled())
+    fin, fout, tokens = 768, 3072, 4096
+    eager, cap_layer = _pair(fin, fout, "row", interval=256)
+    gen = torch.Generator(device="cuda").manual_seed(21)
+    x_static = torch.zeros(tokens, fin, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    gy_static = torch.zeros(tokens, fout, device="cuda", dtype=torch.bfloat16)
+    cap = coset_amd.CapturedQATStep(cap_layer, x_static, gy_static, tune_gemms=True)
+    print(f"selection {cap.gemm_selection}, replays {cap.tune_us}", flush=True)
+    assert (tun.is_enabled(), tun.tuning_is_enabled()) == flags
+    assert cap.gemm_selection in ("default", "tunableop")
+    assert set(cap.tune_us) == {"default", "tunableop"}
+    assert int(cap_layer.step_count) == 0 and cap_layer._host_step == 0
+    # the quantized weight (fixed: no parameter update here), with the
+    # counters it advances restored
+    saved = {n: b.clone() for n, b in eager.named_buffers()}
+    host_step = eager._host_step
+    with torch.no_grad():
+        wq = eager._quantize_weights().float()
+        for n, b in eager.named_buffers():
+            b.copy_(saved[n])
+    eager._host_step = host_step
+    for i in range(3):
+        x = torch.randn(tokens, fin, device="cuda", generator=gen).to(torch.bfloat16)
+        gy = torch.randn(tokens, fout, device="cuda", generator=gen).to(torch.bfloat16)
+        eager.zero_grad(set_to_none=True)
+        xa = x.clone().requires_grad_(True)
+        ya = eager(xa)
+        ya.backward(gy)
+        yb = cap.step(x, gy)
+        torch.cuda.synchronize()
+        print(f"step {i}", flush=True)
+        for name, ga, gb in (("weight", eager.weight.grad, cap_layer.weight.grad),
+                             ("theta", eager.theta_beta.grad, cap_layer.theta_beta.grad),
+                             ("bias", eager.bias.grad, cap_layer.bias.grad)):
+            assert torch.equal(ga, gb), f"{name} gradient differs at step {i}"
+        if cap.gemm_selection == "default":
+            assert torch.equal(ya, yb) and torch.equal(xa.grad, x_static.grad)
+        else:
+            # fp32 sums of exact bf16 products, rounded once to bf16: two
+            # orders differ by at most one bf16 rounding plus the fp32 sums'
+            mag_y = x.float().abs() @ wq.abs().t() + eager.bias.detach().float().abs()
+            mag_dx = gy.float().abs() @ wq.abs()
+            assert ((ya.float() - yb.float()).abs() <= 2.0 ** -7 * mag_y + 1e-30).all(), f"output at step {i}"
+            assert ((xa.grad.float() - x_static.grad.float()).abs() <= 2.0 ** -7 * mag_dx + 1e-30).all(), \
+                f"input gradient at step {i}"
+        assert int(eager.step_count) == int(cap_layer.step_count) == i + 1
+
+
+@pytest.mark.gpu
 def test_captured_forward_only_matches_eager():
     eager, cap_layer = _pair(768, 10, "row", interval=256)
     x = torch.zeros(32, 768, device="cuda")
