@@ -14,6 +14,7 @@
 //   SCALE_LAYER  x_s = x * beta_row;    out = clamp(dec / beta_row, +-clip)
 //                                                                 (layers.py:431,455,463)
 #include <algorithm>
+#include <type_traits>
 
 #include "codec_kernels.hpp"
 #include "tables.hpp"
@@ -41,6 +42,12 @@ __device__ __forceinline__ void two_r_tables(uint32_t w, const uint16_t* map, co
 // Tiles whose theta-derived beta one workgroup of 256 blocks can touch when a
 // tile spans at least 64 blocks.
 constexpr int kWgTiles = 256 / 64 + 2;
+
+// q = 4 in the layer round-trip kernel: true decodes each level through the
+// L2-resident cid map and coarse points (two_r_tables' values), false through
+// the workgroup's LDS table of dyadic_level_acc; both give the reference's
+// residual for every q = 4 code.
+constexpr bool kLayerQ4TableDecode = true;
 
 // WGBETA: layer scaling with beta derived from theta and tiles of at least
 // 64 blocks -- the workgroup derives the beta of each tile it touches once,
@@ -330,15 +337,16 @@ __global__ void __launch_bounds__(256) hnlq_codec_kernel(CodecArgs a)
 template <int Q, int M, bool XBF16, bool THETA>
 __global__ void __launch_bounds__(256) hnlq_layer_rt_kernel(CodecArgs a)
 {
-    static_assert(Q == 8 || Q == 16, "residual_dyadic's q within the codec's q <= 16");
+    static_assert(Q == 4 || Q == 8 || Q == 16, "the table decode's q within the codec's q <= 16");
     static_assert(M >= 1 && M <= 4, "level words stored as one vector");
-    constexpr int kSteps = Q == 8 || M <= 3 ? 1 : 2;
-    constexpr int kLog2Q = Q == 8 ? 3 : 4;
-    constexpr int kOff = Q * (Q == 8 ? (M == 1 ? 1 : M == 2 ? 9 : M == 3 ? 73 : 585)
-                                     : (M == 1 ? 1 : M == 2 ? 17 : M == 3 ? 273 : 4369));  // q sum_m q^m
+    constexpr bool kGdec = Q == 4 && kLayerQ4TableDecode;  // q = 4: the L2-resident decode tables
+    constexpr int kSteps = Q <= 8 || M <= 3 ? 1 : 2;
+    constexpr int kLog2Q = Q == 4 ? 2 : Q == 8 ? 3 : 4;
+    constexpr int kOff = Q * (((1 << (kLog2Q * M)) - 1) / (Q - 1));  // q sum_m q^m
+    using Word = std::conditional_t<(Q <= 4), uint16_t, uint32_t>;  // word_bytes(q)
     // the decode table of dyadic_level_acc, one entry per Z + 2q
-    __shared__ uint4 s_tab[7 * Q];
-    if (threadIdx.x < 7 * Q) s_tab[threadIdx.x] = dyadic_table_entry<Q>((int)threadIdx.x - 2 * Q);
+    __shared__ uint4 s_tab[kGdec ? 1 : 7 * Q];
+    if (!kGdec && threadIdx.x < 7 * Q) s_tab[threadIdx.x] = dyadic_table_entry<Q>((int)threadIdx.x - 2 * Q);
     // THETA: the betas of the rows this workgroup's blocks span (rows of at
     // least 64 blocks: kWgTiles of them at most), derived from theta once
     // per row as the generic kernel does, and recorded with d beta / d theta
@@ -364,6 +372,9 @@ __global__ void __launch_bounds__(256) hnlq_layer_rt_kernel(CodecArgs a)
     __syncthreads();
     const int64_t i = b0 + threadIdx.x;
     if (i == 0 && a.step_counter) *a.step_counter += 1;
+    // the side cast (the layer's bias) in the same launch: one more launch
+    // would be one more dependent node in a captured step
+    if (a.aux_out && i < a.aux_n) aux_cast(a, i);
     if (i >= a.n) return;
     const uint32_t row = u32div((uint32_t)i, a.row_div);
     const float beta = THETA ? s_beta[row - t0] : a.beta_row[row];
@@ -385,27 +396,73 @@ __global__ void __launch_bounds__(256) hnlq_layer_rt_kernel(CodecArgs a)
 #pragma unroll
     for (int j = 0; j < 8; ++j) xl[j] = __fmul_rn(xl[j], beta);
 
-    uint32_t* pw = a.packed ? reinterpret_cast<uint32_t*>(a.packed) + (size_t)i * M : nullptr;
+    Word* pw = a.packed ? reinterpret_cast<Word*>(a.packed) + (size_t)i * M : nullptr;
     // the fast projection's range condition holds at every level once it
     // holds for the first: each level's input is the last one divided by q
     const bool in_range = fast_in_range(xl);
     // 2 x_hat = sum_m q^m (2 r_m) in integers (the float sum of the levels
     // is exact on these half-integers, so its value is the same)
     int acc2[8];
-    {
-        int b[8];
-        encode_level<Q>(xl, 1, Q, b, in_range);
-        if (pw) pw[0] = pack_word<Q>(b, Q);
-        dyadic_level_acc<Q, true>(b, s_tab, 0, acc2);
-    }
-#pragma unroll 1
-    for (int m = 1; m < M; ++m) {
+    if constexpr (kGdec) {
+        // every level encoded first, then the levels' map reads and coarse
+        // point reads issued together (two_r_tables' values: 2 r = 2 G b -
+        // q c); acc2 takes the same q sum_m q^m offset as the table path
+        uint32_t words[M];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) xl[j] = div_q<Q>(xl[j], (float)Q);
-        int b[8];
-        encode_level<Q>(xl, 1, Q, b, in_range);
-        if (pw) pw[m] = pack_word<Q>(b, Q);
-        dyadic_level_acc<Q, false>(b, s_tab, m * kLog2Q, acc2);
+        for (int m = 0; m < M; ++m) {
+            if (m > 0) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) xl[j] = div_q<Q>(xl[j], (float)Q);
+            }
+            int b[8];
+            encode_level<Q>(xl, 1, Q, b, in_range);
+            words[m] = pack_word<Q>(b, Q);
+        }
+        if (pw) {
+            if constexpr (M == 2) {
+                *reinterpret_cast<uint32_t*>(pw) = words[0] | words[1] << 16;
+            } else {
+#pragma unroll
+                for (int m = 0; m < M; ++m) pw[m] = (Word)words[m];
+            }
+        }
+        uint16_t cid[M];
+        uint64_t cc[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) cid[m] = a.dec_map[words[m]];
+#pragma unroll
+        for (int m = 0; m < M; ++m) cc[m] = a.dec_coarse[cid[m]];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc2[j] = kOff;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            int b[8], r2[8];
+            unpack_word<Q>(words[m], Q, b);
+            r2[0] = 4 * b[0] - 2 * b[1] + b[7];
+#pragma unroll
+            for (int j = 1; j < 6; ++j) r2[j] = 2 * (b[j] - b[j + 1]) + b[7];
+            r2[6] = 2 * b[6] + b[7];
+            r2[7] = b[7];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                acc2[j] += (r2[j] - Q * (int)(int8_t)(uint8_t)(cc[m] >> (8 * j))) << (m * kLog2Q);
+        }
+    } else {
+        {
+            int b[8];
+            encode_level<Q>(xl, 1, Q, b, in_range);
+            if (pw) pw[0] = (Word)pack_word<Q>(b, Q);
+            dyadic_level_acc<Q, true>(b, s_tab, 0, acc2);
+        }
+#pragma unroll 1
+        for (int m = 1; m < M; ++m) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) xl[j] = div_q<Q>(xl[j], (float)Q);
+            int b[8];
+            encode_level<Q>(xl, 1, Q, b, in_range);
+            if (pw) pw[m] = (Word)pack_word<Q>(b, Q);
+            dyadic_level_acc<Q, false>(b, s_tab, m * kLog2Q, acc2);
+        }
     }
     float acc[8];  // +0 where the sum is zero, as the float sum of the levels
 #pragma unroll
@@ -450,21 +507,18 @@ static bool layer_rt_supported(const CodecArgs& a, int mode)
     // blocks (fp32 weights: the layer quantizer's input)
     const bool betas = a.use_theta ? a.blocks_per_row >= 64 && a.x_dtype == DT_F32 : a.beta_row != nullptr;
     return g_codec_plain && a.fast_projection && mode == MODE_ROUNDTRIP && a.scale_mode == SCALE_LAYER && betas &&
-           (a.q == 8 || a.q == 16) && a.M >= 1 && a.M <= 4 && !a.dither && !a.codes_f32 &&
+           (a.q == 8 || a.q == 16 ||
+            (a.q == 4 && (!kLayerQ4TableDecode || a.dec_map) && ((uintptr_t)a.packed & 3u) == 0)) &&
+           a.M >= 1 && a.M <= 4 &&
+           !a.dither && !a.codes_f32 &&
            (a.x_dtype == DT_F32 || a.x_dtype == DT_BF16) && (a.out_dtype == DT_F32 || a.out_dtype == DT_BF16) &&
            a.clip > 0.f && a.n <= (int64_t)0xffffffffLL && a.blocks_per_row >= 1 &&
-           a.blocks_per_row <= (int64_t)0xffffffffLL;
+           a.blocks_per_row <= (int64_t)0xffffffffLL && (!a.aux_out || a.aux_n <= a.n);
 }
 
 static hipError_t launch_layer_rt(const CodecArgs& args, hipStream_t s)
 {
     CodecArgs a = args;
-    if (a.aux_out && a.aux_n > 0) {
-        hipLaunchKernelGGL(aux_cast_kernel, dim3((unsigned)((a.aux_n + 255) / 256)), dim3(256), 0, s, a);
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
-        a.aux_out = nullptr;
-    }
     a.row_div = u32div_of((uint32_t)a.blocks_per_row);
     const dim3 grid((unsigned)((a.n + 255) / 256)), block(256);
     const bool bf = a.x_dtype == DT_BF16;
@@ -482,6 +536,7 @@ static hipError_t launch_layer_rt(const CodecArgs& args, hipStream_t s)
     }                                         \
     break;
     switch (a.q) {
+    case 4: COSET_LAYER_Q(4)
     case 8: COSET_LAYER_Q(8)
     default: COSET_LAYER_Q(16)
     }

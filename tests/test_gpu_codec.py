@@ -506,10 +506,10 @@ def test_full_size_c3(ca):
     np.testing.assert_array_equal(got.reshape(-1, 3), O.pack_words(codes, 16).reshape(-1, 3))
 
 
-@pytest.mark.parametrize("q", [8, 16])
+@pytest.mark.parametrize("q", [4, 8, 16])
 def test_layer_roundtrip_kernel_matches_generic(ca, q):
     """The layer round-trip kernel (SCALE_LAYER with stored per-row betas,
-    q = 8, 16, M <= 4: one reciprocal per block and div_by_recip for
+    q = 4, 8, 16, M <= 4: one reciprocal per block and div_by_recip for
     dec / beta, med3 clamp) bit for bit against the generic kernel
     (set_codec_plain(False)): every M, fp32 and bf16 inputs and outputs,
     rows of 1, 7, 96 and 512 blocks, block counts that end inside a

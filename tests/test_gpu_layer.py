@@ -410,11 +410,11 @@ def test_fused_quantizer_writes_the_bias_cast(rows, cols):
     assert torch.equal(Wq, Wq2) and torch.equal(packed, packed2) and torch.equal(beta, beta2)
 
 
-@pytest.mark.parametrize("q,M", [(8, 2), (16, 2), (16, 3), (16, 4)])
+@pytest.mark.parametrize("q,M", [(4, 2), (4, 4), (8, 2), (16, 2), (16, 3), (16, 4)])
 def test_theta_quantizer_layer_kernel_matches_generic(q, M):
-    """The fused quantizer with beta from theta at q = 8, 16 on the layer
-    round-trip kernel (betas derived once per row in the workgroup, the table
-    decode, dec / beta from one reciprocal) against the generic kernel
+    """The fused quantizer with beta from theta at q = 4, 8, 16 on the layer
+    round-trip kernel (betas derived once per row in the workgroup, the
+    decode through tables, dec / beta from one reciprocal) against the generic kernel
     (set_codec_plain(False)), bit for bit: W_q in fp32 and bf16, the level
     words, beta, d beta / d theta, the step counter and the bias cast; rows
     of 64 (the least the per-workgroup betas take), 96 and 384 blocks, and a
