@@ -791,7 +791,7 @@ def bench_c5(torch, ca, args):
         # dense products' library solutions chosen by timing whole replays
         # (torch's default selection or TunableOp's)
         xs = x.detach().clone().requires_grad_(True)
-        cap = ca.CapturedQATStep(layer, xs, gy.clone(), tune_gemms=True)
+        cap = ca.CapturedQATStep(layer, xs, gy.clone(), tune_gemms=args.tune_gemms)
         kg, wg = gpu_time(torch, cap.step, 100, 3, 0.1)
         res["shapes"][f"{fin}x{fout}"] = {"tokens_per_s": round(4096 / k, 1), "ms": round(k * 1e3, 3),
                                           "tflops": round(flops / k / 1e12, 1),
@@ -822,6 +822,9 @@ def main():
                     help="skip the host-CPU baselines (the C oracle on the host cores)")
     ap.add_argument("--only", default="c1,c2,c2stream,c2codes,c2api,c3,c4,c5,peaks",
                     help="comma list of workloads to run")
+    ap.add_argument("--no-tune-gemms", dest="tune_gemms", action="store_false",
+                    help="C5: capture with torch's default product solutions only (no TunableOp pass; "
+                         "for counter runs, where its thousands of tuning dispatches are each serialized)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 512 MiB device copy (HBM counter calibration)")
     args = ap.parse_args()
