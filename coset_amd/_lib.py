@@ -194,7 +194,8 @@ def set_fast_projection(enabled: bool) -> None:
 def set_codec_plain(enabled: bool) -> None:
     """The fixed-format codec kernels where a call qualifies (default) -- the
     table kernel's variant for fp32 in/out, beta = 2^k, no dither, and the
-    layer round-trip kernel for stored per-row betas at q = 8, 16 -- or
+    layer round-trip kernel for stored or theta-derived per-row betas at
+    q = 4, 8, 16 -- or
     always the general ones (bit-identical results)."""
     call("coset_set_option", OPT_CODEC_PLAIN, int(bool(enabled)))
 

@@ -83,7 +83,7 @@ enum {
     COSET_OPT_VLUT_SPLITS = 3, /* vLUT K splits: 0 automatic, n > 0 forced (clamped to the valid range) */
     COSET_OPT_FAST_PROJECTION = 4, /* encoders: 1 fast projection where provably exact (default), 0 never */
     COSET_OPT_CODEC_PLAIN = 5,     /* 1 fixed-format codec kernels where a call qualifies (default: the table kernel's for fp32,
-                                      beta = 2^k calls; the layer round trip's for stored betas at q = 8, 16), 0 never */
+                                      beta = 2^k calls; the layer round trip's for stored or theta-derived betas at q = 4, 8, 16), 0 never */
     COSET_OPT_CODEC_DYNAMIC = 6,   /* fixed-format table kernel: 1 tiles from a counter run per launch (default), 0 grid stride */
     COSET_OPT_VLUT_DEEP = 7,       /* vLUT matmul above 32 tokens: 1 the 64-row deep kernel (default), 0 the 128-row wide one */
     COSET_OPT_GEMM_TN_TILE = 8     /* coset_gemm_tn output tiles: 0 64 x 64 where they fit, else 96 x 96 (default); 64 or 96 only that size */
