@@ -43,12 +43,6 @@ __device__ __forceinline__ void two_r_tables(uint32_t w, const uint16_t* map, co
 // tile spans at least 64 blocks.
 constexpr int kWgTiles = 256 / 64 + 2;
 
-// q = 4 in the layer round-trip kernel: true decodes each level through the
-// L2-resident cid map and coarse points (two_r_tables' values), false through
-// the workgroup's LDS table of dyadic_level_acc; both give the reference's
-// residual for every q = 4 code.
-constexpr bool kLayerQ4TableDecode = true;
-
 // WGBETA: layer scaling with beta derived from theta and tiles of at least
 // 64 blocks -- the workgroup derives the beta of each tile it touches once,
 // in LDS, instead of every block deriving its own.
@@ -339,7 +333,10 @@ __global__ void __launch_bounds__(256) hnlq_layer_rt_kernel(CodecArgs a)
 {
     static_assert(Q == 4 || Q == 8 || Q == 16, "the table decode's q within the codec's q <= 16");
     static_assert(M >= 1 && M <= 4, "level words stored as one vector");
-    constexpr bool kGdec = Q == 4 && kLayerQ4TableDecode;  // q = 4: the L2-resident decode tables
+    // q = 4 decodes each level through the L2-resident cid map and coarse
+    // points (two_r_tables' values; measured faster here than the LDS table
+    // of dyadic_level_acc, which q = 8, 16 take)
+    constexpr bool kGdec = Q == 4;
     constexpr int kSteps = Q <= 8 || M <= 3 ? 1 : 2;
     constexpr int kLog2Q = Q == 4 ? 2 : Q == 8 ? 3 : 4;
     constexpr int kOff = Q * (((1 << (kLog2Q * M)) - 1) / (Q - 1));  // q sum_m q^m
@@ -508,7 +505,7 @@ static bool layer_rt_supported(const CodecArgs& a, int mode)
     const bool betas = a.use_theta ? a.blocks_per_row >= 64 && a.x_dtype == DT_F32 : a.beta_row != nullptr;
     return g_codec_plain && a.fast_projection && mode == MODE_ROUNDTRIP && a.scale_mode == SCALE_LAYER && betas &&
            (a.q == 8 || a.q == 16 ||
-            (a.q == 4 && (!kLayerQ4TableDecode || a.dec_map) && ((uintptr_t)a.packed & 3u) == 0)) &&
+            (a.q == 4 && a.dec_map && ((uintptr_t)a.packed & 3u) == 0)) &&
            a.M >= 1 && a.M <= 4 &&
            !a.dither && !a.codes_f32 &&
            (a.x_dtype == DT_F32 || a.x_dtype == DT_BF16) && (a.out_dtype == DT_F32 || a.out_dtype == DT_BF16) &&
