@@ -39,9 +39,18 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulAr
     static_assert(!SPLIT || (TB > 0 && BF16), "the split staging writes bf16 token rows");
     static_assert(TB == 0 || 2 * CH == kRowsStageKq, "a staged wave range is two chunks");
     constexpr bool DEC = FMT == VLUT_DECODED || FMT == VLUT_DECODED6;  // no table reads
+    // raw words: the cid map (q^8 16-bit entries, 128 KiB at q = 4) staged in
+    // LDS where it fits beside the kernel's other buffers (one 16-token tile,
+    // at most one staged token), so a word's coarse point costs LDS reads
+    // instead of a gather from global memory that waits on the word's load
+    constexpr int kMapN = Q == 2 ? 256 : 65536;
+    constexpr int kLdsOther = (DEC ? 8 : kSwarSlots * 8) + kRowsWaves * NTILE * 4 * 64 * 4 +
+                              (TB == 0 ? 16 : kRowsWaves * TB * kRowsStageRow);
+    constexpr bool LMAP = FMT == VLUT_RAW && kLdsOther + 2 * kMapN <= 160 * 1024;
     __shared__ uint64_t s_tab[DEC ? 1 : kSwarSlots];
     __shared__ float s_red[kRowsWaves][NTILE * 4][64];
     __shared__ __align__(16) unsigned char s_stage[TB == 0 ? 16 : kRowsWaves * TB * kRowsStageRow];
+    __shared__ __align__(16) uint16_t s_map[LMAP ? kMapN : 8];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4;
     const int64_t kb_total = p.K / 8;
@@ -68,9 +77,11 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulAr
     constexpr int W6 = FMT == VLUT_DECODED6 ? CH * kD6Words / kD6Steps : 1;  // 6-byte format: uint32 per lane and chunk
     static_assert(FMT != VLUT_DECODED6 || (CH * kD6Words) % kD6Steps == 0, "whole words per chunk");
     // the epilogue's per-row scale and bias, loaded with the first loads: a
-    // thread's outputs all lie in row r0 + threadIdx.x % 16
+    // thread's outputs all lie in row r0 + threadIdx.x % 16.  The division of
+    // scale_mode 1 waits for its load, so it is done in the epilogue: here it
+    // would hold back every weight load behind one memory round trip.
     const int64_t o_ep = min(r0 + (int64_t)(threadIdx.x & 15), p.rows - 1);
-    const float sc_ep = p.scale ? (p.scale_mode == 0 ? p.scale[o_ep] : 1.f / p.scale[o_ep]) : 1.f;
+    const float sc_raw = p.scale ? p.scale[o_ep] : 1.f;
     const float bias_ep = p.bias ? p.bias[o_ep] : 0.f;
 
     struct Chunk {
@@ -124,6 +135,13 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulAr
                     ck.w[st + 1][0] = v.z;
                     ck.w[st + 1][1 % WN] = v.w;
                 }
+            } else if constexpr (LMAP) {
+                // the words alone; their cids come from s_map when the pair is decoded
+                const uint16_t* src = reinterpret_cast<const uint16_t*>(p.words) +
+                                      vlut_word_index(FMT, ok ? row : r0, ok ? kb : 0, 0, kb_total, M);
+                constexpr uint32_t kMask = kMapN - 1;  // map bounds for any input
+#pragma unroll
+                for (int m = 0; m < M; ++m) ck.w[st][m] = src[m] & kMask;
             } else if constexpr (FMT != VLUT_DECODED6) {
                 load_pair<Q, M, WN>(p, FMT, ok ? row : r0, ok ? kb : 0, kb_total, ck.w[st]);
             }
@@ -135,6 +153,47 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulAr
                     ck.a[st][s] = *reinterpret_cast<const uint4*>(act + (oka ? tok * p.K + kb * 8 : 0));
                 }
             }
+        }
+    };
+    // the decode tables into LDS (every workgroup's own copy), then a barrier;
+    // the map's 16-byte loads (16 a thread at q = 4) all go out before the
+    // first store, so the staging waits for one round trip
+    auto stage_tables = [&]() {
+        if constexpr (!DEC) {
+            // the <a, c> table's loads go out unconditionally (clamped index;
+            // 512 + n_coarse <= kSwarSlots entries), then the stores, so the
+            // staging waits for one round trip, not one per loop iteration
+            constexpr int kThreads = kRowsWaves * 64;
+            constexpr int kTabPer = (kSwarSlots + kThreads - 1) / kThreads;
+            const int n_tab = 512 + p.n_coarse;
+            uint64_t tv[kTabPer];
+#pragma unroll
+            for (int j = 0; j < kTabPer; ++j) {
+                const int i = (int)threadIdx.x + j * kThreads;
+                tv[j] = p.swar[i < n_tab ? i : 0];
+            }
+            if constexpr (LMAP) {
+                constexpr int kVec = kMapN / 8;
+                const uint4* src = reinterpret_cast<const uint4*>(p.map);
+                uint4* dst = reinterpret_cast<uint4*>(s_map);
+                if constexpr (kVec >= kThreads) {
+                    static_assert(kVec % kThreads == 0, "whole rounds of map loads");
+                    constexpr int kPer = kVec / kThreads;
+                    uint4 v[kPer];
+#pragma unroll
+                    for (int j = 0; j < kPer; ++j) v[j] = src[j * kThreads + threadIdx.x];
+#pragma unroll
+                    for (int j = 0; j < kPer; ++j) dst[j * kThreads + threadIdx.x] = v[j];
+                } else {
+                    for (int i = threadIdx.x; i < kVec; i += kThreads) dst[i] = src[i];
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < kTabPer; ++j) {
+                const int i = (int)threadIdx.x + j * kThreads;
+                if (i < n_tab) s_tab[i] = tv[j];
+            }
+            __syncthreads();
         }
     };
     float4_t acc[NTILE];
@@ -172,6 +231,11 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulAr
                 bw = bytes_to_operand<BF16>(x0, x1, f16_off, f32_off);
             } else if constexpr (FMT == VLUT_DECODED) {
                 bw = bytes_to_operand<BF16>(ck.w[st][0], ck.w[st][1 % WN], f16_off, f32_off);
+            } else if constexpr (LMAP) {
+                uint32_t wv[M];
+#pragma unroll
+                for (int m = 0; m < M; ++m) wv[m] = ((uint32_t)s_map[ck.w[st][m]] << 16) | ck.w[st][m];
+                bw = decode_pair_swar<Q, M, BF16>(s_tab, wv, f16_off, f32_off);
             } else {
                 bw = decode_pair_swar<Q, M, BF16>(s_tab, ck.w[st], f16_off, f32_off);
             }
@@ -224,10 +288,7 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulAr
                                (uint32_t)h[pl][4] | ((uint32_t)h[pl][5] << 16),
                                (uint32_t)h[pl][6] | ((uint32_t)h[pl][7] << 16));
         }
-        if constexpr (!DEC) {
-            for (int i = threadIdx.x; i < 512 + p.n_coarse; i += blockDim.x) s_tab[i] = p.swar[i];
-            __syncthreads();
-        }
+        stage_tables();
         run(c_a, w0);
         run(c_b, w0 + CH);
     } else if constexpr (TB > 0) {
@@ -252,10 +313,7 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulAr
             *reinterpret_cast<uint4*>(&s_stage[(wave * TB + t) * kRowsStageRow + lane * 16]) =
                 make_uint4(av[t].x & m, av[t].y & m, av[t].z & m, av[t].w & m);
         }
-        if constexpr (!DEC) {
-            for (int i = threadIdx.x; i < 512 + p.n_coarse; i += blockDim.x) s_tab[i] = p.swar[i];
-            __syncthreads();
-        }
+        stage_tables();
         run(c_a, w0);
         run(c_b, w0 + CH);
     } else {
@@ -264,10 +322,7 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulAr
         int64_t c0 = w0;
         load(c0, c_a);
         // the tables are staged while the first chunk's loads are in flight
-        if constexpr (!DEC) {
-            for (int i = threadIdx.x; i < 512 + p.n_coarse; i += blockDim.x) s_tab[i] = p.swar[i];
-            __syncthreads();
-        }
+        stage_tables();
         for (; c0 < w1; c0 += 2 * CH) {
             const int64_t c1 = c0 + CH;
             load(c1, c_b);
@@ -284,6 +339,7 @@ __global__ void __launch_bounds__(kRowsWaves * 64) vlut_rows_kernel(VlutMatmulAr
 #pragma unroll
         for (int i = 0; i < 4; ++i) s_red[wave][s * 4 + i][lane] = acc[s][i];
     __syncthreads();
+    const float sc_ep = p.scale && p.scale_mode != 0 ? 1.f / sc_raw : sc_raw;
     if (p.planes_b > 0) {
         // one split and one token tile (t_base = 0) hold all three planes:
         // output (b, o) sums each plane's waves as below, scales it, adds the
@@ -350,6 +406,9 @@ hipError_t launch_rows(const VlutMatmulArgs& p, int splits, hipStream_t s)
         const bool bf = p.act_dtype == DT_BF16;
         // the staged kernels take a wave's whole K range (at most kRowsStageKq k-quads) at once
         const bool staged = vlut_rows_staged(p.K, splits);
+        // raw q = 4 words above one token: the kernels without staged activations,
+        // whose LDS holds the cid map beside their other buffers
+        const bool raw_map = Q == 4 && p.prepared == VLUT_RAW;
         if (p.act_planes) {   // fp32 activations split by the staging: one tile, one split
             if (!staged || splits != 1 || p.planes_b <= 0 || p.B != 3 * p.planes_b || p.B > 15)
                 return hipErrorInvalidValue;
@@ -357,9 +416,9 @@ hipError_t launch_rows(const VlutMatmulArgs& p, int splits, hipStream_t s)
             else launch_rows_fmt<Q, M, true, 1, 16, true>(p, splits, s);
         } else if (staged && p.B == 1) {  // staged activations, one token
             if (bf) launch_rows_fmt<Q, M, true, 1, 1>(p, splits, s); else launch_rows_fmt<Q, M, false, 1, 1>(p, splits, s);
-        } else if (staged && p.B <= 8) {  // staged activations, up to 8 tokens
+        } else if (staged && p.B <= 8 && !raw_map) {  // staged activations, up to 8 tokens
             if (bf) launch_rows_fmt<Q, M, true, 1, 8>(p, splits, s); else launch_rows_fmt<Q, M, false, 1, 8>(p, splits, s);
-        } else if (staged && p.B <= 16) {  // staged activations, up to 16 tokens
+        } else if (staged && p.B <= 16 && !raw_map) {  // staged activations, up to 16 tokens
             if (bf) launch_rows_fmt<Q, M, true, 1, 16>(p, splits, s); else launch_rows_fmt<Q, M, false, 1, 16>(p, splits, s);
         } else if (p.B <= 16) {
             if (bf) launch_rows_fmt<Q, M, true, 1, 0>(p, splits, s); else launch_rows_fmt<Q, M, false, 1, 0>(p, splits, s);
